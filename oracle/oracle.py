@@ -1,0 +1,342 @@
+"""ctypes wrapper around liboracle.so -- TEST INFRASTRUCTURE ONLY.
+
+All arrays are numpy float64 (int32 for ids/labels), row-major, 0-based ids.
+See oracle.h for the reference file:line each function restates.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+_D = ctypes.POINTER(ctypes.c_double)
+_I = ctypes.POINTER(ctypes.c_int)
+
+
+class LmCfg(ctypes.Structure):
+    """or_lm_cfg (oracle.h); defaults follow ai/nn/transformer.lua:88-98."""
+    _fields_ = [("vocab", ctypes.c_int), ("dim", ctypes.c_int), ("layers", ctypes.c_int),
+                ("heads", ctypes.c_int), ("ffn", ctypes.c_int), ("causal", ctypes.c_int),
+                ("eps", ctypes.c_double), ("rope_base", ctypes.c_double)]
+
+
+def build():
+    """Compile liboracle.so from oracle.c (gcc, strict IEEE double)."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        _lib = ctypes.CDLL(_LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+def _declare(L):
+    c_int, c_long, c_double = ctypes.c_int, ctypes.c_long, ctypes.c_double
+    sig = {
+        "or_mm": (None, [_D, _D, _D, c_int, c_int, c_int, c_int]),
+        "or_matmul_nt": (None, [_D, _D, _D, c_int, c_int, c_int, c_int]),
+        "or_matmul_tn": (None, [_D, _D, _D, c_int, c_int, c_int, c_int]),
+        "or_rmsnorm_fwd": (None, [_D, _D, _D, _D, c_int, c_int, c_double]),
+        "or_rmsnorm_bwd": (None, [_D, _D, _D, _D, _D, _D, c_int, c_int]),
+        "or_softmax_fwd": (None, [_D, _D, c_int, c_int, c_int, c_int]),
+        "or_softmax_bwd": (None, [_D, _D, _D, c_int, c_int, c_int, c_int]),
+        "or_silu_fwd": (None, [_D, _D, _D, c_long]),
+        "or_silu_bwd": (None, [_D, _D, _D, _D, c_long]),
+        "or_swiglu_fwd": (None, [_D, _D, _D, c_long]),
+        "or_swiglu_bwd": (None, [_D, _D, _D, _D, _D, c_long]),
+        "or_rope_angles": (None, [c_double, c_int, c_int, _D, _D]),
+        "or_rope_fwd": (None, [_D, _D, c_int, c_int, _D, _D, c_int]),
+        "or_rope_bwd": (None, [_D, _D, c_int, c_int, _D, _D, c_int]),
+        "or_rope_heads": (None, [_D, _I, c_int, c_int, c_int, c_int, c_int, c_double, c_int, c_int]),
+        "or_cross_entropy": (c_double, [_D, _I, c_int, c_int, c_int, c_int, _D, _I]),
+        "or_cross_entropy_bwd": (None, [_D, _I, c_int, c_int, c_int, c_int, c_double, c_int, _D]),
+        "or_ce_fused": (None, [_D, _I, _D, _D, c_int, c_int, c_int, c_double]),
+        "or_argmax_rows": (None, [_D, _I, c_int, c_int]),
+        "or_embed_fwd": (None, [_D, _I, _D, c_int, c_int]),
+        "or_embed_bwd": (None, [_D, _I, _D, c_int, c_int, c_double]),
+        "or_grad_norm": (c_double, [_D, c_long]),
+        "or_scale": (None, [_D, c_long, c_double]),
+        "or_sgd_step": (None, [_D, _D, _D, c_long, c_double, c_double, c_double, c_int]),
+        "or_lm_num_params": (c_long, [ctypes.POINTER(LmCfg)]),
+        "or_lm_param_offsets": (c_int, [ctypes.POINTER(LmCfg), ctypes.POINTER(c_long), _I, _I]),
+        "or_lm_window": (c_double, [ctypes.POINTER(LmCfg), _D, _I, _I, c_int, _D, _D, _I]),
+        "or_lm_step_sgd": (c_int, [ctypes.POINTER(LmCfg), _D, _D, _I, _I, c_int, c_int,
+                                   c_double, c_double, c_double, c_double, _D, _D, _I, _D]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+
+
+def _d(a):
+    """float64 C-contiguous view/copy and its pointer."""
+    a = np.ascontiguousarray(a, dtype=np.float64)
+    return a, a.ctypes.data_as(_D)
+
+
+def _i(a):
+    a = np.ascontiguousarray(a, dtype=np.int32)
+    return a, a.ctypes.data_as(_I)
+
+
+def _nul(kind):
+    return ctypes.cast(None, kind)
+
+
+# ---------------------------------------------------------------- GEMM family
+def mm(a, b, out=None, acc=False):
+    """matrix.multiply CPU path (matrix.lua:514-539): a (m,k) . b (k,n)."""
+    a, pa = _d(a); b, pb = _d(b)
+    m, k = a.shape; n = b.shape[1]
+    r = np.zeros((m, n)) if out is None else out
+    assert r.dtype == np.float64 and r.flags.c_contiguous
+    lib().or_mm(pa, pb, r.ctypes.data_as(_D), m, k, n, int(acc))
+    return r
+
+
+def matmul_nt(a, b, out=None, acc=False):
+    """matrix.matmul_nt (matrix.lua:597-625): a (m,k) . b(n,k)^T."""
+    a, pa = _d(a); b, pb = _d(b)
+    m, k = a.shape; n = b.shape[0]
+    r = np.zeros((m, n)) if out is None else out
+    lib().or_matmul_nt(pa, pb, r.ctypes.data_as(_D), m, k, n, int(acc))
+    return r
+
+
+def matmul_tn(a, b, out=None, acc=False):
+    """matrix.matmul_tn (matrix.lua:627-660): a (m,k)^T . b (m,n) -> (k,n)."""
+    a, pa = _d(a); b, pb = _d(b)
+    m, k = a.shape; n = b.shape[1]
+    r = np.zeros((k, n)) if out is None else out
+    lib().or_matmul_tn(pa, pb, r.ctypes.data_as(_D), m, k, n, int(acc))
+    return r
+
+
+# ---------------------------------------------------------------- row ops
+def rmsnorm_fwd(x, w, eps=1e-5):
+    x, px = _d(x); w, pw = _d(w)
+    rows, cols = x.shape
+    out = np.zeros_like(x); inv = np.zeros(rows)
+    lib().or_rmsnorm_fwd(px, pw, out.ctypes.data_as(_D), inv.ctypes.data_as(_D), rows, cols, eps)
+    return out, inv
+
+
+def rmsnorm_bwd(x, w, inv, g):
+    """Returns (dx, dw) starting from zeros (tensor2.lua:641-666)."""
+    x, px = _d(x); w, pw = _d(w); inv, pi = _d(inv); g, pg = _d(g)
+    rows, cols = x.shape
+    dx = np.zeros_like(x); dw = np.zeros(cols)
+    lib().or_rmsnorm_bwd(px, pw, pi, pg, dx.ctypes.data_as(_D), dw.ctypes.data_as(_D), rows, cols)
+    return dx, dw
+
+
+def softmax_fwd(x, causal=False, offset=0):
+    x, px = _d(x)
+    rows, cols = x.shape
+    y = np.zeros_like(x)
+    lib().or_softmax_fwd(px, y.ctypes.data_as(_D), rows, cols, int(causal), offset)
+    return y
+
+
+def softmax_bwd(y, g, causal=False, offset=0):
+    y, py = _d(y); g, pg = _d(g)
+    rows, cols = y.shape
+    dx = np.zeros_like(y)
+    lib().or_softmax_bwd(py, pg, dx.ctypes.data_as(_D), rows, cols, int(causal), offset)
+    return dx
+
+
+def silu_fwd(x):
+    x, px = _d(x)
+    y = np.zeros_like(x); s = np.zeros_like(x)
+    lib().or_silu_fwd(px, y.ctypes.data_as(_D), s.ctypes.data_as(_D), x.size)
+    return y, s
+
+
+def silu_bwd(x, sig, g):
+    x, px = _d(x); sig, ps = _d(sig); g, pg = _d(g)
+    dx = np.zeros_like(x)
+    lib().or_silu_bwd(px, ps, pg, dx.ctypes.data_as(_D), x.size)
+    return dx
+
+
+def swiglu_fwd(gate, up):
+    gate, pg = _d(gate); up, pu = _d(up)
+    h = np.zeros_like(gate)
+    lib().or_swiglu_fwd(pg, pu, h.ctypes.data_as(_D), gate.size)
+    return h
+
+
+def swiglu_bwd(gate, up, dh):
+    gate, pg = _d(gate); up, pu = _d(up); dh, pd = _d(dh)
+    dg = np.zeros_like(gate); du = np.zeros_like(gate)
+    lib().or_swiglu_bwd(pg, pu, pd, dg.ctypes.data_as(_D), du.ctypes.data_as(_D), gate.size)
+    return dg, du
+
+
+def rope_angles(base, hd, maxpos):
+    npairs = hd // 2
+    c = np.zeros((maxpos + 1, npairs)); s = np.zeros((maxpos + 1, npairs))
+    lib().or_rope_angles(base, hd, maxpos, c.ctypes.data_as(_D), s.ctypes.data_as(_D))
+    return c, s
+
+
+def rope_fwd(x, cosr, sinr, npairs=None):
+    x, px = _d(x); cosr, pc = _d(cosr); sinr, ps = _d(sinr)
+    rows, cols = x.shape
+    npairs = cols // 2 if npairs is None else npairs
+    assert cosr.shape[1] == npairs
+    y = np.zeros_like(x)
+    lib().or_rope_fwd(px, y.ctypes.data_as(_D), rows, cols, pc, ps, npairs)
+    return y
+
+
+def rope_bwd(g, cosr, sinr, npairs=None):
+    g, pg = _d(g); cosr, pc = _d(cosr); sinr, ps = _d(sinr)
+    rows, cols = g.shape
+    npairs = cols // 2 if npairs is None else npairs
+    dx = np.zeros_like(g)
+    lib().or_rope_bwd(pg, dx.ctypes.data_as(_D), rows, cols, pc, ps, npairs)
+    return dx
+
+
+def rope_heads(x, heads, hd, row_stride=None, pos_offset=0, theta=10000.0,
+               interleaved=False, inverse=False, pos_ids=None):
+    """luaTL_rope contract in double; returns a rotated copy."""
+    x = np.array(x, dtype=np.float64, copy=True, order="C")
+    rows = x.shape[0]
+    row_stride = x.shape[1] if row_stride is None else row_stride
+    if pos_ids is not None:
+        pid, pp = _i(pos_ids)
+    else:
+        pid, pp = None, _nul(_I)
+    lib().or_rope_heads(x.ctypes.data_as(_D), pp, rows, heads, hd, row_stride, pos_offset,
+                        theta, int(interleaved), int(inverse))
+    return x
+
+
+def cross_entropy(logits, tgt, ignore_index=None):
+    """Tensor.cross_entropy (tensor2.lua:809-857); tgt 0-based. Returns (loss, sm, count)."""
+    x, px = _d(logits); t, pt = _i(tgt)
+    rows, cols = x.shape
+    sm = np.zeros_like(x); cnt = ctypes.c_int(0)
+    loss = lib().or_cross_entropy(px, pt, rows, cols, int(ignore_index is not None),
+                                  int(ignore_index or 0), sm.ctypes.data_as(_D), ctypes.byref(cnt))
+    return loss, sm, cnt.value
+
+
+def cross_entropy_bwd(sm, tgt, count, g=1.0, ignore_index=None):
+    sm, ps = _d(sm); t, pt = _i(tgt)
+    rows, cols = sm.shape
+    lg = np.zeros_like(sm)
+    lib().or_cross_entropy_bwd(ps, pt, rows, cols, int(ignore_index is not None),
+                               int(ignore_index or 0), g, count, lg.ctypes.data_as(_D))
+    return lg
+
+
+def ce_fused(logits, tgt, ignore_index=-1, gscale=1.0):
+    """luaTL_cross_entropy contract: per-row losses and dlogits."""
+    x, px = _d(logits); t, pt = _i(tgt)
+    rows, V = x.shape
+    losses = np.zeros(rows); d = np.zeros_like(x)
+    lib().or_ce_fused(px, pt, losses.ctypes.data_as(_D), d.ctypes.data_as(_D), rows, V,
+                      ignore_index, gscale)
+    return losses, d
+
+
+def argmax_rows(x):
+    x, px = _d(x)
+    rows, cols = x.shape
+    out = np.zeros(rows, dtype=np.int32)
+    lib().or_argmax_rows(px, out.ctypes.data_as(_I), rows, cols)
+    return out
+
+
+def embed_fwd(w, ids):
+    w, pw = _d(w); ids, pi = _i(ids)
+    out = np.zeros((ids.size, w.shape[1]))
+    lib().or_embed_fwd(pw, pi, out.ctypes.data_as(_D), ids.size, w.shape[1])
+    return out
+
+
+def embed_bwd(g, ids, vocab, scale=1.0):
+    g, pg = _d(g); ids, pi = _i(ids)
+    wg = np.zeros((vocab, g.shape[1]))
+    lib().or_embed_bwd(pg, pi, wg.ctypes.data_as(_D), ids.size, g.shape[1], scale)
+    return wg
+
+
+def grad_norm(g):
+    g, pg = _d(g)
+    return lib().or_grad_norm(pg, g.size)
+
+
+def sgd_step(p, g, v, lr, momentum=0.0, wd=0.0, nesterov=False):
+    """In place on float64 arrays p and v (optim2.lua:72-99)."""
+    assert p.dtype == np.float64 and v.dtype == np.float64
+    g, pg = _d(g)
+    lib().or_sgd_step(p.ctypes.data_as(_D), pg, v.ctypes.data_as(_D), p.size, lr, momentum,
+                      wd, int(nesterov))
+
+
+# ---------------------------------------------------------------- LMTrain step
+def lm_cfg(vocab, dim, layers, heads, ffn, causal=True, eps=1e-5, rope_base=10000.0):
+    return LmCfg(vocab, dim, layers, heads, ffn, int(causal), eps, rope_base)
+
+
+def lm_num_params(cfg):
+    return lib().or_lm_num_params(ctypes.byref(cfg))
+
+
+def lm_param_table(cfg):
+    """[(name, offset, rows, cols)] in Transformer:parameters() order."""
+    n = 2 + 9 * cfg.layers
+    offs = (ctypes.c_long * n)(); rows = (ctypes.c_int * n)(); cols = (ctypes.c_int * n)()
+    lib().or_lm_param_offsets(ctypes.byref(cfg), offs, rows, cols)
+    names = ["emb"]
+    for l in range(cfg.layers):
+        names += [f"{nm}.{l}" for nm in ("ln1", "wq", "wk", "wv", "wo", "ln2", "w1", "w3", "w2")]
+    names.append("lnf")
+    return [(names[i], offs[i], rows[i], cols[i]) for i in range(n)]
+
+
+def lm_window(cfg, params, ids, tgt, grads=None):
+    """One window fwd+bwd; returns (loss, grads (accumulated), logits, correct)."""
+    params, pp = _d(params)
+    ids, pi = _i(ids); tgt, pt = _i(tgt)
+    T = ids.size
+    if grads is None:
+        grads = np.zeros(params.size)
+    logits = np.zeros((T, cfg.vocab))
+    corr = ctypes.c_int(0)
+    loss = lib().or_lm_window(ctypes.byref(cfg), pp, pi, pt, T, grads.ctypes.data_as(_D),
+                              logits.ctypes.data_as(_D), ctypes.byref(corr))
+    return loss, grads, logits, corr.value
+
+
+def lm_step_sgd(cfg, params, vel, ids, tgt, lr, momentum=0.9, wd=0.01, clip_norm=1.0):
+    """One LMTrain batch step (optimizer="sgd"); params/vel float64 updated in place.
+
+    ids/tgt are (B, T) 0-based.  Returns dict(losses, gnorm, correct, grads, applied).
+    """
+    assert params.dtype == np.float64 and vel.dtype == np.float64
+    ids, pi = _i(ids); tgt, pt = _i(tgt)
+    B, T = ids.shape
+    losses = np.zeros(B); grads = np.zeros(params.size)
+    gn = ctypes.c_double(0); corr = ctypes.c_int(0)
+    applied = lib().or_lm_step_sgd(ctypes.byref(cfg), params.ctypes.data_as(_D),
+                                   vel.ctypes.data_as(_D), pi, pt, B, T, lr, momentum, wd,
+                                   clip_norm, losses.ctypes.data_as(_D), ctypes.byref(gn),
+                                   ctypes.byref(corr), grads.ctypes.data_as(_D))
+    return dict(losses=losses, gnorm=gn.value, correct=corr.value, grads=grads,
+                applied=bool(applied))

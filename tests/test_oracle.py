@@ -1,0 +1,367 @@
+"""Pins the CPU oracle (oracle/oracle.c) before it is trusted as the parity checker.
+
+Every check below is independent of the oracle's own formula: reference known
+answers (cited), library routines (numpy/scipy/torch float64), closed forms,
+invariants and central finite differences.  CPU only.
+"""
+import math
+
+import numpy as np
+import pytest
+import scipy.special as sps
+
+import oracle as O
+
+RNG = np.random.default_rng(1234)
+
+
+def fd_grad(f, x, h=1e-6):
+    """Central finite-difference gradient of scalar f at x (float64)."""
+    x = np.array(x, dtype=np.float64)
+    g = np.zeros_like(x)
+    it = np.nditer(x, flags=["multi_index"])
+    for _ in it:
+        idx = it.multi_index
+        old = x[idx]
+        x[idx] = old + h; fp = f(x)
+        x[idx] = old - h; fm = f(x)
+        x[idx] = old
+        g[idx] = (fp - fm) / (2 * h)
+    return g
+
+
+# ------------------------------------------------------------------ GEMM family
+def test_mm_reference_known_answers():
+    # tests/core_test.lua:31-34
+    c = O.mm(np.array([[1, 2], [3, 4]]), np.array([[5, 6], [7, 8]]))
+    assert c.ravel().tolist() == [19, 22, 43, 50]
+    # tests/test.lua:445-449 (adapter legacy flat contract)
+    c = O.mm(np.arange(1, 7).reshape(2, 3), np.array([1, 0, 0, 1, 1, 1]).reshape(3, 2))
+    assert c.ravel().tolist() == [4, 5, 10, 11]
+
+
+@pytest.mark.parametrize("m,k,n", [(37, 53, 41), (128, 96, 160), (1, 7, 1), (5, 1, 9)])
+def test_gemm_family_vs_numpy(m, k, n):
+    a = RNG.uniform(-1, 1, (m, k)); b = RNG.uniform(-1, 1, (k, n))
+    np.testing.assert_allclose(O.mm(a, b), a @ b, rtol=1e-12, atol=1e-12)
+    bt = np.ascontiguousarray(b.T)
+    np.testing.assert_allclose(O.matmul_nt(a, bt), a @ b, rtol=1e-12, atol=1e-12)
+    at = np.ascontiguousarray(a.T)            # (k, m) -> A^T B with A stored k x m
+    np.testing.assert_allclose(O.matmul_tn(at, b), a @ b, rtol=1e-12, atol=1e-12)
+    # (AB)^T = B^T A^T
+    np.testing.assert_allclose(O.mm(bt, at), (a @ b).T, rtol=1e-12, atol=1e-12)
+
+
+def test_gemm_accumulate_doubles():
+    # tests/test.lua:115-122: beta = 1 accumulation doubles the product
+    a = RNG.uniform(-1, 1, (6, 4)); b = RNG.uniform(-1, 1, (4, 5))
+    for fn, bb in ((O.mm, b), (O.matmul_nt, np.ascontiguousarray(b.T))):
+        r = fn(a, bb)
+        r2 = fn(a, bb, out=r.copy(), acc=True)
+        np.testing.assert_allclose(r2, 2 * r, rtol=1e-14)
+    at = np.ascontiguousarray(a.T)
+    r = O.matmul_tn(at, b); r2 = O.matmul_tn(at, b, out=r.copy(), acc=True)
+    np.testing.assert_allclose(r2, 2 * r, rtol=1e-14)
+
+
+def test_mm_zero_skip_semantics():
+    # matrix.lua:521,530,650: a==0 terms are skipped, so 0*inf never makes NaN
+    a = np.array([[0.0, 1.0]]); b = np.array([[np.inf], [2.0]])
+    assert O.mm(a, b)[0, 0] == 2.0
+    assert O.matmul_tn(np.ascontiguousarray(a.T), np.array([[np.inf, 1.0]]))[0, 0] == 0.0
+    # matmul_nt has no skip: 0*inf is NaN (matrix.lua:617-619)
+    assert np.isnan(O.matmul_nt(a, np.array([[np.inf, 2.0]]))[0, 0])
+    # inf propagates through a non-zero term (tests/core_test.lua:95-100 intent)
+    assert np.isinf(O.mm(np.array([[np.inf, np.inf]]), np.array([[0.5], [0.5]]))[0, 0])
+
+
+# ------------------------------------------------------------------ RMSNorm
+def test_rmsnorm_forward_invariants():
+    x = RNG.normal(0, 1, (5, 16)); w = np.ones(16)
+    y, inv = O.rmsnorm_fwd(x, w, eps=0.0)
+    np.testing.assert_allclose((y * y).mean(1), 1.0, rtol=1e-12)       # unit RMS
+    y2, _ = O.rmsnorm_fwd(7.5 * x, w, eps=0.0)
+    np.testing.assert_allclose(y2, y, rtol=1e-12)                        # scale invariant
+    np.testing.assert_allclose(inv, 1 / np.sqrt((x * x).mean(1)), rtol=1e-12)
+    wr = RNG.normal(1, 0.1, 16)
+    yw, _ = O.rmsnorm_fwd(x, wr, eps=0.0)
+    np.testing.assert_allclose(yw, y * wr, rtol=1e-12)                   # gain per column
+
+
+def test_rmsnorm_backward_finite_difference():
+    # tests/test.lua:209-243 pattern, but on a random upstream gradient and for dw too
+    rows, cols, eps = 3, 8, 1e-5
+    x = RNG.normal(0, 1, (rows, cols)); w = RNG.normal(1, 0.3, cols); g = RNG.normal(0, 1, (rows, cols))
+    _, inv = O.rmsnorm_fwd(x, w, eps)
+    dx, dw = O.rmsnorm_bwd(x, w, inv, g)
+    fx = lambda xv: float((O.rmsnorm_fwd(xv, w, eps)[0] * g).sum())
+    fw = lambda wv: float((O.rmsnorm_fwd(x, wv, eps)[0] * g).sum())
+    np.testing.assert_allclose(dx, fd_grad(fx, x), rtol=1e-6, atol=1e-8)
+    np.testing.assert_allclose(dw, fd_grad(fw, w), rtol=1e-6, atol=1e-8)
+
+
+# ------------------------------------------------------------------ softmax
+def test_softmax_known_answers_and_invariants():
+    # tests/core_test.lua:48-51: three equal (huge) logits -> 1/3 each
+    y = O.softmax_fwd(np.array([[1000.0, 1000.0, 1000.0]]))
+    np.testing.assert_allclose(y, 1 / 3, rtol=1e-15)
+    x = RNG.normal(0, 2, (9, 9))
+    y = O.softmax_fwd(x)
+    np.testing.assert_allclose(y.sum(1), 1.0, rtol=1e-14)
+    np.testing.assert_allclose(y, sps.softmax(x, axis=1), rtol=1e-13)
+    yc = O.softmax_fwd(x, causal=True)
+    assert np.all(yc[np.triu_indices(9, 1)] == 0.0)                       # mask is exact zero
+    np.testing.assert_allclose(yc.sum(1), 1.0, rtol=1e-14)
+    for i in range(9):
+        np.testing.assert_allclose(yc[i, :i + 1], sps.softmax(x[i, :i + 1]), rtol=1e-13)
+    yo = O.softmax_fwd(x[:4], causal=True, offset=2)                      # offset widens the window
+    assert np.all(yo[0, 3:] == 0) and yo[0, 2] > 0
+    # tests/test.lua:260-262 adapter softmax_causal({1,2,3,4}, 2x2): [1,0; p,1-p]
+    y = O.softmax_fwd(np.array([[1.0, 2.0], [3.0, 4.0]]), causal=True)
+    assert y[0, 0] == 1.0 and y[0, 1] == 0.0
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_softmax_backward(causal):
+    x = RNG.normal(0, 1, (6, 6)); g = RNG.normal(0, 1, (6, 6))
+    y = O.softmax_fwd(x, causal=causal)
+    dx = O.softmax_bwd(y, g, causal=causal)
+    f = lambda xv: float((O.softmax_fwd(xv, causal=causal) * g).sum())
+    np.testing.assert_allclose(dx, fd_grad(f, x), rtol=1e-6, atol=1e-9)
+
+
+# ------------------------------------------------------------------ SiLU / SwiGLU
+def test_silu_swiglu_library_and_fd():
+    x = np.concatenate([RNG.normal(0, 3, 50), [0.0, 40.0, -40.0, -800.0, 800.0]])
+    y, s = O.silu_fwd(x)
+    np.testing.assert_allclose(s, sps.expit(x), rtol=1e-14)              # library sigmoid
+    np.testing.assert_allclose(y, x * sps.expit(x), rtol=1e-14)
+    assert not np.any(np.isnan(y))                                         # stable by sign
+    up = RNG.normal(0, 1, x.size)
+    np.testing.assert_allclose(O.swiglu_fwd(x, up), x * sps.expit(x) * up, rtol=1e-14)
+    gate = RNG.normal(0, 2, (4, 5)); up = RNG.normal(0, 1, (4, 5)); dh = RNG.normal(0, 1, (4, 5))
+    dg, du = O.swiglu_bwd(gate, up, dh)
+    fg = lambda gv: float((O.swiglu_fwd(gv, up) * dh).sum())
+    fu = lambda uv: float((O.swiglu_fwd(gate, uv) * dh).sum())
+    np.testing.assert_allclose(dg, fd_grad(fg, gate), rtol=1e-6, atol=1e-9)
+    np.testing.assert_allclose(du, fd_grad(fu, up), rtol=1e-6, atol=1e-9)
+    dx = O.silu_bwd(gate, sps.expit(gate), dh)
+    fs = lambda gv: float((O.silu_fwd(gv)[0] * dh).sum())
+    np.testing.assert_allclose(dx, fd_grad(fs, gate), rtol=1e-6, atol=1e-9)
+
+
+# ------------------------------------------------------------------ RoPE
+def test_rope_angles_and_rotation():
+    c, s = O.rope_angles(10000.0, 4, 0)
+    # tests/core_test.lua:88-92: position 0 is the identity
+    assert c[0, 0] == 1.0 and s[0, 0] == 0.0
+    hd, T = 16, 12
+    c, s = O.rope_angles(10000.0, hd, T - 1)
+    theta = np.arange(T)[:, None] * 10000.0 ** (-np.arange(0, hd, 2) / hd)[None, :]
+    np.testing.assert_allclose(c, np.cos(theta), rtol=1e-13, atol=1e-15)
+    np.testing.assert_allclose(s, np.sin(theta), rtol=1e-13, atol=1e-15)
+    x = RNG.normal(0, 1, (T, hd))
+    y = O.rope_fwd(x, c, s)
+    np.testing.assert_allclose(y[0], x[0], rtol=0, atol=0)               # pos 0 identity
+    pn = lambda a: a[:, 0::2] ** 2 + a[:, 1::2] ** 2                       # per-pair norms
+    np.testing.assert_allclose(pn(y), pn(x), rtol=1e-12)
+    # complex-number statement of an interleaved rotation
+    z = (x[:, 0::2] + 1j * x[:, 1::2]) * np.exp(1j * theta)
+    np.testing.assert_allclose(y[:, 0::2], z.real, atol=1e-12)
+    np.testing.assert_allclose(y[:, 1::2], z.imag, atol=1e-12)
+    # backward is the transpose (= inverse) rotation: <R x, g> = <x, R^T g>
+    g = RNG.normal(0, 1, (T, hd))
+    np.testing.assert_allclose((y * g).sum(), (x * O.rope_bwd(g, c, s)).sum(), rtol=1e-12)
+    np.testing.assert_allclose(O.rope_bwd(y, c, s), x, atol=1e-12)       # tests/test.lua:277-289
+    # odd width: trailing column passes through
+    x5 = RNG.normal(0, 1, (T, 5)); c2, s2 = O.rope_angles(10000.0, 4, T - 1)
+    assert np.array_equal(O.rope_fwd(x5, c2, s2, 2)[:, 4], x5[:, 4])
+
+
+def test_rope_heads_contract():
+    T, H, hd = 7, 2, 8
+    x = RNG.normal(0, 1, (T, H * hd))
+    c, s = O.rope_angles(10000.0, hd, T - 1)
+    yi = O.rope_heads(x, H, hd, interleaved=True)
+    for h in range(H):                                                    # same as tensor2 rope
+        np.testing.assert_allclose(yi[:, h * hd:(h + 1) * hd], O.rope_fwd(x[:, h * hd:(h + 1) * hd], c, s),
+                                   atol=1e-12)
+    # half-split is the interleaved rotation under the pair permutation
+    # (half-split slot p holds interleaved element 2p, slot p+hd/2 holds 2p+1)
+    perm = np.concatenate([np.arange(0, hd, 2), np.arange(1, hd, 2)])
+    xs = x.copy()
+    for h in range(H):
+        xs[:, h * hd:(h + 1) * hd] = x[:, h * hd + perm]
+    ys = O.rope_heads(xs, H, hd, interleaved=False)
+    for h in range(H):
+        np.testing.assert_allclose(ys[:, h * hd:(h + 1) * hd], yi[:, h * hd + perm], atol=1e-12)
+    back = O.rope_heads(yi, H, hd, interleaved=True, inverse=True)       # inverse = identity
+    np.testing.assert_allclose(back, x, atol=1e-12)
+    pos = np.array([5, 0, 3, 3, 1, 2, 6], dtype=np.int32)
+    yp = O.rope_heads(x, H, hd, interleaved=True, pos_ids=pos)
+    np.testing.assert_allclose(yp[1], x[1], atol=0)                       # pos 0 untouched
+
+
+# ------------------------------------------------------------------ cross-entropy
+def test_cross_entropy_known_answer_and_library():
+    # tests/core_test.lua:54-57: CE([2, 1, 0.1], target 1 (1-based)) = 0.417
+    loss, sm, cnt = O.cross_entropy(np.array([[2.0, 1.0, 0.1]]), [0])
+    assert cnt == 1
+    assert abs(loss - 0.417) < 1e-2                                        # the reference's own bar
+    assert abs(loss - (math.log(math.exp(2) + math.exp(1) + math.exp(0.1)) - 2)) < 1e-15
+    x = RNG.normal(0, 3, (6, 11)); t = RNG.integers(0, 11, 6)
+    loss, sm, cnt = O.cross_entropy(x, t)
+    ref = np.mean(sps.logsumexp(x, axis=1) - x[np.arange(6), t])
+    assert abs(loss - ref) < 1e-13
+    np.testing.assert_allclose(sm, sps.softmax(x, axis=1), rtol=1e-13)
+    dl = O.cross_entropy_bwd(sm, t, cnt)
+    np.testing.assert_allclose(dl.sum(1), 0, atol=1e-15)                  # tests/test.lua:347-355
+    f = lambda xv: O.cross_entropy(xv, t)[0]
+    np.testing.assert_allclose(dl, fd_grad(f, x), rtol=1e-6, atol=1e-9)
+    # uniform logits give ln V
+    assert abs(O.cross_entropy(np.zeros((3, 2000)), [5, 6, 7])[0] - math.log(2000)) < 1e-12
+
+
+def test_cross_entropy_ignore_and_fused_contract():
+    x = RNG.normal(0, 1, (5, 7)); t = np.array([1, 6, 0, 3, 2])
+    loss_i, sm, cnt = O.cross_entropy(x, t, ignore_index=0)
+    assert cnt == 4 and np.all(sm[2] == 0)
+    keep = [0, 1, 3, 4]
+    assert abs(loss_i - O.cross_entropy(x[keep], t[keep])[0]) < 1e-14
+    # fused per-row contract (tests/test.lua:322-357)
+    tt = np.array([2, -1, 7, 3, 9], dtype=np.int32)   # -1 ignored, 7/9 out of range for V=7
+    losses, d = O.ce_fused(x, tt, ignore_index=3, gscale=0.25)
+    assert losses[1] == 0 and losses[2] == 0 and losses[3] == 0 and losses[4] == 0
+    assert np.all(d[1:] == 0)
+    assert abs(losses[0] - (sps.logsumexp(x[0]) - x[0, 2])) < 1e-13
+    np.testing.assert_allclose(d[0], 0.25 * (sps.softmax(x[0]) - np.eye(7)[2]), rtol=1e-13, atol=1e-16)
+
+
+# ------------------------------------------------------------------ argmax / embed
+def test_argmax_known_answer_and_ties():
+    # tests/test.lua:375-379
+    assert O.argmax_rows(np.array([[1, 9, 2], [8, 3, 4]], dtype=float)).tolist() == [1, 0]
+    x = np.array([[3, 7, 7, 1], [np.nan, 2, np.nan, 2], [-np.inf] * 4, [np.nan] * 4,
+                  [-np.inf, -5, np.inf, np.inf]])
+    assert O.argmax_rows(x).tolist() == [1, 1, 0, 0, 2]
+    r = RNG.normal(0, 1, (50, 33))
+    assert np.array_equal(O.argmax_rows(r), np.argmax(r, 1))
+
+
+def test_embed_gather_scatter():
+    # tests/test.lua:291-320: ids {3,0,7,3,1} (0-based on device)
+    V, D = 10, 4
+    tbl = RNG.uniform(-1, 1, (V, D)); ids = np.array([3, 0, 7, 3, 1])
+    out = O.embed_fwd(tbl, ids)
+    assert np.array_equal(out, tbl[ids])
+    dt = O.embed_bwd(np.ones((5, D)), ids, V)
+    assert np.all(dt[3] == 2) and np.all(dt[0] == 1) and np.all(dt[2] == 0)
+
+
+# ------------------------------------------------------------------ optimizer
+def test_grad_norm_and_sgd_closed_form():
+    assert O.grad_norm(np.array([3.0, 4.0])) == 5.0                       # tests/test.lua:157-161
+    p = np.array([1.0, -2.0]); v = np.zeros(2); g = np.array([0.5, 0.25])
+    O.sgd_step(p, g, v, lr=0.1, momentum=0.9, wd=0.01)
+    # step 1: g' = g + wd p = [0.51, 0.23]; v = g'; p -= lr v
+    np.testing.assert_allclose(v, [0.51, 0.23], rtol=1e-15)
+    np.testing.assert_allclose(p, [0.949, -2.023], rtol=1e-15)
+    O.sgd_step(p, g, v, lr=0.1, momentum=0.9, wd=0.01)
+    # step 2: g' = [0.50949, 0.22977]; v = 0.9*[0.51,0.23] + g' = [0.96849, 0.43677]
+    np.testing.assert_allclose(v, [0.96849, 0.43677], rtol=1e-14)
+    np.testing.assert_allclose(p, [0.949 - 0.096849, -2.023 - 0.043677], rtol=1e-14)
+
+
+# ------------------------------------------------------------------ LMTrain
+TINY = dict(vocab=32, dim=16, layers=2, heads=2, ffn=24)
+
+
+def _tiny_params(cfg, scale=0.3, seed=7):
+    rng = np.random.default_rng(seed)
+    tab = O.lm_param_table(cfg)
+    p = np.zeros(O.lm_num_params(cfg))
+    for (name, off, r, c) in tab:
+        if name.startswith("ln"):
+            p[off:off + r * c] = rng.normal(1, 0.1, r * c)
+        else:
+            p[off:off + r * c] = rng.normal(0, scale, r * c)
+    return p, tab
+
+
+def test_lm_param_layout():
+    cfg = O.lm_cfg(2000, 128, 4, 8, 256)
+    # config-2 parameter count: 2000*128 + 4*(2*128 + 4*128*128 + 3*128*256) + 128
+    assert O.lm_num_params(cfg) == 912512
+    tab = O.lm_param_table(cfg)
+    assert tab[0][0] == "emb" and tab[-1][0] == "lnf" and len(tab) == 38
+    assert sum(r * c for (_, _, r, c) in tab) == 912512
+
+
+def test_lm_window_vs_torch_autograd():
+    torch = pytest.importorskip("torch")
+    from tests import lm_torch_ref as ref
+    cfg = O.lm_cfg(**TINY)
+    p, tab = _tiny_params(cfg)
+    rng = np.random.default_rng(3)
+    T = 9
+    ids = rng.integers(0, cfg.vocab, T); tgt = rng.integers(0, cfg.vocab, T)
+    loss, g, logits, corr = O.lm_window(cfg, p, ids, tgt)
+    tl, tg, tlog = ref.window_grad(cfg, p, tab, ids, tgt)
+    assert abs(loss - tl) < 1e-12
+    np.testing.assert_allclose(logits, tlog, rtol=1e-11, atol=1e-13)
+    np.testing.assert_allclose(g, tg, rtol=1e-9, atol=1e-12)
+    assert corr == int((np.argmax(tlog, 1) == tgt).sum())
+    del torch
+
+
+def test_lm_window_finite_difference_spot():
+    cfg = O.lm_cfg(vocab=11, dim=8, layers=1, heads=2, ffn=6)
+    p, tab = _tiny_params(cfg, scale=0.5, seed=11)
+    ids = np.array([1, 4, 4, 9, 0]); tgt = np.array([4, 4, 9, 0, 2])
+    _, g, _, _ = O.lm_window(cfg, p, ids, tgt)
+    rng = np.random.default_rng(5)
+    for idx in rng.choice(p.size, 25, replace=False):
+        h = 1e-6
+        pp = p.copy(); pp[idx] += h; lp = O.lm_window(cfg, pp, ids, tgt)[0]
+        pm = p.copy(); pm[idx] -= h; lm = O.lm_window(cfg, pm, ids, tgt)[0]
+        assert abs((lp - lm) / (2 * h) - g[idx]) < 1e-7 + 1e-5 * abs(g[idx])
+
+
+def test_lm_uniform_logits_give_ln_vocab():
+    cfg = O.lm_cfg(**TINY)
+    p, tab = _tiny_params(cfg)
+    p[tab[0][1]:tab[0][1] + cfg.vocab * cfg.dim] = 0.0                   # zero tied embedding
+    loss = O.lm_window(cfg, p, np.arange(5), np.arange(5))[0]
+    assert abs(loss - math.log(cfg.vocab)) < 1e-13
+
+
+def test_lm_step_sgd_semantics():
+    """lmtrain.lua:1183-1227: mean of window grads, clip, SGD(mom, wd)."""
+    cfg = O.lm_cfg(**TINY)
+    p0, tab = _tiny_params(cfg)
+    rng = np.random.default_rng(9)
+    B, T = 3, 6
+    ids = rng.integers(0, cfg.vocab, (B, T)); tgt = rng.integers(0, cfg.vocab, (B, T))
+    gsum = np.zeros(p0.size); losses = []
+    for b in range(B):
+        l, gsum, _, _ = O.lm_window(cfg, p0, ids[b], tgt[b], grads=gsum)
+        losses.append(l)
+    gmean = gsum / B
+    norm = float(np.sqrt((gmean ** 2).sum()))
+    for clip in (1e9, 0.5 * norm):
+        p = p0.copy(); v = np.zeros_like(p)
+        out = O.lm_step_sgd(cfg, p, v, ids, tgt, lr=0.05, momentum=0.9, wd=0.01, clip_norm=clip)
+        assert out["applied"]
+        np.testing.assert_allclose(out["losses"], losses, rtol=1e-14)
+        assert abs(out["gnorm"] - norm) < 1e-12 * norm
+        gexp = gmean * (clip / norm if norm > clip else 1.0)
+        np.testing.assert_allclose(out["grads"], gexp, rtol=1e-12, atol=1e-16)
+        gp = gexp + 0.01 * p0
+        np.testing.assert_allclose(v, gp, rtol=1e-12, atol=1e-16)
+        np.testing.assert_allclose(p, p0 - 0.05 * gp, rtol=1e-12, atol=1e-16)
+    # a non-finite gradient norm skips the step (lmtrain.lua:1214-1218)
+    bad = p0.copy(); bad[tab[1][1]] = np.nan
+    v = np.zeros_like(bad); before = bad.copy()
+    out = O.lm_step_sgd(cfg, bad, v, ids, tgt, lr=0.05)
+    assert not out["applied"]
+    assert np.array_equal(np.isnan(bad), np.isnan(before)) and np.all(v == 0)
