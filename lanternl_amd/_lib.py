@@ -1,0 +1,98 @@
+"""ctypes binding of liblanternl_hip.so (the C ABI declared in include/lanternl_hip.h).
+
+There is no fallback: if the library is missing or the GPU cannot be
+initialised, every call raises.  Status codes become ``LanternlHipError`` with
+the library's last-error text, the way the reference's Lua ``ck()`` turns a
+luaTL status into a Lua error (ai/gpu/luaTL.lua:240-246).
+"""
+import ctypes
+import os
+
+from .build import LIB_PATH
+
+STATUS = {
+    0: "OK", -1: "NULL", -2: "SHAPE", -3: "DTYPE", -4: "DEVICE",
+    -5: "OOM", -6: "ARG", -7: "CAPACITY", -8: "UNSUPPORTED",
+}
+
+
+class LanternlHipError(RuntimeError):
+    def __init__(self, what, code, msg):
+        self.code = code
+        super().__init__(f"lanternl_hip[{what}]: {msg} ({STATUS.get(code, code)})")
+
+
+class DevInfo(ctypes.Structure):
+    """lhip_devinfo_t"""
+    _fields_ = [
+        ("name", ctypes.c_char * 256), ("arch", ctypes.c_char * 64), ("device", ctypes.c_int),
+        ("compute_units", ctypes.c_int), ("clock_khz", ctypes.c_int), ("wavefront_size", ctypes.c_int),
+        ("total_mem", ctypes.c_longlong), ("lds_per_block", ctypes.c_longlong), ("l2_bytes", ctypes.c_int),
+        ("peak_fp32_matrix_tflops", ctypes.c_double), ("peak_hbm_gbps", ctypes.c_double),
+    ]
+
+
+_i, _f, _d, _ll, _sz = ctypes.c_int, ctypes.c_float, ctypes.c_double, ctypes.c_longlong, ctypes.c_size_t
+_p = ctypes.c_void_p
+_pp = ctypes.POINTER(ctypes.c_void_p)
+
+# name -> (restype, argtypes); every function of include/lanternl_hip.h.
+SIGNATURES = {
+    "lhip_init": (_i, [_i]),
+    "lhip_shutdown": (_i, []),
+    "lhip_is_ready": (_i, []),
+    "lhip_last_error": (ctypes.c_char_p, []),
+    "lhip_clear_error": (None, []),
+    "lhip_device_info": (_i, [ctypes.POINTER(DevInfo)]),
+    "lhip_version": (ctypes.c_char_p, []),
+    "lhip_malloc": (_i, [_pp, _sz]),
+    "lhip_free": (_i, [_p]),
+    "lhip_upload": (_i, [_p, _p, _sz]),
+    "lhip_download": (_i, [_p, _p, _sz]),
+    "lhip_copy": (_i, [_p, _p, _sz]),
+    "lhip_zero": (_i, [_p, _sz]),
+    "lhip_sync": (_i, []),
+    "lhip_stream": (_p, []),
+    "lhip_event_create": (_i, [_pp]),
+    "lhip_event_destroy": (_i, [_p]),
+    "lhip_event_record": (_i, [_p]),
+    "lhip_event_elapsed_ms": (_i, [_p, _p, ctypes.POINTER(_f)]),
+    "lhip_sgemm": (_i, [_i, _i, _i, _i, _i, _f, _p, _i, _p, _i, _f, _p, _i]),
+    "lhip_sgemm_strided_batched": (_i, [_i, _i, _i, _i, _i, _f, _p, _i, _ll, _p, _i, _ll, _f,
+                                        _p, _i, _ll, _i]),
+    "lhip_matmul_host": (_i, [_i, _p, _p, _p, _i, _i, _i, _i]),
+}
+
+_lib = None
+
+
+def lib():
+    """Load the in-tree library (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -m lanternl_amd.build` "
+                               "(or __graft_entry__.build()); there is no CPU fallback")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def last_error():
+    msg = lib().lhip_last_error()
+    return msg.decode(errors="replace") if msg else ""
+
+
+def check(rc, what):
+    if rc != 0:
+        raise LanternlHipError(what, rc, last_error())
+    return rc
+
+
+def call(name, *args):
+    """Call `name` and raise LanternlHipError on a non-zero status."""
+    return check(getattr(lib(), name)(*args), name)

@@ -1,0 +1,234 @@
+// lhip_core.hip -- lifecycle, errors, memory, stream and events of liblanternl_hip.so.
+//
+// Replaces the runtime half of the reference's luaTL core (cuda/luaTL_core.cu:
+// error plumbing 122-166, luaTL_init 1678-1715, devinfo 1755-1763, copies
+// 2031-2094 and 2149-2159).  The reference keeps a caching pool and an arena;
+// here buffers are plain hipMalloc allocations owned by the caller (the LuaJIT
+// side frees them from an ffi.gc finaliser), and all compute work is ordered
+// on one library-owned stream.
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "lhip_internal.h"
+
+namespace lhip {
+
+static State g_state;
+static thread_local char t_err[1024] = {0};
+
+State& st() { return g_state; }
+
+int fail(int code, const char* fmt, ...)
+{
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(t_err, sizeof(t_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what)
+{
+    const int code = (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) ? LHIP_E_OOM : LHIP_E_DEVICE;
+    return fail(code, "%s: %s (%s)", what, hipGetErrorString(e), hipGetErrorName(e));
+}
+
+int check_launch(const char* what)
+{
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(e, what);
+    return LHIP_OK;
+}
+
+}  // namespace lhip
+
+using lhip::fail;
+using lhip::st;
+
+extern "C" {
+
+LHIP_API const char* lhip_version(void) { return "lanternl_hip 0.1.0 (gfx950)"; }
+
+LHIP_API const char* lhip_last_error(void) { return lhip::t_err; }
+
+LHIP_API void lhip_clear_error(void) { lhip::t_err[0] = 0; }
+
+LHIP_API int lhip_is_ready(void) { return st().ready ? 1 : 0; }
+
+LHIP_API int lhip_init(int device)
+{
+    auto& s = st();
+    if (s.ready) {
+        if (s.device == device) return LHIP_OK;
+        return fail(LHIP_E_ARG, "lhip_init: already initialised on device %d (asked for %d); call lhip_shutdown first",
+                    s.device, device);
+    }
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess || count <= 0)
+        return fail(LHIP_E_DEVICE, "lhip_init: no HIP device visible (%s)",
+                    e == hipSuccess ? "device count is 0" : hipGetErrorString(e));
+    if (device < 0 || device >= count)
+        return fail(LHIP_E_ARG, "lhip_init: device %d out of range [0, %d)", device, count);
+    LHIP_CHECK_HIP(hipSetDevice(device), "lhip_init: hipSetDevice");
+    hipDeviceProp_t p;
+    LHIP_CHECK_HIP(hipGetDeviceProperties(&p, device), "lhip_init: hipGetDeviceProperties");
+    if (std::strncmp(p.gcnArchName, "gfx950", 6) != 0)
+        return fail(LHIP_E_UNSUPPORTED, "lhip_init: device %d is %s; this library is built for gfx950 (MI355X) only",
+                    device, p.gcnArchName);
+    // Default-priority, non-blocking stream: independent of the null stream.
+    LHIP_CHECK_HIP(hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking), "lhip_init: hipStreamCreate");
+    s.device = device;
+    s.cu_count = p.multiProcessorCount;
+    s.clock_khz = p.clockRate;
+    s.lds_per_block = p.sharedMemPerBlock;
+    s.total_mem = p.totalGlobalMem;
+    s.l2_bytes = p.l2CacheSize;
+    std::snprintf(s.name, sizeof(s.name), "%s", p.name);
+    std::snprintf(s.arch, sizeof(s.arch), "%s", p.gcnArchName);
+    s.ready = true;
+    return LHIP_OK;
+}
+
+LHIP_API int lhip_shutdown(void)
+{
+    auto& s = st();
+    if (!s.ready) return LHIP_OK;
+    (void)hipStreamSynchronize(s.stream);
+    if (s.d_stage) (void)hipFree(s.d_stage);
+    if (s.h_stage) (void)hipHostFree(s.h_stage);
+    (void)hipStreamDestroy(s.stream);
+    s = lhip::State();
+    return LHIP_OK;
+}
+
+LHIP_API int lhip_device_info(lhip_devinfo_t* out)
+{
+    LHIP_REQUIRE_READY();
+    if (!out) return fail(LHIP_E_NULL, "lhip_device_info: out is NULL");
+    auto& s = st();
+    std::memset(out, 0, sizeof(*out));
+    std::snprintf(out->name, sizeof(out->name), "%s", s.name);
+    std::snprintf(out->arch, sizeof(out->arch), "%s", s.arch);
+    out->device = s.device;
+    out->compute_units = s.cu_count;
+    out->clock_khz = s.clock_khz;
+    out->wavefront_size = 64;
+    out->total_mem = static_cast<long long>(s.total_mem);
+    out->lds_per_block = static_cast<long long>(s.lds_per_block);
+    out->l2_bytes = s.l2_bytes;
+    // CDNA4 fp32 MFMA: 256 flop per clock per CU (4 SIMDs x 64).
+    out->peak_fp32_matrix_tflops = s.cu_count * 256.0 * (s.clock_khz * 1e3) / 1e12;
+    out->peak_hbm_gbps = 8000.0;
+    return LHIP_OK;
+}
+
+LHIP_API int lhip_malloc(void** dptr, size_t bytes)
+{
+    LHIP_REQUIRE_READY();
+    if (!dptr) return fail(LHIP_E_NULL, "lhip_malloc: dptr is NULL");
+    *dptr = nullptr;
+    if (bytes == 0) return fail(LHIP_E_ARG, "lhip_malloc: zero-byte allocation");
+    hipError_t e = hipMalloc(dptr, bytes);
+    if (e != hipSuccess) {
+        *dptr = nullptr;
+        (void)hipGetLastError();
+        return fail(LHIP_E_OOM, "lhip_malloc: %zu bytes: %s", bytes, hipGetErrorString(e));
+    }
+    return LHIP_OK;
+}
+
+LHIP_API int lhip_free(void* dptr)
+{
+    if (!dptr) return LHIP_OK;
+    if (!st().ready) return LHIP_OK;  // after shutdown a late finaliser is a no-op
+    // Work already enqueued may still read the buffer.
+    LHIP_CHECK_HIP(hipStreamSynchronize(st().stream), "lhip_free: stream sync");
+    LHIP_CHECK_HIP(hipFree(dptr), "lhip_free: hipFree");
+    return LHIP_OK;
+}
+
+LHIP_API int lhip_upload(void* dst, const void* src, size_t bytes)
+{
+    LHIP_REQUIRE_READY();
+    if (bytes == 0) return LHIP_OK;
+    if (!dst || !src) return fail(LHIP_E_NULL, "lhip_upload: NULL pointer");
+    LHIP_CHECK_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, st().stream), "lhip_upload");
+    LHIP_CHECK_HIP(hipStreamSynchronize(st().stream), "lhip_upload: sync");
+    return LHIP_OK;
+}
+
+LHIP_API int lhip_download(void* dst, const void* src, size_t bytes)
+{
+    LHIP_REQUIRE_READY();
+    if (bytes == 0) return LHIP_OK;
+    if (!dst || !src) return fail(LHIP_E_NULL, "lhip_download: NULL pointer");
+    LHIP_CHECK_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, st().stream), "lhip_download");
+    LHIP_CHECK_HIP(hipStreamSynchronize(st().stream), "lhip_download: sync");
+    return LHIP_OK;
+}
+
+LHIP_API int lhip_copy(void* dst, const void* src, size_t bytes)
+{
+    LHIP_REQUIRE_READY();
+    if (bytes == 0) return LHIP_OK;
+    if (!dst || !src) return fail(LHIP_E_NULL, "lhip_copy: NULL pointer");
+    LHIP_CHECK_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, st().stream), "lhip_copy");
+    return LHIP_OK;
+}
+
+LHIP_API int lhip_zero(void* dptr, size_t bytes)
+{
+    LHIP_REQUIRE_READY();
+    if (bytes == 0) return LHIP_OK;
+    if (!dptr) return fail(LHIP_E_NULL, "lhip_zero: NULL pointer");
+    LHIP_CHECK_HIP(hipMemsetAsync(dptr, 0, bytes, st().stream), "lhip_zero");
+    return LHIP_OK;
+}
+
+LHIP_API int lhip_sync(void)
+{
+    LHIP_REQUIRE_READY();
+    LHIP_CHECK_HIP(hipStreamSynchronize(st().stream), "lhip_sync");
+    return LHIP_OK;
+}
+
+LHIP_API void* lhip_stream(void) { return st().ready ? static_cast<void*>(st().stream) : nullptr; }
+
+LHIP_API int lhip_event_create(void** ev)
+{
+    LHIP_REQUIRE_READY();
+    if (!ev) return fail(LHIP_E_NULL, "lhip_event_create: ev is NULL");
+    hipEvent_t e;
+    LHIP_CHECK_HIP(hipEventCreate(&e), "lhip_event_create");
+    *ev = static_cast<void*>(e);
+    return LHIP_OK;
+}
+
+LHIP_API int lhip_event_destroy(void* ev)
+{
+    if (!ev || !st().ready) return LHIP_OK;
+    LHIP_CHECK_HIP(hipEventDestroy(static_cast<hipEvent_t>(ev)), "lhip_event_destroy");
+    return LHIP_OK;
+}
+
+LHIP_API int lhip_event_record(void* ev)
+{
+    LHIP_REQUIRE_READY();
+    if (!ev) return fail(LHIP_E_NULL, "lhip_event_record: ev is NULL");
+    LHIP_CHECK_HIP(hipEventRecord(static_cast<hipEvent_t>(ev), st().stream), "lhip_event_record");
+    return LHIP_OK;
+}
+
+LHIP_API int lhip_event_elapsed_ms(void* start, void* stop, float* ms)
+{
+    LHIP_REQUIRE_READY();
+    if (!start || !stop || !ms) return fail(LHIP_E_NULL, "lhip_event_elapsed_ms: NULL argument");
+    LHIP_CHECK_HIP(hipEventSynchronize(static_cast<hipEvent_t>(stop)), "lhip_event_elapsed_ms: sync");
+    LHIP_CHECK_HIP(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop)),
+                   "lhip_event_elapsed_ms");
+    return LHIP_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,370 @@
+// lhip_gemm.hip -- fp32 GEMM family on CDNA4 matrix cores (v_mfma_f32_32x32x2f32).
+//
+// C = alpha * op(A) * op(B) + beta * C, row-major, op = identity or transpose.
+// Serves the three products of the reference's strided luaTL_gemm_ex
+// (cuda/luaTL_train.cu:1075-1094 -> luaTL_gemm_ex_launch 391-476): A.B for the
+// forward, A.B^T (matmul_dx) and A^T.B (matmul_dw) for the backward
+// (ai/gpu/luaTL_train.lua:154-182), and the host-table products of
+// ai/core/matrix.lua (multiply :541, matmul_nt :597, matmul_tn :627).
+//
+// Design (gfx950):
+//   * a workgroup of 4 wave64s computes a BM x BN tile; each wave owns a
+//     (BM/2) x (BN/2) sub-tile made of 32x32 MFMA blocks whose accumulators
+//     stay in registers for the whole K loop;
+//   * both operands are staged in LDS K-major (As[k][m], Bs[k][n]) so that one
+//     MFMA operand fetch is a single ds_read_b32 in which lanes 0-31 read 32
+//     consecutive floats of row k and lanes 32-63 those of row k+1 -- exactly
+//     the A (32x2) / B (2x32) fragment layout of v_mfma_f32_32x32x2f32;
+//   * global->LDS loads are 128-bit and coalesced along the contiguous
+//     dimension of each operand; a transposed operand is transposed on the
+//     LDS write (4 ds_write_b32 per float4), never by a separate pass; the
+//     transposing stores use an odd LDS row stride so that the 32 lanes of a
+//     half-wave hit 32 distinct banks;
+//   * two LDS buffers: the next K tile is fetched into registers while the
+//     current one feeds the MFMAs, one barrier per K tile;
+//   * workgroup ids are remapped so that consecutive tiles of a row band land
+//     on the same XCD (blocks are dispatched round-robin over the 8 XCDs, each
+//     with its own L2), then grouped GROUP_M bands at a time for L2 reuse.
+// Edge tiles (any M, N, K) use bounds-checked scalar loads with zero fill and
+// checked stores; unaligned operands (ld % 4 != 0 or a base not 16-byte
+// aligned) always take the scalar path.
+#include "lhip_internal.h"
+
+namespace lhip {
+namespace {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int kThreads = 256;  // 4 wave64s
+
+// Loads a ROWS x COLS tile of a row-major matrix into registers, float4 per
+// thread per pass, consecutive threads walking the contiguous dimension.
+template <int ROWS, int COLS>
+struct TileRegs {
+    static constexpr int CQ = COLS / 4;            // float4s per tile row
+    static constexpr int RPP = kThreads / CQ;      // tile rows per pass
+    static constexpr int PASSES = ROWS / RPP;
+    static_assert(COLS % 4 == 0 && kThreads % CQ == 0 && ROWS % RPP == 0, "tile/thread mismatch");
+    float4 v[PASSES];
+
+    __device__ __forceinline__ void load(const float* __restrict__ g, int ld, int r0, int c0,
+                                         int rmax, int cmax, bool vec, int tid)
+    {
+        const int cq = tid % CQ;
+        const int rr = tid / CQ;
+        const int gc = c0 + 4 * cq;
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+            const int gr = r0 + rr + p * RPP;
+            const float* src = g + static_cast<long long>(gr) * ld + gc;
+            if (vec && gr < rmax && gc + 3 < cmax) {
+                v[p] = *reinterpret_cast<const float4*>(src);
+            } else {
+                const bool rok = gr < rmax;
+                v[p].x = (rok && gc + 0 < cmax) ? src[0] : 0.f;
+                v[p].y = (rok && gc + 1 < cmax) ? src[1] : 0.f;
+                v[p].z = (rok && gc + 2 < cmax) ? src[2] : 0.f;
+                v[p].w = (rok && gc + 3 < cmax) ? src[3] : 0.f;
+            }
+        }
+    }
+
+    // Store as lds[row][col] (tile orientation kept; LD % 4 == 0).
+    template <int LD>
+    __device__ __forceinline__ void store_direct(float* lds, int tid) const
+    {
+        const int cq = tid % CQ;
+        const int rr = tid / CQ;
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p)
+            *reinterpret_cast<float4*>(lds + (rr + p * RPP) * LD + 4 * cq) = v[p];
+    }
+
+    // Store transposed as lds[col][row].
+    template <int LD>
+    __device__ __forceinline__ void store_transposed(float* lds, int tid) const
+    {
+        const int cq = tid % CQ;
+        const int rr = tid / CQ;
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+            const int r = rr + p * RPP;
+            lds[(4 * cq + 0) * LD + r] = v[p].x;
+            lds[(4 * cq + 1) * LD + r] = v[p].y;
+            lds[(4 * cq + 2) * LD + r] = v[p].z;
+            lds[(4 * cq + 3) * LD + r] = v[p].w;
+        }
+    }
+};
+
+// Map the linear workgroup id to a (tile_m, tile_n) pair: XCD-contiguous
+// chunks, then GROUP_M-row-band grouped raster inside the chunk order.
+__device__ __forceinline__ void tile_coords(int pid, int nwg, int tiles_m, int tiles_n, int& tm, int& tn)
+{
+    constexpr int kXcds = 8;
+    constexpr int kGroupM = 8;
+    if ((nwg % kXcds) == 0) pid = (pid % kXcds) * (nwg / kXcds) + pid / kXcds;
+    const int per_group = kGroupM * tiles_n;
+    const int group = pid / per_group;
+    const int first_m = group * kGroupM;
+    const int gsz = min(tiles_m - first_m, kGroupM);
+    const int in_group = pid - group * per_group;
+    tm = first_m + in_group % gsz;
+    tn = in_group / gsz;
+}
+
+template <int BM, int BN, int BK, bool TA, bool TB>
+__global__ void __launch_bounds__(kThreads)
+sgemm_mfma_kernel(int M, int N, int K, float alpha,
+                  const float* __restrict__ A, int lda, long long sA,
+                  const float* __restrict__ B, int ldb, long long sB, float beta,
+                  float* __restrict__ C, int ldc, long long sC,
+                  int tiles_m, int tiles_n, int vecA, int vecB)
+{
+    constexpr int WM = BM / 2, WN = BN / 2;        // 2x2 waves
+    constexpr int FM = WM / 32, FN = WN / 32;      // 32x32 MFMA blocks per wave
+    static_assert(FM >= 1 && FN >= 1 && BK % 2 == 0, "bad tile");
+    // K-major LDS tiles.  Transposing stores want an odd row stride; direct
+    // float4 stores want a multiple of 4.
+    constexpr int LDA = TA ? BM + 4 : BM + 1;
+    constexpr int LDB = TB ? BN + 1 : BN + 4;
+    __shared__ float As[2][BK * LDA];
+    __shared__ float Bs[2][BK * LDB];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int lr = lane & 31;   // row (A) / column (B) inside a 32-wide fragment
+    const int lk = lane >> 5;   // which of the two k of an MFMA step
+
+    int tm, tn;
+    tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const long long bz = blockIdx.y;
+    A += bz * sA;
+    B += bz * sB;
+    C += bz * sC;
+
+    const int wm = (wave >> 1) * WM;
+    const int wn = (wave & 1) * WN;
+
+    // op(A) tile is BM x BK: rows m, cols k.  Stored (!TA) M x K -> tile (m, k);
+    // stored (TA) K x M -> tile (k, m).
+    TileRegs<TA ? BK : BM, TA ? BM : BK> ra;
+    // op(B) tile is BK x BN.  Stored (!TB) K x N -> tile (k, n); (TB) N x K -> tile (n, k).
+    TileRegs<TB ? BN : BK, TB ? BK : BN> rb;
+
+    auto gload = [&](int k0) {
+        if (TA) ra.load(A, lda, k0, m0, K, M, vecA, tid);
+        else    ra.load(A, lda, m0, k0, M, K, vecA, tid);
+        if (TB) rb.load(B, ldb, n0, k0, N, K, vecB, tid);
+        else    rb.load(B, ldb, k0, n0, K, N, vecB, tid);
+    };
+    auto lstore = [&](int buf) {
+        if (TA) ra.template store_direct<LDA>(As[buf], tid);
+        else    ra.template store_transposed<LDA>(As[buf], tid);
+        if (TB) rb.template store_transposed<LDB>(Bs[buf], tid);
+        else    rb.template store_direct<LDB>(Bs[buf], tid);
+    };
+
+    floatx16 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    const int nk = (K + BK - 1) / BK;
+    if (nk > 0) {
+        gload(0);
+        lstore(0);
+        __syncthreads();
+    }
+    for (int kt = 0; kt < nk; ++kt) {
+        const int cur = kt & 1;
+        const bool more = kt + 1 < nk;
+        if (more) gload((kt + 1) * BK);
+        const float* as = As[cur];
+        const float* bs = Bs[cur];
+#pragma unroll
+        for (int kk = 0; kk < BK; kk += 2) {
+            float a[FM], b[FN];
+#pragma unroll
+            for (int i = 0; i < FM; ++i) a[i] = as[(kk + lk) * LDA + wm + 32 * i + lr];
+#pragma unroll
+            for (int j = 0; j < FN; ++j) b[j] = bs[(kk + lk) * LDB + wn + 32 * j + lr];
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+        if (more) lstore(cur ^ 1);
+        __syncthreads();
+    }
+
+    // Accumulator layout of a 32x32 block: element r of lane l sits at
+    // row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int col = n0 + wn + 32 * j + lr;
+            if (col >= N) continue;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * lk + (r & 3);
+                if (row < M) {
+                    float* dst = C + static_cast<long long>(row) * ldc + col;
+                    const float v = alpha * acc[i][j][r];
+                    *dst = (beta != 0.f) ? v + beta * (*dst) : v;
+                }
+            }
+        }
+}
+
+template <int BM, int BN, int BK>
+int launch_cfg(int ta, int tb, int m, int n, int k, float alpha, const float* A, int lda, long long sA,
+               const float* B, int ldb, long long sB, float beta, float* C, int ldc, long long sC,
+               int batch, int vecA, int vecB, hipStream_t stream)
+{
+    const int tiles_m = ceil_div(m, BM), tiles_n = ceil_div(n, BN);
+    const long long nwg = static_cast<long long>(tiles_m) * tiles_n;
+    if (nwg > 0x7fffffffLL) return fail(LHIP_E_CAPACITY, "sgemm: %lld workgroups exceed the grid limit", nwg);
+    dim3 grid(static_cast<unsigned>(nwg), batch, 1), block(kThreads, 1, 1);
+#define LHIP_GEMM_LAUNCH(TA_, TB_)                                                             \
+    sgemm_mfma_kernel<BM, BN, BK, TA_, TB_><<<grid, block, 0, stream>>>(                        \
+        m, n, k, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC, tiles_m, tiles_n, vecA, vecB)
+    if (!ta && !tb) LHIP_GEMM_LAUNCH(false, false);
+    else if (ta && !tb) LHIP_GEMM_LAUNCH(true, false);
+    else if (!ta && tb) LHIP_GEMM_LAUNCH(false, true);
+    else LHIP_GEMM_LAUNCH(true, true);
+#undef LHIP_GEMM_LAUNCH
+    return check_launch("sgemm: kernel launch");
+}
+
+}  // namespace
+
+int sgemm_launch(int ta, int tb, int m, int n, int k, float alpha,
+                 const float* A, int lda, const float* B, int ldb, float beta,
+                 float* C, int ldc, int batch, long long sA, long long sB, long long sC,
+                 hipStream_t stream)
+{
+    if (m < 0 || n < 0 || k < 0 || batch < 0)
+        return fail(LHIP_E_SHAPE, "sgemm: negative size (m=%d n=%d k=%d batch=%d)", m, n, k, batch);
+    if (m == 0 || n == 0 || batch == 0) return LHIP_OK;
+    if (!C) return fail(LHIP_E_NULL, "sgemm: C is NULL");
+    if (k > 0 && (!A || !B)) return fail(LHIP_E_NULL, "sgemm: A or B is NULL");
+    const int a_cols = ta ? m : k;   // stored column count of A
+    const int b_cols = tb ? k : n;
+    if (k > 0 && lda < (a_cols > 0 ? a_cols : 1))
+        return fail(LHIP_E_SHAPE, "sgemm: lda=%d < %d", lda, a_cols);
+    if (k > 0 && ldb < (b_cols > 0 ? b_cols : 1))
+        return fail(LHIP_E_SHAPE, "sgemm: ldb=%d < %d", ldb, b_cols);
+    if (ldc < n) return fail(LHIP_E_SHAPE, "sgemm: ldc=%d < n=%d", ldc, n);
+    if (batch > 65535) return fail(LHIP_E_CAPACITY, "sgemm: batch %d > 65535", batch);
+    if (batch > 1 && (sA < 0 || sB < 0 || sC < 0))
+        return fail(LHIP_E_SHAPE, "sgemm: negative batch stride");
+    const int vecA = (k > 0 && lda % 4 == 0 && aligned16(A) && (batch == 1 || sA % 4 == 0)) ? 1 : 0;
+    const int vecB = (k > 0 && ldb % 4 == 0 && aligned16(B) && (batch == 1 || sB % 4 == 0)) ? 1 : 0;
+    // Large problems: 128x128 tiles (64x64 per wave).  When that leaves the
+    // chip with fewer workgroups than CUs, use 64x64 tiles for parallelism.
+    const long long big_tiles = static_cast<long long>(ceil_div(m, 128)) * ceil_div(n, 128) * batch;
+    const int cus = st().cu_count > 0 ? st().cu_count : 256;
+    if (big_tiles >= cus)
+        return launch_cfg<128, 128, 32>(ta, tb, m, n, k, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC,
+                                        batch, vecA, vecB, stream);
+    return launch_cfg<64, 64, 32>(ta, tb, m, n, k, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC,
+                                  batch, vecA, vecB, stream);
+}
+
+}  // namespace lhip
+
+using lhip::fail;
+using lhip::st;
+
+extern "C" {
+
+LHIP_API int lhip_sgemm(int transa, int transb, int m, int n, int k, float alpha,
+                        const float* A, int lda, const float* B, int ldb, float beta,
+                        float* C, int ldc)
+{
+    LHIP_REQUIRE_READY();
+    return lhip::sgemm_launch(transa, transb, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc,
+                              1, 0, 0, 0, st().stream);
+}
+
+LHIP_API int lhip_sgemm_strided_batched(int transa, int transb, int m, int n, int k, float alpha,
+                                        const float* A, int lda, long long strideA,
+                                        const float* B, int ldb, long long strideB, float beta,
+                                        float* C, int ldc, long long strideC, int batch)
+{
+    LHIP_REQUIRE_READY();
+    return lhip::sgemm_launch(transa, transb, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc,
+                              batch, strideA, strideB, strideC, st().stream);
+}
+
+LHIP_API int lhip_matmul_host(int op, const double* a, const double* b, double* c,
+                              int m, int k, int n, int acc)
+{
+    LHIP_REQUIRE_READY();
+    if (op < 0 || op > 2) return fail(LHIP_E_ARG, "lhip_matmul_host: op %d not in {0,1,2}", op);
+    if (m < 0 || k < 0 || n < 0) return fail(LHIP_E_SHAPE, "lhip_matmul_host: negative size");
+    // Result shape and operand sizes per op.
+    const long long rows = (op == 2) ? k : m;
+    const long long inner = (op == 2) ? m : k;
+    const long long na = static_cast<long long>(m) * k;
+    const long long nb = (op == 0) ? static_cast<long long>(k) * n
+                                   : (op == 1 ? static_cast<long long>(n) * k : static_cast<long long>(m) * n);
+    const long long nc = rows * n;
+    if (nc == 0) return LHIP_OK;
+    if (!c) return fail(LHIP_E_NULL, "lhip_matmul_host: c is NULL");
+    if (inner == 0) {
+        if (!acc) for (long long i = 0; i < nc; ++i) c[i] = 0.0;
+        return LHIP_OK;
+    }
+    if (!a || !b) return fail(LHIP_E_NULL, "lhip_matmul_host: a or b is NULL");
+    auto& s = st();
+    // Staging: [A | B | C] in fp32, each section padded to 64 floats so every
+    // operand starts 256-byte aligned.
+    auto pad = [](long long x) { return (x + 63) / 64 * 64; };
+    const size_t need = static_cast<size_t>(pad(na) + pad(nb) + pad(nc));
+    if (need > s.d_stage_floats) {
+        if (s.d_stage) { hipStreamSynchronize(s.stream); hipFree(s.d_stage); s.d_stage = nullptr; s.d_stage_floats = 0; }
+        LHIP_CHECK_HIP(hipMalloc(&s.d_stage, need * sizeof(float)), "lhip_matmul_host: device staging");
+        s.d_stage_floats = need;
+    }
+    if (need > s.h_stage_floats) {
+        if (s.h_stage) { hipStreamSynchronize(s.stream); hipHostFree(s.h_stage); s.h_stage = nullptr; s.h_stage_floats = 0; }
+        LHIP_CHECK_HIP(hipHostMalloc(&s.h_stage, need * sizeof(float), hipHostMallocDefault),
+                       "lhip_matmul_host: pinned staging");
+        s.h_stage_floats = need;
+    }
+    float* ha = s.h_stage;
+    float* hb = ha + pad(na);
+    float* hc = hb + pad(nb);
+    for (long long i = 0; i < na; ++i) ha[i] = static_cast<float>(a[i]);
+    for (long long i = 0; i < nb; ++i) hb[i] = static_cast<float>(b[i]);
+    float* da = s.d_stage;
+    float* db = da + pad(na);
+    float* dc = db + pad(nb);
+    LHIP_CHECK_HIP(hipMemcpyAsync(da, ha, (pad(na) + nb) * sizeof(float), hipMemcpyHostToDevice, s.stream),
+                   "lhip_matmul_host: upload");
+    int rc;
+    if (op == 0)       // c(m x n) = a(m x k) b(k x n)
+        rc = lhip::sgemm_launch(0, 0, m, n, k, 1.f, da, k, db, n, 0.f, dc, n, 1, 0, 0, 0, s.stream);
+    else if (op == 1)  // c(m x n) = a(m x k) b(n x k)^T
+        rc = lhip::sgemm_launch(0, 1, m, n, k, 1.f, da, k, db, k, 0.f, dc, n, 1, 0, 0, 0, s.stream);
+    else               // c(k x n) = a(m x k)^T b(m x n)
+        rc = lhip::sgemm_launch(1, 0, k, n, m, 1.f, da, k, db, n, 0.f, dc, n, 1, 0, 0, 0, s.stream);
+    if (rc != LHIP_OK) return rc;
+    LHIP_CHECK_HIP(hipMemcpyAsync(hc, dc, nc * sizeof(float), hipMemcpyDeviceToHost, s.stream),
+                   "lhip_matmul_host: download");
+    LHIP_CHECK_HIP(hipStreamSynchronize(s.stream), "lhip_matmul_host: sync");
+    if (acc) for (long long i = 0; i < nc; ++i) c[i] += static_cast<double>(hc[i]);
+    else     for (long long i = 0; i < nc; ++i) c[i] = static_cast<double>(hc[i]);
+    return LHIP_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,232 @@
+"""GPU parity of the fp32 GEMM family (v_mfma_f32_32x32x2f32) against the CPU oracle.
+
+Bar (north star): relative Frobenius error <= 1e-4 against the double-precision
+restatement of ai/core/matrix.lua's loops, on identical fp32-representable
+inputs.  Large shapes are checked against numpy float64 '@' (an independent
+library product; the oracle's loops agree with it to 1e-12, tests/test_oracle.py).
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle as O
+from lanternl_amd import device, kernels
+from tests.gpu_util import announce, f32, rel_fro, to_dev
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-4
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _dev():
+    device.init(0)
+    yield
+
+
+def _gemm(ta, tb, a, b, alpha=1.0, beta=0.0, c0=None):
+    A, B = to_dev(a), to_dev(b)
+    m = a.shape[1] if ta else a.shape[0]
+    n = b.shape[0] if tb else b.shape[1]
+    C = to_dev(c0) if c0 is not None else device.Buffer((m, n))
+    kernels.sgemm(A, B, C, transa=ta, transb=tb, alpha=alpha, beta=beta)
+    device.sync()
+    return C.download().astype(np.float64)
+
+
+@pytest.mark.parametrize("m,k,n", [(256, 128, 256),          # config C1
+                                   (37, 53, 41), (128, 96, 160),  # tests/test.lua:42,65
+                                   (1, 1, 1), (3, 5, 7), (64, 64, 16), (65, 33, 129),
+                                   (1, 300, 257), (200, 1, 130)])
+def test_gemm_family_vs_oracle(m, k, n):
+    announce("gemm family", m, k, n)
+    rng = np.random.default_rng(1000 + m * 7 + k * 3 + n)
+    a = f32(rng.uniform(-1, 1, (m, k)))
+    b = f32(rng.uniform(-1, 1, (k, n)))
+    ref = O.mm(a, b)                                       # matrix.lua:514-539
+    assert rel_fro(_gemm(False, False, a, b), ref) <= TOL
+    bt = np.ascontiguousarray(b.T)                         # B stored n x k
+    assert rel_fro(_gemm(False, True, a, bt), O.matmul_nt(a, bt)) <= TOL
+    at = np.ascontiguousarray(a.T)                         # A stored k x m: C = at^T . b
+    assert rel_fro(_gemm(True, False, at, b), O.matmul_tn(at, b)) <= TOL
+    assert rel_fro(_gemm(True, True, at, bt), ref) <= TOL
+
+
+def test_gemm_c1_all_variants_bitwise_stable():
+    """Config C1: A 256x128, B 128x256; the three products agree with the oracle
+    and with each other (A.B = (A^T)^T.B = A.(B^T)^T) to fp32 rounding."""
+    announce("gemm C1")
+    rng = np.random.default_rng(1)
+    a = f32(rng.uniform(-1, 1, (256, 128)))
+    b = f32(rng.uniform(-1, 1, (128, 256)))
+    nn = _gemm(False, False, a, b)
+    tn = _gemm(True, False, np.ascontiguousarray(a.T), b)
+    nt = _gemm(False, True, a, np.ascontiguousarray(b.T))
+    ref = O.mm(a, b)
+    for c in (nn, tn, nt):
+        assert rel_fro(c, ref) <= TOL
+    # same accumulation order on every variant -> identical fp32 results
+    assert np.array_equal(nn, tn) and np.array_equal(nn, nt)
+
+
+def test_gemm_alpha_beta_and_nan_in_c():
+    announce("gemm alpha/beta")
+    rng = np.random.default_rng(2)
+    a = f32(rng.uniform(-1, 1, (70, 90)))
+    b = f32(rng.uniform(-1, 1, (90, 50)))
+    ref = O.mm(a, b)
+    # tests/test.lua:115-122: beta = 1 on top of the same product doubles it
+    c1 = _gemm(False, False, a, b)
+    c2 = _gemm(False, False, a, b, beta=1.0, c0=c1)
+    assert rel_fro(c2, 2 * ref) <= TOL
+    c0 = f32(rng.uniform(-1, 1, (70, 50)))
+    c3 = _gemm(False, False, a, b, alpha=-0.5, beta=0.25, c0=c0)
+    assert rel_fro(c3, -0.5 * ref + 0.25 * c0) <= TOL
+    # beta == 0 never reads C
+    cnan = np.full((70, 50), np.nan)
+    c4 = _gemm(False, False, a, b, beta=0.0, c0=cnan)
+    assert np.isfinite(c4).all() and rel_fro(c4, ref) <= TOL
+
+
+def test_gemm_k_zero_scales_c():
+    announce("gemm k=0")
+    c0 = np.arange(12, dtype=np.float64).reshape(3, 4)
+    C = to_dev(c0)
+    A = device.Buffer((3, 1)); B = device.Buffer((1, 4))
+    kernels.sgemm_raw(0, 0, 3, 4, 0, 1.0, A.ptr, 1, B.ptr, 4, 2.0, C.ptr, 4)
+    device.sync()
+    assert np.array_equal(C.download(), 2 * c0)
+
+
+def test_gemm_unaligned_leading_dims_and_views():
+    """Strided sub-matrix views (ld > cols, odd offsets) take the scalar path."""
+    announce("gemm strided views")
+    rng = np.random.default_rng(3)
+    big_a = f32(rng.uniform(-1, 1, (50, 77)))
+    big_b = f32(rng.uniform(-1, 1, (61, 45)))
+    A, B = to_dev(big_a), to_dev(big_b)
+    m, k, n = 33, 41, 29
+    a = big_a[2:2 + m, 3:3 + k]
+    b = big_b[5:5 + k, 1:1 + n]
+    C = device.Buffer((m, n))
+    kernels.sgemm_raw(0, 0, m, n, k, 1.0, A.offset(2 * 77 + 3), 77, B.offset(5 * 45 + 1), 45, 0.0, C.ptr, n)
+    device.sync()
+    assert rel_fro(C.download(), O.mm(np.ascontiguousarray(a), np.ascontiguousarray(b))) <= TOL
+
+
+def test_gemm_strided_batched_per_head_qk():
+    """Per-head Q.K^T through strides (tests/test.lua:128-160: T=8, H=3, hd=4),
+    plus a larger causal-attention shape (T=64, H=8, hd=16)."""
+    for T, H, hd in ((8, 3, 4), (64, 8, 16)):
+        announce("gemm batched qk", T, H, hd)
+        rng = np.random.default_rng(T + H)
+        q = f32(rng.uniform(-1, 1, (T, H * hd)))
+        k = f32(rng.uniform(-1, 1, (T, H * hd)))
+        Q, K = to_dev(q), to_dev(k)
+        S = device.Buffer((H, T, T))
+        kernels.sgemm_strided_batched(0, 1, T, T, hd, 1.0, Q.ptr, H * hd, hd, K.ptr, H * hd, hd,
+                                      0.0, S.ptr, T, T * T, H)
+        device.sync()
+        s = S.download().astype(np.float64)
+        for h in range(H):
+            qh = np.ascontiguousarray(q[:, h * hd:(h + 1) * hd])
+            kh = np.ascontiguousarray(k[:, h * hd:(h + 1) * hd])
+            assert rel_fro(s[h], O.matmul_nt(qh, kh)) <= TOL
+
+
+@pytest.mark.parametrize("n", [1024, 4096])
+def test_gemm_square_large(n):
+    """Config C5 square shapes (1024^3, 4096^3), all three products, vs numpy float64."""
+    announce("gemm square", n)
+    rng = np.random.default_rng(n)
+    a = rng.uniform(-1, 1, (n, n)).astype(np.float32)
+    b = rng.uniform(-1, 1, (n, n)).astype(np.float32)
+    ref = a.astype(np.float64) @ b.astype(np.float64)
+    A, B, C = to_dev(a), to_dev(b), device.Buffer((n, n))
+    for ta, tb, aa, bb in ((0, 0, A, B), (1, 0, None, B), (0, 1, A, None)):
+        if ta:
+            aa = to_dev(np.ascontiguousarray(a.T))
+        if tb:
+            bb = to_dev(np.ascontiguousarray(b.T))
+        kernels.sgemm(aa, bb, C, transa=ta, transb=tb)
+        device.sync()
+        assert rel_fro(C.download(), ref) <= TOL, (ta, tb)
+
+
+@pytest.mark.parametrize("m", [1, 16, 64])
+def test_gemm_skinny(m):
+    """Config C5 skinny shapes: M in {1,16,64}, K=N=4096."""
+    announce("gemm skinny", m)
+    rng = np.random.default_rng(77 + m)
+    a = rng.uniform(-1, 1, (m, 4096)).astype(np.float32)
+    b = rng.uniform(-1, 1, (4096, 4096)).astype(np.float32)
+    ref = a.astype(np.float64) @ b.astype(np.float64)
+    C = device.Buffer((m, 4096))
+    kernels.sgemm(to_dev(a), to_dev(b), C)
+    device.sync()
+    assert rel_fro(C.download(), ref) <= TOL
+
+
+def test_sgemm_rejects_bad_arguments_without_launch():
+    from lanternl_amd._lib import LanternlHipError
+    A = device.Buffer((4, 4))
+    with pytest.raises(LanternlHipError, match="lda"):
+        kernels.sgemm_raw(0, 0, 4, 4, 4, 1.0, A.ptr, 2, A.ptr, 4, 0.0, A.ptr, 4)
+    with pytest.raises(LanternlHipError, match="negative"):
+        kernels.sgemm_raw(0, 0, -1, 4, 4, 1.0, A.ptr, 4, A.ptr, 4, 0.0, A.ptr, 4)
+    with pytest.raises(LanternlHipError, match="NULL"):
+        kernels.sgemm_raw(0, 0, 4, 4, 4, 1.0, None, 4, A.ptr, 4, 0.0, A.ptr, 4)
+
+
+# ------------------------------------------------------- flat-table backend contract
+def test_adapter_legacy_flat_matmul_known_answer():
+    """tests/test.lua:445-449 and tests/core_test.lua:31-34 through the backend module."""
+    announce("adapter known answers")
+    from lanternl_amd import backend
+    assert backend.available, backend.reason
+    assert backend.matmul([1, 2, 3, 4, 5, 6], 2, 3, [1, 0, 0, 1, 1, 1], 2) == [4, 5, 10, 11]
+    assert backend.matmul([1, 2, 3, 4], 2, 2, [5, 6, 7, 8], 2) == [19, 22, 43, 50]
+    # nt: a(2x3) . b(2x3)^T ; tn: a(2x3)^T . b(2x2)
+    assert backend.matmul_nt([1, 2, 3, 4, 5, 6], 2, 3, [1, 0, 0, 0, 1, 1], 2) == [1, 5, 4, 11]
+    assert backend.matmul_tn([1, 2, 3, 4, 5, 6], 2, 3, [1, 0, 0, 1], 2) == [1, 4, 2, 5, 3, 6]
+
+
+def test_matrix_registry_offloads_all_three_products():
+    """ai.Matrix with the backend forced: multiply / matmul_nt / matmul_tn all run on
+    the GPU (last_backend) and match the Lua loops (oracle) at config C1."""
+    announce("matrix registry C1")
+    from lanternl_amd import matrix as MX
+    MX.reset_backends()
+    assert MX.use("luatl_adapter") == "luatl_adapter"
+    try:
+        rng = np.random.default_rng(5)
+        a = f32(rng.uniform(-1, 1, (256, 128)))
+        b = f32(rng.uniform(-1, 1, (128, 256)))
+        r = MX.multiply(MX.Matrix.from_numpy(a), MX.Matrix.from_numpy(b))
+        assert MX.last_backend == "luatl_adapter"
+        assert rel_fro(r.to_numpy(), O.mm(a, b)) <= TOL
+        bt = np.ascontiguousarray(b.T)
+        r = MX.matmul_nt(MX.Matrix.from_numpy(a), MX.Matrix.from_numpy(bt))
+        assert MX.last_backend == "luatl_adapter"
+        assert rel_fro(r.to_numpy(), O.matmul_nt(a, bt)) <= TOL
+        x = f32(rng.uniform(-1, 1, (128, 256)))   # m x k
+        y = f32(rng.uniform(-1, 1, (128, 256)))   # m x n
+        r = MX.matmul_tn(MX.Matrix.from_numpy(x), MX.Matrix.from_numpy(y))
+        assert MX.last_backend == "luatl_adapter"
+        assert rel_fro(r.to_numpy(), O.matmul_tn(x, y)) <= TOL
+    finally:
+        MX.use("auto")
+
+
+def test_matmul_host_accumulate_in_double():
+    announce("matmul_host acc")
+    from lanternl_amd._lib import call
+    rng = np.random.default_rng(9)
+    a = f32(rng.uniform(-1, 1, (20, 30)))
+    b = f32(rng.uniform(-1, 1, (30, 10)))
+    c = rng.uniform(-1, 1, (20, 10))            # arbitrary doubles
+    expect = c + O.mm(a, b)
+    out = c.copy()
+    call("lhip_matmul_host", 0, a.ctypes.data_as(ctypes.c_void_p), b.ctypes.data_as(ctypes.c_void_p),
+         out.ctypes.data_as(ctypes.c_void_p), 20, 30, 10, 1)
+    assert rel_fro(out, expect) <= TOL
