@@ -131,6 +131,99 @@ LHIP_API int lhip_sgemm_strided_batched(int transa, int transb, int m, int n, in
 LHIP_API int lhip_matmul_host(int op, const double* a, const double* b, double* c,
                               int m, int k, int n, int acc);
 
+/* ---- bandwidth-bound kernels (device pointers, fp32 rows, async) ----------
+ * `accumulate` != 0 adds into the output(s) instead of overwriting them, the
+ * way the CPU path's BACKWARD.* functions add into grad buffers. */
+
+/* y = x * w / sqrt(mean_j x^2 + eps) per row; inv[row] = 1/sqrt(...) (may be
+ * NULL).  CPU semantics: Tensor.rmsnorm (ai/core/tensor2.lua:609-634); replaces
+ * luaTL_rmsnorm (cuda/luaTL_core.cu:2329-2341). */
+LHIP_API int lhip_rmsnorm_fwd(const float* x, const float* w, float* y, float* inv,
+                              int rows, int cols, float eps);
+/* dx = dy*w*r - x*(r^3/cols)*sum_j(dy_j w_j x_j); dw = sum over rows of dy*x*r
+ * (dw may be NULL).  Deterministic (no atomics).  CPU: BACKWARD.rmsnorm
+ * (ai/core/tensor2.lua:641-666); replaces luaTL_rmsnorm_bwd (cuda/luaTL_train.cu:1096-1106). */
+LHIP_API int lhip_rmsnorm_bwd(const float* x, const float* w, const float* inv, const float* dy,
+                              float* dx, float* dw, int rows, int cols, int accumulate);
+/* y = softmax(scale * x) over the kept prefix of each row, 0 beyond it.  Without
+ * `causal` the whole row is kept; with it row r keeps
+ * min(max((r % group) + 1 + offset, 1), cols) columns (group <= 0 means rows).
+ * CPU: Tensor.scale + Tensor.softmax_rows (ai/core/tensor2.lua:185-196, 332-383);
+ * replaces luaTL_softmax_ex (cuda/luaTL_train.cu:1108-1118). */
+LHIP_API int lhip_softmax_fwd(const float* x, float* y, int rows, int cols, float scale,
+                              int causal, int offset, int group);
+/* dx = scale * y * (dy - sum_{kept} dy*y) on the kept prefix, 0 beyond.
+ * CPU: BACKWARD.softmax + BACKWARD.scale (ai/core/tensor2.lua:388-408, 185-196);
+ * replaces luaTL_softmax_bwd (cuda/luaTL_train.cu:1120-1129). */
+LHIP_API int lhip_softmax_bwd(const float* y, const float* dy, float* dx, int rows, int cols,
+                              float scale, int causal, int offset, int group, int accumulate);
+/* out = silu(gate) * up over rows x cols with leading dimensions (silu by the
+ * sign-stable sigmoid).  CPU: Tensor.silu + Tensor.mul (ai/core/tensor2.lua:
+ * 272-291, 167-170) as composed at ai/nn/transformer.lua:246-248; replaces
+ * luaTL_swiglu_fwd (cuda/luaTL_train.cu:1131-1140). */
+LHIP_API int lhip_swiglu_fwd(const float* gate, int ld_gate, const float* up, int ld_up,
+                             float* out, int ld_out, int rows, int cols);
+/* dgate = s*(1 + gate*(1-s)) * (up*dout), dup = silu(gate)*dout, s = sigmoid(gate).
+ * CPU: BACKWARD.mul then BACKWARD.silu (ai/core/tensor2.lua:172-183, 293-303);
+ * replaces luaTL_swiglu_bwd (cuda/luaTL_train.cu:1142-1152). */
+LHIP_API int lhip_swiglu_bwd(const float* gate, int ld_gate, const float* up, int ld_up,
+                             const float* dout, int ld_dout, float* dgate, int ld_dgate,
+                             float* dup, int ld_dup, int rows, int cols, int accumulate);
+/* In-place rotary embedding of `heads` heads of `head_dim` columns in each row
+ * (row_stride >= heads*head_dim).  Position of row r: pos_ids[r] if pos_ids,
+ * else (pos_period > 0 ? r % pos_period : r) + pos_offset.  Pair p rotates by
+ * pos / base^(2p/head_dim) (angles in double, as ai/nn/transformer.lua:30-48).
+ * interleaved != 0: pairs (2p, 2p+1) -- the CPU path (ai/core/tensor2.lua:410-446);
+ * else half-split pairs (p, p+head_dim/2).  inverse != 0 rotates by -angle,
+ * which is the backward (ai/core/tensor2.lua:451-473).  Replaces luaTL_rope
+ * (cuda/luaTL_train.cu:1154-1167); head_dim <= 256, even. */
+LHIP_API int lhip_rope(float* x, const int* pos_ids, int rows, int heads, int head_dim, int row_stride,
+                       int pos_offset, int pos_period, double base, int interleaved, int inverse);
+/* Fused softmax + cross-entropy per row: losses[r] = logsumexp(x_r) - x_r[t_r],
+ * dlogits = grad_scale * (softmax(x_r) - onehot(t_r)); rows whose target is < 0,
+ * >= vocab or == ignore_index give 0 and 0.  losses / dlogits may be NULL;
+ * dlogits may alias logits.  CPU: Tensor.cross_entropy + BACKWARD
+ * (ai/core/tensor2.lua:809-882); replaces luaTL_cross_entropy (cuda/luaTL_train.cu:1189-1201). */
+LHIP_API int lhip_ce_fused(const float* logits, const int* targets, float* losses, float* dlogits,
+                           int rows, int vocab, int ignore_index, float grad_scale);
+/* out[r] = first index of the row maximum (strict '>' scan: NaN never wins, a
+ * row of only -inf/NaN gives 0), int32.  CPU: the accuracy loop of
+ * ai/optim/lmtrain.lua:1200-1209; replaces luaTL_argmax_rows (cuda/luaTL_train.cu:1241-1249). */
+LHIP_API int lhip_argmax_rows(const float* x, int* out, int rows, int cols);
+/* out[i] = table[ids[i]] (exact); ids outside [0, vocab) give a zero row.
+ * CPU: Tensor.embed (ai/core/tensor2.lua:572-590); replaces luaTL_embed_fwd
+ * (cuda/luaTL_train.cu:1169-1177). */
+LHIP_API int lhip_embed_fwd(const float* table, const int* ids, float* out, int n, int dim, int vocab);
+/* dtable[v] = (accumulate ? dtable[v] : 0) + scale * sum_{i: ids[i]==v} dout[i],
+ * summed in token order, deterministic (no atomics).  CPU: BACKWARD.embed
+ * (ai/core/tensor2.lua:592-607); replaces luaTL_embed_bwd (cuda/luaTL_train.cu:1179-1187). */
+LHIP_API int lhip_embed_bwd(const float* dout, const int* ids, float* dtable, int n, int dim, int vocab,
+                            float scale, int accumulate);
+
+/* ---- elementwise helpers, reductions and the SGD step ------------------- */
+/* x[0..n) = value (a kernel, safe inside graph capture). */
+LHIP_API int lhip_fill(float* x, long long n, float value);
+/* out = a + b elementwise (the residual adds of ai/nn/transformer.lua:243-249). */
+LHIP_API int lhip_add(const float* a, const float* b, float* out, long long n);
+/* *out (device double) = sum of x^2, deterministic two-stage reduction
+ * (optim2.grad_norm squared, ai/optim/optim2.lua:27-38; replaces luaTL_l2_accum,
+ * cuda/luaTL_train.cu:1215-1221). */
+LHIP_API int lhip_sumsq(const float* x, long long n, double* out);
+/* *out (device float) = scale * sum(x[0..n)) (luaTL_sum_f32, cuda/luaTL_train.cu:1233-1239). */
+LHIP_API int lhip_sum(const float* x, int n, float scale, float* out);
+/* One SGD step with the LMTrain step logic (ai/optim/lmtrain.lua:1212-1226,
+ * ai/optim/optim2.lua:72-99): norm = grad_scale * sqrt(*grad_sumsq) (device
+ * double holding the sum of squares of the raw grads); if the norm is not
+ * finite nothing changes; else g = grads*grad_scale, clipped by clip_norm/norm
+ * when norm > clip_norm > 0, written back to grads; then g += wd*p;
+ * v = momentum*v + g; p -= lr*v (or lr*(g + momentum*v) with nesterov; p -= lr*g
+ * when momentum == 0).  grad_norm_out / applied_out (device, may be NULL)
+ * receive the pre-clip norm and 1/0. */
+LHIP_API int lhip_sgd_step(float* params, float* grads, float* velocity, long long n,
+                           const double* grad_sumsq, float lr, float momentum, float weight_decay,
+                           float grad_scale, float clip_norm, int nesterov,
+                           float* grad_norm_out, int* applied_out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -61,6 +61,22 @@ SIGNATURES = {
     "lhip_sgemm_strided_batched": (_i, [_i, _i, _i, _i, _i, _f, _p, _i, _ll, _p, _i, _ll, _f,
                                         _p, _i, _ll, _i]),
     "lhip_matmul_host": (_i, [_i, _p, _p, _p, _i, _i, _i, _i]),
+    "lhip_rmsnorm_fwd": (_i, [_p, _p, _p, _p, _i, _i, _f]),
+    "lhip_rmsnorm_bwd": (_i, [_p, _p, _p, _p, _p, _p, _i, _i, _i]),
+    "lhip_softmax_fwd": (_i, [_p, _p, _i, _i, _f, _i, _i, _i]),
+    "lhip_softmax_bwd": (_i, [_p, _p, _p, _i, _i, _f, _i, _i, _i, _i]),
+    "lhip_swiglu_fwd": (_i, [_p, _i, _p, _i, _p, _i, _i, _i]),
+    "lhip_swiglu_bwd": (_i, [_p, _i, _p, _i, _p, _i, _p, _i, _p, _i, _i, _i, _i]),
+    "lhip_rope": (_i, [_p, _p, _i, _i, _i, _i, _i, _i, _d, _i, _i]),
+    "lhip_ce_fused": (_i, [_p, _p, _p, _p, _i, _i, _i, _f]),
+    "lhip_argmax_rows": (_i, [_p, _p, _i, _i]),
+    "lhip_embed_fwd": (_i, [_p, _p, _p, _i, _i, _i]),
+    "lhip_embed_bwd": (_i, [_p, _p, _p, _i, _i, _i, _f, _i]),
+    "lhip_fill": (_i, [_p, _ll, _f]),
+    "lhip_add": (_i, [_p, _p, _p, _ll]),
+    "lhip_sumsq": (_i, [_p, _ll, _p]),
+    "lhip_sum": (_i, [_p, _i, _f, _p]),
+    "lhip_sgd_step": (_i, [_p, _p, _p, _ll, _p, _f, _f, _f, _f, _f, _i, _p, _p]),
 }
 
 _lib = None

@@ -41,6 +41,29 @@ int check_launch(const char* what)
     return LHIP_OK;
 }
 
+int workspace(size_t bytes, void** out)
+{
+    auto& s = g_state;
+    if (bytes == 0) bytes = 256;
+    if (bytes > s.work_bytes) {
+        if (s.work) {
+            LHIP_CHECK_HIP(hipStreamSynchronize(s.stream), "workspace: stream sync");
+            LHIP_CHECK_HIP(hipFree(s.work), "workspace: hipFree");
+            s.work = nullptr;
+            s.work_bytes = 0;
+        }
+        const size_t grow = (bytes + (1u << 20) - 1) & ~static_cast<size_t>((1u << 20) - 1);
+        hipError_t e = hipMalloc(&s.work, grow);
+        if (e != hipSuccess) {
+            s.work = nullptr;
+            return fail(LHIP_E_OOM, "workspace: %zu bytes: %s", grow, hipGetErrorString(e));
+        }
+        s.work_bytes = grow;
+    }
+    *out = s.work;
+    return LHIP_OK;
+}
+
 }  // namespace lhip
 
 using lhip::fail;
@@ -98,6 +121,7 @@ LHIP_API int lhip_shutdown(void)
     (void)hipStreamSynchronize(s.stream);
     if (s.d_stage) (void)hipFree(s.d_stage);
     if (s.h_stage) (void)hipHostFree(s.h_stage);
+    if (s.work) (void)hipFree(s.work);
     (void)hipStreamDestroy(s.stream);
     s = lhip::State();
     return LHIP_OK;
@@ -183,8 +207,9 @@ LHIP_API int lhip_zero(void* dptr, size_t bytes)
     LHIP_REQUIRE_READY();
     if (bytes == 0) return LHIP_OK;
     if (!dptr) return fail(LHIP_E_NULL, "lhip_zero: NULL pointer");
-    LHIP_CHECK_HIP(hipMemsetAsync(dptr, 0, bytes, st().stream), "lhip_zero");
-    return LHIP_OK;
+    // a fill kernel rather than hipMemsetAsync, so the call is safe to record
+    // into a captured graph
+    return lhip::zero_bytes(dptr, bytes, st().stream);
 }
 
 LHIP_API int lhip_sync(void)

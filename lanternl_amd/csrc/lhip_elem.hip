@@ -1,0 +1,463 @@
+// lhip_elem.hip -- elementwise and gather/scatter kernels: fill, add, SwiGLU fwd/bwd,
+// RoPE, embedding gather and deterministic scatter-add.
+//
+// HBM-bound; 128-bit (float4) loads and stores wherever the shape and
+// alignment allow, grid-stride loops sized to a few waves per CU.
+// Semantics follow the CPU LMTrain path (ai/core/tensor2.lua):
+//   mul :167-183, silu :272-303 (sigmoid by sign), rope :410-473 with the
+//   angle table of ai/nn/transformer.lua:30-48, embed :572-607;
+// and the batched contracts of cuda/luaTL_train.cu (swiglu :647-686 with
+// leading dimensions, rope :719-767 with pos_ids / pos_offset / half-split /
+// inverse, embed :771-806).
+#include <cmath>
+
+#include "lhip_internal.h"
+
+namespace lhip {
+namespace {
+
+inline int grid_for(long long units, int threads)
+{
+    const long long cap = static_cast<long long>(st().cu_count > 0 ? st().cu_count : 256) * 8;
+    long long g = (units + threads - 1) / threads;
+    if (g > cap) g = cap;
+    return static_cast<int>(g < 1 ? 1 : g);
+}
+
+__global__ void fill_kernel(float* __restrict__ p, long long n, float v)
+{
+    const long long n4 = n >> 2;
+    float4* p4 = reinterpret_cast<float4*>(p);
+    const long long stride = static_cast<long long>(gridDim.x) * blockDim.x;
+    for (long long i = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x; i < n4; i += stride)
+        p4[i] = make_float4(v, v, v, v);
+    for (long long i = 4 * n4 + blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x; i < n; i += stride)
+        p[i] = v;
+}
+
+__global__ void fill_bytes_kernel(unsigned char* __restrict__ p, long long n)
+{
+    const long long stride = static_cast<long long>(gridDim.x) * blockDim.x;
+    for (long long i = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x; i < n; i += stride)
+        p[i] = 0;
+}
+
+__global__ void add_kernel(const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ o,
+                           long long n, int vec)
+{
+    const long long stride = static_cast<long long>(gridDim.x) * blockDim.x;
+    const long long t0 = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
+    if (vec) {
+        const long long n4 = n >> 2;
+        const float4* a4 = reinterpret_cast<const float4*>(a);
+        const float4* b4 = reinterpret_cast<const float4*>(b);
+        float4* o4 = reinterpret_cast<float4*>(o);
+        for (long long i = t0; i < n4; i += stride) {
+            const float4 x = a4[i], y = b4[i];
+            o4[i] = make_float4(x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w);
+        }
+        for (long long i = 4 * n4 + t0; i < n; i += stride) o[i] = a[i] + b[i];
+    } else {
+        for (long long i = t0; i < n; i += stride) o[i] = a[i] + b[i];
+    }
+}
+
+// sigmoid evaluated by sign (tensor2.lua:272-291)
+__device__ __forceinline__ float sigmoid_by_sign(float v)
+{
+    if (v >= 0.f) return 1.0f / (1.0f + expf(-v));
+    const float z = expf(v);
+    return z / (1.0f + z);
+}
+
+// h = silu(g) * u over a rows x cols block with leading dimensions.
+__global__ void swiglu_fwd_kernel(const float* __restrict__ g, int ldg, const float* __restrict__ u, int ldu,
+                                  float* __restrict__ h, int ldh, int rows, int cols, int vec)
+{
+    const long long stride = static_cast<long long>(gridDim.x) * blockDim.x;
+    const long long t0 = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
+    if (vec) {
+        const int c4n = cols >> 2;
+        const long long n = static_cast<long long>(rows) * c4n;
+        for (long long i = t0; i < n; i += stride) {
+            const int r = static_cast<int>(i / c4n), c = 4 * static_cast<int>(i % c4n);
+            const float4 gv = *reinterpret_cast<const float4*>(g + static_cast<long long>(r) * ldg + c);
+            const float4 uv = *reinterpret_cast<const float4*>(u + static_cast<long long>(r) * ldu + c);
+            float4 o;
+            o.x = gv.x * sigmoid_by_sign(gv.x) * uv.x;
+            o.y = gv.y * sigmoid_by_sign(gv.y) * uv.y;
+            o.z = gv.z * sigmoid_by_sign(gv.z) * uv.z;
+            o.w = gv.w * sigmoid_by_sign(gv.w) * uv.w;
+            *reinterpret_cast<float4*>(h + static_cast<long long>(r) * ldh + c) = o;
+        }
+    } else {
+        const long long n = static_cast<long long>(rows) * cols;
+        for (long long i = t0; i < n; i += stride) {
+            const int r = static_cast<int>(i / cols), c = static_cast<int>(i % cols);
+            const float gv = g[static_cast<long long>(r) * ldg + c];
+            h[static_cast<long long>(r) * ldh + c] = gv * sigmoid_by_sign(gv) * u[static_cast<long long>(r) * ldu + c];
+        }
+    }
+}
+
+// dg = s*(1 + g*(1-s)) * (u*dh), du = silu(g)*dh  (BACKWARD.mul then BACKWARD.silu,
+// tensor2.lua:172-183, 293-303); acc adds into dg/du.
+__device__ __forceinline__ void swiglu_bwd_one(float gv, float uv, float dhv, float& dg, float& du)
+{
+    const float s = sigmoid_by_sign(gv);
+    du = (gv * s) * dhv;
+    dg = (s * (1.0f + gv * (1.0f - s))) * (uv * dhv);
+}
+
+__global__ void swiglu_bwd_kernel(const float* __restrict__ g, int ldg, const float* __restrict__ u, int ldu,
+                                  const float* __restrict__ dh, int lddh, float* __restrict__ dg, int lddg,
+                                  float* __restrict__ du, int lddu, int rows, int cols, int acc, int vec)
+{
+    const long long stride = static_cast<long long>(gridDim.x) * blockDim.x;
+    const long long t0 = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
+    if (vec) {
+        const int c4n = cols >> 2;
+        const long long n = static_cast<long long>(rows) * c4n;
+        for (long long i = t0; i < n; i += stride) {
+            const int r = static_cast<int>(i / c4n), c = 4 * static_cast<int>(i % c4n);
+            const float4 gv = *reinterpret_cast<const float4*>(g + static_cast<long long>(r) * ldg + c);
+            const float4 uv = *reinterpret_cast<const float4*>(u + static_cast<long long>(r) * ldu + c);
+            const float4 hv = *reinterpret_cast<const float4*>(dh + static_cast<long long>(r) * lddh + c);
+            float4 a, b;
+            swiglu_bwd_one(gv.x, uv.x, hv.x, a.x, b.x);
+            swiglu_bwd_one(gv.y, uv.y, hv.y, a.y, b.y);
+            swiglu_bwd_one(gv.z, uv.z, hv.z, a.z, b.z);
+            swiglu_bwd_one(gv.w, uv.w, hv.w, a.w, b.w);
+            float4* pg = reinterpret_cast<float4*>(dg + static_cast<long long>(r) * lddg + c);
+            float4* pu = reinterpret_cast<float4*>(du + static_cast<long long>(r) * lddu + c);
+            if (acc) {
+                const float4 og = *pg, ou = *pu;
+                a.x += og.x; a.y += og.y; a.z += og.z; a.w += og.w;
+                b.x += ou.x; b.y += ou.y; b.z += ou.z; b.w += ou.w;
+            }
+            *pg = a;
+            *pu = b;
+        }
+    } else {
+        const long long n = static_cast<long long>(rows) * cols;
+        for (long long i = t0; i < n; i += stride) {
+            const long long r = i / cols, c = i % cols;
+            float a, b;
+            swiglu_bwd_one(g[r * ldg + c], u[r * ldu + c], dh[r * lddh + c], a, b);
+            float* pg = dg + r * lddg + c;
+            float* pu = du + r * lddu + c;
+            *pg = acc ? *pg + a : a;
+            *pu = acc ? *pu + b : b;
+        }
+    }
+}
+
+// --------------------------------------------------------------------- RoPE
+// In place on x[rows][row_stride], heads of hd columns starting at column 0.
+// pos = pos_ids ? pos_ids[r] : (period > 0 ? r % period : r) + pos_offset.
+// Angle of pair p: pos * inv[p], inv[p] = 1 / base^(2p/hd), evaluated in
+// double like the Lua table (transformer.lua:30-48); cos/sin in double, then
+// rounded to fp32.  The table for the block's rows is built once in LDS and
+// shared by every head.  inverse negates sin (the backward rotation).
+constexpr int kRopeMaxPairs = 128;
+constexpr int kRopeRowsPerBlock = 8;
+
+struct RopeFreqs {
+    double inv[kRopeMaxPairs];
+};
+
+__global__ void __launch_bounds__(256)
+rope_kernel(float* __restrict__ x, const int* __restrict__ pos_ids, int rows, int heads, int hd, int row_stride,
+            int pos_offset, int period, int interleaved, int inverse, int vec, RopeFreqs fr)
+{
+    __shared__ float2 tab[kRopeRowsPerBlock * kRopeMaxPairs];   // (cos, sin)
+    const int pairs = hd >> 1;
+    const int r0 = blockIdx.x * kRopeRowsPerBlock;
+    const int nr = min(kRopeRowsPerBlock, rows - r0);
+    for (int i = threadIdx.x; i < nr * pairs; i += blockDim.x) {
+        const int rr = i / pairs, p = i % pairs;
+        const int r = r0 + rr;
+        const int pos = pos_ids ? pos_ids[r] : (period > 0 ? r % period : r) + pos_offset;
+        const double ang = static_cast<double>(pos) * fr.inv[p];
+        double s, c;
+        sincos(ang, &s, &c);
+        tab[rr * kRopeMaxPairs + p] = make_float2(static_cast<float>(c), static_cast<float>(inverse ? -s : s));
+    }
+    __syncthreads();
+    if (vec) {
+        // unit = two adjacent pairs: one float4 (interleaved) or two float2 (half-split)
+        const int units_per_head = pairs >> 1;
+        const int units = nr * heads * units_per_head;
+        const int half = pairs;
+        for (int i = threadIdx.x; i < units; i += blockDim.x) {
+            const int rr = i / (heads * units_per_head);
+            const int rem = i % (heads * units_per_head);
+            const int h = rem / units_per_head, q = rem % units_per_head;
+            const int p = 2 * q;
+            float* base = x + static_cast<long long>(r0 + rr) * row_stride + static_cast<long long>(h) * hd;
+            const float2 cs0 = tab[rr * kRopeMaxPairs + p], cs1 = tab[rr * kRopeMaxPairs + p + 1];
+            if (interleaved) {
+                float4* v4 = reinterpret_cast<float4*>(base + 2 * p);
+                const float4 v = *v4;
+                *v4 = make_float4(v.x * cs0.x - v.y * cs0.y, v.y * cs0.x + v.x * cs0.y,
+                                  v.z * cs1.x - v.w * cs1.y, v.w * cs1.x + v.z * cs1.y);
+            } else {
+                float2* a2 = reinterpret_cast<float2*>(base + p);
+                float2* b2 = reinterpret_cast<float2*>(base + p + half);
+                const float2 a = *a2, b = *b2;
+                *a2 = make_float2(a.x * cs0.x - b.x * cs0.y, a.y * cs1.x - b.y * cs1.y);
+                *b2 = make_float2(b.x * cs0.x + a.x * cs0.y, b.y * cs1.x + a.y * cs1.y);
+            }
+        }
+    } else {
+        const int units = nr * heads * pairs;
+        for (int i = threadIdx.x; i < units; i += blockDim.x) {
+            const int rr = i / (heads * pairs);
+            const int rem = i % (heads * pairs);
+            const int h = rem / pairs, p = rem % pairs;
+            float* base = x + static_cast<long long>(r0 + rr) * row_stride + static_cast<long long>(h) * hd;
+            const float2 cs = tab[rr * kRopeMaxPairs + p];
+            float* a = interleaved ? base + 2 * p : base + p;
+            float* b = interleaved ? base + 2 * p + 1 : base + p + pairs;
+            const float x0 = *a, x1 = *b;
+            *a = x0 * cs.x - x1 * cs.y;
+            *b = x1 * cs.x + x0 * cs.y;
+        }
+    }
+}
+
+// ---------------------------------------------------------------- embedding
+// out[i] = table[ids[i]] (exact copy); an id outside [0, vocab) gives a zero row.
+__global__ void embed_fwd_kernel(const float* __restrict__ table, const int* __restrict__ ids,
+                                 float* __restrict__ out, int n, int dim, int vocab, int vec)
+{
+    const long long stride = static_cast<long long>(gridDim.x) * blockDim.x;
+    const long long t0 = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
+    if (vec) {
+        const int d4 = dim >> 2;
+        const long long total = static_cast<long long>(n) * d4;
+        for (long long i = t0; i < total; i += stride) {
+            const int t = static_cast<int>(i / d4), c = static_cast<int>(i % d4);
+            const int id = ids[t];
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (id >= 0 && id < vocab) v = reinterpret_cast<const float4*>(table + static_cast<long long>(id) * dim)[c];
+            reinterpret_cast<float4*>(out + static_cast<long long>(t) * dim)[c] = v;
+        }
+    } else {
+        const long long total = static_cast<long long>(n) * dim;
+        for (long long i = t0; i < total; i += stride) {
+            const int t = static_cast<int>(i / dim), c = static_cast<int>(i % dim);
+            const int id = ids[t];
+            out[i] = (id >= 0 && id < vocab) ? table[static_cast<long long>(id) * dim + c] : 0.f;
+        }
+    }
+}
+
+// dtable[v] (+)= scale * sum over tokens i with ids[i] == v, added in token
+// order (the Lua loop order, tensor2.lua:592-607), one wave per vocabulary row:
+// the ids are scanned 64 at a time and matches found with a wave ballot.  No
+// atomics, so the result is deterministic.  Ids outside [0, vocab) are skipped.
+constexpr int kEmbedChunk = 512;  // columns per pass (8 per lane)
+
+__global__ void __launch_bounds__(64)
+embed_bwd_kernel(const float* __restrict__ g, const int* __restrict__ ids, float* __restrict__ dtable,
+                 int n, int dim, int vocab, float scale, int acc)
+{
+    const int v = blockIdx.x;
+    const int lane = threadIdx.x;
+    for (int d0 = 0; d0 < dim; d0 += kEmbedChunk) {
+        float a[kEmbedChunk / 64];
+        float* row = dtable + static_cast<long long>(v) * dim;
+#pragma unroll
+        for (int k = 0; k < kEmbedChunk / 64; ++k) {
+            const int d = d0 + lane + 64 * k;
+            a[k] = (acc && d < dim) ? row[d] : 0.f;
+        }
+        for (int i0 = 0; i0 < n; i0 += 64) {
+            const int i = i0 + lane;
+            const bool hit = i < n && ids[i] == v;
+            unsigned long long mask = __ballot(hit);
+            while (mask) {
+                const int b = __ffsll(static_cast<long long>(mask)) - 1;
+                mask &= mask - 1;
+                const float* gr = g + static_cast<long long>(i0 + b) * dim;
+#pragma unroll
+                for (int k = 0; k < kEmbedChunk / 64; ++k) {
+                    const int d = d0 + lane + 64 * k;
+                    if (d < dim) a[k] = a[k] + scale * gr[d];
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < kEmbedChunk / 64; ++k) {
+            const int d = d0 + lane + 64 * k;
+            if (d < dim) row[d] = a[k];
+        }
+    }
+    (void)vocab;
+}
+
+}  // namespace
+
+int fill(float* p, long long n, float v, hipStream_t s)
+{
+    if (n <= 0) return LHIP_OK;
+    if (!p) return fail(LHIP_E_NULL, "fill: NULL pointer");
+    if (!aligned16(p)) return fail(LHIP_E_ARG, "fill: pointer must be 16-byte aligned");
+    fill_kernel<<<grid_for((n + 3) / 4, 256), 256, 0, s>>>(p, n, v);
+    return check_launch("fill");
+}
+
+int zero_bytes(void* p, size_t bytes, hipStream_t s)
+{
+    if (bytes == 0) return LHIP_OK;
+    if (!p) return fail(LHIP_E_NULL, "zero: NULL pointer");
+    if (aligned16(p) && bytes % 4 == 0) return fill(static_cast<float*>(p), static_cast<long long>(bytes / 4), 0.f, s);
+    fill_bytes_kernel<<<grid_for(static_cast<long long>(bytes), 256), 256, 0, s>>>(static_cast<unsigned char*>(p),
+                                                                                  static_cast<long long>(bytes));
+    return check_launch("zero");
+}
+
+int add(const float* a, const float* b, float* o, long long n, hipStream_t s)
+{
+    if (n < 0) return fail(LHIP_E_SHAPE, "add: n < 0");
+    if (n == 0) return LHIP_OK;
+    if (!a || !b || !o) return fail(LHIP_E_NULL, "add: NULL pointer");
+    const int vec = aligned16(a) && aligned16(b) && aligned16(o);
+    add_kernel<<<grid_for(vec ? (n + 3) / 4 : n, 256), 256, 0, s>>>(a, b, o, n, vec);
+    return check_launch("add");
+}
+
+int swiglu_fwd(const float* g, int ldg, const float* u, int ldu, float* h, int ldh, int rows, int cols,
+               hipStream_t s)
+{
+    if (rows < 0 || cols < 0) return fail(LHIP_E_SHAPE, "swiglu_fwd: rows=%d cols=%d", rows, cols);
+    if (rows == 0 || cols == 0) return LHIP_OK;
+    if (!g || !u || !h) return fail(LHIP_E_NULL, "swiglu_fwd: NULL pointer");
+    if (ldg < cols || ldu < cols || ldh < cols) return fail(LHIP_E_SHAPE, "swiglu_fwd: leading dimension < cols");
+    const int vec = cols % 4 == 0 && ldg % 4 == 0 && ldu % 4 == 0 && ldh % 4 == 0 && aligned16(g) &&
+                    aligned16(u) && aligned16(h);
+    const long long units = static_cast<long long>(rows) * (vec ? cols / 4 : cols);
+    swiglu_fwd_kernel<<<grid_for(units, 256), 256, 0, s>>>(g, ldg, u, ldu, h, ldh, rows, cols, vec);
+    return check_launch("swiglu_fwd");
+}
+
+int swiglu_bwd(const float* g, int ldg, const float* u, int ldu, const float* dh, int lddh, float* dg, int lddg,
+               float* du, int lddu, int rows, int cols, int acc, hipStream_t s)
+{
+    if (rows < 0 || cols < 0) return fail(LHIP_E_SHAPE, "swiglu_bwd: rows=%d cols=%d", rows, cols);
+    if (rows == 0 || cols == 0) return LHIP_OK;
+    if (!g || !u || !dh || !dg || !du) return fail(LHIP_E_NULL, "swiglu_bwd: NULL pointer");
+    if (ldg < cols || ldu < cols || lddh < cols || lddg < cols || lddu < cols)
+        return fail(LHIP_E_SHAPE, "swiglu_bwd: leading dimension < cols");
+    const int vec = cols % 4 == 0 && ldg % 4 == 0 && ldu % 4 == 0 && lddh % 4 == 0 && lddg % 4 == 0 &&
+                    lddu % 4 == 0 && aligned16(g) && aligned16(u) && aligned16(dh) && aligned16(dg) && aligned16(du);
+    const long long units = static_cast<long long>(rows) * (vec ? cols / 4 : cols);
+    swiglu_bwd_kernel<<<grid_for(units, 256), 256, 0, s>>>(g, ldg, u, ldu, dh, lddh, dg, lddg, du, lddu, rows,
+                                                           cols, acc, vec);
+    return check_launch("swiglu_bwd");
+}
+
+int rope(float* x, const int* pos_ids, int rows, int heads, int hd, int row_stride, int pos_offset, int period,
+         double base, int interleaved, int inverse, hipStream_t s)
+{
+    if (rows < 0 || heads <= 0 || hd <= 0) return fail(LHIP_E_SHAPE, "rope: rows=%d heads=%d hd=%d", rows, heads, hd);
+    if (rows == 0) return LHIP_OK;
+    if (!x) return fail(LHIP_E_NULL, "rope: x is NULL");
+    if (hd % 2) return fail(LHIP_E_ARG, "rope: head_dim %d must be even", hd);
+    if (hd / 2 > kRopeMaxPairs) return fail(LHIP_E_CAPACITY, "rope: head_dim %d > %d", hd, 2 * kRopeMaxPairs);
+    if (row_stride < heads * hd) return fail(LHIP_E_SHAPE, "rope: row_stride %d < heads*hd %d", row_stride, heads * hd);
+    if (!(base > 0.0)) return fail(LHIP_E_ARG, "rope: base must be > 0");
+    if (period < 0) return fail(LHIP_E_ARG, "rope: period must be >= 0");
+    RopeFreqs fr;
+    const int pairs = hd / 2;
+    for (int p = 0; p < kRopeMaxPairs; ++p)
+        fr.inv[p] = p < pairs ? 1.0 / std::pow(base, static_cast<double>(2 * p) / hd) : 0.0;
+    // vector units need pairs even (two pairs per unit) and 16-byte (interleaved)
+    // or 8-byte (half-split) aligned accesses
+    const bool pairs_even = pairs % 2 == 0;
+    const bool align = interleaved ? (row_stride % 4 == 0 && hd % 4 == 0 && aligned16(x))
+                                   : (row_stride % 2 == 0 && (reinterpret_cast<uintptr_t>(x) & 7u) == 0);
+    const int vec = pairs_even && align;
+    rope_kernel<<<ceil_div(rows, kRopeRowsPerBlock), 256, 0, s>>>(x, pos_ids, rows, heads, hd, row_stride, pos_offset,
+                                                                  period, interleaved, inverse, vec, fr);
+    return check_launch("rope");
+}
+
+int embed_fwd(const float* table, const int* ids, float* out, int n, int dim, int vocab, hipStream_t s)
+{
+    if (n < 0 || dim <= 0 || vocab <= 0) return fail(LHIP_E_SHAPE, "embed_fwd: n=%d dim=%d vocab=%d", n, dim, vocab);
+    if (n == 0) return LHIP_OK;
+    if (!table || !ids || !out) return fail(LHIP_E_NULL, "embed_fwd: NULL pointer");
+    const int vec = dim % 4 == 0 && aligned16(table) && aligned16(out);
+    const long long units = static_cast<long long>(n) * (vec ? dim / 4 : dim);
+    embed_fwd_kernel<<<grid_for(units, 256), 256, 0, s>>>(table, ids, out, n, dim, vocab, vec);
+    return check_launch("embed_fwd");
+}
+
+int embed_bwd(const float* g, const int* ids, float* dtable, int n, int dim, int vocab, float scale, int acc,
+              hipStream_t s)
+{
+    if (n < 0 || dim <= 0 || vocab <= 0) return fail(LHIP_E_SHAPE, "embed_bwd: n=%d dim=%d vocab=%d", n, dim, vocab);
+    if (!dtable) return fail(LHIP_E_NULL, "embed_bwd: dtable is NULL");
+    if (n > 0 && (!g || !ids)) return fail(LHIP_E_NULL, "embed_bwd: NULL g/ids");
+    embed_bwd_kernel<<<vocab, 64, 0, s>>>(g, ids, dtable, n, dim, vocab, scale, acc);
+    return check_launch("embed_bwd");
+}
+
+}  // namespace lhip
+
+using lhip::st;
+
+extern "C" {
+
+LHIP_API int lhip_fill(float* x, long long n, float value)
+{
+    LHIP_REQUIRE_READY();
+    return lhip::fill(x, n, value, st().stream);
+}
+
+LHIP_API int lhip_add(const float* a, const float* b, float* out, long long n)
+{
+    LHIP_REQUIRE_READY();
+    return lhip::add(a, b, out, n, st().stream);
+}
+
+LHIP_API int lhip_swiglu_fwd(const float* gate, int ld_gate, const float* up, int ld_up, float* out, int ld_out,
+                             int rows, int cols)
+{
+    LHIP_REQUIRE_READY();
+    return lhip::swiglu_fwd(gate, ld_gate, up, ld_up, out, ld_out, rows, cols, st().stream);
+}
+
+LHIP_API int lhip_swiglu_bwd(const float* gate, int ld_gate, const float* up, int ld_up, const float* dout,
+                             int ld_dout, float* dgate, int ld_dgate, float* dup, int ld_dup, int rows, int cols,
+                             int accumulate)
+{
+    LHIP_REQUIRE_READY();
+    return lhip::swiglu_bwd(gate, ld_gate, up, ld_up, dout, ld_dout, dgate, ld_dgate, dup, ld_dup, rows, cols,
+                            accumulate, st().stream);
+}
+
+LHIP_API int lhip_rope(float* x, const int* pos_ids, int rows, int heads, int head_dim, int row_stride,
+                       int pos_offset, int pos_period, double base, int interleaved, int inverse)
+{
+    LHIP_REQUIRE_READY();
+    return lhip::rope(x, pos_ids, rows, heads, head_dim, row_stride, pos_offset, pos_period, base, interleaved,
+                      inverse, st().stream);
+}
+
+LHIP_API int lhip_embed_fwd(const float* table, const int* ids, float* out, int n, int dim, int vocab)
+{
+    LHIP_REQUIRE_READY();
+    return lhip::embed_fwd(table, ids, out, n, dim, vocab, st().stream);
+}
+
+LHIP_API int lhip_embed_bwd(const float* dout, const int* ids, float* dtable, int n, int dim, int vocab,
+                            float scale, int accumulate)
+{
+    LHIP_REQUIRE_READY();
+    return lhip::embed_bwd(dout, ids, dtable, n, dim, vocab, scale, accumulate, st().stream);
+}
+
+}  // extern "C"

@@ -31,6 +31,9 @@ struct State {
     size_t d_stage_floats = 0;
     float* h_stage = nullptr;  // pinned
     size_t h_stage_floats = 0;
+    // scratch for reductions of the immediate entry points (grown on demand)
+    void* work = nullptr;
+    size_t work_bytes = 0;
 };
 
 State& st();
@@ -59,7 +62,43 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 inline int ceil_div(long long a, long long b) { return static_cast<int>((a + b - 1) / b); }
 
-// GEMM launcher shared by the immediate entry points and the LM step runner.
+// Library workspace of at least `bytes` (reused; growing it waits for the
+// stream, so it must not be called while a stream capture is in progress).
+int workspace(size_t bytes, void** out);
+
+// Launchers shared by the immediate entry points and the LM step runner.  They
+// validate their arguments and enqueue on `stream`; they never allocate.
+int fill(float* p, long long n, float v, hipStream_t s);
+int zero_bytes(void* p, size_t bytes, hipStream_t s);
+int add(const float* a, const float* b, float* o, long long n, hipStream_t s);
+int rmsnorm_fwd(const float* x, const float* w, float* y, float* inv, int rows, int cols, float eps,
+                hipStream_t s);
+int rmsnorm_bwd_parts(int rows, int cols);
+int rmsnorm_bwd(const float* x, const float* w, const float* inv, const float* dy, float* dx, float* dw,
+                int rows, int cols, int accumulate, float* work, size_t work_floats, hipStream_t s);
+int softmax_fwd(const float* x, float* y, int rows, int cols, float scale, int causal, int offset, int group,
+                hipStream_t s);
+int softmax_bwd(const float* y, const float* dy, float* dx, int rows, int cols, float scale, int causal,
+                int offset, int group, int accumulate, hipStream_t s);
+int ce_fused(const float* logits, const int* tgt, float* losses, float* dlogits, int rows, int V,
+             int ignore_index, float gscale, hipStream_t s);
+int argmax_rows(const float* x, int* out, int rows, int cols, hipStream_t s);
+int swiglu_fwd(const float* g, int ldg, const float* u, int ldu, float* h, int ldh, int rows, int cols,
+               hipStream_t s);
+int swiglu_bwd(const float* g, int ldg, const float* u, int ldu, const float* dh, int lddh, float* dg, int lddg,
+               float* du, int lddu, int rows, int cols, int acc, hipStream_t s);
+int rope(float* x, const int* pos_ids, int rows, int heads, int hd, int row_stride, int pos_offset, int period,
+         double base, int interleaved, int inverse, hipStream_t s);
+int embed_fwd(const float* table, const int* ids, float* out, int n, int dim, int vocab, hipStream_t s);
+int embed_bwd(const float* g, const int* ids, float* dtable, int n, int dim, int vocab, float scale, int acc,
+              hipStream_t s);
+int sumsq_blocks(long long n);
+int sumsq(const float* x, long long n, double* out, double* partial, int partial_len, hipStream_t s);
+int sgd_step(float* p, float* g, float* v, long long n, const double* sumsq_dev, float lr, float momentum,
+             float wd, float grad_scale, float clip_norm, int nesterov, float* gnorm_out, int* applied_out,
+             hipStream_t s);
+int sum_f32(const float* x, int n, float scale, float* out, hipStream_t s);
+
 int sgemm_launch(int transa, int transb, int m, int n, int k, float alpha,
                  const float* A, int lda, const float* B, int ldb, float beta,
                  float* C, int ldc, int batch, long long sA, long long sB, long long sC,

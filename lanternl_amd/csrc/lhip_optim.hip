@@ -1,0 +1,181 @@
+// lhip_optim.hip -- gradient norm and the SGD step of the CPU LMTrain path, on device.
+//
+// optim2.lua: grad_norm :27-38, scale_grads :40-46, SGD :72-99; the step
+// logic of lmtrain.lua:1212-1226 (scale by 1/B, global L2 norm, skip the step
+// when the norm is not finite, clip to clip_norm, update).  The norm never
+// leaves the device: a deterministic two-stage reduction writes it to device
+// memory and the update kernel reads it, so a step needs no host round trip.
+#include <cmath>
+
+#include "lhip_internal.h"
+#include "lhip_reduce.h"
+
+namespace lhip {
+namespace {
+
+constexpr int kRedThreads = 256;
+constexpr int kRedMaxBlocks = 1024;
+
+// partial[b] = sum of x^2 over block b's grid-stride share (double accumulation)
+__global__ void __launch_bounds__(kRedThreads)
+sumsq_stage1(const float* __restrict__ x, long long n, double* __restrict__ partial, int vec)
+{
+    __shared__ double red[kRedThreads / 64];
+    const long long stride = static_cast<long long>(gridDim.x) * kRedThreads;
+    const long long t0 = blockIdx.x * static_cast<long long>(kRedThreads) + threadIdx.x;
+    double s = 0.0;
+    if (vec) {
+        const float4* x4 = reinterpret_cast<const float4*>(x);
+        const long long n4 = n >> 2;
+        for (long long i = t0; i < n4; i += stride) {
+            const float4 v = x4[i];
+            s += static_cast<double>(v.x) * v.x + static_cast<double>(v.y) * v.y +
+                 static_cast<double>(v.z) * v.z + static_cast<double>(v.w) * v.w;
+        }
+        for (long long i = 4 * n4 + t0; i < n; i += stride) s += static_cast<double>(x[i]) * x[i];
+    } else {
+        for (long long i = t0; i < n; i += stride) s += static_cast<double>(x[i]) * x[i];
+    }
+    s = wave_sum(s);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double t = 0.0;
+        for (int i = 0; i < kRedThreads / 64; ++i) t += red[i];
+        partial[blockIdx.x] = t;
+    }
+}
+
+// out[0] = sum of partial[0..nb) in a fixed order
+__global__ void __launch_bounds__(64) sum_stage2(const double* __restrict__ partial, int nb, double* __restrict__ out)
+{
+    double s = 0.0;
+    for (int i = threadIdx.x; i < nb; i += 64) s += partial[i];
+    s = wave_sum(s);
+    if (threadIdx.x == 0) out[0] = s;
+}
+
+// One SGD step over n parameters with the LMTrain step logic.  sumsq is the
+// sum of squares of the RAW gradients; the norm of the scaled gradients is
+// grad_scale * sqrt(sumsq).  g is overwritten with the gradient actually used
+// (after scale and clip) so callers can inspect it, as optim2 mutates grads.
+__global__ void sgd_step_kernel(float* __restrict__ p, float* __restrict__ g, float* __restrict__ v, long long n,
+                                const double* __restrict__ sumsq, float lr, float momentum, float wd,
+                                float grad_scale, float clip_norm, int nesterov, float* __restrict__ gnorm_out,
+                                int* __restrict__ applied_out)
+{
+    const double norm = static_cast<double>(grad_scale) * sqrt(sumsq[0]);
+    const bool finite = isfinite(norm);
+    const long long t0 = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
+    if (t0 == 0) {
+        if (gnorm_out) gnorm_out[0] = static_cast<float>(norm);
+        if (applied_out) applied_out[0] = finite ? 1 : 0;
+    }
+    if (!finite) return;   // lmtrain.lua:1214-1218: skip the step
+    const float clipf = (clip_norm > 0.f && norm > clip_norm) ? static_cast<float>(clip_norm / norm) : 1.0f;
+    const long long stride = static_cast<long long>(gridDim.x) * blockDim.x;
+    for (long long i = t0; i < n; i += stride) {
+        float gk = g[i] * grad_scale;
+        if (clipf != 1.0f) gk = gk * clipf;
+        g[i] = gk;
+        if (wd != 0.f) gk = gk + wd * p[i];
+        if (momentum > 0.f) {
+            const float vk = momentum * v[i] + gk;
+            v[i] = vk;
+            p[i] = nesterov ? p[i] - lr * (gk + momentum * vk) : p[i] - lr * vk;
+        } else {
+            p[i] = p[i] - lr * gk;
+        }
+    }
+}
+
+// out[0] = scale * sum(x[0..n)) (float result from a double accumulation; single block)
+__global__ void __launch_bounds__(256) sum_f32_kernel(const float* __restrict__ x, int n, float scale, float* __restrict__ out)
+{
+    __shared__ double red[4];
+    double s = 0.0;
+    for (int i = threadIdx.x; i < n; i += 256) s += x[i];
+    s = wave_sum(s);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) out[0] = static_cast<float>((red[0] + red[1] + red[2] + red[3]) * scale);
+}
+
+}  // namespace
+
+int sumsq_blocks(long long n)
+{
+    long long b = (n + 4LL * kRedThreads - 1) / (4LL * kRedThreads);
+    if (b > kRedMaxBlocks) b = kRedMaxBlocks;
+    return static_cast<int>(b < 1 ? 1 : b);
+}
+
+int sumsq(const float* x, long long n, double* out, double* partial, int partial_len, hipStream_t s)
+{
+    if (n < 0) return fail(LHIP_E_SHAPE, "sumsq: n < 0");
+    if (!out) return fail(LHIP_E_NULL, "sumsq: out is NULL");
+    if (n > 0 && !x) return fail(LHIP_E_NULL, "sumsq: x is NULL");
+    const int nb = sumsq_blocks(n);
+    if (nb > partial_len) return fail(LHIP_E_CAPACITY, "sumsq: workspace %d < %d blocks", partial_len, nb);
+    sumsq_stage1<<<nb, kRedThreads, 0, s>>>(x, n, partial, aligned16(x) ? 1 : 0);
+    sum_stage2<<<1, 64, 0, s>>>(partial, nb, out);
+    return check_launch("sumsq");
+}
+
+int sgd_step(float* p, float* g, float* v, long long n, const double* sumsq_dev, float lr, float momentum,
+             float wd, float grad_scale, float clip_norm, int nesterov, float* gnorm_out, int* applied_out,
+             hipStream_t s)
+{
+    if (n < 0) return fail(LHIP_E_SHAPE, "sgd_step: n < 0");
+    if (!sumsq_dev) return fail(LHIP_E_NULL, "sgd_step: sumsq is NULL");
+    if (n > 0 && (!p || !g)) return fail(LHIP_E_NULL, "sgd_step: NULL params/grads");
+    if (momentum > 0.f && n > 0 && !v) return fail(LHIP_E_NULL, "sgd_step: momentum > 0 needs a velocity buffer");
+    const int cus = st().cu_count > 0 ? st().cu_count : 256;
+    long long blocks = (n + 255) / 256;
+    if (blocks > 4LL * cus) blocks = 4LL * cus;
+    if (blocks < 1) blocks = 1;
+    sgd_step_kernel<<<static_cast<int>(blocks), 256, 0, s>>>(p, g, v, n, sumsq_dev, lr, momentum, wd, grad_scale,
+                                                           clip_norm, nesterov, gnorm_out, applied_out);
+    return check_launch("sgd_step");
+}
+
+int sum_f32(const float* x, int n, float scale, float* out, hipStream_t s)
+{
+    if (n < 0) return fail(LHIP_E_SHAPE, "sum_f32: n < 0");
+    if (!out || (n > 0 && !x)) return fail(LHIP_E_NULL, "sum_f32: NULL pointer");
+    sum_f32_kernel<<<1, 256, 0, s>>>(x, n, scale, out);
+    return check_launch("sum_f32");
+}
+
+}  // namespace lhip
+
+using lhip::st;
+
+extern "C" {
+
+LHIP_API int lhip_sumsq(const float* x, long long n, double* out)
+{
+    LHIP_REQUIRE_READY();
+    double* partial = nullptr;
+    const int nb = lhip::sumsq_blocks(n);
+    int rc = lhip::workspace(static_cast<size_t>(nb) * sizeof(double), reinterpret_cast<void**>(&partial));
+    if (rc != LHIP_OK) return rc;
+    return lhip::sumsq(x, n, out, partial, nb, st().stream);
+}
+
+LHIP_API int lhip_sgd_step(float* params, float* grads, float* velocity, long long n, const double* grad_sumsq,
+                           float lr, float momentum, float weight_decay, float grad_scale, float clip_norm,
+                           int nesterov, float* grad_norm_out, int* applied_out)
+{
+    LHIP_REQUIRE_READY();
+    return lhip::sgd_step(params, grads, velocity, n, grad_sumsq, lr, momentum, weight_decay, grad_scale, clip_norm,
+                          nesterov, grad_norm_out, applied_out, st().stream);
+}
+
+LHIP_API int lhip_sum(const float* x, int n, float scale, float* out)
+{
+    LHIP_REQUIRE_READY();
+    return lhip::sum_f32(x, n, scale, out, st().stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,679 @@
+// lhip_rows.hip -- row-wise bandwidth kernels: RMSNorm fwd/bwd, row softmax fwd/bwd,
+// fused softmax + cross-entropy, row argmax.
+//
+// All are HBM-bound.  Rows up to a few thousand columns are held in registers
+// by one wave64 per row (float4 = 128-bit loads, NV float4 per lane), so each
+// input byte is read from HBM once and each output byte written once; the
+// reductions stay inside the wave (__shfl_xor butterflies lowered to DPP /
+// ds_swizzle).  Cross-entropy rows (V up to 32768) are held by a whole
+// workgroup.  Shapes outside the register-resident envelope, or unaligned
+// operands, take a generic multi-pass kernel with the same semantics.
+//
+// Semantics follow ai/core/tensor2.lua (the CPU LMTrain path):
+//   rmsnorm  :609-666   softmax_rows :332-408   cross_entropy :809-882
+// and the reference kernels' batched contracts (cuda/luaTL_train.cu):
+//   softmax_ex group-causal mask :545-619, fused CE :837-891, argmax :982-1018.
+#include <cmath>
+
+#include "lhip_internal.h"
+#include "lhip_reduce.h"
+
+namespace lhip {
+namespace {
+
+constexpr int kRowThreads = 256;  // 4 waves, one row each
+constexpr int kWavesPerBlock = kRowThreads / 64;
+
+__device__ __forceinline__ float4 f4zero() { return make_float4(0.f, 0.f, 0.f, 0.f); }
+
+__device__ __forceinline__ float f4get(const float4& v, int e)
+{
+    return e == 0 ? v.x : (e == 1 ? v.y : (e == 2 ? v.z : v.w));
+}
+
+__device__ __forceinline__ void f4set(float4& v, int e, float x)
+{
+    if (e == 0) v.x = x; else if (e == 1) v.y = x; else if (e == 2) v.z = x; else v.w = x;
+}
+
+// ------------------------------------------------------------------ RMSNorm
+// y = x * r * w, r = 1/sqrt(mean_j x^2 + eps); inv[row] = r (tensor2.lua:609-634).
+template <int NV>
+__global__ void __launch_bounds__(kRowThreads)
+rmsnorm_fwd_vec(const float* __restrict__ x, const float* __restrict__ w, float* __restrict__ y,
+                float* __restrict__ inv, int rows, int cols, float eps)
+{
+    const int row = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const int c4n = cols >> 2;
+    const float4* xr = reinterpret_cast<const float4*>(x + static_cast<size_t>(row) * cols);
+    const float4* w4 = reinterpret_cast<const float4*>(w);
+    float4 v[NV];
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int c = lane + 64 * i;
+        v[i] = c < c4n ? xr[c] : f4zero();
+        ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
+    }
+    ss = wave_sum(ss);
+    const float r = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
+    float4* yr = reinterpret_cast<float4*>(y + static_cast<size_t>(row) * cols);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int c = lane + 64 * i;
+        if (c < c4n) {
+            const float4 g = w4[c];
+            yr[c] = make_float4(v[i].x * r * g.x, v[i].y * r * g.y, v[i].z * r * g.z, v[i].w * r * g.w);
+        }
+    }
+    if (inv && lane == 0) inv[row] = r;
+}
+
+__global__ void __launch_bounds__(kRowThreads)
+rmsnorm_fwd_generic(const float* __restrict__ x, const float* __restrict__ w, float* __restrict__ y,
+                    float* __restrict__ inv, int rows, int cols, float eps)
+{
+    const int row = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float* xr = x + static_cast<size_t>(row) * cols;
+    float ss = 0.f;
+    for (int c = lane; c < cols; c += 64) ss += xr[c] * xr[c];
+    ss = wave_sum(ss);
+    const float r = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
+    float* yr = y + static_cast<size_t>(row) * cols;
+    for (int c = lane; c < cols; c += 64) yr[c] = xr[c] * r * w[c];
+    if (inv && lane == 0) inv[row] = r;
+}
+
+// dx = g*w*r - x*(r^3/N)*sum_j(g_j w_j x_j)  (+ dx if acc);
+// per-block partial dw over the block's rows -> partial[block][cols]
+// (tensor2.lua:641-666).  Rows are walked grid-stride, one wave per row.
+template <int NV>
+__global__ void __launch_bounds__(kRowThreads)
+rmsnorm_bwd_vec(const float* __restrict__ x, const float* __restrict__ w, const float* __restrict__ inv,
+                const float* __restrict__ dy, float* __restrict__ dx, float* __restrict__ partial,
+                int rows, int cols, int acc_dx)
+{
+    extern __shared__ float4 sdw[];   // [kWavesPerBlock][cols/4]
+    const int wv = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int c4n = cols >> 2;
+    const float4* w4 = reinterpret_cast<const float4*>(w);
+    float4 wr[NV], dwp[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int c = lane + 64 * i;
+        wr[i] = c < c4n ? w4[c] : f4zero();
+        dwp[i] = f4zero();
+    }
+    const float inv_n = 1.0f / static_cast<float>(cols);
+    for (int row = blockIdx.x * kWavesPerBlock + wv; row < rows; row += gridDim.x * kWavesPerBlock) {
+        const size_t base = static_cast<size_t>(row) * cols;
+        const float4* xr = reinterpret_cast<const float4*>(x + base);
+        const float4* gr = reinterpret_cast<const float4*>(dy + base);
+        float4 xv[NV], gv[NV];
+        float dot = 0.f;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int c = lane + 64 * i;
+            xv[i] = c < c4n ? xr[c] : f4zero();
+            gv[i] = c < c4n ? gr[c] : f4zero();
+            dot += gv[i].x * wr[i].x * xv[i].x + gv[i].y * wr[i].y * xv[i].y +
+                   gv[i].z * wr[i].z * xv[i].z + gv[i].w * wr[i].w * xv[i].w;
+        }
+        dot = wave_sum(dot);
+        const float r = inv[row];
+        const float coef = dot * r * r * r * inv_n;
+        float4* dxr = reinterpret_cast<float4*>(dx + base);
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int c = lane + 64 * i;
+            if (c < c4n) {
+                float4 o;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float gg = f4get(gv[i], e), xx = f4get(xv[i], e);
+                    f4set(o, e, gg * f4get(wr[i], e) * r - xx * coef);
+                    f4set(dwp[i], e, f4get(dwp[i], e) + gg * xx * r);
+                }
+                if (acc_dx) {
+                    const float4 old = dxr[c];
+                    o.x += old.x; o.y += old.y; o.z += old.z; o.w += old.w;
+                }
+                dxr[c] = o;
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int c = lane + 64 * i;
+        if (c < c4n) sdw[wv * c4n + c] = dwp[i];
+    }
+    __syncthreads();
+    float4* pr = reinterpret_cast<float4*>(partial + static_cast<size_t>(blockIdx.x) * cols);
+    for (int c = threadIdx.x; c < c4n; c += kRowThreads) {
+        float4 s = sdw[c];
+#pragma unroll
+        for (int k = 1; k < kWavesPerBlock; ++k) {
+            const float4 t = sdw[k * c4n + c];
+            s.x += t.x; s.y += t.y; s.z += t.z; s.w += t.w;
+        }
+        pr[c] = s;
+    }
+}
+
+__global__ void __launch_bounds__(kRowThreads)
+rmsnorm_bwd_generic(const float* __restrict__ x, const float* __restrict__ w, const float* __restrict__ inv,
+                    const float* __restrict__ dy, float* __restrict__ dx, float* __restrict__ partial,
+                    int rows, int cols, int acc_dx)
+{
+    // one wave per row, rows grid-stride; dw partial per block accumulated
+    // column by column through LDS-free atomics-free passes: each wave owns
+    // its partial row in `partial` ([gridDim.x * waves][cols]).
+    const int wv = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int gw = blockIdx.x * kWavesPerBlock + wv;
+    float* pw = partial + static_cast<size_t>(gw) * cols;
+    for (int c = lane; c < cols; c += 64) pw[c] = 0.f;
+    const float inv_n = 1.0f / static_cast<float>(cols);
+    for (int row = gw; row < rows; row += gridDim.x * kWavesPerBlock) {
+        const size_t base = static_cast<size_t>(row) * cols;
+        float dot = 0.f;
+        for (int c = lane; c < cols; c += 64) dot += dy[base + c] * w[c] * x[base + c];
+        dot = wave_sum(dot);
+        const float r = inv[row];
+        const float coef = dot * r * r * r * inv_n;
+        for (int c = lane; c < cols; c += 64) {
+            const float gg = dy[base + c], xx = x[base + c];
+            const float o = gg * w[c] * r - xx * coef;
+            dx[base + c] = acc_dx ? dx[base + c] + o : o;
+            pw[c] += gg * xx * r;
+        }
+    }
+}
+
+// dw[c] = (acc ? dw[c] : 0) + sum_b partial[b][c], b ascending (deterministic).
+__global__ void __launch_bounds__(256)
+colsum_kernel(const float* __restrict__ partial, float* __restrict__ out, int nparts, int cols, int acc)
+{
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= cols) return;
+    float s = 0.f;
+    for (int b = 0; b < nparts; ++b) s += partial[static_cast<size_t>(b) * cols + c];
+    out[c] = acc ? out[c] + s : s;
+}
+
+// ------------------------------------------------------------- row softmax
+// Row r keeps columns [0, lim): lim = cols, or with the (group-)causal mask
+// lim = clamp((r % group) + 1 + offset, 1, cols) (tensor2.lua:332-383 with
+// Lua's 1-based lim = i + offset; luaTL_softmax_ex's row % group).  Masked
+// entries are exactly 0.  y = softmax(scale * x) over the kept prefix.
+__device__ __forceinline__ int softmax_lim(int row, int cols, int causal, int offset, int group)
+{
+    if (!causal) return cols;
+    int lim = (row % group) + 1 + offset;
+    return lim < 1 ? 1 : (lim > cols ? cols : lim);
+}
+
+template <int NV>
+__global__ void __launch_bounds__(kRowThreads)
+softmax_fwd_vec(const float* __restrict__ x, float* __restrict__ y, int rows, int cols, float scale,
+                int causal, int offset, int group)
+{
+    const int row = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const int lim = softmax_lim(row, cols, causal, offset, group);
+    const int c4n = cols >> 2;
+    const float4* xr = reinterpret_cast<const float4*>(x + static_cast<size_t>(row) * cols);
+    float4 v[NV];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int c = lane + 64 * i;
+        const float4 t = (c < c4n && 4 * c < lim) ? xr[c] : f4zero();
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float s = (4 * c + e < lim) ? scale * f4get(t, e) : -INFINITY;
+            f4set(v[i], e, s);
+            mx = fmaxf(mx, s);
+        }
+    }
+    mx = wave_max(mx);
+    if (mx == -INFINITY || mx != mx) mx = 0.f;
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int c = lane + 64 * i;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float ev = (4 * c + e < lim) ? expf(f4get(v[i], e) - mx) : 0.f;
+            f4set(v[i], e, ev);
+            sum += ev;
+        }
+    }
+    sum = wave_sum(sum);
+    if (!(sum > 0.f)) sum = 1.f;
+    const float is = 1.0f / sum;
+    float4* yr = reinterpret_cast<float4*>(y + static_cast<size_t>(row) * cols);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int c = lane + 64 * i;
+        if (c < c4n) yr[c] = make_float4(v[i].x * is, v[i].y * is, v[i].z * is, v[i].w * is);
+    }
+}
+
+__global__ void __launch_bounds__(kRowThreads)
+softmax_fwd_generic(const float* __restrict__ x, float* __restrict__ y, int rows, int cols, float scale,
+                    int causal, int offset, int group)
+{
+    const int row = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const int lim = softmax_lim(row, cols, causal, offset, group);
+    const float* xr = x + static_cast<size_t>(row) * cols;
+    float* yr = y + static_cast<size_t>(row) * cols;
+    float mx = -INFINITY;
+    for (int c = lane; c < lim; c += 64) mx = fmaxf(mx, scale * xr[c]);
+    mx = wave_max(mx);
+    if (mx == -INFINITY || mx != mx) mx = 0.f;
+    float sum = 0.f;
+    for (int c = lane; c < lim; c += 64) sum += expf(scale * xr[c] - mx);
+    sum = wave_sum(sum);
+    if (!(sum > 0.f)) sum = 1.f;
+    const float is = 1.0f / sum;
+    for (int c = lane; c < cols; c += 64) yr[c] = c < lim ? expf(scale * xr[c] - mx) * is : 0.f;
+}
+
+// dx = scale * y * (dy - sum_{j<lim} dy_j y_j) on the kept prefix, 0 beyond
+// (+ dx if acc) (tensor2.lua:388-408 followed by the scale node's backward).
+template <int NV>
+__global__ void __launch_bounds__(kRowThreads)
+softmax_bwd_vec(const float* __restrict__ y, const float* __restrict__ dy, float* __restrict__ dx,
+                int rows, int cols, float scale, int causal, int offset, int group, int acc)
+{
+    const int row = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const int lim = softmax_lim(row, cols, causal, offset, group);
+    const int c4n = cols >> 2;
+    const size_t base = static_cast<size_t>(row) * cols;
+    const float4* yr = reinterpret_cast<const float4*>(y + base);
+    const float4* gr = reinterpret_cast<const float4*>(dy + base);
+    float4 yv[NV], gv[NV];
+    float dot = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int c = lane + 64 * i;
+        const bool in = c < c4n && 4 * c < lim;
+        yv[i] = in ? yr[c] : f4zero();
+        gv[i] = in ? gr[c] : f4zero();
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (4 * c + e < lim) dot += f4get(gv[i], e) * f4get(yv[i], e);
+    }
+    dot = wave_sum(dot);
+    float4* dr = reinterpret_cast<float4*>(dx + base);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int c = lane + 64 * i;
+        if (c < c4n) {
+            float4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                f4set(o, e, (4 * c + e < lim) ? scale * (f4get(yv[i], e) * (f4get(gv[i], e) - dot)) : 0.f);
+            if (acc) {
+                const float4 old = dr[c];
+                o.x += old.x; o.y += old.y; o.z += old.z; o.w += old.w;
+            }
+            dr[c] = o;
+        }
+    }
+}
+
+__global__ void __launch_bounds__(kRowThreads)
+softmax_bwd_generic(const float* __restrict__ y, const float* __restrict__ dy, float* __restrict__ dx,
+                    int rows, int cols, float scale, int causal, int offset, int group, int acc)
+{
+    const int row = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const int lim = softmax_lim(row, cols, causal, offset, group);
+    const size_t base = static_cast<size_t>(row) * cols;
+    float dot = 0.f;
+    for (int c = lane; c < lim; c += 64) dot += dy[base + c] * y[base + c];
+    dot = wave_sum(dot);
+    for (int c = lane; c < cols; c += 64) {
+        const float o = c < lim ? scale * (y[base + c] * (dy[base + c] - dot)) : 0.f;
+        dx[base + c] = acc ? dx[base + c] + o : o;
+    }
+}
+
+// ------------------------------------------------- fused softmax + cross-entropy
+// Per row r with target t: rows with t < 0, t >= V or t == ignore_index give
+// loss 0 and dlogits 0; otherwise loss[r] = logsumexp(x) - x[t] and
+// dlogits = gscale * (softmax(x) - onehot(t)).  dlogits may alias logits.
+// (tensor2.lua:809-882 per row; cuda/luaTL_train.cu:837-878 contract.)
+template <int NT, int NV>
+__global__ void __launch_bounds__(NT)
+ce_fused_vec(const float* __restrict__ logits, const int* __restrict__ tgt, float* __restrict__ losses,
+             float* dlogits, int rows, int V, int ignore_index, float gscale)
+{
+    constexpr int NW = NT / 64;
+    __shared__ float red[NW];
+    const int row = blockIdx.x;
+    const int t = tgt[row];
+    const size_t base = static_cast<size_t>(row) * V;
+    const int c4n = V >> 2;
+    if (t < 0 || t >= V || t == ignore_index) {
+        if (losses && threadIdx.x == 0) losses[row] = 0.f;
+        if (dlogits) {
+            float4* dr = reinterpret_cast<float4*>(dlogits + base);
+            for (int c = threadIdx.x; c < c4n; c += NT) dr[c] = f4zero();
+        }
+        return;
+    }
+    const float xt = logits[base + t];   // read before any thread writes dlogits
+    const float4* xr = reinterpret_cast<const float4*>(logits + base);
+    float4 v[NV];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int c = threadIdx.x + NT * i;
+        v[i] = c < c4n ? xr[c] : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+        mx = fmaxf(mx, fmaxf(fmaxf(v[i].x, v[i].y), fmaxf(v[i].z, v[i].w)));
+    }
+    mx = block_max<NW>(mx, red);
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int c = threadIdx.x + NT * i;
+        if (c < c4n) {
+            v[i].x = expf(v[i].x - mx); v[i].y = expf(v[i].y - mx);
+            v[i].z = expf(v[i].z - mx); v[i].w = expf(v[i].w - mx);
+            sum += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+        }
+    }
+    sum = block_sum<NW>(sum, red);
+    if (losses && threadIdx.x == 0) losses[row] = (mx + logf(sum)) - xt;
+    if (dlogits) {
+        const float is = 1.0f / sum;
+        float4* dr = reinterpret_cast<float4*>(dlogits + base);
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int c = threadIdx.x + NT * i;
+            if (c < c4n) {
+                float4 o;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float p = f4get(v[i], e) * is;
+                    if (4 * c + e == t) p -= 1.f;
+                    f4set(o, e, gscale * p);
+                }
+                dr[c] = o;
+            }
+        }
+    }
+}
+
+__global__ void __launch_bounds__(256)
+ce_fused_generic(const float* __restrict__ logits, const int* __restrict__ tgt, float* __restrict__ losses,
+                 float* dlogits, int rows, int V, int ignore_index, float gscale)
+{
+    __shared__ float red[4];
+    const int row = blockIdx.x;
+    const int t = tgt[row];
+    const size_t base = static_cast<size_t>(row) * V;
+    if (t < 0 || t >= V || t == ignore_index) {
+        if (losses && threadIdx.x == 0) losses[row] = 0.f;
+        if (dlogits) for (int c = threadIdx.x; c < V; c += 256) dlogits[base + c] = 0.f;
+        return;
+    }
+    const float xt = logits[base + t];
+    float mx = -INFINITY;
+    for (int c = threadIdx.x; c < V; c += 256) mx = fmaxf(mx, logits[base + c]);
+    mx = block_max<4>(mx, red);
+    float sum = 0.f;
+    for (int c = threadIdx.x; c < V; c += 256) sum += expf(logits[base + c] - mx);
+    sum = block_sum<4>(sum, red);
+    if (losses && threadIdx.x == 0) losses[row] = (mx + logf(sum)) - xt;
+    if (dlogits) {
+        const float is = 1.0f / sum;
+        // every element is read before the same thread overwrites it
+        for (int c = threadIdx.x; c < V; c += 256) {
+            float p = expf(logits[base + c] - mx) * is;
+            if (c == t) p -= 1.f;
+            dlogits[base + c] = gscale * p;
+        }
+    }
+}
+
+// ------------------------------------------------------------------ argmax
+// First index of the row maximum under a strict '>' scan from -inf: NaN never
+// wins, ties go to the lowest index, a row of only -inf/NaN gives 0
+// (lmtrain.lua:1200-1209; cuda/luaTL_train.cu:982-1018).  Bit-exact.
+__global__ void __launch_bounds__(kRowThreads)
+argmax_rows_kernel(const float* __restrict__ x, int* __restrict__ out, int rows, int cols)
+{
+    const int row = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float* xr = x + static_cast<size_t>(row) * cols;
+    float bv = -INFINITY;
+    int bi = -1;
+    for (int c = lane; c < cols; c += 64) {
+        const float v = xr[c];
+        if (v > bv) { bv = v; bi = c; }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        const bool take = (oi >= 0) && (bi < 0 || ov > bv || (ov == bv && oi < bi));
+        if (take) { bv = ov; bi = oi; }
+    }
+    if (lane == 0) out[row] = bi < 0 ? 0 : bi;
+}
+
+int nv_for(int cols)  // float4 per lane needed for a wave-resident row
+{
+    const int per_lane = (cols + 255) / 256;
+    if (per_lane <= 1) return 1;
+    if (per_lane <= 2) return 2;
+    if (per_lane <= 4) return 4;
+    if (per_lane <= 8) return 8;
+    if (per_lane <= 16) return 16;
+    return 0;
+}
+
+inline int row_blocks(int rows) { return ceil_div(rows, kWavesPerBlock); }
+
+}  // namespace
+
+// ------------------------------------------------------------------ launchers
+int rmsnorm_fwd(const float* x, const float* w, float* y, float* inv, int rows, int cols, float eps,
+                hipStream_t s)
+{
+    if (rows < 0 || cols <= 0) return fail(LHIP_E_SHAPE, "rmsnorm_fwd: rows=%d cols=%d", rows, cols);
+    if (rows == 0) return LHIP_OK;
+    if (!x || !w || !y) return fail(LHIP_E_NULL, "rmsnorm_fwd: NULL x/w/y");
+    if (!(eps >= 0.f)) return fail(LHIP_E_ARG, "rmsnorm_fwd: eps must be >= 0");
+    const int nv = nv_for(cols);
+    const bool vec = nv && cols % 4 == 0 && aligned16(x) && aligned16(w) && aligned16(y);
+    dim3 g(row_blocks(rows)), b(kRowThreads);
+    if (!vec) rmsnorm_fwd_generic<<<g, b, 0, s>>>(x, w, y, inv, rows, cols, eps);
+    else if (nv == 1) rmsnorm_fwd_vec<1><<<g, b, 0, s>>>(x, w, y, inv, rows, cols, eps);
+    else if (nv == 2) rmsnorm_fwd_vec<2><<<g, b, 0, s>>>(x, w, y, inv, rows, cols, eps);
+    else if (nv == 4) rmsnorm_fwd_vec<4><<<g, b, 0, s>>>(x, w, y, inv, rows, cols, eps);
+    else if (nv == 8) rmsnorm_fwd_vec<8><<<g, b, 0, s>>>(x, w, y, inv, rows, cols, eps);
+    else rmsnorm_fwd_vec<16><<<g, b, 0, s>>>(x, w, y, inv, rows, cols, eps);
+    return check_launch("rmsnorm_fwd");
+}
+
+// Upper bound on the partial-dw rows the backward uses (workspace = parts * cols
+// floats): one per block on the register-resident path, one per wave otherwise.
+int rmsnorm_bwd_parts(int rows, int cols)
+{
+    (void)cols;
+    const int cus = st().cu_count > 0 ? st().cu_count : 256;
+    int blocks = row_blocks(rows);
+    if (blocks > cus) blocks = cus;
+    return blocks * kWavesPerBlock;
+}
+
+int rmsnorm_bwd(const float* x, const float* w, const float* inv, const float* dy, float* dx, float* dw,
+                int rows, int cols, int accumulate, float* work, size_t work_floats, hipStream_t s)
+{
+    if (rows < 0 || cols <= 0) return fail(LHIP_E_SHAPE, "rmsnorm_bwd: rows=%d cols=%d", rows, cols);
+    if (rows == 0) return LHIP_OK;
+    if (!x || !w || !inv || !dy || !dx) return fail(LHIP_E_NULL, "rmsnorm_bwd: NULL argument");
+    const int cus = st().cu_count > 0 ? st().cu_count : 256;
+    int blocks = row_blocks(rows);
+    if (blocks > cus) blocks = cus;
+    const int nv = nv_for(cols);
+    const bool vec = nv && cols % 4 == 0 && aligned16(x) && aligned16(w) && aligned16(dy) && aligned16(dx);
+    const int parts = vec ? blocks : blocks * kWavesPerBlock;
+    if (dw && static_cast<size_t>(parts) * cols > work_floats)
+        return fail(LHIP_E_CAPACITY, "rmsnorm_bwd: workspace of %zu floats < %lld needed", work_floats,
+                    static_cast<long long>(parts) * cols);
+    float* partial = work;
+    dim3 g(blocks), b(kRowThreads);
+    const size_t lds = static_cast<size_t>(kWavesPerBlock) * cols * sizeof(float);
+    if (!vec) rmsnorm_bwd_generic<<<g, b, 0, s>>>(x, w, inv, dy, dx, partial, rows, cols, accumulate);
+    else if (nv == 1) rmsnorm_bwd_vec<1><<<g, b, lds, s>>>(x, w, inv, dy, dx, partial, rows, cols, accumulate);
+    else if (nv == 2) rmsnorm_bwd_vec<2><<<g, b, lds, s>>>(x, w, inv, dy, dx, partial, rows, cols, accumulate);
+    else if (nv == 4) rmsnorm_bwd_vec<4><<<g, b, lds, s>>>(x, w, inv, dy, dx, partial, rows, cols, accumulate);
+    else if (nv == 8) rmsnorm_bwd_vec<8><<<g, b, lds, s>>>(x, w, inv, dy, dx, partial, rows, cols, accumulate);
+    else rmsnorm_bwd_vec<16><<<g, b, lds, s>>>(x, w, inv, dy, dx, partial, rows, cols, accumulate);
+    int rc = check_launch("rmsnorm_bwd");
+    if (rc != LHIP_OK || !dw) return rc;
+    colsum_kernel<<<ceil_div(cols, 256), 256, 0, s>>>(partial, dw, parts, cols, accumulate);
+    return check_launch("rmsnorm_bwd: dw reduce");
+}
+
+int softmax_fwd(const float* x, float* y, int rows, int cols, float scale, int causal, int offset, int group,
+                hipStream_t s)
+{
+    if (rows < 0 || cols <= 0) return fail(LHIP_E_SHAPE, "softmax_fwd: rows=%d cols=%d", rows, cols);
+    if (rows == 0) return LHIP_OK;
+    if (!x || !y) return fail(LHIP_E_NULL, "softmax_fwd: NULL x/y");
+    if (group <= 0) group = rows;
+    const int nv = nv_for(cols);
+    const bool vec = nv && cols % 4 == 0 && aligned16(x) && aligned16(y);
+    dim3 g(row_blocks(rows)), b(kRowThreads);
+#define LHIP_SMF(NV_) softmax_fwd_vec<NV_><<<g, b, 0, s>>>(x, y, rows, cols, scale, causal, offset, group)
+    if (!vec) softmax_fwd_generic<<<g, b, 0, s>>>(x, y, rows, cols, scale, causal, offset, group);
+    else if (nv == 1) LHIP_SMF(1);
+    else if (nv == 2) LHIP_SMF(2);
+    else if (nv == 4) LHIP_SMF(4);
+    else if (nv == 8) LHIP_SMF(8);
+    else LHIP_SMF(16);
+#undef LHIP_SMF
+    return check_launch("softmax_fwd");
+}
+
+int softmax_bwd(const float* y, const float* dy, float* dx, int rows, int cols, float scale, int causal,
+                int offset, int group, int accumulate, hipStream_t s)
+{
+    if (rows < 0 || cols <= 0) return fail(LHIP_E_SHAPE, "softmax_bwd: rows=%d cols=%d", rows, cols);
+    if (rows == 0) return LHIP_OK;
+    if (!y || !dy || !dx) return fail(LHIP_E_NULL, "softmax_bwd: NULL y/dy/dx");
+    if (group <= 0) group = rows;
+    const int nv = nv_for(cols);
+    const bool vec = nv && cols % 4 == 0 && aligned16(y) && aligned16(dy) && aligned16(dx);
+    dim3 g(row_blocks(rows)), b(kRowThreads);
+#define LHIP_SMB(NV_) softmax_bwd_vec<NV_><<<g, b, 0, s>>>(y, dy, dx, rows, cols, scale, causal, offset, group, accumulate)
+    if (!vec) softmax_bwd_generic<<<g, b, 0, s>>>(y, dy, dx, rows, cols, scale, causal, offset, group, accumulate);
+    else if (nv == 1) LHIP_SMB(1);
+    else if (nv == 2) LHIP_SMB(2);
+    else if (nv == 4) LHIP_SMB(4);
+    else if (nv == 8) LHIP_SMB(8);
+    else LHIP_SMB(16);
+#undef LHIP_SMB
+    return check_launch("softmax_bwd");
+}
+
+int ce_fused(const float* logits, const int* tgt, float* losses, float* dlogits, int rows, int V,
+             int ignore_index, float gscale, hipStream_t s)
+{
+    if (rows < 0 || V <= 0) return fail(LHIP_E_SHAPE, "ce_fused: rows=%d vocab=%d", rows, V);
+    if (rows == 0) return LHIP_OK;
+    if (!logits || !tgt) return fail(LHIP_E_NULL, "ce_fused: NULL logits/targets");
+    const bool vec = V % 4 == 0 && aligned16(logits) && (!dlogits || aligned16(dlogits));
+    if (vec && V <= 256 * 4 * 2)
+        ce_fused_vec<256, 2><<<rows, 256, 0, s>>>(logits, tgt, losses, dlogits, rows, V, ignore_index, gscale);
+    else if (vec && V <= 256 * 4 * 8)
+        ce_fused_vec<256, 8><<<rows, 256, 0, s>>>(logits, tgt, losses, dlogits, rows, V, ignore_index, gscale);
+    else if (vec && V <= 1024 * 4 * 8)
+        ce_fused_vec<1024, 8><<<rows, 1024, 0, s>>>(logits, tgt, losses, dlogits, rows, V, ignore_index, gscale);
+    else
+        ce_fused_generic<<<rows, 256, 0, s>>>(logits, tgt, losses, dlogits, rows, V, ignore_index, gscale);
+    return check_launch("ce_fused");
+}
+
+int argmax_rows(const float* x, int* out, int rows, int cols, hipStream_t s)
+{
+    if (rows < 0 || cols <= 0) return fail(LHIP_E_SHAPE, "argmax_rows: rows=%d cols=%d", rows, cols);
+    if (rows == 0) return LHIP_OK;
+    if (!x || !out) return fail(LHIP_E_NULL, "argmax_rows: NULL x/out");
+    argmax_rows_kernel<<<row_blocks(rows), kRowThreads, 0, s>>>(x, out, rows, cols);
+    return check_launch("argmax_rows");
+}
+
+}  // namespace lhip
+
+using lhip::st;
+
+extern "C" {
+
+LHIP_API int lhip_rmsnorm_fwd(const float* x, const float* w, float* y, float* inv, int rows, int cols, float eps)
+{
+    LHIP_REQUIRE_READY();
+    return lhip::rmsnorm_fwd(x, w, y, inv, rows, cols, eps, st().stream);
+}
+
+LHIP_API int lhip_rmsnorm_bwd(const float* x, const float* w, const float* inv, const float* dy,
+                              float* dx, float* dw, int rows, int cols, int accumulate)
+{
+    LHIP_REQUIRE_READY();
+    if (rows < 0 || cols <= 0) return lhip::fail(LHIP_E_SHAPE, "rmsnorm_bwd: rows=%d cols=%d", rows, cols);
+    float* work = nullptr;
+    const size_t need = static_cast<size_t>(lhip::rmsnorm_bwd_parts(rows, cols)) * cols;
+    if (dw && rows > 0) {
+        int rc = lhip::workspace(need * sizeof(float), reinterpret_cast<void**>(&work));
+        if (rc != LHIP_OK) return rc;
+    }
+    return lhip::rmsnorm_bwd(x, w, inv, dy, dx, dw, rows, cols, accumulate, work, need, st().stream);
+}
+
+LHIP_API int lhip_softmax_fwd(const float* x, float* y, int rows, int cols, float scale, int causal,
+                              int offset, int group)
+{
+    LHIP_REQUIRE_READY();
+    return lhip::softmax_fwd(x, y, rows, cols, scale, causal, offset, group, st().stream);
+}
+
+LHIP_API int lhip_softmax_bwd(const float* y, const float* dy, float* dx, int rows, int cols, float scale,
+                              int causal, int offset, int group, int accumulate)
+{
+    LHIP_REQUIRE_READY();
+    return lhip::softmax_bwd(y, dy, dx, rows, cols, scale, causal, offset, group, accumulate, st().stream);
+}
+
+LHIP_API int lhip_ce_fused(const float* logits, const int* targets, float* losses, float* dlogits,
+                           int rows, int vocab, int ignore_index, float grad_scale)
+{
+    LHIP_REQUIRE_READY();
+    return lhip::ce_fused(logits, targets, losses, dlogits, rows, vocab, ignore_index, grad_scale, st().stream);
+}
+
+LHIP_API int lhip_argmax_rows(const float* x, int* out, int rows, int cols)
+{
+    LHIP_REQUIRE_READY();
+    return lhip::argmax_rows(x, out, rows, cols, st().stream);
+}
+
+}  // extern "C"
