@@ -145,7 +145,8 @@ LHIP_API int lhip_rmsnorm_fwd(const float* x, const float* w, float* y, float* i
  * (ai/core/tensor2.lua:641-666); replaces luaTL_rmsnorm_bwd (cuda/luaTL_train.cu:1096-1106). */
 LHIP_API int lhip_rmsnorm_bwd(const float* x, const float* w, const float* inv, const float* dy,
                               float* dx, float* dw, int rows, int cols, int accumulate);
-/* y = softmax(scale * x) over the kept prefix of each row, 0 beyond it.  Without
+/* y = softmax(scale * x) over the kept prefix of each row, 0 beyond it (x and y
+ * must not overlap; likewise y, dy and dx in the backward).  Without
  * `causal` the whole row is kept; with it row r keeps
  * min(max((r % group) + 1 + offset, 1), cols) columns (group <= 0 means rows).
  * CPU: Tensor.scale + Tensor.softmax_rows (ai/core/tensor2.lua:185-196, 332-383);
@@ -223,6 +224,60 @@ LHIP_API int lhip_sgd_step(float* params, float* grads, float* velocity, long lo
                            const double* grad_sumsq, float lr, float momentum, float weight_decay,
                            float grad_scale, float clip_norm, int nesterov,
                            float* grad_norm_out, int* applied_out);
+
+/* ---- the CPU LMTrain step, resident on the GPU ------------------------------
+ * One optimizer step of LMTrain with optimizer = "sgd" over `batch` windows of
+ * `seq` tokens, with the CPU path's model (ai/nn/transformer.lua:84-257:
+ * separate wq/wk/wv and w1/w3/w2, interleaved RoPE, tied head) and step logic
+ * (ai/optim/lmtrain.lua:1183-1227: per-window mean CE, grads summed over
+ * windows and scaled by 1/batch, global-norm skip and clip, SGD with momentum
+ * and weight decay, ai/optim/optim2.lua:48-102).  Parameters are one flat fp32
+ * vector in Transformer:parameters() order (ai/nn/transformer.lua:150-164):
+ * emb, {ln1, wq, wk, wv, wo, ln2, w1, w3, w2} per layer, lnf.  The model owns
+ * every device buffer; a step enqueues everything on the library stream with
+ * no host round trip and no allocation (optionally as a replayed hipGraph).
+ * The reference offers this only as Lua orchestration over luaTL calls; it has
+ * no single C entry point for it. */
+typedef struct {
+    int vocab, dim, layers, heads, ffn;
+    int causal;          /* transformer.lua:93 (default 1) */
+    double eps;          /* RMSNorm eps, transformer.lua:98 (1e-5) */
+    double rope_base;    /* transformer.lua:95 (10000) */
+    int batch;           /* windows per optimizer step (LMTrain batch_size) */
+    int seq;             /* tokens per window (LMTrain max_seq) */
+} lhip_lm_config_t;
+
+typedef struct {
+    float loss;          /* mean over windows of each window's mean CE */
+    float grad_norm;     /* global norm of the 1/batch-scaled grads, before clipping */
+    int applied;         /* 1 when the update ran (finite norm), else 0 */
+    int correct;         /* argmax hits over the batch*seq targets */
+    int steps;           /* steps enqueued since creation */
+} lhip_lm_stats_t;
+
+/* Number of parameters (-1 on a bad config) and each tensor's offset/shape
+ * (2 + 9*layers tensors; any output may be NULL). */
+LHIP_API long long lhip_lm_num_params(const lhip_lm_config_t* cfg);
+LHIP_API int lhip_lm_param_offsets(const lhip_lm_config_t* cfg, long long* offsets, int* rows, int* cols);
+LHIP_API int lhip_lm_create(const lhip_lm_config_t* cfg, void** model);
+LHIP_API int lhip_lm_destroy(void* model);
+/* Synchronous copies of the flat parameter / gradient / velocity vectors. */
+LHIP_API int lhip_lm_set_params(void* model, const float* host, long long n);
+LHIP_API int lhip_lm_get_params(void* model, float* host, long long n);
+LHIP_API int lhip_lm_get_grads(void* model, float* host, long long n);
+LHIP_API int lhip_lm_set_velocity(void* model, const float* host, long long n);
+LHIP_API int lhip_lm_get_velocity(void* model, float* host, long long n);
+/* Token ids and next-token targets, batch*seq each, 0-based, row b*seq + t. */
+LHIP_API int lhip_lm_set_batch(void* model, const int* ids, const int* targets);
+/* Capture the step into a hipGraph on the next call and replay it afterwards. */
+LHIP_API int lhip_lm_use_graph(void* model, int on);
+/* Enqueue one step (asynchronous). */
+LHIP_API int lhip_lm_step_sgd(void* model, float lr, float momentum, float weight_decay, float clip_norm,
+                              int nesterov);
+/* Wait and report the last step; window_losses (may be NULL) gets `batch` values. */
+LHIP_API int lhip_lm_stats(void* model, lhip_lm_stats_t* out, float* window_losses, int nwin);
+/* Row argmax of the last step's logits (batch*seq int32). */
+LHIP_API int lhip_lm_get_argmax(void* model, int* host, int n);
 
 #ifdef __cplusplus
 }

@@ -79,6 +79,38 @@ SIGNATURES = {
     "lhip_sgd_step": (_i, [_p, _p, _p, _ll, _p, _f, _f, _f, _f, _f, _i, _p, _p]),
 }
 
+class LmConfig(ctypes.Structure):
+    """lhip_lm_config_t"""
+    _fields_ = [("vocab", ctypes.c_int), ("dim", ctypes.c_int), ("layers", ctypes.c_int),
+                ("heads", ctypes.c_int), ("ffn", ctypes.c_int), ("causal", ctypes.c_int),
+                ("eps", ctypes.c_double), ("rope_base", ctypes.c_double),
+                ("batch", ctypes.c_int), ("seq", ctypes.c_int)]
+
+
+class LmStats(ctypes.Structure):
+    """lhip_lm_stats_t"""
+    _fields_ = [("loss", ctypes.c_float), ("grad_norm", ctypes.c_float), ("applied", ctypes.c_int),
+                ("correct", ctypes.c_int), ("steps", ctypes.c_int)]
+
+
+_cfgp = ctypes.POINTER(LmConfig)
+SIGNATURES.update({
+    "lhip_lm_num_params": (_ll, [_cfgp]),
+    "lhip_lm_param_offsets": (_i, [_cfgp, _p, _p, _p]),
+    "lhip_lm_create": (_i, [_cfgp, _pp]),
+    "lhip_lm_destroy": (_i, [_p]),
+    "lhip_lm_set_params": (_i, [_p, _p, _ll]),
+    "lhip_lm_get_params": (_i, [_p, _p, _ll]),
+    "lhip_lm_get_grads": (_i, [_p, _p, _ll]),
+    "lhip_lm_set_velocity": (_i, [_p, _p, _ll]),
+    "lhip_lm_get_velocity": (_i, [_p, _p, _ll]),
+    "lhip_lm_set_batch": (_i, [_p, _p, _p]),
+    "lhip_lm_use_graph": (_i, [_p, _i]),
+    "lhip_lm_step_sgd": (_i, [_p, _f, _f, _f, _f, _i]),
+    "lhip_lm_stats": (_i, [_p, ctypes.POINTER(LmStats), _p, _i]),
+    "lhip_lm_get_argmax": (_i, [_p, _p, _i]),
+})
+
 _lib = None
 
 

@@ -119,7 +119,8 @@ sgemm_mfma_kernel(int M, int N, int K, float alpha,
                   const float* __restrict__ A, int lda, long long sA,
                   const float* __restrict__ B, int ldb, long long sB, float beta,
                   float* __restrict__ C, int ldc, long long sC,
-                  int tiles_m, int tiles_n, int vecA, int vecB)
+                  int tiles_m, int tiles_n, int vecA, int vecB,
+                  int inner, long long sA2, long long sB2, long long sC2)
 {
     constexpr int WM = BM / 2, WN = BN / 2;        // 2x2 waves
     constexpr int FM = WM / 32, FN = WN / 32;      // 32x32 MFMA blocks per wave
@@ -140,10 +141,11 @@ sgemm_mfma_kernel(int M, int N, int K, float alpha,
     int tm, tn;
     tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
-    const long long bz = blockIdx.y;
-    A += bz * sA;
-    B += bz * sB;
-    C += bz * sC;
+    // two-level batch: z = outer * inner + inner_index (e.g. window x head)
+    const long long zo = blockIdx.y / inner, zi = blockIdx.y % inner;
+    A += zo * sA2 + zi * sA;
+    B += zo * sB2 + zi * sB;
+    C += zo * sC2 + zi * sC;
 
     const int wm = (wave >> 1) * WM;
     const int wn = (wave & 1) * WN;
@@ -227,7 +229,7 @@ sgemm_mfma_kernel(int M, int N, int K, float alpha,
 template <int BM, int BN, int BK>
 int launch_cfg(int ta, int tb, int m, int n, int k, float alpha, const float* A, int lda, long long sA,
                const float* B, int ldb, long long sB, float beta, float* C, int ldc, long long sC,
-               int batch, int vecA, int vecB, hipStream_t stream)
+               int batch, int vecA, int vecB, const GemmBatch2& b2, hipStream_t stream)
 {
     const int tiles_m = ceil_div(m, BM), tiles_n = ceil_div(n, BN);
     const long long nwg = static_cast<long long>(tiles_m) * tiles_n;
@@ -235,7 +237,8 @@ int launch_cfg(int ta, int tb, int m, int n, int k, float alpha, const float* A,
     dim3 grid(static_cast<unsigned>(nwg), batch, 1), block(kThreads, 1, 1);
 #define LHIP_GEMM_LAUNCH(TA_, TB_)                                                             \
     sgemm_mfma_kernel<BM, BN, BK, TA_, TB_><<<grid, block, 0, stream>>>(                        \
-        m, n, k, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC, tiles_m, tiles_n, vecA, vecB)
+        m, n, k, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC, tiles_m, tiles_n, vecA, vecB, \
+        b2.inner, b2.sA2, b2.sB2, b2.sC2)
     if (!ta && !tb) LHIP_GEMM_LAUNCH(false, false);
     else if (ta && !tb) LHIP_GEMM_LAUNCH(true, false);
     else if (!ta && tb) LHIP_GEMM_LAUNCH(false, true);
@@ -251,6 +254,16 @@ int sgemm_launch(int ta, int tb, int m, int n, int k, float alpha,
                  float* C, int ldc, int batch, long long sA, long long sB, long long sC,
                  hipStream_t stream)
 {
+    GemmBatch2 b2;
+    b2.inner = batch > 0 ? batch : 1;
+    return sgemm_launch2(ta, tb, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc, batch, sA, sB, sC, b2, stream);
+}
+
+int sgemm_launch2(int ta, int tb, int m, int n, int k, float alpha,
+                  const float* A, int lda, const float* B, int ldb, float beta,
+                  float* C, int ldc, int batch, long long sA, long long sB, long long sC,
+                  const GemmBatch2& b2, hipStream_t stream)
+{
     if (m < 0 || n < 0 || k < 0 || batch < 0)
         return fail(LHIP_E_SHAPE, "sgemm: negative size (m=%d n=%d k=%d batch=%d)", m, n, k, batch);
     if (m == 0 || n == 0 || batch == 0) return LHIP_OK;
@@ -264,19 +277,22 @@ int sgemm_launch(int ta, int tb, int m, int n, int k, float alpha,
         return fail(LHIP_E_SHAPE, "sgemm: ldb=%d < %d", ldb, b_cols);
     if (ldc < n) return fail(LHIP_E_SHAPE, "sgemm: ldc=%d < n=%d", ldc, n);
     if (batch > 65535) return fail(LHIP_E_CAPACITY, "sgemm: batch %d > 65535", batch);
-    if (batch > 1 && (sA < 0 || sB < 0 || sC < 0))
+    if (batch > 1 && (sA < 0 || sB < 0 || sC < 0 || b2.sA2 < 0 || b2.sB2 < 0 || b2.sC2 < 0))
         return fail(LHIP_E_SHAPE, "sgemm: negative batch stride");
-    const int vecA = (k > 0 && lda % 4 == 0 && aligned16(A) && (batch == 1 || sA % 4 == 0)) ? 1 : 0;
-    const int vecB = (k > 0 && ldb % 4 == 0 && aligned16(B) && (batch == 1 || sB % 4 == 0)) ? 1 : 0;
+    if (b2.inner <= 0) return fail(LHIP_E_ARG, "sgemm: inner batch count must be > 0");
+    const int vecA = (k > 0 && lda % 4 == 0 && aligned16(A) &&
+                      (batch == 1 || (sA % 4 == 0 && b2.sA2 % 4 == 0))) ? 1 : 0;
+    const int vecB = (k > 0 && ldb % 4 == 0 && aligned16(B) &&
+                      (batch == 1 || (sB % 4 == 0 && b2.sB2 % 4 == 0))) ? 1 : 0;
     // Large problems: 128x128 tiles (64x64 per wave).  When that leaves the
     // chip with fewer workgroups than CUs, use 64x64 tiles for parallelism.
     const long long big_tiles = static_cast<long long>(ceil_div(m, 128)) * ceil_div(n, 128) * batch;
     const int cus = st().cu_count > 0 ? st().cu_count : 256;
     if (big_tiles >= cus)
         return launch_cfg<128, 128, 32>(ta, tb, m, n, k, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC,
-                                        batch, vecA, vecB, stream);
+                                        batch, vecA, vecB, b2, stream);
     return launch_cfg<64, 64, 32>(ta, tb, m, n, k, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC,
-                                  batch, vecA, vecB, stream);
+                                  batch, vecA, vecB, b2, stream);
 }
 
 }  // namespace lhip

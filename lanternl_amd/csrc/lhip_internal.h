@@ -94,10 +94,24 @@ int embed_bwd(const float* g, const int* ids, float* dtable, int n, int dim, int
               hipStream_t s);
 int sumsq_blocks(long long n);
 int sumsq(const float* x, long long n, double* out, double* partial, int partial_len, hipStream_t s);
+// hyper_dev (may be NULL): device floats {lr, momentum, wd, clip_norm, nesterov}
+// that override the by-value arguments (a replayed graph reads them there).
 int sgd_step(float* p, float* g, float* v, long long n, const double* sumsq_dev, float lr, float momentum,
              float wd, float grad_scale, float clip_norm, int nesterov, float* gnorm_out, int* applied_out,
-             hipStream_t s);
+             hipStream_t s, const float* hyper_dev);
 int sum_f32(const float* x, int n, float scale, float* out, hipStream_t s);
+
+// Second batch level: blockIdx.y = outer * inner + i; operand X is offset by
+// outer * sX2 + i * sX (sX = the per-matrix strides of sgemm_launch).
+struct GemmBatch2 {
+    int inner = 1;
+    long long sA2 = 0, sB2 = 0, sC2 = 0;
+};
+
+int sgemm_launch2(int transa, int transb, int m, int n, int k, float alpha,
+                  const float* A, int lda, const float* B, int ldb, float beta,
+                  float* C, int ldc, int batch, long long sA, long long sB, long long sC,
+                  const GemmBatch2& b2, hipStream_t stream);
 
 int sgemm_launch(int transa, int transb, int m, int n, int k, float alpha,
                  const float* A, int lda, const float* B, int ldb, float beta,

@@ -1,0 +1,576 @@
+// lhip_lm.hip -- one LMTrain optimizer step of the CPU path, resident on the GPU.
+//
+// Model and step semantics are the CPU LMTrain path's:
+//   ai/nn/transformer.lua:84-257 (pre-norm decoder: RMSNorm, separate wq/wk/wv,
+//     per-head attention with interleaved-pair RoPE, causal softmax of
+//     scores/sqrt(hd), wo, residual, RMSNorm, SwiGLU with separate w1/w3/w2,
+//     residual, final RMSNorm, head tied to the embedding via matmul_nt);
+//   ai/core/tensor2.lua (each op's forward and backward);
+//   ai/optim/lmtrain.lua:1183-1227 (B windows of T tokens per step, the loss
+//     of each window the mean over its T targets, grads summed over windows
+//     then scaled by 1/B, global-norm skip/clip, optimizer step) with
+//     optimizer "sgd" (ai/optim/optim2.lua:48-102).
+// The B windows are independent sequences, so they are processed together as
+// one [B*T, dim] block: every projection is one GEMM over all B*T rows, the
+// attention products are 2-level batched GEMMs over (window, head), the
+// causal mask restarts every T rows (group = T), and RoPE positions are
+// row % T.  Parameters, gradients and velocities are single flat device
+// buffers in Transformer:parameters() order (transformer.lua:150-164), so the
+// global norm and the SGD update are one reduction and one elementwise pass.
+// The GPU-resident reference path (ai/gpu/gpu_transformer.lua) has different
+// numerics (fused weights, half-split RoPE, AdamW); it is not what this follows.
+//
+// The whole step is enqueued on the library stream with no host round trip
+// (the norm, the skip decision and the clip factor stay on the device) and no
+// allocation, so it can be captured once into a hipGraph and replayed.
+#include <cmath>
+#include <cstring>
+#include <new>
+#include <vector>
+
+#include "lhip_internal.h"
+
+namespace lhip {
+namespace {
+
+enum { P_LN1, P_WQ, P_WK, P_WV, P_WO, P_LN2, P_W1, P_W3, P_W2, P_PER_LAYER };
+
+__global__ void set_hyper_kernel(float* hp, float lr, float momentum, float wd, float clip, float nesterov)
+{
+    if (threadIdx.x == 0) {
+        hp[0] = lr; hp[1] = momentum; hp[2] = wd; hp[3] = clip; hp[4] = nesterov;
+    }
+}
+
+struct LmModel {
+    lhip_lm_config_t c{};
+    int N = 0, D = 0, F = 0, V = 0, H = 0, hd = 0, L = 0, T = 0, B = 0;
+    long long nparam = 0;
+    std::vector<long long> off;   // float offset of each parameter tensor
+    void* arena = nullptr;        // every device buffer below lives in it
+    size_t arena_bytes = 0;
+    float *params = nullptr, *grads = nullptr, *vel = nullptr;
+    int *ids = nullptr, *tgt = nullptr, *amax = nullptr, *applied = nullptr;
+    float *losses = nullptr, *gnorm = nullptr, *hyper = nullptr;
+    double *ss = nullptr, *ss_part = nullptr;
+    int ss_blocks = 0;
+    // saved activations
+    float *x = nullptr, *h = nullptr, *inv1 = nullptr, *qkv = nullptr, *P = nullptr, *ctx = nullptr;
+    float *xmid = nullptr, *h2 = nullptr, *inv2 = nullptr, *zu = nullptr, *a = nullptr;
+    float *xf = nullptr, *invf = nullptr, *logits = nullptr;
+    // backward scratch
+    float *dxf = nullptr, *dx = nullptr, *da = nullptr, *dzu = nullptr, *dh2 = nullptr, *dctx = nullptr;
+    float *dP = nullptr, *dS = nullptr, *dqkv = nullptr, *dh = nullptr, *work = nullptr;
+    size_t work_floats = 0;
+    // graph
+    bool use_graph = false;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    int steps = 0;
+    bool have_batch = false;
+    std::vector<int> h_tgt;
+
+    const float* prm(int tensor) const { return params + off[tensor]; }
+    float* grd(int tensor) const { return grads + off[tensor]; }
+    int lt(int l, int which) const { return 1 + P_PER_LAYER * l + which; }
+};
+
+long long count_params(const lhip_lm_config_t& c)
+{
+    const long long D = c.dim, F = c.ffn, V = c.vocab;
+    return V * D + static_cast<long long>(c.layers) * (2 * D + 4 * D * D + 3 * D * F) + D;
+}
+
+// model dimensions only (parameter layout)
+int check_dims(const lhip_lm_config_t* c)
+{
+    if (!c) return fail(LHIP_E_NULL, "lm: config is NULL");
+    if (c->vocab <= 0 || c->dim <= 0 || c->layers <= 0 || c->heads <= 0 || c->ffn <= 0)
+        return fail(LHIP_E_SHAPE, "lm: every model size must be > 0 (vocab=%d dim=%d layers=%d heads=%d ffn=%d)",
+                    c->vocab, c->dim, c->layers, c->heads, c->ffn);
+    return LHIP_OK;
+}
+
+int check_config(const lhip_lm_config_t* c)
+{
+    if (int rc = check_dims(c)) return rc;
+    if (c->batch <= 0 || c->seq <= 0)
+        return fail(LHIP_E_SHAPE, "lm: batch=%d and seq=%d must be > 0", c->batch, c->seq);
+    if (c->dim % c->heads) return fail(LHIP_E_SHAPE, "lm: dim %d not divisible by heads %d", c->dim, c->heads);
+    const int hd = c->dim / c->heads;
+    if (hd % 2) return fail(LHIP_E_SHAPE, "lm: head_dim %d must be even for RoPE", hd);
+    if (hd > 256) return fail(LHIP_E_CAPACITY, "lm: head_dim %d > 256", hd);
+    if (!(c->eps >= 0.0) || !(c->rope_base > 0.0)) return fail(LHIP_E_ARG, "lm: eps must be >= 0 and rope_base > 0");
+    if (static_cast<long long>(c->batch) * c->seq > (1LL << 28))
+        return fail(LHIP_E_CAPACITY, "lm: batch*seq too large");
+    return LHIP_OK;
+}
+
+// ---- the step ------------------------------------------------------------
+struct Enq {
+    LmModel& m;
+    hipStream_t s;
+
+    int gemm(int ta, int tb, int M, int Nn, int K, const float* A, int lda, const float* Bm, int ldb, float beta,
+             float* C, int ldc) const
+    {
+        return sgemm_launch(ta, tb, M, Nn, K, 1.f, A, lda, Bm, ldb, beta, C, ldc, 1, 0, 0, 0, s);
+    }
+    int bgemm(int ta, int tb, int M, int Nn, int K, const float* A, int lda, long long sa, const float* Bm, int ldb,
+              long long sb, float beta, float* C, int ldc, long long sc, int batch) const
+    {
+        return sgemm_launch(ta, tb, M, Nn, K, 1.f, A, lda, Bm, ldb, beta, C, ldc, batch, sa, sb, sc, s);
+    }
+    // batch (window b, head h): operand offsets b*X2 + h*X
+    int hgemm(int ta, int tb, int M, int Nn, int K, const float* A, int lda, long long sa, long long sa2,
+              const float* Bm, int ldb, long long sb, long long sb2, float* C, int ldc, long long sc,
+              long long sc2) const
+    {
+        GemmBatch2 b2;
+        b2.inner = m.H;
+        b2.sA2 = sa2; b2.sB2 = sb2; b2.sC2 = sc2;
+        return sgemm_launch2(ta, tb, M, Nn, K, 1.f, A, lda, Bm, ldb, 0.f, C, ldc, m.B * m.H, sa, sb, sc, b2, s);
+    }
+    int copy(float* dst, const float* src, long long n) const
+    {
+        hipError_t e = hipMemcpyAsync(dst, src, static_cast<size_t>(n) * sizeof(float), hipMemcpyDeviceToDevice, s);
+        return e == hipSuccess ? LHIP_OK : hip_fail(e, "lm: device copy");
+    }
+};
+
+#define LM_TRY(expr)                       \
+    do {                                   \
+        int _rc = (expr);                  \
+        if (_rc != LHIP_OK) return _rc;    \
+    } while (0)
+
+int enqueue_step(LmModel& m, hipStream_t s)
+{
+    const Enq q{m, s};
+    const int N = m.N, D = m.D, F = m.F, V = m.V, H = m.H, hd = m.hd, T = m.T, L = m.L;
+    const long long ND = static_cast<long long>(N) * D, NF = static_cast<long long>(N) * F;
+    const long long TT = static_cast<long long>(T) * T, HTT = H * TT, TD = static_cast<long long>(T) * D;
+    const long long PL = static_cast<long long>(m.B) * HTT;          // softmax block per layer
+    const float scale = 1.0f / std::sqrt(static_cast<float>(hd));
+    const int causal = m.c.causal ? 1 : 0;
+    const float eps = static_cast<float>(m.c.eps);
+    const double base = m.c.rope_base;
+    const float* emb = m.prm(0);
+    const float* lnf = m.prm(1 + P_PER_LAYER * L);
+
+    LM_TRY(fill(m.grads, m.nparam, 0.f, s));   // opt.zero_grad()
+
+    // ---------------- forward (transformer.lua:228-257) ----------------
+    LM_TRY(embed_fwd(emb, m.ids, m.x, N, D, V, s));
+    for (int l = 0; l < L; ++l) {
+        const float* xl = m.x + l * ND;
+        float* h = m.h + l * ND;
+        float* inv1 = m.inv1 + static_cast<long long>(l) * N;
+        float* qkv = m.qkv + l * 3 * ND;
+        float* P = m.P + l * PL;
+        float* ctx = m.ctx + l * ND;
+        float* xmid = m.xmid + l * ND;
+        float* h2 = m.h2 + l * ND;
+        float* inv2 = m.inv2 + static_cast<long long>(l) * N;
+        float* zu = m.zu + l * 2 * NF;
+        float* a = m.a + l * NF;
+        float* xn = m.x + (l + 1) * ND;
+        LM_TRY(rmsnorm_fwd(xl, m.prm(m.lt(l, P_LN1)), h, inv1, N, D, eps, s));
+        // q, k, v = h.Wq, h.Wk, h.Wv: one batched GEMM (the three weights are adjacent)
+        LM_TRY(q.bgemm(0, 0, N, D, D, h, D, 0, m.prm(m.lt(l, P_WQ)), D, static_cast<long long>(D) * D, 0.f, qkv, D, ND, 3));
+        // RoPE on q and k (2N rows, positions row % T), interleaved pairs
+        LM_TRY(rope(qkv, nullptr, 2 * N, H, hd, D, 0, T, base, 1, 0, s));
+        // scores = q_bh . k_bh^T per (window, head), into the (forward-idle) dP
+        // scratch; P = softmax(scale * scores)
+        LM_TRY(q.hgemm(0, 1, T, T, hd, qkv, D, hd, TD, qkv + ND, D, hd, TD, m.dP, T, TT, HTT));
+        LM_TRY(softmax_fwd(m.dP, P, m.B * H * T, T, scale, causal, 0, T, s));
+        // ctx[:, h*hd:] = P_bh . v_bh
+        LM_TRY(q.hgemm(0, 0, T, hd, T, P, T, TT, HTT, qkv + 2 * ND, D, hd, TD, ctx, D, hd, TD));
+        // x_mid = x + ctx . Wo
+        LM_TRY(q.copy(xmid, xl, ND));
+        LM_TRY(q.gemm(0, 0, N, D, D, ctx, D, m.prm(m.lt(l, P_WO)), D, 1.f, xmid, D));
+        LM_TRY(rmsnorm_fwd(xmid, m.prm(m.lt(l, P_LN2)), h2, inv2, N, D, eps, s));
+        // z1 = h2.W1, u = h2.W3 (adjacent weights, one batched GEMM); a = silu(z1) * u
+        LM_TRY(q.bgemm(0, 0, N, F, D, h2, D, 0, m.prm(m.lt(l, P_W1)), F, static_cast<long long>(D) * F, 0.f, zu, F, NF, 2));
+        LM_TRY(swiglu_fwd(zu, F, zu + NF, F, a, F, N, F, s));
+        // x_{l+1} = x_mid + a . W2
+        LM_TRY(q.copy(xn, xmid, ND));
+        LM_TRY(q.gemm(0, 0, N, D, F, a, F, m.prm(m.lt(l, P_W2)), D, 1.f, xn, D));
+    }
+    const float* xL = m.x + static_cast<long long>(L) * ND;
+    LM_TRY(rmsnorm_fwd(xL, lnf, m.xf, m.invf, N, D, eps, s));
+    // tied head: logits = xf . emb^T
+    LM_TRY(q.gemm(0, 1, N, V, D, m.xf, D, emb, D, 0.f, m.logits, V));
+    LM_TRY(argmax_rows(m.logits, m.amax, N, V, s));
+    // per-row losses; dlogits = (softmax - onehot) / T written over the logits
+    LM_TRY(ce_fused(m.logits, m.tgt, m.losses, m.logits, N, V, -1, 1.0f / T, s));
+
+    // ---------------- backward ----------------
+    const float* dlg = m.logits;
+    LM_TRY(q.gemm(0, 0, N, D, V, dlg, V, emb, D, 0.f, m.dxf, D));                // dxf = dlogits . emb
+    LM_TRY(q.gemm(1, 0, V, D, N, dlg, V, m.xf, D, 1.f, m.grd(0), D));             // gemb += dlogits^T . xf
+    LM_TRY(rmsnorm_bwd(xL, lnf, m.invf, m.dxf, m.dx, m.grd(1 + P_PER_LAYER * L), N, D, 0, m.work, m.work_floats, s));
+    for (int l = L - 1; l >= 0; --l) {
+        const float* xl = m.x + l * ND;
+        const float* h = m.h + l * ND;
+        const float* inv1 = m.inv1 + static_cast<long long>(l) * N;
+        const float* qkv = m.qkv + l * 3 * ND;
+        const float* P = m.P + l * PL;
+        const float* ctx = m.ctx + l * ND;
+        const float* xmid = m.xmid + l * ND;
+        const float* h2 = m.h2 + l * ND;
+        const float* inv2 = m.inv2 + static_cast<long long>(l) * N;
+        const float* zu = m.zu + l * 2 * NF;
+        const float* a = m.a + l * NF;
+        // f = a . W2
+        LM_TRY(q.gemm(0, 1, N, F, D, m.dx, D, m.prm(m.lt(l, P_W2)), D, 0.f, m.da, F));      // da = dx . W2^T
+        LM_TRY(q.gemm(1, 0, F, D, N, a, F, m.dx, D, 0.f, m.grd(m.lt(l, P_W2)), D));         // gW2 = a^T . dx
+        LM_TRY(swiglu_bwd(zu, F, zu + NF, F, m.da, F, m.dzu, F, m.dzu + NF, F, N, F, 0, s));
+        LM_TRY(q.gemm(0, 1, N, D, F, m.dzu, F, m.prm(m.lt(l, P_W1)), F, 0.f, m.dh2, D));    // dh2 = dz1 . W1^T
+        LM_TRY(q.gemm(0, 1, N, D, F, m.dzu + NF, F, m.prm(m.lt(l, P_W3)), F, 1.f, m.dh2, D)); //     + du . W3^T
+        LM_TRY(q.bgemm(1, 0, D, F, N, h2, D, 0, m.dzu, F, NF, 0.f, m.grd(m.lt(l, P_W1)), F,
+                       static_cast<long long>(D) * F, 2));                                   // gW1, gW3
+        LM_TRY(rmsnorm_bwd(xmid, m.prm(m.lt(l, P_LN2)), inv2, m.dh2, m.dx, m.grd(m.lt(l, P_LN2)), N, D, 1, m.work,
+                           m.work_floats, s));
+        // o = ctx . Wo
+        LM_TRY(q.gemm(0, 1, N, D, D, m.dx, D, m.prm(m.lt(l, P_WO)), D, 0.f, m.dctx, D));    // dctx = dx . Wo^T
+        LM_TRY(q.gemm(1, 0, D, D, N, ctx, D, m.dx, D, 0.f, m.grd(m.lt(l, P_WO)), D));       // gWo = ctx^T . dx
+        // per (window, head): dP = dO . v^T ; dv = P^T . dO
+        LM_TRY(q.hgemm(0, 1, T, T, hd, m.dctx, D, hd, TD, qkv + 2 * ND, D, hd, TD, m.dP, T, TT, HTT));
+        LM_TRY(q.hgemm(1, 0, T, hd, T, P, T, TT, HTT, m.dctx, D, hd, TD, m.dqkv + 2 * ND, D, hd, TD));
+        // dS = scale * softmax_bwd(P, dP)
+        LM_TRY(softmax_bwd(P, m.dP, m.dS, m.B * H * T, T, scale, causal, 0, T, 0, s));
+        // dq = dS . k_rot ; dk = dS^T . q_rot
+        LM_TRY(q.hgemm(0, 0, T, hd, T, m.dS, T, TT, HTT, qkv + ND, D, hd, TD, m.dqkv, D, hd, TD));
+        LM_TRY(q.hgemm(1, 0, T, hd, T, m.dS, T, TT, HTT, qkv, D, hd, TD, m.dqkv + ND, D, hd, TD));
+        // RoPE backward (inverse rotation) on dq and dk
+        LM_TRY(rope(m.dqkv, nullptr, 2 * N, H, hd, D, 0, T, base, 1, 1, s));
+        // dh = dq.Wq^T + dk.Wk^T + dv.Wv^T ; gW{q,k,v} = h^T . d{q,k,v}
+        LM_TRY(q.gemm(0, 1, N, D, D, m.dqkv, D, m.prm(m.lt(l, P_WQ)), D, 0.f, m.dh, D));
+        LM_TRY(q.gemm(0, 1, N, D, D, m.dqkv + ND, D, m.prm(m.lt(l, P_WK)), D, 1.f, m.dh, D));
+        LM_TRY(q.gemm(0, 1, N, D, D, m.dqkv + 2 * ND, D, m.prm(m.lt(l, P_WV)), D, 1.f, m.dh, D));
+        LM_TRY(q.bgemm(1, 0, D, D, N, h, D, 0, m.dqkv, D, ND, 0.f, m.grd(m.lt(l, P_WQ)), D,
+                       static_cast<long long>(D) * D, 3));
+        LM_TRY(rmsnorm_bwd(xl, m.prm(m.lt(l, P_LN1)), inv1, m.dh, m.dx, m.grd(m.lt(l, P_LN1)), N, D, 1, m.work,
+                           m.work_floats, s));
+    }
+    LM_TRY(embed_bwd(m.dx, m.ids, m.grd(0), N, D, V, 1.f, 1, s));
+
+    // ---------------- optimizer (lmtrain.lua:1212-1226) ----------------
+    LM_TRY(sumsq(m.grads, m.nparam, m.ss, m.ss_part, m.ss_blocks, s));
+    const float gscale = m.B > 1 ? 1.0f / m.B : 1.0f;
+    LM_TRY(sgd_step(m.params, m.grads, m.vel, m.nparam, m.ss, 0.f, 0.f, 0.f, gscale, 0.f, 0, m.gnorm, m.applied, s,
+                    m.hyper));
+    return LHIP_OK;
+}
+
+void drop_graph(LmModel& m)
+{
+    if (m.exec) (void)hipGraphExecDestroy(m.exec);
+    if (m.graph) (void)hipGraphDestroy(m.graph);
+    m.exec = nullptr;
+    m.graph = nullptr;
+}
+
+int capture_step(LmModel& m, hipStream_t s)
+{
+    drop_graph(m);
+    LHIP_CHECK_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "lm: begin capture");
+    const int rc = enqueue_step(m, s);
+    hipGraph_t g = nullptr;
+    const hipError_t e = hipStreamEndCapture(s, &g);
+    if (rc != LHIP_OK) {
+        if (g) (void)hipGraphDestroy(g);
+        return rc;
+    }
+    if (e != hipSuccess) return hip_fail(e, "lm: end capture");
+    m.graph = g;
+    const hipError_t e2 = hipGraphInstantiate(&m.exec, m.graph, nullptr, nullptr, 0);
+    if (e2 != hipSuccess) {
+        drop_graph(m);
+        return hip_fail(e2, "lm: graph instantiate");
+    }
+    return LHIP_OK;
+}
+
+LmModel* as_model(void* p) { return static_cast<LmModel*>(p); }
+
+}  // namespace
+}  // namespace lhip
+
+using lhip::fail;
+using lhip::st;
+
+extern "C" {
+
+LHIP_API long long lhip_lm_num_params(const lhip_lm_config_t* cfg)
+{
+    if (lhip::check_dims(cfg) != LHIP_OK) return -1;
+    return lhip::count_params(*cfg);
+}
+
+LHIP_API int lhip_lm_param_offsets(const lhip_lm_config_t* cfg, long long* offsets, int* rows, int* cols)
+{
+    if (int rc = lhip::check_dims(cfg)) return rc;
+    const int D = cfg->dim, F = cfg->ffn, V = cfg->vocab;
+    long long off = 0;
+    int idx = 0;
+    auto add = [&](int r, int c) {
+        if (offsets) offsets[idx] = off;
+        if (rows) rows[idx] = r;
+        if (cols) cols[idx] = c;
+        off += static_cast<long long>(r) * c;
+        ++idx;
+    };
+    add(V, D);
+    for (int l = 0; l < cfg->layers; ++l) {
+        add(1, D); add(D, D); add(D, D); add(D, D); add(D, D);
+        add(1, D); add(D, F); add(D, F); add(F, D);
+    }
+    add(1, D);
+    return LHIP_OK;
+}
+
+LHIP_API int lhip_lm_create(const lhip_lm_config_t* cfg, void** model)
+{
+    LHIP_REQUIRE_READY();
+    if (!model) return fail(LHIP_E_NULL, "lhip_lm_create: model is NULL");
+    *model = nullptr;
+    if (int rc = lhip::check_config(cfg)) return rc;
+    auto* m = new (std::nothrow) lhip::LmModel();
+    if (!m) return fail(LHIP_E_OOM, "lhip_lm_create: host allocation");
+    m->c = *cfg;
+    m->D = cfg->dim; m->F = cfg->ffn; m->V = cfg->vocab; m->H = cfg->heads; m->L = cfg->layers;
+    m->T = cfg->seq; m->B = cfg->batch; m->hd = m->D / m->H; m->N = m->B * m->T;
+    m->nparam = lhip::count_params(*cfg);
+    const int ntens = 2 + lhip::P_PER_LAYER * m->L;
+    m->off.resize(ntens);
+    lhip_lm_param_offsets(cfg, m->off.data(), nullptr, nullptr);
+
+    const long long N = m->N, D = m->D, F = m->F, V = m->V, L = m->L;
+    const long long ND = N * D, NF = N * F, PL = static_cast<long long>(m->B) * m->H * m->T * m->T;
+    m->ss_blocks = lhip::sumsq_blocks(m->nparam);
+    m->work_floats = static_cast<size_t>(lhip::rmsnorm_bwd_parts(m->N, m->D)) * m->D;
+    // carve every buffer out of one allocation, each 256-byte aligned
+    struct Slot { void** dst; size_t bytes; };
+    std::vector<Slot> slots = {
+        {reinterpret_cast<void**>(&m->params), sizeof(float) * m->nparam},
+        {reinterpret_cast<void**>(&m->grads), sizeof(float) * m->nparam},
+        {reinterpret_cast<void**>(&m->vel), sizeof(float) * m->nparam},
+        {reinterpret_cast<void**>(&m->ids), sizeof(int) * N},
+        {reinterpret_cast<void**>(&m->tgt), sizeof(int) * N},
+        {reinterpret_cast<void**>(&m->amax), sizeof(int) * N},
+        {reinterpret_cast<void**>(&m->applied), sizeof(int) * 4},
+        {reinterpret_cast<void**>(&m->losses), sizeof(float) * N},
+        {reinterpret_cast<void**>(&m->gnorm), sizeof(float) * 4},
+        {reinterpret_cast<void**>(&m->hyper), sizeof(float) * 8},
+        {reinterpret_cast<void**>(&m->ss), sizeof(double) * 2},
+        {reinterpret_cast<void**>(&m->ss_part), sizeof(double) * m->ss_blocks},
+        {reinterpret_cast<void**>(&m->x), sizeof(float) * (L + 1) * ND},
+        {reinterpret_cast<void**>(&m->h), sizeof(float) * L * ND},
+        {reinterpret_cast<void**>(&m->inv1), sizeof(float) * L * N},
+        {reinterpret_cast<void**>(&m->qkv), sizeof(float) * L * 3 * ND},
+        {reinterpret_cast<void**>(&m->P), sizeof(float) * L * PL},
+        {reinterpret_cast<void**>(&m->ctx), sizeof(float) * L * ND},
+        {reinterpret_cast<void**>(&m->xmid), sizeof(float) * L * ND},
+        {reinterpret_cast<void**>(&m->h2), sizeof(float) * L * ND},
+        {reinterpret_cast<void**>(&m->inv2), sizeof(float) * L * N},
+        {reinterpret_cast<void**>(&m->zu), sizeof(float) * L * 2 * NF},
+        {reinterpret_cast<void**>(&m->a), sizeof(float) * L * NF},
+        {reinterpret_cast<void**>(&m->xf), sizeof(float) * ND},
+        {reinterpret_cast<void**>(&m->invf), sizeof(float) * N},
+        {reinterpret_cast<void**>(&m->logits), sizeof(float) * N * V},
+        {reinterpret_cast<void**>(&m->dxf), sizeof(float) * ND},
+        {reinterpret_cast<void**>(&m->dx), sizeof(float) * ND},
+        {reinterpret_cast<void**>(&m->da), sizeof(float) * NF},
+        {reinterpret_cast<void**>(&m->dzu), sizeof(float) * 2 * NF},
+        {reinterpret_cast<void**>(&m->dh2), sizeof(float) * ND},
+        {reinterpret_cast<void**>(&m->dctx), sizeof(float) * ND},
+        {reinterpret_cast<void**>(&m->dP), sizeof(float) * PL},
+        {reinterpret_cast<void**>(&m->dS), sizeof(float) * PL},
+        {reinterpret_cast<void**>(&m->dqkv), sizeof(float) * 3 * ND},
+        {reinterpret_cast<void**>(&m->dh), sizeof(float) * ND},
+        {reinterpret_cast<void**>(&m->work), sizeof(float) * m->work_floats},
+    };
+    size_t total = 0;
+    for (auto& sl : slots) total += (sl.bytes + 255) & ~static_cast<size_t>(255);
+    hipError_t e = hipMalloc(&m->arena, total);
+    if (e != hipSuccess) {
+        delete m;
+        return fail(LHIP_E_OOM, "lhip_lm_create: %zu bytes of device memory: %s", total, hipGetErrorString(e));
+    }
+    m->arena_bytes = total;
+    char* p = static_cast<char*>(m->arena);
+    for (auto& sl : slots) {
+        *sl.dst = p;
+        p += (sl.bytes + 255) & ~static_cast<size_t>(255);
+    }
+    // zero state: params, grads, velocity, ids (a fresh model is all zeros until set_params)
+    int rc = lhip::zero_bytes(m->arena, total, st().stream);
+    if (rc == LHIP_OK) {
+        hipError_t se = hipStreamSynchronize(st().stream);
+        if (se != hipSuccess) rc = lhip::hip_fail(se, "lhip_lm_create: sync");
+    }
+    if (rc != LHIP_OK) {
+        (void)hipFree(m->arena);
+        delete m;
+        return rc;
+    }
+    m->h_tgt.assign(static_cast<size_t>(N), 0);
+    *model = m;
+    return LHIP_OK;
+}
+
+LHIP_API int lhip_lm_destroy(void* model)
+{
+    if (!model) return LHIP_OK;
+    auto* m = lhip::as_model(model);
+    if (st().ready) {
+        (void)hipStreamSynchronize(st().stream);
+        lhip::drop_graph(*m);
+        (void)hipFree(m->arena);
+    }
+    delete m;
+    return LHIP_OK;
+}
+
+static int lm_copy(void* model, float* host, long long n, int which, int to_device)
+{
+    LHIP_REQUIRE_READY();
+    if (!model || !host) return fail(LHIP_E_NULL, "lhip_lm: NULL argument");
+    auto* m = lhip::as_model(model);
+    if (n != m->nparam) return fail(LHIP_E_SHAPE, "lhip_lm: %lld values given, model has %lld", n, m->nparam);
+    float* d = which == 0 ? m->params : (which == 1 ? m->grads : m->vel);
+    const size_t bytes = static_cast<size_t>(n) * sizeof(float);
+    hipError_t e = to_device ? hipMemcpyAsync(d, host, bytes, hipMemcpyHostToDevice, st().stream)
+                             : hipMemcpyAsync(host, d, bytes, hipMemcpyDeviceToHost, st().stream);
+    if (e != hipSuccess) return lhip::hip_fail(e, "lhip_lm: copy");
+    LHIP_CHECK_HIP(hipStreamSynchronize(st().stream), "lhip_lm: sync");
+    return LHIP_OK;
+}
+
+LHIP_API int lhip_lm_set_params(void* model, const float* host, long long n)
+{
+    return lm_copy(model, const_cast<float*>(host), n, 0, 1);
+}
+
+LHIP_API int lhip_lm_get_params(void* model, float* host, long long n) { return lm_copy(model, host, n, 0, 0); }
+
+LHIP_API int lhip_lm_get_grads(void* model, float* host, long long n) { return lm_copy(model, host, n, 1, 0); }
+
+LHIP_API int lhip_lm_set_velocity(void* model, const float* host, long long n)
+{
+    return lm_copy(model, const_cast<float*>(host), n, 2, 1);
+}
+
+LHIP_API int lhip_lm_get_velocity(void* model, float* host, long long n) { return lm_copy(model, host, n, 2, 0); }
+
+LHIP_API int lhip_lm_set_batch(void* model, const int* ids, const int* targets)
+{
+    LHIP_REQUIRE_READY();
+    if (!model || !ids || !targets) return fail(LHIP_E_NULL, "lhip_lm_set_batch: NULL argument");
+    auto* m = lhip::as_model(model);
+    for (int i = 0; i < m->N; ++i) {
+        if (ids[i] < 0 || ids[i] >= m->V)
+            return fail(LHIP_E_ARG, "lhip_lm_set_batch: ids[%d] = %d outside [0, %d)", i, ids[i], m->V);
+        if (targets[i] < 0 || targets[i] >= m->V)
+            return fail(LHIP_E_ARG, "lhip_lm_set_batch: targets[%d] = %d outside [0, %d)", i, targets[i], m->V);
+    }
+    const size_t bytes = static_cast<size_t>(m->N) * sizeof(int);
+    LHIP_CHECK_HIP(hipMemcpyAsync(m->ids, ids, bytes, hipMemcpyHostToDevice, st().stream), "lhip_lm_set_batch: ids");
+    LHIP_CHECK_HIP(hipMemcpyAsync(m->tgt, targets, bytes, hipMemcpyHostToDevice, st().stream),
+                   "lhip_lm_set_batch: targets");
+    LHIP_CHECK_HIP(hipStreamSynchronize(st().stream), "lhip_lm_set_batch: sync");
+    std::memcpy(m->h_tgt.data(), targets, bytes);
+    m->have_batch = true;
+    return LHIP_OK;
+}
+
+LHIP_API int lhip_lm_use_graph(void* model, int on)
+{
+    LHIP_REQUIRE_READY();
+    if (!model) return fail(LHIP_E_NULL, "lhip_lm_use_graph: model is NULL");
+    auto* m = lhip::as_model(model);
+    m->use_graph = on != 0;
+    if (!m->use_graph) {
+        (void)hipStreamSynchronize(st().stream);
+        lhip::drop_graph(*m);
+    }
+    return LHIP_OK;
+}
+
+LHIP_API int lhip_lm_step_sgd(void* model, float lr, float momentum, float weight_decay, float clip_norm,
+                              int nesterov)
+{
+    LHIP_REQUIRE_READY();
+    if (!model) return fail(LHIP_E_NULL, "lhip_lm_step_sgd: model is NULL");
+    auto* m = lhip::as_model(model);
+    if (!m->have_batch) return fail(LHIP_E_ARG, "lhip_lm_step_sgd: no batch (call lhip_lm_set_batch)");
+    if (!(lr >= 0.f) || !(momentum >= 0.f) || !(weight_decay >= 0.f) || !(clip_norm >= 0.f))
+        return fail(LHIP_E_ARG, "lhip_lm_step_sgd: lr, momentum, weight_decay and clip_norm must be >= 0");
+    hipStream_t s = st().stream;
+    lhip::set_hyper_kernel<<<1, 64, 0, s>>>(m->hyper, lr, momentum, weight_decay, clip_norm, nesterov ? 1.f : 0.f);
+    if (int rc = lhip::check_launch("lhip_lm_step_sgd: hyper")) return rc;
+    if (m->use_graph) {
+        if (!m->exec)
+            if (int rc = lhip::capture_step(*m, s)) return rc;
+        LHIP_CHECK_HIP(hipGraphLaunch(m->exec, s), "lhip_lm_step_sgd: graph launch");
+    } else {
+        if (int rc = lhip::enqueue_step(*m, s)) return rc;
+    }
+    ++m->steps;
+    return LHIP_OK;
+}
+
+LHIP_API int lhip_lm_stats(void* model, lhip_lm_stats_t* out, float* window_losses, int nwin)
+{
+    LHIP_REQUIRE_READY();
+    if (!model || !out) return fail(LHIP_E_NULL, "lhip_lm_stats: NULL argument");
+    auto* m = lhip::as_model(model);
+    if (window_losses && nwin != m->B)
+        return fail(LHIP_E_SHAPE, "lhip_lm_stats: %d window slots given, batch is %d", nwin, m->B);
+    std::vector<float> losses(static_cast<size_t>(m->N));
+    std::vector<int> am(static_cast<size_t>(m->N));
+    float gn = 0.f;
+    int applied = 0;
+    hipStream_t s = st().stream;
+    LHIP_CHECK_HIP(hipMemcpyAsync(losses.data(), m->losses, losses.size() * sizeof(float), hipMemcpyDeviceToHost, s),
+                   "lhip_lm_stats: losses");
+    LHIP_CHECK_HIP(hipMemcpyAsync(am.data(), m->amax, am.size() * sizeof(int), hipMemcpyDeviceToHost, s),
+                   "lhip_lm_stats: argmax");
+    LHIP_CHECK_HIP(hipMemcpyAsync(&gn, m->gnorm, sizeof(float), hipMemcpyDeviceToHost, s), "lhip_lm_stats: norm");
+    LHIP_CHECK_HIP(hipMemcpyAsync(&applied, m->applied, sizeof(int), hipMemcpyDeviceToHost, s),
+                   "lhip_lm_stats: applied");
+    LHIP_CHECK_HIP(hipStreamSynchronize(s), "lhip_lm_stats: sync");
+    // per-window mean of the row losses (Tensor.cross_entropy's mean over T),
+    // then the mean over windows
+    double total = 0.0;
+    for (int b = 0; b < m->B; ++b) {
+        double w = 0.0;
+        for (int t = 0; t < m->T; ++t) w += losses[static_cast<size_t>(b) * m->T + t];
+        w /= m->T;
+        if (window_losses) window_losses[b] = static_cast<float>(w);
+        total += w;
+    }
+    int correct = 0;
+    for (int i = 0; i < m->N; ++i) correct += am[i] == m->h_tgt[i];
+    out->loss = static_cast<float>(total / m->B);
+    out->grad_norm = gn;
+    out->applied = applied;
+    out->correct = correct;
+    out->steps = m->steps;
+    return LHIP_OK;
+}
+
+LHIP_API int lhip_lm_get_argmax(void* model, int* host, int n)
+{
+    LHIP_REQUIRE_READY();
+    if (!model || !host) return fail(LHIP_E_NULL, "lhip_lm_get_argmax: NULL argument");
+    auto* m = lhip::as_model(model);
+    if (n != m->N) return fail(LHIP_E_SHAPE, "lhip_lm_get_argmax: n=%d, batch*seq=%d", n, m->N);
+    LHIP_CHECK_HIP(hipMemcpyAsync(host, m->amax, sizeof(int) * n, hipMemcpyDeviceToHost, st().stream), "argmax copy");
+    LHIP_CHECK_HIP(hipStreamSynchronize(st().stream), "lhip_lm_get_argmax: sync");
+    return LHIP_OK;
+}
+
+}  // extern "C"

@@ -62,8 +62,12 @@ __global__ void __launch_bounds__(64) sum_stage2(const double* __restrict__ part
 __global__ void sgd_step_kernel(float* __restrict__ p, float* __restrict__ g, float* __restrict__ v, long long n,
                                 const double* __restrict__ sumsq, float lr, float momentum, float wd,
                                 float grad_scale, float clip_norm, int nesterov, float* __restrict__ gnorm_out,
-                                int* __restrict__ applied_out)
+                                int* __restrict__ applied_out, const float* __restrict__ hyper)
 {
+    if (hyper) {   // hyper-parameters resident on the device (graph replay)
+        lr = hyper[0]; momentum = hyper[1]; wd = hyper[2]; clip_norm = hyper[3];
+        nesterov = hyper[4] != 0.f;
+    }
     const double norm = static_cast<double>(grad_scale) * sqrt(sumsq[0]);
     const bool finite = isfinite(norm);
     const long long t0 = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
@@ -124,18 +128,19 @@ int sumsq(const float* x, long long n, double* out, double* partial, int partial
 
 int sgd_step(float* p, float* g, float* v, long long n, const double* sumsq_dev, float lr, float momentum,
              float wd, float grad_scale, float clip_norm, int nesterov, float* gnorm_out, int* applied_out,
-             hipStream_t s)
+             hipStream_t s, const float* hyper_dev)
 {
     if (n < 0) return fail(LHIP_E_SHAPE, "sgd_step: n < 0");
     if (!sumsq_dev) return fail(LHIP_E_NULL, "sgd_step: sumsq is NULL");
     if (n > 0 && (!p || !g)) return fail(LHIP_E_NULL, "sgd_step: NULL params/grads");
-    if (momentum > 0.f && n > 0 && !v) return fail(LHIP_E_NULL, "sgd_step: momentum > 0 needs a velocity buffer");
+    if ((momentum > 0.f || hyper_dev) && n > 0 && !v)
+        return fail(LHIP_E_NULL, "sgd_step: momentum > 0 needs a velocity buffer");
     const int cus = st().cu_count > 0 ? st().cu_count : 256;
     long long blocks = (n + 255) / 256;
     if (blocks > 4LL * cus) blocks = 4LL * cus;
     if (blocks < 1) blocks = 1;
     sgd_step_kernel<<<static_cast<int>(blocks), 256, 0, s>>>(p, g, v, n, sumsq_dev, lr, momentum, wd, grad_scale,
-                                                           clip_norm, nesterov, gnorm_out, applied_out);
+                                                           clip_norm, nesterov, gnorm_out, applied_out, hyper_dev);
     return check_launch("sgd_step");
 }
 
@@ -169,7 +174,7 @@ LHIP_API int lhip_sgd_step(float* params, float* grads, float* velocity, long lo
 {
     LHIP_REQUIRE_READY();
     return lhip::sgd_step(params, grads, velocity, n, grad_sumsq, lr, momentum, weight_decay, grad_scale, clip_norm,
-                          nesterov, grad_norm_out, applied_out, st().stream);
+                          nesterov, grad_norm_out, applied_out, st().stream, nullptr);
 }
 
 LHIP_API int lhip_sum(const float* x, int n, float scale, float* out)

@@ -210,7 +210,8 @@ colsum_kernel(const float* __restrict__ partial, float* __restrict__ out, int np
 // Row r keeps columns [0, lim): lim = cols, or with the (group-)causal mask
 // lim = clamp((r % group) + 1 + offset, 1, cols) (tensor2.lua:332-383 with
 // Lua's 1-based lim = i + offset; luaTL_softmax_ex's row % group).  Masked
-// entries are exactly 0.  y = softmax(scale * x) over the kept prefix.
+// entries are exactly 0.  y = softmax(scale * x) over the kept prefix.  x and
+// y must not overlap (the kernels are compiled with __restrict__).
 __device__ __forceinline__ int softmax_lim(int row, int cols, int causal, int offset, int group)
 {
     if (!causal) return cols;
@@ -359,7 +360,7 @@ softmax_bwd_generic(const float* __restrict__ y, const float* __restrict__ dy, f
 // (tensor2.lua:809-882 per row; cuda/luaTL_train.cu:837-878 contract.)
 template <int NT, int NV>
 __global__ void __launch_bounds__(NT)
-ce_fused_vec(const float* __restrict__ logits, const int* __restrict__ tgt, float* __restrict__ losses,
+ce_fused_vec(const float* logits, const int* __restrict__ tgt, float* __restrict__ losses,
              float* dlogits, int rows, int V, int ignore_index, float gscale)
 {
     constexpr int NW = NT / 64;
@@ -420,7 +421,7 @@ ce_fused_vec(const float* __restrict__ logits, const int* __restrict__ tgt, floa
 }
 
 __global__ void __launch_bounds__(256)
-ce_fused_generic(const float* __restrict__ logits, const int* __restrict__ tgt, float* __restrict__ losses,
+ce_fused_generic(const float* logits, const int* __restrict__ tgt, float* __restrict__ losses,
                  float* dlogits, int rows, int V, int ignore_index, float gscale)
 {
     __shared__ float red[4];

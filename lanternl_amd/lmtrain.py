@@ -1,0 +1,151 @@
+"""The CPU LMTrain step (optimizer "sgd") run on the GPU through lhip_lm_*.
+
+Host-side mirror of the parts of ai/optim/lmtrain.lua that feed one optimizer
+step: ``build_windows`` (lmtrain.lua:535-558) cuts token sequences into
+(input, target) windows, and ``GpuLMStep.step`` runs the batch body of
+LMTrain:run (lmtrain.lua:1183-1227) for ``batch`` windows: forward, mean CE
+per window, backward, grads scaled by 1/batch, global-norm skip and clip, and
+the SGD update (optim2.lua:48-102), all on the device.  Ids are 0-based here
+(Lua's are 1-based).
+
+Windows must be full (``seq`` tokens each); the reference's shorter trailing
+window of a sequence is not supported by the device step.
+"""
+import ctypes
+
+import numpy as np
+
+from . import device
+from ._lib import LmConfig, LmStats, call, lib
+
+PARAM_NAMES_PER_LAYER = ("ln1", "wq", "wk", "wv", "wo", "ln2", "w1", "w3", "w2")
+
+
+def build_windows(sequences, max_seq, stride=None):
+    """[(inp, tgt, n)] exactly as lmtrain.lua:535-558 (0-based lists)."""
+    stride = stride or max_seq
+    windows = []
+    for seq in sequences:
+        n_tok = len(seq)
+        start = 0
+        while start < n_tok - 1:
+            stop = min(start + max_seq, n_tok - 1)
+            inp = list(seq[start:stop])
+            tgt = list(seq[start + 1:stop + 1])
+            if inp:
+                windows.append((inp, tgt, len(inp)))
+            if stop >= n_tok - 1:
+                break
+            start += stride
+    return windows
+
+
+def config(vocab, dim, layers, heads, ffn, batch, seq, causal=True, eps=1e-5, rope_base=10000.0):
+    return LmConfig(vocab, dim, layers, heads, ffn, int(bool(causal)), eps, rope_base, batch, seq)
+
+
+def param_table(cfg):
+    """[(name, offset, rows, cols)] in Transformer:parameters() order."""
+    n = 2 + 9 * cfg.layers
+    offs = (ctypes.c_longlong * n)()
+    rows = (ctypes.c_int * n)()
+    cols = (ctypes.c_int * n)()
+    call("lhip_lm_param_offsets", ctypes.byref(cfg), offs, rows, cols)
+    names = ["emb"] + [f"{p}.{l}" for l in range(cfg.layers) for p in PARAM_NAMES_PER_LAYER] + ["lnf"]
+    return [(names[i], offs[i], rows[i], cols[i]) for i in range(n)]
+
+
+def num_params(cfg):
+    n = lib().lhip_lm_num_params(ctypes.byref(cfg))
+    if n < 0:
+        raise ValueError("invalid LM config")
+    return n
+
+
+def init_params(cfg, rng, std=0.02):
+    """All weight matrices N(0, std), RMSNorm gains 1 (the synthetic C2 init)."""
+    p = np.zeros(num_params(cfg), dtype=np.float32)
+    for name, off, r, c in param_table(cfg):
+        if name.startswith(("ln1", "ln2", "lnf")):
+            p[off:off + r * c] = 1.0
+        else:
+            p[off:off + r * c] = rng.normal(0.0, std, r * c)
+    return p
+
+
+class GpuLMStep:
+    """Device-resident model + SGD state for one LMTrain configuration."""
+
+    def __init__(self, vocab, dim, layers, heads, ffn, batch, seq, causal=True, eps=1e-5, rope_base=10000.0):
+        device.init(0)
+        self.cfg = config(vocab, dim, layers, heads, ffn, batch, seq, causal, eps, rope_base)
+        self.batch, self.seq = batch, seq
+        self.n = num_params(self.cfg)
+        self._h = ctypes.c_void_p()
+        call("lhip_lm_create", ctypes.byref(self.cfg), ctypes.byref(self._h))
+
+    # -- state ---------------------------------------------------------------
+    def _vec(self, name, arr=None):
+        if arr is None:
+            out = np.empty(self.n, dtype=np.float32)
+            call(name, self._h, out.ctypes.data, self.n)
+            return out
+        a = np.ascontiguousarray(arr, dtype=np.float32).reshape(-1)
+        if a.size != self.n:
+            raise ValueError(f"{a.size} values given, model has {self.n}")
+        call(name, self._h, a.ctypes.data, self.n)
+        return None
+
+    def set_params(self, p):
+        self._vec("lhip_lm_set_params", p)
+
+    def params(self):
+        return self._vec("lhip_lm_get_params")
+
+    def grads(self):
+        return self._vec("lhip_lm_get_grads")
+
+    def set_velocity(self, v):
+        self._vec("lhip_lm_set_velocity", v)
+
+    def velocity(self):
+        return self._vec("lhip_lm_get_velocity")
+
+    def set_batch(self, ids, targets):
+        ids = np.ascontiguousarray(ids, dtype=np.int32).reshape(-1)
+        tgt = np.ascontiguousarray(targets, dtype=np.int32).reshape(-1)
+        if ids.size != self.batch * self.seq or tgt.size != ids.size:
+            raise ValueError(f"expected {self.batch}x{self.seq} ids and targets")
+        call("lhip_lm_set_batch", self._h, ids.ctypes.data, tgt.ctypes.data)
+
+    def use_graph(self, on=True):
+        call("lhip_lm_use_graph", self._h, int(bool(on)))
+
+    # -- the step --------------------------------------------------------------
+    def step(self, lr, momentum=0.9, weight_decay=0.01, clip_norm=1.0, nesterov=False):
+        """Enqueue one optimizer step (asynchronous; stats() waits)."""
+        call("lhip_lm_step_sgd", self._h, float(lr), float(momentum), float(weight_decay),
+             float(clip_norm), int(bool(nesterov)))
+
+    def stats(self):
+        st = LmStats()
+        wl = np.zeros(self.batch, dtype=np.float32)
+        call("lhip_lm_stats", self._h, ctypes.byref(st), wl.ctypes.data, self.batch)
+        return {"loss": float(st.loss), "window_losses": wl.astype(np.float64), "grad_norm": float(st.grad_norm),
+                "applied": bool(st.applied), "correct": int(st.correct), "steps": int(st.steps)}
+
+    def argmax(self):
+        out = np.empty(self.batch * self.seq, dtype=np.int32)
+        call("lhip_lm_get_argmax", self._h, out.ctypes.data, out.size)
+        return out
+
+    def close(self):
+        if self._h is not None and self._h.value:
+            lib().lhip_lm_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
