@@ -1,14 +1,18 @@
 #!/usr/bin/env python3
 """Benchmark of the lanternl MI355X backend on one GPU.
 
-Default: times the hot path on synthetic data and prints ONE JSON line with the
-metric of BASELINE.json, a `roofline` object for the dominant kernel (timed
-live with hipEvents on the library stream) and a `cpu_baseline` object (the
-CPU oracle -- a single-threaded C restatement of lanternl's pure-Lua loops --
-timed on a bounded sample on this host).
+Default workload ("C2"): one full LMTrain step --
+forward, cross-entropy, backward and the SGD update -- for vocab 2000, dim 128,
+4 layers, 8 heads, ffn 256, 8 windows x 64 tokens, resident on the GPU and
+replayed as a hipGraph.  Prints ONE JSON line: steps/s, a `roofline` object
+for the step's dominant kernel (timed live with hipEvents on the library
+stream), and a `cpu_baseline` object (the CPU oracle -- a single-threaded C
+restatement of lanternl's pure-Lua loops in double -- timed on this host).
 
-  python bench.py [--steps K] [--warmup W] [--workload gemm4096]
-  python bench.py --suite gemm       # config C5 sweep, one JSON line per shape
+  python bench.py [--steps K] [--warmup W]
+  python bench.py --workload gemm4096      # the 4096^3 fp32 GEMM (C5) instead
+  python bench.py --suite gemm             # C1/C3/C5 GEMM shapes, one JSON line each
+  python bench.py --suite bandwidth        # C3/C4 bandwidth kernels, one JSON line each
 
 Only one GPU is used; --gpus above 1 exits with a message.
 """
@@ -29,6 +33,8 @@ if ROOT not in sys.path:
 PEAK_FP32_MFMA_TFLOPS = 157.3   # MI355X dense fp32 matrix, published
 PEAK_HBM_GBPS = 8000.0          # MI355X HBM3E, published
 METRIC = "fp32 GEMM TFLOP/s and % of MFMA peak; LMTrain steps/sec at 1 MI355X"
+C2 = dict(vocab=2000, dim=128, layers=4, heads=8, ffn=256, batch=8, seq=64)
+MALL_BYTES = 256 << 20          # Infinity Cache: rotate working sets past it
 
 
 def _cpu_model():
@@ -43,21 +49,22 @@ def _cpu_model():
 
 
 def time_launches(fn, steps, warmup):
-    """Average ms per call of fn() over `steps` back-to-back calls, bracketed by
+    """Average ms per call of fn(i) over `steps` back-to-back calls, bracketed by
     hipEvents recorded on the library stream (where fn enqueues its kernels)."""
     from lanternl_amd import device
-    for _ in range(warmup):
-        fn()
+    for i in range(warmup):
+        fn(i)
     device.sync()
     t = device.Timer()
     t.start()
-    for _ in range(steps):
-        fn()
+    for i in range(steps):
+        fn(i)
     t.stop()
     device.sync()
     return t.ms() / steps
 
 
+# ----------------------------------------------------------------------- GEMM
 def bench_gemm(m, n, k, ta=False, tb=False, steps=20, warmup=3, seed=0):
     from lanternl_amd import device, kernels
     rng = np.random.default_rng(seed)
@@ -67,7 +74,7 @@ def bench_gemm(m, n, k, ta=False, tb=False, steps=20, warmup=3, seed=0):
     B = device.Buffer.from_numpy(rng.uniform(-1, 1, b_shape).astype(np.float32))
     C = device.Buffer((m, n))
 
-    def run():
+    def run(_):
         kernels.sgemm(A, B, C, transa=ta, transb=tb)
     ms = time_launches(run, steps, warmup)
     flops = 2.0 * m * n * k
@@ -77,7 +84,7 @@ def bench_gemm(m, n, k, ta=False, tb=False, steps=20, warmup=3, seed=0):
             "bytes": 4.0 * (m * k + k * n + m * n)}
 
 
-def cpu_baseline_gemm(n=512, reps=2):
+def cpu_baseline_gemm(n=512, reps=4):
     """The CPU oracle's matrix.lua `mm` loop order (double, 1 thread), n^3."""
     import oracle as O
     rng = np.random.default_rng(0)
@@ -89,15 +96,81 @@ def cpu_baseline_gemm(n=512, reps=2):
         O.mm(a, b)
     dt = (time.perf_counter() - t0) / reps
     return {"value": 2.0 * n ** 3 / dt / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
-            "sample": f"{reps}x {n}^3 double GEMM, matrix.lua mm i-p-j order (C restatement, "
-                      f"not LuaJIT), {_cpu_model()}"}
+            "sample": f"{reps}x {n}^3 double GEMM in matrix.lua's mm loop order (C restatement of the "
+                      f"Lua loop, not LuaJIT: LuaJIT is not installed), {_cpu_model()}"}
+
+
+# ------------------------------------------------------------ LMTrain step (C2)
+# The step's dominant kernel at C2 (from the rocprofv3 kernel trace of this
+# workload): the tied-head backward GEMM dxf = dlogits . emb, an NN product of
+# [B*T, vocab] x [vocab, dim].  It is timed alone, with the step's shapes, on
+# the library stream.
+def dominant_kernel_c2(steps, warmup):
+    r = bench_gemm(C2["batch"] * C2["seq"], C2["dim"], C2["vocab"], steps=max(steps, 50), warmup=warmup)
+    return r
+
+
+def cpu_baseline_lm(nsteps=5):
+    import oracle as O
+    cfg = O.lm_cfg(C2["vocab"], C2["dim"], C2["layers"], C2["heads"], C2["ffn"])
+    rng = np.random.default_rng(0)
+    n = O.lm_num_params(cfg)
+    p = rng.normal(0, 0.02, n).astype(np.float32).astype(np.float64)
+    v = np.zeros(n)
+    ids = rng.integers(0, C2["vocab"], (C2["batch"], C2["seq"])).astype(np.int32)
+    tgt = rng.integers(0, C2["vocab"], (C2["batch"], C2["seq"])).astype(np.int32)
+    t0 = time.perf_counter()
+    for _ in range(nsteps):
+        O.lm_step_sgd(cfg, p, v, ids, tgt, 0.1)
+    dt = (time.perf_counter() - t0) / nsteps
+    return {"value": 1.0 / dt, "unit": "steps/s", "cores": 1, "kind": "port",
+            "sample": f"{nsteps} full C2 LMTrain SGD steps (8 windows x 64 tokens, fwd+bwd+update) of the "
+                      f"double-precision C restatement of the Lua CPU path (not LuaJIT: LuaJIT is not "
+                      f"installed), {_cpu_model()}"}
+
+
+def run_lm_workload(args):
+    from lanternl_amd import device, lmtrain
+    device.init(0)
+    rng = np.random.default_rng(0)
+    gpu = lmtrain.GpuLMStep(**C2)
+    gpu.set_params(lmtrain.init_params(gpu.cfg, rng, 0.02))
+    gpu.set_batch(rng.integers(0, C2["vocab"], (C2["batch"], C2["seq"])),
+                  rng.integers(0, C2["vocab"], (C2["batch"], C2["seq"])))
+    gpu.use_graph(not args.eager)
+
+    def step(_):
+        gpu.step(0.1, 0.9, 0.01, 1.0)
+    ms = time_launches(step, args.steps, args.warmup)
+    st = gpu.stats()
+    if not np.isfinite(st["loss"]):
+        raise RuntimeError(f"non-finite loss after the timed steps: {st}")
+    dom = dominant_kernel_c2(args.steps, args.warmup)
+    flops = 3 * 1_000_341_504 * 1.0   # GEMM flops of one fwd+bwd step (forward x 3)
+    line = {
+        "metric": METRIC, "value": 1000.0 / ms, "unit": "steps/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic: token ids/targets uniform in [0,2000), weights N(0,0.02), gains 1",
+        "config": {"workload": "lmtrain_step_c2 (BASELINE configs[1]): one SGD step, fwd+CE+bwd+update",
+                   **C2, "optimizer": "sgd(lr=0.1, momentum=0.9, wd=0.01, clip=1.0)",
+                   "graph_replay": not args.eager},
+        "step_gemm_tflops": flops / (ms * 1e-3) / 1e12,
+        "last_step": {"loss": st["loss"], "grad_norm": st["grad_norm"], "applied": st["applied"]},
+        "roofline": {"bound": "mfma", "achieved": dom["tflops"], "peak": PEAK_FP32_MFMA_TFLOPS,
+                     "unit": "TFLOP/s", "frac": dom["frac"], "traffic": None,
+                     "kernel": f"sgemm NN {dom['m']}x{dom['n']}x{dom['k']} (tied-head dX = dlogits . emb)",
+                     "kernel_ms": dom["ms"]},
+        "cpu_baseline": cpu_baseline_lm(),
+    }
+    gpu.close()
+    print(json.dumps(line), flush=True)
 
 
 def run_gemm_workload(args):
     from lanternl_amd import device
     device.init(0)
     r = bench_gemm(4096, 4096, 4096, steps=args.steps, warmup=args.warmup)
-    cpu = cpu_baseline_gemm()
     line = {
         "metric": METRIC, "value": r["tflops"], "unit": "TFLOP/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": r["ms"],
@@ -106,7 +179,7 @@ def run_gemm_workload(args):
         "config": {"workload": "gemm_nn_4096^3 (config C5)", "m": 4096, "n": 4096, "k": 4096},
         "roofline": {"bound": "mfma", "achieved": r["tflops"], "peak": PEAK_FP32_MFMA_TFLOPS,
                      "unit": "TFLOP/s", "frac": r["frac"], "traffic": None},
-        "cpu_baseline": cpu,
+        "cpu_baseline": cpu_baseline_gemm(),
     }
     print(json.dumps(line), flush=True)
 
@@ -118,21 +191,106 @@ def run_gemm_suite(args):
     cases += [(m, 4096, 4096, False, False) for m in (1, 16, 64)]
     cases += [(4096, 4096, 4096, True, False), (4096, 4096, 4096, False, True)]
     cases += [(256, 256, 128, False, False), (256, 256, 128, True, False), (256, 256, 128, False, True)]
+    # C3: LM head logits, dW (A^T.B) and dhidden (A.B^T)
+    cases += [(512, 32000, 128, False, False), (128, 32000, 512, True, False), (512, 128, 32000, False, True)]
     for m, n, k, ta, tb in cases:
-        steps = max(3, min(args.steps, int(2e12 / (2.0 * m * n * k)) + 3))
+        steps = max(5, min(args.steps, int(4e12 / (2.0 * m * n * k)) + 5))
         r = bench_gemm(m, n, k, ta, tb, steps=steps, warmup=args.warmup)
-        if m < 128:
-            r["hbm_gbps"] = r["bytes"] / (r["ms"] * 1e-3) / 1e9
+        r["hbm_gbps_algorithmic"] = r["bytes"] / (r["ms"] * 1e-3) / 1e9
         print(json.dumps({"suite": "gemm", **r}), flush=True)
+
+
+# ------------------------------------------------------------ bandwidth kernels
+def bench_bandwidth(name, nbytes, make_set, launch, steps, warmup):
+    """Rotate over enough independent buffer sets that one pass over them
+    exceeds the 256 MB Infinity Cache, so the timed traffic is HBM traffic."""
+    nsets = max(2, -(-2 * MALL_BYTES // int(nbytes)))
+    sets = [make_set(i) for i in range(nsets)]
+
+    def run(i):
+        launch(sets[i % nsets])
+    ms = time_launches(run, steps, warmup)
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    return {"suite": "bandwidth", "kernel": name, "ms": ms, "bytes": nbytes, "gbps": gbps,
+            "frac": gbps / PEAK_HBM_GBPS, "buffer_sets": nsets}
+
+
+def run_bandwidth_suite(args):
+    from lanternl_amd import device
+    from lanternl_amd._lib import call
+    device.init(0)
+    rng = np.random.default_rng(0)
+    B = device.Buffer
+    T, Dm, Fm = 4096, 1024, 4096
+
+    def arr(*shape, scale=1.0, loc=0.0):
+        return B.from_numpy((rng.standard_normal(shape) * scale + loc).astype(np.float32))
+
+    out = []
+    steps, warm = max(args.steps, 20), args.warmup
+    # RMSNorm 4096 x 1024 (eps 1e-6, gain N(1, 0.1))
+    w = arr(Dm, scale=0.1, loc=1.0)
+    nb = 4 * (2 * T * Dm + Dm + T)
+    out.append(bench_bandwidth("rmsnorm_fwd 4096x1024", nb,
+                               lambda i: (arr(T, Dm), B((T, Dm)), B((T,))),
+                               lambda s: call("lhip_rmsnorm_fwd", s[0].ptr, w.ptr, s[1].ptr, s[2].ptr, T, Dm, 1e-6),
+                               steps, warm))
+    nb = 4 * (3 * T * Dm + 2 * Dm + T)
+    inv = B.from_numpy(np.ones(T, np.float32))
+    dw = B((Dm,))
+    out.append(bench_bandwidth("rmsnorm_bwd 4096x1024", nb,
+                               lambda i: (arr(T, Dm), arr(T, Dm), B((T, Dm))),
+                               lambda s: call("lhip_rmsnorm_bwd", s[0].ptr, w.ptr, inv.ptr, s[1].ptr, s[2].ptr,
+                                              dw.ptr, T, Dm, 0),
+                               steps, warm))
+    # RoPE 4096 tokens x 16 heads x 64, base 1e4, in place (fwd and inverse)
+    nb = 4 * 2 * T * 16 * 64
+    for inverse in (0, 1):
+        out.append(bench_bandwidth(f"rope_{'bwd' if inverse else 'fwd'} 4096x16x64", nb,
+                                   lambda i: (arr(T, 16 * 64),),
+                                   lambda s, inv_=inverse: call("lhip_rope", s[0].ptr, None, T, 16, 64, 16 * 64, 0, 0,
+                                                                10000.0, 0, inv_),
+                                   steps, warm))
+    # SwiGLU 4096 x 4096
+    n = T * Fm
+    out.append(bench_bandwidth("swiglu_fwd 4096x4096", 4 * 3 * n,
+                               lambda i: (arr(T, Fm), arr(T, Fm), B((T, Fm))),
+                               lambda s: call("lhip_swiglu_fwd", s[0].ptr, Fm, s[1].ptr, Fm, s[2].ptr, Fm, T, Fm),
+                               steps, warm))
+    out.append(bench_bandwidth("swiglu_bwd 4096x4096", 4 * 5 * n,
+                               lambda i: (arr(T, Fm), arr(T, Fm), arr(T, Fm), B((T, Fm)), B((T, Fm))),
+                               lambda s: call("lhip_swiglu_bwd", s[0].ptr, Fm, s[1].ptr, Fm, s[2].ptr, Fm, s[3].ptr,
+                                              Fm, s[4].ptr, Fm, T, Fm, 0),
+                               steps, warm))
+    # row softmax 4096 x 4096, scores N(0, 4)
+    out.append(bench_bandwidth("softmax_fwd 4096x4096", 4 * 2 * n,
+                               lambda i: (arr(T, T, scale=2.0), B((T, T))),
+                               lambda s: call("lhip_softmax_fwd", s[0].ptr, s[1].ptr, T, T, 1.0, 0, 0, 0),
+                               steps, warm))
+    out.append(bench_bandwidth("softmax_bwd 4096x4096", 4 * 3 * n,
+                               lambda i: (arr(T, T), arr(T, T), B((T, T))),
+                               lambda s: call("lhip_softmax_bwd", s[0].ptr, s[1].ptr, s[2].ptr, T, T, 1.0, 0, 0, 0, 0),
+                               steps, warm))
+    # C3 fused softmax + CE: 512 x 32000 logits, labels uniform
+    R, V = 512, 32000
+    labels = B.from_numpy(rng.integers(0, V, R).astype(np.int32), np.int32)
+    out.append(bench_bandwidth("ce_fused 512x32000", 4 * (2 * R * V + 2 * R),
+                               lambda i: (arr(R, V), B((R, V)), B((R,))),
+                               lambda s: call("lhip_ce_fused", s[0].ptr, labels.ptr, s[2].ptr, s[1].ptr, R, V, -1,
+                                              1.0 / R),
+                               steps, warm))
+    for r in out:
+        print(json.dumps(r), flush=True)
 
 
 def main():
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=50)
-    p.add_argument("--warmup", type=int, default=5)
-    p.add_argument("--workload", default="gemm4096", choices=["gemm4096"])
-    p.add_argument("--suite", default=None, choices=["gemm"])
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--workload", default="lmtrain_c2", choices=["lmtrain_c2", "gemm4096"])
+    p.add_argument("--eager", action="store_true", help="launch the LM step kernel by kernel, no graph")
+    p.add_argument("--suite", default=None, choices=["gemm", "bandwidth"])
     args = p.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py: this build measures ONE GPU only (asked for {args.gpus}); "
@@ -141,8 +299,12 @@ def main():
         sys.exit(2)
     if args.suite == "gemm":
         run_gemm_suite(args)
-    else:
+    elif args.suite == "bandwidth":
+        run_bandwidth_suite(args)
+    elif args.workload == "gemm4096":
         run_gemm_workload(args)
+    else:
+        run_lm_workload(args)
 
 
 if __name__ == "__main__":

@@ -28,6 +28,8 @@
 // Edge tiles (any M, N, K) use bounds-checked scalar loads with zero fill and
 // checked stores; unaligned operands (ld % 4 != 0 or a base not 16-byte
 // aligned) always take the scalar path.
+#include <algorithm>
+
 #include "lhip_internal.h"
 
 namespace lhip {
@@ -120,7 +122,8 @@ sgemm_mfma_kernel(int M, int N, int K, float alpha,
                   const float* __restrict__ B, int ldb, long long sB, float beta,
                   float* __restrict__ C, int ldc, long long sC,
                   int tiles_m, int tiles_n, int vecA, int vecB,
-                  int inner, long long sA2, long long sB2, long long sC2)
+                  int inner, long long sA2, long long sB2, long long sC2,
+                  int kchunk, float* __restrict__ ws)
 {
     constexpr int WM = BM / 2, WN = BN / 2;        // 2x2 waves
     constexpr int FM = WM / 32, FN = WN / 32;      // 32x32 MFMA blocks per wave
@@ -156,11 +159,14 @@ sgemm_mfma_kernel(int M, int N, int K, float alpha,
     // op(B) tile is BK x BN.  Stored (!TB) K x N -> tile (k, n); (TB) N x K -> tile (n, k).
     TileRegs<TB ? BN : BK, TB ? BK : BN> rb;
 
+    // split-K: this workgroup reduces k in [kbeg, kend) (kchunk = K when unsplit)
+    const int kbeg = blockIdx.z * kchunk;
+    const int kend = min(K, kbeg + kchunk);
     auto gload = [&](int k0) {
-        if (TA) ra.load(A, lda, k0, m0, K, M, vecA, tid);
-        else    ra.load(A, lda, m0, k0, M, K, vecA, tid);
-        if (TB) rb.load(B, ldb, n0, k0, N, K, vecB, tid);
-        else    rb.load(B, ldb, k0, n0, K, N, vecB, tid);
+        if (TA) ra.load(A, lda, k0, m0, kend, M, vecA, tid);
+        else    ra.load(A, lda, m0, k0, M, kend, vecA, tid);
+        if (TB) rb.load(B, ldb, n0, k0, N, kend, vecB, tid);
+        else    rb.load(B, ldb, k0, n0, kend, N, vecB, tid);
     };
     auto lstore = [&](int buf) {
         if (TA) ra.template store_direct<LDA>(As[buf], tid);
@@ -177,16 +183,16 @@ sgemm_mfma_kernel(int M, int N, int K, float alpha,
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-    const int nk = (K + BK - 1) / BK;
+    const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
     if (nk > 0) {
-        gload(0);
+        gload(kbeg);
         lstore(0);
         __syncthreads();
     }
     for (int kt = 0; kt < nk; ++kt) {
         const int cur = kt & 1;
         const bool more = kt + 1 < nk;
-        if (more) gload((kt + 1) * BK);
+        if (more) gload(kbeg + (kt + 1) * BK);
         const float* as = As[cur];
         const float* bs = Bs[cur];
 #pragma unroll
@@ -208,6 +214,23 @@ sgemm_mfma_kernel(int M, int N, int K, float alpha,
 
     // Accumulator layout of a 32x32 block: element r of lane l sits at
     // row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+    if (ws) {
+        // split-K partial: dense [split][batch][M][N] slice, reduced by splitk_reduce
+        float* wz = ws + (static_cast<long long>(blockIdx.z) * gridDim.y + blockIdx.y) * M * static_cast<long long>(N);
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                const int col = n0 + wn + 32 * j + lr;
+                if (col >= N) continue;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int row = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * lk + (r & 3);
+                    if (row < M) wz[static_cast<long long>(row) * N + col] = acc[i][j][r];
+                }
+            }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -226,25 +249,54 @@ sgemm_mfma_kernel(int M, int N, int K, float alpha,
         }
 }
 
+// C = alpha * sum_s ws[s] + beta * C, the splits summed in order (deterministic).
+__global__ void __launch_bounds__(256)
+splitk_reduce(const float* __restrict__ ws, int splits, int batch, int M, int N, float alpha, float beta,
+              float* __restrict__ C, int ldc, long long sC, int inner, long long sC2)
+{
+    const long long mn = static_cast<long long>(M) * N;
+    const long long total = mn * batch;
+    const long long stride = static_cast<long long>(gridDim.x) * blockDim.x;
+    for (long long idx = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x; idx < total; idx += stride) {
+        const long long z = idx / mn, rc = idx - z * mn;
+        const int row = static_cast<int>(rc / N), col = static_cast<int>(rc - static_cast<long long>(row) * N);
+        float sum = 0.f;
+        for (int p = 0; p < splits; ++p) sum += ws[(static_cast<long long>(p) * batch + z) * mn + rc];
+        float* dst = C + (z / inner) * sC2 + (z % inner) * sC + static_cast<long long>(row) * ldc + col;
+        const float v = alpha * sum;
+        *dst = (beta != 0.f) ? v + beta * (*dst) : v;
+    }
+}
+
 template <int BM, int BN, int BK>
 int launch_cfg(int ta, int tb, int m, int n, int k, float alpha, const float* A, int lda, long long sA,
                const float* B, int ldb, long long sB, float beta, float* C, int ldc, long long sC,
-               int batch, int vecA, int vecB, const GemmBatch2& b2, hipStream_t stream)
+               int batch, int vecA, int vecB, const GemmBatch2& b2, hipStream_t stream,
+               int splits = 1, int kchunk = 0, float* ws = nullptr)
 {
     const int tiles_m = ceil_div(m, BM), tiles_n = ceil_div(n, BN);
     const long long nwg = static_cast<long long>(tiles_m) * tiles_n;
     if (nwg > 0x7fffffffLL) return fail(LHIP_E_CAPACITY, "sgemm: %lld workgroups exceed the grid limit", nwg);
-    dim3 grid(static_cast<unsigned>(nwg), batch, 1), block(kThreads, 1, 1);
+    if (splits <= 1) { splits = 1; kchunk = k; ws = nullptr; }
+    dim3 grid(static_cast<unsigned>(nwg), batch, splits), block(kThreads, 1, 1);
 #define LHIP_GEMM_LAUNCH(TA_, TB_)                                                             \
     sgemm_mfma_kernel<BM, BN, BK, TA_, TB_><<<grid, block, 0, stream>>>(                        \
         m, n, k, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC, tiles_m, tiles_n, vecA, vecB, \
-        b2.inner, b2.sA2, b2.sB2, b2.sC2)
+        b2.inner, b2.sA2, b2.sB2, b2.sC2, kchunk, ws)
     if (!ta && !tb) LHIP_GEMM_LAUNCH(false, false);
     else if (ta && !tb) LHIP_GEMM_LAUNCH(true, false);
     else if (!ta && tb) LHIP_GEMM_LAUNCH(false, true);
     else LHIP_GEMM_LAUNCH(true, true);
 #undef LHIP_GEMM_LAUNCH
-    return check_launch("sgemm: kernel launch");
+    int rc = check_launch("sgemm: kernel launch");
+    if (rc != LHIP_OK || !ws) return rc;
+    const long long total = static_cast<long long>(m) * n * batch;
+    long long rg = (total + 255) / 256;
+    const long long cap = static_cast<long long>(st().cu_count > 0 ? st().cu_count : 256) * 4;
+    if (rg > cap) rg = cap;
+    splitk_reduce<<<static_cast<int>(rg), 256, 0, stream>>>(ws, splits, batch, m, n, alpha, beta, C, ldc, sC,
+                                                            b2.inner, b2.sC2);
+    return check_launch("sgemm: split-K reduce");
 }
 
 }  // namespace
@@ -259,10 +311,31 @@ int sgemm_launch(int ta, int tb, int m, int n, int k, float alpha,
     return sgemm_launch2(ta, tb, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc, batch, sA, sB, sC, b2, stream);
 }
 
+int splitk_plan(int m, int n, int k, int batch, size_t ws_floats, int* kchunk_out)
+{
+    // Only the 64x64-tile configuration (fewer tiles than CUs) is split.
+    constexpr int BM = 64, BN = 64, BK = 32;
+    const int cus = st().cu_count > 0 ? st().cu_count : 256;
+    const long long tiles = static_cast<long long>(ceil_div(m, BM)) * ceil_div(n, BN) * batch;
+    const long long big_tiles = static_cast<long long>(ceil_div(m, 128)) * ceil_div(n, 128) * batch;
+    if (big_tiles >= cus || tiles >= cus || k < 4 * BK) return 1;
+    long long s = (2LL * cus + tiles - 1) / tiles;        // aim at ~2 workgroups per CU
+    s = std::min<long long>(s, k / (2 * BK));              // >= 2 K tiles per split
+    s = std::min<long long>(s, 64);
+    const long long mnb = static_cast<long long>(m) * n * batch;
+    if (mnb > 0) s = std::min<long long>(s, static_cast<long long>(ws_floats / mnb));
+    if (s < 2) return 1;
+    int kchunk = ceil_div(ceil_div(k, s), BK) * BK;
+    const int splits = ceil_div(k, kchunk);
+    if (splits < 2) return 1;
+    *kchunk_out = kchunk;
+    return splits;
+}
+
 int sgemm_launch2(int ta, int tb, int m, int n, int k, float alpha,
                   const float* A, int lda, const float* B, int ldb, float beta,
                   float* C, int ldc, int batch, long long sA, long long sB, long long sC,
-                  const GemmBatch2& b2, hipStream_t stream)
+                  const GemmBatch2& b2, hipStream_t stream, float* ws, size_t ws_floats)
 {
     if (m < 0 || n < 0 || k < 0 || batch < 0)
         return fail(LHIP_E_SHAPE, "sgemm: negative size (m=%d n=%d k=%d batch=%d)", m, n, k, batch);
@@ -291,8 +364,10 @@ int sgemm_launch2(int ta, int tb, int m, int n, int k, float alpha,
     if (big_tiles >= cus)
         return launch_cfg<128, 128, 32>(ta, tb, m, n, k, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC,
                                         batch, vecA, vecB, b2, stream);
+    int kchunk = 0;
+    const int splits = ws ? splitk_plan(m, n, k, batch, ws_floats, &kchunk) : 1;
     return launch_cfg<64, 64, 32>(ta, tb, m, n, k, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC,
-                                  batch, vecA, vecB, b2, stream);
+                                  batch, vecA, vecB, b2, stream, splits, kchunk, splits > 1 ? ws : nullptr);
 }
 
 }  // namespace lhip
@@ -302,13 +377,35 @@ using lhip::st;
 
 extern "C" {
 
+// Immediate calls: split-K partials live in the library workspace (sized here,
+// before any launch).
+static int sgemm_immediate(int transa, int transb, int m, int n, int k, float alpha, const float* A, int lda,
+                           long long sA, const float* B, int ldb, long long sB, float beta, float* C, int ldc,
+                           long long sC, int batch)
+{
+    float* ws = nullptr;
+    size_t ws_floats = 0;
+    int kchunk = 0;
+    if (m > 0 && n > 0 && k > 0 && batch > 0) {
+        const int splits = lhip::splitk_plan(m, n, k, batch, static_cast<size_t>(1) << 26, &kchunk);
+        if (splits > 1) {
+            ws_floats = static_cast<size_t>(splits) * m * n * batch;
+            int rc = lhip::workspace(ws_floats * sizeof(float), reinterpret_cast<void**>(&ws));
+            if (rc != LHIP_OK) return rc;
+        }
+    }
+    lhip::GemmBatch2 b2;
+    b2.inner = batch > 0 ? batch : 1;
+    return lhip::sgemm_launch2(transa, transb, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc, batch, sA, sB, sC, b2,
+                               st().stream, ws, ws_floats);
+}
+
 LHIP_API int lhip_sgemm(int transa, int transb, int m, int n, int k, float alpha,
                         const float* A, int lda, const float* B, int ldb, float beta,
                         float* C, int ldc)
 {
     LHIP_REQUIRE_READY();
-    return lhip::sgemm_launch(transa, transb, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc,
-                              1, 0, 0, 0, st().stream);
+    return sgemm_immediate(transa, transb, m, n, k, alpha, A, lda, 0, B, ldb, 0, beta, C, ldc, 0, 1);
 }
 
 LHIP_API int lhip_sgemm_strided_batched(int transa, int transb, int m, int n, int k, float alpha,
@@ -317,8 +414,8 @@ LHIP_API int lhip_sgemm_strided_batched(int transa, int transb, int m, int n, in
                                         float* C, int ldc, long long strideC, int batch)
 {
     LHIP_REQUIRE_READY();
-    return lhip::sgemm_launch(transa, transb, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc,
-                              batch, strideA, strideB, strideC, st().stream);
+    return sgemm_immediate(transa, transb, m, n, k, alpha, A, lda, strideA, B, ldb, strideB, beta, C, ldc, strideC,
+                           batch);
 }
 
 LHIP_API int lhip_matmul_host(int op, const double* a, const double* b, double* c,

@@ -108,10 +108,15 @@ struct GemmBatch2 {
     long long sA2 = 0, sB2 = 0, sC2 = 0;
 };
 
+// ws / ws_floats (optional): device scratch for split-K partials.  Shapes with
+// fewer output tiles than CUs and a long K are split over K into up to 64
+// slices written to ws and summed in order by a second kernel (deterministic).
 int sgemm_launch2(int transa, int transb, int m, int n, int k, float alpha,
                   const float* A, int lda, const float* B, int ldb, float beta,
                   float* C, int ldc, int batch, long long sA, long long sB, long long sC,
-                  const GemmBatch2& b2, hipStream_t stream);
+                  const GemmBatch2& b2, hipStream_t stream, float* ws = nullptr, size_t ws_floats = 0);
+// Number of K splits sgemm_launch2 would use (1 = none); *kchunk receives the slice length.
+int splitk_plan(int m, int n, int k, int batch, size_t ws_floats, int* kchunk);
 
 int sgemm_launch(int transa, int transb, int m, int n, int k, float alpha,
                  const float* A, int lda, const float* B, int ldb, float beta,

@@ -62,6 +62,8 @@ struct LmModel {
     float *dxf = nullptr, *dx = nullptr, *da = nullptr, *dzu = nullptr, *dh2 = nullptr, *dctx = nullptr;
     float *dP = nullptr, *dS = nullptr, *dqkv = nullptr, *dh = nullptr, *work = nullptr;
     size_t work_floats = 0;
+    float* splitk = nullptr;      // split-K partials of the small-tile GEMMs
+    size_t splitk_floats = 0;
     // graph
     bool use_graph = false;
     hipGraph_t graph = nullptr;
@@ -114,12 +116,17 @@ struct Enq {
     int gemm(int ta, int tb, int M, int Nn, int K, const float* A, int lda, const float* Bm, int ldb, float beta,
              float* C, int ldc) const
     {
-        return sgemm_launch(ta, tb, M, Nn, K, 1.f, A, lda, Bm, ldb, beta, C, ldc, 1, 0, 0, 0, s);
+        GemmBatch2 b2;
+        return sgemm_launch2(ta, tb, M, Nn, K, 1.f, A, lda, Bm, ldb, beta, C, ldc, 1, 0, 0, 0, b2, s, m.splitk,
+                             m.splitk_floats);
     }
     int bgemm(int ta, int tb, int M, int Nn, int K, const float* A, int lda, long long sa, const float* Bm, int ldb,
               long long sb, float beta, float* C, int ldc, long long sc, int batch) const
     {
-        return sgemm_launch(ta, tb, M, Nn, K, 1.f, A, lda, Bm, ldb, beta, C, ldc, batch, sa, sb, sc, s);
+        GemmBatch2 b2;
+        b2.inner = batch;
+        return sgemm_launch2(ta, tb, M, Nn, K, 1.f, A, lda, Bm, ldb, beta, C, ldc, batch, sa, sb, sc, b2, s,
+                             m.splitk, m.splitk_floats);
     }
     // batch (window b, head h): operand offsets b*X2 + h*X
     int hgemm(int ta, int tb, int M, int Nn, int K, const float* A, int lda, long long sa, long long sa2,
@@ -129,7 +136,8 @@ struct Enq {
         GemmBatch2 b2;
         b2.inner = m.H;
         b2.sA2 = sa2; b2.sB2 = sb2; b2.sC2 = sc2;
-        return sgemm_launch2(ta, tb, M, Nn, K, 1.f, A, lda, Bm, ldb, 0.f, C, ldc, m.B * m.H, sa, sb, sc, b2, s);
+        return sgemm_launch2(ta, tb, M, Nn, K, 1.f, A, lda, Bm, ldb, 0.f, C, ldc, m.B * m.H, sa, sb, sc, b2, s,
+                             m.splitk, m.splitk_floats);
     }
     int copy(float* dst, const float* src, long long n) const
     {
@@ -351,6 +359,7 @@ LHIP_API int lhip_lm_create(const lhip_lm_config_t* cfg, void** model)
     const long long ND = N * D, NF = N * F, PL = static_cast<long long>(m->B) * m->H * m->T * m->T;
     m->ss_blocks = lhip::sumsq_blocks(m->nparam);
     m->work_floats = static_cast<size_t>(lhip::rmsnorm_bwd_parts(m->N, m->D)) * m->D;
+    m->splitk_floats = static_cast<size_t>(1) << 23;   // 32 MiB; the planner caps splits to fit
     // carve every buffer out of one allocation, each 256-byte aligned
     struct Slot { void** dst; size_t bytes; };
     std::vector<Slot> slots = {
@@ -391,6 +400,7 @@ LHIP_API int lhip_lm_create(const lhip_lm_config_t* cfg, void** model)
         {reinterpret_cast<void**>(&m->dqkv), sizeof(float) * 3 * ND},
         {reinterpret_cast<void**>(&m->dh), sizeof(float) * ND},
         {reinterpret_cast<void**>(&m->work), sizeof(float) * m->work_floats},
+        {reinterpret_cast<void**>(&m->splitk), sizeof(float) * m->splitk_floats},
     };
     size_t total = 0;
     for (auto& sl : slots) total += (sl.bytes + 255) & ~static_cast<size_t>(255);

@@ -195,15 +195,26 @@ rmsnorm_bwd_generic(const float* __restrict__ x, const float* __restrict__ w, co
     }
 }
 
-// dw[c] = (acc ? dw[c] : 0) + sum_b partial[b][c], b ascending (deterministic).
+// dw[c] = (acc ? dw[c] : 0) + sum_b partial[b][c] in a fixed order: 64 columns
+// per block, 4 thread groups each summing every 4th partial row (independent,
+// unrolled loads), then the 4 group sums added in group order.  Deterministic.
 __global__ void __launch_bounds__(256)
 colsum_kernel(const float* __restrict__ partial, float* __restrict__ out, int nparts, int cols, int acc)
 {
-    const int c = blockIdx.x * blockDim.x + threadIdx.x;
-    if (c >= cols) return;
+    __shared__ float red[4][64];
+    const int cl = threadIdx.x & 63, g = threadIdx.x >> 6;
+    const int c = blockIdx.x * 64 + cl;
     float s = 0.f;
-    for (int b = 0; b < nparts; ++b) s += partial[static_cast<size_t>(b) * cols + c];
-    out[c] = acc ? out[c] + s : s;
+    if (c < cols) {
+#pragma unroll 8
+        for (int b = g; b < nparts; b += 4) s += partial[static_cast<size_t>(b) * cols + c];
+    }
+    red[g][cl] = s;
+    __syncthreads();
+    if (g == 0 && c < cols) {
+        const float t = (red[0][cl] + red[1][cl]) + (red[2][cl] + red[3][cl]);
+        out[c] = acc ? out[c] + t : t;
+    }
 }
 
 // ------------------------------------------------------------- row softmax
@@ -514,15 +525,21 @@ int rmsnorm_fwd(const float* x, const float* w, float* y, float* inv, int rows, 
     return check_launch("rmsnorm_fwd");
 }
 
+// Workgroups of the backward: each wave walks >= 4 rows, at most one block per CU.
+int rmsnorm_bwd_blocks(int rows)
+{
+    const int cus = st().cu_count > 0 ? st().cu_count : 256;
+    int blocks = ceil_div(rows, 4 * kWavesPerBlock);
+    if (blocks > cus) blocks = cus;
+    return blocks < 1 ? 1 : blocks;
+}
+
 // Upper bound on the partial-dw rows the backward uses (workspace = parts * cols
 // floats): one per block on the register-resident path, one per wave otherwise.
 int rmsnorm_bwd_parts(int rows, int cols)
 {
     (void)cols;
-    const int cus = st().cu_count > 0 ? st().cu_count : 256;
-    int blocks = row_blocks(rows);
-    if (blocks > cus) blocks = cus;
-    return blocks * kWavesPerBlock;
+    return rmsnorm_bwd_blocks(rows) * kWavesPerBlock;
 }
 
 int rmsnorm_bwd(const float* x, const float* w, const float* inv, const float* dy, float* dx, float* dw,
@@ -531,9 +548,7 @@ int rmsnorm_bwd(const float* x, const float* w, const float* inv, const float* d
     if (rows < 0 || cols <= 0) return fail(LHIP_E_SHAPE, "rmsnorm_bwd: rows=%d cols=%d", rows, cols);
     if (rows == 0) return LHIP_OK;
     if (!x || !w || !inv || !dy || !dx) return fail(LHIP_E_NULL, "rmsnorm_bwd: NULL argument");
-    const int cus = st().cu_count > 0 ? st().cu_count : 256;
-    int blocks = row_blocks(rows);
-    if (blocks > cus) blocks = cus;
+    const int blocks = rmsnorm_bwd_blocks(rows);
     const int nv = nv_for(cols);
     const bool vec = nv && cols % 4 == 0 && aligned16(x) && aligned16(w) && aligned16(dy) && aligned16(dx);
     const int parts = vec ? blocks : blocks * kWavesPerBlock;
@@ -551,7 +566,7 @@ int rmsnorm_bwd(const float* x, const float* w, const float* inv, const float* d
     else rmsnorm_bwd_vec<16><<<g, b, lds, s>>>(x, w, inv, dy, dx, partial, rows, cols, accumulate);
     int rc = check_launch("rmsnorm_bwd");
     if (rc != LHIP_OK || !dw) return rc;
-    colsum_kernel<<<ceil_div(cols, 256), 256, 0, s>>>(partial, dw, parts, cols, accumulate);
+    colsum_kernel<<<ceil_div(cols, 64), 256, 0, s>>>(partial, dw, parts, cols, accumulate);
     return check_launch("rmsnorm_bwd: dw reduce");
 }
 

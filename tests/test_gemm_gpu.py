@@ -230,3 +230,45 @@ def test_matmul_host_accumulate_in_double():
     call("lhip_matmul_host", 0, a.ctypes.data_as(ctypes.c_void_p), b.ctypes.data_as(ctypes.c_void_p),
          out.ctypes.data_as(ctypes.c_void_p), 20, 30, 10, 1)
     assert rel_fro(out, expect) <= TOL
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1)])
+def test_gemm_c3_lm_head_shapes(ta, tb):
+    """Config C3: logits = hidden(512x128) . W(128x32000); dW = hidden^T . dlogits;
+    dhidden = dlogits . W^T (K = 32000, the split-K path)."""
+    announce("gemm C3", ta, tb)
+    rng = np.random.default_rng(30 + 2 * ta + tb)
+    hidden = rng.standard_normal((512, 128)).astype(np.float32)
+    W = (rng.standard_normal((128, 32000)) * 0.02).astype(np.float32)
+    dlog = (rng.standard_normal((512, 32000)) * 1e-3).astype(np.float32)
+    if (ta, tb) == (0, 0):
+        a, b, ref = hidden, W, hidden.astype(np.float64) @ W.astype(np.float64)
+    elif (ta, tb) == (1, 0):
+        a, b, ref = hidden, dlog, hidden.T.astype(np.float64) @ dlog.astype(np.float64)
+    else:
+        a, b, ref = dlog, W, dlog.astype(np.float64) @ W.T.astype(np.float64)
+    got = _gemm(bool(ta), bool(tb), a, b)
+    assert rel_fro(got, ref) <= TOL
+
+
+@pytest.mark.parametrize("m,n,k,batch", [(512, 128, 2000, 1), (128, 128, 4096, 3), (64, 64, 1000, 2),
+                                         (33, 70, 999, 1), (1, 4096, 4096, 1)])
+def test_gemm_split_k_alpha_beta_batched(m, n, k, batch):
+    """Shapes with fewer output tiles than CUs and long K take the split-K path;
+    alpha/beta apply once, after the ordered sum of the slices."""
+    announce("gemm split-k", m, n, k, batch)
+    rng = np.random.default_rng(m + n + k)
+    a = f32(rng.uniform(-1, 1, (batch, m, k)))
+    b = f32(rng.uniform(-1, 1, (batch, k, n)))
+    c0 = f32(rng.uniform(-1, 1, (batch, m, n)))
+    A, B, C = to_dev(a), to_dev(b), to_dev(c0)
+    kernels.sgemm_strided_batched(0, 0, m, n, k, 0.5, A.ptr, k, m * k, B.ptr, n, k * n, -2.0, C.ptr, n, m * n, batch)
+    device.sync()
+    got = C.download().astype(np.float64)
+    for z in range(batch):
+        assert rel_fro(got[z], 0.5 * (a[z] @ b[z]) - 2.0 * c0[z]) <= TOL
+    # deterministic: the same call twice gives bit-identical results
+    C2 = to_dev(c0)
+    kernels.sgemm_strided_batched(0, 0, m, n, k, 0.5, A.ptr, k, m * k, B.ptr, n, k * n, -2.0, C2.ptr, n, m * n, batch)
+    device.sync()
+    assert np.array_equal(C2.download(), C.download())
