@@ -38,6 +38,7 @@ namespace {
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int kThreads = 256;  // 4 wave64s
+constexpr int kSmallU = 8;     // K steps whose loads the small kernel issues together
 
 // Loads a ROWS x COLS tile of a row-major matrix into registers, float4 per
 // thread per pass, consecutive threads walking the contiguous dimension.
@@ -115,15 +116,48 @@ __device__ __forceinline__ void tile_coords(int pid, int nwg, int tiles_m, int t
     tn = in_group / gsz;
 }
 
+// Kernel arguments (one struct: the launch passes it by value).
+struct GemmArgs {
+    int M, N, K;
+    float alpha, beta;
+    const float* A; int lda; long long sA, sA2;
+    const float* B; int ldb; long long sB, sB2;
+    float* C; int ldc; long long sC, sC2;
+    const float* R; int ldr;          // the beta term reads R (R == C unless a residual is given)
+    int tiles_m, tiles_n, vecA, vecB, inner;
+    int splits, kchunk;               // split-K: blockIdx.z = slice, K range [z*kchunk, (z+1)*kchunk)
+    float* ws;                        // split-K partials [split][batch][M][N]
+};
+
+// C = alpha * sum_s ws[s] + beta * R, the slices summed in order (deterministic).
+__global__ void __launch_bounds__(256)
+splitk_reduce(const GemmArgs g, int batch)
+{
+    const long long mn = static_cast<long long>(g.M) * g.N;
+    const long long total = mn * batch;
+    const long long pstride = mn * batch;
+    const long long stride = static_cast<long long>(gridDim.x) * blockDim.x;
+    for (long long idx = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x; idx < total; idx += stride) {
+        const long long z = idx / mn, rc = idx - z * mn;
+        const int row = static_cast<int>(rc / g.N), col = static_cast<int>(rc - static_cast<long long>(row) * g.N);
+        float sum = 0.f;
+        const float* src = g.ws + idx;
+        for (int p = 0; p < g.splits; ++p) sum += src[p * pstride];
+        const long long coff = (z / g.inner) * g.sC2 + (z % g.inner) * g.sC;
+        float* dst = g.C + coff + static_cast<long long>(row) * g.ldc + col;
+        const float v = g.alpha * sum;
+        if (g.beta != 0.f) {
+            const float* r = g.R ? g.R + coff + static_cast<long long>(row) * g.ldr + col : dst;
+            *dst = v + g.beta * (*r);
+        } else {
+            *dst = v;
+        }
+    }
+}
+
 template <int BM, int BN, int BK, bool TA, bool TB>
 __global__ void __launch_bounds__(kThreads)
-sgemm_mfma_kernel(int M, int N, int K, float alpha,
-                  const float* __restrict__ A, int lda, long long sA,
-                  const float* __restrict__ B, int ldb, long long sB, float beta,
-                  float* __restrict__ C, int ldc, long long sC,
-                  int tiles_m, int tiles_n, int vecA, int vecB,
-                  int inner, long long sA2, long long sB2, long long sC2,
-                  int kchunk, float* __restrict__ ws)
+sgemm_mfma_kernel(const GemmArgs g)
 {
     constexpr int WM = BM / 2, WN = BN / 2;        // 2x2 waves
     constexpr int FM = WM / 32, FN = WN / 32;      // 32x32 MFMA blocks per wave
@@ -135,6 +169,7 @@ sgemm_mfma_kernel(int M, int N, int K, float alpha,
     __shared__ float As[2][BK * LDA];
     __shared__ float Bs[2][BK * LDB];
 
+    const int M = g.M, N = g.N;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -142,13 +177,13 @@ sgemm_mfma_kernel(int M, int N, int K, float alpha,
     const int lk = lane >> 5;   // which of the two k of an MFMA step
 
     int tm, tn;
-    tile_coords(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+    tile_coords(blockIdx.x, gridDim.x, g.tiles_m, g.tiles_n, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
     // two-level batch: z = outer * inner + inner_index (e.g. window x head)
-    const long long zo = blockIdx.y / inner, zi = blockIdx.y % inner;
-    A += zo * sA2 + zi * sA;
-    B += zo * sB2 + zi * sB;
-    C += zo * sC2 + zi * sC;
+    const long long zo = blockIdx.y / g.inner, zi = blockIdx.y % g.inner;
+    const float* __restrict__ A = g.A + zo * g.sA2 + zi * g.sA;
+    const float* __restrict__ B = g.B + zo * g.sB2 + zi * g.sB;
+    const long long coff = zo * g.sC2 + zi * g.sC;
 
     const int wm = (wave >> 1) * WM;
     const int wn = (wave & 1) * WN;
@@ -160,13 +195,13 @@ sgemm_mfma_kernel(int M, int N, int K, float alpha,
     TileRegs<TB ? BN : BK, TB ? BK : BN> rb;
 
     // split-K: this workgroup reduces k in [kbeg, kend) (kchunk = K when unsplit)
-    const int kbeg = blockIdx.z * kchunk;
-    const int kend = min(K, kbeg + kchunk);
+    const int kbeg = blockIdx.z * g.kchunk;
+    const int kend = min(g.K, kbeg + g.kchunk);
     auto gload = [&](int k0) {
-        if (TA) ra.load(A, lda, k0, m0, kend, M, vecA, tid);
-        else    ra.load(A, lda, m0, k0, M, kend, vecA, tid);
-        if (TB) rb.load(B, ldb, n0, k0, N, kend, vecB, tid);
-        else    rb.load(B, ldb, k0, n0, kend, N, vecB, tid);
+        if (TA) ra.load(A, g.lda, k0, m0, kend, M, g.vecA, tid);
+        else    ra.load(A, g.lda, m0, k0, M, kend, g.vecA, tid);
+        if (TB) rb.load(B, g.ldb, n0, k0, N, kend, g.vecB, tid);
+        else    rb.load(B, g.ldb, k0, n0, kend, N, g.vecB, tid);
     };
     auto lstore = [&](int buf) {
         if (TA) ra.template store_direct<LDA>(As[buf], tid);
@@ -214,9 +249,12 @@ sgemm_mfma_kernel(int M, int N, int K, float alpha,
 
     // Accumulator layout of a 32x32 block: element r of lane l sits at
     // row 8*(r/4) + 4*(l/32) + r%4, column l%32.
-    if (ws) {
-        // split-K partial: dense [split][batch][M][N] slice, reduced by splitk_reduce
-        float* wz = ws + (static_cast<long long>(blockIdx.z) * gridDim.y + blockIdx.y) * M * static_cast<long long>(N);
+    if (g.splits > 1) {
+        // split-K partial of this slice: dense [split][batch][M][N], summed in
+        // slice order by splitk_reduce (a second launch: a device-scope fence
+        // inside this kernel would have to write back the per-XCD L2)
+        float* wz = g.ws + (static_cast<long long>(blockIdx.z) * gridDim.y + blockIdx.y) *
+                               (static_cast<long long>(M) * N);
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -231,6 +269,9 @@ sgemm_mfma_kernel(int M, int N, int K, float alpha,
             }
         return;
     }
+    float* __restrict__ C = g.C + coff;
+    const float* R = g.R ? g.R + coff : C;
+    const int ldr = g.R ? g.ldr : g.ldc;
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -241,101 +282,228 @@ sgemm_mfma_kernel(int M, int N, int K, float alpha,
             for (int r = 0; r < 16; ++r) {
                 const int row = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * lk + (r & 3);
                 if (row < M) {
-                    float* dst = C + static_cast<long long>(row) * ldc + col;
-                    const float v = alpha * acc[i][j][r];
-                    *dst = (beta != 0.f) ? v + beta * (*dst) : v;
+                    const float v = g.alpha * acc[i][j][r];
+                    C[static_cast<long long>(row) * g.ldc + col] =
+                        (g.beta != 0.f) ? v + g.beta * R[static_cast<long long>(row) * ldr + col] : v;
                 }
             }
         }
 }
 
-// C = alpha * sum_s ws[s] + beta * C, the splits summed in order (deterministic).
-__global__ void __launch_bounds__(256)
-splitk_reduce(const float* __restrict__ ws, int splits, int batch, int M, int N, float alpha, float beta,
-              float* __restrict__ C, int ldc, long long sC, int inner, long long sC2)
+// ---------------------------------------------------------------------------
+// Small problems (fewer 64x64 output tiles than CUs, e.g. every GEMM of the
+// C2 LMTrain step): one workgroup per 32x32 output tile, and the four waves of
+// the workgroup split K among themselves -- wave w takes the 8-deep K steps
+// w, w+4, w+8, ... -- each accumulating the whole 32x32 tile, so one tile's
+// K loop runs on all four SIMDs of its CU.  The partial tiles are summed in
+// LDS in wave order (deterministic).  Operands are loaded straight from
+// global memory into MFMA fragments: for an 8-deep K step, lane l (row or
+// column l%32, half h = l/32) holds op(A)[row][k0+4h .. k0+4h+3] and
+// op(B)[k0+4h .. k0+4h+3][col]; MFMA i of the step multiplies element i of
+// both, so the two halves of one v_mfma_f32_32x32x2f32 cover k0+i and
+// k0+4+i and the four MFMAs cover k0 .. k0+7 exactly once.  The contiguous
+// operand dimension is read as float4 when aligned, otherwise element-wise.
+template <bool TA, bool TB>
+__global__ void __launch_bounds__(kThreads)
+sgemm_small_kernel(const GemmArgs g)
 {
-    const long long mn = static_cast<long long>(M) * N;
-    const long long total = mn * batch;
-    const long long stride = static_cast<long long>(gridDim.x) * blockDim.x;
-    for (long long idx = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x; idx < total; idx += stride) {
-        const long long z = idx / mn, rc = idx - z * mn;
-        const int row = static_cast<int>(rc / N), col = static_cast<int>(rc - static_cast<long long>(row) * N);
-        float sum = 0.f;
-        for (int p = 0; p < splits; ++p) sum += ws[(static_cast<long long>(p) * batch + z) * mn + rc];
-        float* dst = C + (z / inner) * sC2 + (z % inner) * sC + static_cast<long long>(row) * ldc + col;
-        const float v = alpha * sum;
-        *dst = (beta != 0.f) ? v + beta * (*dst) : v;
+    __shared__ float red[4][16][64];
+    const int M = g.M, N = g.N;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int lr = lane & 31;
+    const int h = lane >> 5;
+    const int tm = blockIdx.x / g.tiles_n, tn = blockIdx.x % g.tiles_n;
+    const int m0 = tm * 32, n0 = tn * 32;
+    const long long zo = blockIdx.y / g.inner, zi = blockIdx.y % g.inner;
+    const float* __restrict__ A = g.A + zo * g.sA2 + zi * g.sA;
+    const float* __restrict__ B = g.B + zo * g.sB2 + zi * g.sB;
+    const long long coff = zo * g.sC2 + zi * g.sC;
+    const int kbeg = blockIdx.z * g.kchunk;
+    const int kend = min(g.K, kbeg + g.kchunk);
+    const int row = m0 + lr;      // this lane's A row
+    const int col = n0 + lr;      // this lane's B column
+    const bool rok = row < M, cok = col < N;
+
+    floatx16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+
+    // Each pass issues the loads of kSmallU K steps before any of their MFMAs,
+    // so that many loads are in flight per wave (these launches have few
+    // workgroups: latency, not bandwidth, bounds them).
+    constexpr int U = kSmallU;
+    for (int kp = kbeg + 8 * wave; kp < kend; kp += 32 * U) {
+        float a[U][4], b[U][4];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int kb = kp + 32 * u + 4 * h;   // first of this lane's four k
+            const bool kfull = kb + 3 < kend;
+            if (!TA) {
+                const float* src = A + static_cast<long long>(row) * g.lda + kb;
+                if (g.vecA && rok && kfull) {
+                    const float4 v = *reinterpret_cast<const float4*>(src);
+                    a[u][0] = v.x; a[u][1] = v.y; a[u][2] = v.z; a[u][3] = v.w;
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) a[u][i] = (rok && kb + i < kend) ? src[i] : 0.f;
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    a[u][i] = (rok && kb + i < kend) ? A[static_cast<long long>(kb + i) * g.lda + row] : 0.f;
+            }
+            if (!TB) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    b[u][i] = (cok && kb + i < kend) ? B[static_cast<long long>(kb + i) * g.ldb + col] : 0.f;
+            } else {
+                const float* src = B + static_cast<long long>(col) * g.ldb + kb;
+                if (g.vecB && cok && kfull) {
+                    const float4 v = *reinterpret_cast<const float4*>(src);
+                    b[u][0] = v.x; b[u][1] = v.y; b[u][2] = v.z; b[u][3] = v.w;
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) b[u][i] = (cok && kb + i < kend) ? src[i] : 0.f;
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[u][i], b[u][i], acc, 0, 0, 0);
+    }
+
+    // sum the four waves' tiles in wave order; thread (wave w, lane l) finishes
+    // accumulator registers 4w .. 4w+3 of lane l
+#pragma unroll
+    for (int r = 0; r < 16; ++r) red[wave][r][lane] = acc[r];
+    __syncthreads();
+    const int ocol = n0 + (lane & 31);
+    const int lk = lane >> 5;
+    float* wz = nullptr;
+    if (g.splits > 1)
+        wz = g.ws + (static_cast<long long>(blockIdx.z) * gridDim.y + blockIdx.y) * (static_cast<long long>(M) * N);
+    float* __restrict__ C = g.C + coff;
+    const float* R = g.R ? g.R + coff : C;
+    const int ldr = g.R ? g.ldr : g.ldc;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int r = 4 * wave + q;
+        const float v = ((red[0][r][lane] + red[1][r][lane]) + red[2][r][lane]) + red[3][r][lane];
+        const int orow = m0 + 8 * (r >> 2) + 4 * lk + (r & 3);
+        if (orow >= M || ocol >= N) continue;
+        if (wz) {
+            wz[static_cast<long long>(orow) * N + ocol] = v;
+        } else {
+            const float o = g.alpha * v;
+            C[static_cast<long long>(orow) * g.ldc + ocol] =
+                (g.beta != 0.f) ? o + g.beta * R[static_cast<long long>(orow) * ldr + ocol] : o;
+        }
     }
 }
 
-template <int BM, int BN, int BK>
-int launch_cfg(int ta, int tb, int m, int n, int k, float alpha, const float* A, int lda, long long sA,
-               const float* B, int ldb, long long sB, float beta, float* C, int ldc, long long sC,
-               int batch, int vecA, int vecB, const GemmBatch2& b2, hipStream_t stream,
-               int splits = 1, int kchunk = 0, float* ws = nullptr)
+template <bool TA, bool TB>
+void launch_small_t(const GemmArgs& g, dim3 grid, hipStream_t stream)
 {
-    const int tiles_m = ceil_div(m, BM), tiles_n = ceil_div(n, BN);
-    const long long nwg = static_cast<long long>(tiles_m) * tiles_n;
+    sgemm_small_kernel<TA, TB><<<grid, dim3(kThreads), 0, stream>>>(g);
+}
+
+int launch_reduce(const GemmArgs& g, int batch, hipStream_t stream);
+
+int launch_small(int ta, int tb, GemmArgs g, int batch, hipStream_t stream)
+{
+    g.tiles_m = ceil_div(g.M, 32);
+    g.tiles_n = ceil_div(g.N, 32);
+    const long long nwg = static_cast<long long>(g.tiles_m) * g.tiles_n;
     if (nwg > 0x7fffffffLL) return fail(LHIP_E_CAPACITY, "sgemm: %lld workgroups exceed the grid limit", nwg);
-    if (splits <= 1) { splits = 1; kchunk = k; ws = nullptr; }
-    dim3 grid(static_cast<unsigned>(nwg), batch, splits), block(kThreads, 1, 1);
-#define LHIP_GEMM_LAUNCH(TA_, TB_)                                                             \
-    sgemm_mfma_kernel<BM, BN, BK, TA_, TB_><<<grid, block, 0, stream>>>(                        \
-        m, n, k, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC, tiles_m, tiles_n, vecA, vecB, \
-        b2.inner, b2.sA2, b2.sB2, b2.sC2, kchunk, ws)
-    if (!ta && !tb) LHIP_GEMM_LAUNCH(false, false);
-    else if (ta && !tb) LHIP_GEMM_LAUNCH(true, false);
-    else if (!ta && tb) LHIP_GEMM_LAUNCH(false, true);
-    else LHIP_GEMM_LAUNCH(true, true);
-#undef LHIP_GEMM_LAUNCH
+    if (g.splits <= 1) { g.splits = 1; g.kchunk = g.K; g.ws = nullptr; }
+    dim3 grid(static_cast<unsigned>(nwg), batch, g.splits);
+    if (!ta && !tb) launch_small_t<false, false>(g, grid, stream);
+    else if (ta && !tb) launch_small_t<true, false>(g, grid, stream);
+    else if (!ta && tb) launch_small_t<false, true>(g, grid, stream);
+    else launch_small_t<true, true>(g, grid, stream);
+    int rc = check_launch("sgemm (small): kernel launch");
+    if (rc != LHIP_OK || g.splits <= 1) return rc;
+    return launch_reduce(g, batch, stream);
+}
+
+template <int BM, int BN, int BK>
+int launch_cfg(int ta, int tb, GemmArgs g, int batch, hipStream_t stream)
+{
+    g.tiles_m = ceil_div(g.M, BM);
+    g.tiles_n = ceil_div(g.N, BN);
+    const long long nwg = static_cast<long long>(g.tiles_m) * g.tiles_n;
+    if (nwg > 0x7fffffffLL) return fail(LHIP_E_CAPACITY, "sgemm: %lld workgroups exceed the grid limit", nwg);
+    if (g.splits <= 1) { g.splits = 1; g.kchunk = g.K; g.ws = nullptr; }
+    dim3 grid(static_cast<unsigned>(nwg), batch, g.splits), block(kThreads, 1, 1);
+    if (!ta && !tb) sgemm_mfma_kernel<BM, BN, BK, false, false><<<grid, block, 0, stream>>>(g);
+    else if (ta && !tb) sgemm_mfma_kernel<BM, BN, BK, true, false><<<grid, block, 0, stream>>>(g);
+    else if (!ta && tb) sgemm_mfma_kernel<BM, BN, BK, false, true><<<grid, block, 0, stream>>>(g);
+    else sgemm_mfma_kernel<BM, BN, BK, true, true><<<grid, block, 0, stream>>>(g);
     int rc = check_launch("sgemm: kernel launch");
-    if (rc != LHIP_OK || !ws) return rc;
-    const long long total = static_cast<long long>(m) * n * batch;
+    if (rc != LHIP_OK || g.splits <= 1) return rc;
+    return launch_reduce(g, batch, stream);
+}
+
+int launch_reduce(const GemmArgs& g, int batch, hipStream_t stream)
+{
+    const long long total = static_cast<long long>(g.M) * g.N * batch;
     long long rg = (total + 255) / 256;
     const long long cap = static_cast<long long>(st().cu_count > 0 ? st().cu_count : 256) * 4;
     if (rg > cap) rg = cap;
-    splitk_reduce<<<static_cast<int>(rg), 256, 0, stream>>>(ws, splits, batch, m, n, alpha, beta, C, ldc, sC,
-                                                            b2.inner, b2.sC2);
+    splitk_reduce<<<static_cast<int>(rg), 256, 0, stream>>>(g, batch);
     return check_launch("sgemm: split-K reduce");
 }
 
 }  // namespace
 
-int sgemm_launch(int ta, int tb, int m, int n, int k, float alpha,
-                 const float* A, int lda, const float* B, int ldb, float beta,
-                 float* C, int ldc, int batch, long long sA, long long sB, long long sC,
-                 hipStream_t stream)
-{
-    GemmBatch2 b2;
-    b2.inner = batch > 0 ? batch : 1;
-    return sgemm_launch2(ta, tb, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc, batch, sA, sB, sC, b2, stream);
-}
+// Below the 64x64-tile threshold, the 32x32 small kernel is used unless K is
+// long AND both output dimensions exceed 64: its 32-wide tiles re-read A N/32
+// times and B M/32 times, which for long K costs more L2/MALL traffic than
+// the 64x64 tiles (+ split-K) save in latency.
+bool use_small_kernel(int m, int n, int k) { return k <= 2048 || m <= 64 || n <= 64; }
 
 int splitk_plan(int m, int n, int k, int batch, size_t ws_floats, int* kchunk_out)
 {
-    // Only the 64x64-tile configuration (fewer tiles than CUs) is split.
-    constexpr int BM = 64, BN = 64, BK = 32;
     const int cus = st().cu_count > 0 ? st().cu_count : 256;
-    const long long tiles = static_cast<long long>(ceil_div(m, BM)) * ceil_div(n, BN) * batch;
+    const long long tiles64 = static_cast<long long>(ceil_div(m, 64)) * ceil_div(n, 64) * batch;
     const long long big_tiles = static_cast<long long>(ceil_div(m, 128)) * ceil_div(n, 128) * batch;
-    if (big_tiles >= cus || tiles >= cus || k < 4 * BK) return 1;
-    long long s = (2LL * cus + tiles - 1) / tiles;        // aim at ~2 workgroups per CU
-    s = std::min<long long>(s, k / (2 * BK));              // >= 2 K tiles per split
+    if (big_tiles >= cus || tiles64 >= cus) return 1;
+    long long tiles, min_k;
+    int unit;
+    if (use_small_kernel(m, n, k)) {
+        // 32x32 tiles, K shared by four waves: split only very long K (a wave
+        // covers K/4 at ~64 clocks per k; below 2048 the extra reduce launch
+        // costs more than it saves)
+        if (k < 2048) return 1;
+        tiles = static_cast<long long>(ceil_div(m, 32)) * ceil_div(n, 32) * batch;
+        unit = 32;
+        min_k = 512;
+    } else {
+        // 64x64 tiles, 32-deep K tiles walked by one workgroup
+        tiles = tiles64;
+        unit = 32;
+        min_k = 128;
+    }
+    long long s = (2LL * cus + tiles - 1) / tiles;          // aim at ~2 workgroups per CU
+    s = std::min<long long>(s, k / min_k);
     s = std::min<long long>(s, 64);
     const long long mnb = static_cast<long long>(m) * n * batch;
     if (mnb > 0) s = std::min<long long>(s, static_cast<long long>(ws_floats / mnb));
     if (s < 2) return 1;
-    int kchunk = ceil_div(ceil_div(k, s), BK) * BK;
+    const int kchunk = ceil_div(ceil_div(k, s), unit) * unit;
     const int splits = ceil_div(k, kchunk);
     if (splits < 2) return 1;
     *kchunk_out = kchunk;
     return splits;
 }
 
-int sgemm_launch2(int ta, int tb, int m, int n, int k, float alpha,
-                  const float* A, int lda, const float* B, int ldb, float beta,
-                  float* C, int ldc, int batch, long long sA, long long sB, long long sC,
-                  const GemmBatch2& b2, hipStream_t stream, float* ws, size_t ws_floats)
+int sgemm_run(int ta, int tb, int m, int n, int k, float alpha,
+              const float* A, int lda, long long sA, const float* B, int ldb, long long sB, float beta,
+              float* C, int ldc, long long sC, int batch, const GemmOpts& o, hipStream_t stream)
 {
     if (m < 0 || n < 0 || k < 0 || batch < 0)
         return fail(LHIP_E_SHAPE, "sgemm: negative size (m=%d n=%d k=%d batch=%d)", m, n, k, batch);
@@ -349,25 +517,44 @@ int sgemm_launch2(int ta, int tb, int m, int n, int k, float alpha,
     if (k > 0 && ldb < (b_cols > 0 ? b_cols : 1))
         return fail(LHIP_E_SHAPE, "sgemm: ldb=%d < %d", ldb, b_cols);
     if (ldc < n) return fail(LHIP_E_SHAPE, "sgemm: ldc=%d < n=%d", ldc, n);
+    if (o.R && o.ldr < n) return fail(LHIP_E_SHAPE, "sgemm: ldr=%d < n=%d", o.ldr, n);
     if (batch > 65535) return fail(LHIP_E_CAPACITY, "sgemm: batch %d > 65535", batch);
-    if (batch > 1 && (sA < 0 || sB < 0 || sC < 0 || b2.sA2 < 0 || b2.sB2 < 0 || b2.sC2 < 0))
+    if (batch > 1 && (sA < 0 || sB < 0 || sC < 0 || o.sA2 < 0 || o.sB2 < 0 || o.sC2 < 0))
         return fail(LHIP_E_SHAPE, "sgemm: negative batch stride");
-    if (b2.inner <= 0) return fail(LHIP_E_ARG, "sgemm: inner batch count must be > 0");
-    const int vecA = (k > 0 && lda % 4 == 0 && aligned16(A) &&
-                      (batch == 1 || (sA % 4 == 0 && b2.sA2 % 4 == 0))) ? 1 : 0;
-    const int vecB = (k > 0 && ldb % 4 == 0 && aligned16(B) &&
-                      (batch == 1 || (sB % 4 == 0 && b2.sB2 % 4 == 0))) ? 1 : 0;
-    // Large problems: 128x128 tiles (64x64 per wave).  When that leaves the
-    // chip with fewer workgroups than CUs, use 64x64 tiles for parallelism.
+    if (o.inner <= 0) return fail(LHIP_E_ARG, "sgemm: inner batch count must be > 0");
+    GemmArgs g{};
+    g.M = m; g.N = n; g.K = k; g.alpha = alpha; g.beta = beta;
+    g.A = A; g.lda = lda; g.sA = sA; g.sA2 = o.sA2;
+    g.B = B; g.ldb = ldb; g.sB = sB; g.sB2 = o.sB2;
+    g.C = C; g.ldc = ldc; g.sC = sC; g.sC2 = o.sC2;
+    g.R = o.R; g.ldr = o.ldr;
+    g.inner = o.inner;
+    g.vecA = (k > 0 && lda % 4 == 0 && aligned16(A) && (batch == 1 || (sA % 4 == 0 && o.sA2 % 4 == 0))) ? 1 : 0;
+    g.vecB = (k > 0 && ldb % 4 == 0 && aligned16(B) && (batch == 1 || (sB % 4 == 0 && o.sB2 % 4 == 0))) ? 1 : 0;
+    // Large problems: 128x128 tiles (64x64 per wave); mid-size: 64x64 tiles;
+    // small (fewer 64x64 tiles than CUs): 32x32 tiles with K shared by the
+    // four waves of a workgroup, split over workgroups when K is very long
+    // (split-K partials in o.ws).
     const long long big_tiles = static_cast<long long>(ceil_div(m, 128)) * ceil_div(n, 128) * batch;
     const int cus = st().cu_count > 0 ? st().cu_count : 256;
-    if (big_tiles >= cus)
-        return launch_cfg<128, 128, 32>(ta, tb, m, n, k, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC,
-                                        batch, vecA, vecB, b2, stream);
-    int kchunk = 0;
-    const int splits = ws ? splitk_plan(m, n, k, batch, ws_floats, &kchunk) : 1;
-    return launch_cfg<64, 64, 32>(ta, tb, m, n, k, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC,
-                                  batch, vecA, vecB, b2, stream, splits, kchunk, splits > 1 ? ws : nullptr);
+    if (big_tiles >= cus) return launch_cfg<128, 128, 32>(ta, tb, g, batch, stream);
+    const long long tiles64 = static_cast<long long>(ceil_div(m, 64)) * ceil_div(n, 64) * batch;
+    if (tiles64 >= cus) return launch_cfg<64, 64, 32>(ta, tb, g, batch, stream);
+    const bool small = use_small_kernel(m, n, k);
+    g.splits = o.ws ? splitk_plan(m, n, k, batch, o.ws_floats, &g.kchunk) : 1;
+    g.ws = o.ws;
+    if (small) return launch_small(ta, tb, g, batch, stream);
+    return launch_cfg<64, 64, 32>(ta, tb, g, batch, stream);
+}
+
+int sgemm_launch(int ta, int tb, int m, int n, int k, float alpha,
+                 const float* A, int lda, const float* B, int ldb, float beta,
+                 float* C, int ldc, int batch, long long sA, long long sB, long long sC,
+                 hipStream_t stream)
+{
+    GemmOpts o;
+    o.inner = batch > 0 ? batch : 1;
+    return sgemm_run(ta, tb, m, n, k, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC, batch, o, stream);
 }
 
 }  // namespace lhip
@@ -383,21 +570,19 @@ static int sgemm_immediate(int transa, int transb, int m, int n, int k, float al
                            long long sA, const float* B, int ldb, long long sB, float beta, float* C, int ldc,
                            long long sC, int batch)
 {
-    float* ws = nullptr;
-    size_t ws_floats = 0;
+    lhip::GemmOpts o;
+    o.inner = batch > 0 ? batch : 1;
     int kchunk = 0;
     if (m > 0 && n > 0 && k > 0 && batch > 0) {
         const int splits = lhip::splitk_plan(m, n, k, batch, static_cast<size_t>(1) << 26, &kchunk);
         if (splits > 1) {
-            ws_floats = static_cast<size_t>(splits) * m * n * batch;
-            int rc = lhip::workspace(ws_floats * sizeof(float), reinterpret_cast<void**>(&ws));
+            o.ws_floats = static_cast<size_t>(splits) * m * n * batch;
+            int rc = lhip::workspace(o.ws_floats * sizeof(float), reinterpret_cast<void**>(&o.ws));
             if (rc != LHIP_OK) return rc;
         }
     }
-    lhip::GemmBatch2 b2;
-    b2.inner = batch > 0 ? batch : 1;
-    return lhip::sgemm_launch2(transa, transb, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc, batch, sA, sB, sC, b2,
-                               st().stream, ws, ws_floats);
+    return lhip::sgemm_run(transa, transb, m, n, k, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC, batch, o,
+                           st().stream);
 }
 
 LHIP_API int lhip_sgemm(int transa, int transb, int m, int n, int k, float alpha,

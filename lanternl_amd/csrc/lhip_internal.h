@@ -101,21 +101,26 @@ int sgd_step(float* p, float* g, float* v, long long n, const double* sumsq_dev,
              hipStream_t s, const float* hyper_dev);
 int sum_f32(const float* x, int n, float scale, float* out, hipStream_t s);
 
-// Second batch level: blockIdx.y = outer * inner + i; operand X is offset by
-// outer * sX2 + i * sX (sX = the per-matrix strides of sgemm_launch).
-struct GemmBatch2 {
+// Options of the GEMM launcher.
+//   inner / s?2 : second batch level -- blockIdx.y = outer * inner + i and operand
+//                 X is offset by outer * sX2 + i * sX (e.g. window x head);
+//   R / ldr     : the beta term reads R instead of C (C = alpha*AB + beta*R);
+//   ws          : split-K.  Shapes with fewer output tiles than CUs and K >= 512
+//                 are split over K into up to 64 slices; partials go to ws and a
+//                 second kernel sums them in slice order (deterministic).
+struct GemmOpts {
     int inner = 1;
     long long sA2 = 0, sB2 = 0, sC2 = 0;
+    const float* R = nullptr;
+    int ldr = 0;
+    float* ws = nullptr;
+    size_t ws_floats = 0;
 };
 
-// ws / ws_floats (optional): device scratch for split-K partials.  Shapes with
-// fewer output tiles than CUs and a long K are split over K into up to 64
-// slices written to ws and summed in order by a second kernel (deterministic).
-int sgemm_launch2(int transa, int transb, int m, int n, int k, float alpha,
-                  const float* A, int lda, const float* B, int ldb, float beta,
-                  float* C, int ldc, int batch, long long sA, long long sB, long long sC,
-                  const GemmBatch2& b2, hipStream_t stream, float* ws = nullptr, size_t ws_floats = 0);
-// Number of K splits sgemm_launch2 would use (1 = none); *kchunk receives the slice length.
+int sgemm_run(int transa, int transb, int m, int n, int k, float alpha,
+              const float* A, int lda, long long sA, const float* B, int ldb, long long sB, float beta,
+              float* C, int ldc, long long sC, int batch, const GemmOpts& o, hipStream_t stream);
+// Number of K slices sgemm_run would use (1 = none); *kchunk receives the slice length.
 int splitk_plan(int m, int n, int k, int batch, size_t ws_floats, int* kchunk);
 
 int sgemm_launch(int transa, int transb, int m, int n, int k, float alpha,

@@ -113,36 +113,41 @@ struct Enq {
     LmModel& m;
     hipStream_t s;
 
+    GemmOpts opts(int inner = 1) const
+    {
+        GemmOpts o;
+        o.inner = inner;
+        o.ws = m.splitk;
+        o.ws_floats = m.splitk_floats;
+        return o;
+    }
     int gemm(int ta, int tb, int M, int Nn, int K, const float* A, int lda, const float* Bm, int ldb, float beta,
              float* C, int ldc) const
     {
-        GemmBatch2 b2;
-        return sgemm_launch2(ta, tb, M, Nn, K, 1.f, A, lda, Bm, ldb, beta, C, ldc, 1, 0, 0, 0, b2, s, m.splitk,
-                             m.splitk_floats);
+        return sgemm_run(ta, tb, M, Nn, K, 1.f, A, lda, 0, Bm, ldb, 0, beta, C, ldc, 0, 1, opts(), s);
+    }
+    // C = A.B + R (the residual add fused into the GEMM epilogue)
+    int gemm_res(int M, int Nn, int K, const float* A, int lda, const float* Bm, int ldb, const float* R, float* C,
+                 int ldc) const
+    {
+        GemmOpts o = opts();
+        o.R = R;
+        o.ldr = ldc;
+        return sgemm_run(0, 0, M, Nn, K, 1.f, A, lda, 0, Bm, ldb, 0, 1.f, C, ldc, 0, 1, o, s);
     }
     int bgemm(int ta, int tb, int M, int Nn, int K, const float* A, int lda, long long sa, const float* Bm, int ldb,
               long long sb, float beta, float* C, int ldc, long long sc, int batch) const
     {
-        GemmBatch2 b2;
-        b2.inner = batch;
-        return sgemm_launch2(ta, tb, M, Nn, K, 1.f, A, lda, Bm, ldb, beta, C, ldc, batch, sa, sb, sc, b2, s,
-                             m.splitk, m.splitk_floats);
+        return sgemm_run(ta, tb, M, Nn, K, 1.f, A, lda, sa, Bm, ldb, sb, beta, C, ldc, sc, batch, opts(batch), s);
     }
     // batch (window b, head h): operand offsets b*X2 + h*X
     int hgemm(int ta, int tb, int M, int Nn, int K, const float* A, int lda, long long sa, long long sa2,
               const float* Bm, int ldb, long long sb, long long sb2, float* C, int ldc, long long sc,
               long long sc2) const
     {
-        GemmBatch2 b2;
-        b2.inner = m.H;
-        b2.sA2 = sa2; b2.sB2 = sb2; b2.sC2 = sc2;
-        return sgemm_launch2(ta, tb, M, Nn, K, 1.f, A, lda, Bm, ldb, 0.f, C, ldc, m.B * m.H, sa, sb, sc, b2, s,
-                             m.splitk, m.splitk_floats);
-    }
-    int copy(float* dst, const float* src, long long n) const
-    {
-        hipError_t e = hipMemcpyAsync(dst, src, static_cast<size_t>(n) * sizeof(float), hipMemcpyDeviceToDevice, s);
-        return e == hipSuccess ? LHIP_OK : hip_fail(e, "lm: device copy");
+        GemmOpts o = opts(m.H);
+        o.sA2 = sa2; o.sB2 = sb2; o.sC2 = sc2;
+        return sgemm_run(ta, tb, M, Nn, K, 1.f, A, lda, sa, Bm, ldb, sb, 0.f, C, ldc, sc, m.B * m.H, o, s);
     }
 };
 
@@ -195,15 +200,13 @@ int enqueue_step(LmModel& m, hipStream_t s)
         // ctx[:, h*hd:] = P_bh . v_bh
         LM_TRY(q.hgemm(0, 0, T, hd, T, P, T, TT, HTT, qkv + 2 * ND, D, hd, TD, ctx, D, hd, TD));
         // x_mid = x + ctx . Wo
-        LM_TRY(q.copy(xmid, xl, ND));
-        LM_TRY(q.gemm(0, 0, N, D, D, ctx, D, m.prm(m.lt(l, P_WO)), D, 1.f, xmid, D));
+        LM_TRY(q.gemm_res(N, D, D, ctx, D, m.prm(m.lt(l, P_WO)), D, xl, xmid, D));
         LM_TRY(rmsnorm_fwd(xmid, m.prm(m.lt(l, P_LN2)), h2, inv2, N, D, eps, s));
         // z1 = h2.W1, u = h2.W3 (adjacent weights, one batched GEMM); a = silu(z1) * u
         LM_TRY(q.bgemm(0, 0, N, F, D, h2, D, 0, m.prm(m.lt(l, P_W1)), F, static_cast<long long>(D) * F, 0.f, zu, F, NF, 2));
         LM_TRY(swiglu_fwd(zu, F, zu + NF, F, a, F, N, F, s));
         // x_{l+1} = x_mid + a . W2
-        LM_TRY(q.copy(xn, xmid, ND));
-        LM_TRY(q.gemm(0, 0, N, D, F, a, F, m.prm(m.lt(l, P_W2)), D, 1.f, xn, D));
+        LM_TRY(q.gemm_res(N, D, F, a, F, m.prm(m.lt(l, P_W2)), D, xmid, xn, D));
     }
     const float* xL = m.x + static_cast<long long>(L) * ND;
     LM_TRY(rmsnorm_fwd(xL, lnf, m.xf, m.invf, N, D, eps, s));
