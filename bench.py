@@ -13,6 +13,7 @@ restatement of lanternl's pure-Lua loops in double -- timed on this host).
   python bench.py --workload gemm4096      # the 4096^3 fp32 GEMM (C5) instead
   python bench.py --suite gemm             # C1/C3/C5 GEMM shapes, one JSON line each
   python bench.py --suite bandwidth        # C3/C4 bandwidth kernels, one JSON line each
+  python bench.py --suite copy             # plain streaming kernel of known bytes (counter calibration)
 
 Only one GPU is used; --gpus above 1 exits with a message.
 """
@@ -201,9 +202,11 @@ def run_gemm_suite(args):
 
 
 # ------------------------------------------------------------ bandwidth kernels
-def bench_bandwidth(name, nbytes, make_set, launch, steps, warmup):
+def bench_bandwidth(name, nbytes, make_set, launch, steps, warmup, only=None):
     """Rotate over enough independent buffer sets that one pass over them
     exceeds the 256 MB Infinity Cache, so the timed traffic is HBM traffic."""
+    if only and only not in name:
+        return None
     nsets = max(2, -(-2 * MALL_BYTES // int(nbytes)))
     sets = [make_set(i) for i in range(nsets)]
 
@@ -234,7 +237,7 @@ def run_bandwidth_suite(args):
     out.append(bench_bandwidth("rmsnorm_fwd 4096x1024", nb,
                                lambda i: (arr(T, Dm), B((T, Dm)), B((T,))),
                                lambda s: call("lhip_rmsnorm_fwd", s[0].ptr, w.ptr, s[1].ptr, s[2].ptr, T, Dm, 1e-6),
-                               steps, warm))
+                               steps, warm, args.only))
     nb = 4 * (3 * T * Dm + 2 * Dm + T)
     inv = B.from_numpy(np.ones(T, np.float32))
     dw = B((Dm,))
@@ -242,7 +245,7 @@ def run_bandwidth_suite(args):
                                lambda i: (arr(T, Dm), arr(T, Dm), B((T, Dm))),
                                lambda s: call("lhip_rmsnorm_bwd", s[0].ptr, w.ptr, inv.ptr, s[1].ptr, s[2].ptr,
                                               dw.ptr, T, Dm, 0),
-                               steps, warm))
+                               steps, warm, args.only))
     # RoPE 4096 tokens x 16 heads x 64, base 1e4, in place (fwd and inverse)
     nb = 4 * 2 * T * 16 * 64
     for inverse in (0, 1):
@@ -250,27 +253,27 @@ def run_bandwidth_suite(args):
                                    lambda i: (arr(T, 16 * 64),),
                                    lambda s, inv_=inverse: call("lhip_rope", s[0].ptr, None, T, 16, 64, 16 * 64, 0, 0,
                                                                 10000.0, 0, inv_),
-                                   steps, warm))
+                                   steps, warm, args.only))
     # SwiGLU 4096 x 4096
     n = T * Fm
     out.append(bench_bandwidth("swiglu_fwd 4096x4096", 4 * 3 * n,
                                lambda i: (arr(T, Fm), arr(T, Fm), B((T, Fm))),
                                lambda s: call("lhip_swiglu_fwd", s[0].ptr, Fm, s[1].ptr, Fm, s[2].ptr, Fm, T, Fm),
-                               steps, warm))
+                               steps, warm, args.only))
     out.append(bench_bandwidth("swiglu_bwd 4096x4096", 4 * 5 * n,
                                lambda i: (arr(T, Fm), arr(T, Fm), arr(T, Fm), B((T, Fm)), B((T, Fm))),
                                lambda s: call("lhip_swiglu_bwd", s[0].ptr, Fm, s[1].ptr, Fm, s[2].ptr, Fm, s[3].ptr,
                                               Fm, s[4].ptr, Fm, T, Fm, 0),
-                               steps, warm))
+                               steps, warm, args.only))
     # row softmax 4096 x 4096, scores N(0, 4)
     out.append(bench_bandwidth("softmax_fwd 4096x4096", 4 * 2 * n,
                                lambda i: (arr(T, T, scale=2.0), B((T, T))),
                                lambda s: call("lhip_softmax_fwd", s[0].ptr, s[1].ptr, T, T, 1.0, 0, 0, 0),
-                               steps, warm))
+                               steps, warm, args.only))
     out.append(bench_bandwidth("softmax_bwd 4096x4096", 4 * 3 * n,
                                lambda i: (arr(T, T), arr(T, T), B((T, T))),
                                lambda s: call("lhip_softmax_bwd", s[0].ptr, s[1].ptr, s[2].ptr, T, T, 1.0, 0, 0, 0, 0),
-                               steps, warm))
+                               steps, warm, args.only))
     # C3 fused softmax + CE: 512 x 32000 logits, labels uniform
     R, V = 512, 32000
     labels = B.from_numpy(rng.integers(0, V, R).astype(np.int32), np.int32)
@@ -278,9 +281,30 @@ def run_bandwidth_suite(args):
                                lambda i: (arr(R, V), B((R, V)), B((R,))),
                                lambda s: call("lhip_ce_fused", s[0].ptr, labels.ptr, s[2].ptr, s[1].ptr, R, V, -1,
                                               1.0 / R),
-                               steps, warm))
+                               steps, warm, args.only))
     for r in out:
-        print(json.dumps(r), flush=True)
+        if r is not None:
+            print(json.dumps(r), flush=True)
+
+
+def run_copy_suite(args):
+    """out = a + b over 64 Mi floats (768 MiB of traffic per launch: two 256 MiB
+    reads, one 256 MiB write), the reference for scaling FETCH_SIZE/WRITE_SIZE."""
+    from lanternl_amd import device
+    from lanternl_amd._lib import call
+    device.init(0)
+    n = 64 << 20
+    a = device.Buffer((n,)).zero()
+    b = device.Buffer((n,)).zero()
+    o = device.Buffer((n,))
+
+    def run(_):
+        call("lhip_add", a.ptr, b.ptr, o.ptr, n)
+    ms = time_launches(run, max(args.steps, 5), args.warmup)
+    nbytes = 3 * 4 * n
+    print(json.dumps({"suite": "copy", "kernel": "add_kernel 64Mi floats", "ms": ms, "bytes": nbytes,
+                      "read_bytes": 2 * 4 * n, "write_bytes": 4 * n,
+                      "gbps": nbytes / (ms * 1e-3) / 1e9}), flush=True)
 
 
 def main():
@@ -290,7 +314,8 @@ def main():
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--workload", default="lmtrain_c2", choices=["lmtrain_c2", "gemm4096"])
     p.add_argument("--eager", action="store_true", help="launch the LM step kernel by kernel, no graph")
-    p.add_argument("--suite", default=None, choices=["gemm", "bandwidth"])
+    p.add_argument("--suite", default=None, choices=["gemm", "bandwidth", "copy"])
+    p.add_argument("--only", default=None, help="bandwidth suite: run only kernels whose name contains this")
     args = p.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py: this build measures ONE GPU only (asked for {args.gpus}); "
@@ -301,6 +326,8 @@ def main():
         run_gemm_suite(args)
     elif args.suite == "bandwidth":
         run_bandwidth_suite(args)
+    elif args.suite == "copy":
+        run_copy_suite(args)
     elif args.workload == "gemm4096":
         run_gemm_workload(args)
     else:
