@@ -16,12 +16,25 @@
 namespace lhip {
 namespace {
 
+// One unit (usually a float4) per thread: on MI355X a grid-stride loop over a
+// few blocks per CU streams at ~4.8 TB/s, one float4 per thread at ~6.2 TB/s
+// (measured on a 1 GiB copy).  The cap only matters for enormous arrays, which
+// the kernels' grid-stride loops then cover.
 inline int grid_for(long long units, int threads)
 {
-    const long long cap = static_cast<long long>(st().cu_count > 0 ? st().cu_count : 256) * 8;
+    const long long cap = 1LL << 22;
     long long g = (units + threads - 1) / threads;
     if (g > cap) g = cap;
     return static_cast<int>(g < 1 ? 1 : g);
+}
+
+typedef float vf4 __attribute__((ext_vector_type(4)));
+
+// 128-bit load of data read exactly once (non-temporal hint)
+__device__ __forceinline__ float4 ld_stream(const float* p)
+{
+    const vf4 v = __builtin_nontemporal_load(reinterpret_cast<const vf4*>(p));
+    return make_float4(v.x, v.y, v.z, v.w);
 }
 
 __global__ void fill_kernel(float* __restrict__ p, long long n, float v)
@@ -79,16 +92,26 @@ __global__ void swiglu_fwd_kernel(const float* __restrict__ g, int ldg, const fl
     if (vec) {
         const int c4n = cols >> 2;
         const long long n = static_cast<long long>(rows) * c4n;
+        const bool flat = ldg == cols && ldu == cols && ldh == cols;
         for (long long i = t0; i < n; i += stride) {
-            const int r = static_cast<int>(i / c4n), c = 4 * static_cast<int>(i % c4n);
-            const float4 gv = *reinterpret_cast<const float4*>(g + static_cast<long long>(r) * ldg + c);
-            const float4 uv = *reinterpret_cast<const float4*>(u + static_cast<long long>(r) * ldu + c);
+            long long og, ou, oh;
+            if (flat) {
+                og = ou = oh = 4 * i;
+            } else {
+                const unsigned r = static_cast<unsigned>(i) / static_cast<unsigned>(c4n);
+                const unsigned c = 4 * (static_cast<unsigned>(i) - r * static_cast<unsigned>(c4n));
+                og = static_cast<long long>(r) * ldg + c;
+                ou = static_cast<long long>(r) * ldu + c;
+                oh = static_cast<long long>(r) * ldh + c;
+            }
+            const float4 gv = ld_stream(g + og);
+            const float4 uv = ld_stream(u + ou);
             float4 o;
             o.x = gv.x * sigmoid_by_sign(gv.x) * uv.x;
             o.y = gv.y * sigmoid_by_sign(gv.y) * uv.y;
             o.z = gv.z * sigmoid_by_sign(gv.z) * uv.z;
             o.w = gv.w * sigmoid_by_sign(gv.w) * uv.w;
-            *reinterpret_cast<float4*>(h + static_cast<long long>(r) * ldh + c) = o;
+            *reinterpret_cast<float4*>(h + oh) = o;
         }
     } else {
         const long long n = static_cast<long long>(rows) * cols;
@@ -118,18 +141,27 @@ __global__ void swiglu_bwd_kernel(const float* __restrict__ g, int ldg, const fl
     if (vec) {
         const int c4n = cols >> 2;
         const long long n = static_cast<long long>(rows) * c4n;
+        const bool flat = ldg == cols && ldu == cols && lddh == cols && lddg == cols && lddu == cols;
         for (long long i = t0; i < n; i += stride) {
-            const int r = static_cast<int>(i / c4n), c = 4 * static_cast<int>(i % c4n);
-            const float4 gv = *reinterpret_cast<const float4*>(g + static_cast<long long>(r) * ldg + c);
-            const float4 uv = *reinterpret_cast<const float4*>(u + static_cast<long long>(r) * ldu + c);
-            const float4 hv = *reinterpret_cast<const float4*>(dh + static_cast<long long>(r) * lddh + c);
+            long long r, c;
+            if (flat) {
+                r = 0;
+                c = 4 * i;
+            } else {
+                const unsigned ru = static_cast<unsigned>(i) / static_cast<unsigned>(c4n);
+                r = ru;
+                c = 4 * (static_cast<unsigned>(i) - ru * static_cast<unsigned>(c4n));
+            }
+            const float4 gv = ld_stream(g + r * ldg + c);
+            const float4 uv = ld_stream(u + r * ldu + c);
+            const float4 hv = ld_stream(dh + r * lddh + c);
             float4 a, b;
             swiglu_bwd_one(gv.x, uv.x, hv.x, a.x, b.x);
             swiglu_bwd_one(gv.y, uv.y, hv.y, a.y, b.y);
             swiglu_bwd_one(gv.z, uv.z, hv.z, a.z, b.z);
             swiglu_bwd_one(gv.w, uv.w, hv.w, a.w, b.w);
-            float4* pg = reinterpret_cast<float4*>(dg + static_cast<long long>(r) * lddg + c);
-            float4* pu = reinterpret_cast<float4*>(du + static_cast<long long>(r) * lddu + c);
+            float4* pg = reinterpret_cast<float4*>(dg + r * lddg + c);
+            float4* pu = reinterpret_cast<float4*>(du + r * lddu + c);
             if (acc) {
                 const float4 og = *pg, ou = *pu;
                 a.x += og.x; a.y += og.y; a.z += og.z; a.w += og.w;
@@ -336,7 +368,8 @@ int swiglu_fwd(const float* g, int ldg, const float* u, int ldu, float* h, int l
     if (!g || !u || !h) return fail(LHIP_E_NULL, "swiglu_fwd: NULL pointer");
     if (ldg < cols || ldu < cols || ldh < cols) return fail(LHIP_E_SHAPE, "swiglu_fwd: leading dimension < cols");
     const int vec = cols % 4 == 0 && ldg % 4 == 0 && ldu % 4 == 0 && ldh % 4 == 0 && aligned16(g) &&
-                    aligned16(u) && aligned16(h);
+                    aligned16(u) && aligned16(h) &&
+                    static_cast<long long>(rows) * (cols / 4) < (1LL << 31);
     const long long units = static_cast<long long>(rows) * (vec ? cols / 4 : cols);
     swiglu_fwd_kernel<<<grid_for(units, 256), 256, 0, s>>>(g, ldg, u, ldu, h, ldh, rows, cols, vec);
     return check_launch("swiglu_fwd");
@@ -351,7 +384,8 @@ int swiglu_bwd(const float* g, int ldg, const float* u, int ldu, const float* dh
     if (ldg < cols || ldu < cols || lddh < cols || lddg < cols || lddu < cols)
         return fail(LHIP_E_SHAPE, "swiglu_bwd: leading dimension < cols");
     const int vec = cols % 4 == 0 && ldg % 4 == 0 && ldu % 4 == 0 && lddh % 4 == 0 && lddg % 4 == 0 &&
-                    lddu % 4 == 0 && aligned16(g) && aligned16(u) && aligned16(dh) && aligned16(dg) && aligned16(du);
+                    lddu % 4 == 0 && aligned16(g) && aligned16(u) && aligned16(dh) && aligned16(dg) && aligned16(du) &&
+                    static_cast<long long>(rows) * (cols / 4) < (1LL << 31);
     const long long units = static_cast<long long>(rows) * (vec ? cols / 4 : cols);
     swiglu_bwd_kernel<<<grid_for(units, 256), 256, 0, s>>>(g, ldg, u, ldu, dh, lddh, dg, lddg, du, lddu, rows,
                                                            cols, acc, vec);

@@ -36,6 +36,61 @@ __device__ __forceinline__ void f4set(float4& v, int e, float x)
     if (e == 0) v.x = x; else if (e == 1) v.y = x; else if (e == 2) v.z = x; else v.w = x;
 }
 
+typedef float vf4 __attribute__((ext_vector_type(4)));
+
+// 128-bit load of data this kernel reads exactly once (non-temporal hint)
+__device__ __forceinline__ float4 ld_stream(const float4* p)
+{
+    const vf4 v = __builtin_nontemporal_load(reinterpret_cast<const vf4*>(p));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+
+// Waves walk rows grid-stride (row += total waves) and prefetch their next
+// row into a second register set while they reduce and store the current
+// one, so that reads and writes of different rows overlap.  The grid is sized
+// to about two waves per SIMD, which keeps every wave busy to the end instead
+// of leaving a partial last round of one-row waves.
+inline int row_wave_blocks(int rows)
+{
+    const int cus = st().cu_count > 0 ? st().cu_count : 256;
+    int b = ceil_div(rows, kWavesPerBlock);
+    if (b > 2 * cus) b = 2 * cus;
+    return b < 1 ? 1 : b;
+}
+
+// Run body(buf, row) over this wave's rows with a one-row prefetch:
+// load(buf, row) fills a register set, body consumes it.
+template <class Regs, class Load, class Body>
+__device__ __forceinline__ void walk_rows(int rows, Load load, Body body)
+{
+    const int nw = gridDim.x * kWavesPerBlock;
+    int row = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    Regs a, b;
+    load(a, row);
+    while (true) {
+        int next = row + nw;
+        if (next < rows) load(b, next);
+        body(a, row);
+        if (next >= rows) break;
+        row = next;
+        next = row + nw;
+        if (next < rows) load(a, next);
+        body(b, row);
+        if (next >= rows) break;
+        row = next;
+    }
+}
+
+template <int NV>
+struct Row1 {
+    float4 v[NV];
+};
+template <int NV>
+struct Row2 {
+    float4 v[NV], g[NV];
+};
+
 // ------------------------------------------------------------------ RMSNorm
 // y = x * r * w, r = 1/sqrt(mean_j x^2 + eps); inv[row] = r (tensor2.lua:609-634).
 template <int NV>
@@ -43,32 +98,36 @@ __global__ void __launch_bounds__(kRowThreads)
 rmsnorm_fwd_vec(const float* __restrict__ x, const float* __restrict__ w, float* __restrict__ y,
                 float* __restrict__ inv, int rows, int cols, float eps)
 {
-    const int row = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    if (row >= rows) return;
     const int c4n = cols >> 2;
-    const float4* xr = reinterpret_cast<const float4*>(x + static_cast<size_t>(row) * cols);
     const float4* w4 = reinterpret_cast<const float4*>(w);
-    float4 v[NV];
-    float ss = 0.f;
+    auto load = [&](Row1<NV>& r, int row) {
+        const float4* xr = reinterpret_cast<const float4*>(x + static_cast<size_t>(row) * cols);
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        const int c = lane + 64 * i;
-        v[i] = c < c4n ? xr[c] : f4zero();
-        ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
-    }
-    ss = wave_sum(ss);
-    const float r = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
-    float4* yr = reinterpret_cast<float4*>(y + static_cast<size_t>(row) * cols);
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        const int c = lane + 64 * i;
-        if (c < c4n) {
-            const float4 g = w4[c];
-            yr[c] = make_float4(v[i].x * r * g.x, v[i].y * r * g.y, v[i].z * r * g.z, v[i].w * r * g.w);
+        for (int i = 0; i < NV; ++i) {
+            const int c = lane + 64 * i;
+            r.v[i] = c < c4n ? ld_stream(xr + c) : f4zero();
         }
-    }
-    if (inv && lane == 0) inv[row] = r;
+    };
+    auto body = [&](const Row1<NV>& r, int row) {
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < NV; ++i)
+            ss += r.v[i].x * r.v[i].x + r.v[i].y * r.v[i].y + r.v[i].z * r.v[i].z + r.v[i].w * r.v[i].w;
+        ss = wave_sum(ss);
+        const float rs = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
+        float4* yr = reinterpret_cast<float4*>(y + static_cast<size_t>(row) * cols);
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int c = lane + 64 * i;
+            if (c < c4n) {
+                const float4 g = w4[c];
+                yr[c] = make_float4(r.v[i].x * rs * g.x, r.v[i].y * rs * g.y, r.v[i].z * rs * g.z, r.v[i].w * rs * g.w);
+            }
+        }
+        if (inv && lane == 0) inv[row] = rs;
+    };
+    walk_rows<Row1<NV>>(rows, load, body);
 }
 
 __global__ void __launch_bounds__(kRowThreads)
@@ -235,47 +294,55 @@ __global__ void __launch_bounds__(kRowThreads)
 softmax_fwd_vec(const float* __restrict__ x, float* __restrict__ y, int rows, int cols, float scale,
                 int causal, int offset, int group)
 {
-    const int row = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    if (row >= rows) return;
-    const int lim = softmax_lim(row, cols, causal, offset, group);
     const int c4n = cols >> 2;
-    const float4* xr = reinterpret_cast<const float4*>(x + static_cast<size_t>(row) * cols);
-    float4 v[NV];
-    float mx = -INFINITY;
+    auto load = [&](Row1<NV>& r, int row) {
+        const int lim = softmax_lim(row, cols, causal, offset, group);
+        const float4* xr = reinterpret_cast<const float4*>(x + static_cast<size_t>(row) * cols);
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        const int c = lane + 64 * i;
-        const float4 t = (c < c4n && 4 * c < lim) ? xr[c] : f4zero();
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float s = (4 * c + e < lim) ? scale * f4get(t, e) : -INFINITY;
-            f4set(v[i], e, s);
-            mx = fmaxf(mx, s);
+        for (int i = 0; i < NV; ++i) {
+            const int c = lane + 64 * i;
+            r.v[i] = (c < c4n && 4 * c < lim) ? ld_stream(xr + c) : f4zero();
         }
-    }
-    mx = wave_max(mx);
-    if (mx == -INFINITY || mx != mx) mx = 0.f;
-    float sum = 0.f;
+    };
+    auto body = [&](Row1<NV>& r, int row) {
+        const int lim = softmax_lim(row, cols, causal, offset, group);
+        float4* v = r.v;                     // transformed in place (register pressure)
+        float mx = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        const int c = lane + 64 * i;
+        for (int i = 0; i < NV; ++i) {
+            const int c = lane + 64 * i;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float ev = (4 * c + e < lim) ? expf(f4get(v[i], e) - mx) : 0.f;
-            f4set(v[i], e, ev);
-            sum += ev;
+            for (int e = 0; e < 4; ++e) {
+                const float sv = (4 * c + e < lim) ? scale * f4get(v[i], e) : -INFINITY;
+                f4set(v[i], e, sv);
+                mx = fmaxf(mx, sv);
+            }
         }
-    }
-    sum = wave_sum(sum);
-    if (!(sum > 0.f)) sum = 1.f;
-    const float is = 1.0f / sum;
-    float4* yr = reinterpret_cast<float4*>(y + static_cast<size_t>(row) * cols);
+        mx = wave_max(mx);
+        if (mx == -INFINITY || mx != mx) mx = 0.f;
+        float sum = 0.f;
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        const int c = lane + 64 * i;
-        if (c < c4n) yr[c] = make_float4(v[i].x * is, v[i].y * is, v[i].z * is, v[i].w * is);
-    }
+        for (int i = 0; i < NV; ++i) {
+            const int c = lane + 64 * i;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float ev = (4 * c + e < lim) ? expf(f4get(v[i], e) - mx) : 0.f;
+                f4set(v[i], e, ev);
+                sum += ev;
+            }
+        }
+        sum = wave_sum(sum);
+        if (!(sum > 0.f)) sum = 1.f;
+        const float is = 1.0f / sum;
+        float4* yr = reinterpret_cast<float4*>(y + static_cast<size_t>(row) * cols);
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int c = lane + 64 * i;
+            if (c < c4n) yr[c] = make_float4(v[i].x * is, v[i].y * is, v[i].z * is, v[i].w * is);
+        }
+    };
+    walk_rows<Row1<NV>>(rows, load, body);
 }
 
 __global__ void __launch_bounds__(kRowThreads)
@@ -307,43 +374,50 @@ __global__ void __launch_bounds__(kRowThreads)
 softmax_bwd_vec(const float* __restrict__ y, const float* __restrict__ dy, float* __restrict__ dx,
                 int rows, int cols, float scale, int causal, int offset, int group, int acc)
 {
-    const int row = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    if (row >= rows) return;
-    const int lim = softmax_lim(row, cols, causal, offset, group);
     const int c4n = cols >> 2;
-    const size_t base = static_cast<size_t>(row) * cols;
-    const float4* yr = reinterpret_cast<const float4*>(y + base);
-    const float4* gr = reinterpret_cast<const float4*>(dy + base);
-    float4 yv[NV], gv[NV];
-    float dot = 0.f;
+    auto load = [&](Row2<NV>& r, int row) {
+        const int lim = softmax_lim(row, cols, causal, offset, group);
+        const size_t base = static_cast<size_t>(row) * cols;
+        const float4* yr = reinterpret_cast<const float4*>(y + base);
+        const float4* gr = reinterpret_cast<const float4*>(dy + base);
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        const int c = lane + 64 * i;
-        const bool in = c < c4n && 4 * c < lim;
-        yv[i] = in ? yr[c] : f4zero();
-        gv[i] = in ? gr[c] : f4zero();
+        for (int i = 0; i < NV; ++i) {
+            const int c = lane + 64 * i;
+            const bool in = c < c4n && 4 * c < lim;
+            r.v[i] = in ? ld_stream(yr + c) : f4zero();
+            r.g[i] = in ? ld_stream(gr + c) : f4zero();
+        }
+    };
+    auto body = [&](const Row2<NV>& r, int row) {
+        const int lim = softmax_lim(row, cols, causal, offset, group);
+        float dot = 0.f;
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-            if (4 * c + e < lim) dot += f4get(gv[i], e) * f4get(yv[i], e);
-    }
-    dot = wave_sum(dot);
-    float4* dr = reinterpret_cast<float4*>(dx + base);
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        const int c = lane + 64 * i;
-        if (c < c4n) {
-            float4 o;
+        for (int i = 0; i < NV; ++i) {
+            const int c = lane + 64 * i;
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-                f4set(o, e, (4 * c + e < lim) ? scale * (f4get(yv[i], e) * (f4get(gv[i], e) - dot)) : 0.f);
-            if (acc) {
-                const float4 old = dr[c];
-                o.x += old.x; o.y += old.y; o.z += old.z; o.w += old.w;
-            }
-            dr[c] = o;
+                if (4 * c + e < lim) dot += f4get(r.g[i], e) * f4get(r.v[i], e);
         }
-    }
+        dot = wave_sum(dot);
+        float4* dr = reinterpret_cast<float4*>(dx + static_cast<size_t>(row) * cols);
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int c = lane + 64 * i;
+            if (c < c4n) {
+                float4 o;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    f4set(o, e, (4 * c + e < lim) ? scale * (f4get(r.v[i], e) * (f4get(r.g[i], e) - dot)) : 0.f);
+                if (acc) {
+                    const float4 old = dr[c];
+                    o.x += old.x; o.y += old.y; o.z += old.z; o.w += old.w;
+                }
+                dr[c] = o;
+            }
+        }
+    };
+    walk_rows<Row2<NV>>(rows, load, body);
 }
 
 __global__ void __launch_bounds__(kRowThreads)
@@ -369,65 +443,96 @@ softmax_bwd_generic(const float* __restrict__ y, const float* __restrict__ dy, f
 // loss 0 and dlogits 0; otherwise loss[r] = logsumexp(x) - x[t] and
 // dlogits = gscale * (softmax(x) - onehot(t)).  dlogits may alias logits.
 // (tensor2.lua:809-882 per row; cuda/luaTL_train.cu:837-878 contract.)
-template <int NT, int NV>
+template <int NT, int NV, bool PF>
 __global__ void __launch_bounds__(NT)
 ce_fused_vec(const float* logits, const int* __restrict__ tgt, float* __restrict__ losses,
              float* dlogits, int rows, int V, int ignore_index, float gscale)
 {
+    // One workgroup per row at a time.  With PF, rows are walked block-stride
+    // and the next row is prefetched into registers while the current one is
+    // reduced and its dlogits written (reads and writes of different rows
+    // overlap); without PF (rows too long for two register copies) each
+    // workgroup takes one row.
     constexpr int NW = NT / 64;
     __shared__ float red[NW];
-    const int row = blockIdx.x;
-    const int t = tgt[row];
-    const size_t base = static_cast<size_t>(row) * V;
     const int c4n = V >> 2;
-    if (t < 0 || t >= V || t == ignore_index) {
-        if (losses && threadIdx.x == 0) losses[row] = 0.f;
-        if (dlogits) {
-            float4* dr = reinterpret_cast<float4*>(dlogits + base);
-            for (int c = threadIdx.x; c < c4n; c += NT) dr[c] = f4zero();
-        }
-        return;
-    }
-    const float xt = logits[base + t];   // read before any thread writes dlogits
-    const float4* xr = reinterpret_cast<const float4*>(logits + base);
-    float4 v[NV];
-    float mx = -INFINITY;
+    auto load = [&](Row1<NV>& r, int row) {
+        const float4* xr = reinterpret_cast<const float4*>(logits + static_cast<size_t>(row) * V);
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        const int c = threadIdx.x + NT * i;
-        v[i] = c < c4n ? xr[c] : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
-        mx = fmaxf(mx, fmaxf(fmaxf(v[i].x, v[i].y), fmaxf(v[i].z, v[i].w)));
-    }
-    mx = block_max<NW>(mx, red);
-    float sum = 0.f;
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        const int c = threadIdx.x + NT * i;
-        if (c < c4n) {
-            v[i].x = expf(v[i].x - mx); v[i].y = expf(v[i].y - mx);
-            v[i].z = expf(v[i].z - mx); v[i].w = expf(v[i].w - mx);
-            sum += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+        for (int i = 0; i < NV; ++i) {
+            const int c = threadIdx.x + NT * i;
+            r.v[i] = c < c4n ? ld_stream(xr + c) : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
         }
-    }
-    sum = block_sum<NW>(sum, red);
-    if (losses && threadIdx.x == 0) losses[row] = (mx + logf(sum)) - xt;
-    if (dlogits) {
-        const float is = 1.0f / sum;
-        float4* dr = reinterpret_cast<float4*>(dlogits + base);
+    };
+    auto body = [&](Row1<NV>& r, int row) {
+        const int t = tgt[row];
+        const size_t base = static_cast<size_t>(row) * V;
+        if (t < 0 || t >= V || t == ignore_index) {      // uniform in the block
+            if (losses && threadIdx.x == 0) losses[row] = 0.f;
+            if (dlogits) {
+                float4* dr = reinterpret_cast<float4*>(dlogits + base);
+                for (int c = threadIdx.x; c < c4n; c += NT) dr[c] = f4zero();
+            }
+            return;
+        }
+        const float xt = logits[base + t];   // read before any thread writes this row's dlogits
+        float4* v = r.v;                     // transformed in place (register pressure)
+        float mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) mx = fmaxf(mx, fmaxf(fmaxf(v[i].x, v[i].y), fmaxf(v[i].z, v[i].w)));
+        mx = block_max<NW>(mx, red);
+        float sum = 0.f;
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const int c = threadIdx.x + NT * i;
             if (c < c4n) {
-                float4 o;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    float p = f4get(v[i], e) * is;
-                    if (4 * c + e == t) p -= 1.f;
-                    f4set(o, e, gscale * p);
-                }
-                dr[c] = o;
+                v[i].x = expf(v[i].x - mx); v[i].y = expf(v[i].y - mx);
+                v[i].z = expf(v[i].z - mx); v[i].w = expf(v[i].w - mx);
+                sum += (v[i].x + v[i].y) + (v[i].z + v[i].w);
             }
         }
+        sum = block_sum<NW>(sum, red);
+        if (losses && threadIdx.x == 0) losses[row] = (mx + logf(sum)) - xt;
+        if (dlogits) {
+            const float is = 1.0f / sum;
+            float4* dr = reinterpret_cast<float4*>(dlogits + base);
+#pragma unroll
+            for (int i = 0; i < NV; ++i) {
+                const int c = threadIdx.x + NT * i;
+                if (c < c4n) {
+                    float4 o;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        float p = f4get(v[i], e) * is;
+                        if (4 * c + e == t) p -= 1.f;
+                        f4set(o, e, gscale * p);
+                    }
+                    dr[c] = o;
+                }
+            }
+        }
+        __syncthreads();   // red[] is reused by the next row's reductions
+    };
+    int row = blockIdx.x;
+    if (row >= rows) return;
+    Row1<NV> a;
+    load(a, row);
+    if (!PF) {
+        body(a, row);
+        return;
+    }
+    Row1<NV> b;
+    while (true) {
+        int next = row + gridDim.x;
+        if (next < rows) load(b, next);
+        body(a, row);
+        if (next >= rows) break;
+        row = next;
+        next = row + gridDim.x;
+        if (next < rows) load(a, next);
+        body(b, row);
+        if (next >= rows) break;
+        row = next;
     }
 }
 
@@ -515,7 +620,7 @@ int rmsnorm_fwd(const float* x, const float* w, float* y, float* inv, int rows, 
     if (!(eps >= 0.f)) return fail(LHIP_E_ARG, "rmsnorm_fwd: eps must be >= 0");
     const int nv = nv_for(cols);
     const bool vec = nv && cols % 4 == 0 && aligned16(x) && aligned16(w) && aligned16(y);
-    dim3 g(row_blocks(rows)), b(kRowThreads);
+    dim3 g(vec ? row_wave_blocks(rows) : row_blocks(rows)), b(kRowThreads);
     if (!vec) rmsnorm_fwd_generic<<<g, b, 0, s>>>(x, w, y, inv, rows, cols, eps);
     else if (nv == 1) rmsnorm_fwd_vec<1><<<g, b, 0, s>>>(x, w, y, inv, rows, cols, eps);
     else if (nv == 2) rmsnorm_fwd_vec<2><<<g, b, 0, s>>>(x, w, y, inv, rows, cols, eps);
@@ -579,7 +684,7 @@ int softmax_fwd(const float* x, float* y, int rows, int cols, float scale, int c
     if (group <= 0) group = rows;
     const int nv = nv_for(cols);
     const bool vec = nv && cols % 4 == 0 && aligned16(x) && aligned16(y);
-    dim3 g(row_blocks(rows)), b(kRowThreads);
+    dim3 g(vec ? row_wave_blocks(rows) : row_blocks(rows)), b(kRowThreads);
 #define LHIP_SMF(NV_) softmax_fwd_vec<NV_><<<g, b, 0, s>>>(x, y, rows, cols, scale, causal, offset, group)
     if (!vec) softmax_fwd_generic<<<g, b, 0, s>>>(x, y, rows, cols, scale, causal, offset, group);
     else if (nv == 1) LHIP_SMF(1);
@@ -600,7 +705,7 @@ int softmax_bwd(const float* y, const float* dy, float* dx, int rows, int cols, 
     if (group <= 0) group = rows;
     const int nv = nv_for(cols);
     const bool vec = nv && cols % 4 == 0 && aligned16(y) && aligned16(dy) && aligned16(dx);
-    dim3 g(row_blocks(rows)), b(kRowThreads);
+    dim3 g(vec ? row_wave_blocks(rows) : row_blocks(rows)), b(kRowThreads);
 #define LHIP_SMB(NV_) softmax_bwd_vec<NV_><<<g, b, 0, s>>>(y, dy, dx, rows, cols, scale, causal, offset, group, accumulate)
     if (!vec) softmax_bwd_generic<<<g, b, 0, s>>>(y, dy, dx, rows, cols, scale, causal, offset, group, accumulate);
     else if (nv == 1) LHIP_SMB(1);
@@ -619,12 +724,15 @@ int ce_fused(const float* logits, const int* tgt, float* losses, float* dlogits,
     if (rows == 0) return LHIP_OK;
     if (!logits || !tgt) return fail(LHIP_E_NULL, "ce_fused: NULL logits/targets");
     const bool vec = V % 4 == 0 && aligned16(logits) && (!dlogits || aligned16(dlogits));
+    const int cus = st().cu_count > 0 ? st().cu_count : 256;
+    // rows walked block-stride: about 2 rows per workgroup once rows exceed the CUs
+    const int nb_small = rows < 4 * cus ? rows : 4 * cus;
     if (vec && V <= 256 * 4 * 2)
-        ce_fused_vec<256, 2><<<rows, 256, 0, s>>>(logits, tgt, losses, dlogits, rows, V, ignore_index, gscale);
+        ce_fused_vec<256, 2, true><<<nb_small, 256, 0, s>>>(logits, tgt, losses, dlogits, rows, V, ignore_index, gscale);
     else if (vec && V <= 256 * 4 * 8)
-        ce_fused_vec<256, 8><<<rows, 256, 0, s>>>(logits, tgt, losses, dlogits, rows, V, ignore_index, gscale);
+        ce_fused_vec<256, 8, true><<<nb_small, 256, 0, s>>>(logits, tgt, losses, dlogits, rows, V, ignore_index, gscale);
     else if (vec && V <= 1024 * 4 * 8)
-        ce_fused_vec<1024, 8><<<rows, 1024, 0, s>>>(logits, tgt, losses, dlogits, rows, V, ignore_index, gscale);
+        ce_fused_vec<1024, 8, false><<<rows, 1024, 0, s>>>(logits, tgt, losses, dlogits, rows, V, ignore_index, gscale);
     else
         ce_fused_generic<<<rows, 256, 0, s>>>(logits, tgt, losses, dlogits, rows, V, ignore_index, gscale);
     return check_launch("ce_fused");
