@@ -100,6 +100,12 @@ int sgd_step(float* p, float* g, float* v, long long n, const double* sumsq_dev,
              float wd, float grad_scale, float clip_norm, int nesterov, float* gnorm_out, int* applied_out,
              hipStream_t s, const float* hyper_dev);
 int sum_f32(const float* x, int n, float scale, float* out, hipStream_t s);
+// Fused per-(window, head) attention of the LMTrain step (T <= 64, head_dim <= 64, even).
+bool attn_fused_ok(int T, int hd);
+int attn_fwd(const float* qkv, const float2* cs, float* P, float* ctx, int B, int H, int T, int hd, float scale,
+             int causal, hipStream_t s);
+int attn_bwd(const float* qkv, const float2* cs, const float* P, const float* dctx, float* dqkv, int B, int H, int T,
+             int hd, float scale, int causal, hipStream_t s);
 
 // Options of the GEMM launcher.
 //   inner / s?2 : second batch level -- blockIdx.y = outer * inner + i and operand

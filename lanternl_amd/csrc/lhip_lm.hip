@@ -64,6 +64,8 @@ struct LmModel {
     size_t work_floats = 0;
     float* splitk = nullptr;      // split-K partials of the small-tile GEMMs
     size_t splitk_floats = 0;
+    float2* rope_cs = nullptr;    // (cos, sin) of positions 0..T-1, pairs 0..hd/2-1
+    bool fused_attn = false;      // per-(window, head) fused attention kernels
     // graph
     bool use_graph = false;
     hipGraph_t graph = nullptr;
@@ -191,14 +193,20 @@ int enqueue_step(LmModel& m, hipStream_t s)
         LM_TRY(rmsnorm_fwd(xl, m.prm(m.lt(l, P_LN1)), h, inv1, N, D, eps, s));
         // q, k, v = h.Wq, h.Wk, h.Wv: one batched GEMM (the three weights are adjacent)
         LM_TRY(q.bgemm(0, 0, N, D, D, h, D, 0, m.prm(m.lt(l, P_WQ)), D, static_cast<long long>(D) * D, 0.f, qkv, D, ND, 3));
-        // RoPE on q and k (2N rows, positions row % T), interleaved pairs
-        LM_TRY(rope(qkv, nullptr, 2 * N, H, hd, D, 0, T, base, 1, 0, s));
-        // scores = q_bh . k_bh^T per (window, head), into the (forward-idle) dP
-        // scratch; P = softmax(scale * scores)
-        LM_TRY(q.hgemm(0, 1, T, T, hd, qkv, D, hd, TD, qkv + ND, D, hd, TD, m.dP, T, TT, HTT));
-        LM_TRY(softmax_fwd(m.dP, P, m.B * H * T, T, scale, causal, 0, T, s));
-        // ctx[:, h*hd:] = P_bh . v_bh
-        LM_TRY(q.hgemm(0, 0, T, hd, T, P, T, TT, HTT, qkv + 2 * ND, D, hd, TD, ctx, D, hd, TD));
+        if (m.fused_attn) {
+            // RoPE, scores, causal softmax and P.v per (window, head) in one launch;
+            // qkv keeps the unrotated q, k (the backward rotates again)
+            LM_TRY(attn_fwd(qkv, m.rope_cs, P, ctx, m.B, H, T, hd, scale, causal, s));
+        } else {
+            // RoPE on q and k (2N rows, positions row % T), interleaved pairs
+            LM_TRY(rope(qkv, nullptr, 2 * N, H, hd, D, 0, T, base, 1, 0, s));
+            // scores = q_bh . k_bh^T per (window, head), into the (forward-idle) dP
+            // scratch; P = softmax(scale * scores)
+            LM_TRY(q.hgemm(0, 1, T, T, hd, qkv, D, hd, TD, qkv + ND, D, hd, TD, m.dP, T, TT, HTT));
+            LM_TRY(softmax_fwd(m.dP, P, m.B * H * T, T, scale, causal, 0, T, s));
+            // ctx[:, h*hd:] = P_bh . v_bh
+            LM_TRY(q.hgemm(0, 0, T, hd, T, P, T, TT, HTT, qkv + 2 * ND, D, hd, TD, ctx, D, hd, TD));
+        }
         // x_mid = x + ctx . Wo
         LM_TRY(q.gemm_res(N, D, D, ctx, D, m.prm(m.lt(l, P_WO)), D, xl, xmid, D));
         LM_TRY(rmsnorm_fwd(xmid, m.prm(m.lt(l, P_LN2)), h2, inv2, N, D, eps, s));
@@ -246,16 +254,21 @@ int enqueue_step(LmModel& m, hipStream_t s)
         // o = ctx . Wo
         LM_TRY(q.gemm(0, 1, N, D, D, m.dx, D, m.prm(m.lt(l, P_WO)), D, 0.f, m.dctx, D));    // dctx = dx . Wo^T
         LM_TRY(q.gemm(1, 0, D, D, N, ctx, D, m.dx, D, 0.f, m.grd(m.lt(l, P_WO)), D));       // gWo = ctx^T . dx
-        // per (window, head): dP = dO . v^T ; dv = P^T . dO
-        LM_TRY(q.hgemm(0, 1, T, T, hd, m.dctx, D, hd, TD, qkv + 2 * ND, D, hd, TD, m.dP, T, TT, HTT));
-        LM_TRY(q.hgemm(1, 0, T, hd, T, P, T, TT, HTT, m.dctx, D, hd, TD, m.dqkv + 2 * ND, D, hd, TD));
-        // dS = scale * softmax_bwd(P, dP)
-        LM_TRY(softmax_bwd(P, m.dP, m.dS, m.B * H * T, T, scale, causal, 0, T, 0, s));
-        // dq = dS . k_rot ; dk = dS^T . q_rot
-        LM_TRY(q.hgemm(0, 0, T, hd, T, m.dS, T, TT, HTT, qkv + ND, D, hd, TD, m.dqkv, D, hd, TD));
-        LM_TRY(q.hgemm(1, 0, T, hd, T, m.dS, T, TT, HTT, qkv, D, hd, TD, m.dqkv + ND, D, hd, TD));
-        // RoPE backward (inverse rotation) on dq and dk
-        LM_TRY(rope(m.dqkv, nullptr, 2 * N, H, hd, D, 0, T, base, 1, 1, s));
+        if (m.fused_attn) {
+            // dP, dv, softmax backward, dq, dk and the inverse RoPE per (window, head)
+            LM_TRY(attn_bwd(qkv, m.rope_cs, P, m.dctx, m.dqkv, m.B, H, T, hd, scale, causal, s));
+        } else {
+            // per (window, head): dP = dO . v^T ; dv = P^T . dO
+            LM_TRY(q.hgemm(0, 1, T, T, hd, m.dctx, D, hd, TD, qkv + 2 * ND, D, hd, TD, m.dP, T, TT, HTT));
+            LM_TRY(q.hgemm(1, 0, T, hd, T, P, T, TT, HTT, m.dctx, D, hd, TD, m.dqkv + 2 * ND, D, hd, TD));
+            // dS = scale * softmax_bwd(P, dP)
+            LM_TRY(softmax_bwd(P, m.dP, m.dS, m.B * H * T, T, scale, causal, 0, T, 0, s));
+            // dq = dS . k_rot ; dk = dS^T . q_rot
+            LM_TRY(q.hgemm(0, 0, T, hd, T, m.dS, T, TT, HTT, qkv + ND, D, hd, TD, m.dqkv, D, hd, TD));
+            LM_TRY(q.hgemm(1, 0, T, hd, T, m.dS, T, TT, HTT, qkv, D, hd, TD, m.dqkv + ND, D, hd, TD));
+            // RoPE backward (inverse rotation) on dq and dk
+            LM_TRY(rope(m.dqkv, nullptr, 2 * N, H, hd, D, 0, T, base, 1, 1, s));
+        }
         // dh = dq.Wq^T + dk.Wk^T + dv.Wv^T ; gW{q,k,v} = h^T . d{q,k,v}
         LM_TRY(q.gemm(0, 1, N, D, D, m.dqkv, D, m.prm(m.lt(l, P_WQ)), D, 0.f, m.dh, D));
         LM_TRY(q.gemm(0, 1, N, D, D, m.dqkv + ND, D, m.prm(m.lt(l, P_WK)), D, 1.f, m.dh, D));
@@ -404,6 +417,7 @@ LHIP_API int lhip_lm_create(const lhip_lm_config_t* cfg, void** model)
         {reinterpret_cast<void**>(&m->dh), sizeof(float) * ND},
         {reinterpret_cast<void**>(&m->work), sizeof(float) * m->work_floats},
         {reinterpret_cast<void**>(&m->splitk), sizeof(float) * m->splitk_floats},
+        {reinterpret_cast<void**>(&m->rope_cs), sizeof(float2) * m->T * (m->hd / 2)},
     };
     size_t total = 0;
     for (auto& sl : slots) total += (sl.bytes + 255) & ~static_cast<size_t>(255);
@@ -429,6 +443,27 @@ LHIP_API int lhip_lm_create(const lhip_lm_config_t* cfg, void** model)
         delete m;
         return rc;
     }
+    // RoPE table for positions 0..T-1: angle = t / base^(2p/hd) in double, as
+    // build_rope (transformer.lua:30-48), rounded to fp32 once
+    {
+        const int pairs = m->hd / 2;
+        std::vector<float2> tab(static_cast<size_t>(m->T) * pairs);
+        for (int p = 0; p < pairs; ++p) {
+            const double inv = 1.0 / std::pow(cfg->rope_base, static_cast<double>(2 * p) / m->hd);
+            for (int t = 0; t < m->T; ++t) {
+                const double ang = t * inv;
+                tab[static_cast<size_t>(t) * pairs + p] =
+                    make_float2(static_cast<float>(std::cos(ang)), static_cast<float>(std::sin(ang)));
+            }
+        }
+        hipError_t ue = hipMemcpy(m->rope_cs, tab.data(), tab.size() * sizeof(float2), hipMemcpyHostToDevice);
+        if (ue != hipSuccess) {
+            (void)hipFree(m->arena);
+            delete m;
+            return lhip::hip_fail(ue, "lhip_lm_create: rope table");
+        }
+    }
+    m->fused_attn = lhip::attn_fused_ok(m->T, m->hd);
     m->h_tgt.assign(static_cast<size_t>(N), 0);
     *model = m;
     return LHIP_OK;

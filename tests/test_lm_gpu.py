@@ -183,3 +183,20 @@ def test_lm_rejects_out_of_range_ids():
     with pytest.raises(LanternlHipError, match="no batch"):
         gpu.step(0.1)
     gpu.close()
+
+
+def test_lm_step_unfused_attention_path():
+    """Windows longer than 64 tokens take the unfused attention path (separate
+    RoPE, score GEMM, softmax, PV GEMM and their backwards); same parity bars."""
+    announce("lm unfused attention")
+    gpu, res = _run_case(48, 16, 1, 2, 32, 2, 80, steps=2, lr=0.1, std=0.3, seed=12)
+    _check(res)
+    gpu.close()
+
+
+def test_lm_step_head_dim_64_fused_limit():
+    """head_dim 64 and T 64: the largest fused attention configuration."""
+    announce("lm hd64")
+    gpu, res = _run_case(64, 128, 1, 2, 64, 2, 64, steps=1, lr=0.05, std=0.1, seed=13)
+    _check(res)
+    gpu.close()
