@@ -36,6 +36,7 @@ namespace lhip {
 namespace {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;  // 4 wave64s
 constexpr int kSmallU = 8;     // K steps whose loads the small kernel issues together
@@ -127,6 +128,8 @@ struct GemmArgs {
     int tiles_m, tiles_n, vecA, vecB, inner;
     int splits, kchunk;               // split-K: blockIdx.z = slice, K range [z*kchunk, (z+1)*kchunk)
     float* ws;                        // split-K partials [split][batch][M][N]
+    int Kb;                           // batch-reduce: K = kblocks * Kb, block j reads A + j*sAk, B + j*sBk
+    long long sAk, sBk;
 };
 
 // C = alpha * sum_s ws[s] + beta * R, the slices summed in order (deterministic).
@@ -292,22 +295,27 @@ sgemm_mfma_kernel(const GemmArgs g)
 
 // ---------------------------------------------------------------------------
 // Small problems (fewer 64x64 output tiles than CUs, e.g. every GEMM of the
-// C2 LMTrain step): one workgroup per 32x32 output tile, and the four waves of
-// the workgroup split K among themselves -- wave w takes the 8-deep K steps
-// w, w+4, w+8, ... -- each accumulating the whole 32x32 tile, so one tile's
-// K loop runs on all four SIMDs of its CU.  The partial tiles are summed in
-// LDS in wave order (deterministic).  Operands are loaded straight from
+// C2 LMTrain step): one workgroup per 32x32 output tile, and the NW waves of
+// the workgroup (4, or 8 once K >= 256) split K among themselves -- wave w
+// takes the 8-deep K steps w, w+NW, w+2NW, ... -- each accumulating the whole
+// 32x32 tile, so one tile's K loop runs on all four SIMDs of its CU.  The
+// partial tiles are summed in LDS in wave order (deterministic).  Operands are loaded straight from
 // global memory into MFMA fragments: for an 8-deep K step, lane l (row or
 // column l%32, half h = l/32) holds op(A)[row][k0+4h .. k0+4h+3] and
 // op(B)[k0+4h .. k0+4h+3][col]; MFMA i of the step multiplies element i of
 // both, so the two halves of one v_mfma_f32_32x32x2f32 cover k0+i and
 // k0+4+i and the four MFMAs cover k0 .. k0+7 exactly once.  The contiguous
 // operand dimension is read as float4 when aligned, otherwise element-wise.
-template <bool TA, bool TB>
-__global__ void __launch_bounds__(kThreads)
+//
+// With BR (batch-reduce, non-transposed A only) the K range is kblocks blocks
+// of Kb (Kb % 4 == 0): logical k lies in block j = k / Kb, whose operands start
+// at A + j*sAk and B + j*sBk, so C = alpha * sum_j A_j . op(B_j) + beta * R in
+// one launch.  A lane's four k never straddle a block.
+template <bool TA, bool TB, bool BR, int NW>
+__global__ void __launch_bounds__(64 * NW)
 sgemm_small_kernel(const GemmArgs g)
 {
-    __shared__ float red[4][16][64];
+    __shared__ float red[NW][16][64];
     const int M = g.M, N = g.N;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -334,38 +342,48 @@ sgemm_small_kernel(const GemmArgs g)
     // so that many loads are in flight per wave (these launches have few
     // workgroups: latency, not bandwidth, bounds them).
     constexpr int U = kSmallU;
-    for (int kp = kbeg + 8 * wave; kp < kend; kp += 32 * U) {
+    for (int kp = kbeg + 8 * wave; kp < kend; kp += 8 * NW * U) {
         float a[U][4], b[U][4];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int kb = kp + 32 * u + 4 * h;   // first of this lane's four k
-            const bool kfull = kb + 3 < kend;
+            const int kl = kp + 8 * NW * u + 4 * h;   // first of this lane's four k (logical)
+            const bool kfull = kl + 3 < kend;
+            const int kend_l = kend - kl;         // valid k from kl on: i < kend_l
+            int kb = kl;
+            const float* __restrict__ Ab = A;
+            const float* __restrict__ Bb = B;
+            if (BR) {
+                const int j = kl / g.Kb;
+                kb = kl - j * g.Kb;
+                Ab = A + j * g.sAk;
+                Bb = B + j * g.sBk;
+            }
             if (!TA) {
-                const float* src = A + static_cast<long long>(row) * g.lda + kb;
+                const float* src = Ab + static_cast<long long>(row) * g.lda + kb;
                 if (g.vecA && rok && kfull) {
                     const float4 v = *reinterpret_cast<const float4*>(src);
                     a[u][0] = v.x; a[u][1] = v.y; a[u][2] = v.z; a[u][3] = v.w;
                 } else {
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) a[u][i] = (rok && kb + i < kend) ? src[i] : 0.f;
+                    for (int i = 0; i < 4; ++i) a[u][i] = (rok && i < kend_l) ? src[i] : 0.f;
                 }
             } else {
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    a[u][i] = (rok && kb + i < kend) ? A[static_cast<long long>(kb + i) * g.lda + row] : 0.f;
+                    a[u][i] = (rok && i < kend_l) ? Ab[static_cast<long long>(kb + i) * g.lda + row] : 0.f;
             }
             if (!TB) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    b[u][i] = (cok && kb + i < kend) ? B[static_cast<long long>(kb + i) * g.ldb + col] : 0.f;
+                    b[u][i] = (cok && i < kend_l) ? Bb[static_cast<long long>(kb + i) * g.ldb + col] : 0.f;
             } else {
-                const float* src = B + static_cast<long long>(col) * g.ldb + kb;
+                const float* src = Bb + static_cast<long long>(col) * g.ldb + kb;
                 if (g.vecB && cok && kfull) {
                     const float4 v = *reinterpret_cast<const float4*>(src);
                     b[u][0] = v.x; b[u][1] = v.y; b[u][2] = v.z; b[u][3] = v.w;
                 } else {
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) b[u][i] = (cok && kb + i < kend) ? src[i] : 0.f;
+                    for (int i = 0; i < 4; ++i) b[u][i] = (cok && i < kend_l) ? src[i] : 0.f;
                 }
             }
         }
@@ -376,8 +394,8 @@ sgemm_small_kernel(const GemmArgs g)
                 acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[u][i], b[u][i], acc, 0, 0, 0);
     }
 
-    // sum the four waves' tiles in wave order; thread (wave w, lane l) finishes
-    // accumulator registers 4w .. 4w+3 of lane l
+    // sum the waves' tiles in wave order; thread (wave w, lane l) finishes
+    // accumulator registers (16/NW)w .. (16/NW)(w+1)-1 of lane l
 #pragma unroll
     for (int r = 0; r < 16; ++r) red[wave][r][lane] = acc[r];
     __syncthreads();
@@ -389,10 +407,13 @@ sgemm_small_kernel(const GemmArgs g)
     float* __restrict__ C = g.C + coff;
     const float* R = g.R ? g.R + coff : C;
     const int ldr = g.R ? g.ldr : g.ldc;
+    constexpr int RPW = 16 / NW;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const int r = 4 * wave + q;
-        const float v = ((red[0][r][lane] + red[1][r][lane]) + red[2][r][lane]) + red[3][r][lane];
+    for (int q = 0; q < RPW; ++q) {
+        const int r = RPW * wave + q;
+        float v = red[0][r][lane];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) v += red[w][r][lane];
         const int orow = m0 + 8 * (r >> 2) + 4 * lk + (r & 3);
         if (orow >= M || ocol >= N) continue;
         if (wz) {
@@ -405,13 +426,154 @@ sgemm_small_kernel(const GemmArgs g)
     }
 }
 
-template <bool TA, bool TB>
+// ---------------------------------------------------------------------------
+// Tiny problems (fewer 32x32 output tiles than CUs, e.g. the 512x128 outputs
+// of the C2 step): one workgroup per 16x16 output tile, four times as many
+// workgroups as the 32x32 kernel, so the fp32 MFMA work (64 cycles per
+// 32x32x2 or 32 per 16x16x4 instruction and SIMD) spreads over more CUs.
+// Same scheme as the small kernel with v_mfma_f32_16x16x4f32: for a 16-deep
+// K step at k0, lane l (row or column l%16, group q = l/16) holds
+// op(A)[row][k0+4q .. k0+4q+3] and op(B)[k0+4q .. k0+4q+3][col]; MFMA i of the
+// step multiplies element i of both, so its four k slots (one per lane group)
+// are k0+4q+i and the four MFMAs cover k0 .. k0+15 exactly once.  The four
+// waves take the 16-deep steps w, w+4, ...; their tiles are summed in LDS in
+// wave order.  Steps wholly past the end of K issue no MFMA.  BR as above.
+template <bool TA, bool TB, bool BR>
+__global__ void __launch_bounds__(256)
+sgemm_tiny_kernel(const GemmArgs g)
+{
+    __shared__ float red[4][4][64];
+    const int M = g.M, N = g.N;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int lr = lane & 15;
+    const int q = lane >> 4;
+    const int tm = blockIdx.x / g.tiles_n, tn = blockIdx.x % g.tiles_n;
+    const int m0 = tm * 16, n0 = tn * 16;
+    const long long zo = blockIdx.y / g.inner, zi = blockIdx.y % g.inner;
+    const float* __restrict__ A = g.A + zo * g.sA2 + zi * g.sA;
+    const float* __restrict__ B = g.B + zo * g.sB2 + zi * g.sB;
+    const long long coff = zo * g.sC2 + zi * g.sC;
+    const int kbeg = blockIdx.z * g.kchunk;
+    const int kend = min(g.K, kbeg + g.kchunk);
+    const int row = m0 + lr;
+    const int col = n0 + lr;
+    const bool rok = row < M, cok = col < N;
+
+    floatx4 acc;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[r] = 0.f;
+
+    constexpr int U = kSmallU;
+    for (int kp = kbeg + 16 * wave; kp < kend; kp += 64 * U) {
+        float a[U][4], b[U][4];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int kl = kp + 64 * u + 4 * q;
+            const bool kfull = kl + 3 < kend;
+            const int kend_l = kend - kl;
+            int kb = kl;
+            const float* __restrict__ Ab = A;
+            const float* __restrict__ Bb = B;
+            if (BR) {
+                const int j = kl / g.Kb;
+                kb = kl - j * g.Kb;
+                Ab = A + j * g.sAk;
+                Bb = B + j * g.sBk;
+            }
+            if (!TA) {
+                const float* src = Ab + static_cast<long long>(row) * g.lda + kb;
+                if (g.vecA && rok && kfull) {
+                    const float4 v = *reinterpret_cast<const float4*>(src);
+                    a[u][0] = v.x; a[u][1] = v.y; a[u][2] = v.z; a[u][3] = v.w;
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) a[u][i] = (rok && i < kend_l) ? src[i] : 0.f;
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    a[u][i] = (rok && i < kend_l) ? Ab[static_cast<long long>(kb + i) * g.lda + row] : 0.f;
+            }
+            if (!TB) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    b[u][i] = (cok && i < kend_l) ? Bb[static_cast<long long>(kb + i) * g.ldb + col] : 0.f;
+            } else {
+                const float* src = Bb + static_cast<long long>(col) * g.ldb + kb;
+                if (g.vecB && cok && kfull) {
+                    const float4 v = *reinterpret_cast<const float4*>(src);
+                    b[u][0] = v.x; b[u][1] = v.y; b[u][2] = v.z; b[u][3] = v.w;
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) b[u][i] = (cok && i < kend_l) ? src[i] : 0.f;
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (kp + 64 * u >= kend) break;   // wave-uniform: nothing left in this pass
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u][i], b[u][i], acc, 0, 0, 0);
+        }
+    }
+
+    // thread (wave w, lane l) finishes accumulator register w of lane l
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[wave][r][lane] = acc[r];
+    __syncthreads();
+    const float v = ((red[0][wave][lane] + red[1][wave][lane]) + red[2][wave][lane]) + red[3][wave][lane];
+    const int orow = m0 + 4 * q + wave;
+    const int ocol = n0 + lr;
+    if (orow >= M || ocol >= N) return;
+    if (g.splits > 1) {
+        float* wz = g.ws + (static_cast<long long>(blockIdx.z) * gridDim.y + blockIdx.y) * (static_cast<long long>(M) * N);
+        wz[static_cast<long long>(orow) * N + ocol] = v;
+        return;
+    }
+    float* __restrict__ C = g.C + coff;
+    const float* R = g.R ? g.R + coff : C;
+    const int ldr = g.R ? g.ldr : g.ldc;
+    const float o = g.alpha * v;
+    C[static_cast<long long>(orow) * g.ldc + ocol] =
+        (g.beta != 0.f) ? o + g.beta * R[static_cast<long long>(orow) * ldr + ocol] : o;
+}
+
+// Eight waves share K once it is long enough for each to get a full pass.
+constexpr int kSmallWavesLongK = 8;
+inline bool small_long_k(const GemmArgs& g) { return g.kchunk >= 8 * 4 * kSmallU; }
+
+template <bool TA, bool TB, bool BR>
 void launch_small_t(const GemmArgs& g, dim3 grid, hipStream_t stream)
 {
-    sgemm_small_kernel<TA, TB><<<grid, dim3(kThreads), 0, stream>>>(g);
+    if (small_long_k(g))
+        sgemm_small_kernel<TA, TB, BR, kSmallWavesLongK><<<grid, dim3(64 * kSmallWavesLongK), 0, stream>>>(g);
+    else
+        sgemm_small_kernel<TA, TB, BR, 4><<<grid, dim3(256), 0, stream>>>(g);
 }
 
 int launch_reduce(const GemmArgs& g, int batch, hipStream_t stream);
+
+int launch_tiny(int ta, int tb, GemmArgs g, int batch, hipStream_t stream)
+{
+    g.tiles_m = ceil_div(g.M, 16);
+    g.tiles_n = ceil_div(g.N, 16);
+    const long long nwg = static_cast<long long>(g.tiles_m) * g.tiles_n;
+    if (nwg > 0x7fffffffLL) return fail(LHIP_E_CAPACITY, "sgemm: %lld workgroups exceed the grid limit", nwg);
+    if (g.splits <= 1) { g.splits = 1; g.kchunk = g.K; g.ws = nullptr; }
+    dim3 grid(static_cast<unsigned>(nwg), batch, g.splits), block(256);
+    if (g.Kb != g.K) {
+        if (!tb) sgemm_tiny_kernel<false, false, true><<<grid, block, 0, stream>>>(g);
+        else sgemm_tiny_kernel<false, true, true><<<grid, block, 0, stream>>>(g);
+    } else if (!ta && !tb) sgemm_tiny_kernel<false, false, false><<<grid, block, 0, stream>>>(g);
+    else if (ta && !tb) sgemm_tiny_kernel<true, false, false><<<grid, block, 0, stream>>>(g);
+    else if (!ta && tb) sgemm_tiny_kernel<false, true, false><<<grid, block, 0, stream>>>(g);
+    else sgemm_tiny_kernel<true, true, false><<<grid, block, 0, stream>>>(g);
+    int rc = check_launch("sgemm (tiny): kernel launch");
+    if (rc != LHIP_OK || g.splits <= 1) return rc;
+    return launch_reduce(g, batch, stream);
+}
 
 int launch_small(int ta, int tb, GemmArgs g, int batch, hipStream_t stream)
 {
@@ -421,10 +583,13 @@ int launch_small(int ta, int tb, GemmArgs g, int batch, hipStream_t stream)
     if (nwg > 0x7fffffffLL) return fail(LHIP_E_CAPACITY, "sgemm: %lld workgroups exceed the grid limit", nwg);
     if (g.splits <= 1) { g.splits = 1; g.kchunk = g.K; g.ws = nullptr; }
     dim3 grid(static_cast<unsigned>(nwg), batch, g.splits);
-    if (!ta && !tb) launch_small_t<false, false>(g, grid, stream);
-    else if (ta && !tb) launch_small_t<true, false>(g, grid, stream);
-    else if (!ta && tb) launch_small_t<false, true>(g, grid, stream);
-    else launch_small_t<true, true>(g, grid, stream);
+    if (g.Kb != g.K) {   // batch-reduce (sgemm_run admits it for non-transposed A only)
+        if (!tb) launch_small_t<false, false, true>(g, grid, stream);
+        else launch_small_t<false, true, true>(g, grid, stream);
+    } else if (!ta && !tb) launch_small_t<false, false, false>(g, grid, stream);
+    else if (ta && !tb) launch_small_t<true, false, false>(g, grid, stream);
+    else if (!ta && tb) launch_small_t<false, true, false>(g, grid, stream);
+    else launch_small_t<true, true, false>(g, grid, stream);
     int rc = check_launch("sgemm (small): kernel launch");
     if (rc != LHIP_OK || g.splits <= 1) return rc;
     return launch_reduce(g, batch, stream);
@@ -475,13 +640,17 @@ int splitk_plan(int m, int n, int k, int batch, size_t ws_floats, int* kchunk_ou
     long long tiles, min_k;
     int unit;
     if (use_small_kernel(m, n, k)) {
-        // 32x32 tiles, K shared by four waves: split only very long K (a wave
-        // covers K/4 at ~64 clocks per k; below 2048 the extra reduce launch
-        // costs more than it saves)
-        if (k < 2048) return 1;
+        // 32x32 tiles, K shared by four waves: split only long K (each wave
+        // walks K/4 serially; below 1024 the extra reduce launch costs more
+        // than the shorter walk saves)
+        if (k < 1024) return 1;
         tiles = static_cast<long long>(ceil_div(m, 32)) * ceil_div(n, 32) * batch;
         unit = 32;
-        min_k = 512;
+        min_k = 256;
+        if (tiles < cus) {   // 16x16 tiles: a pass of the four waves covers 512 k
+            tiles = static_cast<long long>(ceil_div(m, 16)) * ceil_div(n, 16) * batch;
+            min_k = 512;
+        }
     } else {
         // 64x64 tiles, 32-deep K tiles walked by one workgroup
         tiles = tiles64;
@@ -522,27 +691,53 @@ int sgemm_run(int ta, int tb, int m, int n, int k, float alpha,
     if (batch > 1 && (sA < 0 || sB < 0 || sC < 0 || o.sA2 < 0 || o.sB2 < 0 || o.sC2 < 0))
         return fail(LHIP_E_SHAPE, "sgemm: negative batch stride");
     if (o.inner <= 0) return fail(LHIP_E_ARG, "sgemm: inner batch count must be > 0");
+    if (o.kblocks <= 0) return fail(LHIP_E_ARG, "sgemm: kblocks must be > 0");
+    const long long big_tiles = static_cast<long long>(ceil_div(m, 128)) * ceil_div(n, 128) * batch;
+    const long long tiles64 = static_cast<long long>(ceil_div(m, 64)) * ceil_div(n, 64) * batch;
+    const int cus = st().cu_count > 0 ? st().cu_count : 256;
+    const long long k_all = static_cast<long long>(k) * o.kblocks;
+    if (o.kblocks > 1 && k > 0) {
+        // One launch when the small kernel takes the whole K range; otherwise
+        // (transposed A, K not a multiple of 4, or a large problem) the blocks
+        // are accumulated by successive launches.
+        const bool one = !ta && k % 4 == 0 && k_all <= 0x7fffffffLL && big_tiles < cus && tiles64 < cus &&
+                         use_small_kernel(m, n, static_cast<int>(k_all));
+        if (!one) {
+            GemmOpts oj = o;
+            oj.kblocks = 1;
+            for (int j = 0; j < o.kblocks; ++j) {
+                if (j == 1) { oj.R = nullptr; oj.ldr = 0; }
+                const int rc = sgemm_run(ta, tb, m, n, k, alpha, A + j * o.sAk, lda, sA, B + j * o.sBk, ldb, sB,
+                                         j == 0 ? beta : 1.f, C, ldc, sC, batch, oj, stream);
+                if (rc != LHIP_OK) return rc;
+            }
+            return LHIP_OK;
+        }
+    }
+    const bool br = o.kblocks > 1 && k > 0;
     GemmArgs g{};
-    g.M = m; g.N = n; g.K = k; g.alpha = alpha; g.beta = beta;
+    g.M = m; g.N = n; g.K = static_cast<int>(br ? k_all : k); g.alpha = alpha; g.beta = beta;
+    g.Kb = k; g.sAk = br ? o.sAk : 0; g.sBk = br ? o.sBk : 0;
     g.A = A; g.lda = lda; g.sA = sA; g.sA2 = o.sA2;
     g.B = B; g.ldb = ldb; g.sB = sB; g.sB2 = o.sB2;
     g.C = C; g.ldc = ldc; g.sC = sC; g.sC2 = o.sC2;
     g.R = o.R; g.ldr = o.ldr;
     g.inner = o.inner;
-    g.vecA = (k > 0 && lda % 4 == 0 && aligned16(A) && (batch == 1 || (sA % 4 == 0 && o.sA2 % 4 == 0))) ? 1 : 0;
-    g.vecB = (k > 0 && ldb % 4 == 0 && aligned16(B) && (batch == 1 || (sB % 4 == 0 && o.sB2 % 4 == 0))) ? 1 : 0;
+    g.vecA = (k > 0 && lda % 4 == 0 && aligned16(A) && (batch == 1 || (sA % 4 == 0 && o.sA2 % 4 == 0)) &&
+              g.sAk % 4 == 0) ? 1 : 0;
+    g.vecB = (k > 0 && ldb % 4 == 0 && aligned16(B) && (batch == 1 || (sB % 4 == 0 && o.sB2 % 4 == 0)) &&
+              g.sBk % 4 == 0) ? 1 : 0;
     // Large problems: 128x128 tiles (64x64 per wave); mid-size: 64x64 tiles;
     // small (fewer 64x64 tiles than CUs): 32x32 tiles with K shared by the
     // four waves of a workgroup, split over workgroups when K is very long
     // (split-K partials in o.ws).
-    const long long big_tiles = static_cast<long long>(ceil_div(m, 128)) * ceil_div(n, 128) * batch;
-    const int cus = st().cu_count > 0 ? st().cu_count : 256;
     if (big_tiles >= cus) return launch_cfg<128, 128, 32>(ta, tb, g, batch, stream);
-    const long long tiles64 = static_cast<long long>(ceil_div(m, 64)) * ceil_div(n, 64) * batch;
     if (tiles64 >= cus) return launch_cfg<64, 64, 32>(ta, tb, g, batch, stream);
-    const bool small = use_small_kernel(m, n, k);
-    g.splits = o.ws ? splitk_plan(m, n, k, batch, o.ws_floats, &g.kchunk) : 1;
+    const bool small = use_small_kernel(m, n, g.K);
+    g.splits = o.ws ? splitk_plan(m, n, g.K, batch, o.ws_floats, &g.kchunk) : 1;
     g.ws = o.ws;
+    const long long tiles32 = static_cast<long long>(ceil_div(m, 32)) * ceil_div(n, 32) * batch;
+    if (small && tiles32 < cus) return launch_tiny(ta, tb, g, batch, stream);
     if (small) return launch_small(ta, tb, g, batch, stream);
     return launch_cfg<64, 64, 32>(ta, tb, g, batch, stream);
 }

@@ -76,12 +76,20 @@ int rmsnorm_fwd(const float* x, const float* w, float* y, float* inv, int rows, 
 int rmsnorm_bwd_parts(int rows, int cols);
 int rmsnorm_bwd(const float* x, const float* w, const float* inv, const float* dy, float* dx, float* dw,
                 int rows, int cols, int accumulate, float* work, size_t work_floats, hipStream_t s);
+// The two halves of rmsnorm_bwd: dx = (dres ? dres : 0) + the norm's backward,
+// with per-block dw partials into `partial` (skipped when NULL; *parts_out
+// receives their count), then the ordered column sum of the partials into dw.
+int rmsnorm_bwd_rows(const float* x, const float* w, const float* inv, const float* dy, float* dx,
+                     const float* dres, float* partial, size_t partial_floats, int rows, int cols, int* parts_out,
+                     hipStream_t s);
+int rmsnorm_bwd_colsum(const float* partial, int parts, float* dw, int cols, int accumulate, hipStream_t s);
 int softmax_fwd(const float* x, float* y, int rows, int cols, float scale, int causal, int offset, int group,
                 hipStream_t s);
 int softmax_bwd(const float* y, const float* dy, float* dx, int rows, int cols, float scale, int causal,
                 int offset, int group, int accumulate, hipStream_t s);
+// amax (optional): first index of each row's maximum logit, written in the same pass
 int ce_fused(const float* logits, const int* tgt, float* losses, float* dlogits, int rows, int V,
-             int ignore_index, float gscale, hipStream_t s);
+             int ignore_index, float gscale, hipStream_t s, int* amax = nullptr);
 int argmax_rows(const float* x, int* out, int rows, int cols, hipStream_t s);
 int swiglu_fwd(const float* g, int ldg, const float* u, int ldu, float* h, int ldh, int rows, int cols,
                hipStream_t s);
@@ -94,11 +102,14 @@ int embed_bwd(const float* g, const int* ids, float* dtable, int n, int dim, int
               hipStream_t s);
 int sumsq_blocks(long long n);
 int sumsq(const float* x, long long n, double* out, double* partial, int partial_len, hipStream_t s);
+// stage 1 only: sumsq_blocks(n) partial sums into `partial`
+int sumsq_partials(const float* x, long long n, double* partial, int partial_len, hipStream_t s);
 // hyper_dev (may be NULL): device floats {lr, momentum, wd, clip_norm, nesterov}
 // that override the by-value arguments (a replayed graph reads them there).
+// nparts > 0: sumsq_dev holds that many stage-1 partials, summed in the kernel.
 int sgd_step(float* p, float* g, float* v, long long n, const double* sumsq_dev, float lr, float momentum,
              float wd, float grad_scale, float clip_norm, int nesterov, float* gnorm_out, int* applied_out,
-             hipStream_t s, const float* hyper_dev);
+             hipStream_t s, const float* hyper_dev, int nparts = 0);
 int sum_f32(const float* x, int n, float scale, float* out, hipStream_t s);
 // Fused per-(window, head) attention of the LMTrain step (T <= 64, head_dim <= 64, even).
 bool attn_fused_ok(int T, int hd);
@@ -121,6 +132,9 @@ struct GemmOpts {
     int ldr = 0;
     float* ws = nullptr;
     size_t ws_floats = 0;
+    // batch-reduce: C = alpha * sum_{j<kblocks} op(A + j*sAk) . op(B + j*sBk) + beta * R
+    int kblocks = 1;
+    long long sAk = 0, sBk = 0;
 };
 
 int sgemm_run(int transa, int transb, int m, int n, int k, float alpha,

@@ -58,12 +58,19 @@ struct LmModel {
     float *x = nullptr, *h = nullptr, *inv1 = nullptr, *qkv = nullptr, *P = nullptr, *ctx = nullptr;
     float *xmid = nullptr, *h2 = nullptr, *inv2 = nullptr, *zu = nullptr, *a = nullptr;
     float *xf = nullptr, *invf = nullptr, *logits = nullptr;
-    // backward scratch
-    float *dxf = nullptr, *dx = nullptr, *da = nullptr, *dzu = nullptr, *dh2 = nullptr, *dctx = nullptr;
-    float *dP = nullptr, *dS = nullptr, *dqkv = nullptr, *dh = nullptr, *work = nullptr;
-    size_t work_floats = 0;
-    float* splitk = nullptr;      // split-K partials of the small-tile GEMMs
-    size_t splitk_floats = 0;
+    // backward: gradient-chain buffers are per layer (gx[l] = dL/dx_l,
+    // gmid[l] = dL/dxmid_l, dzu[l], dqkv[l], the dw partials of each norm) so
+    // that nothing the side stream reads is overwritten within a step
+    float *dxf = nullptr, *gx = nullptr, *gmid = nullptr, *da = nullptr, *dzu = nullptr, *dh2 = nullptr;
+    float *dctx = nullptr, *dP = nullptr, *dS = nullptr, *dqkv = nullptr, *dh = nullptr, *work = nullptr;
+    size_t work_floats = 0;       // per norm call; work holds 2L+1 of them
+    float* splitk = nullptr;      // split-K partials: first half main stream, second half side stream
+    size_t splitk_floats = 0;     // per stream
+    // The weight gradients (dW GEMMs, norm-gain column sums, embedding) run on
+    // a side stream forked from and joined back into the step stream with
+    // events; captured together into the graph.
+    hipStream_t side = nullptr;
+    std::vector<hipEvent_t> ev;
     float2* rope_cs = nullptr;    // (cos, sin) of positions 0..T-1, pairs 0..hd/2-1
     bool fused_attn = false;      // per-(window, head) fused attention kernels
     // graph
@@ -114,14 +121,25 @@ int check_config(const lhip_lm_config_t* c)
 struct Enq {
     LmModel& m;
     hipStream_t s;
+    float* ws;   // split-K partials owned by this stream
 
     GemmOpts opts(int inner = 1) const
     {
         GemmOpts o;
         o.inner = inner;
-        o.ws = m.splitk;
+        o.ws = ws;
         o.ws_floats = m.splitk_floats;
         return o;
+    }
+    // C = sum_j A_j . op(B_j) over kb blocks (A_j = A + j*sak, B_j = B + j*sbk)
+    int brgemm(int tb, int M, int Nn, int K, int kb, const float* A, int lda, long long sak, const float* Bm,
+               int ldb, long long sbk, float* C, int ldc) const
+    {
+        GemmOpts o = opts();
+        o.kblocks = kb;
+        o.sAk = sak;
+        o.sBk = sbk;
+        return sgemm_run(0, tb, M, Nn, K, 1.f, A, lda, 0, Bm, ldb, 0, 0.f, C, ldc, 0, 1, o, s);
     }
     int gemm(int ta, int tb, int M, int Nn, int K, const float* A, int lda, const float* Bm, int ldb, float beta,
              float* C, int ldc) const
@@ -159,9 +177,38 @@ struct Enq {
         if (_rc != LHIP_OK) return _rc;    \
     } while (0)
 
-int enqueue_step(LmModel& m, hipStream_t s)
+// Event fork/join between the step stream and the side stream.  Every fork
+// uses a fresh event, so the same code serves eager launches and capture.
+struct Forker {
+    LmModel& m;
+    hipStream_t main;
+    size_t next = 0;
+
+    int link(hipStream_t from, hipStream_t to)
+    {
+        if (next >= m.ev.size()) return fail(LHIP_E_CAPACITY, "lm: out of step events");
+        hipEvent_t e = m.ev[next++];
+        LHIP_CHECK_HIP(hipEventRecord(e, from), "lm: event record");
+        LHIP_CHECK_HIP(hipStreamWaitEvent(to, e, 0), "lm: stream wait");
+        return LHIP_OK;
+    }
+    int fork() { return link(main, m.side); }   // side waits for all main-stream work so far
+    int join() { return link(m.side, main); }   // main waits for all side-stream work so far
+};
+
+// Optimizer hyper-parameters passed by value (eager launches); a captured
+// step passes none and reads them from m.hyper, which each launch refreshes.
+struct Hyper {
+    float lr, momentum, wd, clip;
+    int nesterov;
+};
+
+int enqueue_step(LmModel& m, hipStream_t s, const Hyper* hp)
 {
-    const Enq q{m, s};
+    const Enq q{m, s, m.splitk};
+    const Enq q2{m, m.side, m.splitk + m.splitk_floats};
+    Forker fk{m, s};
+    const hipStream_t s2 = m.side;
     const int N = m.N, D = m.D, F = m.F, V = m.V, H = m.H, hd = m.hd, T = m.T, L = m.L;
     const long long ND = static_cast<long long>(N) * D, NF = static_cast<long long>(N) * F;
     const long long TT = static_cast<long long>(T) * T, HTT = H * TT, TD = static_cast<long long>(T) * D;
@@ -173,7 +220,8 @@ int enqueue_step(LmModel& m, hipStream_t s)
     const float* emb = m.prm(0);
     const float* lnf = m.prm(1 + P_PER_LAYER * L);
 
-    LM_TRY(fill(m.grads, m.nparam, 0.f, s));   // opt.zero_grad()
+    // opt.zero_grad() needs no pass: every gradient tensor's first writer in
+    // the backward overwrites it (beta = 0 GEMMs, accumulate = 0 column sums)
 
     // ---------------- forward (transformer.lua:228-257) ----------------
     LM_TRY(embed_fwd(emb, m.ids, m.x, N, D, V, s));
@@ -220,15 +268,22 @@ int enqueue_step(LmModel& m, hipStream_t s)
     LM_TRY(rmsnorm_fwd(xL, lnf, m.xf, m.invf, N, D, eps, s));
     // tied head: logits = xf . emb^T
     LM_TRY(q.gemm(0, 1, N, V, D, m.xf, D, emb, D, 0.f, m.logits, V));
-    LM_TRY(argmax_rows(m.logits, m.amax, N, V, s));
     // per-row losses; dlogits = (softmax - onehot) / T written over the logits
-    LM_TRY(ce_fused(m.logits, m.tgt, m.losses, m.logits, N, V, -1, 1.0f / T, s));
+    LM_TRY(ce_fused(m.logits, m.tgt, m.losses, m.logits, N, V, -1, 1.0f / T, s, m.amax));
 
     // ---------------- backward ----------------
+    // Main stream: the chain dlogits -> dx_L -> ... -> dx_0.  Side stream:
+    // every weight gradient, forked as soon as its inputs exist.
     const float* dlg = m.logits;
+    const size_t wf = m.work_floats;
+    auto gxl = [&](int l) { return m.gx + l * ND; };
+    LM_TRY(fk.fork());
+    LM_TRY(q2.gemm(1, 0, V, D, N, dlg, V, m.xf, D, 0.f, m.grd(0), D));            // gemb = dlogits^T . xf
     LM_TRY(q.gemm(0, 0, N, D, V, dlg, V, emb, D, 0.f, m.dxf, D));                // dxf = dlogits . emb
-    LM_TRY(q.gemm(1, 0, V, D, N, dlg, V, m.xf, D, 1.f, m.grd(0), D));             // gemb += dlogits^T . xf
-    LM_TRY(rmsnorm_bwd(xL, lnf, m.invf, m.dxf, m.dx, m.grd(1 + P_PER_LAYER * L), N, D, 0, m.work, m.work_floats, s));
+    int parts = 0, parts_ln1 = 0;
+    LM_TRY(rmsnorm_bwd_rows(xL, lnf, m.invf, m.dxf, gxl(L), nullptr, m.work, wf, N, D, &parts, s));
+    LM_TRY(fk.fork());
+    LM_TRY(rmsnorm_bwd_colsum(m.work, parts, m.grd(1 + P_PER_LAYER * L), D, 0, s2));
     for (int l = L - 1; l >= 0; --l) {
         const float* xl = m.x + l * ND;
         const float* h = m.h + l * ND;
@@ -241,50 +296,66 @@ int enqueue_step(LmModel& m, hipStream_t s)
         const float* inv2 = m.inv2 + static_cast<long long>(l) * N;
         const float* zu = m.zu + l * 2 * NF;
         const float* a = m.a + l * NF;
-        // f = a . W2
-        LM_TRY(q.gemm(0, 1, N, F, D, m.dx, D, m.prm(m.lt(l, P_W2)), D, 0.f, m.da, F));      // da = dx . W2^T
-        LM_TRY(q.gemm(1, 0, F, D, N, a, F, m.dx, D, 0.f, m.grd(m.lt(l, P_W2)), D));         // gW2 = a^T . dx
-        LM_TRY(swiglu_bwd(zu, F, zu + NF, F, m.da, F, m.dzu, F, m.dzu + NF, F, N, F, 0, s));
-        LM_TRY(q.gemm(0, 1, N, D, F, m.dzu, F, m.prm(m.lt(l, P_W1)), F, 0.f, m.dh2, D));    // dh2 = dz1 . W1^T
-        LM_TRY(q.gemm(0, 1, N, D, F, m.dzu + NF, F, m.prm(m.lt(l, P_W3)), F, 1.f, m.dh2, D)); //     + du . W3^T
-        LM_TRY(q.bgemm(1, 0, D, F, N, h2, D, 0, m.dzu, F, NF, 0.f, m.grd(m.lt(l, P_W1)), F,
-                       static_cast<long long>(D) * F, 2));                                   // gW1, gW3
-        LM_TRY(rmsnorm_bwd(xmid, m.prm(m.lt(l, P_LN2)), inv2, m.dh2, m.dx, m.grd(m.lt(l, P_LN2)), N, D, 1, m.work,
-                           m.work_floats, s));
+        const float* gin = gxl(l + 1);                 // dL/dx_{l+1}
+        float* gmid = m.gmid + l * ND;                 // dL/dxmid_l
+        float* dzu = m.dzu + l * 2 * NF;
+        float* dqkv = m.dqkv + l * 3 * ND;
+        float* work2 = m.work + (2 * l + 1) * wf;      // ln2 dw partials
+        float* work1 = m.work + (2 * l + 2) * wf;      // ln1 dw partials
+        // f = a . W2 ; a = silu(z1) * u
+        LM_TRY(q.gemm(0, 1, N, F, D, gin, D, m.prm(m.lt(l, P_W2)), D, 0.f, m.da, F));      // da = gin . W2^T
+        LM_TRY(swiglu_bwd(zu, F, zu + NF, F, m.da, F, dzu, F, dzu + NF, F, N, F, 0, s));
+        LM_TRY(fk.fork());
+        if (l + 1 < L)   // ln1 dw of the layer above (its partials are ready since the last fork)
+            LM_TRY(rmsnorm_bwd_colsum(m.work + (2 * (l + 1) + 2) * wf, parts_ln1, m.grd(m.lt(l + 1, P_LN1)), D, 0, s2));
+        LM_TRY(q2.gemm(1, 0, F, D, N, a, F, gin, D, 0.f, m.grd(m.lt(l, P_W2)), D));         // gW2 = a^T . gin
+        LM_TRY(q2.bgemm(1, 0, D, F, N, h2, D, 0, dzu, F, NF, 0.f, m.grd(m.lt(l, P_W1)), F,
+                        static_cast<long long>(D) * F, 2));                                   // gW1, gW3
+        // dh2 = dz1 . W1^T + du . W3^T (adjacent weights: one batch-reduce GEMM)
+        LM_TRY(q.brgemm(1, N, D, F, 2, dzu, F, NF, m.prm(m.lt(l, P_W1)), F, static_cast<long long>(D) * F, m.dh2, D));
+        LM_TRY(rmsnorm_bwd_rows(xmid, m.prm(m.lt(l, P_LN2)), inv2, m.dh2, gmid, gin, work2, wf, N, D, &parts, s));
         // o = ctx . Wo
-        LM_TRY(q.gemm(0, 1, N, D, D, m.dx, D, m.prm(m.lt(l, P_WO)), D, 0.f, m.dctx, D));    // dctx = dx . Wo^T
-        LM_TRY(q.gemm(1, 0, D, D, N, ctx, D, m.dx, D, 0.f, m.grd(m.lt(l, P_WO)), D));       // gWo = ctx^T . dx
+        LM_TRY(q.gemm(0, 1, N, D, D, gmid, D, m.prm(m.lt(l, P_WO)), D, 0.f, m.dctx, D));    // dctx = gmid . Wo^T
         if (m.fused_attn) {
             // dP, dv, softmax backward, dq, dk and the inverse RoPE per (window, head)
-            LM_TRY(attn_bwd(qkv, m.rope_cs, P, m.dctx, m.dqkv, m.B, H, T, hd, scale, causal, s));
+            LM_TRY(attn_bwd(qkv, m.rope_cs, P, m.dctx, dqkv, m.B, H, T, hd, scale, causal, s));
         } else {
             // per (window, head): dP = dO . v^T ; dv = P^T . dO
             LM_TRY(q.hgemm(0, 1, T, T, hd, m.dctx, D, hd, TD, qkv + 2 * ND, D, hd, TD, m.dP, T, TT, HTT));
-            LM_TRY(q.hgemm(1, 0, T, hd, T, P, T, TT, HTT, m.dctx, D, hd, TD, m.dqkv + 2 * ND, D, hd, TD));
+            LM_TRY(q.hgemm(1, 0, T, hd, T, P, T, TT, HTT, m.dctx, D, hd, TD, dqkv + 2 * ND, D, hd, TD));
             // dS = scale * softmax_bwd(P, dP)
             LM_TRY(softmax_bwd(P, m.dP, m.dS, m.B * H * T, T, scale, causal, 0, T, 0, s));
             // dq = dS . k_rot ; dk = dS^T . q_rot
-            LM_TRY(q.hgemm(0, 0, T, hd, T, m.dS, T, TT, HTT, qkv + ND, D, hd, TD, m.dqkv, D, hd, TD));
-            LM_TRY(q.hgemm(1, 0, T, hd, T, m.dS, T, TT, HTT, qkv, D, hd, TD, m.dqkv + ND, D, hd, TD));
+            LM_TRY(q.hgemm(0, 0, T, hd, T, m.dS, T, TT, HTT, qkv + ND, D, hd, TD, dqkv, D, hd, TD));
+            LM_TRY(q.hgemm(1, 0, T, hd, T, m.dS, T, TT, HTT, qkv, D, hd, TD, dqkv + ND, D, hd, TD));
             // RoPE backward (inverse rotation) on dq and dk
-            LM_TRY(rope(m.dqkv, nullptr, 2 * N, H, hd, D, 0, T, base, 1, 1, s));
+            LM_TRY(rope(dqkv, nullptr, 2 * N, H, hd, D, 0, T, base, 1, 1, s));
         }
-        // dh = dq.Wq^T + dk.Wk^T + dv.Wv^T ; gW{q,k,v} = h^T . d{q,k,v}
-        LM_TRY(q.gemm(0, 1, N, D, D, m.dqkv, D, m.prm(m.lt(l, P_WQ)), D, 0.f, m.dh, D));
-        LM_TRY(q.gemm(0, 1, N, D, D, m.dqkv + ND, D, m.prm(m.lt(l, P_WK)), D, 1.f, m.dh, D));
-        LM_TRY(q.gemm(0, 1, N, D, D, m.dqkv + 2 * ND, D, m.prm(m.lt(l, P_WV)), D, 1.f, m.dh, D));
-        LM_TRY(q.bgemm(1, 0, D, D, N, h, D, 0, m.dqkv, D, ND, 0.f, m.grd(m.lt(l, P_WQ)), D,
-                       static_cast<long long>(D) * D, 3));
-        LM_TRY(rmsnorm_bwd(xl, m.prm(m.lt(l, P_LN1)), inv1, m.dh, m.dx, m.grd(m.lt(l, P_LN1)), N, D, 1, m.work,
-                           m.work_floats, s));
+        LM_TRY(fk.fork());
+        LM_TRY(rmsnorm_bwd_colsum(work2, parts, m.grd(m.lt(l, P_LN2)), D, 0, s2));
+        LM_TRY(q2.gemm(1, 0, D, D, N, ctx, D, gmid, D, 0.f, m.grd(m.lt(l, P_WO)), D));       // gWo = ctx^T . gmid
+        LM_TRY(q2.bgemm(1, 0, D, D, N, h, D, 0, dqkv, D, ND, 0.f, m.grd(m.lt(l, P_WQ)), D,
+                        static_cast<long long>(D) * D, 3));                                   // gW{q,k,v}
+        // dh = dq.Wq^T + dk.Wk^T + dv.Wv^T (adjacent weights: one batch-reduce GEMM)
+        LM_TRY(q.brgemm(1, N, D, D, 3, dqkv, D, ND, m.prm(m.lt(l, P_WQ)), D, static_cast<long long>(D) * D, m.dh, D));
+        LM_TRY(rmsnorm_bwd_rows(xl, m.prm(m.lt(l, P_LN1)), inv1, m.dh, gxl(l), gmid, work1, wf, N, D, &parts_ln1,
+                                s));
     }
-    LM_TRY(embed_bwd(m.dx, m.ids, m.grd(0), N, D, V, 1.f, 1, s));
+    LM_TRY(fk.fork());
+    LM_TRY(rmsnorm_bwd_colsum(m.work + 2 * wf, parts_ln1, m.grd(m.lt(0, P_LN1)), D, 0, s2));
+    LM_TRY(embed_bwd(gxl(0), m.ids, m.grd(0), N, D, V, 1.f, 1, s2));   // after gemb: same stream
+    LM_TRY(fk.join());
 
     // ---------------- optimizer (lmtrain.lua:1212-1226) ----------------
-    LM_TRY(sumsq(m.grads, m.nparam, m.ss, m.ss_part, m.ss_blocks, s));
+    // squared-norm partials; the SGD kernel finishes the sum itself
+    LM_TRY(sumsq_partials(m.grads, m.nparam, m.ss_part, m.ss_blocks, s));
     const float gscale = m.B > 1 ? 1.0f / m.B : 1.0f;
-    LM_TRY(sgd_step(m.params, m.grads, m.vel, m.nparam, m.ss, 0.f, 0.f, 0.f, gscale, 0.f, 0, m.gnorm, m.applied, s,
-                    m.hyper));
+    if (hp)
+        LM_TRY(sgd_step(m.params, m.grads, m.vel, m.nparam, m.ss_part, hp->lr, hp->momentum, hp->wd, gscale, hp->clip,
+                        hp->nesterov, m.gnorm, m.applied, s, nullptr, m.ss_blocks));
+    else
+        LM_TRY(sgd_step(m.params, m.grads, m.vel, m.nparam, m.ss_part, 0.f, 0.f, 0.f, gscale, 0.f, 0, m.gnorm,
+                        m.applied, s, m.hyper, m.ss_blocks));
     return LHIP_OK;
 }
 
@@ -300,7 +371,7 @@ int capture_step(LmModel& m, hipStream_t s)
 {
     drop_graph(m);
     LHIP_CHECK_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "lm: begin capture");
-    const int rc = enqueue_step(m, s);
+    const int rc = enqueue_step(m, s, nullptr);
     hipGraph_t g = nullptr;
     const hipError_t e = hipStreamEndCapture(s, &g);
     if (rc != LHIP_OK) {
@@ -318,6 +389,32 @@ int capture_step(LmModel& m, hipStream_t s)
 }
 
 LmModel* as_model(void* p) { return static_cast<LmModel*>(p); }
+
+// Device resources of a model (graph, events, side stream, arena); the caller
+// has synchronized.
+void release(LmModel& m)
+{
+    drop_graph(m);
+    for (hipEvent_t e : m.ev) (void)hipEventDestroy(e);
+    m.ev.clear();
+    if (m.side) (void)hipStreamDestroy(m.side);
+    m.side = nullptr;
+    if (m.arena) (void)hipFree(m.arena);
+    m.arena = nullptr;
+}
+
+// Side stream (default priority) and the fork/join events of one step.
+int make_streams(LmModel& m)
+{
+    LHIP_CHECK_HIP(hipStreamCreateWithFlags(&m.side, hipStreamNonBlocking), "lhip_lm_create: side stream");
+    const int nev = 2 * m.L + 8;
+    for (int i = 0; i < nev; ++i) {
+        hipEvent_t e = nullptr;
+        LHIP_CHECK_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming), "lhip_lm_create: event");
+        m.ev.push_back(e);
+    }
+    return LHIP_OK;
+}
 
 }  // namespace
 }  // namespace lhip
@@ -375,7 +472,7 @@ LHIP_API int lhip_lm_create(const lhip_lm_config_t* cfg, void** model)
     const long long ND = N * D, NF = N * F, PL = static_cast<long long>(m->B) * m->H * m->T * m->T;
     m->ss_blocks = lhip::sumsq_blocks(m->nparam);
     m->work_floats = static_cast<size_t>(lhip::rmsnorm_bwd_parts(m->N, m->D)) * m->D;
-    m->splitk_floats = static_cast<size_t>(1) << 23;   // 32 MiB; the planner caps splits to fit
+    m->splitk_floats = static_cast<size_t>(1) << 22;   // 16 MiB per stream; the planner caps splits to fit
     // carve every buffer out of one allocation, each 256-byte aligned
     struct Slot { void** dst; size_t bytes; };
     std::vector<Slot> slots = {
@@ -406,17 +503,18 @@ LHIP_API int lhip_lm_create(const lhip_lm_config_t* cfg, void** model)
         {reinterpret_cast<void**>(&m->invf), sizeof(float) * N},
         {reinterpret_cast<void**>(&m->logits), sizeof(float) * N * V},
         {reinterpret_cast<void**>(&m->dxf), sizeof(float) * ND},
-        {reinterpret_cast<void**>(&m->dx), sizeof(float) * ND},
+        {reinterpret_cast<void**>(&m->gx), sizeof(float) * (L + 1) * ND},
+        {reinterpret_cast<void**>(&m->gmid), sizeof(float) * L * ND},
         {reinterpret_cast<void**>(&m->da), sizeof(float) * NF},
-        {reinterpret_cast<void**>(&m->dzu), sizeof(float) * 2 * NF},
+        {reinterpret_cast<void**>(&m->dzu), sizeof(float) * L * 2 * NF},
         {reinterpret_cast<void**>(&m->dh2), sizeof(float) * ND},
         {reinterpret_cast<void**>(&m->dctx), sizeof(float) * ND},
         {reinterpret_cast<void**>(&m->dP), sizeof(float) * PL},
         {reinterpret_cast<void**>(&m->dS), sizeof(float) * PL},
-        {reinterpret_cast<void**>(&m->dqkv), sizeof(float) * 3 * ND},
+        {reinterpret_cast<void**>(&m->dqkv), sizeof(float) * L * 3 * ND},
         {reinterpret_cast<void**>(&m->dh), sizeof(float) * ND},
-        {reinterpret_cast<void**>(&m->work), sizeof(float) * m->work_floats},
-        {reinterpret_cast<void**>(&m->splitk), sizeof(float) * m->splitk_floats},
+        {reinterpret_cast<void**>(&m->work), sizeof(float) * (2 * L + 1) * m->work_floats},
+        {reinterpret_cast<void**>(&m->splitk), sizeof(float) * 2 * m->splitk_floats},
         {reinterpret_cast<void**>(&m->rope_cs), sizeof(float2) * m->T * (m->hd / 2)},
     };
     size_t total = 0;
@@ -465,6 +563,11 @@ LHIP_API int lhip_lm_create(const lhip_lm_config_t* cfg, void** model)
     }
     m->fused_attn = lhip::attn_fused_ok(m->T, m->hd);
     m->h_tgt.assign(static_cast<size_t>(N), 0);
+    if (int src = lhip::make_streams(*m)) {
+        lhip::release(*m);
+        delete m;
+        return src;
+    }
     *model = m;
     return LHIP_OK;
 }
@@ -475,8 +578,8 @@ LHIP_API int lhip_lm_destroy(void* model)
     auto* m = lhip::as_model(model);
     if (st().ready) {
         (void)hipStreamSynchronize(st().stream);
-        lhip::drop_graph(*m);
-        (void)hipFree(m->arena);
+        if (m->side) (void)hipStreamSynchronize(m->side);
+        lhip::release(*m);
     }
     delete m;
     return LHIP_OK;
@@ -557,14 +660,15 @@ LHIP_API int lhip_lm_step_sgd(void* model, float lr, float momentum, float weigh
     if (!(lr >= 0.f) || !(momentum >= 0.f) || !(weight_decay >= 0.f) || !(clip_norm >= 0.f))
         return fail(LHIP_E_ARG, "lhip_lm_step_sgd: lr, momentum, weight_decay and clip_norm must be >= 0");
     hipStream_t s = st().stream;
-    lhip::set_hyper_kernel<<<1, 64, 0, s>>>(m->hyper, lr, momentum, weight_decay, clip_norm, nesterov ? 1.f : 0.f);
-    if (int rc = lhip::check_launch("lhip_lm_step_sgd: hyper")) return rc;
     if (m->use_graph) {
+        lhip::set_hyper_kernel<<<1, 64, 0, s>>>(m->hyper, lr, momentum, weight_decay, clip_norm, nesterov ? 1.f : 0.f);
+        if (int rc = lhip::check_launch("lhip_lm_step_sgd: hyper")) return rc;
         if (!m->exec)
             if (int rc = lhip::capture_step(*m, s)) return rc;
         LHIP_CHECK_HIP(hipGraphLaunch(m->exec, s), "lhip_lm_step_sgd: graph launch");
     } else {
-        if (int rc = lhip::enqueue_step(*m, s)) return rc;
+        const lhip::Hyper hp{lr, momentum, weight_decay, clip_norm, nesterov ? 1 : 0};
+        if (int rc = lhip::enqueue_step(*m, s, &hp)) return rc;
     }
     ++m->steps;
     return LHIP_OK;

@@ -59,16 +59,35 @@ __global__ void __launch_bounds__(64) sum_stage2(const double* __restrict__ part
 // sum of squares of the RAW gradients; the norm of the scaled gradients is
 // grad_scale * sqrt(sumsq).  g is overwritten with the gradient actually used
 // (after scale and clip) so callers can inspect it, as optim2 mutates grads.
-__global__ void sgd_step_kernel(float* __restrict__ p, float* __restrict__ g, float* __restrict__ v, long long n,
-                                const double* __restrict__ sumsq, float lr, float momentum, float wd,
-                                float grad_scale, float clip_norm, int nesterov, float* __restrict__ gnorm_out,
-                                int* __restrict__ applied_out, const float* __restrict__ hyper)
+//
+// With nparts > 0, `sumsq` holds the nparts stage-1 partials instead of the
+// total: every block sums them in sum_stage2's order (so all blocks, and the
+// two-kernel form, agree bit for bit), which saves the second reduction launch.
+__global__ void __launch_bounds__(256)
+sgd_step_kernel(float* __restrict__ p, float* __restrict__ g, float* __restrict__ v, long long n,
+                const double* __restrict__ sumsq, int nparts, float lr, float momentum, float wd,
+                float grad_scale, float clip_norm, int nesterov, float* __restrict__ gnorm_out,
+                int* __restrict__ applied_out, const float* __restrict__ hyper)
 {
     if (hyper) {   // hyper-parameters resident on the device (graph replay)
         lr = hyper[0]; momentum = hyper[1]; wd = hyper[2]; clip_norm = hyper[3];
         nesterov = hyper[4] != 0.f;
     }
-    const double norm = static_cast<double>(grad_scale) * sqrt(sumsq[0]);
+    double total;
+    if (nparts > 0) {
+        __shared__ double tot;
+        if (threadIdx.x < 64) {
+            double s = 0.0;
+            for (int i = threadIdx.x; i < nparts; i += 64) s += sumsq[i];
+            s = wave_sum(s);
+            if (threadIdx.x == 0) tot = s;
+        }
+        __syncthreads();
+        total = tot;
+    } else {
+        total = sumsq[0];
+    }
+    const double norm = static_cast<double>(grad_scale) * sqrt(total);
     const bool finite = isfinite(norm);
     const long long t0 = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
     if (t0 == 0) {
@@ -109,7 +128,9 @@ __global__ void __launch_bounds__(256) sum_f32_kernel(const float* __restrict__ 
 
 int sumsq_blocks(long long n)
 {
-    long long b = (n + 4LL * kRedThreads - 1) / (4LL * kRedThreads);
+    // 16 values per thread: few partials, so the SGD kernel's blocks can each
+    // finish the reduction themselves
+    long long b = (n + 16LL * kRedThreads - 1) / (16LL * kRedThreads);
     if (b > kRedMaxBlocks) b = kRedMaxBlocks;
     return static_cast<int>(b < 1 ? 1 : b);
 }
@@ -126,9 +147,19 @@ int sumsq(const float* x, long long n, double* out, double* partial, int partial
     return check_launch("sumsq");
 }
 
+int sumsq_partials(const float* x, long long n, double* partial, int partial_len, hipStream_t s)
+{
+    if (n < 0) return fail(LHIP_E_SHAPE, "sumsq: n < 0");
+    if (n > 0 && !x) return fail(LHIP_E_NULL, "sumsq: x is NULL");
+    const int nb = sumsq_blocks(n);
+    if (nb > partial_len) return fail(LHIP_E_CAPACITY, "sumsq: workspace %d < %d blocks", partial_len, nb);
+    sumsq_stage1<<<nb, kRedThreads, 0, s>>>(x, n, partial, aligned16(x) ? 1 : 0);
+    return check_launch("sumsq");
+}
+
 int sgd_step(float* p, float* g, float* v, long long n, const double* sumsq_dev, float lr, float momentum,
              float wd, float grad_scale, float clip_norm, int nesterov, float* gnorm_out, int* applied_out,
-             hipStream_t s, const float* hyper_dev)
+             hipStream_t s, const float* hyper_dev, int nparts)
 {
     if (n < 0) return fail(LHIP_E_SHAPE, "sgd_step: n < 0");
     if (!sumsq_dev) return fail(LHIP_E_NULL, "sgd_step: sumsq is NULL");
@@ -139,8 +170,9 @@ int sgd_step(float* p, float* g, float* v, long long n, const double* sumsq_dev,
     long long blocks = (n + 255) / 256;
     if (blocks > 4LL * cus) blocks = 4LL * cus;
     if (blocks < 1) blocks = 1;
-    sgd_step_kernel<<<static_cast<int>(blocks), 256, 0, s>>>(p, g, v, n, sumsq_dev, lr, momentum, wd, grad_scale,
-                                                           clip_norm, nesterov, gnorm_out, applied_out, hyper_dev);
+    sgd_step_kernel<<<static_cast<int>(blocks), 256, 0, s>>>(p, g, v, n, sumsq_dev, nparts, lr, momentum, wd,
+                                                           grad_scale, clip_norm, nesterov, gnorm_out, applied_out,
+                                                           hyper_dev);
     return check_launch("sgd_step");
 }
 

@@ -147,14 +147,16 @@ rmsnorm_fwd_generic(const float* __restrict__ x, const float* __restrict__ w, fl
     if (inv && lane == 0) inv[row] = r;
 }
 
-// dx = g*w*r - x*(r^3/N)*sum_j(g_j w_j x_j)  (+ dx if acc);
-// per-block partial dw over the block's rows -> partial[block][cols]
-// (tensor2.lua:641-666).  Rows are walked grid-stride, one wave per row.
+// dx = g*w*r - x*(r^3/N)*sum_j(g_j w_j x_j)  (+ dres, the incoming residual
+// gradient, when given; dres may be dx itself);
+// per-block partial dw over the block's rows -> partial[block][cols], skipped
+// when partial is NULL (tensor2.lua:641-666).  Rows are walked grid-stride,
+// one wave per row.
 template <int NV>
 __global__ void __launch_bounds__(kRowThreads)
 rmsnorm_bwd_vec(const float* __restrict__ x, const float* __restrict__ w, const float* __restrict__ inv,
-                const float* __restrict__ dy, float* __restrict__ dx, float* __restrict__ partial,
-                int rows, int cols, int acc_dx)
+                const float* __restrict__ dy, float* dx, const float* dres, float* __restrict__ partial,
+                int rows, int cols)
 {
     extern __shared__ float4 sdw[];   // [kWavesPerBlock][cols/4]
     const int wv = threadIdx.x >> 6;
@@ -187,6 +189,7 @@ rmsnorm_bwd_vec(const float* __restrict__ x, const float* __restrict__ w, const 
         const float r = inv[row];
         const float coef = dot * r * r * r * inv_n;
         float4* dxr = reinterpret_cast<float4*>(dx + base);
+        const float4* drr = reinterpret_cast<const float4*>(dres + base);
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const int c = lane + 64 * i;
@@ -198,14 +201,15 @@ rmsnorm_bwd_vec(const float* __restrict__ x, const float* __restrict__ w, const 
                     f4set(o, e, gg * f4get(wr[i], e) * r - xx * coef);
                     f4set(dwp[i], e, f4get(dwp[i], e) + gg * xx * r);
                 }
-                if (acc_dx) {
-                    const float4 old = dxr[c];
+                if (dres) {
+                    const float4 old = drr[c];
                     o.x += old.x; o.y += old.y; o.z += old.z; o.w += old.w;
                 }
                 dxr[c] = o;
             }
         }
     }
+    if (!partial) return;   // uniform: no dw wanted
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
         const int c = lane + 64 * i;
@@ -226,17 +230,18 @@ rmsnorm_bwd_vec(const float* __restrict__ x, const float* __restrict__ w, const 
 
 __global__ void __launch_bounds__(kRowThreads)
 rmsnorm_bwd_generic(const float* __restrict__ x, const float* __restrict__ w, const float* __restrict__ inv,
-                    const float* __restrict__ dy, float* __restrict__ dx, float* __restrict__ partial,
-                    int rows, int cols, int acc_dx)
+                    const float* __restrict__ dy, float* dx, const float* dres, float* __restrict__ partial,
+                    int rows, int cols)
 {
     // one wave per row, rows grid-stride; dw partial per block accumulated
     // column by column through LDS-free atomics-free passes: each wave owns
-    // its partial row in `partial` ([gridDim.x * waves][cols]).
+    // its partial row in `partial` ([gridDim.x * waves][cols]), if given.
     const int wv = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
     const int gw = blockIdx.x * kWavesPerBlock + wv;
-    float* pw = partial + static_cast<size_t>(gw) * cols;
-    for (int c = lane; c < cols; c += 64) pw[c] = 0.f;
+    float* pw = partial ? partial + static_cast<size_t>(gw) * cols : nullptr;
+    if (pw)
+        for (int c = lane; c < cols; c += 64) pw[c] = 0.f;
     const float inv_n = 1.0f / static_cast<float>(cols);
     for (int row = gw; row < rows; row += gridDim.x * kWavesPerBlock) {
         const size_t base = static_cast<size_t>(row) * cols;
@@ -248,8 +253,8 @@ rmsnorm_bwd_generic(const float* __restrict__ x, const float* __restrict__ w, co
         for (int c = lane; c < cols; c += 64) {
             const float gg = dy[base + c], xx = x[base + c];
             const float o = gg * w[c] * r - xx * coef;
-            dx[base + c] = acc_dx ? dx[base + c] + o : o;
-            pw[c] += gg * xx * r;
+            dx[base + c] = dres ? dres[base + c] + o : o;
+            if (pw) pw[c] += gg * xx * r;
         }
     }
 }
@@ -446,7 +451,7 @@ softmax_bwd_generic(const float* __restrict__ y, const float* __restrict__ dy, f
 template <int NT, int NV, bool PF>
 __global__ void __launch_bounds__(NT)
 ce_fused_vec(const float* logits, const int* __restrict__ tgt, float* __restrict__ losses,
-             float* dlogits, int rows, int V, int ignore_index, float gscale)
+             float* dlogits, int* __restrict__ amax, int rows, int V, int ignore_index, float gscale)
 {
     // One workgroup per row at a time.  With PF, rows are walked block-stride
     // and the next row is prefetched into registers while the current one is
@@ -455,6 +460,8 @@ ce_fused_vec(const float* logits, const int* __restrict__ tgt, float* __restrict
     // workgroup takes one row.
     constexpr int NW = NT / 64;
     __shared__ float red[NW];
+    __shared__ float redv[NW];
+    __shared__ int redi[NW];
     const int c4n = V >> 2;
     auto load = [&](Row1<NV>& r, int row) {
         const float4* xr = reinterpret_cast<const float4*>(logits + static_cast<size_t>(row) * V);
@@ -467,6 +474,19 @@ ce_fused_vec(const float* logits, const int* __restrict__ tgt, float* __restrict
     auto body = [&](Row1<NV>& r, int row) {
         const int t = tgt[row];
         const size_t base = static_cast<size_t>(row) * V;
+        if (amax) {   // argmax of the raw logits, for every row (ignored targets included)
+            float bv = -INFINITY;
+            int bi = -1;
+#pragma unroll
+            for (int i = 0; i < NV; ++i) {
+                const int c = threadIdx.x + NT * i;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (c < c4n && f4get(r.v[i], e) > bv) { bv = f4get(r.v[i], e); bi = 4 * c + e; }
+            }
+            const int am = block_argmax<NW>(bv, bi, redv, redi);
+            if (threadIdx.x == 0) amax[row] = am < 0 ? 0 : am;
+        }
         if (t < 0 || t >= V || t == ignore_index) {      // uniform in the block
             if (losses && threadIdx.x == 0) losses[row] = 0.f;
             if (dlogits) {
@@ -538,12 +558,22 @@ ce_fused_vec(const float* logits, const int* __restrict__ tgt, float* __restrict
 
 __global__ void __launch_bounds__(256)
 ce_fused_generic(const float* logits, const int* __restrict__ tgt, float* __restrict__ losses,
-                 float* dlogits, int rows, int V, int ignore_index, float gscale)
+                 float* dlogits, int* __restrict__ amax, int rows, int V, int ignore_index, float gscale)
 {
     __shared__ float red[4];
+    __shared__ float redv[4];
+    __shared__ int redi[4];
     const int row = blockIdx.x;
     const int t = tgt[row];
     const size_t base = static_cast<size_t>(row) * V;
+    if (amax) {
+        float bv = -INFINITY;
+        int bi = -1;
+        for (int c = threadIdx.x; c < V; c += 256)
+            if (logits[base + c] > bv) { bv = logits[base + c]; bi = c; }
+        const int am = block_argmax<4>(bv, bi, redv, redi);
+        if (threadIdx.x == 0) amax[row] = am < 0 ? 0 : am;
+    }
     if (t < 0 || t >= V || t == ignore_index) {
         if (losses && threadIdx.x == 0) losses[row] = 0.f;
         if (dlogits) for (int c = threadIdx.x; c < V; c += 256) dlogits[base + c] = 0.f;
@@ -585,13 +615,7 @@ argmax_rows_kernel(const float* __restrict__ x, int* __restrict__ out, int rows,
         const float v = xr[c];
         if (v > bv) { bv = v; bi = c; }
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(bv, o, 64);
-        const int oi = __shfl_xor(bi, o, 64);
-        const bool take = (oi >= 0) && (bi < 0 || ov > bv || (ov == bv && oi < bi));
-        if (take) { bv = ov; bi = oi; }
-    }
+    wave_argmax(bv, bi);
     if (lane == 0) out[row] = bi < 0 ? 0 : bi;
 }
 
@@ -647,32 +671,52 @@ int rmsnorm_bwd_parts(int rows, int cols)
     return rmsnorm_bwd_blocks(rows) * kWavesPerBlock;
 }
 
-int rmsnorm_bwd(const float* x, const float* w, const float* inv, const float* dy, float* dx, float* dw,
-                int rows, int cols, int accumulate, float* work, size_t work_floats, hipStream_t s)
+int rmsnorm_bwd_rows(const float* x, const float* w, const float* inv, const float* dy, float* dx,
+                     const float* dres, float* partial, size_t partial_floats, int rows, int cols, int* parts_out,
+                     hipStream_t s)
 {
     if (rows < 0 || cols <= 0) return fail(LHIP_E_SHAPE, "rmsnorm_bwd: rows=%d cols=%d", rows, cols);
+    if (parts_out) *parts_out = 0;
     if (rows == 0) return LHIP_OK;
     if (!x || !w || !inv || !dy || !dx) return fail(LHIP_E_NULL, "rmsnorm_bwd: NULL argument");
     const int blocks = rmsnorm_bwd_blocks(rows);
     const int nv = nv_for(cols);
-    const bool vec = nv && cols % 4 == 0 && aligned16(x) && aligned16(w) && aligned16(dy) && aligned16(dx);
+    const bool vec = nv && cols % 4 == 0 && aligned16(x) && aligned16(w) && aligned16(dy) && aligned16(dx) &&
+                     (!dres || aligned16(dres));
     const int parts = vec ? blocks : blocks * kWavesPerBlock;
-    if (dw && static_cast<size_t>(parts) * cols > work_floats)
-        return fail(LHIP_E_CAPACITY, "rmsnorm_bwd: workspace of %zu floats < %lld needed", work_floats,
+    if (partial && static_cast<size_t>(parts) * cols > partial_floats)
+        return fail(LHIP_E_CAPACITY, "rmsnorm_bwd: workspace of %zu floats < %lld needed", partial_floats,
                     static_cast<long long>(parts) * cols);
-    float* partial = work;
     dim3 g(blocks), b(kRowThreads);
     const size_t lds = static_cast<size_t>(kWavesPerBlock) * cols * sizeof(float);
-    if (!vec) rmsnorm_bwd_generic<<<g, b, 0, s>>>(x, w, inv, dy, dx, partial, rows, cols, accumulate);
-    else if (nv == 1) rmsnorm_bwd_vec<1><<<g, b, lds, s>>>(x, w, inv, dy, dx, partial, rows, cols, accumulate);
-    else if (nv == 2) rmsnorm_bwd_vec<2><<<g, b, lds, s>>>(x, w, inv, dy, dx, partial, rows, cols, accumulate);
-    else if (nv == 4) rmsnorm_bwd_vec<4><<<g, b, lds, s>>>(x, w, inv, dy, dx, partial, rows, cols, accumulate);
-    else if (nv == 8) rmsnorm_bwd_vec<8><<<g, b, lds, s>>>(x, w, inv, dy, dx, partial, rows, cols, accumulate);
-    else rmsnorm_bwd_vec<16><<<g, b, lds, s>>>(x, w, inv, dy, dx, partial, rows, cols, accumulate);
-    int rc = check_launch("rmsnorm_bwd");
-    if (rc != LHIP_OK || !dw) return rc;
+#define LHIP_RBV(NV_) rmsnorm_bwd_vec<NV_><<<g, b, lds, s>>>(x, w, inv, dy, dx, dres, partial, rows, cols)
+    if (!vec) rmsnorm_bwd_generic<<<g, b, 0, s>>>(x, w, inv, dy, dx, dres, partial, rows, cols);
+    else if (nv == 1) LHIP_RBV(1);
+    else if (nv == 2) LHIP_RBV(2);
+    else if (nv == 4) LHIP_RBV(4);
+    else if (nv == 8) LHIP_RBV(8);
+    else LHIP_RBV(16);
+#undef LHIP_RBV
+    if (parts_out) *parts_out = parts;
+    return check_launch("rmsnorm_bwd");
+}
+
+int rmsnorm_bwd_colsum(const float* partial, int parts, float* dw, int cols, int accumulate, hipStream_t s)
+{
+    if (parts <= 0) return LHIP_OK;
     colsum_kernel<<<ceil_div(cols, 64), 256, 0, s>>>(partial, dw, parts, cols, accumulate);
     return check_launch("rmsnorm_bwd: dw reduce");
+}
+
+int rmsnorm_bwd(const float* x, const float* w, const float* inv, const float* dy, float* dx, float* dw,
+                int rows, int cols, int accumulate, float* work, size_t work_floats, hipStream_t s)
+{
+    if (dw && !work) return fail(LHIP_E_NULL, "rmsnorm_bwd: no workspace for dw");
+    int parts = 0;
+    int rc = rmsnorm_bwd_rows(x, w, inv, dy, dx, accumulate ? dx : nullptr, dw ? work : nullptr, work_floats,
+                              rows, cols, &parts, s);
+    if (rc != LHIP_OK || !dw) return rc;
+    return rmsnorm_bwd_colsum(work, parts, dw, cols, accumulate, s);
 }
 
 int softmax_fwd(const float* x, float* y, int rows, int cols, float scale, int causal, int offset, int group,
@@ -718,7 +762,7 @@ int softmax_bwd(const float* y, const float* dy, float* dx, int rows, int cols, 
 }
 
 int ce_fused(const float* logits, const int* tgt, float* losses, float* dlogits, int rows, int V,
-             int ignore_index, float gscale, hipStream_t s)
+             int ignore_index, float gscale, hipStream_t s, int* amax)
 {
     if (rows < 0 || V <= 0) return fail(LHIP_E_SHAPE, "ce_fused: rows=%d vocab=%d", rows, V);
     if (rows == 0) return LHIP_OK;
@@ -728,13 +772,13 @@ int ce_fused(const float* logits, const int* tgt, float* losses, float* dlogits,
     // rows walked block-stride: about 2 rows per workgroup once rows exceed the CUs
     const int nb_small = rows < 4 * cus ? rows : 4 * cus;
     if (vec && V <= 256 * 4 * 2)
-        ce_fused_vec<256, 2, true><<<nb_small, 256, 0, s>>>(logits, tgt, losses, dlogits, rows, V, ignore_index, gscale);
+        ce_fused_vec<256, 2, true><<<nb_small, 256, 0, s>>>(logits, tgt, losses, dlogits, amax, rows, V, ignore_index, gscale);
     else if (vec && V <= 256 * 4 * 8)
-        ce_fused_vec<256, 8, true><<<nb_small, 256, 0, s>>>(logits, tgt, losses, dlogits, rows, V, ignore_index, gscale);
+        ce_fused_vec<256, 8, true><<<nb_small, 256, 0, s>>>(logits, tgt, losses, dlogits, amax, rows, V, ignore_index, gscale);
     else if (vec && V <= 1024 * 4 * 8)
-        ce_fused_vec<1024, 8, false><<<rows, 1024, 0, s>>>(logits, tgt, losses, dlogits, rows, V, ignore_index, gscale);
+        ce_fused_vec<1024, 8, false><<<rows, 1024, 0, s>>>(logits, tgt, losses, dlogits, amax, rows, V, ignore_index, gscale);
     else
-        ce_fused_generic<<<rows, 256, 0, s>>>(logits, tgt, losses, dlogits, rows, V, ignore_index, gscale);
+        ce_fused_generic<<<rows, 256, 0, s>>>(logits, tgt, losses, dlogits, amax, rows, V, ignore_index, gscale);
     return check_launch("ce_fused");
 }
 

@@ -251,7 +251,7 @@ def test_gemm_c3_lm_head_shapes(ta, tb):
     assert rel_fro(got, ref) <= TOL
 
 
-@pytest.mark.parametrize("m,n,k,batch", [(512, 128, 2000, 1), (128, 128, 4096, 3), (64, 64, 1000, 2),
+@pytest.mark.parametrize("m,n,k,batch", [(512, 128, 2000, 1), (128, 128, 4096, 3), (64, 64, 1000, 2), (96, 64, 1100, 2),
                                          (33, 70, 999, 1), (1, 4096, 4096, 1)])
 def test_gemm_split_k_alpha_beta_batched(m, n, k, batch):
     """Shapes with fewer output tiles than CUs and long K take the split-K path;

@@ -55,6 +55,10 @@ def test_rmsnorm_fwd_bwd(rows, cols, eps):
     call("lhip_rmsnorm_bwd", X.ptr, W.ptr, INV.ptr, G.ptr, DX.ptr, DW.ptr, rows, cols, 1)
     assert rel_fro(dl(DX), 2 * dx_ref) <= EW
     assert rel_fro(dl(DW), 2 * dw_ref) <= EW
+    # dw = NULL: dx only (no partials are written)
+    DX2 = device.Buffer((rows, cols))
+    call("lhip_rmsnorm_bwd", X.ptr, W.ptr, INV.ptr, G.ptr, DX2.ptr, None, rows, cols, 0)
+    assert rel_fro(dl(DX2), dx_ref) <= EW
 
 
 def test_rmsnorm_bwd_finite_differences_of_gpu_forward():
