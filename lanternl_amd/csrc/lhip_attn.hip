@@ -8,18 +8,22 @@
 // Backward (tensor2.lua BACKWARD.* in reverse order):
 //   dP = dO . v^T, dv = P^T . dO, dS = scale * P o (dP - rowsum(dP o P)),
 //   dqr = dS . kr, dkr = dS^T . qr, dq, dk = inverse RoPE of dqr, dkr.
-// One workgroup (4 wave64s) per (window, head) keeps q, k, v, S/P and the
+// One workgroup (4 wave64s) per (window, head) keeps q, k, v, P and the
 // gradients of the head in LDS, so each direction is one launch instead of
 // five or six (RoPE, scores GEMM, softmax, PV GEMM / dP and dv GEMMs, softmax
-// backward, dq and dk GEMMs, RoPE backward).  Every product runs on
-// v_mfma_f32_16x16x4f32: 16x16 output blocks are dealt round-robin to the
-// four waves; lane l supplies A[i0 + l%16][k0 + l/16] and B[k0 + l/16][j0 +
-// l%16] read from LDS (odd row strides keep those column reads conflict-free)
-// and receives D[i0 + 4*(l/16) + r][j0 + l%16] in accumulator r.  Operands
-// are zero-padded in LDS to whole 16-blocks so padded lanes contribute 0.
-// The inverse RoPE on dqr/dkr pairs columns (2p, 2p+1), which sit in
-// neighbouring lanes of the MFMA result: one __shfl_xor(v, 1) brings the
-// partner in.
+// backward, dq and dk GEMMs, RoPE backward).  Wave w owns the 16 query rows
+// 16w .. 16w+15 (and, backward, the 16 key rows of the same block), so row
+// work needs no workgroup barrier.  Every product runs on
+// v_mfma_f32_16x16x4f32: lane l supplies A[i0 + l%16][k0 + l/16] and
+// B[k0 + l/16][j0 + l%16] from LDS copies stored k-contiguous (row stride
+// 68 = 4 mod 64 banks, so these reads are conflict-free) and receives
+// D[i0 + 4*(l/16) + e][j0 + l%16] in accumulator e.  A row of a 16x16 block
+// therefore lies in one 16-lane DPP row: the softmax and its backward reduce
+// the accumulators in place with DPP (no LDS round trip).  Causal blocks above
+// the diagonal are skipped.  Operands are zero-padded in LDS to whole
+// 16-blocks so padded lanes contribute 0.  The inverse RoPE on dqr/dkr pairs
+// columns (2p, 2p+1), which sit in neighbouring lanes of the MFMA result: one
+// DPP quad permute brings the partner in.
 //
 // Layouts: qkv[3][N][D] with N = B*T rows (window b's rows b*T .. b*T+T-1) and
 // head h in columns h*hd .. h*hd+hd-1; P[B][H][T][T]; rope table cs[T][hd/2]
@@ -34,9 +38,10 @@ namespace {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-constexpr int kAttnThreads = 256;
-constexpr int kMax = 64;          // T and head_dim limits of the fused path
-constexpr int kLd = kMax + 1;     // LDS row stride (odd: conflict-free column reads)
+constexpr int kAttnThreads = 256;  // four waves; wave w owns query (and key) rows 16w .. 16w+15
+constexpr int kMax = 64;           // T and head_dim limits of the fused path
+constexpr int kLd = kMax + 4;      // LDS row stride: 68 = 4 (mod 64 banks), so the operand
+                                   // reads X[(base + l%16) * kLd + k0 + l/16] hit 64 banks
 
 struct AttnArgs {
     const float* qkv;     // [3][N][D]
@@ -53,21 +58,43 @@ struct AttnArgs {
 __device__ __forceinline__ int round16(int x) { return (x + 15) & ~15; }
 __device__ __forceinline__ int attn_lim(int i, int T, int causal) { return causal ? (i + 1 < T ? i + 1 : T) : T; }
 
-// Load this head's q and k rotated (forward RoPE) and v into LDS [64][kLd],
-// zero outside [T][hd].  Each thread first issues all of its global loads
-// (fully unrolled, float2 pairs), then rotates and stores, so the loads of a
-// thread are in flight together instead of one round trip per pair.
-__device__ __forceinline__ void load_head(const AttnArgs& a, int b, int h, float* qs, float* ks, float* vs)
+// 16x16 block sum_{k0 <= k < k1} A(i0 + l%16, k) B(k, j0 + l%16) for NB blocks
+// side by side (independent accumulator chains); lane l reads
+// A(i0 + l%16, k0 + l/16) = a[(i0 + l%16) * kLd + k] and the B element
+// b_j[(j0 + l%16) * kLd + k] of block j (both operands stored k-contiguous).
+template <int NB>
+__device__ __forceinline__ void mfma_rows(floatx4 (&acc)[NB], const float* a, int i0, const float* b, int j0,
+                                          int jstep, int nb, int k0, int k1)
+{
+    const int lane = threadIdx.x & 63, r = lane & 15, q = lane >> 4;
+#pragma unroll
+    for (int j = 0; j < NB; ++j) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int k = k0; k < k1; k += 4) {
+        const float av = a[(i0 + r) * kLd + k + q];
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+            if (j < nb) acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, b[(j0 + j * jstep + r) * kLd + k + q], acc[j], 0, 0, 0);
+    }
+}
+
+// Load this head's q and k rotated by the forward RoPE and v into LDS, zero on
+// [T16, hd16) padding: row-major (rm, [t][d]) and/or transposed (tr, [d][t])
+// copies as the caller asks (NULL = not wanted).  Each thread issues all of
+// its global loads before any LDS store.
+__device__ __forceinline__ void load_qkv(const AttnArgs& a, int b, int h, float* q_rm, float* q_tr, float* k_rm,
+                                         float* k_tr, float* v_rm, float* v_tr)
 {
     constexpr int U = kMax * (kMax / 2) / kAttnThreads;   // pair slots per thread
     const int T = a.T, hd = a.hd, D = a.D, pairs = hd >> 1;
+    const int T16 = round16(T), p16 = round16(hd) >> 1;
     const long long ND = static_cast<long long>(a.N) * D;
     float2 qv[U], kv[U], vv[U], cv[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const int idx = threadIdx.x + kAttnThreads * u;
-        const int t = idx / (kMax / 2), p = idx - t * (kMax / 2);
-        qv[u] = kv[u] = vv[u] = cv[u] = make_float2(0.f, 0.f);
+        const int t = idx / p16, p = idx - t * p16;
+        qv[u] = kv[u] = vv[u] = make_float2(0.f, 0.f);
+        cv[u] = make_float2(1.f, 0.f);
         if (t < T && p < pairs) {
             const long long off = static_cast<long long>(b * T + t) * D + h * hd + 2 * p;
             qv[u] = *reinterpret_cast<const float2*>(a.qkv + off);
@@ -79,108 +106,161 @@ __device__ __forceinline__ void load_head(const AttnArgs& a, int b, int h, float
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const int idx = threadIdx.x + kAttnThreads * u;
-        const int t = idx / (kMax / 2), p = idx - t * (kMax / 2);
-        const float2 c = cv[u];
-        qs[t * kLd + 2 * p] = qv[u].x * c.x - qv[u].y * c.y;
-        qs[t * kLd + 2 * p + 1] = qv[u].x * c.y + qv[u].y * c.x;
-        ks[t * kLd + 2 * p] = kv[u].x * c.x - kv[u].y * c.y;
-        ks[t * kLd + 2 * p + 1] = kv[u].x * c.y + kv[u].y * c.x;
-        vs[t * kLd + 2 * p] = vv[u].x;
-        vs[t * kLd + 2 * p + 1] = vv[u].y;
+        const int t = idx / p16, p = idx - t * p16;
+        if (t < T16) {
+            const float2 c = cv[u];
+            const int d = 2 * p;
+            const float q0 = qv[u].x * c.x - qv[u].y * c.y, q1 = qv[u].x * c.y + qv[u].y * c.x;
+            const float k0 = kv[u].x * c.x - kv[u].y * c.y, k1 = kv[u].x * c.y + kv[u].y * c.x;
+            if (q_rm) { q_rm[t * kLd + d] = q0; q_rm[t * kLd + d + 1] = q1; }
+            if (q_tr) { q_tr[d * kLd + t] = q0; q_tr[(d + 1) * kLd + t] = q1; }
+            if (k_rm) { k_rm[t * kLd + d] = k0; k_rm[t * kLd + d + 1] = k1; }
+            if (k_tr) { k_tr[d * kLd + t] = k0; k_tr[(d + 1) * kLd + t] = k1; }
+            if (v_rm) { v_rm[t * kLd + d] = vv[u].x; v_rm[t * kLd + d + 1] = vv[u].y; }
+            if (v_tr) { v_tr[d * kLd + t] = vv[u].x; v_tr[(d + 1) * kLd + t] = vv[u].y; }
+        }
     }
 }
 
-// One 16x16 output block of sum_k A(i, k) B(k, j), k < K4 (K4 % 4 == 0, zero padded).
-template <class FA, class FB>
-__device__ __forceinline__ floatx4 mfma_block(int i0, int j0, int K4, FA fa, FB fb)
-{
-    const int lane = threadIdx.x & 63, r = lane & 15, q = lane >> 4;
-    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int k0 = 0; k0 < K4; k0 += 4)
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(fa(i0 + r, k0 + q), fb(k0 + q, j0 + r), acc, 0, 0, 0);
-    return acc;
-}
-
+// Forward.  Wave w: S = scale * qr kr^T for its 16 query rows against the key
+// blocks it can see (all, or blocks 0..w when causal), the row softmax in the
+// MFMA accumulators (each row's 16 columns of a block sit in one 16-lane DPP
+// row), P to global and to LDS, then ctx = P v.
 __global__ void __launch_bounds__(kAttnThreads) attn_fwd_kernel(const AttnArgs a)
 {
-    __shared__ float qs[kMax * kLd];
-    __shared__ float ks[kMax * kLd];
-    __shared__ float vs[kMax * kLd];
-    __shared__ float S[kMax * kLd];
+    __shared__ float qs[kMax * kLd];   // [t][d] rotated q
+    __shared__ float ks[kMax * kLd];   // [t][d] rotated k
+    __shared__ float vT[kMax * kLd];   // [d][t]
+    __shared__ float Ps[kMax * kLd];   // [i][j]
     const int b = blockIdx.x / a.H, h = blockIdx.x - b * a.H;
     const int T = a.T, hd = a.hd;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int T16 = round16(T), hd16 = round16(hd), hd4 = (hd + 3) & ~3, T4 = (T + 3) & ~3;
-    load_head(a, b, h, qs, ks, vs);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r = lane & 15, q = lane >> 4;
+    const int nbt = round16(T) >> 4, nbd = round16(hd) >> 4, hd4 = (hd + 3) & ~3, T4 = (T + 3) & ~3;
+    load_qkv(a, b, h, qs, nullptr, ks, nullptr, nullptr, vT);
     __syncthreads();
-    // S = scale * qr . kr^T on the kept prefix, -inf beyond (never read)
-    {
-        const int nbj = T16 / 16, nblk = nbj * nbj;
-        for (int blk = wave; blk < nblk; blk += 4) {
-            const int i0 = (blk / nbj) * 16, j0 = (blk % nbj) * 16;
-            const floatx4 acc = mfma_block(i0, j0, hd4, [&](int i, int k) { return qs[i * kLd + k]; },
-                                           [&](int k, int j) { return ks[j * kLd + k]; });
-            const int j = j0 + (lane & 15);
+    const int i0 = 16 * wave;
+    const bool active = i0 < T;
+    const int nj = a.causal ? min(wave + 1, nbt) : nbt;   // key blocks this wave sees
+    float* Pg = a.P + (static_cast<long long>(b) * a.H + h) * T * T;
+    if (active) {
+        // S(i, j) = sum_d q(i, d) k(j, d)
+        floatx4 S[4];
+        mfma_rows<4>(S, qs, i0, ks, 0, 16, nj, 0, hd4);
+        float mx[4], sum[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int i = i0 + 4 * (lane >> 4) + r;
-                S[i * kLd + j] = acc[r] * a.scale;
+        for (int e = 0; e < 4; ++e) {
+            const int i = i0 + 4 * q + e, lim = attn_lim(i, T, a.causal);
+            float m = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float v = (j < nj && 16 * j + r < lim) ? S[j][e] * a.scale : -INFINITY;
+                S[j][e] = v;
+                m = fmaxf(m, v);
+            }
+            m = row16_max(m);
+            mx[e] = (m == -INFINITY || m != m) ? 0.f : m;
+            float sm = 0.f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float ev = (j < nj && 16 * j + r < lim) ? expf(S[j][e] - mx[e]) : 0.f;
+                S[j][e] = ev;
+                sm += ev;
+            }
+            sm = row16_sum(sm);
+            sum[e] = sm > 0.f ? 1.0f / sm : 1.0f;
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int i = i0 + 4 * q + e;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int c = 16 * j + r;
+                const float p = S[j][e] * sum[e];
+                if (j < nj) Ps[i * kLd + c] = p;
+                if (i < T && c < T && j < nbt) Pg[i * T + c] = j < nj ? p : 0.f;
             }
         }
     }
     __syncthreads();
-    // row softmax: one wave per row, one lane per column (T <= 64)
-    float* Pg = a.P + (static_cast<long long>(b) * a.H + h) * T * T;
-    for (int i = wave; i < T; i += 4) {
-        const int lim = attn_lim(i, T, a.causal);
-        const float v = lane < lim ? S[i * kLd + lane] : -INFINITY;
-        float mx = wave_max(v);
-        if (mx == -INFINITY || mx != mx) mx = 0.f;
-        const float e = lane < lim ? expf(v - mx) : 0.f;
-        float sum = wave_sum(e);
-        if (!(sum > 0.f)) sum = 1.f;
-        const float p = e * (1.0f / sum);
-        S[i * kLd + lane] = p;                // zero beyond the kept prefix (and past T)
-        if (lane < T) Pg[i * T + lane] = p;
-    }
-    for (int i = T + wave; i < T4; i += 4) S[i * kLd + lane] = 0.f;
-    __syncthreads();
-    // ctx_h = P . v
-    {
-        const int nbi = T16 / 16, nbj = hd16 / 16, nblk = nbi * nbj;
-        for (int blk = wave; blk < nblk; blk += 4) {
-            const int i0 = (blk / nbj) * 16, j0 = (blk % nbj) * 16;
-            const floatx4 acc = mfma_block(i0, j0, T4, [&](int i, int k) { return S[i * kLd + k]; },
-                                           [&](int k, int j) { return vs[k * kLd + j]; });
-            const int d = j0 + (lane & 15);
-            if (d < hd) {
+    if (active) {
+        // ctx(i, d) = sum_j P(i, j) v(j, d), j below the causal edge of this block
+        const int kend = min(T4, 16 * nj);
+        floatx4 O[4];
+        mfma_rows<4>(O, Ps, i0, vT, 0, 16, nbd, 0, kend);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int i = i0 + 4 * (lane >> 4) + r;
-                    if (i < T) a.ctx[static_cast<long long>(b * T + i) * a.D + h * hd + d] = acc[r];
+        for (int db = 0; db < 4; ++db) {
+            const int d = 16 * db + r;
+            if (db < nbd && d < hd) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int i = i0 + 4 * q + e;
+                    if (i < T) a.ctx[static_cast<long long>(b * T + i) * a.D + h * hd + d] = O[db][e];
                 }
             }
         }
     }
 }
 
+// Inverse RoPE of a 16x16 result block in MFMA layout (rows t0 + 4q + e,
+// columns d0 + l%16) and its store: the pair partner of column d is column
+// d ^ 1, held by lane l ^ 1 (DPP quad_perm [1,0,3,2]).
+__device__ __forceinline__ void store_unrotated(const AttnArgs& a, float* dst, const floatx4& acc, int b, int h,
+                                                int t0, int d0)
+{
+    const int lane = threadIdx.x & 63, r = lane & 15, q = lane >> 4;
+    const int d = d0 + r, pairs = a.hd >> 1;
+    const bool odd = d & 1;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float mine = acc[e];
+        const float other = dpp_f<0xB1>(mine);
+        const int t = t0 + 4 * q + e;
+        if (t < a.T && d < a.hd) {
+            const float2 c = a.cs[t * pairs + (d >> 1)];
+            const float g0 = odd ? other : mine, g1 = odd ? mine : other;
+            dst[static_cast<long long>(b * a.T + t) * a.D + h * a.hd + d] =
+                odd ? (-g0 * c.y + g1 * c.x) : (g0 * c.x + g1 * c.y);
+        }
+    }
+}
+
+// Backward.  Wave w owns query rows 16w.. (dP, dS, dq) and key rows 16w..
+// (dv, dk).  Phase 1: dP = dO v^T and dS = scale P o (dP - rowsum(dP o P)) in
+// the accumulators (P read from global in the same layout), dS to LDS in both
+// orientations, dv = P^T dO.  Phase 2 (after a barrier, all of dS present):
+// dq = dS kr, dk = dS^T qr, each through the inverse RoPE.
 __global__ void __launch_bounds__(kAttnThreads) attn_bwd_kernel(const AttnArgs a)
 {
-    __shared__ float qs[kMax * kLd];
-    __shared__ float ks[kMax * kLd];
-    __shared__ float vs[kMax * kLd];
-    __shared__ float dO[kMax * kLd];
-    __shared__ float Ps[kMax * kLd];
-    __shared__ float dS[kMax * kLd];
+    __shared__ float qT[kMax * kLd];    // [d][t] rotated q
+    __shared__ float kT[kMax * kLd];    // [d][t] rotated k
+    __shared__ float vs[kMax * kLd];    // [t][d]
+    __shared__ float dOs[kMax * kLd];   // [t][d]
+    __shared__ float dOT[kMax * kLd];   // [d][t]
+    __shared__ float PT[kMax * kLd];    // [j][i]
+    __shared__ float dSs[kMax * kLd];   // [i][j]
+    __shared__ float dST[kMax * kLd];   // [j][i]
     const int b = blockIdx.x / a.H, h = blockIdx.x - b * a.H;
-    const int T = a.T, hd = a.hd, D = a.D, pairs = hd >> 1;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int T16 = round16(T), hd16 = round16(hd), hd4 = (hd + 3) & ~3, T4 = (T + 3) & ~3;
+    const int T = a.T, hd = a.hd, D = a.D;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r = lane & 15, q = lane >> 4;
+    const int T16 = round16(T), hd16 = round16(hd);
+    const int nbt = T16 >> 4, nbd = hd16 >> 4, hd4 = (hd + 3) & ~3, T4 = (T + 3) & ~3;
     const long long ND = static_cast<long long>(a.N) * D;
-    load_head(a, b, h, qs, ks, vs);
+    const int i0 = 16 * wave;
+    const bool active = i0 < T;
+    const int nj = a.causal ? min(wave + 1, nbt) : nbt;
     const float* Pg = a.P + (static_cast<long long>(b) * a.H + h) * T * T;
+    // this wave's P rows in accumulator layout, loaded with everything else
+    float Pd[4][4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int i = i0 + 4 * q + e, c = 16 * j + r;
+            Pd[j][e] = (active && j < nj && i < T && c < T) ? Pg[i * T + c] : 0.f;
+        }
+    load_qkv(a, b, h, nullptr, qT, nullptr, kT, vs, nullptr);
     {
-        // all of this thread's P and dO loads first, then the LDS stores
+        // P^T, dO and dO^T over [T16) x [T16) / [T16) x [hd16), zero padded
         constexpr int U = kMax * kMax / kAttnThreads;
         float pv[U], ov[U];
 #pragma unroll
@@ -194,81 +274,60 @@ __global__ void __launch_bounds__(kAttnThreads) attn_bwd_kernel(const AttnArgs a
         for (int u = 0; u < U; ++u) {
             const int idx = threadIdx.x + kAttnThreads * u;
             const int i = idx / kMax, j = idx - i * kMax;
-            Ps[i * kLd + j] = pv[u];
-            dO[i * kLd + j] = ov[u];
+            if (i < T16 && j < T16) PT[j * kLd + i] = pv[u];
+            if (i < T16 && j < hd16) { dOs[i * kLd + j] = ov[u]; dOT[j * kLd + i] = ov[u]; }
         }
     }
     __syncthreads();
-    // dP = dO . v^T (T x T, into dS); dv = P^T . dO (T x hd, to global)
-    {
-        const int nbt = T16 / 16, nbd = hd16 / 16;
-        const int n1 = nbt * nbt, n2 = nbt * nbd;
-        for (int blk = wave; blk < n1 + n2; blk += 4) {
-            if (blk < n1) {
-                const int i0 = (blk / nbt) * 16, j0 = (blk % nbt) * 16;
-                const floatx4 acc = mfma_block(i0, j0, hd4, [&](int i, int k) { return dO[i * kLd + k]; },
-                                               [&](int k, int j) { return vs[j * kLd + k]; });
-                const int j = j0 + (lane & 15);
+    if (active) {
+        // dP(i, j) = sum_d dO(i, d) v(j, d)
+        floatx4 G[4];
+        mfma_rows<4>(G, dOs, i0, vs, 0, 16, nj, 0, hd4);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) dS[(i0 + 4 * (lane >> 4) + r) * kLd + j] = acc[r];
-            } else {
-                const int bb = blk - n1;
-                const int i0 = (bb / nbd) * 16, j0 = (bb % nbd) * 16;   // i: key row j, j: d
-                const floatx4 acc = mfma_block(i0, j0, T4, [&](int i, int k) { return Ps[k * kLd + i]; },
-                                               [&](int k, int j) { return dO[k * kLd + j]; });
-                const int d = j0 + (lane & 15);
-                if (d < hd) {
+        for (int e = 0; e < 4; ++e) {
+            float dot = 0.f;
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const int t = i0 + 4 * (lane >> 4) + r;
-                        if (t < T) a.dqkv[2 * ND + static_cast<long long>(b * T + t) * D + h * hd + d] = acc[r];
-                    }
+            for (int j = 0; j < 4; ++j) dot += (j < nj) ? G[j][e] * Pd[j][e] : 0.f;
+            dot = row16_sum(dot);
+            const int i = i0 + 4 * q + e;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (j < nj) {
+                    const float ds = a.scale * (Pd[j][e] * (G[j][e] - dot));
+                    dSs[i * kLd + 16 * j + r] = ds;
+                    dST[(16 * j + r) * kLd + i] = ds;
+                }
+            }
+        }
+        // dv(j, d) = sum_i P(i, j) dO(i, d) over query rows i >= 16w (causal) for keys j in block w
+        const int kbeg = a.causal ? i0 : 0;
+        floatx4 V[4];
+        mfma_rows<4>(V, PT, i0, dOT, 0, 16, nbd, kbeg, T4);
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+            const int d = 16 * db + r;
+            if (db < nbd && d < hd) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int t = i0 + 4 * q + e;
+                    if (t < T) a.dqkv[2 * ND + static_cast<long long>(b * T + t) * D + h * hd + d] = V[db][e];
                 }
             }
         }
     }
     __syncthreads();
-    // dS = scale * P o (dP - sum_{j<lim} dP P); zero beyond the kept prefix and past T
-    for (int i = wave; i < kMax; i += 4) {
-        if (i < T) {
-            const int lim = attn_lim(i, T, a.causal);
-            const float p = lane < lim ? Ps[i * kLd + lane] : 0.f;
-            const float g = lane < lim ? dS[i * kLd + lane] : 0.f;
-            const float dot = wave_sum(g * p);
-            dS[i * kLd + lane] = lane < lim ? a.scale * (p * (g - dot)) : 0.f;
-        } else {
-            dS[i * kLd + lane] = 0.f;
-        }
-    }
-    __syncthreads();
-    // dqr = dS . kr, dkr = dS^T . qr, then the inverse rotation of each pair
-    {
-        const int nbt = T16 / 16, nbd = hd16 / 16, n = nbt * nbd;
-        for (int blk = wave; blk < 2 * n; blk += 4) {
-            const bool isq = blk < n;
-            const int bb = isq ? blk : blk - n;
-            const int i0 = (bb / nbd) * 16, j0 = (bb % nbd) * 16;
-            floatx4 acc;
-            if (isq)
-                acc = mfma_block(i0, j0, T4, [&](int i, int k) { return dS[i * kLd + k]; },
-                                 [&](int k, int j) { return ks[k * kLd + j]; });
-            else
-                acc = mfma_block(i0, j0, T4, [&](int i, int k) { return dS[k * kLd + i]; },
-                                 [&](int k, int j) { return qs[k * kLd + j]; });
-            const int d = j0 + (lane & 15);
-            const bool odd = d & 1;
-            float* dst = a.dqkv + (isq ? 0 : ND);
+    if (active) {
+        // dqr(i, d) = sum_j dS(i, j) kr(j, d) ; dkr(j, d) = sum_i dS(i, j) qr(i, d)
+        const int kend = min(T4, 16 * nj);
+        const int kbeg = a.causal ? i0 : 0;
+        floatx4 Q[4], K[4];
+        mfma_rows<4>(Q, dSs, i0, kT, 0, 16, nbd, 0, kend);
+        mfma_rows<4>(K, dST, i0, qT, 0, 16, nbd, kbeg, T4);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int t = i0 + 4 * (lane >> 4) + r;
-                const float mine = acc[r];
-                const float other = __shfl_xor(mine, 1, 64);   // column d ^ 1 of the same row
-                if (t < T && d < hd) {
-                    const float2 c = a.cs[t * pairs + (d >> 1)];
-                    const float g0 = odd ? other : mine, g1 = odd ? mine : other;
-                    dst[static_cast<long long>(b * T + t) * D + h * hd + d] =
-                        odd ? (-g0 * c.y + g1 * c.x) : (g0 * c.x + g1 * c.y);
-                }
+        for (int db = 0; db < 4; ++db) {
+            if (db < nbd) {
+                store_unrotated(a, a.dqkv, Q[db], b, h, i0, 16 * db);
+                store_unrotated(a, a.dqkv + ND, K[db], b, h, i0, 16 * db);
             }
         }
     }

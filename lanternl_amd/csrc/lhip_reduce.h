@@ -5,26 +5,99 @@
 
 namespace lhip {
 
-__device__ __forceinline__ float wave_sum(float v)
+// Cross-lane moves inside a 16-lane row use DPP (a VALU operand modifier, a
+// few cycles) instead of __shfl_xor, which is an LDS permute with an LDS round
+// trip per step.  The four row results of a wave are combined with
+// v_readlane, which leaves the value wave-uniform.
+//   0xB1  quad_perm [1,0,3,2]: lane i <- i^1
+//   0x4E  quad_perm [2,3,0,1]: lane i <- i^2
+//   0x141 row_half_mirror:     lane i <- 7-i within each 8 lanes
+//   0x140 row_mirror:          lane i <- 15-i within each 16 lanes
+// After the two quad steps every lane holds its quad's value; the half
+// mirror pairs the two quads of each 8 lanes, the mirror the two halves of
+// each 16, so four steps reduce a row and leave the result in all 16 lanes
+// (each step combines a lane with its partner in both orders; + and max are
+// commutative, so the 16 lanes agree bit for bit).
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v)
 {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, true);
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v)
+{
+    return __builtin_bit_cast(float, dpp_i<CTRL>(__builtin_bit_cast(int, v)));
+}
+
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double v)
+{
+    const long long b = __builtin_bit_cast(long long, v);
+    const int lo = dpp_i<CTRL>(static_cast<int>(b));
+    const int hi = dpp_i<CTRL>(static_cast<int>(b >> 32));
+    return __builtin_bit_cast(double, (static_cast<long long>(hi) << 32) | static_cast<unsigned int>(lo));
+}
+
+__device__ __forceinline__ float lane_f(float v, int l)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+
+__device__ __forceinline__ double lane_d(double v, int l)
+{
+    const long long b = __builtin_bit_cast(long long, v);
+    const int lo = __builtin_amdgcn_readlane(static_cast<int>(b), l);
+    const int hi = __builtin_amdgcn_readlane(static_cast<int>(b >> 32), l);
+    return __builtin_bit_cast(double, (static_cast<long long>(hi) << 32) | static_cast<unsigned int>(lo));
+}
+
+// sum / max over each 16-lane row, result in every lane of the row
+__device__ __forceinline__ float row16_sum(float v)
+{
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    v += dpp_f<0x141>(v);
+    v += dpp_f<0x140>(v);
     return v;
 }
 
-__device__ __forceinline__ double wave_sum(double v)
+__device__ __forceinline__ double row16_sum(double v)
 {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    v += dpp_d<0xB1>(v);
+    v += dpp_d<0x4E>(v);
+    v += dpp_d<0x141>(v);
+    v += dpp_d<0x140>(v);
     return v;
 }
 
 // fmaxf ignores a NaN operand, like the Lua `if v > mx` scan.
+__device__ __forceinline__ float row16_max(float v)
+{
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x141>(v));
+    v = fmaxf(v, dpp_f<0x140>(v));
+    return v;
+}
+
+// Whole-wave reductions (every lane active); the result is wave-uniform.
+__device__ __forceinline__ float wave_sum(float v)
+{
+    v = row16_sum(v);
+    return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
+}
+
+__device__ __forceinline__ double wave_sum(double v)
+{
+    v = row16_sum(v);
+    return (lane_d(v, 0) + lane_d(v, 16)) + (lane_d(v, 32) + lane_d(v, 48));
+}
+
 __device__ __forceinline__ float wave_max(float v)
 {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
+    v = row16_max(v);
+    return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
 }
 
 // Workgroup reductions for NW waves; `red` is LDS scratch of >= NW floats.
@@ -66,14 +139,29 @@ __device__ __forceinline__ void argmax_merge(float& bv, int& bi, float ov, int o
     if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) { bv = ov; bi = oi; }
 }
 
+template <int CTRL>
+__device__ __forceinline__ void argmax_step(float& bv, int& bi)
+{
+    const float ov = dpp_f<CTRL>(bv);
+    const int oi = dpp_i<CTRL>(bi);
+    argmax_merge(bv, bi, ov, oi);
+}
+
+// Whole-wave argmax (every lane active); the result is wave-uniform.  The
+// merge is a total order (valid beats none, larger value, then lower index),
+// so the reduction order does not change the result.
 __device__ __forceinline__ void wave_argmax(float& bv, int& bi)
 {
+    argmax_step<0xB1>(bv, bi);
+    argmax_step<0x4E>(bv, bi);
+    argmax_step<0x141>(bv, bi);
+    argmax_step<0x140>(bv, bi);
+    float v = lane_f(bv, 0);
+    int i = __builtin_amdgcn_readlane(bi, 0);
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(bv, o, 64);
-        const int oi = __shfl_xor(bi, o, 64);
-        argmax_merge(bv, bi, ov, oi);
-    }
+    for (int r = 16; r < 64; r += 16) argmax_merge(v, i, lane_f(bv, r), __builtin_amdgcn_readlane(bi, r));
+    bv = v;
+    bi = i;
 }
 
 // Workgroup argmax for NW waves; redv/redi are LDS scratch of >= NW entries.
