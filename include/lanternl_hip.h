@@ -224,6 +224,20 @@ LHIP_API int lhip_sgd_step(float* params, float* grads, float* velocity, long lo
                            const double* grad_sumsq, float lr, float momentum, float weight_decay,
                            float grad_scale, float clip_norm, int nesterov,
                            float* grad_norm_out, int* applied_out);
+/* One AdamW step (ai/optim/optim2.lua:116-147, LMTrain's default optimizer,
+ * optim2.create at :166-171) with the same step logic as lhip_sgd_step: if the
+ * norm is finite, g = grads*grad_scale (clipped, written back), then
+ * m = beta1*m + (1-beta1)*g, v = beta2*v + (1-beta2)*g^2,
+ * p -= lr*wd*p, p -= (lr/(1-beta1^step)) * m / (sqrt(v/(1-beta2^step)) + eps).
+ * `step` is the 1-based AdamW step count this update uses (optim2's self.t
+ * after its increment); the caller advances it only when *applied_out is 1.
+ * Replaces the reference's luaTL_adamw_kernel (cuda/luaTL_core.cu:1346-1380),
+ * whose per-element clip and bias-correction arguments differ; this follows
+ * the CPU path. */
+LHIP_API int lhip_adamw_step(float* params, float* grads, float* m, float* v, long long n,
+                             const double* grad_sumsq, float lr, float beta1, float beta2, float eps,
+                             float weight_decay, float grad_scale, float clip_norm, int step,
+                             float* grad_norm_out, int* applied_out);
 
 /* ---- the CPU LMTrain step, resident on the GPU ------------------------------
  * One optimizer step of LMTrain with optimizer = "sgd" over `batch` windows of
@@ -274,6 +288,16 @@ LHIP_API int lhip_lm_use_graph(void* model, int on);
 /* Enqueue one step (asynchronous). */
 LHIP_API int lhip_lm_step_sgd(void* model, float lr, float momentum, float weight_decay, float clip_norm,
                               int nesterov);
+/* The same step with optimizer = "adamw" (ai/optim/optim2.lua:104-164; LMTrain
+ * defaults lr 1e-3, beta1 0.9, beta2 0.95, eps 1e-8, wd 0.01,
+ * ai/optim/lmtrain.lua:25-26).  The AdamW step count lives on the device and
+ * advances only for applied steps, as optim2's self.t does. */
+LHIP_API int lhip_lm_step_adamw(void* model, float lr, float beta1, float beta2, float eps, float weight_decay,
+                                float clip_norm);
+/* AdamW moments (n = parameter count each; either pointer may be NULL) and the
+ * step count: set (e.g. on resume) and get (synchronous). */
+LHIP_API int lhip_lm_set_adam_state(void* model, const float* m, const float* v, long long n, int step);
+LHIP_API int lhip_lm_get_adam_state(void* model, float* m, float* v, long long n, int* step);
 /* Wait and report the last step; window_losses (may be NULL) gets `batch` values. */
 LHIP_API int lhip_lm_stats(void* model, lhip_lm_stats_t* out, float* window_losses, int nwin);
 /* Row argmax of the last step's logits (batch*seq int32). */

@@ -77,6 +77,7 @@ SIGNATURES = {
     "lhip_sumsq": (_i, [_p, _ll, _p]),
     "lhip_sum": (_i, [_p, _i, _f, _p]),
     "lhip_sgd_step": (_i, [_p, _p, _p, _ll, _p, _f, _f, _f, _f, _f, _i, _p, _p]),
+    "lhip_adamw_step": (_i, [_p, _p, _p, _p, _ll, _p, _f, _f, _f, _f, _f, _f, _f, _i, _p, _p]),
 }
 
 class LmConfig(ctypes.Structure):
@@ -107,6 +108,9 @@ SIGNATURES.update({
     "lhip_lm_set_batch": (_i, [_p, _p, _p]),
     "lhip_lm_use_graph": (_i, [_p, _i]),
     "lhip_lm_step_sgd": (_i, [_p, _f, _f, _f, _f, _i]),
+    "lhip_lm_step_adamw": (_i, [_p, _f, _f, _f, _f, _f, _f]),
+    "lhip_lm_set_adam_state": (_i, [_p, _p, _p, _ll, _i]),
+    "lhip_lm_get_adam_state": (_i, [_p, _p, _p, _ll, _p]),
     "lhip_lm_stats": (_i, [_p, ctypes.POINTER(LmStats), _p, _i]),
     "lhip_lm_get_argmax": (_i, [_p, _p, _i]),
 })

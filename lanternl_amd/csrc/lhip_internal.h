@@ -110,6 +110,13 @@ int sumsq_partials(const float* x, long long n, double* partial, int partial_len
 int sgd_step(float* p, float* g, float* v, long long n, const double* sumsq_dev, float lr, float momentum,
              float wd, float grad_scale, float clip_norm, int nesterov, float* gnorm_out, int* applied_out,
              hipStream_t s, const float* hyper_dev, int nparts = 0);
+// AdamW (optim2.lua:116-147) with the same step logic; nparts as sgd_step.
+// Step count: t_in when tcount is NULL, else read from tcount[parity] and the
+// advanced count written to tcount[parity ^ 1].  hyper_dev: {lr, -, wd, clip,
+// -, beta1, beta2, eps, parity} overriding the by-value arguments.
+int adamw_step(float* p, float* g, float* m, float* v, long long n, const double* sumsq_dev, int nparts, float lr,
+               float beta1, float beta2, float eps, float wd, float grad_scale, float clip_norm, int t_in,
+               int* tcount, int parity, float* gnorm_out, int* applied_out, hipStream_t s, const float* hyper_dev);
 int sum_f32(const float* x, int n, float scale, float* out, hipStream_t s);
 // Fused per-(window, head) attention of the LMTrain step (T <= 64, head_dim <= 64, even).
 bool attn_fused_ok(int T, int hd);

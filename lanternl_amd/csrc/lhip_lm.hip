@@ -35,10 +35,22 @@ namespace {
 
 enum { P_LN1, P_WQ, P_WK, P_WV, P_WO, P_LN2, P_W1, P_W3, P_W2, P_PER_LAYER };
 
-__global__ void set_hyper_kernel(float* hp, float lr, float momentum, float wd, float clip, float nesterov)
+enum { OPT_SGD = 0, OPT_ADAMW = 1 };
+
+// Optimizer hyper-parameters of one step.  Eager launches pass them by value;
+// a captured step reads them from the device copy m.hyper, laid out as
+// {lr, momentum, wd, clip, nesterov, beta1, beta2, eps, parity}, which
+// set_hyper_kernel refreshes before each replay.
+struct Hyper {
+    float lr, momentum, wd, clip, nesterov, beta1, beta2, eps, parity;
+    int opt;
+};
+
+__global__ void set_hyper_kernel(float* hp, const Hyper h)
 {
     if (threadIdx.x == 0) {
-        hp[0] = lr; hp[1] = momentum; hp[2] = wd; hp[3] = clip; hp[4] = nesterov;
+        hp[0] = h.lr; hp[1] = h.momentum; hp[2] = h.wd; hp[3] = h.clip; hp[4] = h.nesterov;
+        hp[5] = h.beta1; hp[6] = h.beta2; hp[7] = h.eps; hp[8] = h.parity;
     }
 }
 
@@ -52,6 +64,9 @@ struct LmModel {
     float *params = nullptr, *grads = nullptr, *vel = nullptr;
     int *ids = nullptr, *tgt = nullptr, *amax = nullptr, *applied = nullptr;
     float *losses = nullptr, *gnorm = nullptr, *hyper = nullptr;
+    float *adam_m = nullptr, *adam_v = nullptr;   // AdamW moments
+    int* tcount = nullptr;                         // AdamW step count, two parity slots
+    long long adam_calls = 0;                      // AdamW steps enqueued (slot parity)
     double *ss = nullptr, *ss_part = nullptr;
     int ss_blocks = 0;
     // saved activations
@@ -75,6 +90,7 @@ struct LmModel {
     bool fused_attn = false;      // per-(window, head) fused attention kernels
     // graph
     bool use_graph = false;
+    int graph_opt = -1;           // optimizer of the captured step
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     int steps = 0;
@@ -196,14 +212,8 @@ struct Forker {
     int join() { return link(m.side, main); }   // main waits for all side-stream work so far
 };
 
-// Optimizer hyper-parameters passed by value (eager launches); a captured
-// step passes none and reads them from m.hyper, which each launch refreshes.
-struct Hyper {
-    float lr, momentum, wd, clip;
-    int nesterov;
-};
-
-int enqueue_step(LmModel& m, hipStream_t s, const Hyper* hp)
+// device_hyper: read the hyper-parameters from m.hyper (captured steps)
+int enqueue_step(LmModel& m, hipStream_t s, const Hyper& hp, bool device_hyper)
 {
     const Enq q{m, s, m.splitk};
     const Enq q2{m, m.side, m.splitk + m.splitk_floats};
@@ -347,15 +357,17 @@ int enqueue_step(LmModel& m, hipStream_t s, const Hyper* hp)
     LM_TRY(fk.join());
 
     // ---------------- optimizer (lmtrain.lua:1212-1226) ----------------
-    // squared-norm partials; the SGD kernel finishes the sum itself
+    // squared-norm partials; the optimizer kernel finishes the sum itself
     LM_TRY(sumsq_partials(m.grads, m.nparam, m.ss_part, m.ss_blocks, s));
     const float gscale = m.B > 1 ? 1.0f / m.B : 1.0f;
-    if (hp)
-        LM_TRY(sgd_step(m.params, m.grads, m.vel, m.nparam, m.ss_part, hp->lr, hp->momentum, hp->wd, gscale, hp->clip,
-                        hp->nesterov, m.gnorm, m.applied, s, nullptr, m.ss_blocks));
+    const float* hdev = device_hyper ? m.hyper : nullptr;
+    if (hp.opt == OPT_ADAMW)
+        LM_TRY(adamw_step(m.params, m.grads, m.adam_m, m.adam_v, m.nparam, m.ss_part, m.ss_blocks, hp.lr, hp.beta1,
+                          hp.beta2, hp.eps, hp.wd, gscale, hp.clip, 0, m.tcount, hp.parity != 0.f ? 1 : 0, m.gnorm,
+                          m.applied, s, hdev));
     else
-        LM_TRY(sgd_step(m.params, m.grads, m.vel, m.nparam, m.ss_part, 0.f, 0.f, 0.f, gscale, 0.f, 0, m.gnorm,
-                        m.applied, s, m.hyper, m.ss_blocks));
+        LM_TRY(sgd_step(m.params, m.grads, m.vel, m.nparam, m.ss_part, hp.lr, hp.momentum, hp.wd, gscale, hp.clip,
+                        hp.nesterov != 0.f ? 1 : 0, m.gnorm, m.applied, s, hdev, m.ss_blocks));
     return LHIP_OK;
 }
 
@@ -367,11 +379,11 @@ void drop_graph(LmModel& m)
     m.graph = nullptr;
 }
 
-int capture_step(LmModel& m, hipStream_t s)
+int capture_step(LmModel& m, hipStream_t s, const Hyper& hp)
 {
     drop_graph(m);
     LHIP_CHECK_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "lm: begin capture");
-    const int rc = enqueue_step(m, s, nullptr);
+    const int rc = enqueue_step(m, s, hp, true);
     hipGraph_t g = nullptr;
     const hipError_t e = hipStreamEndCapture(s, &g);
     if (rc != LHIP_OK) {
@@ -385,6 +397,26 @@ int capture_step(LmModel& m, hipStream_t s)
         drop_graph(m);
         return hip_fail(e2, "lm: graph instantiate");
     }
+    m.graph_opt = hp.opt;
+    return LHIP_OK;
+}
+
+// One step with the given optimizer: graph replay (capturing first when
+// needed) or eager launches.
+int run_step(LmModel& m, const Hyper& hp)
+{
+    hipStream_t s = st().stream;
+    if (m.use_graph) {
+        set_hyper_kernel<<<1, 64, 0, s>>>(m.hyper, hp);
+        if (int rc = check_launch("lm step: hyper")) return rc;
+        if (!m.exec || m.graph_opt != hp.opt)
+            if (int rc = capture_step(m, s, hp)) return rc;
+        LHIP_CHECK_HIP(hipGraphLaunch(m.exec, s), "lm step: graph launch");
+    } else {
+        if (int rc = enqueue_step(m, s, hp, false)) return rc;
+    }
+    ++m.steps;
+    if (hp.opt == OPT_ADAMW) ++m.adam_calls;
     return LHIP_OK;
 }
 
@@ -485,7 +517,10 @@ LHIP_API int lhip_lm_create(const lhip_lm_config_t* cfg, void** model)
         {reinterpret_cast<void**>(&m->applied), sizeof(int) * 4},
         {reinterpret_cast<void**>(&m->losses), sizeof(float) * N},
         {reinterpret_cast<void**>(&m->gnorm), sizeof(float) * 4},
-        {reinterpret_cast<void**>(&m->hyper), sizeof(float) * 8},
+        {reinterpret_cast<void**>(&m->hyper), sizeof(float) * 16},
+        {reinterpret_cast<void**>(&m->adam_m), sizeof(float) * m->nparam},
+        {reinterpret_cast<void**>(&m->adam_v), sizeof(float) * m->nparam},
+        {reinterpret_cast<void**>(&m->tcount), sizeof(int) * 4},
         {reinterpret_cast<void**>(&m->ss), sizeof(double) * 2},
         {reinterpret_cast<void**>(&m->ss_part), sizeof(double) * m->ss_blocks},
         {reinterpret_cast<void**>(&m->x), sizeof(float) * (L + 1) * ND},
@@ -659,18 +694,66 @@ LHIP_API int lhip_lm_step_sgd(void* model, float lr, float momentum, float weigh
     if (!m->have_batch) return fail(LHIP_E_ARG, "lhip_lm_step_sgd: no batch (call lhip_lm_set_batch)");
     if (!(lr >= 0.f) || !(momentum >= 0.f) || !(weight_decay >= 0.f) || !(clip_norm >= 0.f))
         return fail(LHIP_E_ARG, "lhip_lm_step_sgd: lr, momentum, weight_decay and clip_norm must be >= 0");
+    lhip::Hyper hp{};
+    hp.lr = lr; hp.momentum = momentum; hp.wd = weight_decay; hp.clip = clip_norm;
+    hp.nesterov = nesterov ? 1.f : 0.f;
+    hp.opt = lhip::OPT_SGD;
+    return lhip::run_step(*m, hp);
+}
+
+LHIP_API int lhip_lm_step_adamw(void* model, float lr, float beta1, float beta2, float eps, float weight_decay,
+                                float clip_norm)
+{
+    LHIP_REQUIRE_READY();
+    if (!model) return fail(LHIP_E_NULL, "lhip_lm_step_adamw: model is NULL");
+    auto* m = lhip::as_model(model);
+    if (!m->have_batch) return fail(LHIP_E_ARG, "lhip_lm_step_adamw: no batch (call lhip_lm_set_batch)");
+    if (!(lr >= 0.f) || !(beta1 >= 0.f && beta1 < 1.f) || !(beta2 >= 0.f && beta2 < 1.f) || !(eps >= 0.f) ||
+        !(weight_decay >= 0.f) || !(clip_norm >= 0.f))
+        return fail(LHIP_E_ARG, "lhip_lm_step_adamw: lr, eps, weight_decay, clip_norm >= 0 and betas in [0, 1)");
+    lhip::Hyper hp{};
+    hp.lr = lr; hp.wd = weight_decay; hp.clip = clip_norm;
+    hp.beta1 = beta1; hp.beta2 = beta2; hp.eps = eps;
+    hp.parity = static_cast<float>(m->adam_calls & 1);
+    hp.opt = lhip::OPT_ADAMW;
+    return lhip::run_step(*m, hp);
+}
+
+LHIP_API int lhip_lm_set_adam_state(void* model, const float* mom, const float* var, long long n, int step)
+{
+    LHIP_REQUIRE_READY();
+    if (!model) return fail(LHIP_E_NULL, "lhip_lm_set_adam_state: model is NULL");
+    auto* m = lhip::as_model(model);
+    if (n != m->nparam) return fail(LHIP_E_SHAPE, "lhip_lm_set_adam_state: %lld values given, model has %lld", n,
+                                    m->nparam);
+    if (step < 0) return fail(LHIP_E_ARG, "lhip_lm_set_adam_state: step %d < 0", step);
     hipStream_t s = st().stream;
-    if (m->use_graph) {
-        lhip::set_hyper_kernel<<<1, 64, 0, s>>>(m->hyper, lr, momentum, weight_decay, clip_norm, nesterov ? 1.f : 0.f);
-        if (int rc = lhip::check_launch("lhip_lm_step_sgd: hyper")) return rc;
-        if (!m->exec)
-            if (int rc = lhip::capture_step(*m, s)) return rc;
-        LHIP_CHECK_HIP(hipGraphLaunch(m->exec, s), "lhip_lm_step_sgd: graph launch");
-    } else {
-        const lhip::Hyper hp{lr, momentum, weight_decay, clip_norm, nesterov ? 1 : 0};
-        if (int rc = lhip::enqueue_step(*m, s, &hp)) return rc;
-    }
-    ++m->steps;
+    const size_t bytes = static_cast<size_t>(n) * sizeof(float);
+    if (mom) LHIP_CHECK_HIP(hipMemcpyAsync(m->adam_m, mom, bytes, hipMemcpyHostToDevice, s), "set_adam_state: m");
+    if (var) LHIP_CHECK_HIP(hipMemcpyAsync(m->adam_v, var, bytes, hipMemcpyHostToDevice, s), "set_adam_state: v");
+    // the slot the next AdamW step reads
+    int* slot = m->tcount + (m->adam_calls & 1);
+    LHIP_CHECK_HIP(hipMemcpyAsync(slot, &step, sizeof(int), hipMemcpyHostToDevice, s), "set_adam_state: step");
+    LHIP_CHECK_HIP(hipStreamSynchronize(s), "set_adam_state: sync");
+    return LHIP_OK;
+}
+
+LHIP_API int lhip_lm_get_adam_state(void* model, float* mom, float* var, long long n, int* step)
+{
+    LHIP_REQUIRE_READY();
+    if (!model) return fail(LHIP_E_NULL, "lhip_lm_get_adam_state: model is NULL");
+    auto* m = lhip::as_model(model);
+    if (n != m->nparam) return fail(LHIP_E_SHAPE, "lhip_lm_get_adam_state: %lld values asked, model has %lld", n,
+                                    m->nparam);
+    hipStream_t s = st().stream;
+    const size_t bytes = static_cast<size_t>(n) * sizeof(float);
+    if (mom) LHIP_CHECK_HIP(hipMemcpyAsync(mom, m->adam_m, bytes, hipMemcpyDeviceToHost, s), "get_adam_state: m");
+    if (var) LHIP_CHECK_HIP(hipMemcpyAsync(var, m->adam_v, bytes, hipMemcpyDeviceToHost, s), "get_adam_state: v");
+    int t = 0;
+    LHIP_CHECK_HIP(hipMemcpyAsync(&t, m->tcount + (m->adam_calls & 1), sizeof(int), hipMemcpyDeviceToHost, s),
+                   "get_adam_state: step");
+    LHIP_CHECK_HIP(hipStreamSynchronize(s), "get_adam_state: sync");
+    if (step) *step = t;
     return LHIP_OK;
 }
 

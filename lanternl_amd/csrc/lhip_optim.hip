@@ -112,6 +112,74 @@ sgd_step_kernel(float* __restrict__ p, float* __restrict__ g, float* __restrict_
     }
 }
 
+// One AdamW step (optim2.lua:116-147) inside the same LMTrain step logic as
+// sgd_step_kernel (scale, finite check, global-norm clip; g overwritten with
+// the gradient used).  The step count t (bias corrections 1 - beta^t) is
+// t_in when tcount is NULL; otherwise it lives on the device in two slots:
+// the kernel reads tcount[parity] and block 0 writes the advanced count
+// (advanced only when the step applies) to tcount[parity ^ 1], so no block
+// can read a half-updated counter; the caller alternates parity per call.
+// Device hyper-parameters (graph replay): {lr, -, wd, clip, -, beta1, beta2,
+// eps, parity}.
+__global__ void __launch_bounds__(256)
+adamw_step_kernel(float* __restrict__ p, float* __restrict__ g, float* __restrict__ m, float* __restrict__ v,
+                  long long n, const double* __restrict__ sumsq, int nparts, float lr, float beta1, float beta2,
+                  float eps, float wd, float grad_scale, float clip_norm, int t_in, int* __restrict__ tcount,
+                  int parity, float* __restrict__ gnorm_out, int* __restrict__ applied_out,
+                  const float* __restrict__ hyper)
+{
+    if (hyper) {
+        lr = hyper[0]; wd = hyper[2]; clip_norm = hyper[3];
+        beta1 = hyper[5]; beta2 = hyper[6]; eps = hyper[7]; parity = hyper[8] != 0.f ? 1 : 0;
+    }
+    double total;
+    if (nparts > 0) {
+        __shared__ double tot;
+        if (threadIdx.x < 64) {
+            double s = 0.0;
+            for (int i = threadIdx.x; i < nparts; i += 64) s += sumsq[i];
+            s = wave_sum(s);
+            if (threadIdx.x == 0) tot = s;
+        }
+        __syncthreads();
+        total = tot;
+    } else {
+        total = sumsq[0];
+    }
+    const double norm = static_cast<double>(grad_scale) * sqrt(total);
+    const bool finite = isfinite(norm);
+    const int t_old = tcount ? tcount[parity] : t_in - 1;
+    const int t = t_old + 1;
+    const long long t0 = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
+    if (t0 == 0) {
+        if (gnorm_out) gnorm_out[0] = static_cast<float>(norm);
+        if (applied_out) applied_out[0] = finite ? 1 : 0;
+        if (tcount) tcount[parity ^ 1] = finite ? t : t_old;
+    }
+    if (!finite) return;
+    const float clipf = (clip_norm > 0.f && norm > clip_norm) ? static_cast<float>(clip_norm / norm) : 1.0f;
+    const double bc1 = 1.0 - pow(static_cast<double>(beta1), t);
+    const double bc2 = 1.0 - pow(static_cast<double>(beta2), t);
+    const float step_size = static_cast<float>(lr / bc1);
+    const float inv_bc2 = static_cast<float>(1.0 / bc2);
+    const float decay = wd != 0.f ? lr * wd : 0.f;
+    const float c1 = 1.0f - beta1, c2 = 1.0f - beta2;
+    const long long stride = static_cast<long long>(gridDim.x) * blockDim.x;
+    for (long long i = t0; i < n; i += stride) {
+        float gk = g[i] * grad_scale;
+        if (clipf != 1.0f) gk = gk * clipf;
+        g[i] = gk;
+        const float mk = beta1 * m[i] + c1 * gk;
+        const float vk = beta2 * v[i] + c2 * gk * gk;
+        m[i] = mk;
+        v[i] = vk;
+        const float denom = sqrtf(vk * inv_bc2) + eps;
+        float pk = p[i];
+        if (decay != 0.f) pk = pk - decay * pk;
+        p[i] = pk - step_size * mk / denom;
+    }
+}
+
 // out[0] = scale * sum(x[0..n)) (float result from a double accumulation; single block)
 __global__ void __launch_bounds__(256) sum_f32_kernel(const float* __restrict__ x, int n, float scale, float* __restrict__ out)
 {
@@ -176,6 +244,24 @@ int sgd_step(float* p, float* g, float* v, long long n, const double* sumsq_dev,
     return check_launch("sgd_step");
 }
 
+int adamw_step(float* p, float* g, float* m, float* v, long long n, const double* sumsq_dev, int nparts, float lr,
+               float beta1, float beta2, float eps, float wd, float grad_scale, float clip_norm, int t_in,
+               int* tcount, int parity, float* gnorm_out, int* applied_out, hipStream_t s, const float* hyper_dev)
+{
+    if (n < 0) return fail(LHIP_E_SHAPE, "adamw_step: n < 0");
+    if (!sumsq_dev) return fail(LHIP_E_NULL, "adamw_step: sumsq is NULL");
+    if (n > 0 && (!p || !g || !m || !v)) return fail(LHIP_E_NULL, "adamw_step: NULL params/grads/moments");
+    if (!tcount && t_in < 1) return fail(LHIP_E_ARG, "adamw_step: step %d must be >= 1", t_in);
+    const int cus = st().cu_count > 0 ? st().cu_count : 256;
+    long long blocks = (n + 255) / 256;
+    if (blocks > 4LL * cus) blocks = 4LL * cus;
+    if (blocks < 1) blocks = 1;
+    adamw_step_kernel<<<static_cast<int>(blocks), 256, 0, s>>>(p, g, m, v, n, sumsq_dev, nparts, lr, beta1, beta2,
+                                                             eps, wd, grad_scale, clip_norm, t_in, tcount, parity,
+                                                             gnorm_out, applied_out, hyper_dev);
+    return check_launch("adamw_step");
+}
+
 int sum_f32(const float* x, int n, float scale, float* out, hipStream_t s)
 {
     if (n < 0) return fail(LHIP_E_SHAPE, "sum_f32: n < 0");
@@ -207,6 +293,18 @@ LHIP_API int lhip_sgd_step(float* params, float* grads, float* velocity, long lo
     LHIP_REQUIRE_READY();
     return lhip::sgd_step(params, grads, velocity, n, grad_sumsq, lr, momentum, weight_decay, grad_scale, clip_norm,
                           nesterov, grad_norm_out, applied_out, st().stream, nullptr);
+}
+
+LHIP_API int lhip_adamw_step(float* params, float* grads, float* m, float* v, long long n, const double* grad_sumsq,
+                             float lr, float beta1, float beta2, float eps, float weight_decay, float grad_scale,
+                             float clip_norm, int step, float* grad_norm_out, int* applied_out)
+{
+    LHIP_REQUIRE_READY();
+    if (!(lr >= 0.f) || !(beta1 >= 0.f && beta1 < 1.f) || !(beta2 >= 0.f && beta2 < 1.f) || !(eps >= 0.f) ||
+        !(weight_decay >= 0.f) || !(clip_norm >= 0.f))
+        return lhip::fail(LHIP_E_ARG, "lhip_adamw_step: lr, eps, weight_decay, clip_norm >= 0 and betas in [0, 1)");
+    return lhip::adamw_step(params, grads, m, v, n, grad_sumsq, 0, lr, beta1, beta2, eps, weight_decay, grad_scale,
+                            clip_norm, step, nullptr, 0, grad_norm_out, applied_out, st().stream, nullptr);
 }
 
 LHIP_API int lhip_sum(const float* x, int n, float scale, float* out)

@@ -74,7 +74,7 @@ def init_params(cfg, rng, std=0.02):
 
 
 class GpuLMStep:
-    """Device-resident model + SGD state for one LMTrain configuration."""
+    """Device-resident model + optimizer state (SGD or AdamW) for one LMTrain configuration."""
 
     def __init__(self, vocab, dim, layers, heads, ffn, batch, seq, causal=True, eps=1e-5, rope_base=10000.0):
         device.init(0)
@@ -123,9 +123,34 @@ class GpuLMStep:
 
     # -- the step --------------------------------------------------------------
     def step(self, lr, momentum=0.9, weight_decay=0.01, clip_norm=1.0, nesterov=False):
-        """Enqueue one optimizer step (asynchronous; stats() waits)."""
+        """Enqueue one SGD step (asynchronous; stats() waits)."""
         call("lhip_lm_step_sgd", self._h, float(lr), float(momentum), float(weight_decay),
              float(clip_norm), int(bool(nesterov)))
+
+    def step_adamw(self, lr=1e-3, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.01, clip_norm=1.0):
+        """Enqueue one AdamW step (LMTrain's default optimizer; asynchronous)."""
+        call("lhip_lm_step_adamw", self._h, float(lr), float(beta1), float(beta2), float(eps),
+             float(weight_decay), float(clip_norm))
+
+    def set_adam_state(self, m=None, v=None, step=0):
+        arrs = []
+        for a in (m, v):
+            if a is None:
+                arrs.append(None)
+                continue
+            a = np.ascontiguousarray(a, dtype=np.float32).reshape(-1)
+            if a.size != self.n:
+                raise ValueError(f"{a.size} values given, model has {self.n}")
+            arrs.append(a)
+        call("lhip_lm_set_adam_state", self._h, None if arrs[0] is None else arrs[0].ctypes.data,
+             None if arrs[1] is None else arrs[1].ctypes.data, self.n, int(step))
+
+    def adam_state(self):
+        """(m, v, step) of the AdamW optimizer."""
+        m = np.empty(self.n, dtype=np.float32); v = np.empty(self.n, dtype=np.float32)
+        t = ctypes.c_int(0)
+        call("lhip_lm_get_adam_state", self._h, m.ctypes.data, v.ctypes.data, self.n, ctypes.byref(t))
+        return m, v, int(t.value)
 
     def stats(self):
         st = LmStats()

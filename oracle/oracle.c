@@ -439,6 +439,30 @@ void or_sgd_step(double* p, const double* g, double* v, long n,
     }
 }
 
+/* optim2.lua:116-147 (AdamW.step after self.t has been advanced to t):
+ * m = b1 m + (1-b1) g, v = b2 v + (1-b2) g^2, p -= lr*wd*p (decoupled),
+ * p -= (lr / (1 - b1^t)) * m / (sqrt(v / (1 - b2^t)) + eps). */
+void or_adamw_step(double* p, const double* g, double* m, double* v, long n,
+                   double lr, double b1, double b2, double eps, double wd, int t)
+{
+    const double bc1 = 1 - pow(b1, t);
+    const double bc2 = 1 - pow(b2, t);
+    const double step_size = lr / bc1;
+    const double inv_bc2 = 1 / bc2;
+    const double decay = wd != 0 ? lr * wd : 0;
+    for (long k = 0; k < n; ++k) {
+        const double gk = g[k];
+        const double mk = b1 * m[k] + (1 - b1) * gk;
+        const double vk = b2 * v[k] + (1 - b2) * gk * gk;
+        m[k] = mk;
+        v[k] = vk;
+        const double denom = sqrt(vk * inv_bc2) + eps;
+        double pk = p[k];
+        if (decay != 0) pk = pk - decay * pk;
+        p[k] = pk - step_size * mk / denom;
+    }
+}
+
 /* ====================================================================== */
 /* Transformer window forward/backward and the LMTrain SGD step            */
 /* ====================================================================== */
@@ -716,11 +740,12 @@ double or_lm_window(const or_lm_cfg* c, const double* params, const int* ids, co
     return loss;
 }
 
-/* lmtrain.lua:1183-1227 with optimizer = "sgd" (optim2.lua:48-102) */
-int or_lm_step_sgd(const or_lm_cfg* c, double* params, double* vel,
-                   const int* ids, const int* tgt, int B, int T,
-                   double lr, double momentum, double wd, double clip_norm,
-                   double* losses, double* gnorm, int* correct, double* grads)
+/* the batch part of lmtrain.lua:1183-1222 shared by both optimizers: zero
+ * grads, every window, scale 1/B, norm, finite check, clip.  Returns 1 when
+ * the optimizer step is to be applied. */
+static int lm_batch_grads(const or_lm_cfg* c, const double* params, const int* ids, const int* tgt,
+                          int B, int T, double clip_norm, double* losses, double* gnorm, int* correct,
+                          double* grads)
 {
     const long n = or_lm_num_params(c);
     for (long e = 0; e < n; ++e) grads[e] = 0;                       /* opt.zero_grad() */
@@ -736,6 +761,29 @@ int or_lm_step_sgd(const or_lm_cfg* c, double* params, double* vel,
     if (gnorm) *gnorm = norm;
     if (!(norm == norm) || norm == HUGE_VAL || norm == -HUGE_VAL) return 0;
     if (clip_norm > 0 && norm > clip_norm) or_scale(grads, n, clip_norm / norm);
-    or_sgd_step(params, grads, vel, n, lr, momentum, wd, 0);
+    return 1;
+}
+
+/* lmtrain.lua:1183-1227 with optimizer = "adamw" (optim2.lua:104-164); *t is
+ * the AdamW step count, advanced only when the step is applied. */
+int or_lm_step_adamw(const or_lm_cfg* c, double* params, double* m, double* v, int* t,
+                     const int* ids, const int* tgt, int B, int T,
+                     double lr, double b1, double b2, double eps, double wd, double clip_norm,
+                     double* losses, double* gnorm, int* correct, double* grads)
+{
+    if (!lm_batch_grads(c, params, ids, tgt, B, T, clip_norm, losses, gnorm, correct, grads)) return 0;
+    *t = *t + 1;
+    or_adamw_step(params, grads, m, v, or_lm_num_params(c), lr, b1, b2, eps, wd, *t);
+    return 1;
+}
+
+/* lmtrain.lua:1183-1227 with optimizer = "sgd" (optim2.lua:48-102) */
+int or_lm_step_sgd(const or_lm_cfg* c, double* params, double* vel,
+                   const int* ids, const int* tgt, int B, int T,
+                   double lr, double momentum, double wd, double clip_norm,
+                   double* losses, double* gnorm, int* correct, double* grads)
+{
+    if (!lm_batch_grads(c, params, ids, tgt, B, T, clip_norm, losses, gnorm, correct, grads)) return 0;
+    or_sgd_step(params, grads, vel, or_lm_num_params(c), lr, momentum, wd, 0);
     return 1;
 }

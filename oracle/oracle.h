@@ -32,6 +32,10 @@
  *                       ties/NaN/-inf brute force.
  *   or_embed_*        : scatter of ids {3,0,7,3,1} (tests/test.lua:291-320).
  *   or_sgd_step / or_grad_norm : closed forms; l2(3,4)=25 (tests/test.lua:157-164).
+ *   or_adamw_step     : closed forms (no reference test holds AdamW vectors):
+ *                       constant gradient g gives m/bc1 = g, v/bc2 = g^2 at every
+ *                       t, so each step is p(1-lr*wd) - lr*g/(|g|+eps); zero
+ *                       gradient gives p(1-lr*wd)^t; moments vs their recurrences.
  *   or_lm_*           : float64 torch.autograd of the same model (independent
  *                       derivative), finite differences on a tiny model, ln V at
  *                       near-uniform logits.
@@ -118,6 +122,9 @@ double or_grad_norm(const double* g, long n);                 /* :27-38 */
 void   or_scale(double* g, long n, double f);                 /* :40-46 */
 void   or_sgd_step(double* p, const double* g, double* v, long n,
                    double lr, double momentum, double wd, int nesterov);  /* :72-99 */
+/* AdamW.step with the step count already advanced to t (>= 1)  :116-147 */
+void   or_adamw_step(double* p, const double* g, double* m, double* v, long n,
+                     double lr, double b1, double b2, double eps, double wd, int t);
 
 /* ---- the CPU LMTrain step: ai/nn/transformer.lua:84-257 +
  *      ai/optim/lmtrain.lua:1183-1227 --------------------------------- */
@@ -151,6 +158,13 @@ int or_lm_step_sgd(const or_lm_cfg* c, double* params, double* vel,
                    const int* ids, const int* tgt, int B, int T,
                    double lr, double momentum, double wd, double clip_norm,
                    double* losses, double* gnorm, int* correct, double* grads);
+
+/* The same step with optimizer="adamw": *t (the AdamW step count) is advanced
+ * and the AdamW update applied only when the norm is finite.  m, v: moments. */
+int or_lm_step_adamw(const or_lm_cfg* c, double* params, double* m, double* v, int* t,
+                     const int* ids, const int* tgt, int B, int T,
+                     double lr, double b1, double b2, double eps, double wd, double clip_norm,
+                     double* losses, double* gnorm, int* correct, double* grads);
 
 #ifdef __cplusplus
 }

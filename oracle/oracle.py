@@ -66,11 +66,16 @@ def _declare(L):
         "or_grad_norm": (c_double, [_D, c_long]),
         "or_scale": (None, [_D, c_long, c_double]),
         "or_sgd_step": (None, [_D, _D, _D, c_long, c_double, c_double, c_double, c_int]),
+        "or_adamw_step": (None, [_D, _D, _D, _D, c_long, c_double, c_double, c_double, c_double,
+                                 c_double, c_int]),
         "or_lm_num_params": (c_long, [ctypes.POINTER(LmCfg)]),
         "or_lm_param_offsets": (c_int, [ctypes.POINTER(LmCfg), ctypes.POINTER(c_long), _I, _I]),
         "or_lm_window": (c_double, [ctypes.POINTER(LmCfg), _D, _I, _I, c_int, _D, _D, _I]),
         "or_lm_step_sgd": (c_int, [ctypes.POINTER(LmCfg), _D, _D, _I, _I, c_int, c_int,
                                    c_double, c_double, c_double, c_double, _D, _D, _I, _D]),
+        "or_lm_step_adamw": (c_int, [ctypes.POINTER(LmCfg), _D, _D, _D, _I, _I, _I, c_int, c_int,
+                                     c_double, c_double, c_double, c_double, c_double, c_double,
+                                     _D, _D, _I, _D]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -289,6 +294,16 @@ def sgd_step(p, g, v, lr, momentum=0.0, wd=0.0, nesterov=False):
                       wd, int(nesterov))
 
 
+def adamw_step(p, g, m, v, t, lr, beta1=0.9, beta2=0.95, eps=1e-8, wd=0.01):
+    """In place on float64 p, m, v; t is the already advanced step count
+    (optim2.lua:116-147)."""
+    for a in (p, m, v):
+        assert a.dtype == np.float64
+    g, pg = _d(g)
+    lib().or_adamw_step(p.ctypes.data_as(_D), pg, m.ctypes.data_as(_D), v.ctypes.data_as(_D), p.size,
+                        lr, beta1, beta2, eps, wd, int(t))
+
+
 # ---------------------------------------------------------------- LMTrain step
 def lm_cfg(vocab, dim, layers, heads, ffn, causal=True, eps=1e-5, rope_base=10000.0):
     return LmCfg(vocab, dim, layers, heads, ffn, int(causal), eps, rope_base)
@@ -340,3 +355,22 @@ def lm_step_sgd(cfg, params, vel, ids, tgt, lr, momentum=0.9, wd=0.01, clip_norm
                                    ctypes.byref(corr), grads.ctypes.data_as(_D))
     return dict(losses=losses, gnorm=gn.value, correct=corr.value, grads=grads,
                 applied=bool(applied))
+
+
+def lm_step_adamw(cfg, params, m, v, t, ids, tgt, lr, beta1=0.9, beta2=0.95, eps=1e-8, wd=0.01,
+                  clip_norm=1.0):
+    """One LMTrain batch step (optimizer="adamw"); params, m, v float64 updated in
+    place.  t is the AdamW step count before the call.  Returns dict(losses,
+    gnorm, correct, grads, applied, t) with t advanced when the step applied."""
+    for a in (params, m, v):
+        assert a.dtype == np.float64
+    ids, pi = _i(ids); tgt, pt = _i(tgt)
+    B, T = ids.shape
+    losses = np.zeros(B); grads = np.zeros(params.size)
+    gn = ctypes.c_double(0); corr = ctypes.c_int(0); tc = ctypes.c_int(int(t))
+    applied = lib().or_lm_step_adamw(ctypes.byref(cfg), params.ctypes.data_as(_D), m.ctypes.data_as(_D),
+                                     v.ctypes.data_as(_D), ctypes.byref(tc), pi, pt, B, T, lr, beta1,
+                                     beta2, eps, wd, clip_norm, losses.ctypes.data_as(_D),
+                                     ctypes.byref(gn), ctypes.byref(corr), grads.ctypes.data_as(_D))
+    return dict(losses=losses, gnorm=gn.value, correct=corr.value, grads=grads,
+                applied=bool(applied), t=tc.value)

@@ -200,3 +200,109 @@ def test_lm_step_head_dim_64_fused_limit():
     gpu, res = _run_case(64, 128, 1, 2, 64, 2, 64, steps=1, lr=0.05, std=0.1, seed=13)
     _check(res)
     gpu.close()
+
+
+# ------------------------------------------------------------------ AdamW
+def _run_adamw(V, D, L, H, F, B, T, steps, lr, std, seed, graph=False, clip=1.0, b1=0.9, b2=0.95, eps=1e-8,
+               wd=0.01, poison_step=None):
+    """Chained AdamW steps; before each, the oracle takes the GPU's params,
+    moments and step count, so each step is compared on its own."""
+    rng = np.random.default_rng(seed)
+    cfg = O.lm_cfg(V, D, L, H, F)
+    gpu = lmtrain.GpuLMStep(V, D, L, H, F, B, T)
+    gpu.set_params(lmtrain.init_params(gpu.cfg, rng, std))
+    if graph:
+        gpu.use_graph(True)
+    out = []
+    for s in range(steps):
+        ids = rng.integers(0, V, (B, T)).astype(np.int32)
+        tgt = rng.integers(0, V, (B, T)).astype(np.int32)
+        if poison_step == s:
+            p = gpu.params()
+            p[V * D + 3] = np.nan            # a first-layer norm gain: every gradient turns NaN
+            gpu.set_params(p)
+        gpu.set_batch(ids, tgt)
+        p0 = gpu.params().astype(np.float64)
+        m0, v0, t0 = gpu.adam_state()
+        gpu.step_adamw(lr, b1, b2, eps, wd, clip)
+        st = gpu.stats()
+        m1, v1, t1 = gpu.adam_state()
+        pr, mr, vr = p0.copy(), m0.astype(np.float64), v0.astype(np.float64)
+        ref = O.lm_step_adamw(cfg, pr, mr, vr, t0, ids, tgt, lr, b1, b2, eps, wd, clip)
+        out.append(dict(st=st, ref=ref, p0=p0, p1=gpu.params().astype(np.float64), m1=m1, v1=v1, t1=t1,
+                        pr=pr, mr=mr, vr=vr, grads=gpu.grads().astype(np.float64)))
+    return gpu, out
+
+
+def _check_adamw(out, loss_tol=1e-5):
+    for r in out:
+        st, ref = r["st"], r["ref"]
+        assert st["applied"] == ref["applied"]
+        assert r["t1"] == ref["t"]
+        if not ref["applied"]:
+            continue
+        assert np.max(np.abs(st["window_losses"] - ref["losses"])) <= loss_tol
+        assert abs(st["grad_norm"] - ref["gnorm"]) <= 1e-5 * ref["gnorm"]
+        assert rel_fro(r["grads"], ref["grads"]) <= 1e-4
+        assert rel_fro(r["m1"], r["mr"]) <= 1e-4
+        assert rel_fro(r["v1"], r["vr"]) <= 1e-4
+        # Adam's update is ~lr*sign(g) per element: compare the update itself
+        assert rel_fro(r["p1"] - r["p0"], r["pr"] - r["p0"]) <= 1e-3
+
+
+def test_lm_adamw_tiny_chained_steps():
+    """AdamW (optim2.lua:104-164) over three chained steps: bias corrections at t = 1, 2, 3."""
+    announce("lm adamw tiny")
+    gpu, out = _run_adamw(32, 16, 1, 2, 32, 2, 8, steps=3, lr=1e-2, std=0.3, seed=21)
+    assert [r["t1"] for r in out] == [1, 2, 3]
+    _check_adamw(out)
+    gpu.close()
+
+
+def test_lm_adamw_config_c2_graph():
+    """Config C2 with LMTrain's AdamW defaults (lr 1e-3, betas 0.9/0.95, eps 1e-8, wd 0.01,
+    lmtrain.lua:25-26), replayed from a captured graph."""
+    announce("lm adamw C2 graph")
+    gpu, out = _run_adamw(2000, 128, 4, 8, 256, 8, 64, steps=2, lr=1e-3, std=0.02, seed=22, graph=True)
+    _check_adamw(out)
+    gpu.close()
+
+
+def test_lm_adamw_skip_keeps_step_count():
+    """A non-finite norm skips the update and leaves the AdamW step count where it was
+    (optim2's self.t advances inside step(), which LMTrain does not call then)."""
+    announce("lm adamw skip")
+    gpu, out = _run_adamw(32, 16, 1, 2, 32, 2, 8, steps=2, lr=1e-2, std=0.3, seed=23, poison_step=1)
+    assert out[0]["ref"]["applied"] and not out[1]["ref"]["applied"]
+    assert out[1]["t1"] == 1
+    _check_adamw(out)
+    gpu.close()
+
+
+def test_lm_adamw_graph_matches_eager_and_state_round_trip():
+    """Graph replay and eager launches agree bit for bit over AdamW steps (the
+    step-count slots alternate per call); set/get of the AdamW state round-trips;
+    switching optimizers re-captures."""
+    announce("lm adamw graph==eager")
+    V, D, L, H, F, B, T = 64, 32, 2, 4, 64, 2, 16
+    rng = np.random.default_rng(24)
+    p = lmtrain.init_params(lmtrain.config(V, D, L, H, F, B, T), rng, 0.1)
+    a = lmtrain.GpuLMStep(V, D, L, H, F, B, T)
+    b = lmtrain.GpuLMStep(V, D, L, H, F, B, T)
+    a.set_params(p); b.set_params(p)
+    b.use_graph(True)
+    for s in range(4):
+        ids = rng.integers(0, V, (B, T)); tgt = rng.integers(0, V, (B, T))
+        a.set_batch(ids, tgt); b.set_batch(ids, tgt)
+        if s == 2:      # one SGD step in between: the graph is captured again for it
+            a.step(0.01); b.step(0.01)
+        else:
+            a.step_adamw(2e-3); b.step_adamw(2e-3)
+        assert np.array_equal(a.params(), b.params())
+    ma, va, ta = a.adam_state(); mb, vb, tb = b.adam_state()
+    assert ta == tb == 3 and np.array_equal(ma, mb) and np.array_equal(va, vb)
+    m = rng.standard_normal(a.n).astype(np.float32); v = np.abs(rng.standard_normal(a.n)).astype(np.float32)
+    a.set_adam_state(m, v, 7)
+    m2, v2, t2 = a.adam_state()
+    assert t2 == 7 and np.array_equal(m2, m) and np.array_equal(v2, v)
+    a.close(); b.close()

@@ -390,6 +390,42 @@ def test_sumsq_and_sgd_step_vs_oracle(clip, B, nan):
         assert np.array_equal(dl(P), p) and np.array_equal(dl(Vb), v)
 
 
+@pytest.mark.parametrize("clip,B,nan,step", [(1.0, 8, False, 1), (1e6, 1, False, 5), (1.0, 4, True, 2)])
+def test_adamw_step_vs_oracle(clip, B, nan, step):
+    """lhip_adamw_step: the LMTrain step logic around optim2.AdamW.step at step count `step`."""
+    rng = np.random.default_rng(18)
+    n = 912_512
+    p = f32(rng.standard_normal(n) * 0.02)
+    g = f32(rng.standard_normal(n) * 0.01)
+    m = f32(rng.standard_normal(n) * 0.001)
+    v = f32(np.abs(rng.standard_normal(n)) * 1e-5)
+    if nan:
+        g[77] = np.inf
+    P, G, M, Vb = to_dev(p), to_dev(g), to_dev(m), to_dev(v)
+    SS = device.Buffer((2,))
+    NORM, APP = device.Buffer((1,)), device.Buffer((1,), np.int32)
+    call("lhip_sumsq", G.ptr, n, SS.ptr)
+    lr, b1, b2, eps, wd = 1e-3, 0.9, 0.95, 1e-8, 0.01
+    call("lhip_adamw_step", P.ptr, G.ptr, M.ptr, Vb.ptr, n, SS.ptr, lr, b1, b2, eps, wd, 1.0 / B, clip, step,
+         NORM.ptr, APP.ptr)
+    device.sync()
+    gg = g / B if B > 1 else g.copy()
+    norm = O.grad_norm(gg)
+    applied = bool(np.isfinite(norm))
+    assert APP.download()[0] == int(applied)
+    if not applied:
+        assert np.array_equal(dl(P), p) and np.array_equal(dl(M), m) and np.array_equal(dl(Vb), v)
+        return
+    if norm > clip:
+        gg = gg * (clip / norm)
+    pr, mr, vr = p.copy(), m.copy(), v.copy()
+    O.adamw_step(pr, gg, mr, vr, step, lr, b1, b2, eps, wd)
+    assert abs(NORM.download()[0] - norm) <= 1e-6 * norm
+    assert rel_fro(dl(G), gg) <= EW
+    assert rel_fro(dl(M), mr) <= EW and rel_fro(dl(Vb), vr) <= EW
+    assert rel_fro(dl(P) - p, pr - p) <= 1e-4
+
+
 def test_sum_and_fill_and_add():
     x = np.arange(1, 1001, dtype=np.float64)
     X, OUT = to_dev(x), device.Buffer((1,))

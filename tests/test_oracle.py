@@ -272,6 +272,42 @@ def test_grad_norm_and_sgd_closed_form():
     np.testing.assert_allclose(p, [0.949 - 0.096849, -2.023 - 0.043677], rtol=1e-14)
 
 
+def test_adamw_closed_forms():
+    """optim2.lua:116-147.  No reference test holds AdamW vectors, so the
+    restatement is pinned by what the algorithm fixes: with a constant
+    gradient the bias corrections make m/bc1 = g and v/bc2 = g^2 exactly at
+    every t, so each step is p <- p(1 - lr*wd) - lr*g/(|g| + eps); with a zero
+    gradient p decays as (1 - lr*wd)^t and the moments stay 0; the moments
+    follow their recurrences (a wrong beta, a missing or misplaced bias
+    correction, or coupled decay fails one of these)."""
+    lr, b1, b2, eps, wd = 0.1, 0.9, 0.95, 1e-8, 0.01
+    g = np.array([2.0, -0.5, 1e-3, 0.0])
+    p = np.array([1.0, 3.0, -2.0, 0.5]); m = np.zeros(4); v = np.zeros(4)
+    pexp = p.copy()
+    for t in range(1, 8):
+        O.adamw_step(p, g, m, v, t, lr, b1, b2, eps, wd)
+        pexp = pexp * (1 - lr * wd) - lr * g / (np.abs(g) + eps)
+        np.testing.assert_allclose(p, pexp, rtol=1e-13, atol=1e-15)
+        np.testing.assert_allclose(m, (1 - b1 ** t) * g, rtol=1e-13, atol=0)
+        np.testing.assert_allclose(v, (1 - b2 ** t) * g * g, rtol=1e-13, atol=0)
+    # zero gradient: pure decoupled decay
+    p = np.array([1.0, -4.0]); m = np.zeros(2); v = np.zeros(2)
+    for t in range(1, 6):
+        O.adamw_step(p, np.zeros(2), m, v, t, lr, b1, b2, eps, wd)
+    np.testing.assert_allclose(p, np.array([1.0, -4.0]) * (1 - lr * wd) ** 5, rtol=1e-14)
+    assert np.all(m == 0) and np.all(v == 0)
+    # changing gradient, two steps by hand: t=1 then t=2
+    p = np.array([1.0]); m = np.zeros(1); v = np.zeros(1)
+    O.adamw_step(p, np.array([1.0]), m, v, 1, lr, b1, b2, eps, wd)
+    O.adamw_step(p, np.array([-3.0]), m, v, 2, lr, b1, b2, eps, wd)
+    m2 = b1 * (1 - b1) * 1.0 + (1 - b1) * -3.0          # = -0.21
+    v2 = b2 * (1 - b2) * 1.0 + (1 - b2) * 9.0            # = 0.4975
+    p1 = (1.0 - lr * wd) - lr * 1.0 / (1.0 + eps)
+    p2 = p1 * (1 - lr * wd) - lr / (1 - b1 ** 2) * m2 / (np.sqrt(v2 / (1 - b2 ** 2)) + eps)
+    assert abs(m[0] - m2) < 1e-15 and abs(v[0] - v2) < 1e-15
+    assert abs(p[0] - p2) < 1e-14
+
+
 # ------------------------------------------------------------------ LMTrain
 TINY = dict(vocab=32, dim=16, layers=2, heads=2, ffn=24)
 
@@ -365,3 +401,30 @@ def test_lm_step_sgd_semantics():
     out = O.lm_step_sgd(cfg, bad, v, ids, tgt, lr=0.05)
     assert not out["applied"]
     assert np.array_equal(np.isnan(bad), np.isnan(before)) and np.all(v == 0)
+
+
+def test_lm_step_adamw_semantics():
+    """lmtrain.lua:1183-1227 with optimizer "adamw": the same batch gradient as
+    the SGD step (scale 1/B, clip), then AdamW with t advanced only for an
+    applied step; a skipped step leaves params, moments and t unchanged."""
+    cfg = O.lm_cfg(**TINY)
+    p0, tab = _tiny_params(cfg)
+    rng = np.random.default_rng(19)
+    B, T = 2, 5
+    ids = rng.integers(0, cfg.vocab, (B, T)); tgt = rng.integers(0, cfg.vocab, (B, T))
+    ps = p0.copy(); vs = np.zeros_like(ps)
+    ref = O.lm_step_sgd(cfg, ps, vs, ids, tgt, lr=0.0, momentum=0.0, wd=0.0, clip_norm=0.3)
+    p = p0.copy(); m = np.zeros_like(p); v = np.zeros_like(p)
+    out = O.lm_step_adamw(cfg, p, m, v, 0, ids, tgt, lr=1e-2, beta1=0.9, beta2=0.95, eps=1e-8, wd=0.01,
+                          clip_norm=0.3)
+    assert out["applied"] and out["t"] == 1
+    np.testing.assert_allclose(out["grads"], ref["grads"], rtol=1e-14, atol=0)
+    pe = p0.copy(); me = np.zeros_like(pe); ve = np.zeros_like(pe)
+    O.adamw_step(pe, ref["grads"], me, ve, 1, 1e-2, 0.9, 0.95, 1e-8, 0.01)
+    np.testing.assert_allclose(p, pe, rtol=1e-14, atol=0)
+    np.testing.assert_allclose(m, me, rtol=1e-14, atol=0)
+    bad = p.copy(); bad[tab[1][1]] = np.nan
+    mb, vb = m.copy(), v.copy()
+    out = O.lm_step_adamw(cfg, bad, mb, vb, 1, ids, tgt, lr=1e-2)
+    assert not out["applied"] and out["t"] == 1
+    assert np.array_equal(mb, m) and np.array_equal(vb, v)
