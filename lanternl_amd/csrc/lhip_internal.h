@@ -118,6 +118,38 @@ int adamw_step(float* p, float* g, float* m, float* v, long long n, const double
                float beta1, float beta2, float eps, float wd, float grad_scale, float clip_norm, int t_in,
                int* tcount, int parity, float* gnorm_out, int* applied_out, hipStream_t s, const float* hyper_dev);
 int sum_f32(const float* x, int n, float scale, float* out, hipStream_t s);
+// GEMMs of the LMTrain step with their neighbouring stages fused in (16x16
+// tiles, K <= 512 in one pass).  Mode bits:
+//   FB_NORM       A := rmsnorm(A; nw, eps); h (ld K) and inv receive the
+//                 normalized rows and 1/rms
+//   FB_DUAL       C = A'.B, C2 = A'.B2, Aout = silu(C) * C2 (batch 1)
+//   FB_SWIGLU_BWD G = A'.B^T, then dZ, dU = SwiGLU backward of (Z, U) with G
+//   FB_TB         B is N x K (NT)
+//   FB_NORMBWD    A := dres + RMSNorm backward (x = nbx, gain nw, 1/rms nbinv,
+//                 upstream dy = A); nbout (ld K) receives those rows and nbpart
+//                 [ceil(M/16)][K] the per-16-row dw partials
+// Otherwise C + y*sC = A'.(B + y*sB) for y < batch.  C/C2/Aout/Z/U/dZ/dU share ldc.
+enum { FB_NORM = 1, FB_DUAL = 2, FB_SWIGLU_BWD = 4, FB_TB = 8, FB_NORMBWD = 16 };
+enum {
+    FUSE_NORM = FB_NORM,
+    FUSE_NORM_SWIGLU = FB_NORM | FB_DUAL,
+    FUSE_SWIGLU_BWD = FB_SWIGLU_BWD | FB_TB,
+    FUSE_NB_SWIGLU_BWD = FB_NORMBWD | FB_SWIGLU_BWD | FB_TB,
+    FUSE_NB_NT = FB_NORMBWD | FB_TB,
+};
+struct FuseCall {
+    int mode = 0, M = 0, N = 0, K = 0, batch = 1;
+    const float* A = nullptr; int lda = 0;
+    const float* B = nullptr; int ldb = 0; long long sB = 0;
+    float* C = nullptr; int ldc = 0; long long sC = 0;
+    const float* nw = nullptr; float eps = 0.f; float* h = nullptr; float* inv = nullptr;
+    const float* B2 = nullptr; float* C2 = nullptr; float* Aout = nullptr;
+    const float* Z = nullptr; const float* U = nullptr; float* dZ = nullptr; float* dU = nullptr;
+    const float* nbx = nullptr; const float* nbres = nullptr; const float* nbinv = nullptr;
+    float* nbout = nullptr; float* nbpart = nullptr;
+};
+bool lm_fuse_ok(int K, int lda, int ldb_nt);
+int lm_fused_gemm(const FuseCall& c, hipStream_t s);
 // Fused per-(window, head) attention of the LMTrain step (T <= 64, head_dim <= 64, even).
 bool attn_fused_ok(int T, int hd);
 int attn_fwd(const float* qkv, const float2* cs, float* P, float* ctx, int B, int H, int T, int hd, float scale,

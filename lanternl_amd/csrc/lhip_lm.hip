@@ -23,6 +23,7 @@
 // The whole step is enqueued on the library stream with no host round trip
 // (the norm, the skip decision and the clip factor stay on the device) and no
 // allocation, so it can be captured once into a hipGraph and replayed.
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <new>
@@ -88,6 +89,7 @@ struct LmModel {
     std::vector<hipEvent_t> ev;
     float2* rope_cs = nullptr;    // (cos, sin) of positions 0..T-1, pairs 0..hd/2-1
     bool fused_attn = false;      // per-(window, head) fused attention kernels
+    bool fused_gemm = false;      // norm / SwiGLU stages fused into their GEMMs
     // graph
     bool use_graph = false;
     int graph_opt = -1;           // optimizer of the captured step
@@ -248,9 +250,19 @@ int enqueue_step(LmModel& m, hipStream_t s, const Hyper& hp, bool device_hyper)
         float* zu = m.zu + l * 2 * NF;
         float* a = m.a + l * NF;
         float* xn = m.x + (l + 1) * ND;
-        LM_TRY(rmsnorm_fwd(xl, m.prm(m.lt(l, P_LN1)), h, inv1, N, D, eps, s));
-        // q, k, v = h.Wq, h.Wk, h.Wv: one batched GEMM (the three weights are adjacent)
-        LM_TRY(q.bgemm(0, 0, N, D, D, h, D, 0, m.prm(m.lt(l, P_WQ)), D, static_cast<long long>(D) * D, 0.f, qkv, D, ND, 3));
+        // h = rmsnorm(x); q, k, v = h.Wq, h.Wk, h.Wv (the three weights are adjacent)
+        if (m.fused_gemm) {
+            FuseCall c;
+            c.mode = FUSE_NORM; c.M = N; c.N = D; c.K = D; c.batch = 3;
+            c.A = xl; c.lda = D; c.B = m.prm(m.lt(l, P_WQ)); c.ldb = D; c.sB = static_cast<long long>(D) * D;
+            c.C = qkv; c.ldc = D; c.sC = ND;
+            c.nw = m.prm(m.lt(l, P_LN1)); c.eps = eps; c.h = h; c.inv = inv1;
+            LM_TRY(lm_fused_gemm(c, s));
+        } else {
+            LM_TRY(rmsnorm_fwd(xl, m.prm(m.lt(l, P_LN1)), h, inv1, N, D, eps, s));
+            LM_TRY(q.bgemm(0, 0, N, D, D, h, D, 0, m.prm(m.lt(l, P_WQ)), D, static_cast<long long>(D) * D, 0.f, qkv, D,
+                           ND, 3));
+        }
         if (m.fused_attn) {
             // RoPE, scores, causal softmax and P.v per (window, head) in one launch;
             // qkv keeps the unrotated q, k (the backward rotates again)
@@ -267,10 +279,20 @@ int enqueue_step(LmModel& m, hipStream_t s, const Hyper& hp, bool device_hyper)
         }
         // x_mid = x + ctx . Wo
         LM_TRY(q.gemm_res(N, D, D, ctx, D, m.prm(m.lt(l, P_WO)), D, xl, xmid, D));
-        LM_TRY(rmsnorm_fwd(xmid, m.prm(m.lt(l, P_LN2)), h2, inv2, N, D, eps, s));
-        // z1 = h2.W1, u = h2.W3 (adjacent weights, one batched GEMM); a = silu(z1) * u
-        LM_TRY(q.bgemm(0, 0, N, F, D, h2, D, 0, m.prm(m.lt(l, P_W1)), F, static_cast<long long>(D) * F, 0.f, zu, F, NF, 2));
-        LM_TRY(swiglu_fwd(zu, F, zu + NF, F, a, F, N, F, s));
+        // h2 = rmsnorm(x_mid); z1 = h2.W1, u = h2.W3; a = silu(z1) * u
+        if (m.fused_gemm) {
+            FuseCall c;
+            c.mode = FUSE_NORM_SWIGLU; c.M = N; c.N = F; c.K = D;
+            c.A = xmid; c.lda = D; c.B = m.prm(m.lt(l, P_W1)); c.ldb = F; c.B2 = m.prm(m.lt(l, P_W3));
+            c.C = zu; c.C2 = zu + NF; c.Aout = a; c.ldc = F;
+            c.nw = m.prm(m.lt(l, P_LN2)); c.eps = eps; c.h = h2; c.inv = inv2;
+            LM_TRY(lm_fused_gemm(c, s));
+        } else {
+            LM_TRY(rmsnorm_fwd(xmid, m.prm(m.lt(l, P_LN2)), h2, inv2, N, D, eps, s));
+            LM_TRY(q.bgemm(0, 0, N, F, D, h2, D, 0, m.prm(m.lt(l, P_W1)), F, static_cast<long long>(D) * F, 0.f, zu, F,
+                           NF, 2));
+            LM_TRY(swiglu_fwd(zu, F, zu + NF, F, a, F, N, F, s));
+        }
         // x_{l+1} = x_mid + a . W2
         LM_TRY(q.gemm_res(N, D, F, a, F, m.prm(m.lt(l, P_W2)), D, xmid, xn, D));
     }
@@ -287,13 +309,27 @@ int enqueue_step(LmModel& m, hipStream_t s, const Hyper& hp, bool device_hyper)
     const float* dlg = m.logits;
     const size_t wf = m.work_floats;
     auto gxl = [&](int l) { return m.gx + l * ND; };
+    // An RMSNorm backward whose dx rows the next NT GEMM of the chain consumes:
+    // with fused GEMMs it runs as that GEMM's A prologue, otherwise as its own
+    // launch just before.  Its gain's dw partials are summed on the side stream.
+    struct NormBwd {
+        const float *x, *w, *inv, *dy, *dres;
+        float *out, *part, *gw;
+        int parts;
+    };
+    const int tiles_m = ceil_div(N, 16);
+    auto norm_standalone = [&](NormBwd& nb) {
+        return rmsnorm_bwd_rows(nb.x, nb.w, nb.inv, nb.dy, nb.out, nb.dres, nb.part, wf, N, D, &nb.parts, s);
+    };
+    auto norm_prologue = [&](FuseCall& c, NormBwd& nb) {
+        c.A = nb.dy; c.lda = D; c.nw = nb.w; c.nbx = nb.x; c.nbres = nb.dres; c.nbinv = nb.inv;
+        c.nbout = nb.out; c.nbpart = nb.part;
+        nb.parts = tiles_m;
+    };
     LM_TRY(fk.fork());
     LM_TRY(q2.gemm(1, 0, V, D, N, dlg, V, m.xf, D, 0.f, m.grd(0), D));            // gemb = dlogits^T . xf
     LM_TRY(q.gemm(0, 0, N, D, V, dlg, V, emb, D, 0.f, m.dxf, D));                // dxf = dlogits . emb
-    int parts = 0, parts_ln1 = 0;
-    LM_TRY(rmsnorm_bwd_rows(xL, lnf, m.invf, m.dxf, gxl(L), nullptr, m.work, wf, N, D, &parts, s));
-    LM_TRY(fk.fork());
-    LM_TRY(rmsnorm_bwd_colsum(m.work, parts, m.grd(1 + P_PER_LAYER * L), D, 0, s2));
+    NormBwd pend{xL, lnf, m.invf, m.dxf, nullptr, gxl(L), m.work, m.grd(1 + P_PER_LAYER * L), 0};
     for (int l = L - 1; l >= 0; --l) {
         const float* xl = m.x + l * ND;
         const float* h = m.h + l * ND;
@@ -306,26 +342,43 @@ int enqueue_step(LmModel& m, hipStream_t s, const Hyper& hp, bool device_hyper)
         const float* inv2 = m.inv2 + static_cast<long long>(l) * N;
         const float* zu = m.zu + l * 2 * NF;
         const float* a = m.a + l * NF;
-        const float* gin = gxl(l + 1);                 // dL/dx_{l+1}
+        const float* gin = gxl(l + 1);                 // dL/dx_{l+1} (written by the pending norm backward)
         float* gmid = m.gmid + l * ND;                 // dL/dxmid_l
         float* dzu = m.dzu + l * 2 * NF;
         float* dqkv = m.dqkv + l * 3 * ND;
-        float* work2 = m.work + (2 * l + 1) * wf;      // ln2 dw partials
-        float* work1 = m.work + (2 * l + 2) * wf;      // ln1 dw partials
-        // f = a . W2 ; a = silu(z1) * u
-        LM_TRY(q.gemm(0, 1, N, F, D, gin, D, m.prm(m.lt(l, P_W2)), D, 0.f, m.da, F));      // da = gin . W2^T
-        LM_TRY(swiglu_bwd(zu, F, zu + NF, F, m.da, F, dzu, F, dzu + NF, F, N, F, 0, s));
+        // f = a . W2 ; a = silu(z1) * u:  da = gin . W2^T, then the SwiGLU backward into dz1, du
+        if (m.fused_gemm) {
+            FuseCall c;
+            c.mode = FUSE_NB_SWIGLU_BWD; c.M = N; c.N = F; c.K = D;
+            c.B = m.prm(m.lt(l, P_W2)); c.ldb = D; c.ldc = F;
+            c.Z = zu; c.U = zu + NF; c.dZ = dzu; c.dU = dzu + NF;
+            norm_prologue(c, pend);
+            LM_TRY(lm_fused_gemm(c, s));
+        } else {
+            LM_TRY(norm_standalone(pend));
+            LM_TRY(q.gemm(0, 1, N, F, D, gin, D, m.prm(m.lt(l, P_W2)), D, 0.f, m.da, F));
+            LM_TRY(swiglu_bwd(zu, F, zu + NF, F, m.da, F, dzu, F, dzu + NF, F, N, F, 0, s));
+        }
         LM_TRY(fk.fork());
-        if (l + 1 < L)   // ln1 dw of the layer above (its partials are ready since the last fork)
-            LM_TRY(rmsnorm_bwd_colsum(m.work + (2 * (l + 1) + 2) * wf, parts_ln1, m.grd(m.lt(l + 1, P_LN1)), D, 0, s2));
+        LM_TRY(rmsnorm_bwd_colsum(pend.part, pend.parts, pend.gw, D, 0, s2));
         LM_TRY(q2.gemm(1, 0, F, D, N, a, F, gin, D, 0.f, m.grd(m.lt(l, P_W2)), D));         // gW2 = a^T . gin
         LM_TRY(q2.bgemm(1, 0, D, F, N, h2, D, 0, dzu, F, NF, 0.f, m.grd(m.lt(l, P_W1)), F,
                         static_cast<long long>(D) * F, 2));                                   // gW1, gW3
         // dh2 = dz1 . W1^T + du . W3^T (adjacent weights: one batch-reduce GEMM)
         LM_TRY(q.brgemm(1, N, D, F, 2, dzu, F, NF, m.prm(m.lt(l, P_W1)), F, static_cast<long long>(D) * F, m.dh2, D));
-        LM_TRY(rmsnorm_bwd_rows(xmid, m.prm(m.lt(l, P_LN2)), inv2, m.dh2, gmid, gin, work2, wf, N, D, &parts, s));
-        // o = ctx . Wo
-        LM_TRY(q.gemm(0, 1, N, D, D, gmid, D, m.prm(m.lt(l, P_WO)), D, 0.f, m.dctx, D));    // dctx = gmid . Wo^T
+        // gmid = gin + RMSNorm backward (ln2); o = ctx . Wo: dctx = gmid . Wo^T
+        NormBwd n2{xmid, m.prm(m.lt(l, P_LN2)), inv2, m.dh2, gin, gmid, m.work + (2 * l + 1) * wf,
+                   m.grd(m.lt(l, P_LN2)), 0};
+        if (m.fused_gemm) {
+            FuseCall c;
+            c.mode = FUSE_NB_NT; c.M = N; c.N = D; c.K = D;
+            c.B = m.prm(m.lt(l, P_WO)); c.ldb = D; c.C = m.dctx; c.ldc = D;
+            norm_prologue(c, n2);
+            LM_TRY(lm_fused_gemm(c, s));
+        } else {
+            LM_TRY(norm_standalone(n2));
+            LM_TRY(q.gemm(0, 1, N, D, D, gmid, D, m.prm(m.lt(l, P_WO)), D, 0.f, m.dctx, D));
+        }
         if (m.fused_attn) {
             // dP, dv, softmax backward, dq, dk and the inverse RoPE per (window, head)
             LM_TRY(attn_bwd(qkv, m.rope_cs, P, m.dctx, dqkv, m.B, H, T, hd, scale, causal, s));
@@ -342,17 +395,19 @@ int enqueue_step(LmModel& m, hipStream_t s, const Hyper& hp, bool device_hyper)
             LM_TRY(rope(dqkv, nullptr, 2 * N, H, hd, D, 0, T, base, 1, 1, s));
         }
         LM_TRY(fk.fork());
-        LM_TRY(rmsnorm_bwd_colsum(work2, parts, m.grd(m.lt(l, P_LN2)), D, 0, s2));
+        LM_TRY(rmsnorm_bwd_colsum(n2.part, n2.parts, n2.gw, D, 0, s2));
         LM_TRY(q2.gemm(1, 0, D, D, N, ctx, D, gmid, D, 0.f, m.grd(m.lt(l, P_WO)), D));       // gWo = ctx^T . gmid
         LM_TRY(q2.bgemm(1, 0, D, D, N, h, D, 0, dqkv, D, ND, 0.f, m.grd(m.lt(l, P_WQ)), D,
                         static_cast<long long>(D) * D, 3));                                   // gW{q,k,v}
         // dh = dq.Wq^T + dk.Wk^T + dv.Wv^T (adjacent weights: one batch-reduce GEMM)
         LM_TRY(q.brgemm(1, N, D, D, 3, dqkv, D, ND, m.prm(m.lt(l, P_WQ)), D, static_cast<long long>(D) * D, m.dh, D));
-        LM_TRY(rmsnorm_bwd_rows(xl, m.prm(m.lt(l, P_LN1)), inv1, m.dh, gxl(l), gmid, work1, wf, N, D, &parts_ln1,
-                                s));
+        // dx_l = gmid + RMSNorm backward (ln1): runs with the next layer's first GEMM
+        pend = NormBwd{xl, m.prm(m.lt(l, P_LN1)), inv1, m.dh, gmid, gxl(l), m.work + (2 * l + 2) * wf,
+                       m.grd(m.lt(l, P_LN1)), 0};
     }
+    LM_TRY(norm_standalone(pend));                       // dx_0 (no GEMM follows it)
     LM_TRY(fk.fork());
-    LM_TRY(rmsnorm_bwd_colsum(m.work + 2 * wf, parts_ln1, m.grd(m.lt(0, P_LN1)), D, 0, s2));
+    LM_TRY(rmsnorm_bwd_colsum(pend.part, pend.parts, pend.gw, D, 0, s2));
     LM_TRY(embed_bwd(gxl(0), m.ids, m.grd(0), N, D, V, 1.f, 1, s2));   // after gemb: same stream
     LM_TRY(fk.join());
 
@@ -503,7 +558,9 @@ LHIP_API int lhip_lm_create(const lhip_lm_config_t* cfg, void** model)
     const long long N = m->N, D = m->D, F = m->F, V = m->V, L = m->L;
     const long long ND = N * D, NF = N * F, PL = static_cast<long long>(m->B) * m->H * m->T * m->T;
     m->ss_blocks = lhip::sumsq_blocks(m->nparam);
-    m->work_floats = static_cast<size_t>(lhip::rmsnorm_bwd_parts(m->N, m->D)) * m->D;
+    // dw partials of one norm backward: the stand-alone kernel's, or one row per 16-row tile when fused
+    m->work_floats = static_cast<size_t>(std::max(lhip::rmsnorm_bwd_parts(m->N, m->D), lhip::ceil_div(m->N, 16))) *
+                     m->D;
     m->splitk_floats = static_cast<size_t>(1) << 22;   // 16 MiB per stream; the planner caps splits to fit
     // carve every buffer out of one allocation, each 256-byte aligned
     struct Slot { void** dst; size_t bytes; };
@@ -597,6 +654,7 @@ LHIP_API int lhip_lm_create(const lhip_lm_config_t* cfg, void** model)
         }
     }
     m->fused_attn = lhip::attn_fused_ok(m->T, m->hd);
+    m->fused_gemm = lhip::lm_fuse_ok(m->D, m->D, m->D) && m->F % 4 == 0;
     m->h_tgt.assign(static_cast<size_t>(N), 0);
     if (int src = lhip::make_streams(*m)) {
         lhip::release(*m);

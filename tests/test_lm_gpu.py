@@ -194,6 +194,15 @@ def test_lm_step_unfused_attention_path():
     gpu.close()
 
 
+def test_lm_step_unfused_gemm_path():
+    """dim 6 (not a multiple of 4) takes the separate RMSNorm, projection GEMM,
+    SwiGLU and SwiGLU-backward launches instead of the fused GEMMs."""
+    announce("lm unfused gemm")
+    gpu, res = _run_case(40, 6, 2, 1, 10, 2, 5, steps=2, lr=0.1, std=0.3, seed=14)
+    _check(res)
+    gpu.close()
+
+
 def test_lm_step_head_dim_64_fused_limit():
     """head_dim 64 and T 64: the largest fused attention configuration."""
     announce("lm hd64")
