@@ -130,6 +130,7 @@ struct GemmArgs {
     float* ws;                        // split-K partials [split][batch][M][N]
     int Kb;                           // batch-reduce: K = kblocks * Kb, block j reads A + j*sAk, B + j*sBk
     long long sAk, sBk;
+    int skip_reduce;                  // split-K slices stay in ws for the caller to sum
 };
 
 // C = alpha * sum_s ws[s] + beta * R, the slices summed in order (deterministic).
@@ -322,7 +323,8 @@ sgemm_small_kernel(const GemmArgs g)
     const int wave = tid >> 6;
     const int lr = lane & 31;
     const int h = lane >> 5;
-    const int tm = blockIdx.x / g.tiles_n, tn = blockIdx.x % g.tiles_n;
+    int tm, tn;
+    xcd_tile(blockIdx.x, gridDim.x, g.tiles_n, tm, tn);
     const int m0 = tm * 32, n0 = tn * 32;
     const long long zo = blockIdx.y / g.inner, zi = blockIdx.y % g.inner;
     const float* __restrict__ A = g.A + zo * g.sA2 + zi * g.sA;
@@ -449,7 +451,8 @@ sgemm_tiny_kernel(const GemmArgs g)
     const int wave = tid >> 6;
     const int lr = lane & 15;
     const int q = lane >> 4;
-    const int tm = blockIdx.x / g.tiles_n, tn = blockIdx.x % g.tiles_n;
+    int tm, tn;
+    xcd_tile(blockIdx.x, gridDim.x, g.tiles_n, tm, tn);
     const int m0 = tm * 16, n0 = tn * 16;
     const long long zo = blockIdx.y / g.inner, zi = blockIdx.y % g.inner;
     const float* __restrict__ A = g.A + zo * g.sA2 + zi * g.sA;
@@ -465,9 +468,11 @@ sgemm_tiny_kernel(const GemmArgs g)
 #pragma unroll
     for (int r = 0; r < 4; ++r) acc[r] = 0.f;
 
+    // A pass covers the wave's next U 16-deep steps; with more than one pass
+    // the next pass's loads are issued before this pass's MFMAs (two register
+    // sets), so the passes' load latencies overlap.
     constexpr int U = kSmallU;
-    for (int kp = kbeg + 16 * wave; kp < kend; kp += 64 * U) {
-        float a[U][4], b[U][4];
+    auto load_pass = [&](int kp, float (&a)[U][4], float (&b)[U][4]) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int kl = kp + 64 * u + 4 * q;
@@ -511,11 +516,29 @@ sgemm_tiny_kernel(const GemmArgs g)
                 }
             }
         }
+    };
+    auto mma_pass = [&](int kp, const float (&a)[U][4], const float (&b)[U][4]) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             if (kp + 64 * u >= kend) break;   // wave-uniform: nothing left in this pass
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u][i], b[u][i], acc, 0, 0, 0);
+        }
+    };
+    int kp = kbeg + 16 * wave;
+    if (kp < kend) {
+        float a0[U][4], b0[U][4], a1[U][4], b1[U][4];
+        load_pass(kp, a0, b0);
+        while (true) {
+            const int k1 = kp + 64 * U;
+            if (k1 < kend) load_pass(k1, a1, b1);
+            mma_pass(kp, a0, b0);
+            if (k1 >= kend) break;
+            const int k2 = k1 + 64 * U;
+            if (k2 < kend) load_pass(k2, a0, b0);
+            mma_pass(k1, a1, b1);
+            if (k2 >= kend) break;
+            kp = k2;
         }
     }
 
@@ -571,7 +594,7 @@ int launch_tiny(int ta, int tb, GemmArgs g, int batch, hipStream_t stream)
     else if (!ta && tb) sgemm_tiny_kernel<false, true, false><<<grid, block, 0, stream>>>(g);
     else sgemm_tiny_kernel<true, true, false><<<grid, block, 0, stream>>>(g);
     int rc = check_launch("sgemm (tiny): kernel launch");
-    if (rc != LHIP_OK || g.splits <= 1) return rc;
+    if (rc != LHIP_OK || g.splits <= 1 || g.skip_reduce) return rc;
     return launch_reduce(g, batch, stream);
 }
 
@@ -591,7 +614,7 @@ int launch_small(int ta, int tb, GemmArgs g, int batch, hipStream_t stream)
     else if (!ta && tb) launch_small_t<false, true, false>(g, grid, stream);
     else launch_small_t<true, true, false>(g, grid, stream);
     int rc = check_launch("sgemm (small): kernel launch");
-    if (rc != LHIP_OK || g.splits <= 1) return rc;
+    if (rc != LHIP_OK || g.splits <= 1 || g.skip_reduce) return rc;
     return launch_reduce(g, batch, stream);
 }
 
@@ -609,7 +632,7 @@ int launch_cfg(int ta, int tb, GemmArgs g, int batch, hipStream_t stream)
     else if (!ta && tb) sgemm_mfma_kernel<BM, BN, BK, false, true><<<grid, block, 0, stream>>>(g);
     else sgemm_mfma_kernel<BM, BN, BK, true, true><<<grid, block, 0, stream>>>(g);
     int rc = check_launch("sgemm: kernel launch");
-    if (rc != LHIP_OK || g.splits <= 1) return rc;
+    if (rc != LHIP_OK || g.splits <= 1 || g.skip_reduce) return rc;
     return launch_reduce(g, batch, stream);
 }
 
@@ -631,6 +654,7 @@ int launch_reduce(const GemmArgs& g, int batch, hipStream_t stream)
 // the 64x64 tiles (+ split-K) save in latency.
 bool use_small_kernel(int m, int n, int k) { return k <= 2048 || m <= 64 || n <= 64; }
 
+
 int splitk_plan(int m, int n, int k, int batch, size_t ws_floats, int* kchunk_out)
 {
     const int cus = st().cu_count > 0 ? st().cu_count : 256;
@@ -647,10 +671,9 @@ int splitk_plan(int m, int n, int k, int batch, size_t ws_floats, int* kchunk_ou
         tiles = static_cast<long long>(ceil_div(m, 32)) * ceil_div(n, 32) * batch;
         unit = 32;
         min_k = 256;
-        if (tiles < cus) {   // 16x16 tiles: a pass of the four waves covers 512 k
-            tiles = static_cast<long long>(ceil_div(m, 16)) * ceil_div(n, 16) * batch;
-            min_k = 512;
-        }
+        // 16x16 tiles (fewer 32x32 tiles than CUs) take long K unsplit: their
+        // passes are software-pipelined, which beats a split plus its reduce
+        if (tiles < cus) return 1;
     } else {
         // 64x64 tiles, 32-deep K tiles walked by one workgroup
         tiles = tiles64;
@@ -736,6 +759,12 @@ int sgemm_run(int ta, int tb, int m, int n, int k, float alpha,
     const bool small = use_small_kernel(m, n, g.K);
     g.splits = o.ws ? splitk_plan(m, n, g.K, batch, o.ws_floats, &g.kchunk) : 1;
     g.ws = o.ws;
+    if (o.splits_out) {
+        if (alpha != 1.f || beta != 0.f || batch != 1 || o.R)
+            return fail(LHIP_E_ARG, "sgemm: unreduced split-K needs alpha 1, beta 0, batch 1");
+        *o.splits_out = g.splits > 1 ? g.splits : 1;
+        g.skip_reduce = g.splits > 1 ? 1 : 0;
+    }
     const long long tiles32 = static_cast<long long>(ceil_div(m, 32)) * ceil_div(n, 32) * batch;
     if (small && tiles32 < cus) return launch_tiny(ta, tb, g, batch, stream);
     if (small) return launch_small(ta, tb, g, batch, stream);

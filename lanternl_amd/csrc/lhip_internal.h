@@ -62,6 +62,18 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 inline int ceil_div(long long a, long long b) { return static_cast<int>((a + b - 1) / b); }
 
+// Workgroup id -> (tile row, tile column), row-major over tiles_n columns, in
+// XCD-contiguous chunks: workgroups are dispatched round-robin over the 8
+// XCDs, so id p runs on XCD p % 8; giving each XCD one contiguous run of
+// tiles (whole row bands) keeps each A row band in one XCD's L2.
+__device__ __forceinline__ void xcd_tile(int pid, int nwg, int tiles_n, int& tm, int& tn)
+{
+    constexpr int kXcds = 8;
+    if ((nwg % kXcds) == 0) pid = (pid % kXcds) * (nwg / kXcds) + pid / kXcds;
+    tm = pid / tiles_n;
+    tn = pid - tm * tiles_n;
+}
+
 // Library workspace of at least `bytes` (reused; growing it waits for the
 // stream, so it must not be called while a stream capture is in progress).
 int workspace(size_t bytes, void** out);
@@ -147,6 +159,7 @@ struct FuseCall {
     const float* Z = nullptr; const float* U = nullptr; float* dZ = nullptr; float* dU = nullptr;
     const float* nbx = nullptr; const float* nbres = nullptr; const float* nbinv = nullptr;
     float* nbout = nullptr; float* nbpart = nullptr;
+    int a_parts = 1; long long a_pstride = 0;   // A = sum of a_parts slices a_pstride apart (in order)
 };
 bool lm_fuse_ok(int K, int lda, int ldb_nt);
 int lm_fused_gemm(const FuseCall& c, hipStream_t s);
@@ -174,6 +187,10 @@ struct GemmOpts {
     // batch-reduce: C = alpha * sum_{j<kblocks} op(A + j*sAk) . op(B + j*sBk) + beta * R
     int kblocks = 1;
     long long sAk = 0, sBk = 0;
+    // split-K without the reduce launch (alpha 1, beta 0, batch 1 only): when K
+    // is split, the slices stay in ws as [split][M][N] and *splits_out receives
+    // their count (1: the product went to C as usual); the consumer sums them
+    int* splits_out = nullptr;
 };
 
 int sgemm_run(int transa, int transb, int m, int n, int k, float alpha,

@@ -316,6 +316,7 @@ int enqueue_step(LmModel& m, hipStream_t s, const Hyper& hp, bool device_hyper)
         const float *x, *w, *inv, *dy, *dres;
         float *out, *part, *gw;
         int parts;
+        int dy_parts;   // dy = sum of this many [N][D] slices (unreduced split-K)
     };
     const int tiles_m = ceil_div(N, 16);
     auto norm_standalone = [&](NormBwd& nb) {
@@ -324,12 +325,21 @@ int enqueue_step(LmModel& m, hipStream_t s, const Hyper& hp, bool device_hyper)
     auto norm_prologue = [&](FuseCall& c, NormBwd& nb) {
         c.A = nb.dy; c.lda = D; c.nw = nb.w; c.nbx = nb.x; c.nbres = nb.dres; c.nbinv = nb.inv;
         c.nbout = nb.out; c.nbpart = nb.part;
+        c.a_parts = nb.dy_parts; c.a_pstride = ND;
         nb.parts = tiles_m;
     };
     LM_TRY(fk.fork());
     LM_TRY(q2.gemm(1, 0, V, D, N, dlg, V, m.xf, D, 0.f, m.grd(0), D));            // gemb = dlogits^T . xf
-    LM_TRY(q.gemm(0, 0, N, D, V, dlg, V, emb, D, 0.f, m.dxf, D));                // dxf = dlogits . emb
-    NormBwd pend{xL, lnf, m.invf, m.dxf, nullptr, gxl(L), m.work, m.grd(1 + P_PER_LAYER * L), 0};
+    // dxf = dlogits . emb; with fused GEMMs its split-K slices are left
+    // unreduced and summed by the norm-backward prologue that consumes dxf
+    int dxf_parts = 1;
+    {
+        GemmOpts o = q.opts();
+        if (m.fused_gemm) o.splits_out = &dxf_parts;
+        LM_TRY(sgemm_run(0, 0, N, D, V, 1.f, dlg, V, 0, emb, D, 0, 0.f, m.dxf, D, 0, 1, o, s));
+    }
+    NormBwd pend{xL, lnf, m.invf, dxf_parts > 1 ? q.ws : m.dxf, nullptr, gxl(L), m.work,
+                 m.grd(1 + P_PER_LAYER * L), 0, dxf_parts};
     for (int l = L - 1; l >= 0; --l) {
         const float* xl = m.x + l * ND;
         const float* h = m.h + l * ND;
@@ -368,7 +378,7 @@ int enqueue_step(LmModel& m, hipStream_t s, const Hyper& hp, bool device_hyper)
         LM_TRY(q.brgemm(1, N, D, F, 2, dzu, F, NF, m.prm(m.lt(l, P_W1)), F, static_cast<long long>(D) * F, m.dh2, D));
         // gmid = gin + RMSNorm backward (ln2); o = ctx . Wo: dctx = gmid . Wo^T
         NormBwd n2{xmid, m.prm(m.lt(l, P_LN2)), inv2, m.dh2, gin, gmid, m.work + (2 * l + 1) * wf,
-                   m.grd(m.lt(l, P_LN2)), 0};
+                   m.grd(m.lt(l, P_LN2)), 0, 1};
         if (m.fused_gemm) {
             FuseCall c;
             c.mode = FUSE_NB_NT; c.M = N; c.N = D; c.K = D;
@@ -403,7 +413,7 @@ int enqueue_step(LmModel& m, hipStream_t s, const Hyper& hp, bool device_hyper)
         LM_TRY(q.brgemm(1, N, D, D, 3, dqkv, D, ND, m.prm(m.lt(l, P_WQ)), D, static_cast<long long>(D) * D, m.dh, D));
         // dx_l = gmid + RMSNorm backward (ln1): runs with the next layer's first GEMM
         pend = NormBwd{xl, m.prm(m.lt(l, P_LN1)), inv1, m.dh, gmid, gxl(l), m.work + (2 * l + 2) * wf,
-                       m.grd(m.lt(l, P_LN1)), 0};
+                       m.grd(m.lt(l, P_LN1)), 0, 1};
     }
     LM_TRY(norm_standalone(pend));                       // dx_0 (no GEMM follows it)
     LM_TRY(fk.fork());

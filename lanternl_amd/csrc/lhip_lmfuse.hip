@@ -45,6 +45,7 @@ struct FuseArgs {
     const float* B2; float* C2; float* Aout;             // FUSE_NORM_SWIGLU: W3, U, a (ld ldc)
     const float* Z; const float* U; float* dZ; float* dU; // SwiGLU backward epilogue (ld ldc)
     const float* nbx; const float* nbres; const float* nbinv; float* nbout; float* nbpart;  // norm-backward prologue
+    int a_parts; long long a_pstride;   // A = sum of a_parts slices (split-K partials), summed in order
 };
 
 __device__ __forceinline__ float sigmoid_sign(float v)
@@ -71,7 +72,8 @@ __global__ void __launch_bounds__(256) lm_fused_gemm_kernel(const FuseArgs f)
     __shared__ float ssr[4][64];
     __shared__ float row_s[16];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, lr = lane & 15, q = lane >> 4;
-    const int tm = blockIdx.x / f.tiles_n, tn = blockIdx.x - tm * f.tiles_n;
+    int tm, tn;
+    xcd_tile(blockIdx.x, gridDim.x, f.tiles_n, tm, tn);
     const int m0 = tm * 16, n0 = tn * 16;
     const int y = blockIdx.y;
     const int K = f.K;
@@ -88,7 +90,14 @@ __global__ void __launch_bounds__(256) lm_fused_gemm_kernel(const FuseArgs f)
         const bool kin = k < K;
         const long long ro = static_cast<long long>(row) * f.lda + k;
         const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
-        to4(a[u], (rok && kin) ? ld4(f.A + ro) : z4);
+        float4 av = (rok && kin) ? ld4(f.A + ro) : z4;
+        for (int p = 1; p < f.a_parts; ++p) {
+            if (rok && kin) {
+                const float4 t = ld4(f.A + p * f.a_pstride + ro);
+                av.x += t.x; av.y += t.y; av.z += t.z; av.w += t.w;
+            }
+        }
+        to4(a[u], av);
         to4(w[u], ((NORM || NB) && kin) ? ld4(f.nw + k) : z4);
         if constexpr (NB) {
             to4(x[u], (rok && kin) ? ld4(f.nbx + ro) : z4);
@@ -255,6 +264,7 @@ int lm_fused_gemm(const FuseCall& c, hipStream_t s)
     f.B2 = c.B2; f.C2 = c.C2; f.Aout = c.Aout;
     f.Z = c.Z; f.U = c.U; f.dZ = c.dZ; f.dU = c.dU;
     f.nbx = c.nbx; f.nbres = c.nbres; f.nbinv = c.nbinv; f.nbout = c.nbout; f.nbpart = c.nbpart;
+    f.a_parts = c.a_parts > 0 ? c.a_parts : 1; f.a_pstride = c.a_pstride;
     const long long nwg = static_cast<long long>(ceil_div(c.M, 16)) * f.tiles_n;
     if (nwg > 0x7fffffffLL || c.batch > 65535) return fail(LHIP_E_CAPACITY, "lm_fused_gemm: grid too large");
     dim3 grid(static_cast<unsigned>(nwg), c.batch);

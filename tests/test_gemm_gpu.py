@@ -251,11 +251,13 @@ def test_gemm_c3_lm_head_shapes(ta, tb):
     assert rel_fro(got, ref) <= TOL
 
 
-@pytest.mark.parametrize("m,n,k,batch", [(512, 128, 2000, 1), (128, 128, 4096, 3), (64, 64, 1000, 2), (96, 64, 1100, 2),
-                                         (33, 70, 999, 1), (1, 4096, 4096, 1)])
+@pytest.mark.parametrize("m,n,k,batch", [(512, 128, 2000, 1), (128, 128, 4096, 3), (64, 64, 1000, 2),
+                                         (96, 64, 1100, 2), (512, 512, 2048, 1), (33, 70, 999, 1),
+                                         (1, 4096, 4096, 1)])
 def test_gemm_split_k_alpha_beta_batched(m, n, k, batch):
-    """Shapes with fewer output tiles than CUs and long K take the split-K path;
-    alpha/beta apply once, after the ordered sum of the slices."""
+    """Long-K shapes with few output tiles: the 64x64 and 32x32 kernels split K
+    (alpha/beta apply once, after the ordered sum of the slices); the 16x16
+    kernel walks long K in software-pipelined passes."""
     announce("gemm split-k", m, n, k, batch)
     rng = np.random.default_rng(m + n + k)
     a = f32(rng.uniform(-1, 1, (batch, m, k)))
