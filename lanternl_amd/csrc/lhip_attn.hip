@@ -66,28 +66,14 @@ template <int NB>
 __device__ __forceinline__ void mfma_rows(floatx4 (&acc)[NB], const float* a, int i0, const float* b, int j0,
                                           int jstep, int nb, int k0, int k1)
 {
-    // k1 - k0 is a multiple of 4; each 16-deep chunk reads all of its LDS
-    // operands before its MFMAs, so the chain waits on LDS once per chunk
     const int lane = threadIdx.x & 63, r = lane & 15, q = lane >> 4;
 #pragma unroll
     for (int j = 0; j < NB; ++j) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
-    for (int k = k0; k < k1; k += 16) {
-        float av[4], bv[NB][4];
+    for (int k = k0; k < k1; k += 4) {
+        const float av = a[(i0 + r) * kLd + k + q];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const bool in = k + 4 * t < k1;
-            av[t] = in ? a[(i0 + r) * kLd + k + 4 * t + q] : 0.f;
-#pragma unroll
-            for (int j = 0; j < NB; ++j)
-                bv[j][t] = (in && j < nb) ? b[(j0 + j * jstep + r) * kLd + k + 4 * t + q] : 0.f;
-        }
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            if (k + 4 * t >= k1) break;   // wave-uniform
-#pragma unroll
-            for (int j = 0; j < NB; ++j)
-                if (j < nb) acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[t], bv[j][t], acc[j], 0, 0, 0);
-        }
+        for (int j = 0; j < NB; ++j)
+            if (j < nb) acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, b[(j0 + j * jstep + r) * kLd + k + q], acc[j], 0, 0, 0);
     }
 }
 

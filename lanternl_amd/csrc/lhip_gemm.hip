@@ -440,7 +440,7 @@ sgemm_small_kernel(const GemmArgs g)
 // are k0+4q+i and the four MFMAs cover k0 .. k0+15 exactly once.  The four
 // waves take the 16-deep steps w, w+4, ...; their tiles are summed in LDS in
 // wave order.  Steps wholly past the end of K issue no MFMA.  BR as above.
-template <bool TA, bool TB, bool BR>
+template <bool TA, bool TB, bool BR, bool PIPE>
 __global__ void __launch_bounds__(256)
 sgemm_tiny_kernel(const GemmArgs g)
 {
@@ -482,7 +482,15 @@ sgemm_tiny_kernel(const GemmArgs g)
             const float* __restrict__ Ab = A;
             const float* __restrict__ Bb = B;
             if (BR) {
-                const int j = kl / g.Kb;
+                // block of this k: with Kb % 16 == 0 a 16-deep step lies in one
+                // block, so the index is the wave-uniform step start's
+                int j;
+                if (g.Kb % 16 == 0) {
+                    const int ks = __builtin_amdgcn_readfirstlane(kp + 64 * u);
+                    j = ks / g.Kb;
+                } else {
+                    j = kl / g.Kb;
+                }
                 kb = kl - j * g.Kb;
                 Ab = A + j * g.sAk;
                 Bb = B + j * g.sBk;
@@ -526,7 +534,13 @@ sgemm_tiny_kernel(const GemmArgs g)
         }
     };
     int kp = kbeg + 16 * wave;
-    if (kp < kend) {
+    if (!PIPE) {   // K fits one pass: one register set
+        if (kp < kend) {
+            float a0[U][4], b0[U][4];
+            load_pass(kp, a0, b0);
+            mma_pass(kp, a0, b0);
+        }
+    } else if (kp < kend) {
         float a0[U][4], b0[U][4], a1[U][4], b1[U][4];
         load_pass(kp, a0, b0);
         while (true) {
@@ -578,6 +592,19 @@ void launch_small_t(const GemmArgs& g, dim3 grid, hipStream_t stream)
 
 int launch_reduce(const GemmArgs& g, int batch, hipStream_t stream);
 
+// PIPE: K needs more than one pass of the four waves (64 * kSmallU deep)
+template <bool PIPE>
+void launch_tiny_t(int ta, int tb, const GemmArgs& g, dim3 grid, dim3 block, hipStream_t stream)
+{
+    if (g.Kb != g.K) {
+        if (!tb) sgemm_tiny_kernel<false, false, true, PIPE><<<grid, block, 0, stream>>>(g);
+        else sgemm_tiny_kernel<false, true, true, PIPE><<<grid, block, 0, stream>>>(g);
+    } else if (!ta && !tb) sgemm_tiny_kernel<false, false, false, PIPE><<<grid, block, 0, stream>>>(g);
+    else if (ta && !tb) sgemm_tiny_kernel<true, false, false, PIPE><<<grid, block, 0, stream>>>(g);
+    else if (!ta && tb) sgemm_tiny_kernel<false, true, false, PIPE><<<grid, block, 0, stream>>>(g);
+    else sgemm_tiny_kernel<true, true, false, PIPE><<<grid, block, 0, stream>>>(g);
+}
+
 int launch_tiny(int ta, int tb, GemmArgs g, int batch, hipStream_t stream)
 {
     g.tiles_m = ceil_div(g.M, 16);
@@ -586,13 +613,8 @@ int launch_tiny(int ta, int tb, GemmArgs g, int batch, hipStream_t stream)
     if (nwg > 0x7fffffffLL) return fail(LHIP_E_CAPACITY, "sgemm: %lld workgroups exceed the grid limit", nwg);
     if (g.splits <= 1) { g.splits = 1; g.kchunk = g.K; g.ws = nullptr; }
     dim3 grid(static_cast<unsigned>(nwg), batch, g.splits), block(256);
-    if (g.Kb != g.K) {
-        if (!tb) sgemm_tiny_kernel<false, false, true><<<grid, block, 0, stream>>>(g);
-        else sgemm_tiny_kernel<false, true, true><<<grid, block, 0, stream>>>(g);
-    } else if (!ta && !tb) sgemm_tiny_kernel<false, false, false><<<grid, block, 0, stream>>>(g);
-    else if (ta && !tb) sgemm_tiny_kernel<true, false, false><<<grid, block, 0, stream>>>(g);
-    else if (!ta && tb) sgemm_tiny_kernel<false, true, false><<<grid, block, 0, stream>>>(g);
-    else sgemm_tiny_kernel<true, true, false><<<grid, block, 0, stream>>>(g);
+    if (g.kchunk > 64 * kSmallU) launch_tiny_t<true>(ta, tb, g, grid, block, stream);
+    else launch_tiny_t<false>(ta, tb, g, grid, block, stream);
     int rc = check_launch("sgemm (tiny): kernel launch");
     if (rc != LHIP_OK || g.splits <= 1 || g.skip_reduce) return rc;
     return launch_reduce(g, batch, stream);
@@ -646,7 +668,91 @@ int launch_reduce(const GemmArgs& g, int batch, hipStream_t stream)
     return check_launch("sgemm: split-K reduce");
 }
 
+// Grouped transposed-A products (the weight gradients of one transformer
+// layer: dW = X^T . dY with X, dY row-major over the same B*T rows) in one
+// launch.  Workgroup id -> (group, tile) through the groups' first-tile table;
+// each tile is computed like sgemm_tiny_kernel<TA, !TB>: 16x16 outputs, four
+// waves over 16-deep K steps, lane l holding A^T[row][k0+4q..+3] (four scalar
+// loads down a column of the stored A, coalesced over the 16 rows) and
+// B[k0+4q..+3][col], partial tiles summed in LDS in wave order.
+struct GroupedTNArgs {
+    GroupedTN e[kGroupedMax];
+    int tile0[kGroupedMax + 1];
+    int tiles_n[kGroupedMax];
+    int ngroups, K;
+};
+
+__global__ void __launch_bounds__(256) sgemm_grouped_tn_kernel(const GroupedTNArgs ga)
+{
+    __shared__ float red[4][4][64];
+    const int id = blockIdx.x;
+    int gi = 0;
+    for (int i = 1; i < ga.ngroups; ++i)
+        if (id >= ga.tile0[i]) gi = i;
+    const GroupedTN& e = ga.e[gi];
+    const int local = id - ga.tile0[gi];
+    const int tm = local / ga.tiles_n[gi], tn = local - tm * ga.tiles_n[gi];
+    const int K = ga.K;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, lr = lane & 15, q = lane >> 4;
+    const int m0 = tm * 16, n0 = tn * 16;
+    const int row = m0 + lr, col = n0 + lr;
+    const bool rok = row < e.M, cok = col < e.N;
+    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+    constexpr int U = kSmallU;
+    for (int kp = 16 * wave; kp < K; kp += 64 * U) {
+        float a[U][4], b[U][4];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int k = kp + 64 * u + 4 * q;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const bool kin = k + i < K;
+                a[u][i] = (rok && kin) ? e.A[static_cast<long long>(k + i) * e.lda + row] : 0.f;
+                b[u][i] = (cok && kin) ? e.B[static_cast<long long>(k + i) * e.ldb + col] : 0.f;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (kp + 64 * u >= K) break;   // wave-uniform
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u][i], b[u][i], acc, 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[wave][r][lane] = acc[r];
+    __syncthreads();
+    const float v = ((red[0][wave][lane] + red[1][wave][lane]) + red[2][wave][lane]) + red[3][wave][lane];
+    const int orow = m0 + 4 * q + wave, ocol = n0 + lr;
+    if (orow < e.M && ocol < e.N) e.C[static_cast<long long>(orow) * e.ldc + ocol] = v;
+}
+
 }  // namespace
+
+int sgemm_grouped_tn(const GroupedTN* g, int ngroups, int K, hipStream_t stream)
+{
+    if (ngroups <= 0) return LHIP_OK;
+    if (ngroups > kGroupedMax) return fail(LHIP_E_ARG, "sgemm_grouped_tn: %d groups (at most %d)", ngroups, kGroupedMax);
+    if (K <= 0) return fail(LHIP_E_SHAPE, "sgemm_grouped_tn: K=%d", K);
+    GroupedTNArgs ga{};
+    long long tiles = 0;
+    for (int i = 0; i < ngroups; ++i) {
+        const GroupedTN& e = g[i];
+        if (e.M <= 0 || e.N <= 0) return fail(LHIP_E_SHAPE, "sgemm_grouped_tn: group %d is %dx%d", i, e.M, e.N);
+        if (!e.A || !e.B || !e.C) return fail(LHIP_E_NULL, "sgemm_grouped_tn: group %d has a NULL operand", i);
+        if (e.lda < e.M || e.ldb < e.N || e.ldc < e.N)
+            return fail(LHIP_E_SHAPE, "sgemm_grouped_tn: group %d leading dimensions", i);
+        ga.e[i] = e;
+        ga.tile0[i] = static_cast<int>(tiles);
+        ga.tiles_n[i] = ceil_div(e.N, 16);
+        tiles += static_cast<long long>(ceil_div(e.M, 16)) * ga.tiles_n[i];
+        if (tiles > 0x7fffffffLL) return fail(LHIP_E_CAPACITY, "sgemm_grouped_tn: too many tiles");
+    }
+    ga.tile0[ngroups] = static_cast<int>(tiles);
+    ga.ngroups = ngroups;
+    ga.K = K;
+    sgemm_grouped_tn_kernel<<<static_cast<unsigned>(tiles), 256, 0, stream>>>(ga);
+    return check_launch("sgemm_grouped_tn");
+}
 
 // Below the 64x64-tile threshold, the 32x32 small kernel is used unless K is
 // long AND both output dimensions exceed 64: its 32-wide tiles re-read A N/32

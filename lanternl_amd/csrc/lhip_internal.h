@@ -95,6 +95,10 @@ int rmsnorm_bwd_rows(const float* x, const float* w, const float* inv, const flo
                      const float* dres, float* partial, size_t partial_floats, int rows, int cols, int* parts_out,
                      hipStream_t s);
 int rmsnorm_bwd_colsum(const float* partial, int parts, float* dw, int cols, int accumulate, hipStream_t s);
+// several independent column sums in one launch (jobs with parts <= 0 are skipped)
+constexpr int kColsumJobs = 4;
+int rmsnorm_bwd_colsum_multi(const float* const* partials, const int* parts, float* const* dws, int njobs, int cols,
+                             int accumulate, hipStream_t s);
 int softmax_fwd(const float* x, float* y, int rows, int cols, float scale, int causal, int offset, int group,
                 hipStream_t s);
 int softmax_bwd(const float* y, const float* dy, float* dx, int rows, int cols, float scale, int causal,
@@ -193,6 +197,16 @@ struct GemmOpts {
     int* splits_out = nullptr;
 };
 
+// Grouped C_g = A_g^T . B_g (A_g stored K x M_g, B_g stored K x N_g, beta 0)
+// for up to kGroupedMax products sharing K, in one launch of 16x16 tiles.
+constexpr int kGroupedMax = 8;
+struct GroupedTN {
+    const float* A; int lda;
+    const float* B; int ldb;
+    float* C; int ldc;
+    int M, N;
+};
+int sgemm_grouped_tn(const GroupedTN* g, int ngroups, int K, hipStream_t stream);
 int sgemm_run(int transa, int transb, int m, int n, int k, float alpha,
               const float* A, int lda, long long sA, const float* B, int ldb, long long sB, float beta,
               float* C, int ldc, long long sC, int batch, const GemmOpts& o, hipStream_t stream);

@@ -369,11 +369,6 @@ int enqueue_step(LmModel& m, hipStream_t s, const Hyper& hp, bool device_hyper)
             LM_TRY(q.gemm(0, 1, N, F, D, gin, D, m.prm(m.lt(l, P_W2)), D, 0.f, m.da, F));
             LM_TRY(swiglu_bwd(zu, F, zu + NF, F, m.da, F, dzu, F, dzu + NF, F, N, F, 0, s));
         }
-        LM_TRY(fk.fork());
-        LM_TRY(rmsnorm_bwd_colsum(pend.part, pend.parts, pend.gw, D, 0, s2));
-        LM_TRY(q2.gemm(1, 0, F, D, N, a, F, gin, D, 0.f, m.grd(m.lt(l, P_W2)), D));         // gW2 = a^T . gin
-        LM_TRY(q2.bgemm(1, 0, D, F, N, h2, D, 0, dzu, F, NF, 0.f, m.grd(m.lt(l, P_W1)), F,
-                        static_cast<long long>(D) * F, 2));                                   // gW1, gW3
         // dh2 = dz1 . W1^T + du . W3^T (adjacent weights: one batch-reduce GEMM)
         LM_TRY(q.brgemm(1, N, D, F, 2, dzu, F, NF, m.prm(m.lt(l, P_W1)), F, static_cast<long long>(D) * F, m.dh2, D));
         // gmid = gin + RMSNorm backward (ln2); o = ctx . Wo: dctx = gmid . Wo^T
@@ -404,11 +399,27 @@ int enqueue_step(LmModel& m, hipStream_t s, const Hyper& hp, bool device_hyper)
             // RoPE backward (inverse rotation) on dq and dk
             LM_TRY(rope(dqkv, nullptr, 2 * N, H, hd, D, 0, T, base, 1, 1, s));
         }
+        // Side stream, one fork per layer: the two norm gains' column sums
+        // (the pending norm above this layer and ln2) and the layer's seven
+        // weight gradients dW = X^T . dY as one grouped launch.
         LM_TRY(fk.fork());
-        LM_TRY(rmsnorm_bwd_colsum(n2.part, n2.parts, n2.gw, D, 0, s2));
-        LM_TRY(q2.gemm(1, 0, D, D, N, ctx, D, gmid, D, 0.f, m.grd(m.lt(l, P_WO)), D));       // gWo = ctx^T . gmid
-        LM_TRY(q2.bgemm(1, 0, D, D, N, h, D, 0, dqkv, D, ND, 0.f, m.grd(m.lt(l, P_WQ)), D,
-                        static_cast<long long>(D) * D, 3));                                   // gW{q,k,v}
+        {
+            const float* parts_p[2] = {pend.part, n2.part};
+            const int parts_n[2] = {pend.parts, n2.parts};
+            float* parts_o[2] = {pend.gw, n2.gw};
+            LM_TRY(rmsnorm_bwd_colsum_multi(parts_p, parts_n, parts_o, 2, D, 0, s2));
+            const long long DD = static_cast<long long>(D) * D;
+            const GroupedTN gw[7] = {
+                {a, F, gin, D, m.grd(m.lt(l, P_W2)), D, F, D},                 // gW2 = a^T . gin
+                {h2, D, dzu, F, m.grd(m.lt(l, P_W1)), F, D, F},                // gW1 = h2^T . dz1
+                {h2, D, dzu + NF, F, m.grd(m.lt(l, P_W3)), F, D, F},           // gW3 = h2^T . du
+                {ctx, D, gmid, D, m.grd(m.lt(l, P_WO)), D, D, D},              // gWo = ctx^T . gmid
+                {h, D, dqkv, D, m.grd(m.lt(l, P_WQ)), D, D, D},                // gWq = h^T . dq
+                {h, D, dqkv + ND, D, m.grd(m.lt(l, P_WQ)) + DD, D, D, D},      // gWk = h^T . dk
+                {h, D, dqkv + 2 * ND, D, m.grd(m.lt(l, P_WQ)) + 2 * DD, D, D, D},  // gWv = h^T . dv
+            };
+            LM_TRY(sgemm_grouped_tn(gw, 7, N, s2));
+        }
         // dh = dq.Wq^T + dk.Wk^T + dv.Wv^T (adjacent weights: one batch-reduce GEMM)
         LM_TRY(q.brgemm(1, N, D, D, 3, dqkv, D, ND, m.prm(m.lt(l, P_WQ)), D, static_cast<long long>(D) * D, m.dh, D));
         // dx_l = gmid + RMSNorm backward (ln1): runs with the next layer's first GEMM

@@ -262,10 +262,20 @@ rmsnorm_bwd_generic(const float* __restrict__ x, const float* __restrict__ w, co
 // dw[c] = (acc ? dw[c] : 0) + sum_b partial[b][c] in a fixed order: 64 columns
 // per block, 4 thread groups each summing every 4th partial row (independent,
 // unrolled loads), then the 4 group sums added in group order.  Deterministic.
+// blockIdx.y selects one of up to kColsumJobs independent (partial, out) jobs.
+struct ColsumJobs {
+    const float* partial[kColsumJobs];
+    float* out[kColsumJobs];
+    int nparts[kColsumJobs];
+};
+
 __global__ void __launch_bounds__(256)
-colsum_kernel(const float* __restrict__ partial, float* __restrict__ out, int nparts, int cols, int acc)
+colsum_kernel(const ColsumJobs jobs, int cols, int acc)
 {
     __shared__ float red[4][64];
+    const float* __restrict__ partial = jobs.partial[blockIdx.y];
+    float* __restrict__ out = jobs.out[blockIdx.y];
+    const int nparts = jobs.nparts[blockIdx.y];
     const int cl = threadIdx.x & 63, g = threadIdx.x >> 6;
     const int c = blockIdx.x * 64 + cl;
     float s = 0.f;
@@ -703,8 +713,25 @@ int rmsnorm_bwd_rows(const float* x, const float* w, const float* inv, const flo
 
 int rmsnorm_bwd_colsum(const float* partial, int parts, float* dw, int cols, int accumulate, hipStream_t s)
 {
-    if (parts <= 0) return LHIP_OK;
-    colsum_kernel<<<ceil_div(cols, 64), 256, 0, s>>>(partial, dw, parts, cols, accumulate);
+    return rmsnorm_bwd_colsum_multi(&partial, &parts, &dw, 1, cols, accumulate, s);
+}
+
+int rmsnorm_bwd_colsum_multi(const float* const* partials, const int* parts, float* const* dws, int njobs, int cols,
+                             int accumulate, hipStream_t s)
+{
+    if (njobs < 0 || njobs > kColsumJobs) return fail(LHIP_E_ARG, "colsum: %d jobs (at most %d)", njobs, kColsumJobs);
+    ColsumJobs jobs{};
+    int n = 0;
+    for (int i = 0; i < njobs; ++i) {
+        if (parts[i] <= 0) continue;
+        if (!partials[i] || !dws[i]) return fail(LHIP_E_NULL, "colsum: NULL partials/output");
+        jobs.partial[n] = partials[i];
+        jobs.out[n] = dws[i];
+        jobs.nparts[n] = parts[i];
+        ++n;
+    }
+    if (n == 0) return LHIP_OK;
+    colsum_kernel<<<dim3(ceil_div(cols, 64), n), 256, 0, s>>>(jobs, cols, accumulate);
     return check_launch("rmsnorm_bwd: dw reduce");
 }
 
