@@ -3,8 +3,9 @@
 
 Default workload ("C2"): one full LMTrain step --
 forward, cross-entropy, backward and the SGD update -- for vocab 2000, dim 128,
-4 layers, 8 heads, ffn 256, 8 windows x 64 tokens, resident on the GPU and
-replayed as a hipGraph.  Prints ONE JSON line: steps/s, a `roofline` object
+4 layers, 8 heads, ffn 256, 8 windows x 64 tokens, resident on the GPU,
+launched on the step stream and the weight-gradient stream (`--graph`:
+replayed from a captured hipGraph instead).  Prints ONE JSON line: steps/s, a `roofline` object
 for the step's dominant kernel (timed live with hipEvents on the library
 stream), and a `cpu_baseline` object (the CPU oracle -- a single-threaded C
 restatement of lanternl's pure-Lua loops in double -- timed on this host).
@@ -102,13 +103,28 @@ def cpu_baseline_gemm(n=512, reps=4):
 
 
 # ------------------------------------------------------------ LMTrain step (C2)
-# The step's dominant kernel at C2 (from the rocprofv3 kernel trace of this
-# workload): the tied-head backward GEMM dxf = dlogits . emb, an NN product of
-# [B*T, vocab] x [vocab, dim].  It is timed alone, with the step's shapes, on
-# the library stream.
+# The step's dominant kernel at C2 (largest share of kernel time in the
+# rocprofv3 trace of this workload, profiles/lmtrain_c2_step.md): the
+# batch-reduce NT GEMM of the backward, here in its dh2 form
+# dh2 = dz1 . W1^T + du . W3^T, [B*T, ffn] x [ffn, dim] twice into one
+# [B*T, dim] output.  It is timed alone, with the step's shapes and layout
+# (the two gradients and the two weights adjacent), with hipEvents on the
+# library stream it runs on.
 def dominant_kernel_c2(steps, warmup):
-    r = bench_gemm(C2["batch"] * C2["seq"], C2["dim"], C2["vocab"], steps=max(steps, 50), warmup=warmup)
-    return r
+    from lanternl_amd import device, kernels
+    rng = np.random.default_rng(5)
+    N, D, F = C2["batch"] * C2["seq"], C2["dim"], C2["ffn"]
+    dzu = device.Buffer.from_numpy(rng.standard_normal((2, N, F)).astype(np.float32))
+    w13 = device.Buffer.from_numpy((rng.standard_normal((2, D, F)) * 0.02).astype(np.float32))
+    out = device.Buffer((N, D))
+
+    def run(_):
+        kernels.sgemm_batched_reduce(0, 1, N, D, F, 1.0, dzu.ptr, F, N * F, w13.ptr, F, D * F, 0.0, out.ptr, D, 2)
+    ms = time_launches(run, max(steps, 50), warmup)
+    flops = 2.0 * N * D * (2 * F)
+    tflops = flops / (ms * 1e-3) / 1e12
+    return {"ms": ms, "tflops": tflops, "frac": tflops / PEAK_FP32_MFMA_TFLOPS, "m": N, "n": D, "k": 2 * F,
+            "flops": flops}
 
 
 def cpu_baseline_lm(nsteps=5):
@@ -160,7 +176,8 @@ def run_lm_workload(args):
         "last_step": {"loss": st["loss"], "grad_norm": st["grad_norm"], "applied": st["applied"]},
         "roofline": {"bound": "mfma", "achieved": dom["tflops"], "peak": PEAK_FP32_MFMA_TFLOPS,
                      "unit": "TFLOP/s", "frac": dom["frac"], "traffic": None,
-                     "kernel": f"sgemm NN {dom['m']}x{dom['n']}x{dom['k']} (tied-head dX = dlogits . emb)",
+                     "kernel": f"batch-reduce sgemm NT {dom['m']}x{dom['n']}x(2x{dom['k'] // 2}) "
+                               f"(dh2 = dz1 . W1^T + du . W3^T), {dom['flops']:.0f} flop per launch",
                      "kernel_ms": dom["ms"]},
         "cpu_baseline": cpu_baseline_lm(),
     }

@@ -119,6 +119,17 @@ LHIP_API int lhip_sgemm_strided_batched(int transa, int transb, int m, int n, in
                                         const float* A, int lda, long long strideA,
                                         const float* B, int ldb, long long strideB, float beta,
                                         float* C, int ldc, long long strideC, int batch);
+/* Batch-reduce: C = alpha * sum_{j<count} op(A + j*strideA) * op(B + j*strideB)
+ * + beta * C, one launch (the products share C and are summed before alpha).
+ * This is the accumulation the CPU backward performs one product at a time:
+ * grad_of(a) receives matrix.matmul_nt(g, b, grad, acc = true) from every
+ * consumer of a (ai/core/tensor2.lua:208-211,222-228), and the reference GPU
+ * path chains luaTL.matmul_dx with beta = 1 (ai/gpu/luaTL_train.lua:175-177),
+ * e.g. dX = dQ.Wq^T + dK.Wk^T + dV.Wv^T.  count >= 1; strides >= 0. */
+LHIP_API int lhip_sgemm_batched_reduce(int transa, int transb, int m, int n, int k, float alpha,
+                                       const float* A, int lda, long long strideA,
+                                       const float* B, int ldb, long long strideB, float beta,
+                                       float* C, int ldc, int count);
 
 /* Host-table GEMM for the flat-table backend contract (matrix.lua:178-202 ->
  * luatl_adapter.lua:128-135).  a, b, c are HOST double arrays, row-major:

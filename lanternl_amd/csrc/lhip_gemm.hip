@@ -933,6 +933,32 @@ LHIP_API int lhip_sgemm_strided_batched(int transa, int transb, int m, int n, in
                            batch);
 }
 
+LHIP_API int lhip_sgemm_batched_reduce(int transa, int transb, int m, int n, int k, float alpha,
+                                       const float* A, int lda, long long strideA,
+                                       const float* B, int ldb, long long strideB, float beta,
+                                       float* C, int ldc, int count)
+{
+    LHIP_REQUIRE_READY();
+    if (count <= 0) return fail(LHIP_E_ARG, "lhip_sgemm_batched_reduce: count %d must be >= 1", count);
+    if (count > 1 && (strideA < 0 || strideB < 0))
+        return fail(LHIP_E_SHAPE, "lhip_sgemm_batched_reduce: negative stride");
+    lhip::GemmOpts o;
+    o.kblocks = count;
+    o.sAk = strideA;
+    o.sBk = strideB;
+    const long long kall = static_cast<long long>(k) * count;
+    if (m > 0 && n > 0 && k > 0 && kall <= 0x7fffffffLL) {
+        int kchunk = 0;
+        const int splits = lhip::splitk_plan(m, n, static_cast<int>(kall), 1, static_cast<size_t>(1) << 26, &kchunk);
+        if (splits > 1) {
+            o.ws_floats = static_cast<size_t>(splits) * m * n;
+            int rc = lhip::workspace(o.ws_floats * sizeof(float), reinterpret_cast<void**>(&o.ws));
+            if (rc != LHIP_OK) return rc;
+        }
+    }
+    return lhip::sgemm_run(transa, transb, m, n, k, alpha, A, lda, 0, B, ldb, 0, beta, C, ldc, 0, 1, o, st().stream);
+}
+
 LHIP_API int lhip_matmul_host(int op, const double* a, const double* b, double* c,
                               int m, int k, int n, int acc)
 {

@@ -38,3 +38,9 @@ def sgemm_strided_batched(transa, transb, m, n, k, alpha, a_ptr, lda, sa, b_ptr,
                           beta, c_ptr, ldc, sc, batch):
     call("lhip_sgemm_strided_batched", int(bool(transa)), int(bool(transb)), m, n, k, float(alpha),
          a_ptr, lda, sa, b_ptr, ldb, sb, float(beta), c_ptr, ldc, sc, batch)
+
+
+def sgemm_batched_reduce(transa, transb, m, n, k, alpha, a_ptr, lda, sa, b_ptr, ldb, sb, beta, c_ptr, ldc, count):
+    """C = alpha * sum_j op(A_j) op(B_j) + beta * C over `count` strided operand pairs (raw pointers)."""
+    call("lhip_sgemm_batched_reduce", int(bool(transa)), int(bool(transb)), m, n, k, float(alpha),
+         a_ptr, lda, sa, b_ptr, ldb, sb, float(beta), c_ptr, ldc, count)

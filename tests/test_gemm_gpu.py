@@ -274,3 +274,55 @@ def test_gemm_split_k_alpha_beta_batched(m, n, k, batch):
     kernels.sgemm_strided_batched(0, 0, m, n, k, 0.5, A.ptr, k, m * k, B.ptr, n, k * n, -2.0, C2.ptr, n, m * n, batch)
     device.sync()
     assert np.array_equal(C2.download(), C.download())
+
+
+def _ref_op(x, t):
+    return x.T if t else x
+
+
+@pytest.mark.parametrize("ta,tb,m,n,k,count", [
+    (0, 1, 512, 128, 256, 2),     # C2 dh2 = dz1.W1^T + du.W3^T
+    (0, 1, 512, 128, 128, 3),     # C2 dh = dq.Wq^T + dk.Wk^T + dv.Wv^T
+    (0, 0, 37, 53, 40, 3),        # ragged tiles, NN
+    (0, 1, 45, 19, 10, 2),        # K not a multiple of 4: block by block
+    (1, 0, 64, 48, 32, 2),        # transposed A: block by block
+    (0, 0, 1024, 1024, 256, 2),   # large: the 128x128 kernel, block by block
+    (0, 1, 300, 200, 64, 1),      # count 1 = a plain GEMM
+])
+def test_gemm_batched_reduce_vs_oracle(ta, tb, m, n, k, count):
+    """lhip_sgemm_batched_reduce: C = alpha * sum_j op(A_j) op(B_j) + beta * C, checked
+    against the oracle's products summed in double (matrix.lua mm / matmul_nt /
+    matmul_tn with acc, the CPU backward's accumulation)."""
+    announce("gemm batch-reduce", ta, tb, m, n, k, count)
+    rng = np.random.default_rng(m * 7 + n + k + count)
+    a_shape = (k, m) if ta else (m, k)
+    b_shape = (n, k) if tb else (k, n)
+    a = f32(rng.uniform(-1, 1, (count,) + a_shape))
+    b = f32(rng.uniform(-1, 1, (count,) + b_shape))
+    c0 = f32(rng.uniform(-1, 1, (m, n)))
+    alpha, beta = 0.75, 0.5
+    A, B, C = to_dev(a), to_dev(b), to_dev(c0)
+    sa, sb = int(np.prod(a_shape)), int(np.prod(b_shape))
+    kernels.sgemm_batched_reduce(ta, tb, m, n, k, alpha, A.ptr, a_shape[1], sa, B.ptr, b_shape[1], sb, beta,
+                                 C.ptr, n, count)
+    device.sync()
+    got = C.download().astype(np.float64)
+    ref = beta * c0.astype(np.float64)
+    acc = np.zeros((m, n))
+    for j in range(count):
+        aj, bj = a[j].astype(np.float64), b[j].astype(np.float64)
+        if ta:
+            acc += O.matmul_tn(aj, bj) if not tb else _ref_op(aj, 1) @ _ref_op(bj, 1)
+        elif tb:
+            acc += O.matmul_nt(aj, bj)
+        else:
+            acc += O.mm(aj, bj)
+    ref += alpha * acc
+    assert rel_fro(got, ref) <= TOL
+
+
+def test_gemm_batched_reduce_rejects_bad_count():
+    from lanternl_amd._lib import LanternlHipError
+    A = device.Buffer((4, 4))
+    with pytest.raises(LanternlHipError):
+        kernels.sgemm_batched_reduce(0, 0, 4, 4, 4, 1.0, A.ptr, 4, 16, A.ptr, 4, 16, 0.0, A.ptr, 4, 0)
