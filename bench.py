@@ -110,6 +110,11 @@ def cpu_baseline_gemm(n=512, reps=4):
 # [B*T, dim] output.  It is timed alone, with the step's shapes and layout
 # (the two gradients and the two weights adjacent), with hipEvents on the
 # library stream it runs on.
+# HBM bytes per launch of that kernel from rocprofv3 FETCH_SIZE / WRITE_SIZE
+# (scaled by the copy-kernel calibration): profiles/sgemm_batched_reduce_dh2.md.
+DOMINANT_C2_TRAFFIC_BYTES = 3_564_544
+
+
 def dominant_kernel_c2(steps, warmup):
     from lanternl_amd import device, kernels
     rng = np.random.default_rng(5)
@@ -175,7 +180,7 @@ def run_lm_workload(args):
         "step_gemm_tflops": flops / (ms * 1e-3) / 1e12,
         "last_step": {"loss": st["loss"], "grad_norm": st["grad_norm"], "applied": st["applied"]},
         "roofline": {"bound": "mfma", "achieved": dom["tflops"], "peak": PEAK_FP32_MFMA_TFLOPS,
-                     "unit": "TFLOP/s", "frac": dom["frac"], "traffic": None,
+                     "unit": "TFLOP/s", "frac": dom["frac"], "traffic": DOMINANT_C2_TRAFFIC_BYTES,
                      "kernel": f"batch-reduce sgemm NT {dom['m']}x{dom['n']}x(2x{dom['k'] // 2}) "
                                f"(dh2 = dz1 . W1^T + du . W3^T), {dom['flops']:.0f} flop per launch",
                      "kernel_ms": dom["ms"]},
@@ -183,6 +188,11 @@ def run_lm_workload(args):
     }
     gpu.close()
     print(json.dumps(line), flush=True)
+
+
+# HBM bytes per 4096^3 NN launch from FETCH_SIZE / WRITE_SIZE with the copy
+# calibration: 809,225 KiB (profiles/sgemm_nn_4096.md).
+GEMM4096_TRAFFIC_BYTES = 809_225 * 1024
 
 
 def run_gemm_workload(args):
@@ -196,7 +206,7 @@ def run_gemm_workload(args):
         "data": "synthetic uniform[-1,1] seeded",
         "config": {"workload": "gemm_nn_4096^3 (config C5)", "m": 4096, "n": 4096, "k": 4096},
         "roofline": {"bound": "mfma", "achieved": r["tflops"], "peak": PEAK_FP32_MFMA_TFLOPS,
-                     "unit": "TFLOP/s", "frac": r["frac"], "traffic": None},
+                     "unit": "TFLOP/s", "frac": r["frac"], "traffic": GEMM4096_TRAFFIC_BYTES},
         "cpu_baseline": cpu_baseline_gemm(),
     }
     print(json.dumps(line), flush=True)
