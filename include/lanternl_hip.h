@@ -314,6 +314,52 @@ LHIP_API int lhip_lm_stats(void* model, lhip_lm_stats_t* out, float* window_loss
 /* Row argmax of the last step's logits (batch*seq int32). */
 LHIP_API int lhip_lm_get_argmax(void* model, int* host, int n);
 
+/* ---- LMTrain checkpoints (lmio v3) -------------------------------------------
+ * The checkpoint format of ai/optim/lmio.lua (tag line "lanternl-checkpoint 3",
+ * a key=value header, then every tensor of Transformer:parameters() as
+ * "<rows> <cols>\n" + raw little-endian fp32 (format bin) or
+ * "<rows> <cols>|v,v,...\n" with %.9g (format text); lmio.lua:5-13,226-313).
+ * Writes are atomic: "<path>.tmp<pid>" in the same directory, every write
+ * checked, the older files rotated (keep = K > 1: path.(K-1) removed,
+ * path.i -> path.(i+1), path -> path.1), then renamed over path
+ * (lmio.lua:127-135,320-368).  Reads take v3 and v2 (tagged) and v1 (untagged)
+ * files, bin or text, f32 or f64 values (lmio.lua:393-611), and check the
+ * model sizes, the tensor count and every tensor's shape.  The model is the
+ * tied-head RoPE transformer of lhip_lm_config_t; a checkpoint with pos other
+ * than rope or tie=0 is refused (LHIP_E_UNSUPPORTED). */
+typedef struct {
+    int format;          /* 0 = bin (lmio's default with ffi), 1 = text */
+    int keep;            /* keep_last rotation depth; <= 1 overwrites path only */
+    int epoch;           /* header epoch= */
+    double loss;         /* header loss= (%.9g; non-finite -> nan) */
+    double best_loss;    /* header best_loss= (%.9g; non-finite -> nan) */
+    const char* backend; /* header backend= (NULL -> "luatl_adapter") */
+    const char* extra;   /* appended to the header line as is (may be NULL) */
+} lhip_ckpt_info_t;
+
+typedef struct {
+    int version;         /* 1, 2 or 3 */
+    int format;          /* 0 bin, 1 text */
+    int dtype_bytes;     /* 4 (f32) or 8 (f64) */
+    int epoch;           /* -1 when absent */
+    double loss, best_loss;   /* NaN when absent or nan */
+    int causal, tie, max_seq; /* -1 when absent */
+    double rope_base;    /* NaN when absent */
+} lhip_ckpt_header_t;
+
+/* Host-side save/load of a flat parameter vector of lhip_lm_num_params(cfg)
+ * values (no device involved; the LMTrain:_write_checkpoint / LMTrain:load
+ * counterparts, lmio.lua:315-368,393-611).  cfg->seq is written as max_seq. */
+LHIP_API int lhip_ckpt_save_host(const char* path, const lhip_lm_config_t* cfg, const lhip_ckpt_info_t* info,
+                                 const float* params, long long n);
+LHIP_API int lhip_ckpt_load_host(const char* path, const lhip_lm_config_t* cfg, float* params, long long n,
+                                 lhip_ckpt_header_t* header);
+/* The same for a device model, streamed through a fixed pinned buffer (the GPU
+ * path's _param_get/_param_set hooks, lmio.lua:186-211, lmtrain_gpu.lua:46-59).
+ * A failed load may leave the parameters partly replaced, as LMTrain:load does. */
+LHIP_API int lhip_lm_save(void* model, const char* path, const lhip_ckpt_info_t* info);
+LHIP_API int lhip_lm_load(void* model, const char* path, lhip_ckpt_header_t* header);
+
 #ifdef __cplusplus
 }
 #endif

@@ -95,6 +95,21 @@ class LmStats(ctypes.Structure):
                 ("correct", ctypes.c_int), ("steps", ctypes.c_int)]
 
 
+class CkptInfo(ctypes.Structure):
+    """lhip_ckpt_info_t"""
+    _fields_ = [("format", ctypes.c_int), ("keep", ctypes.c_int), ("epoch", ctypes.c_int),
+                ("loss", ctypes.c_double), ("best_loss", ctypes.c_double),
+                ("backend", ctypes.c_char_p), ("extra", ctypes.c_char_p)]
+
+
+class CkptHeader(ctypes.Structure):
+    """lhip_ckpt_header_t"""
+    _fields_ = [("version", ctypes.c_int), ("format", ctypes.c_int), ("dtype_bytes", ctypes.c_int),
+                ("epoch", ctypes.c_int), ("loss", ctypes.c_double), ("best_loss", ctypes.c_double),
+                ("causal", ctypes.c_int), ("tie", ctypes.c_int), ("max_seq", ctypes.c_int),
+                ("rope_base", ctypes.c_double)]
+
+
 _cfgp = ctypes.POINTER(LmConfig)
 SIGNATURES.update({
     "lhip_lm_num_params": (_ll, [_cfgp]),
@@ -114,6 +129,10 @@ SIGNATURES.update({
     "lhip_lm_get_adam_state": (_i, [_p, _p, _p, _ll, _p]),
     "lhip_lm_stats": (_i, [_p, ctypes.POINTER(LmStats), _p, _i]),
     "lhip_lm_get_argmax": (_i, [_p, _p, _i]),
+    "lhip_ckpt_save_host": (_i, [ctypes.c_char_p, _cfgp, ctypes.POINTER(CkptInfo), _p, _ll]),
+    "lhip_ckpt_load_host": (_i, [ctypes.c_char_p, _cfgp, _p, _ll, ctypes.POINTER(CkptHeader)]),
+    "lhip_lm_save": (_i, [_p, ctypes.c_char_p, ctypes.POINTER(CkptInfo)]),
+    "lhip_lm_load": (_i, [_p, ctypes.c_char_p, ctypes.POINTER(CkptHeader)]),
 })
 
 _lib = None

@@ -167,6 +167,10 @@ struct FuseCall {
 };
 bool lm_fuse_ok(int K, int lda, int ldb_nt);
 int lm_fused_gemm(const FuseCall& c, hipStream_t s);
+// Checkpoint save (save = true) or load of a device parameter vector laid out
+// for cfg, through one pinned staging buffer.
+int lm_checkpoint_io(const lhip_lm_config_t& cfg, float* dev_params, const char* path, const lhip_ckpt_info_t* info,
+                     lhip_ckpt_header_t* header, bool save);
 // Fused per-(window, head) attention of the LMTrain step (T <= 64, head_dim <= 64, even).
 bool attn_fused_ok(int T, int hd);
 int attn_fwd(const float* qkv, const float2* cs, float* P, float* ctx, int B, int H, int T, int hd, float scale,

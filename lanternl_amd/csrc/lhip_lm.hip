@@ -798,6 +798,22 @@ LHIP_API int lhip_lm_step_adamw(void* model, float lr, float beta1, float beta2,
     return lhip::run_step(*m, hp);
 }
 
+LHIP_API int lhip_lm_save(void* model, const char* path, const lhip_ckpt_info_t* info)
+{
+    LHIP_REQUIRE_READY();
+    if (!model) return fail(LHIP_E_NULL, "lhip_lm_save: model is NULL");
+    auto* m = lhip::as_model(model);
+    return lhip::lm_checkpoint_io(m->c, m->params, path, info, nullptr, true);
+}
+
+LHIP_API int lhip_lm_load(void* model, const char* path, lhip_ckpt_header_t* header)
+{
+    LHIP_REQUIRE_READY();
+    if (!model) return fail(LHIP_E_NULL, "lhip_lm_load: model is NULL");
+    auto* m = lhip::as_model(model);
+    return lhip::lm_checkpoint_io(m->c, m->params, path, nullptr, header, false);
+}
+
 LHIP_API int lhip_lm_set_adam_state(void* model, const float* mom, const float* var, long long n, int step)
 {
     LHIP_REQUIRE_READY();

@@ -1,12 +1,14 @@
-"""The CPU LMTrain step (optimizer "sgd") run on the GPU through lhip_lm_*.
+"""The CPU LMTrain step (optimizer "sgd" or "adamw") run on the GPU through lhip_lm_*.
 
 Host-side mirror of the parts of ai/optim/lmtrain.lua that feed one optimizer
 step: ``build_windows`` (lmtrain.lua:535-558) cuts token sequences into
-(input, target) windows, and ``GpuLMStep.step`` runs the batch body of
-LMTrain:run (lmtrain.lua:1183-1227) for ``batch`` windows: forward, mean CE
-per window, backward, grads scaled by 1/batch, global-norm skip and clip, and
-the SGD update (optim2.lua:48-102), all on the device.  Ids are 0-based here
-(Lua's are 1-based).
+(input, target) windows, and ``GpuLMStep.step`` / ``step_adamw`` run the batch
+body of LMTrain:run (lmtrain.lua:1183-1227) for ``batch`` windows: forward,
+mean CE per window, backward, grads scaled by 1/batch, global-norm skip and
+clip, and the SGD (optim2.lua:48-102) or AdamW (optim2.lua:104-164) update,
+all on the device.  ``save_checkpoint`` / ``load_checkpoint`` and
+``GpuLMStep.save`` / ``load`` read and write the lmio v3 checkpoint format
+(ai/optim/lmio.lua).  Ids are 0-based here (Lua's are 1-based).
 
 Windows must be full (``seq`` tokens each); the reference's shorter trailing
 window of a sequence is not supported by the device step.
@@ -71,6 +73,40 @@ def init_params(cfg, rng, std=0.02):
         else:
             p[off:off + r * c] = rng.normal(0.0, std, r * c)
     return p
+
+
+def _ckpt_info(fmt="bin", keep=1, epoch=0, loss=float("nan"), best_loss=float("nan"), backend=None, extra=None):
+    from ._lib import CkptInfo
+    if fmt not in ("bin", "text"):
+        raise ValueError("format must be 'bin' or 'text'")
+    return CkptInfo(0 if fmt == "bin" else 1, int(keep), int(epoch), float(loss), float(best_loss),
+                    backend.encode() if backend else None, extra.encode() if extra else None)
+
+
+def _ckpt_header_dict(h):
+    return {"version": h.version, "format": "bin" if h.format == 0 else "text",
+            "dtype": "f32" if h.dtype_bytes == 4 else "f64", "epoch": h.epoch, "loss": h.loss,
+            "best_loss": h.best_loss, "causal": h.causal, "tie": h.tie, "max_seq": h.max_seq,
+            "rope_base": h.rope_base}
+
+
+def save_checkpoint(path, cfg, params, **info):
+    """Write the flat parameter vector in the lmio v3 checkpoint format
+    (ai/optim/lmio.lua; host side, no device).  info: fmt ('bin'|'text'), keep,
+    epoch, loss, best_loss, backend, extra."""
+    p = np.ascontiguousarray(params, dtype=np.float32).reshape(-1)
+    ci = _ckpt_info(**info)
+    call("lhip_ckpt_save_host", str(path).encode(), ctypes.byref(cfg), ctypes.byref(ci), p.ctypes.data, p.size)
+
+
+def load_checkpoint(path, cfg):
+    """Read an lmio checkpoint (v1/v2/v3, bin/text, f32/f64) into a flat fp32
+    vector for cfg; returns (params, header dict)."""
+    from ._lib import CkptHeader
+    out = np.empty(num_params(cfg), dtype=np.float32)
+    h = CkptHeader()
+    call("lhip_ckpt_load_host", str(path).encode(), ctypes.byref(cfg), out.ctypes.data, out.size, ctypes.byref(h))
+    return out, _ckpt_header_dict(h)
 
 
 class GpuLMStep:
@@ -144,6 +180,18 @@ class GpuLMStep:
             arrs.append(a)
         call("lhip_lm_set_adam_state", self._h, None if arrs[0] is None else arrs[0].ctypes.data,
              None if arrs[1] is None else arrs[1].ctypes.data, self.n, int(step))
+
+    def save(self, path, **info):
+        """Checkpoint the device parameters (lmio v3; see save_checkpoint for info)."""
+        ci = _ckpt_info(**info)
+        call("lhip_lm_save", self._h, str(path).encode(), ctypes.byref(ci))
+
+    def load(self, path):
+        """Load a checkpoint into the device parameters; returns its header dict."""
+        from ._lib import CkptHeader
+        h = CkptHeader()
+        call("lhip_lm_load", self._h, str(path).encode(), ctypes.byref(h))
+        return _ckpt_header_dict(h)
 
     def adam_state(self):
         """(m, v, step) of the AdamW optimizer."""

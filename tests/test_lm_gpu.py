@@ -315,3 +315,32 @@ def test_lm_adamw_graph_matches_eager_and_state_round_trip():
     m2, v2, t2 = a.adam_state()
     assert t2 == 7 and np.array_equal(m2, m) and np.array_equal(v2, v)
     a.close(); b.close()
+
+
+def test_lm_checkpoint_save_load_device(tmp_path):
+    """lhip_lm_save streams the device parameters into an lmio v3 file identical
+    to the host writer's; lhip_lm_load puts them back, and a step from the
+    loaded model equals a step from set_params."""
+    announce("lm checkpoint")
+    V, D, L, H, F, B, T = 64, 32, 2, 4, 64, 2, 16
+    rng = np.random.default_rng(31)
+    a = lmtrain.GpuLMStep(V, D, L, H, F, B, T)
+    p = lmtrain.init_params(a.cfg, rng, 0.1)
+    a.set_params(p)
+    for fmt in ("bin", "text"):
+        path = tmp_path / f"dev.{fmt}"
+        a.save(path, fmt=fmt, epoch=3, loss=1.5)
+        ref = tmp_path / f"host.{fmt}"
+        lmtrain.save_checkpoint(ref, a.cfg, p, fmt=fmt, epoch=3, loss=1.5)
+        assert path.read_bytes() == ref.read_bytes()
+    b = lmtrain.GpuLMStep(V, D, L, H, F, B, T)
+    hdr = b.load(tmp_path / "dev.bin")
+    assert hdr["epoch"] == 3 and hdr["loss"] == 1.5
+    assert np.array_equal(b.params(), p)
+    ids = rng.integers(0, V, (B, T)); tgt = rng.integers(0, V, (B, T))
+    a.set_batch(ids, tgt); b.set_batch(ids, tgt)
+    a.step(0.05); b.step(0.05)
+    assert np.array_equal(a.params(), b.params())
+    with pytest.raises(Exception):
+        lmtrain.GpuLMStep(V, 48, L, H, F, B, T).load(tmp_path / "dev.bin")
+    a.close(); b.close()
