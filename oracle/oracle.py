@@ -103,8 +103,9 @@ def mm(a, b, out=None, acc=False):
     """matrix.multiply CPU path (matrix.lua:514-539): a (m,k) . b (k,n)."""
     a, pa = _d(a); b, pb = _d(b)
     m, k = a.shape; n = b.shape[1]
+    assert b.shape[0] == k, (a.shape, b.shape)
     r = np.zeros((m, n)) if out is None else out
-    assert r.dtype == np.float64 and r.flags.c_contiguous
+    assert r.dtype == np.float64 and r.flags.c_contiguous and r.shape == (m, n)
     lib().or_mm(pa, pb, r.ctypes.data_as(_D), m, k, n, int(acc))
     return r
 
@@ -113,7 +114,9 @@ def matmul_nt(a, b, out=None, acc=False):
     """matrix.matmul_nt (matrix.lua:597-625): a (m,k) . b(n,k)^T."""
     a, pa = _d(a); b, pb = _d(b)
     m, k = a.shape; n = b.shape[0]
+    assert b.shape[1] == k, (a.shape, b.shape)
     r = np.zeros((m, n)) if out is None else out
+    assert r.dtype == np.float64 and r.flags.c_contiguous and r.shape == (m, n)
     lib().or_matmul_nt(pa, pb, r.ctypes.data_as(_D), m, k, n, int(acc))
     return r
 
@@ -122,7 +125,9 @@ def matmul_tn(a, b, out=None, acc=False):
     """matrix.matmul_tn (matrix.lua:627-660): a (m,k)^T . b (m,n) -> (k,n)."""
     a, pa = _d(a); b, pb = _d(b)
     m, k = a.shape; n = b.shape[1]
+    assert b.shape[0] == m, (a.shape, b.shape)
     r = np.zeros((k, n)) if out is None else out
+    assert r.dtype == np.float64 and r.flags.c_contiguous and r.shape == (k, n)
     lib().or_matmul_tn(pa, pb, r.ctypes.data_as(_D), m, k, n, int(acc))
     return r
 

@@ -68,7 +68,8 @@ def test_mm_zero_skip_semantics():
     # matrix.lua:521,530,650: a==0 terms are skipped, so 0*inf never makes NaN
     a = np.array([[0.0, 1.0]]); b = np.array([[np.inf], [2.0]])
     assert O.mm(a, b)[0, 0] == 2.0
-    assert O.matmul_tn(np.ascontiguousarray(a.T), np.array([[np.inf, 1.0]]))[0, 0] == 0.0
+    # matmul_tn: a^T (1x2) . b (2x1) with a[0] = 0 facing b[0] = inf -> the term is skipped
+    assert O.matmul_tn(np.ascontiguousarray(a.T), np.array([[np.inf], [0.0]]))[0, 0] == 0.0
     # matmul_nt has no skip: 0*inf is NaN (matrix.lua:617-619)
     assert np.isnan(O.matmul_nt(a, np.array([[np.inf, 2.0]]))[0, 0])
     # inf propagates through a non-zero term (tests/core_test.lua:95-100 intent)
