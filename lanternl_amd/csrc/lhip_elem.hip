@@ -206,42 +206,81 @@ rope_kernel(float* __restrict__ x, const int* __restrict__ pos_ids, int rows, in
     const int pairs = hd >> 1;
     const int r0 = blockIdx.x * kRopeRowsPerBlock;
     const int nr = min(kRopeRowsPerBlock, rows - r0);
-    for (int i = threadIdx.x; i < nr * pairs; i += blockDim.x) {
-        const int rr = i / pairs, p = i % pairs;
-        const int r = r0 + rr;
-        const int pos = pos_ids ? pos_ids[r] : (period > 0 ? r % period : r) + pos_offset;
-        const double ang = static_cast<double>(pos) * fr.inv[p];
-        double s, c;
-        sincos(ang, &s, &c);
-        tab[rr * kRopeMaxPairs + p] = make_float2(static_cast<float>(c), static_cast<float>(inverse ? -s : s));
-    }
-    __syncthreads();
+    auto make_table = [&]() {
+        for (int i = threadIdx.x; i < nr * pairs; i += blockDim.x) {
+            const int rr = i / pairs, p = i % pairs;
+            const int r = r0 + rr;
+            const int pos = pos_ids ? pos_ids[r] : (period > 0 ? r % period : r) + pos_offset;
+            const double ang = static_cast<double>(pos) * fr.inv[p];
+            double sn, cs;
+            sincos(ang, &sn, &cs);
+            tab[rr * kRopeMaxPairs + p] = make_float2(static_cast<float>(cs), static_cast<float>(inverse ? -sn : sn));
+        }
+        __syncthreads();
+    };
     if (vec) {
-        // unit = two adjacent pairs: one float4 (interleaved) or two float2 (half-split)
+        // unit = two adjacent pairs: one float4 (interleaved) or two float2
+        // (half-split).  A thread takes kU units per batch: all of the batch's
+        // loads are issued first (the first batch's before the angle table is
+        // computed, so the two overlap), then rotated and stored.
+        constexpr int kU = 8;
         const int units_per_head = pairs >> 1;
-        const int units = nr * heads * units_per_head;
+        const int per_row = heads * units_per_head;
+        const int units = nr * per_row;
         const int half = pairs;
-        for (int i = threadIdx.x; i < units; i += blockDim.x) {
-            const int rr = i / (heads * units_per_head);
-            const int rem = i % (heads * units_per_head);
-            const int h = rem / units_per_head, q = rem % units_per_head;
-            const int p = 2 * q;
-            float* base = x + static_cast<long long>(r0 + rr) * row_stride + static_cast<long long>(h) * hd;
-            const float2 cs0 = tab[rr * kRopeMaxPairs + p], cs1 = tab[rr * kRopeMaxPairs + p + 1];
-            if (interleaved) {
-                float4* v4 = reinterpret_cast<float4*>(base + 2 * p);
-                const float4 v = *v4;
-                *v4 = make_float4(v.x * cs0.x - v.y * cs0.y, v.y * cs0.x + v.x * cs0.y,
-                                  v.z * cs1.x - v.w * cs1.y, v.w * cs1.x + v.z * cs1.y);
-            } else {
-                float2* a2 = reinterpret_cast<float2*>(base + p);
-                float2* b2 = reinterpret_cast<float2*>(base + p + half);
-                const float2 a = *a2, b = *b2;
-                *a2 = make_float2(a.x * cs0.x - b.x * cs0.y, a.y * cs1.x - b.y * cs1.y);
-                *b2 = make_float2(b.x * cs0.x + a.x * cs0.y, b.y * cs1.x + a.y * cs1.y);
+        float4 v[kU];
+        float* ptr[kU];
+        int slot[kU];
+        auto load = [&](int i0) {
+#pragma unroll
+            for (int u = 0; u < kU; ++u) {
+                const int i = i0 + u * static_cast<int>(blockDim.x);
+                ptr[u] = nullptr;
+                if (i < units) {
+                    const int rr = i / per_row, rem = i - rr * per_row;
+                    const int h = rem / units_per_head, p = 2 * (rem - h * units_per_head);
+                    float* base = x + static_cast<long long>(r0 + rr) * row_stride + static_cast<long long>(h) * hd;
+                    slot[u] = rr * kRopeMaxPairs + p;
+                    if (interleaved) {
+                        ptr[u] = base + 2 * p;
+                        v[u] = *reinterpret_cast<const float4*>(ptr[u]);
+                    } else {
+                        ptr[u] = base + p;
+                        const float2 a = *reinterpret_cast<const float2*>(ptr[u]);
+                        const float2 b = *reinterpret_cast<const float2*>(ptr[u] + half);
+                        v[u] = make_float4(a.x, a.y, b.x, b.y);
+                    }
+                }
             }
+        };
+        auto rotate_store = [&]() {
+#pragma unroll
+            for (int u = 0; u < kU; ++u) {
+                if (!ptr[u]) continue;
+                const float2 c0 = tab[slot[u]], c1 = tab[slot[u] + 1];
+                const float4 t = v[u];
+                if (interleaved) {
+                    *reinterpret_cast<float4*>(ptr[u]) =
+                        make_float4(t.x * c0.x - t.y * c0.y, t.y * c0.x + t.x * c0.y, t.z * c1.x - t.w * c1.y,
+                                    t.w * c1.x + t.z * c1.y);
+                } else {
+                    // t = (a0, a1, b0, b1): pairs (a0, b0) at p and (a1, b1) at p + 1
+                    *reinterpret_cast<float2*>(ptr[u]) = make_float2(t.x * c0.x - t.z * c0.y, t.y * c1.x - t.w * c1.y);
+                    *reinterpret_cast<float2*>(ptr[u] + half) =
+                        make_float2(t.z * c0.x + t.x * c0.y, t.w * c1.x + t.y * c1.y);
+                }
+            }
+        };
+        const int step = kU * static_cast<int>(blockDim.x);
+        load(threadIdx.x);
+        make_table();
+        rotate_store();
+        for (int i0 = threadIdx.x + step; i0 < units; i0 += step) {
+            load(i0);
+            rotate_store();
         }
     } else {
+        make_table();
         const int units = nr * heads * pairs;
         for (int i = threadIdx.x; i < units; i += blockDim.x) {
             const int rr = i / (heads * pairs);

@@ -171,22 +171,27 @@ rmsnorm_bwd_vec(const float* __restrict__ x, const float* __restrict__ w, const 
         dwp[i] = f4zero();
     }
     const float inv_n = 1.0f / static_cast<float>(cols);
-    for (int row = blockIdx.x * kWavesPerBlock + wv; row < rows; row += gridDim.x * kWavesPerBlock) {
+    // rows walked with a one-row prefetch of x and dy (walk_rows)
+    auto load = [&](Row2<NV>& rr, int row) {
         const size_t base = static_cast<size_t>(row) * cols;
         const float4* xr = reinterpret_cast<const float4*>(x + base);
         const float4* gr = reinterpret_cast<const float4*>(dy + base);
-        float4 xv[NV], gv[NV];
-        float dot = 0.f;
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const int c = lane + 64 * i;
-            xv[i] = c < c4n ? xr[c] : f4zero();
-            gv[i] = c < c4n ? gr[c] : f4zero();
-            dot += gv[i].x * wr[i].x * xv[i].x + gv[i].y * wr[i].y * xv[i].y +
-                   gv[i].z * wr[i].z * xv[i].z + gv[i].w * wr[i].w * xv[i].w;
+            rr.v[i] = c < c4n ? ld_stream(xr + c) : f4zero();
+            rr.g[i] = c < c4n ? ld_stream(gr + c) : f4zero();
         }
-        dot = wave_sum(dot);
+    };
+    auto body = [&](const Row2<NV>& rr, int row) {
+        const size_t base = static_cast<size_t>(row) * cols;
         const float r = inv[row];
+        float dot = 0.f;
+#pragma unroll
+        for (int i = 0; i < NV; ++i)
+            dot += rr.g[i].x * wr[i].x * rr.v[i].x + rr.g[i].y * wr[i].y * rr.v[i].y +
+                   rr.g[i].z * wr[i].z * rr.v[i].z + rr.g[i].w * wr[i].w * rr.v[i].w;
+        dot = wave_sum(dot);
         const float coef = dot * r * r * r * inv_n;
         float4* dxr = reinterpret_cast<float4*>(dx + base);
         const float4* drr = reinterpret_cast<const float4*>(dres + base);
@@ -197,7 +202,7 @@ rmsnorm_bwd_vec(const float* __restrict__ x, const float* __restrict__ w, const 
                 float4 o;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const float gg = f4get(gv[i], e), xx = f4get(xv[i], e);
+                    const float gg = f4get(rr.g[i], e), xx = f4get(rr.v[i], e);
                     f4set(o, e, gg * f4get(wr[i], e) * r - xx * coef);
                     f4set(dwp[i], e, f4get(dwp[i], e) + gg * xx * r);
                 }
@@ -208,7 +213,8 @@ rmsnorm_bwd_vec(const float* __restrict__ x, const float* __restrict__ w, const 
                 dxr[c] = o;
             }
         }
-    }
+    };
+    walk_rows<Row2<NV>>(rows, load, body);
     if (!partial) return;   // uniform: no dw wanted
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
@@ -259,9 +265,9 @@ rmsnorm_bwd_generic(const float* __restrict__ x, const float* __restrict__ w, co
     }
 }
 
-// dw[c] = (acc ? dw[c] : 0) + sum_b partial[b][c] in a fixed order: 64 columns
-// per block, 4 thread groups each summing every 4th partial row (independent,
-// unrolled loads), then the 4 group sums added in group order.  Deterministic.
+// dw[c] = (acc ? dw[c] : 0) + sum_b partial[b][c] in a fixed order: 32 columns
+// per block, 8 thread groups each summing every 8th partial row (independent,
+// unrolled loads), then the 8 group sums added in a fixed tree.  Deterministic.
 // blockIdx.y selects one of up to kColsumJobs independent (partial, out) jobs.
 struct ColsumJobs {
     const float* partial[kColsumJobs];
@@ -272,21 +278,23 @@ struct ColsumJobs {
 __global__ void __launch_bounds__(256)
 colsum_kernel(const ColsumJobs jobs, int cols, int acc)
 {
-    __shared__ float red[4][64];
+    // 32 columns per block, 8 thread groups each summing every 8th partial row
+    __shared__ float red[8][32];
     const float* __restrict__ partial = jobs.partial[blockIdx.y];
     float* __restrict__ out = jobs.out[blockIdx.y];
     const int nparts = jobs.nparts[blockIdx.y];
-    const int cl = threadIdx.x & 63, g = threadIdx.x >> 6;
-    const int c = blockIdx.x * 64 + cl;
+    const int cl = threadIdx.x & 31, g = threadIdx.x >> 5;
+    const int c = blockIdx.x * 32 + cl;
     float s = 0.f;
     if (c < cols) {
 #pragma unroll 8
-        for (int b = g; b < nparts; b += 4) s += partial[static_cast<size_t>(b) * cols + c];
+        for (int b = g; b < nparts; b += 8) s += partial[static_cast<size_t>(b) * cols + c];
     }
     red[g][cl] = s;
     __syncthreads();
     if (g == 0 && c < cols) {
-        const float t = (red[0][cl] + red[1][cl]) + (red[2][cl] + red[3][cl]);
+        const float t = ((red[0][cl] + red[1][cl]) + (red[2][cl] + red[3][cl])) +
+                        ((red[4][cl] + red[5][cl]) + (red[6][cl] + red[7][cl]));
         out[c] = acc ? out[c] + t : t;
     }
 }
@@ -667,6 +675,8 @@ int rmsnorm_fwd(const float* x, const float* w, float* y, float* inv, int rows, 
 // Workgroups of the backward: each wave walks >= 4 rows, at most one block per CU.
 int rmsnorm_bwd_blocks(int rows)
 {
+    // about 4 rows per wave, walked with a one-row prefetch; one block per CU
+    // at most, which bounds the dw partial rows (one per block) to the CUs
     const int cus = st().cu_count > 0 ? st().cu_count : 256;
     int blocks = ceil_div(rows, 4 * kWavesPerBlock);
     if (blocks > cus) blocks = cus;
@@ -731,7 +741,7 @@ int rmsnorm_bwd_colsum_multi(const float* const* partials, const int* parts, flo
         ++n;
     }
     if (n == 0) return LHIP_OK;
-    colsum_kernel<<<dim3(ceil_div(cols, 64), n), 256, 0, s>>>(jobs, cols, accumulate);
+    colsum_kernel<<<dim3(ceil_div(cols, 32), n), 256, 0, s>>>(jobs, cols, accumulate);
     return check_launch("rmsnorm_bwd: dw reduce");
 }
 
