@@ -29,6 +29,7 @@
 // checked stores; unaligned operands (ld % 4 != 0 or a base not 16-byte
 // aligned) always take the scalar path.
 #include <algorithm>
+#include <type_traits>
 
 #include "lhip_internal.h"
 
@@ -292,6 +293,218 @@ sgemm_mfma_kernel(const GemmArgs g)
                 }
             }
         }
+}
+
+// ---------------------------------------------------------------------------
+// Large problems (at least one 256x256 tile per CU): 256x256 output tiles,
+// four waves of 128x128 (16 v_mfma_f32_32x32x2f32 accumulators each, 256
+// AGPRs, one wave per SIMD), 16-deep K tiles double-buffered in LDS.
+//
+// Both LDS tiles are k-contiguous: As[m][k], Bs[n][k] with a row stride of
+// kLd256 = 20 floats.  For an 8-deep K step at k0, lane l (row or column
+// r = l%32 of a 32-block, half h = l/32) fetches op(A)[r][k0+4h .. k0+4h+3]
+// and op(B)[k0+4h .. +3][c] with one ds_read_b128 each; MFMA t of the step
+// multiplies element t of both, so its two k slots are k0+t and k0+4+t and the
+// four MFMAs cover k0 .. k0+7 once.  A wave thus reads 8 b128 per 64 MFMAs.
+// A row stride of 20 floats puts 8 consecutive rows (one 8-lane phase of a
+// b128 access) on 8 distinct 4-bank groups, so those reads are conflict-free.
+//
+// Global -> LDS: an operand stored with k contiguous (A when !TA, B when TB)
+// is read as float4 along k and written with ds_write_b128; an operand stored
+// K-major (A when TA, B when !TB) is read as four scalars from four
+// consecutive k-rows (each instruction 64 consecutive floats of one row),
+// gathered per lane into one float4 and written with one ds_write_b128 --
+// conflict-free for 8 consecutive columns, like the reads.
+__device__ __forceinline__ float f4get(const float4& v, int t)
+{
+    return t == 0 ? v.x : t == 1 ? v.y : t == 2 ? v.z : v.w;   // t is a compile-time constant after unrolling
+}
+
+constexpr int kBig = 256;
+constexpr int kBigK = 16;
+constexpr int kLd256 = 20;
+
+template <bool KMAJOR, bool FULL>
+struct BigTileRegs {
+    // 256 rows (m or n) x 16 k of one operand: 16 floats per thread
+    float4 v[4];
+
+    // stored: element (row, k) at X[row * ld + k] (!KMAJOR) or X[k * ld + row] (KMAJOR)
+    __device__ __forceinline__ void load(const float* __restrict__ X, int ld, int r0, int k0, int rmax, int kmax,
+                                         bool vec, int tid)
+    {
+        if (!KMAJOR) {
+            const int k4 = tid & 3;
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const int row = (tid >> 2) + 64 * p;
+                const int gr = r0 + row, gk = k0 + 4 * k4;
+                const float* src = X + static_cast<long long>(gr) * ld + gk;
+                if (FULL || (vec && gr < rmax && gk + 3 < kmax)) {
+                    const float4 t = *reinterpret_cast<const float4*>(src);
+                    v[p].x = t.x; v[p].y = t.y; v[p].z = t.z; v[p].w = t.w;   // per component: stays in VGPRs
+                } else {
+                    const bool rok = gr < rmax;
+                    v[p].x = (rok && gk + 0 < kmax) ? src[0] : 0.f;
+                    v[p].y = (rok && gk + 1 < kmax) ? src[1] : 0.f;
+                    v[p].z = (rok && gk + 2 < kmax) ? src[2] : 0.f;
+                    v[p].w = (rok && gk + 3 < kmax) ? src[3] : 0.f;
+                }
+            }
+        } else {
+            const int q = tid >> 6;            // k quad 0..3
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int row = (tid & 63) + 64 * e;
+                const int gr = r0 + row;
+                float t[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int gk = k0 + 4 * q + i;
+                    t[i] = (FULL || (gr < rmax && gk < kmax)) ? X[static_cast<long long>(gk) * ld + gr] : 0.f;
+                }
+                v[e] = make_float4(t[0], t[1], t[2], t[3]);
+            }
+        }
+    }
+
+    __device__ __forceinline__ void store(float* lds, int tid) const
+    {
+        if (!KMAJOR) {
+            const int k4 = tid & 3;
+#pragma unroll
+            for (int p = 0; p < 4; ++p)
+                *reinterpret_cast<float4*>(lds + ((tid >> 2) + 64 * p) * kLd256 + 4 * k4) = v[p];
+        } else {
+            const int q = tid >> 6;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                *reinterpret_cast<float4*>(lds + ((tid & 63) + 64 * e) * kLd256 + 4 * q) = v[e];
+        }
+    }
+};
+
+// FULL: M and N multiples of 256, K of 16, k-contiguous operands 16-byte
+// aligned -- every tile load is in bounds and unconditional.
+template <bool TA, bool TB, bool FULL>
+__global__ void __launch_bounds__(kThreads)
+sgemm_256_kernel(const GemmArgs g)
+{
+    __shared__ float As[2][kBig * kLd256];
+    __shared__ float Bs[2][kBig * kLd256];
+    const int M = g.M, N = g.N;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int lr = lane & 31;
+    const int h = lane >> 5;
+    int tm, tn;
+    tile_coords(blockIdx.x, gridDim.x, g.tiles_m, g.tiles_n, tm, tn);
+    const int m0 = tm * kBig, n0 = tn * kBig;
+    const long long zo = blockIdx.y / g.inner, zi = blockIdx.y % g.inner;
+    const float* __restrict__ A = g.A + zo * g.sA2 + zi * g.sA;
+    const float* __restrict__ B = g.B + zo * g.sB2 + zi * g.sB;
+    const long long coff = zo * g.sC2 + zi * g.sC;
+    const int wm = (wave >> 1) * 128, wn = (wave & 1) * 128;
+
+    BigTileRegs<TA, FULL> ra;    // op(A): row m; stored M x K (!TA) or K x M (TA)
+    BigTileRegs<!TB, FULL> rb;   // op(B): row n; stored N x K (TB) or K x N (!TB)
+    const int K = g.K;
+    auto gload = [&](int k0) {
+        ra.load(A, g.lda, m0, k0, M, K, g.vecA, tid);
+        rb.load(B, g.ldb, n0, k0, N, K, g.vecB, tid);
+    };
+    auto lstore = [&](int buf) {
+        ra.store(As[buf], tid);
+        rb.store(Bs[buf], tid);
+    };
+
+    floatx16 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    const int nk = (K + kBigK - 1) / kBigK;
+    if (nk > 0) {
+        gload(0);
+        lstore(0);
+        __syncthreads();
+    }
+    for (int kt = 0; kt < nk; ++kt) {
+        const int cur = kt & 1;
+        const bool more = kt + 1 < nk;
+        if (more) gload((kt + 1) * kBigK);
+        const float* as = As[cur] + (wm + lr) * kLd256 + 4 * h;
+        const float* bs = Bs[cur] + (wn + lr) * kLd256 + 4 * h;
+#pragma unroll
+        for (int k0 = 0; k0 < kBigK; k0 += 8) {
+            float4 a4[4], b4[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) a4[i] = *reinterpret_cast<const float4*>(as + 32 * i * kLd256 + k0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) b4[j] = *reinterpret_cast<const float4*>(bs + 32 * j * kLd256 + k0);
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(f4get(a4[i], t), f4get(b4[j], t), acc[i][j],
+                                                                        0, 0, 0);
+        }
+        if (more) lstore(cur ^ 1);
+        __syncthreads();
+    }
+
+    float* __restrict__ C = g.C + coff;
+    const float* R = g.R ? g.R + coff : C;
+    const int ldr = g.R ? g.ldr : g.ldc;
+    // The beta test sits outside the unrolled stores (one branch, not 256).
+    auto epilogue = [&](auto use_rc) {
+        constexpr bool USE_R = decltype(use_rc)::value;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int col = n0 + wn + 32 * j + lr;
+                if (!FULL && col >= N) continue;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int row = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+                    if (FULL || row < M) {
+                        float v = g.alpha * acc[i][j][r];
+                        if (USE_R) v += g.beta * R[static_cast<long long>(row) * ldr + col];
+                        C[static_cast<long long>(row) * g.ldc + col] = v;
+                    }
+                }
+            }
+    };
+    if (g.beta != 0.f) epilogue(std::true_type{});
+    else epilogue(std::false_type{});
+}
+
+int launch_256(int ta, int tb, GemmArgs g, int batch, hipStream_t stream)
+{
+    g.tiles_m = ceil_div(g.M, kBig);
+    g.tiles_n = ceil_div(g.N, kBig);
+    const long long nwg = static_cast<long long>(g.tiles_m) * g.tiles_n;
+    if (nwg > 0x7fffffffLL) return fail(LHIP_E_CAPACITY, "sgemm: %lld workgroups exceed the grid limit", nwg);
+    g.splits = 1; g.kchunk = g.K; g.ws = nullptr;
+    dim3 grid(static_cast<unsigned>(nwg), batch, 1), block(kThreads, 1, 1);
+    const bool full = g.M % kBig == 0 && g.N % kBig == 0 && g.K % kBigK == 0 && (ta || g.vecA) && (!tb || g.vecB);
+    auto go = [&](auto fullc) {
+        constexpr bool F = decltype(fullc)::value;
+        if (!ta && !tb) sgemm_256_kernel<false, false, F><<<grid, block, 0, stream>>>(g);
+        else if (ta && !tb) sgemm_256_kernel<true, false, F><<<grid, block, 0, stream>>>(g);
+        else if (!ta && tb) sgemm_256_kernel<false, true, F><<<grid, block, 0, stream>>>(g);
+        else sgemm_256_kernel<true, true, F><<<grid, block, 0, stream>>>(g);
+    };
+    if (full) go(std::true_type{});
+    else go(std::false_type{});
+    return check_launch("sgemm (256): kernel launch");
 }
 
 // ---------------------------------------------------------------------------
@@ -860,6 +1073,8 @@ int sgemm_run(int ta, int tb, int m, int n, int k, float alpha,
     // small (fewer 64x64 tiles than CUs): 32x32 tiles with K shared by the
     // four waves of a workgroup, split over workgroups when K is very long
     // (split-K partials in o.ws).
+    const long long tiles256 = static_cast<long long>(ceil_div(m, kBig)) * ceil_div(n, kBig) * batch;
+    if (tiles256 >= cus) return launch_256(ta, tb, g, batch, stream);
     if (big_tiles >= cus) return launch_cfg<128, 128, 32>(ta, tb, g, batch, stream);
     if (tiles64 >= cus) return launch_cfg<64, 64, 32>(ta, tb, g, batch, stream);
     const bool small = use_small_kernel(m, n, g.K);

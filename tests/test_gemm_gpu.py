@@ -326,3 +326,37 @@ def test_gemm_batched_reduce_rejects_bad_count():
     A = device.Buffer((4, 4))
     with pytest.raises(LanternlHipError):
         kernels.sgemm_batched_reduce(0, 0, 4, 4, 4, 1.0, A.ptr, 4, 16, A.ptr, 4, 16, 0.0, A.ptr, 4, 0)
+
+
+@pytest.mark.parametrize("m,n,k,batch,ld_pad", [(4096, 4096, 48, 1, 0),     # every tile full
+                                                (4000, 4100, 203, 1, 0),   # ragged M, N and K
+                                                (4096, 4096, 64, 1, 1),    # ld % 4 != 0: scalar loads
+                                                (1024, 1024, 80, 16, 0)])  # 16 x 16 tiles per batch
+def test_gemm_256_tile_path(m, n, k, batch, ld_pad):
+    """Problems with at least one 256x256 output tile per CU: all four operand
+    layouts, alpha/beta, vs numpy float64 on each batch entry."""
+    announce("gemm 256 tiles", m, n, k, batch, ld_pad)
+    rng = np.random.default_rng(m + n + k + batch + ld_pad)
+    a = rng.uniform(-1, 1, (batch, m, k)).astype(np.float32)
+    b = rng.uniform(-1, 1, (batch, k, n)).astype(np.float32)
+    c0 = rng.uniform(-1, 1, (batch, m, n)).astype(np.float32)
+    ref = 0.5 * np.matmul(a.astype(np.float64), b.astype(np.float64)) - 2.0 * c0
+    for ta, tb in ((0, 0), (1, 0), (0, 1), (1, 1)):
+        sa = np.ascontiguousarray(a.transpose(0, 2, 1)) if ta else a
+        sb = np.ascontiguousarray(b.transpose(0, 2, 1)) if tb else b
+        lda, ldb, ldc = sa.shape[2] + ld_pad, sb.shape[2] + ld_pad, n + ld_pad
+        pa = np.zeros((batch, sa.shape[1], lda), np.float32)
+        pa[:, :, :sa.shape[2]] = sa
+        pb = np.zeros((batch, sb.shape[1], ldb), np.float32)
+        pb[:, :, :sb.shape[2]] = sb
+        pc = np.full((batch, m, ldc), np.nan, np.float32)
+        pc[:, :, :n] = c0
+        A, B, C = to_dev(pa), to_dev(pb), to_dev(pc)
+        kernels.sgemm_strided_batched(ta, tb, m, n, k, 0.5, A.ptr, lda, pa[0].size, B.ptr, ldb, pb[0].size,
+                                      -2.0, C.ptr, ldc, pc[0].size, batch)
+        device.sync()
+        got = C.download().reshape(batch, m, ldc)
+        for z in range(batch):
+            assert rel_fro(got[z, :, :n], ref[z]) <= TOL, (ta, tb, z)
+        if ld_pad:
+            assert np.isnan(got[:, :, n:]).all(), "wrote outside the n columns"
