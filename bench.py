@@ -191,8 +191,8 @@ def run_lm_workload(args):
 
 
 # HBM bytes per 4096^3 NN launch from FETCH_SIZE / WRITE_SIZE with the copy
-# calibration: 809,225 KiB (profiles/sgemm_nn_4096.md).
-GEMM4096_TRAFFIC_BYTES = 809_225 * 1024
+# calibration: 2 x 196,747 + 65,536 = 459,030 KiB (profiles/sgemm_nn_4096.md).
+GEMM4096_TRAFFIC_BYTES = 459_030 * 1024
 
 
 def run_gemm_workload(args):

@@ -298,100 +298,104 @@ sgemm_mfma_kernel(const GemmArgs g)
 // ---------------------------------------------------------------------------
 // Large problems (at least one 256x256 tile per CU): 256x256 output tiles,
 // four waves of 128x128 (16 v_mfma_f32_32x32x2f32 accumulators each, 256
-// AGPRs, one wave per SIMD), 16-deep K tiles double-buffered in LDS.
+// AGPRs, one wave per SIMD), 32-deep K tiles double-buffered in LDS (128 KB).
 //
-// Both LDS tiles are k-contiguous: As[m][k], Bs[n][k] with a row stride of
-// kLd256 = 20 floats.  For an 8-deep K step at k0, lane l (row or column
-// r = l%32 of a 32-block, half h = l/32) fetches op(A)[r][k0+4h .. k0+4h+3]
-// and op(B)[k0+4h .. +3][c] with one ds_read_b128 each; MFMA t of the step
-// multiplies element t of both, so its two k slots are k0+t and k0+4+t and the
-// four MFMAs cover k0 .. k0+7 once.  A wave thus reads 8 b128 per 64 MFMAs.
-// A row stride of 20 floats puts 8 consecutive rows (one 8-lane phase of a
-// b128 access) on 8 distinct 4-bank groups, so those reads are conflict-free.
+// Both LDS tiles are k-contiguous: As[m][k], Bs[n][k], 32 floats (8 quads of
+// 4 k) per row, quad q of row r stored at quad position q ^ swz(r) with
+// swz(r) = (r ^ (r >> 3)) & 7.  For an 8-deep K step at k0, lane l (row or
+// column r = l%32 of a 32-block, half h = l/32) fetches op(A)[r][k0+4h ..
+// k0+4h+3] and op(B)[k0+4h .. +3][c] with one ds_read_b128 each; MFMA t of
+// the step multiplies element t of both, so its two k slots are k0+t and
+// k0+4+t and the four MFMAs cover k0 .. k0+7 once.  A wave thus reads 8 b128
+// per 64 MFMAs.  The swizzle maps any 8 rows 8m .. 8m+7 (one 8-lane phase of
+// those reads) and any 8 rows 32m + 4j + c, j = 0..7 (a phase of the
+// transposed writes below) to 8 distinct quad positions: both are free of
+// bank conflicts.
 //
-// Global -> LDS: an operand stored with k contiguous (A when !TA, B when TB)
-// is read as float4 along k and written with ds_write_b128; an operand stored
-// K-major (A when TA, B when !TB) is read as four scalars from four
-// consecutive k-rows (each instruction 64 consecutive floats of one row),
-// gathered per lane into one float4 and written with one ds_write_b128 --
-// conflict-free for 8 consecutive columns, like the reads.
+// Global -> LDS, float4 loads along the stored contiguous dimension:
+//  - operand stored k-contiguous (A when !TA, B when TB): 8 lanes read one
+//    row's 32 k, written as they are (ds_write_b128);
+//  - operand stored K-major (A when TA, B when !TB): a lane reads a 4 k x 4
+//    column block (4 float4 from 4 k-rows, 64 lanes = 1 KB of a row per
+//    instruction) and writes it transposed: column c's 4 k as one b128.
 __device__ __forceinline__ float f4get(const float4& v, int t)
 {
     return t == 0 ? v.x : t == 1 ? v.y : t == 2 ? v.z : v.w;   // t is a compile-time constant after unrolling
 }
 
 constexpr int kBig = 256;
-constexpr int kBigK = 16;
-constexpr int kLd256 = 20;
+constexpr int kBigK = 32;
+constexpr int kLd256 = kBigK;        // floats per LDS row (quad-swizzled, no padding)
+constexpr int kBigQ = kBigK / 4;     // k quads per row of a tile
+constexpr int kBigLds = kBig * kLd256;
+
+__device__ __forceinline__ int big_swz(int row) { return (row ^ (row >> 3)) & 7; }
 
 template <bool KMAJOR, bool FULL>
 struct BigTileRegs {
-    // 256 rows (m or n) x 16 k of one operand: 16 floats per thread
-    float4 v[4];
+    // 256 rows (m or n) x kBigK k of one operand: kBigQ float4 per thread
+    float4 v[kBigQ];
 
-    // stored: element (row, k) at X[row * ld + k] (!KMAJOR) or X[k * ld + row] (KMAJOR)
-    __device__ __forceinline__ void load(const float* __restrict__ X, int ld, int r0, int k0, int rmax, int kmax,
-                                         bool vec, int tid)
+    // stored: element (row, k) at X[row * ld + k] (!KMAJOR) or X[k * ld + row] (KMAJOR).
+    // Slot s (0 .. kBigQ-1) is one float4 load:
+    // !KMAJOR: row tid/8 + 32s, k quad tid%8;
+    // KMAJOR: k row 4kq + s%4 of block (columns 4(tid%64) .. +3, k quad kq = tid/64 + 4(s/4)).
+    // The slots are loaded and stored one at a time so that the main loop can
+    // spread them between MFMA groups; a KMAJOR store slot needs the four
+    // load slots of its block.
+    __device__ __forceinline__ void load_slot(int s, const float* __restrict__ X, int ld, int r0, int k0, int rmax,
+                                              int kmax, bool vec, int tid)
     {
+        int gr, gk;
+        const float* src;
         if (!KMAJOR) {
-            const int k4 = tid & 3;
-#pragma unroll
-            for (int p = 0; p < 4; ++p) {
-                const int row = (tid >> 2) + 64 * p;
-                const int gr = r0 + row, gk = k0 + 4 * k4;
-                const float* src = X + static_cast<long long>(gr) * ld + gk;
-                if (FULL || (vec && gr < rmax && gk + 3 < kmax)) {
-                    const float4 t = *reinterpret_cast<const float4*>(src);
-                    v[p].x = t.x; v[p].y = t.y; v[p].z = t.z; v[p].w = t.w;   // per component: stays in VGPRs
-                } else {
-                    const bool rok = gr < rmax;
-                    v[p].x = (rok && gk + 0 < kmax) ? src[0] : 0.f;
-                    v[p].y = (rok && gk + 1 < kmax) ? src[1] : 0.f;
-                    v[p].z = (rok && gk + 2 < kmax) ? src[2] : 0.f;
-                    v[p].w = (rok && gk + 3 < kmax) ? src[3] : 0.f;
-                }
-            }
+            gr = r0 + tid / kBigQ + (kThreads / kBigQ) * s;
+            gk = k0 + 4 * (tid % kBigQ);
+            src = X + static_cast<long long>(gr) * ld + gk;
         } else {
-            const int q = tid >> 6;            // k quad 0..3
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int row = (tid & 63) + 64 * e;
-                const int gr = r0 + row;
-                float t[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int gk = k0 + 4 * q + i;
-                    t[i] = (FULL || (gr < rmax && gk < kmax)) ? X[static_cast<long long>(gk) * ld + gr] : 0.f;
-                }
-                v[e] = make_float4(t[0], t[1], t[2], t[3]);
-            }
+            gr = r0 + 4 * (tid & 63);
+            gk = k0 + 4 * ((tid >> 6) + 4 * (s >> 2)) + (s & 3);
+            src = X + static_cast<long long>(gk) * ld + gr;
+        }
+        // the 4 contiguous elements: (row gr, k gk..gk+3) or (k gk, columns gr..gr+3)
+        const int lim = KMAJOR ? rmax - gr : kmax - gk;
+        const bool lineok = KMAJOR ? gk < kmax : gr < rmax;
+        if (FULL || (vec && lineok && lim >= 4)) {
+            const float4 t = *reinterpret_cast<const float4*>(src);
+            v[s].x = t.x; v[s].y = t.y; v[s].z = t.z; v[s].w = t.w;   // per component: stays in VGPRs
+        } else {
+            v[s].x = (lineok && lim > 0) ? src[0] : 0.f;
+            v[s].y = (lineok && lim > 1) ? src[1] : 0.f;
+            v[s].z = (lineok && lim > 2) ? src[2] : 0.f;
+            v[s].w = (lineok && lim > 3) ? src[3] : 0.f;
         }
     }
 
-    __device__ __forceinline__ void store(float* lds, int tid) const
+    __device__ __forceinline__ void store_slot(int s, float* lds, int tid) const
     {
         if (!KMAJOR) {
-            const int k4 = tid & 3;
-#pragma unroll
-            for (int p = 0; p < 4; ++p)
-                *reinterpret_cast<float4*>(lds + ((tid >> 2) + 64 * p) * kLd256 + 4 * k4) = v[p];
+            const int row = tid / kBigQ + (kThreads / kBigQ) * s;
+            *reinterpret_cast<float4*>(lds + row * kLd256 + 4 * ((tid % kBigQ) ^ big_swz(row))) = v[s];
         } else {
-            const int q = tid >> 6;
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                *reinterpret_cast<float4*>(lds + ((tid & 63) + 64 * e) * kLd256 + 4 * q) = v[e];
+            // column 4(tid%64) + s%4 of block s/4: its four k from the block's four loads
+            const int b = s >> 2, c = s & 3;
+            const int row = 4 * (tid & 63) + c;
+            const int kq = (tid >> 6) + 4 * b;
+            const float4 t = make_float4(f4get(v[4 * b + 0], c), f4get(v[4 * b + 1], c), f4get(v[4 * b + 2], c),
+                                         f4get(v[4 * b + 3], c));
+            *reinterpret_cast<float4*>(lds + row * kLd256 + 4 * (kq ^ big_swz(row))) = t;
         }
     }
 };
 
-// FULL: M and N multiples of 256, K of 16, k-contiguous operands 16-byte
+// FULL: M and N multiples of 256, K of kBigK, k-contiguous operands 16-byte
 // aligned -- every tile load is in bounds and unconditional.
 template <bool TA, bool TB, bool FULL>
 __global__ void __launch_bounds__(kThreads)
 sgemm_256_kernel(const GemmArgs g)
 {
-    __shared__ float As[2][kBig * kLd256];
-    __shared__ float Bs[2][kBig * kLd256];
+    __shared__ float As[2][kBigLds];
+    __shared__ float Bs[2][kBigLds];
     const int M = g.M, N = g.N;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -410,13 +414,13 @@ sgemm_256_kernel(const GemmArgs g)
     BigTileRegs<TA, FULL> ra;    // op(A): row m; stored M x K (!TA) or K x M (TA)
     BigTileRegs<!TB, FULL> rb;   // op(B): row n; stored N x K (TB) or K x N (!TB)
     const int K = g.K;
-    auto gload = [&](int k0) {
-        ra.load(A, g.lda, m0, k0, M, K, g.vecA, tid);
-        rb.load(B, g.ldb, n0, k0, N, K, g.vecB, tid);
+    auto gload = [&](int s, int k0) {
+        ra.load_slot(s, A, g.lda, m0, k0, M, K, g.vecA, tid);
+        rb.load_slot(s, B, g.ldb, n0, k0, N, K, g.vecB, tid);
     };
-    auto lstore = [&](int buf) {
-        ra.store(As[buf], tid);
-        rb.store(Bs[buf], tid);
+    auto lstore = [&](int s, int buf) {
+        ra.store_slot(s, As[buf], tid);
+        rb.store_slot(s, Bs[buf], tid);
     };
 
     floatx16 acc[4][4];
@@ -427,36 +431,85 @@ sgemm_256_kernel(const GemmArgs g)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
+    // Fragments of one 8-deep step: a[i] = op(A) rows wm+32i+lr, b[j] = op(B)
+    // columns wn+32j+lr, k = k0+4h .. k0+4h+3 each.
+    // Quad k0/4 + h of row wm + 32i + lr sits at position (k0/4 + h) ^ swz, with
+    // swz = (lr ^ (lr >> 3) ^ 4(i & 1)) & 7 (wm, wn are multiples of 128);
+    // k0/4 is even, so the position is (k0/4) ^ g with g = h ^ swz.
+    struct Frag { float4 a[4], b[4]; };
+    const int g_even = (h ^ lr ^ (lr >> 3)) & 7;
+    auto read_frag = [&](Frag& f, int buf, int k0) {
+        const float* as = As[buf] + (wm + lr) * kLd256;
+        const float* bs = Bs[buf] + (wn + lr) * kLd256;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            f.a[i] = *reinterpret_cast<const float4*>(as + 32 * i * kLd256 + 4 * ((k0 / 4) ^ g_even ^ (4 * (i & 1))));
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            f.b[j] = *reinterpret_cast<const float4*>(bs + 32 * j * kLd256 + 4 * ((k0 / 4) ^ g_even ^ (4 * (j & 1))));
+    };
+    auto mma_t = [&](const Frag& f, int t) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(f4get(f.a[i], t), f4get(f.b[j], t), acc[i][j],
+                                                                0, 0, 0);
+    };
+
+    // Software pipeline over the four 8-deep steps of a K tile:
+    //   steps 0-2: read the next step's fragments, then four groups of 16
+    //     MFMAs; after each group, steps 0-1 issue one slot of the next tile's
+    //     global loads (8 slots), step 2 writes two slots to the other LDS
+    //     buffer (so the loads have had two steps to land);
+    //   barrier; read the next tile's step-0 fragments; step 3's MFMAs.
+    // Spreading the loads and LDS writes keeps the MFMA pipe fed (a CU's
+    // address path takes 64 B/clk: a whole tile's 64 KB issued at once stalls
+    // the waves for ~1K cycles).  All reads of an LDS buffer are issued before
+    // the barrier that precedes its next write.
+    constexpr int kSteps = kBigK / 8;
+    static_assert(kSteps == 4 && kBigQ == 8, "the load/store schedule assumes 32-deep K tiles");
     const int nk = (K + kBigK - 1) / kBigK;
+    Frag f[2];
     if (nk > 0) {
-        gload(0);
-        lstore(0);
+#pragma unroll
+        for (int sl = 0; sl < kBigQ; ++sl) gload(sl, 0);
+#pragma unroll
+        for (int sl = 0; sl < kBigQ; ++sl) lstore(sl, 0);
         __syncthreads();
+        read_frag(f[0], 0, 0);
     }
+    // The loads, stores and reads of the next tile are unconditional (no
+    // branches for the waitcnt placement to be conservative about): on the
+    // last tile they repeat the current tile's loads into the idle buffer.
     for (int kt = 0; kt < nk; ++kt) {
         const int cur = kt & 1;
-        const bool more = kt + 1 < nk;
-        if (more) gload((kt + 1) * kBigK);
-        const float* as = As[cur] + (wm + lr) * kLd256 + 4 * h;
-        const float* bs = Bs[cur] + (wn + lr) * kLd256 + 4 * h;
+        const int kn = (kt + 1 < nk ? kt + 1 : kt) * kBigK;
 #pragma unroll
-        for (int k0 = 0; k0 < kBigK; k0 += 8) {
-            float4 a4[4], b4[4];
+        for (int st = 0; st + 1 < kSteps; ++st) {
+            read_frag(f[(st + 1) & 1], cur, 8 * (st + 1));
 #pragma unroll
-            for (int i = 0; i < 4; ++i) a4[i] = *reinterpret_cast<const float4*>(as + 32 * i * kLd256 + k0);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) b4[j] = *reinterpret_cast<const float4*>(bs + 32 * j * kLd256 + k0);
-#pragma unroll
-            for (int t = 0; t < 4; ++t)
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-#pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(f4get(a4[i], t), f4get(b4[j], t), acc[i][j],
-                                                                        0, 0, 0);
+            for (int t = 0; t < 4; ++t) {
+                __builtin_amdgcn_sched_barrier(0);
+                mma_t(f[st & 1], t);
+                __builtin_amdgcn_sched_barrier(0);
+                if (st < 2) {
+                    gload(4 * st + t, kn);
+                } else {
+                    lstore(2 * t, cur ^ 1);
+                    lstore(2 * t + 1, cur ^ 1);
+                }
+            }
         }
-        if (more) lstore(cur ^ 1);
+        __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
+        read_frag(f[0], cur ^ 1, 0);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            __builtin_amdgcn_sched_barrier(0);
+            mma_t(f[1], t);
+        }
+        __builtin_amdgcn_sched_barrier(0);
     }
 
     float* __restrict__ C = g.C + coff;
