@@ -328,7 +328,7 @@ def test_gemm_batched_reduce_rejects_bad_count():
         kernels.sgemm_batched_reduce(0, 0, 4, 4, 4, 1.0, A.ptr, 4, 16, A.ptr, 4, 16, 0.0, A.ptr, 4, 0)
 
 
-@pytest.mark.parametrize("m,n,k,batch,ld_pad", [(4096, 4096, 48, 1, 0),     # every tile full
+@pytest.mark.parametrize("m,n,k,batch,ld_pad", [(4096, 4096, 96, 1, 0),     # every tile full
                                                 (4000, 4100, 203, 1, 0),   # ragged M, N and K
                                                 (4096, 4096, 64, 1, 1),    # ld % 4 != 0: scalar loads
                                                 (1024, 1024, 80, 16, 0)])  # 16 x 16 tiles per batch
