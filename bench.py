@@ -50,14 +50,30 @@ def _cpu_model():
     return platform.processor() or "unknown"
 
 
-def time_launches(fn, steps, warmup):
+def time_launches(fn, steps, warmup, recorded=False):
     """Average ms per call of fn(i) over `steps` back-to-back calls, bracketed by
-    hipEvents recorded on the library stream (where fn enqueues its kernels)."""
+    hipEvents recorded on the library stream (where fn enqueues its kernels).
+
+    recorded=True: after the eager warm-up (at least one call, which also sizes
+    the library workspace), the `steps` calls are recorded once as a program
+    (lhip_program_begin/end) and the timed region is one replay of it, so the
+    kernels run back to back on the device with no Python or host launch cost
+    between them.  fn must then only enqueue work."""
     from lanternl_amd import device
-    for i in range(warmup):
+    for i in range(max(warmup, 1 if recorded else 0)):
         fn(i)
     device.sync()
     t = device.Timer()
+    if recorded:
+        prog = device.Program.record(lambda: [fn(i) for i in range(steps)])
+        prog.replay()            # first replay uploads the graph
+        device.sync()
+        t.start()
+        prog.replay()
+        t.stop()
+        device.sync()
+        prog.free()
+        return t.ms() / steps
     t.start()
     for i in range(steps):
         fn(i)
@@ -78,7 +94,7 @@ def bench_gemm(m, n, k, ta=False, tb=False, steps=20, warmup=3, seed=0):
 
     def run(_):
         kernels.sgemm(A, B, C, transa=ta, transb=tb)
-    ms = time_launches(run, steps, warmup)
+    ms = time_launches(run, steps, warmup, recorded=True)
     flops = 2.0 * m * n * k
     tflops = flops / (ms * 1e-3) / 1e12
     return {"m": m, "n": n, "k": k, "op": ("T" if ta else "N") + ("T" if tb else "N"),
@@ -125,7 +141,7 @@ def dominant_kernel_c2(steps, warmup):
 
     def run(_):
         kernels.sgemm_batched_reduce(0, 1, N, D, F, 1.0, dzu.ptr, F, N * F, w13.ptr, F, D * F, 0.0, out.ptr, D, 2)
-    ms = time_launches(run, max(steps, 50), warmup)
+    ms = time_launches(run, max(steps, 50), warmup, recorded=True)
     flops = 2.0 * N * D * (2 * F)
     tflops = flops / (ms * 1e-3) / 1e12
     return {"ms": ms, "tflops": tflops, "frac": tflops / PEAK_FP32_MFMA_TFLOPS, "m": N, "n": D, "k": 2 * F,
@@ -239,7 +255,7 @@ def bench_bandwidth(name, nbytes, make_set, launch, steps, warmup, only=None):
 
     def run(i):
         launch(sets[i % nsets])
-    ms = time_launches(run, steps, warmup)
+    ms = time_launches(run, steps, warmup, recorded=True)
     gbps = nbytes / (ms * 1e-3) / 1e9
     return {"suite": "bandwidth", "kernel": name, "ms": ms, "bytes": nbytes, "gbps": gbps,
             "frac": gbps / PEAK_HBM_GBPS, "buffer_sets": nsets}
@@ -273,14 +289,17 @@ def run_bandwidth_suite(args):
                                lambda s: call("lhip_rmsnorm_bwd", s[0].ptr, w.ptr, inv.ptr, s[1].ptr, s[2].ptr,
                                               dw.ptr, T, Dm, 0),
                                steps, warm, args.only))
-    # RoPE 4096 tokens x 16 heads x 64, base 1e4, in place (fwd and inverse)
+    # RoPE 4096 tokens x 16 heads x 64, base 1e4, in place (fwd and inverse),
+    # interleaved pairs (the CPU path's layout) and half-split pairs
     nb = 4 * 2 * T * 16 * 64
-    for inverse in (0, 1):
-        out.append(bench_bandwidth(f"rope_{'bwd' if inverse else 'fwd'} 4096x16x64", nb,
-                                   lambda i: (arr(T, 16 * 64),),
-                                   lambda s, inv_=inverse: call("lhip_rope", s[0].ptr, None, T, 16, 64, 16 * 64, 0, 0,
-                                                                10000.0, 0, inv_),
-                                   steps, warm, args.only))
+    for il in (1, 0):
+        for inverse in (0, 1):
+            out.append(bench_bandwidth(f"rope_{'bwd' if inverse else 'fwd'} 4096x16x64 "
+                                       f"{'interleaved' if il else 'half-split'}", nb,
+                                       lambda i: (arr(T, 16 * 64),),
+                                       lambda s, inv_=inverse, il_=il: call("lhip_rope", s[0].ptr, None, T, 16, 64,
+                                                                            16 * 64, 0, 0, 10000.0, il_, inv_),
+                                       steps, warm, args.only))
     # SwiGLU 4096 x 4096
     n = T * Fm
     out.append(bench_bandwidth("swiglu_fwd 4096x4096", 4 * 3 * n,

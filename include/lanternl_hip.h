@@ -102,6 +102,26 @@ LHIP_API int lhip_event_destroy(void* ev);
 LHIP_API int lhip_event_record(void* ev);
 LHIP_API int lhip_event_elapsed_ms(void* start, void* stop, float* ms);
 
+/* ---- programs: record a sequence of calls once, replay it as a hipGraph ----
+ * Between lhip_program_begin and lhip_program_end, compute calls are recorded
+ * from the library stream instead of being executed; lhip_program_end turns
+ * the recording into an executable program, and lhip_program_replay enqueues
+ * it `times` times on the library stream (asynchronous, like every compute
+ * call).  A program keeps the pointers and scalar arguments it was recorded
+ * with.  While recording, calls that synchronise, allocate, free or read back
+ * to the host (upload, download, sync, malloc, free, event timing,
+ * lhip_matmul_host, every lhip_lm_* call) fail with LHIP_E_UNSUPPORTED, and
+ * so does a call whose library workspace would have to grow: issue the same
+ * calls once before recording them.  lhip_program_end(NULL) discards the
+ * recording.  Replaces the Program command buffer with its capture/replay
+ * (ai/gpu/luaTL_train.lua:327-627; luaTL_prog_run / luaTL_prog_capture /
+ * luaTL_prog_replay / luaTL_prog_graph_free, cuda/luaTL_train.cu:1505-1690). */
+LHIP_API int lhip_program_begin(void);
+LHIP_API int lhip_program_end(void** program);
+LHIP_API int lhip_program_replay(void* program, int times);
+LHIP_API int lhip_program_free(void* program);
+LHIP_API int lhip_is_recording(void);
+
 /* ---- GEMM family (fp32 on v_mfma_f32_32x32x2f32) ---------------------------
  * C(m x n) = alpha * op(A)(m x k) * op(B)(k x n) + beta * C, row-major.
  *   transa == 0: A is m x k, lda >= k;   transa != 0: A is stored k x m, lda >= m

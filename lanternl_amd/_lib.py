@@ -57,6 +57,11 @@ SIGNATURES = {
     "lhip_event_destroy": (_i, [_p]),
     "lhip_event_record": (_i, [_p]),
     "lhip_event_elapsed_ms": (_i, [_p, _p, ctypes.POINTER(_f)]),
+    "lhip_program_begin": (_i, []),
+    "lhip_program_end": (_i, [_pp]),
+    "lhip_program_replay": (_i, [_p, _i]),
+    "lhip_program_free": (_i, [_p]),
+    "lhip_is_recording": (_i, []),
     "lhip_sgemm": (_i, [_i, _i, _i, _i, _i, _f, _p, _i, _p, _i, _f, _p, _i]),
     "lhip_sgemm_strided_batched": (_i, [_i, _i, _i, _i, _i, _f, _p, _i, _ll, _p, _i, _ll, _f,
                                         _p, _i, _ll, _i]),

@@ -46,6 +46,10 @@ int workspace(size_t bytes, void** out)
     auto& s = g_state;
     if (bytes == 0) bytes = 256;
     if (bytes > s.work_bytes) {
+        if (s.recording)
+            return fail(LHIP_E_UNSUPPORTED,
+                        "workspace: %zu bytes needed (%zu held) while a program is being recorded; run the same "
+                        "calls once before recording them", bytes, s.work_bytes);
         if (s.work) {
             LHIP_CHECK_HIP(hipStreamSynchronize(s.stream), "workspace: stream sync");
             LHIP_CHECK_HIP(hipFree(s.work), "workspace: hipFree");
@@ -118,6 +122,12 @@ LHIP_API int lhip_shutdown(void)
 {
     auto& s = st();
     if (!s.ready) return LHIP_OK;
+    if (s.recording) {   // abandon the recording: its graph is discarded
+        hipGraph_t g = nullptr;
+        if (hipStreamEndCapture(s.stream, &g) == hipSuccess && g) (void)hipGraphDestroy(g);
+        (void)hipGetLastError();
+        s.recording = false;
+    }
     (void)hipStreamSynchronize(s.stream);
     if (s.d_stage) (void)hipFree(s.d_stage);
     if (s.h_stage) (void)hipHostFree(s.h_stage);
@@ -151,6 +161,7 @@ LHIP_API int lhip_device_info(lhip_devinfo_t* out)
 LHIP_API int lhip_malloc(void** dptr, size_t bytes)
 {
     LHIP_REQUIRE_READY();
+    LHIP_REFUSE_RECORDING();
     if (!dptr) return fail(LHIP_E_NULL, "lhip_malloc: dptr is NULL");
     *dptr = nullptr;
     if (bytes == 0) return fail(LHIP_E_ARG, "lhip_malloc: zero-byte allocation");
@@ -167,6 +178,7 @@ LHIP_API int lhip_free(void* dptr)
 {
     if (!dptr) return LHIP_OK;
     if (!st().ready) return LHIP_OK;  // after shutdown a late finaliser is a no-op
+    LHIP_REFUSE_RECORDING();
     // Work already enqueued may still read the buffer.
     LHIP_CHECK_HIP(hipStreamSynchronize(st().stream), "lhip_free: stream sync");
     LHIP_CHECK_HIP(hipFree(dptr), "lhip_free: hipFree");
@@ -176,6 +188,7 @@ LHIP_API int lhip_free(void* dptr)
 LHIP_API int lhip_upload(void* dst, const void* src, size_t bytes)
 {
     LHIP_REQUIRE_READY();
+    LHIP_REFUSE_RECORDING();
     if (bytes == 0) return LHIP_OK;
     if (!dst || !src) return fail(LHIP_E_NULL, "lhip_upload: NULL pointer");
     LHIP_CHECK_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, st().stream), "lhip_upload");
@@ -186,6 +199,7 @@ LHIP_API int lhip_upload(void* dst, const void* src, size_t bytes)
 LHIP_API int lhip_download(void* dst, const void* src, size_t bytes)
 {
     LHIP_REQUIRE_READY();
+    LHIP_REFUSE_RECORDING();
     if (bytes == 0) return LHIP_OK;
     if (!dst || !src) return fail(LHIP_E_NULL, "lhip_download: NULL pointer");
     LHIP_CHECK_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, st().stream), "lhip_download");
@@ -215,6 +229,7 @@ LHIP_API int lhip_zero(void* dptr, size_t bytes)
 LHIP_API int lhip_sync(void)
 {
     LHIP_REQUIRE_READY();
+    LHIP_REFUSE_RECORDING();
     LHIP_CHECK_HIP(hipStreamSynchronize(st().stream), "lhip_sync");
     return LHIP_OK;
 }
@@ -249,11 +264,78 @@ LHIP_API int lhip_event_record(void* ev)
 LHIP_API int lhip_event_elapsed_ms(void* start, void* stop, float* ms)
 {
     LHIP_REQUIRE_READY();
+    LHIP_REFUSE_RECORDING();
     if (!start || !stop || !ms) return fail(LHIP_E_NULL, "lhip_event_elapsed_ms: NULL argument");
     LHIP_CHECK_HIP(hipEventSynchronize(static_cast<hipEvent_t>(stop)), "lhip_event_elapsed_ms: sync");
     LHIP_CHECK_HIP(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop)),
                    "lhip_event_elapsed_ms");
     return LHIP_OK;
 }
+
+
+// ---- programs: recorded sequences of compute calls, replayed as a hipGraph ----
+// The counterpart of luaTL's command-buffer Program with capture/replay
+// (ai/gpu/luaTL_train.lua:327-627, luaTL_prog_capture / luaTL_prog_replay):
+// instead of an op list that a C interpreter walks, the calls themselves are
+// captured from the library stream into a graph, so every entry point that
+// only enqueues work can be recorded.
+
+LHIP_API int lhip_program_begin(void)
+{
+    LHIP_REQUIRE_READY();
+    auto& s = st();
+    if (s.recording) return fail(LHIP_E_ARG, "lhip_program_begin: a program is already being recorded");
+    LHIP_CHECK_HIP(hipStreamBeginCapture(s.stream, hipStreamCaptureModeRelaxed), "lhip_program_begin");
+    s.recording = true;
+    return LHIP_OK;
+}
+
+LHIP_API int lhip_program_end(void** program)
+{
+    LHIP_REQUIRE_READY();
+    auto& s = st();
+    if (!s.recording) return fail(LHIP_E_ARG, "lhip_program_end: no program is being recorded");
+    if (program) *program = nullptr;
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(s.stream, &g);
+    s.recording = false;
+    if (e != hipSuccess) {
+        if (g) (void)hipGraphDestroy(g);
+        return lhip::hip_fail(e, "lhip_program_end: end capture");
+    }
+    if (!program) {   // recording discarded
+        (void)hipGraphDestroy(g);
+        return LHIP_OK;
+    }
+    hipGraphExec_t x = nullptr;
+    e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return lhip::hip_fail(e, "lhip_program_end: instantiate");
+    *program = static_cast<void*>(x);
+    return LHIP_OK;
+}
+
+LHIP_API int lhip_program_replay(void* program, int times)
+{
+    LHIP_REQUIRE_READY();
+    LHIP_REFUSE_RECORDING();
+    if (!program) return fail(LHIP_E_NULL, "lhip_program_replay: program is NULL");
+    if (times < 1) return fail(LHIP_E_ARG, "lhip_program_replay: times %d must be >= 1", times);
+    for (int i = 0; i < times; ++i)
+        LHIP_CHECK_HIP(hipGraphLaunch(static_cast<hipGraphExec_t>(program), st().stream), "lhip_program_replay");
+    return LHIP_OK;
+}
+
+LHIP_API int lhip_program_free(void* program)
+{
+    if (!program || !st().ready) return LHIP_OK;
+    LHIP_REFUSE_RECORDING();
+    // a replay still in flight uses the executable graph
+    LHIP_CHECK_HIP(hipStreamSynchronize(st().stream), "lhip_program_free: stream sync");
+    LHIP_CHECK_HIP(hipGraphExecDestroy(static_cast<hipGraphExec_t>(program)), "lhip_program_free");
+    return LHIP_OK;
+}
+
+LHIP_API int lhip_is_recording(void) { return st().recording ? 1 : 0; }
 
 }  // extern "C"

@@ -37,6 +37,14 @@ __device__ __forceinline__ float4 ld_stream(const float* p)
     return make_float4(v.x, v.y, v.z, v.w);
 }
 
+// 128-bit store of data written once and not read back by this kernel
+// (non-temporal hint: streamed out rather than held dirty in L2 until the
+// end-of-kernel write-back).
+__device__ __forceinline__ void st_stream(float* p, const float4& v)
+{
+    __builtin_nontemporal_store(vf4{v.x, v.y, v.z, v.w}, reinterpret_cast<vf4*>(p));
+}
+
 __global__ void fill_kernel(float* __restrict__ p, long long n, float v)
 {
     const long long n4 = n >> 2;
@@ -111,7 +119,7 @@ __global__ void swiglu_fwd_kernel(const float* __restrict__ g, int ldg, const fl
             o.y = gv.y * sigmoid_by_sign(gv.y) * uv.y;
             o.z = gv.z * sigmoid_by_sign(gv.z) * uv.z;
             o.w = gv.w * sigmoid_by_sign(gv.w) * uv.w;
-            *reinterpret_cast<float4*>(h + oh) = o;
+            st_stream(h + oh, o);
         }
     } else {
         const long long n = static_cast<long long>(rows) * cols;
@@ -167,8 +175,8 @@ __global__ void swiglu_bwd_kernel(const float* __restrict__ g, int ldg, const fl
                 a.x += og.x; a.y += og.y; a.z += og.z; a.w += og.w;
                 b.x += ou.x; b.y += ou.y; b.z += ou.z; b.w += ou.w;
             }
-            *pg = a;
-            *pu = b;
+            st_stream(dg + r * lddg + c, a);
+            st_stream(du + r * lddu + c, b);
         }
     } else {
         const long long n = static_cast<long long>(rows) * cols;
@@ -198,9 +206,22 @@ struct RopeFreqs {
     double inv[kRopeMaxPairs];
 };
 
+// Vector access modes of one unit (a run of pairs sharing the row and head):
+//   ROPE_IL4: interleaved, two pairs (x0,y0,x1,y1) in one float4;
+//   ROPE_HS4: half-split, four pairs: float4 of first halves at p, float4 of
+//             second halves at p + hd/2;
+//   ROPE_HS2: half-split, two pairs as two float2 (8-byte alignment only).
+enum { ROPE_IL4 = 0, ROPE_HS4 = 1, ROPE_HS2 = 2, ROPE_SCALAR = 3 };
+
+__device__ __forceinline__ float2 rope_rot(float a, float b, float2 cs)
+{
+    return make_float2(a * cs.x - b * cs.y, b * cs.x + a * cs.y);
+}
+
+template <int MODE>
 __global__ void __launch_bounds__(256)
 rope_kernel(float* __restrict__ x, const int* __restrict__ pos_ids, int rows, int heads, int hd, int row_stride,
-            int pos_offset, int period, int interleaved, int inverse, int vec, RopeFreqs fr)
+            int pos_offset, int period, int interleaved, int inverse, RopeFreqs fr)
 {
     __shared__ float2 tab[kRopeRowsPerBlock * kRopeMaxPairs];   // (cos, sin)
     const int pairs = hd >> 1;
@@ -218,68 +239,7 @@ rope_kernel(float* __restrict__ x, const int* __restrict__ pos_ids, int rows, in
         }
         __syncthreads();
     };
-    if (vec) {
-        // unit = two adjacent pairs: one float4 (interleaved) or two float2
-        // (half-split).  A thread takes kU units per batch: all of the batch's
-        // loads are issued first (the first batch's before the angle table is
-        // computed, so the two overlap), then rotated and stored.
-        constexpr int kU = 8;
-        const int units_per_head = pairs >> 1;
-        const int per_row = heads * units_per_head;
-        const int units = nr * per_row;
-        const int half = pairs;
-        float4 v[kU];
-        float* ptr[kU];
-        int slot[kU];
-        auto load = [&](int i0) {
-#pragma unroll
-            for (int u = 0; u < kU; ++u) {
-                const int i = i0 + u * static_cast<int>(blockDim.x);
-                ptr[u] = nullptr;
-                if (i < units) {
-                    const int rr = i / per_row, rem = i - rr * per_row;
-                    const int h = rem / units_per_head, p = 2 * (rem - h * units_per_head);
-                    float* base = x + static_cast<long long>(r0 + rr) * row_stride + static_cast<long long>(h) * hd;
-                    slot[u] = rr * kRopeMaxPairs + p;
-                    if (interleaved) {
-                        ptr[u] = base + 2 * p;
-                        v[u] = *reinterpret_cast<const float4*>(ptr[u]);
-                    } else {
-                        ptr[u] = base + p;
-                        const float2 a = *reinterpret_cast<const float2*>(ptr[u]);
-                        const float2 b = *reinterpret_cast<const float2*>(ptr[u] + half);
-                        v[u] = make_float4(a.x, a.y, b.x, b.y);
-                    }
-                }
-            }
-        };
-        auto rotate_store = [&]() {
-#pragma unroll
-            for (int u = 0; u < kU; ++u) {
-                if (!ptr[u]) continue;
-                const float2 c0 = tab[slot[u]], c1 = tab[slot[u] + 1];
-                const float4 t = v[u];
-                if (interleaved) {
-                    *reinterpret_cast<float4*>(ptr[u]) =
-                        make_float4(t.x * c0.x - t.y * c0.y, t.y * c0.x + t.x * c0.y, t.z * c1.x - t.w * c1.y,
-                                    t.w * c1.x + t.z * c1.y);
-                } else {
-                    // t = (a0, a1, b0, b1): pairs (a0, b0) at p and (a1, b1) at p + 1
-                    *reinterpret_cast<float2*>(ptr[u]) = make_float2(t.x * c0.x - t.z * c0.y, t.y * c1.x - t.w * c1.y);
-                    *reinterpret_cast<float2*>(ptr[u] + half) =
-                        make_float2(t.z * c0.x + t.x * c0.y, t.w * c1.x + t.y * c1.y);
-                }
-            }
-        };
-        const int step = kU * static_cast<int>(blockDim.x);
-        load(threadIdx.x);
-        make_table();
-        rotate_store();
-        for (int i0 = threadIdx.x + step; i0 < units; i0 += step) {
-            load(i0);
-            rotate_store();
-        }
-    } else {
+    if constexpr (MODE == ROPE_SCALAR) {
         make_table();
         const int units = nr * heads * pairs;
         for (int i = threadIdx.x; i < units; i += blockDim.x) {
@@ -291,8 +251,79 @@ rope_kernel(float* __restrict__ x, const int* __restrict__ pos_ids, int rows, in
             float* a = interleaved ? base + 2 * p : base + p;
             float* b = interleaved ? base + 2 * p + 1 : base + p + pairs;
             const float x0 = *a, x1 = *b;
-            *a = x0 * cs.x - x1 * cs.y;
-            *b = x1 * cs.x + x0 * cs.y;
+            const float2 o = rope_rot(x0, x1, cs);
+            *a = o.x;
+            *b = o.y;
+        }
+    } else {
+        // A thread takes kU units per batch: the batch's loads are all issued
+        // first (the first batch's before the angle table is computed, so the
+        // two overlap), then rotated and stored.
+        constexpr int kPPU = MODE == ROPE_HS4 ? 4 : 2;     // pairs per unit
+        constexpr int kU = MODE == ROPE_HS4 ? 4 : 8;       // units per thread per batch
+        const int units_per_head = pairs / kPPU;
+        const int per_row = heads * units_per_head;
+        const int units = nr * per_row;
+        float4 va[kU], vb[kU];
+        float* ptr[kU];
+        int slot[kU];
+        auto load = [&](int i0) {
+#pragma unroll
+            for (int u = 0; u < kU; ++u) {
+                const int i = i0 + u * static_cast<int>(blockDim.x);
+                ptr[u] = nullptr;
+                if (i < units) {
+                    const int rr = i / per_row, rem = i - rr * per_row;
+                    const int h = rem / units_per_head, p = kPPU * (rem - h * units_per_head);
+                    float* base = x + static_cast<long long>(r0 + rr) * row_stride + static_cast<long long>(h) * hd;
+                    slot[u] = rr * kRopeMaxPairs + p;
+                    if constexpr (MODE == ROPE_IL4) {
+                        ptr[u] = base + 2 * p;
+                        va[u] = ld_stream(ptr[u]);
+                    } else if constexpr (MODE == ROPE_HS4) {
+                        ptr[u] = base + p;
+                        va[u] = ld_stream(ptr[u]);
+                        vb[u] = ld_stream(ptr[u] + pairs);
+                    } else {
+                        ptr[u] = base + p;
+                        const float2 a = *reinterpret_cast<const float2*>(ptr[u]);
+                        const float2 b = *reinterpret_cast<const float2*>(ptr[u] + pairs);
+                        va[u] = make_float4(a.x, a.y, b.x, b.y);
+                    }
+                }
+            }
+        };
+        auto rotate_store = [&]() {
+#pragma unroll
+            for (int u = 0; u < kU; ++u) {
+                if (!ptr[u]) continue;
+                const float4 t = va[u];
+                const float2 c0 = tab[slot[u]], c1 = tab[slot[u] + 1];
+                if constexpr (MODE == ROPE_IL4) {
+                    const float2 o0 = rope_rot(t.x, t.y, c0), o1 = rope_rot(t.z, t.w, c1);
+                    st_stream(ptr[u], make_float4(o0.x, o0.y, o1.x, o1.y));
+                } else if constexpr (MODE == ROPE_HS4) {
+                    const float2 c2 = tab[slot[u] + 2], c3 = tab[slot[u] + 3];
+                    const float4 b = vb[u];
+                    const float2 o0 = rope_rot(t.x, b.x, c0), o1 = rope_rot(t.y, b.y, c1);
+                    const float2 o2 = rope_rot(t.z, b.z, c2), o3 = rope_rot(t.w, b.w, c3);
+                    st_stream(ptr[u], make_float4(o0.x, o1.x, o2.x, o3.x));
+                    st_stream(ptr[u] + pairs, make_float4(o0.y, o1.y, o2.y, o3.y));
+                } else {
+                    // t = (a0, a1, b0, b1): pairs (a0, b0) at p and (a1, b1) at p + 1
+                    const float2 o0 = rope_rot(t.x, t.z, c0), o1 = rope_rot(t.y, t.w, c1);
+                    *reinterpret_cast<float2*>(ptr[u]) = make_float2(o0.x, o1.x);
+                    *reinterpret_cast<float2*>(ptr[u] + pairs) = make_float2(o0.y, o1.y);
+                }
+            }
+        };
+        const int step = kU * static_cast<int>(blockDim.x);
+        load(threadIdx.x);
+        make_table();
+        rotate_store();
+        for (int i0 = threadIdx.x + step; i0 < units; i0 += step) {
+            load(i0);
+            rotate_store();
         }
     }
 }
@@ -446,14 +477,21 @@ int rope(float* x, const int* pos_ids, int rows, int heads, int hd, int row_stri
     const int pairs = hd / 2;
     for (int p = 0; p < kRopeMaxPairs; ++p)
         fr.inv[p] = p < pairs ? 1.0 / std::pow(base, static_cast<double>(2 * p) / hd) : 0.0;
-    // vector units need pairs even (two pairs per unit) and 16-byte (interleaved)
-    // or 8-byte (half-split) aligned accesses
-    const bool pairs_even = pairs % 2 == 0;
-    const bool align = interleaved ? (row_stride % 4 == 0 && hd % 4 == 0 && aligned16(x))
-                                   : (row_stride % 2 == 0 && (reinterpret_cast<uintptr_t>(x) & 7u) == 0);
-    const int vec = pairs_even && align;
-    rope_kernel<<<ceil_div(rows, kRopeRowsPerBlock), 256, 0, s>>>(x, pos_ids, rows, heads, hd, row_stride, pos_offset,
-                                                                  period, interleaved, inverse, vec, fr);
+    // vector units: two pairs per float4 (interleaved), four pairs as two
+    // float4 (half-split, pairs % 4 == 0), or two pairs as two float2
+    // (half-split, 8-byte alignment); anything else takes scalar accesses
+    const bool il4 = interleaved && pairs % 2 == 0 && row_stride % 4 == 0 && hd % 4 == 0 && aligned16(x);
+    const bool hs4 = !interleaved && pairs % 4 == 0 && row_stride % 4 == 0 && aligned16(x);
+    const bool hs2 = !interleaved && pairs % 2 == 0 && row_stride % 2 == 0 &&
+                     (reinterpret_cast<uintptr_t>(x) & 7u) == 0;
+    const dim3 grid(ceil_div(rows, kRopeRowsPerBlock));
+#define LHIP_ROPE(M_) rope_kernel<M_><<<grid, 256, 0, s>>>(x, pos_ids, rows, heads, hd, row_stride, pos_offset, \
+                                                           period, interleaved, inverse, fr)
+    if (il4) LHIP_ROPE(ROPE_IL4);
+    else if (hs4) LHIP_ROPE(ROPE_HS4);
+    else if (hs2) LHIP_ROPE(ROPE_HS2);
+    else LHIP_ROPE(ROPE_SCALAR);
+#undef LHIP_ROPE
     return check_launch("rope");
 }
 

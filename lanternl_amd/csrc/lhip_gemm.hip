@@ -1231,6 +1231,7 @@ LHIP_API int lhip_matmul_host(int op, const double* a, const double* b, double* 
                               int m, int k, int n, int acc)
 {
     LHIP_REQUIRE_READY();
+    LHIP_REFUSE_RECORDING();
     if (op < 0 || op > 2) return fail(LHIP_E_ARG, "lhip_matmul_host: op %d not in {0,1,2}", op);
     if (m < 0 || k < 0 || n < 0) return fail(LHIP_E_SHAPE, "lhip_matmul_host: negative size");
     // Result shape and operand sizes per op.

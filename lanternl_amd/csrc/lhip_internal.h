@@ -34,6 +34,8 @@ struct State {
     // scratch for reductions of the immediate entry points (grown on demand)
     void* work = nullptr;
     size_t work_bytes = 0;
+    // a program (stream capture of the library stream) is being recorded
+    bool recording = false;
 };
 
 State& st();
@@ -47,6 +49,15 @@ int hip_fail(hipError_t e, const char* what);
     do {                                                                          \
         if (!::lhip::st().ready)                                                  \
             return ::lhip::fail(LHIP_E_DEVICE, "%s: library not initialised (call lhip_init)", __func__); \
+    } while (0)
+
+// Entry points that synchronise the stream, allocate or free memory, or read
+// results back to the host cannot be part of a recorded program.
+#define LHIP_REFUSE_RECORDING()                                                   \
+    do {                                                                          \
+        if (::lhip::st().recording)                                               \
+            return ::lhip::fail(LHIP_E_UNSUPPORTED,                               \
+                                "%s: not allowed while a program is being recorded", __func__); \
     } while (0)
 
 #define LHIP_CHECK_HIP(expr, what)                                                \
@@ -75,7 +86,8 @@ __device__ __forceinline__ void xcd_tile(int pid, int nwg, int tiles_n, int& tm,
 }
 
 // Library workspace of at least `bytes` (reused; growing it waits for the
-// stream, so it must not be called while a stream capture is in progress).
+// stream, so while a program is being recorded a call that would grow it fails
+// with LHIP_E_UNSUPPORTED).
 int workspace(size_t bytes, void** out);
 
 // Launchers shared by the immediate entry points and the LM step runner.  They

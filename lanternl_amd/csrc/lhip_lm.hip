@@ -563,6 +563,7 @@ LHIP_API int lhip_lm_param_offsets(const lhip_lm_config_t* cfg, long long* offse
 LHIP_API int lhip_lm_create(const lhip_lm_config_t* cfg, void** model)
 {
     LHIP_REQUIRE_READY();
+    LHIP_REFUSE_RECORDING();
     if (!model) return fail(LHIP_E_NULL, "lhip_lm_create: model is NULL");
     *model = nullptr;
     if (int rc = lhip::check_config(cfg)) return rc;
@@ -689,6 +690,7 @@ LHIP_API int lhip_lm_create(const lhip_lm_config_t* cfg, void** model)
 LHIP_API int lhip_lm_destroy(void* model)
 {
     if (!model) return LHIP_OK;
+    if (st().ready) LHIP_REFUSE_RECORDING();
     auto* m = lhip::as_model(model);
     if (st().ready) {
         (void)hipStreamSynchronize(st().stream);
@@ -702,6 +704,7 @@ LHIP_API int lhip_lm_destroy(void* model)
 static int lm_copy(void* model, float* host, long long n, int which, int to_device)
 {
     LHIP_REQUIRE_READY();
+    LHIP_REFUSE_RECORDING();
     if (!model || !host) return fail(LHIP_E_NULL, "lhip_lm: NULL argument");
     auto* m = lhip::as_model(model);
     if (n != m->nparam) return fail(LHIP_E_SHAPE, "lhip_lm: %lld values given, model has %lld", n, m->nparam);
@@ -733,6 +736,7 @@ LHIP_API int lhip_lm_get_velocity(void* model, float* host, long long n) { retur
 LHIP_API int lhip_lm_set_batch(void* model, const int* ids, const int* targets)
 {
     LHIP_REQUIRE_READY();
+    LHIP_REFUSE_RECORDING();
     if (!model || !ids || !targets) return fail(LHIP_E_NULL, "lhip_lm_set_batch: NULL argument");
     auto* m = lhip::as_model(model);
     for (int i = 0; i < m->N; ++i) {
@@ -754,6 +758,7 @@ LHIP_API int lhip_lm_set_batch(void* model, const int* ids, const int* targets)
 LHIP_API int lhip_lm_use_graph(void* model, int on)
 {
     LHIP_REQUIRE_READY();
+    LHIP_REFUSE_RECORDING();
     if (!model) return fail(LHIP_E_NULL, "lhip_lm_use_graph: model is NULL");
     auto* m = lhip::as_model(model);
     m->use_graph = on != 0;
@@ -768,6 +773,7 @@ LHIP_API int lhip_lm_step_sgd(void* model, float lr, float momentum, float weigh
                               int nesterov)
 {
     LHIP_REQUIRE_READY();
+    LHIP_REFUSE_RECORDING();
     if (!model) return fail(LHIP_E_NULL, "lhip_lm_step_sgd: model is NULL");
     auto* m = lhip::as_model(model);
     if (!m->have_batch) return fail(LHIP_E_ARG, "lhip_lm_step_sgd: no batch (call lhip_lm_set_batch)");
@@ -784,6 +790,7 @@ LHIP_API int lhip_lm_step_adamw(void* model, float lr, float beta1, float beta2,
                                 float clip_norm)
 {
     LHIP_REQUIRE_READY();
+    LHIP_REFUSE_RECORDING();
     if (!model) return fail(LHIP_E_NULL, "lhip_lm_step_adamw: model is NULL");
     auto* m = lhip::as_model(model);
     if (!m->have_batch) return fail(LHIP_E_ARG, "lhip_lm_step_adamw: no batch (call lhip_lm_set_batch)");
@@ -801,6 +808,7 @@ LHIP_API int lhip_lm_step_adamw(void* model, float lr, float beta1, float beta2,
 LHIP_API int lhip_lm_save(void* model, const char* path, const lhip_ckpt_info_t* info)
 {
     LHIP_REQUIRE_READY();
+    LHIP_REFUSE_RECORDING();
     if (!model) return fail(LHIP_E_NULL, "lhip_lm_save: model is NULL");
     auto* m = lhip::as_model(model);
     return lhip::lm_checkpoint_io(m->c, m->params, path, info, nullptr, true);
@@ -809,6 +817,7 @@ LHIP_API int lhip_lm_save(void* model, const char* path, const lhip_ckpt_info_t*
 LHIP_API int lhip_lm_load(void* model, const char* path, lhip_ckpt_header_t* header)
 {
     LHIP_REQUIRE_READY();
+    LHIP_REFUSE_RECORDING();
     if (!model) return fail(LHIP_E_NULL, "lhip_lm_load: model is NULL");
     auto* m = lhip::as_model(model);
     return lhip::lm_checkpoint_io(m->c, m->params, path, nullptr, header, false);
@@ -817,6 +826,7 @@ LHIP_API int lhip_lm_load(void* model, const char* path, lhip_ckpt_header_t* hea
 LHIP_API int lhip_lm_set_adam_state(void* model, const float* mom, const float* var, long long n, int step)
 {
     LHIP_REQUIRE_READY();
+    LHIP_REFUSE_RECORDING();
     if (!model) return fail(LHIP_E_NULL, "lhip_lm_set_adam_state: model is NULL");
     auto* m = lhip::as_model(model);
     if (n != m->nparam) return fail(LHIP_E_SHAPE, "lhip_lm_set_adam_state: %lld values given, model has %lld", n,
@@ -836,6 +846,7 @@ LHIP_API int lhip_lm_set_adam_state(void* model, const float* mom, const float* 
 LHIP_API int lhip_lm_get_adam_state(void* model, float* mom, float* var, long long n, int* step)
 {
     LHIP_REQUIRE_READY();
+    LHIP_REFUSE_RECORDING();
     if (!model) return fail(LHIP_E_NULL, "lhip_lm_get_adam_state: model is NULL");
     auto* m = lhip::as_model(model);
     if (n != m->nparam) return fail(LHIP_E_SHAPE, "lhip_lm_get_adam_state: %lld values asked, model has %lld", n,
@@ -855,6 +866,7 @@ LHIP_API int lhip_lm_get_adam_state(void* model, float* mom, float* var, long lo
 LHIP_API int lhip_lm_stats(void* model, lhip_lm_stats_t* out, float* window_losses, int nwin)
 {
     LHIP_REQUIRE_READY();
+    LHIP_REFUSE_RECORDING();
     if (!model || !out) return fail(LHIP_E_NULL, "lhip_lm_stats: NULL argument");
     auto* m = lhip::as_model(model);
     if (window_losses && nwin != m->B)
@@ -895,6 +907,7 @@ LHIP_API int lhip_lm_stats(void* model, lhip_lm_stats_t* out, float* window_loss
 LHIP_API int lhip_lm_get_argmax(void* model, int* host, int n)
 {
     LHIP_REQUIRE_READY();
+    LHIP_REFUSE_RECORDING();
     if (!model || !host) return fail(LHIP_E_NULL, "lhip_lm_get_argmax: NULL argument");
     auto* m = lhip::as_model(model);
     if (n != m->N) return fail(LHIP_E_SHAPE, "lhip_lm_get_argmax: n=%d, batch*seq=%d", n, m->N);

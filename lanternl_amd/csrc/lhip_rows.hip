@@ -45,16 +45,25 @@ __device__ __forceinline__ float4 ld_stream(const float4* p)
     return make_float4(v.x, v.y, v.z, v.w);
 }
 
+// 128-bit store of data this kernel writes once and does not read back
+// (non-temporal hint: streamed to memory instead of being kept dirty in L2,
+// which the end-of-kernel L2 write-back would otherwise have to flush).
+__device__ __forceinline__ void st_stream(float4* p, const float4& v)
+{
+    __builtin_nontemporal_store(vf4{v.x, v.y, v.z, v.w}, reinterpret_cast<vf4*>(p));
+}
+
 // Waves walk rows grid-stride (row += total waves) and prefetch their next
 // row into a second register set while they reduce and store the current
-// one, so that reads and writes of different rows overlap.  The grid is sized
-// to about two waves per SIMD, which keeps every wave busy to the end instead
-// of leaving a partial last round of one-row waves.
+// one, so that reads and writes of different rows overlap.  The grid is
+// capped at four workgroups (16 waves) per CU: up to 4 x 4 x CUs rows every
+// wave takes one row and all of them are in flight at once; beyond that the
+// waves walk and prefetch.
 inline int row_wave_blocks(int rows)
 {
     const int cus = st().cu_count > 0 ? st().cu_count : 256;
     int b = ceil_div(rows, kWavesPerBlock);
-    if (b > 2 * cus) b = 2 * cus;
+    if (b > 4 * cus) b = 4 * cus;
     return b < 1 ? 1 : b;
 }
 
@@ -122,7 +131,8 @@ rmsnorm_fwd_vec(const float* __restrict__ x, const float* __restrict__ w, float*
             const int c = lane + 64 * i;
             if (c < c4n) {
                 const float4 g = w4[c];
-                yr[c] = make_float4(r.v[i].x * rs * g.x, r.v[i].y * rs * g.y, r.v[i].z * rs * g.z, r.v[i].w * rs * g.w);
+                st_stream(yr + c, make_float4(r.v[i].x * rs * g.x, r.v[i].y * rs * g.y, r.v[i].z * rs * g.z,
+                                             r.v[i].w * rs * g.w));
             }
         }
         if (inv && lane == 0) inv[row] = rs;
@@ -210,7 +220,7 @@ rmsnorm_bwd_vec(const float* __restrict__ x, const float* __restrict__ w, const 
                     const float4 old = drr[c];
                     o.x += old.x; o.y += old.y; o.z += old.z; o.w += old.w;
                 }
-                dxr[c] = o;
+                st_stream(dxr + c, o);
             }
         }
     };
@@ -362,7 +372,7 @@ softmax_fwd_vec(const float* __restrict__ x, float* __restrict__ y, int rows, in
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const int c = lane + 64 * i;
-            if (c < c4n) yr[c] = make_float4(v[i].x * is, v[i].y * is, v[i].z * is, v[i].w * is);
+            if (c < c4n) st_stream(yr + c, make_float4(v[i].x * is, v[i].y * is, v[i].z * is, v[i].w * is));
         }
     };
     walk_rows<Row1<NV>>(rows, load, body);
@@ -436,7 +446,7 @@ softmax_bwd_vec(const float* __restrict__ y, const float* __restrict__ dy, float
                     const float4 old = dr[c];
                     o.x += old.x; o.y += old.y; o.z += old.z; o.w += old.w;
                 }
-                dr[c] = o;
+                st_stream(dr + c, o);
             }
         }
     };
@@ -509,7 +519,7 @@ ce_fused_vec(const float* logits, const int* __restrict__ tgt, float* __restrict
             if (losses && threadIdx.x == 0) losses[row] = 0.f;
             if (dlogits) {
                 float4* dr = reinterpret_cast<float4*>(dlogits + base);
-                for (int c = threadIdx.x; c < c4n; c += NT) dr[c] = f4zero();
+                for (int c = threadIdx.x; c < c4n; c += NT) st_stream(dr + c, f4zero());
             }
             return;
         }
@@ -545,7 +555,7 @@ ce_fused_vec(const float* logits, const int* __restrict__ tgt, float* __restrict
                         if (4 * c + e == t) p -= 1.f;
                         f4set(o, e, gscale * p);
                     }
-                    dr[c] = o;
+                    st_stream(dr + c, o);
                 }
             }
         }

@@ -138,3 +138,52 @@ class Timer:
             lib().lhip_event_destroy(self._b)
         except Exception:
             pass
+
+
+class Program:
+    """A recorded sequence of library calls, replayed as one hipGraph launch.
+
+    The counterpart of luaTL.Program's capture/replay
+    (ai/gpu/luaTL_train.lua:327-627): ``record(fn)`` runs ``fn()`` while the
+    library stream is being captured, so the compute calls fn makes are
+    recorded rather than executed; ``replay(times)`` enqueues the recording.
+    Calls that synchronise or allocate are refused while recording (run fn
+    once eagerly first so that the library workspace is already sized).
+    """
+
+    def __init__(self):
+        self._h = ctypes.c_void_p()
+
+    @classmethod
+    def record(cls, fn):
+        prog = cls()
+        call("lhip_program_begin")
+        try:
+            fn()
+        except BaseException:
+            lib().lhip_program_end(None)   # discard the partial recording
+            raise
+        call("lhip_program_end", ctypes.byref(prog._h))
+        return prog
+
+    def replay(self, times=1):
+        if not self._h.value:
+            raise RuntimeError("program has been freed")
+        call("lhip_program_replay", self._h, int(times))
+
+    def free(self):
+        if self._h is not None and self._h.value:
+            try:
+                lib().lhip_program_free(self._h)
+            finally:
+                self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def recording():
+    return bool(lib().lhip_is_recording())

@@ -179,8 +179,11 @@ def test_swiglu_closed_form_known_values():
 
 
 # ------------------------------------------------------------------ RoPE
+# access modes: interleaved float4 (hd % 4 == 0), half-split 2 x float4
+# (hd % 8 == 0), half-split 2 x float2 (hd 12), scalar (odd pair counts)
 @pytest.mark.parametrize("rows,heads,hd,interleaved", [(4096, 16, 64, 1), (4096, 16, 64, 0), (64, 8, 16, 1),
-                                                       (50, 3, 6, 1), (50, 3, 6, 0), (10, 2, 10, 0)])
+                                                       (50, 3, 6, 1), (50, 3, 6, 0), (10, 2, 10, 0),
+                                                       (33, 5, 12, 0), (33, 5, 12, 1), (9, 3, 256, 0)])
 def test_rope_vs_oracle_heads(rows, heads, hd, interleaved):
     announce("rope", rows, heads, hd, interleaved)
     rng = np.random.default_rng(rows + hd)
