@@ -13,6 +13,7 @@
 //   rmsnorm  :609-666   softmax_rows :332-408   cross_entropy :809-882
 // and the reference kernels' batched contracts (cuda/luaTL_train.cu):
 //   softmax_ex group-causal mask :545-619, fused CE :837-891, argmax :982-1018.
+#include <algorithm>
 #include <cmath>
 
 #include "lhip_internal.h"
@@ -56,24 +57,24 @@ __device__ __forceinline__ void st_stream(float4* p, const float4& v)
 // Waves walk rows grid-stride (row += total waves) and prefetch their next
 // row into a second register set while they reduce and store the current
 // one, so that reads and writes of different rows overlap.  The grid is
-// capped at four workgroups (16 waves) per CU: up to 4 x 4 x CUs rows every
-// wave takes one row and all of them are in flight at once; beyond that the
-// waves walk and prefetch.
+// capped at two workgroups (8 waves) per CU: on 4096 x 4096 softmax rows that
+// runs at 68% of HBM against 62% with one row per wave and 16 waves per CU
+// (all loads first, then all stores).
 inline int row_wave_blocks(int rows)
 {
     const int cus = st().cu_count > 0 ? st().cu_count : 256;
     int b = ceil_div(rows, kWavesPerBlock);
-    if (b > 4 * cus) b = 4 * cus;
+    if (b > 2 * cus) b = 2 * cus;
     return b < 1 ? 1 : b;
 }
 
 // Run body(buf, row) over this wave's rows with a one-row prefetch:
 // load(buf, row) fills a register set, body consumes it.
-template <class Regs, class Load, class Body>
+template <class Regs, int WPB = kWavesPerBlock, class Load, class Body>
 __device__ __forceinline__ void walk_rows(int rows, Load load, Body body)
 {
-    const int nw = gridDim.x * kWavesPerBlock;
-    int row = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+    const int nw = gridDim.x * WPB;
+    int row = blockIdx.x * WPB + (threadIdx.x >> 6);
     if (row >= rows) return;
     Regs a, b;
     load(a, row);
@@ -98,6 +99,7 @@ struct Row1 {
 template <int NV>
 struct Row2 {
     float4 v[NV], g[NV];
+    float r;   // per-row scalar loaded with the row (RMSNorm backward: 1/rms)
 };
 
 // ------------------------------------------------------------------ RMSNorm
@@ -160,15 +162,16 @@ rmsnorm_fwd_generic(const float* __restrict__ x, const float* __restrict__ w, fl
 // dx = g*w*r - x*(r^3/N)*sum_j(g_j w_j x_j)  (+ dres, the incoming residual
 // gradient, when given; dres may be dx itself);
 // per-block partial dw over the block's rows -> partial[block][cols], skipped
-// when partial is NULL (tensor2.lua:641-666).  Rows are walked grid-stride,
-// one wave per row.
-template <int NV>
-__global__ void __launch_bounds__(kRowThreads)
+// when partial is NULL (tensor2.lua:641-666).  NW waves per block, one row per
+// wave at a time, rows walked grid-stride with a one-row prefetch; the waves'
+// dw sums meet in LDS and are added in wave order.
+template <int NV, int NW>
+__global__ void __launch_bounds__(64 * NW)
 rmsnorm_bwd_vec(const float* __restrict__ x, const float* __restrict__ w, const float* __restrict__ inv,
                 const float* __restrict__ dy, float* dx, const float* dres, float* __restrict__ partial,
                 int rows, int cols)
 {
-    extern __shared__ float4 sdw[];   // [kWavesPerBlock][cols/4]
+    extern __shared__ float4 sdw[];   // [NW][cols/4]
     const int wv = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
     const int c4n = cols >> 2;
@@ -181,11 +184,11 @@ rmsnorm_bwd_vec(const float* __restrict__ x, const float* __restrict__ w, const 
         dwp[i] = f4zero();
     }
     const float inv_n = 1.0f / static_cast<float>(cols);
-    // rows walked with a one-row prefetch of x and dy (walk_rows)
     auto load = [&](Row2<NV>& rr, int row) {
         const size_t base = static_cast<size_t>(row) * cols;
         const float4* xr = reinterpret_cast<const float4*>(x + base);
         const float4* gr = reinterpret_cast<const float4*>(dy + base);
+        rr.r = inv[row];
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const int c = lane + 64 * i;
@@ -195,7 +198,7 @@ rmsnorm_bwd_vec(const float* __restrict__ x, const float* __restrict__ w, const 
     };
     auto body = [&](const Row2<NV>& rr, int row) {
         const size_t base = static_cast<size_t>(row) * cols;
-        const float r = inv[row];
+        const float r = rr.r;
         float dot = 0.f;
 #pragma unroll
         for (int i = 0; i < NV; ++i)
@@ -224,7 +227,7 @@ rmsnorm_bwd_vec(const float* __restrict__ x, const float* __restrict__ w, const 
             }
         }
     };
-    walk_rows<Row2<NV>>(rows, load, body);
+    walk_rows<Row2<NV>, NW>(rows, load, body);
     if (!partial) return;   // uniform: no dw wanted
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
@@ -233,10 +236,10 @@ rmsnorm_bwd_vec(const float* __restrict__ x, const float* __restrict__ w, const 
     }
     __syncthreads();
     float4* pr = reinterpret_cast<float4*>(partial + static_cast<size_t>(blockIdx.x) * cols);
-    for (int c = threadIdx.x; c < c4n; c += kRowThreads) {
+    for (int c = threadIdx.x; c < c4n; c += 64 * NW) {
         float4 s = sdw[c];
 #pragma unroll
-        for (int k = 1; k < kWavesPerBlock; ++k) {
+        for (int k = 1; k < NW; ++k) {
             const float4 t = sdw[k * c4n + c];
             s.x += t.x; s.y += t.y; s.z += t.z; s.w += t.w;
         }
@@ -284,6 +287,58 @@ struct ColsumJobs {
     float* out[kColsumJobs];
     int nparts[kColsumJobs];
 };
+
+// Float4 variant (cols % 4 == 0, 16-byte aligned partial rows and outputs):
+// 32 columns per block; thread (g, q) sums column quad q over the partial rows
+// g, g + 32, ... (eight loads in flight at a time), then the 32 group sums are
+// added in a fixed tree.  Deterministic.
+__global__ void __launch_bounds__(256)
+colsum4_kernel(const ColsumJobs jobs, int cols, int acc)
+{
+    __shared__ float4 red[32][8];
+    const float* __restrict__ partial = jobs.partial[blockIdx.y];
+    float* __restrict__ out = jobs.out[blockIdx.y];
+    const int nparts = jobs.nparts[blockIdx.y];
+    const int q = threadIdx.x & 7, g = threadIdx.x >> 3;
+    const int c = blockIdx.x * 32 + 4 * q;
+    float4 s = f4zero();
+    if (c < cols) {
+        int b = g;
+        for (; b + 7 * 32 < nparts; b += 8 * 32) {
+            float4 t[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                t[u] = *reinterpret_cast<const float4*>(partial + static_cast<size_t>(b + u * 32) * cols + c);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) { s.x += t[u].x; s.y += t[u].y; s.z += t[u].z; s.w += t[u].w; }
+        }
+        for (; b < nparts; b += 32) {
+            const float4 t = *reinterpret_cast<const float4*>(partial + static_cast<size_t>(b) * cols + c);
+            s.x += t.x; s.y += t.y; s.z += t.z; s.w += t.w;
+        }
+    }
+    red[g][q] = s;
+    __syncthreads();
+#pragma unroll
+    for (int half = 16; half > 0; half >>= 1) {
+        if (g < half) {
+            const float4 t = red[g + half][q];
+            float4 u = red[g][q];
+            u.x += t.x; u.y += t.y; u.z += t.z; u.w += t.w;
+            red[g][q] = u;
+        }
+        __syncthreads();
+    }
+    if (g == 0 && c < cols) {
+        float4 t = red[0][q];
+        float4* o = reinterpret_cast<float4*>(out + c);
+        if (acc) {
+            const float4 v = *o;
+            t.x += v.x; t.y += v.y; t.z += v.z; t.w += v.w;
+        }
+        *o = t;
+    }
+}
 
 __global__ void __launch_bounds__(256)
 colsum_kernel(const ColsumJobs jobs, int cols, int acc)
@@ -682,13 +737,23 @@ int rmsnorm_fwd(const float* x, const float* w, float* y, float* inv, int rows, 
     return check_launch("rmsnorm_fwd");
 }
 
-// Workgroups of the backward: each wave walks >= 4 rows, at most one block per CU.
-int rmsnorm_bwd_blocks(int rows)
+// Waves per workgroup of the register-resident backward: 8 for rows up to
+// 2048 floats, 4 up to 4096 (the waves' dw partials then fill at most 64 KB of
+// LDS, and two rows of x and dy -- the prefetch -- plus w and the dw sums fit a
+// wave's registers).  With one workgroup per CU, 8 waves walking two rows each
+// beat 16 waves taking one row each (all loads first, then all stores) by 25%
+// at 4096 x 1024.
+int rmsnorm_bwd_waves(int cols)
 {
-    // about 4 rows per wave, walked with a one-row prefetch; one block per CU
-    // at most, which bounds the dw partial rows (one per block) to the CUs
+    return nv_for(cols) == 16 ? 4 : 8;
+}
+
+// Workgroups of the backward: at most one per CU (which bounds the dw partial
+// rows, one per workgroup), each wave taking a row at a time.
+int rmsnorm_bwd_blocks(int rows, int waves)
+{
     const int cus = st().cu_count > 0 ? st().cu_count : 256;
-    int blocks = ceil_div(rows, 4 * kWavesPerBlock);
+    int blocks = ceil_div(rows, waves);
     if (blocks > cus) blocks = cus;
     return blocks < 1 ? 1 : blocks;
 }
@@ -697,8 +762,8 @@ int rmsnorm_bwd_blocks(int rows)
 // floats): one per block on the register-resident path, one per wave otherwise.
 int rmsnorm_bwd_parts(int rows, int cols)
 {
-    (void)cols;
-    return rmsnorm_bwd_blocks(rows) * kWavesPerBlock;
+    return std::max(rmsnorm_bwd_blocks(rows, rmsnorm_bwd_waves(cols)),
+                    rmsnorm_bwd_blocks(rows, kWavesPerBlock) * kWavesPerBlock);
 }
 
 int rmsnorm_bwd_rows(const float* x, const float* w, const float* inv, const float* dy, float* dx,
@@ -709,23 +774,25 @@ int rmsnorm_bwd_rows(const float* x, const float* w, const float* inv, const flo
     if (parts_out) *parts_out = 0;
     if (rows == 0) return LHIP_OK;
     if (!x || !w || !inv || !dy || !dx) return fail(LHIP_E_NULL, "rmsnorm_bwd: NULL argument");
-    const int blocks = rmsnorm_bwd_blocks(rows);
     const int nv = nv_for(cols);
     const bool vec = nv && cols % 4 == 0 && aligned16(x) && aligned16(w) && aligned16(dy) && aligned16(dx) &&
                      (!dres || aligned16(dres));
+    const int nw = vec ? rmsnorm_bwd_waves(cols) : kWavesPerBlock;
+    const int blocks = rmsnorm_bwd_blocks(rows, nw);
     const int parts = vec ? blocks : blocks * kWavesPerBlock;
     if (partial && static_cast<size_t>(parts) * cols > partial_floats)
         return fail(LHIP_E_CAPACITY, "rmsnorm_bwd: workspace of %zu floats < %lld needed", partial_floats,
                     static_cast<long long>(parts) * cols);
-    dim3 g(blocks), b(kRowThreads);
-    const size_t lds = static_cast<size_t>(kWavesPerBlock) * cols * sizeof(float);
-#define LHIP_RBV(NV_) rmsnorm_bwd_vec<NV_><<<g, b, lds, s>>>(x, w, inv, dy, dx, dres, partial, rows, cols)
-    if (!vec) rmsnorm_bwd_generic<<<g, b, 0, s>>>(x, w, inv, dy, dx, dres, partial, rows, cols);
-    else if (nv == 1) LHIP_RBV(1);
-    else if (nv == 2) LHIP_RBV(2);
-    else if (nv == 4) LHIP_RBV(4);
-    else if (nv == 8) LHIP_RBV(8);
-    else LHIP_RBV(16);
+    const dim3 g(blocks);
+    const size_t lds = static_cast<size_t>(nw) * cols * sizeof(float);
+#define LHIP_RBV(NV_, NW_) \
+    rmsnorm_bwd_vec<NV_, NW_><<<g, 64 * NW_, lds, s>>>(x, w, inv, dy, dx, dres, partial, rows, cols)
+    if (!vec) rmsnorm_bwd_generic<<<g, kRowThreads, 0, s>>>(x, w, inv, dy, dx, dres, partial, rows, cols);
+    else if (nv == 1) LHIP_RBV(1, 8);
+    else if (nv == 2) LHIP_RBV(2, 8);
+    else if (nv == 4) LHIP_RBV(4, 8);
+    else if (nv == 8) LHIP_RBV(8, 8);
+    else LHIP_RBV(16, 4);
 #undef LHIP_RBV
     if (parts_out) *parts_out = parts;
     return check_launch("rmsnorm_bwd");
@@ -751,7 +818,10 @@ int rmsnorm_bwd_colsum_multi(const float* const* partials, const int* parts, flo
         ++n;
     }
     if (n == 0) return LHIP_OK;
-    colsum_kernel<<<dim3(ceil_div(cols, 32), n), 256, 0, s>>>(jobs, cols, accumulate);
+    bool vec = cols % 4 == 0;
+    for (int i = 0; i < n; ++i) vec = vec && aligned16(jobs.partial[i]) && aligned16(jobs.out[i]);
+    if (vec) colsum4_kernel<<<dim3(ceil_div(cols, 32), n), 256, 0, s>>>(jobs, cols, accumulate);
+    else colsum_kernel<<<dim3(ceil_div(cols, 32), n), 256, 0, s>>>(jobs, cols, accumulate);
     return check_launch("rmsnorm_bwd: dw reduce");
 }
 
