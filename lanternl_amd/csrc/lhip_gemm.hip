@@ -132,6 +132,7 @@ struct GemmArgs {
     int Kb;                           // batch-reduce: K = kblocks * Kb, block j reads A + j*sAk, B + j*sBk
     long long sAk, sBk;
     int skip_reduce;                  // split-K slices stay in ws for the caller to sum
+    size_t ws_floats_avail;           // floats available at ws (skinny path's split plan)
 };
 
 // C = alpha * sum_s ws[s] + beta * R, the slices summed in order (deterministic).
@@ -157,6 +158,41 @@ splitk_reduce(const GemmArgs g, int batch)
         } else {
             *dst = v;
         }
+    }
+}
+
+// Float4 form of splitk_reduce for batch 1 (N % 4 == 0, ldc % 4 == 0 and
+// 16-byte aligned C, R): four columns per thread, the slices' loads issued
+// eight at a time, summed in slice order.
+__global__ void __launch_bounds__(256)
+splitk_reduce4(const GemmArgs g)
+{
+    const long long mn4 = static_cast<long long>(g.M) * g.N / 4;
+    const long long stride = static_cast<long long>(gridDim.x) * blockDim.x;
+    const int n4 = g.N / 4;
+    for (long long idx = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x; idx < mn4; idx += stride) {
+        const int row = static_cast<int>(idx / n4), col = 4 * static_cast<int>(idx - static_cast<long long>(row) * n4);
+        const float4* src = reinterpret_cast<const float4*>(g.ws) + idx;
+        float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
+        int p = 0;
+        for (; p + 8 <= g.splits; p += 8) {
+            float4 t[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) t[u] = src[(p + u) * mn4];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) { sum.x += t[u].x; sum.y += t[u].y; sum.z += t[u].z; sum.w += t[u].w; }
+        }
+        for (; p < g.splits; ++p) {
+            const float4 t = src[p * mn4];
+            sum.x += t.x; sum.y += t.y; sum.z += t.z; sum.w += t.w;
+        }
+        float4* dst = reinterpret_cast<float4*>(g.C + static_cast<long long>(row) * g.ldc + col);
+        float4 v = make_float4(g.alpha * sum.x, g.alpha * sum.y, g.alpha * sum.z, g.alpha * sum.w);
+        if (g.beta != 0.f) {
+            const float4 r = g.R ? *reinterpret_cast<const float4*>(g.R + static_cast<long long>(row) * g.ldr + col) : *dst;
+            v.x += g.beta * r.x; v.y += g.beta * r.y; v.z += g.beta * r.z; v.w += g.beta * r.w;
+        }
+        *dst = v;
     }
 }
 
@@ -695,6 +731,245 @@ sgemm_small_kernel(const GemmArgs g)
 }
 
 // ---------------------------------------------------------------------------
+// Skinny products (M <= 16 rows of C, B stored K x N): the work is one
+// streaming pass over B, HBM-bound.  With one or two rows of C this VALU form
+// streams B (2 to 4 FMAs per float4 of B); three to sixteen rows take the MFMA
+// form below, since at 16 rows the 64 FMAs per float4 outrun the VALU (packed
+// fp32 is not used).  Each wave covers 256 columns with one float4 per lane.  The workgroup walks its K slice in chunks of kSkinnyKC
+// rows: the chunk of A is staged in LDS as [k][m] (zero past M and past the
+// slice), then wave w streams rows [w*KC/4, (w+1)*KC/4) of the chunk, U rows of
+// B in flight, reading the M values of A of a row as broadcast LDS reads.
+// Waves 1..3 hand their sums to wave 0 through LDS, added in wave order.  A K
+// split over blockIdx.y writes [split][M][N] partials that splitk_reduce adds
+// in split order.
+constexpr int kSkinnyMax = 16;
+constexpr int kSkinnyCols = 256;    // columns per workgroup (64 lanes x float4)
+constexpr int kSkinnyKC = 256;      // K rows of A staged per chunk
+
+template <int MS, bool TA, bool VEC>
+__global__ void __launch_bounds__(256)
+sgemm_skinny_kernel(const GemmArgs g)
+{
+    constexpr int U = MS >= 8 ? 4 : 8;
+    constexpr int KC = kSkinnyKC;
+    static_assert(KC % (4 * U) == 0, "a chunk must split into whole U-row steps per wave");
+    constexpr int kRed = 3 * MS * 64;                    // float4s: waves 1..3 x MS rows x 64 lanes
+    constexpr int kTab = KC * MS / 4;                    // float4s: A chunk [KC][MS]
+    __shared__ float4 smem[kRed > kTab ? kRed : kTab];
+    float* atab = reinterpret_cast<float*>(smem);
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int M = g.M, N = g.N;
+    const int n0 = blockIdx.x * kSkinnyCols + 4 * lane;
+    const int k0 = blockIdx.y * g.kchunk;
+    const int k1 = min(g.K, k0 + g.kchunk);
+    const bool colfull = VEC && n0 + 3 < N;
+    float4 acc[MS];
+#pragma unroll
+    for (int m = 0; m < MS; ++m) acc[m] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int kc0 = k0; kc0 < k1; kc0 += KC) {
+        const int nk = min(KC, k1 - kc0);
+        for (int i = tid; i < KC * MS; i += 256) {
+            const int c = TA ? i / MS : i % KC;
+            const int m = TA ? i % MS : i / KC;
+            float v = 0.f;
+            if (c < nk && m < M)
+                v = TA ? g.A[static_cast<long long>(kc0 + c) * g.lda + m]
+                       : g.A[static_cast<long long>(m) * g.lda + kc0 + c];
+            atab[c * MS + m] = v;
+        }
+        __syncthreads();
+        const int rpw = (nk + 4 * U - 1) / (4 * U) * U;   // rows per wave in this chunk
+        const int rb = wv * rpw;
+        const int re = min(rb + rpw, nk);
+        for (int r = rb; r < re; r += U) {
+            float4 b[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                b[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (r + u < re) {
+                    const float* src = g.B + static_cast<long long>(kc0 + r + u) * g.ldb + n0;
+                    if (colfull) {
+                        const floatx4 v = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(src));
+                        b[u] = make_float4(v.x, v.y, v.z, v.w);
+                    } else {
+                        b[u].x = n0 + 0 < N ? src[0] : 0.f;
+                        b[u].y = n0 + 1 < N ? src[1] : 0.f;
+                        b[u].z = n0 + 2 < N ? src[2] : 0.f;
+                        b[u].w = n0 + 3 < N ? src[3] : 0.f;
+                    }
+                }
+            }
+            // rows past the slice hold zeros in both atab and b
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                float a[MS];
+                const float* arow = atab + (r + u) * MS;
+                if constexpr (MS >= 4) {
+#pragma unroll
+                    for (int q = 0; q < MS / 4; ++q) {
+                        const float4 t = reinterpret_cast<const float4*>(arow)[q];
+                        a[4 * q] = t.x; a[4 * q + 1] = t.y; a[4 * q + 2] = t.z; a[4 * q + 3] = t.w;
+                    }
+                } else {
+#pragma unroll
+                    for (int m = 0; m < MS; ++m) a[m] = arow[m];
+                }
+#pragma unroll
+                for (int m = 0; m < MS; ++m) {
+                    acc[m].x += a[m] * b[u].x;
+                    acc[m].y += a[m] * b[u].y;
+                    acc[m].z += a[m] * b[u].z;
+                    acc[m].w += a[m] * b[u].w;
+                }
+            }
+        }
+        __syncthreads();   // atab is rewritten by the next chunk (and reused below)
+    }
+    if (wv > 0) {
+#pragma unroll
+        for (int m = 0; m < MS; ++m) smem[((wv - 1) * MS + m) * 64 + lane] = acc[m];
+    }
+    __syncthreads();
+    if (wv != 0) return;
+#pragma unroll
+    for (int m = 0; m < MS; ++m) {
+#pragma unroll
+        for (int w = 0; w < 3; ++w) {
+            const float4 t = smem[(w * MS + m) * 64 + lane];
+            acc[m].x += t.x; acc[m].y += t.y; acc[m].z += t.z; acc[m].w += t.w;
+        }
+    }
+    const bool split = g.splits > 1;
+    float* base = split ? g.ws + static_cast<long long>(blockIdx.y) * M * N : g.C;
+    const int ld = split ? N : g.ldc;
+    const bool vst = colfull && (split ? (N % 4 == 0) : (g.ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(g.C) & 15u) == 0));
+#pragma unroll
+    for (int m = 0; m < MS; ++m) {
+        if (m < M) {
+            float v[4] = {acc[m].x, acc[m].y, acc[m].z, acc[m].w};
+            float* dst = base + static_cast<long long>(m) * ld + n0;
+            if (!split) {
+                const float* rr = g.R ? g.R + static_cast<long long>(m) * g.ldr + n0 : dst;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (n0 + e < N) v[e] = g.alpha * v[e] + (g.beta != 0.f ? g.beta * rr[e] : 0.f);
+            }
+            if (vst) {
+                *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (n0 + e < N) dst[e] = v[e];
+            }
+        }
+    }
+}
+
+// Skinny products with 3..16 rows of C on the matrix cores.  The VALU form
+// above would spend up to 64 FMAs per float4 of B, more than the VALU issues at
+// HBM rate; v_mfma_f32_16x16x4f32 covers 16 rows at once.  Each wave covers 64
+// columns: lane (q = l/16, p = l%16) loads the float4 B[k][c0+4p .. c0+4p+3] of
+// row k = k0 + 4s + q of step s (four 256-byte row segments per step), and MFMA
+// e (e = 0..3) multiplies element e of it, so MFMA e computes the columns
+// c0 + 4p + e with A[p][k] as its A operand (zero for p >= M).  Accumulator
+// register r of MFMA e then holds C[4q + r][c0 + 4p + e]: each lane owns a 4x4
+// block, stored as four float4 rows.  Waves take the 4-row steps w, w+4, ...
+// of the workgroup's K slice, U steps in flight, and hand their sums to wave 0
+// through LDS (added in wave order).  Splits as in the VALU form.
+constexpr int kSkinnyMfmaCols = 64;
+
+template <bool TA, bool VEC>
+__global__ void __launch_bounds__(256)
+sgemm_skinny_mfma_kernel(const GemmArgs g)
+{
+    constexpr int U = 8;
+    __shared__ floatx4 red[3][4][64];
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int p = lane & 15, q = lane >> 4;
+    const int M = g.M, N = g.N;
+    const int col = blockIdx.x * kSkinnyMfmaCols + 4 * p;
+    const int k0 = blockIdx.y * g.kchunk;
+    const int k1 = min(g.K, k0 + g.kchunk);
+    const bool colfull = VEC && col + 3 < N;
+    const bool mok = p < M;
+    const int nsteps = (k1 - k0 + 3) / 4;
+    floatx4 acc[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int s0 = wv; s0 < nsteps; s0 += 4 * U) {
+        float4 b[U];
+        float a[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int kk = k0 + 4 * (s0 + 4 * u) + q;
+            b[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+            a[u] = 0.f;
+            if (kk < k1) {
+                const float* src = g.B + static_cast<long long>(kk) * g.ldb + col;
+                if (colfull) {
+                    const floatx4 v = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(src));
+                    b[u] = make_float4(v.x, v.y, v.z, v.w);
+                } else {
+                    b[u].x = col + 0 < N ? src[0] : 0.f;
+                    b[u].y = col + 1 < N ? src[1] : 0.f;
+                    b[u].z = col + 2 < N ? src[2] : 0.f;
+                    b[u].w = col + 3 < N ? src[3] : 0.f;
+                }
+                if (mok)
+                    a[u] = TA ? g.A[static_cast<long long>(kk) * g.lda + p] : g.A[static_cast<long long>(p) * g.lda + kk];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (s0 + 4 * u < nsteps) {     // uniform
+                acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u], b[u].x, acc[0], 0, 0, 0);
+                acc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u], b[u].y, acc[1], 0, 0, 0);
+                acc[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u], b[u].z, acc[2], 0, 0, 0);
+                acc[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u], b[u].w, acc[3], 0, 0, 0);
+            }
+        }
+    }
+    if (wv > 0) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) red[wv - 1][e][lane] = acc[e];
+    }
+    __syncthreads();
+    if (wv != 0) return;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+#pragma unroll
+        for (int w = 0; w < 3; ++w) acc[e] += red[w][e][lane];
+    }
+    const bool split = g.splits > 1;
+    float* base = split ? g.ws + static_cast<long long>(blockIdx.y) * M * N : g.C;
+    const int ld = split ? N : g.ldc;
+    const bool vst = colfull && (split ? (N % 4 == 0) : (g.ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(g.C) & 15u) == 0));
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int row = 4 * q + r;
+        if (row >= M) continue;
+        float v[4] = {acc[0][r], acc[1][r], acc[2][r], acc[3][r]};
+        float* dst = base + static_cast<long long>(row) * ld + col;
+        if (!split) {
+            const float* rr = g.R ? g.R + static_cast<long long>(row) * g.ldr + col : dst;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (col + e < N) v[e] = g.alpha * v[e] + (g.beta != 0.f ? g.beta * rr[e] : 0.f);
+        }
+        if (vst) {
+            *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (col + e < N) dst[e] = v[e];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Tiny problems (fewer 32x32 output tiles than CUs, e.g. the 512x128 outputs
 // of the C2 step): one workgroup per 16x16 output tile, four times as many
 // workgroups as the 32x32 kernel, so the fp32 MFMA work (64 cycles per
@@ -906,6 +1181,70 @@ int launch_small(int ta, int tb, GemmArgs g, int batch, hipStream_t stream)
     return launch_reduce(g, batch, stream);
 }
 
+// Skinny path: M <= 16, B not transposed, one product (no batch, no
+// batch-reduce), at least one full wave of columns.
+bool skinny_ok(int ta, int tb, int m, int n, int batch, int kblocks)
+{
+    (void)ta;
+    return !tb && m >= 1 && m <= kSkinnyMax && n >= kSkinnyCols && batch == 1 && kblocks == 1;
+}
+
+// Rows of C up to which the VALU form is used; 3..16 rows take the MFMA form.
+constexpr int kSkinnyValuMax = 2;
+
+// K slices of the skinny path: about two workgroups per CU, at least 64 K rows
+// per workgroup, and partials (written, then read back by the reduce) at most
+// a quarter of B's bytes: 2 * s * m * n <= k * n / 4.
+int skinny_plan(int m, int n, int k, size_t ws_floats, int* kchunk_out)
+{
+    const int cus = st().cu_count > 0 ? st().cu_count : 256;
+    const long long cb = ceil_div(n, m <= kSkinnyValuMax ? kSkinnyCols : kSkinnyMfmaCols);
+    long long s = (2LL * cus + cb - 1) / cb;
+    s = std::min<long long>(s, k / 64);
+    s = std::min<long long>(s, std::max<long long>(1, k / (8LL * m)));
+    const long long mn = static_cast<long long>(m) * n;
+    if (mn > 0) s = std::min<long long>(s, static_cast<long long>(ws_floats / mn));
+    if (s < 2) {
+        *kchunk_out = k;
+        return 1;
+    }
+    const int kchunk = ceil_div(ceil_div(k, s), 4) * 4;
+    *kchunk_out = kchunk;
+    return ceil_div(k, kchunk);
+}
+
+template <bool TA, bool VEC>
+void launch_skinny_t(const GemmArgs& g, dim3 grid, hipStream_t stream)
+{
+    if (g.M == 1) sgemm_skinny_kernel<1, TA, VEC><<<grid, 256, 0, stream>>>(g);
+    else sgemm_skinny_kernel<2, TA, VEC><<<grid, 256, 0, stream>>>(g);
+}
+
+int launch_skinny(int ta, GemmArgs g, hipStream_t stream)
+{
+    g.kchunk = g.K;
+    g.splits = g.ws ? skinny_plan(g.M, g.N, g.K, g.ws_floats_avail, &g.kchunk) : 1;
+    if (g.splits <= 1) { g.splits = 1; g.kchunk = g.K; }
+    const bool vec = g.vecB;
+    if (g.M <= kSkinnyValuMax) {
+        const dim3 grid(ceil_div(g.N, kSkinnyCols), g.splits);
+        if (ta) { if (vec) launch_skinny_t<true, true>(g, grid, stream); else launch_skinny_t<true, false>(g, grid, stream); }
+        else { if (vec) launch_skinny_t<false, true>(g, grid, stream); else launch_skinny_t<false, false>(g, grid, stream); }
+    } else {
+        const dim3 grid(ceil_div(g.N, kSkinnyMfmaCols), g.splits);
+        if (ta) {
+            if (vec) sgemm_skinny_mfma_kernel<true, true><<<grid, 256, 0, stream>>>(g);
+            else sgemm_skinny_mfma_kernel<true, false><<<grid, 256, 0, stream>>>(g);
+        } else {
+            if (vec) sgemm_skinny_mfma_kernel<false, true><<<grid, 256, 0, stream>>>(g);
+            else sgemm_skinny_mfma_kernel<false, false><<<grid, 256, 0, stream>>>(g);
+        }
+    }
+    int rc = check_launch("sgemm (skinny): kernel launch");
+    if (rc != LHIP_OK || g.splits <= 1) return rc;
+    return launch_reduce(g, 1, stream);
+}
+
 template <int BM, int BN, int BK>
 int launch_cfg(int ta, int tb, GemmArgs g, int batch, hipStream_t stream)
 {
@@ -926,6 +1265,16 @@ int launch_cfg(int ta, int tb, GemmArgs g, int batch, hipStream_t stream)
 
 int launch_reduce(const GemmArgs& g, int batch, hipStream_t stream)
 {
+    const bool vec4 = batch == 1 && g.N % 4 == 0 && g.ldc % 4 == 0 && aligned16(g.C) && aligned16(g.ws) &&
+                      (!g.R || (g.ldr % 4 == 0 && aligned16(g.R)));
+    if (vec4) {
+        const long long total4 = static_cast<long long>(g.M) * g.N / 4;
+        long long rg = (total4 + 255) / 256;
+        const long long cap = static_cast<long long>(st().cu_count > 0 ? st().cu_count : 256) * 4;
+        if (rg > cap) rg = cap;
+        splitk_reduce4<<<static_cast<int>(rg), 256, 0, stream>>>(g);
+        return check_launch("sgemm: split-K reduce");
+    }
     const long long total = static_cast<long long>(g.M) * g.N * batch;
     long long rg = (total + 255) / 256;
     const long long cap = static_cast<long long>(st().cu_count > 0 ? st().cu_count : 256) * 4;
@@ -1126,6 +1475,11 @@ int sgemm_run(int ta, int tb, int m, int n, int k, float alpha,
     // small (fewer 64x64 tiles than CUs): 32x32 tiles with K shared by the
     // four waves of a workgroup, split over workgroups when K is very long
     // (split-K partials in o.ws).
+    if (skinny_ok(ta, tb, m, n, batch, br ? o.kblocks : 1) && !o.splits_out && k > 0) {
+        g.ws = o.ws;
+        g.ws_floats_avail = o.ws ? o.ws_floats : 0;
+        return launch_skinny(ta, g, stream);
+    }
     const long long tiles256 = static_cast<long long>(ceil_div(m, kBig)) * ceil_div(n, kBig) * batch;
     if (tiles256 >= cus) return launch_256(ta, tb, g, batch, stream);
     if (big_tiles >= cus) return launch_cfg<128, 128, 32>(ta, tb, g, batch, stream);
@@ -1172,7 +1526,10 @@ static int sgemm_immediate(int transa, int transb, int m, int n, int k, float al
     o.inner = batch > 0 ? batch : 1;
     int kchunk = 0;
     if (m > 0 && n > 0 && k > 0 && batch > 0) {
-        const int splits = lhip::splitk_plan(m, n, k, batch, static_cast<size_t>(1) << 26, &kchunk);
+        const size_t cap = static_cast<size_t>(1) << 26;
+        const int splits = lhip::skinny_ok(transa, transb, m, n, batch, 1)
+                               ? lhip::skinny_plan(m, n, k, cap, &kchunk)
+                               : lhip::splitk_plan(m, n, k, batch, cap, &kchunk);
         if (splits > 1) {
             o.ws_floats = static_cast<size_t>(splits) * m * n * batch;
             int rc = lhip::workspace(o.ws_floats * sizeof(float), reinterpret_cast<void**>(&o.ws));

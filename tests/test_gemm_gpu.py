@@ -360,3 +360,39 @@ def test_gemm_256_tile_path(m, n, k, batch, ld_pad):
             assert rel_fro(got[z, :, :n], ref[z]) <= TOL, (ta, tb, z)
         if ld_pad:
             assert np.isnan(got[:, :, n:]).all(), "wrote outside the n columns"
+
+
+# ------------------------------------------------------------ skinny products
+# M <= 16 with B stored K x N take the streaming kernel (one pass over B,
+# K split into slices summed in order); edge columns, unaligned leading
+# dimensions, transposed A, alpha/beta and K shorter than a slice are covered.
+@pytest.mark.parametrize("m,k,n", [(1, 4096, 4096), (16, 4096, 4096), (1, 7, 256), (2, 64, 300),
+                                   (3, 1000, 513), (5, 333, 1024), (8, 4097, 257), (13, 129, 777),
+                                   (16, 64, 256), (11, 2, 4096)])
+def test_gemm_skinny_vs_oracle(m, k, n):
+    announce("gemm skinny", m, k, n)
+    rng = np.random.default_rng(7000 + m * 11 + k + n)
+    a = f32(rng.uniform(-1, 1, (m, k)))
+    b = f32(rng.uniform(-1, 1, (k, n)))
+    ref = a @ b if k * n > 1 << 22 else O.mm(a, b)
+    assert rel_fro(_gemm(False, False, a, b), ref) <= TOL
+    at = np.ascontiguousarray(a.T)
+    assert rel_fro(_gemm(True, False, at, b), ref) <= TOL
+    c0 = f32(rng.uniform(-1, 1, (m, n)))
+    assert rel_fro(_gemm(False, False, a, b, alpha=0.5, beta=-2.0, c0=c0), 0.5 * ref - 2.0 * c0) <= TOL
+
+
+def test_gemm_skinny_strided_views_and_matrix_multiply_gate():
+    """Skinny shapes through strided views (scalar B loads) and ldc > n."""
+    announce("gemm skinny strided")
+    rng = np.random.default_rng(71)
+    big_a = f32(rng.uniform(-1, 1, (9, 803)))
+    big_b = f32(rng.uniform(-1, 1, (801, 611)))
+    A, B = to_dev(big_a), to_dev(big_b)
+    m, k, n = 7, 799, 601
+    C = device.Buffer((m, 605))
+    kernels.sgemm_raw(0, 0, m, n, k, 1.0, A.offset(1 * 803 + 2), 803, B.offset(1 * 611 + 3), 611, 0.0, C.ptr, 605)
+    device.sync()
+    got = C.download()[:, :n]
+    ref = O.mm(np.ascontiguousarray(big_a[1:1 + m, 2:2 + k]), np.ascontiguousarray(big_b[1:1 + k, 3:3 + n]))
+    assert rel_fro(got, ref) <= TOL
