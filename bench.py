@@ -4,8 +4,8 @@
 Default workload ("C2"): one full LMTrain step --
 forward, cross-entropy, backward and the SGD update -- for vocab 2000, dim 128,
 4 layers, 8 heads, ffn 256, 8 windows x 64 tokens, resident on the GPU,
-launched on the step stream and the weight-gradient stream (`--graph`:
-replayed from a captured hipGraph instead).  Prints ONE JSON line: steps/s, a `roofline` object
+launched eagerly on the library stream (`--graph`: replayed from a captured
+hipGraph instead).  Prints ONE JSON line: steps/s, a `roofline` object
 for the step's dominant kernel (timed live with hipEvents on the library
 stream), and a `cpu_baseline` object (the CPU oracle -- a single-threaded C
 restatement of lanternl's pure-Lua loops in double -- timed on this host).
@@ -192,7 +192,7 @@ def run_lm_workload(args):
         "data": "synthetic: token ids/targets uniform in [0,2000), weights N(0,0.02), gains 1",
         "config": {"workload": "lmtrain_step_c2 (BASELINE configs[1]): one SGD step, fwd+CE+bwd+update",
                    **C2, "optimizer": "sgd(lr=0.1, momentum=0.9, wd=0.01, clip=1.0)",
-                   "graph_replay": bool(args.graph), "streams": 2},
+                   "graph_replay": bool(args.graph), "streams": 1},
         "step_gemm_tflops": flops / (ms * 1e-3) / 1e12,
         "last_step": {"loss": st["loss"], "grad_norm": st["grad_norm"], "applied": st["applied"]},
         "roofline": {"bound": "mfma", "achieved": dom["tflops"], "peak": PEAK_FP32_MFMA_TFLOPS,
@@ -360,8 +360,8 @@ def main():
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--workload", default="lmtrain_c2", choices=["lmtrain_c2", "gemm4096"])
     p.add_argument("--graph", action="store_true",
-                   help="replay the LM step from a captured hipGraph (default: eager launches on the step and "
-                        "weight-gradient streams, faster on ROCm for this two-stream step)")
+                   help="replay the LM step from a captured hipGraph (default: eager launches on the library "
+                        "stream)")
     p.add_argument("--suite", default=None, choices=["gemm", "bandwidth", "copy"])
     p.add_argument("--only", default=None, help="bandwidth suite: run only kernels whose name contains this")
     args = p.parse_args()

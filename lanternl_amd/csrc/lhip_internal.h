@@ -108,7 +108,7 @@ int rmsnorm_bwd_rows(const float* x, const float* w, const float* inv, const flo
                      hipStream_t s);
 int rmsnorm_bwd_colsum(const float* partial, int parts, float* dw, int cols, int accumulate, hipStream_t s);
 // several independent column sums in one launch (jobs with parts <= 0 are skipped)
-constexpr int kColsumJobs = 4;
+constexpr int kColsumJobs = 16;
 int rmsnorm_bwd_colsum_multi(const float* const* partials, const int* parts, float* const* dws, int njobs, int cols,
                              int accumulate, hipStream_t s);
 int softmax_fwd(const float* x, float* y, int rows, int cols, float scale, int causal, int offset, int group,
@@ -215,7 +215,7 @@ struct GemmOpts {
 
 // Grouped C_g = A_g^T . B_g (A_g stored K x M_g, B_g stored K x N_g, beta 0)
 // for up to kGroupedMax products sharing K, in one launch of 16x16 tiles.
-constexpr int kGroupedMax = 8;
+constexpr int kGroupedMax = 32;
 struct GroupedTN {
     const float* A; int lda;
     const float* B; int ldb;

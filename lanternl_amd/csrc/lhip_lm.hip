@@ -76,17 +76,12 @@ struct LmModel {
     float *xf = nullptr, *invf = nullptr, *logits = nullptr;
     // backward: gradient-chain buffers are per layer (gx[l] = dL/dx_l,
     // gmid[l] = dL/dxmid_l, dzu[l], dqkv[l], the dw partials of each norm) so
-    // that nothing the side stream reads is overwritten within a step
+    // that the weight gradients, issued after the whole chain, still find them
     float *dxf = nullptr, *gx = nullptr, *gmid = nullptr, *da = nullptr, *dzu = nullptr, *dh2 = nullptr;
     float *dctx = nullptr, *dP = nullptr, *dS = nullptr, *dqkv = nullptr, *dh = nullptr, *work = nullptr;
     size_t work_floats = 0;       // per norm call; work holds 2L+1 of them
-    float* splitk = nullptr;      // split-K partials: first half main stream, second half side stream
-    size_t splitk_floats = 0;     // per stream
-    // The weight gradients (dW GEMMs, norm-gain column sums, embedding) run on
-    // a side stream forked from and joined back into the step stream with
-    // events; captured together into the graph.
-    hipStream_t side = nullptr;
-    std::vector<hipEvent_t> ev;
+    float* splitk = nullptr;      // split-K partials
+    size_t splitk_floats = 0;
     float2* rope_cs = nullptr;    // (cos, sin) of positions 0..T-1, pairs 0..hd/2-1
     bool fused_attn = false;      // per-(window, head) fused attention kernels
     bool fused_gemm = false;      // norm / SwiGLU stages fused into their GEMMs
@@ -139,7 +134,7 @@ int check_config(const lhip_lm_config_t* c)
 struct Enq {
     LmModel& m;
     hipStream_t s;
-    float* ws;   // split-K partials owned by this stream
+    float* ws;   // split-K partials
 
     GemmOpts opts(int inner = 1) const
     {
@@ -195,32 +190,10 @@ struct Enq {
         if (_rc != LHIP_OK) return _rc;    \
     } while (0)
 
-// Event fork/join between the step stream and the side stream.  Every fork
-// uses a fresh event, so the same code serves eager launches and capture.
-struct Forker {
-    LmModel& m;
-    hipStream_t main;
-    size_t next = 0;
-
-    int link(hipStream_t from, hipStream_t to)
-    {
-        if (next >= m.ev.size()) return fail(LHIP_E_CAPACITY, "lm: out of step events");
-        hipEvent_t e = m.ev[next++];
-        LHIP_CHECK_HIP(hipEventRecord(e, from), "lm: event record");
-        LHIP_CHECK_HIP(hipStreamWaitEvent(to, e, 0), "lm: stream wait");
-        return LHIP_OK;
-    }
-    int fork() { return link(main, m.side); }   // side waits for all main-stream work so far
-    int join() { return link(m.side, main); }   // main waits for all side-stream work so far
-};
-
 // device_hyper: read the hyper-parameters from m.hyper (captured steps)
 int enqueue_step(LmModel& m, hipStream_t s, const Hyper& hp, bool device_hyper)
 {
     const Enq q{m, s, m.splitk};
-    const Enq q2{m, m.side, m.splitk + m.splitk_floats};
-    Forker fk{m, s};
-    const hipStream_t s2 = m.side;
     const int N = m.N, D = m.D, F = m.F, V = m.V, H = m.H, hd = m.hd, T = m.T, L = m.L;
     const long long ND = static_cast<long long>(N) * D, NF = static_cast<long long>(N) * F;
     const long long TT = static_cast<long long>(T) * T, HTT = H * TT, TD = static_cast<long long>(T) * D;
@@ -304,14 +277,13 @@ int enqueue_step(LmModel& m, hipStream_t s, const Hyper& hp, bool device_hyper)
     LM_TRY(ce_fused(m.logits, m.tgt, m.losses, m.logits, N, V, -1, 1.0f / T, s, m.amax));
 
     // ---------------- backward ----------------
-    // Main stream: the chain dlogits -> dx_L -> ... -> dx_0.  Side stream:
-    // every weight gradient, forked as soon as its inputs exist.
+    // The chain dlogits -> dx_L -> ... -> dx_0 first, then the weight gradients.
     const float* dlg = m.logits;
     const size_t wf = m.work_floats;
     auto gxl = [&](int l) { return m.gx + l * ND; };
     // An RMSNorm backward whose dx rows the next NT GEMM of the chain consumes:
     // with fused GEMMs it runs as that GEMM's A prologue, otherwise as its own
-    // launch just before.  Its gain's dw partials are summed on the side stream.
+    // launch just before.  Its gain's dw partials are column-summed after the chain.
     struct NormBwd {
         const float *x, *w, *inv, *dy, *dres;
         float *out, *part, *gw;
@@ -328,8 +300,20 @@ int enqueue_step(LmModel& m, hipStream_t s, const Hyper& hp, bool device_hyper)
         c.a_parts = nb.dy_parts; c.a_pstride = ND;
         nb.parts = tiles_m;
     };
-    LM_TRY(fk.fork());
-    LM_TRY(q2.gemm(1, 0, V, D, N, dlg, V, m.xf, D, 0.f, m.grd(0), D));            // gemb = dlogits^T . xf
+    // Weight gradients dW = X^T . dY and the norm gains' column sums are
+    // collected and issued after the backward chain, as one grouped launch and
+    // one column-sum launch (every buffer they read is per layer, so nothing is
+    // overwritten before then).  Forking them per layer onto a second stream
+    // was measured slower: each event record + stream wait costs ~13 us of host
+    // time on this ROCm, and the forks kept the host behind the GPU.
+    GroupedTN dw_all[kGroupedMax];
+    int ndw = 0;
+    const float* cs_p[kColsumJobs];
+    int cs_n[kColsumJobs];
+    float* cs_o[kColsumJobs];
+    int ncs = 0;
+    const GroupedTN gemb{dlg, V, m.xf, D, m.grd(0), D, V, D};                     // gemb = dlogits^T . xf
+    dw_all[ndw++] = gemb;
     // dxf = dlogits . emb; with fused GEMMs its split-K slices are left
     // unreduced and summed by the norm-backward prologue that consumes dxf
     int dxf_parts = 1;
@@ -399,15 +383,13 @@ int enqueue_step(LmModel& m, hipStream_t s, const Hyper& hp, bool device_hyper)
             // RoPE backward (inverse rotation) on dq and dk
             LM_TRY(rope(dqkv, nullptr, 2 * N, H, hd, D, 0, T, base, 1, 1, s));
         }
-        // Side stream, one fork per layer: the two norm gains' column sums
-        // (the pending norm above this layer and ln2) and the layer's seven
-        // weight gradients dW = X^T . dY as one grouped launch.
-        LM_TRY(fk.fork());
+        // This layer's share of the deferred work: the two norm gains' column
+        // sums (the pending norm above this layer and ln2) and the layer's
+        // seven weight gradients dW = X^T . dY.
         {
             const float* parts_p[2] = {pend.part, n2.part};
             const int parts_n[2] = {pend.parts, n2.parts};
             float* parts_o[2] = {pend.gw, n2.gw};
-            LM_TRY(rmsnorm_bwd_colsum_multi(parts_p, parts_n, parts_o, 2, D, 0, s2));
             const long long DD = static_cast<long long>(D) * D;
             const GroupedTN gw[7] = {
                 {a, F, gin, D, m.grd(m.lt(l, P_W2)), D, F, D},                 // gW2 = a^T . gin
@@ -418,7 +400,17 @@ int enqueue_step(LmModel& m, hipStream_t s, const Hyper& hp, bool device_hyper)
                 {h, D, dqkv + ND, D, m.grd(m.lt(l, P_WQ)) + DD, D, D, D},      // gWk = h^T . dk
                 {h, D, dqkv + 2 * ND, D, m.grd(m.lt(l, P_WQ)) + 2 * DD, D, D, D},  // gWv = h^T . dv
             };
-            LM_TRY(sgemm_grouped_tn(gw, 7, N, s2));
+            // a full batch is issued now (deep models); the rest waits for the end
+            if (ndw + 7 > kGroupedMax) {
+                LM_TRY(sgemm_grouped_tn(dw_all, ndw, N, s));
+                ndw = 0;
+            }
+            if (ncs + 2 > kColsumJobs) {
+                LM_TRY(rmsnorm_bwd_colsum_multi(cs_p, cs_n, cs_o, ncs, D, 0, s));
+                ncs = 0;
+            }
+            for (int i = 0; i < 7; ++i) dw_all[ndw++] = gw[i];
+            for (int i = 0; i < 2; ++i) { cs_p[ncs] = parts_p[i]; cs_n[ncs] = parts_n[i]; cs_o[ncs] = parts_o[i]; ++ncs; }
         }
         // dh = dq.Wq^T + dk.Wk^T + dv.Wv^T (adjacent weights: one batch-reduce GEMM)
         LM_TRY(q.brgemm(1, N, D, D, 3, dqkv, D, ND, m.prm(m.lt(l, P_WQ)), D, static_cast<long long>(D) * D, m.dh, D));
@@ -427,10 +419,14 @@ int enqueue_step(LmModel& m, hipStream_t s, const Hyper& hp, bool device_hyper)
                        m.grd(m.lt(l, P_LN1)), 0, 1};
     }
     LM_TRY(norm_standalone(pend));                       // dx_0 (no GEMM follows it)
-    LM_TRY(fk.fork());
-    LM_TRY(rmsnorm_bwd_colsum(pend.part, pend.parts, pend.gw, D, 0, s2));
-    LM_TRY(embed_bwd(gxl(0), m.ids, m.grd(0), N, D, V, 1.f, 1, s2));   // after gemb: same stream
-    LM_TRY(fk.join());
+    if (ncs + 1 > kColsumJobs) {
+        LM_TRY(rmsnorm_bwd_colsum_multi(cs_p, cs_n, cs_o, ncs, D, 0, s));
+        ncs = 0;
+    }
+    cs_p[ncs] = pend.part; cs_n[ncs] = pend.parts; cs_o[ncs] = pend.gw; ++ncs;
+    LM_TRY(sgemm_grouped_tn(dw_all, ndw, N, s));
+    LM_TRY(rmsnorm_bwd_colsum_multi(cs_p, cs_n, cs_o, ncs, D, 0, s));
+    LM_TRY(embed_bwd(gxl(0), m.ids, m.grd(0), N, D, V, 1.f, 1, s));    // after gemb (same launch order)
 
     // ---------------- optimizer (lmtrain.lua:1212-1226) ----------------
     // squared-norm partials; the optimizer kernel finishes the sum itself
@@ -498,30 +494,12 @@ int run_step(LmModel& m, const Hyper& hp)
 
 LmModel* as_model(void* p) { return static_cast<LmModel*>(p); }
 
-// Device resources of a model (graph, events, side stream, arena); the caller
-// has synchronized.
+// Device resources of a model (graph, arena); the caller has synchronized.
 void release(LmModel& m)
 {
     drop_graph(m);
-    for (hipEvent_t e : m.ev) (void)hipEventDestroy(e);
-    m.ev.clear();
-    if (m.side) (void)hipStreamDestroy(m.side);
-    m.side = nullptr;
     if (m.arena) (void)hipFree(m.arena);
     m.arena = nullptr;
-}
-
-// Side stream (default priority) and the fork/join events of one step.
-int make_streams(LmModel& m)
-{
-    LHIP_CHECK_HIP(hipStreamCreateWithFlags(&m.side, hipStreamNonBlocking), "lhip_lm_create: side stream");
-    const int nev = 2 * m.L + 8;
-    for (int i = 0; i < nev; ++i) {
-        hipEvent_t e = nullptr;
-        LHIP_CHECK_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming), "lhip_lm_create: event");
-        m.ev.push_back(e);
-    }
-    return LHIP_OK;
 }
 
 }  // namespace
@@ -583,7 +561,7 @@ LHIP_API int lhip_lm_create(const lhip_lm_config_t* cfg, void** model)
     // dw partials of one norm backward: the stand-alone kernel's, or one row per 16-row tile when fused
     m->work_floats = static_cast<size_t>(std::max(lhip::rmsnorm_bwd_parts(m->N, m->D), lhip::ceil_div(m->N, 16))) *
                      m->D;
-    m->splitk_floats = static_cast<size_t>(1) << 22;   // 16 MiB per stream; the planner caps splits to fit
+    m->splitk_floats = static_cast<size_t>(1) << 22;   // 16 MiB; the planner caps splits to fit
     // carve every buffer out of one allocation, each 256-byte aligned
     struct Slot { void** dst; size_t bytes; };
     std::vector<Slot> slots = {
@@ -628,7 +606,7 @@ LHIP_API int lhip_lm_create(const lhip_lm_config_t* cfg, void** model)
         {reinterpret_cast<void**>(&m->dqkv), sizeof(float) * L * 3 * ND},
         {reinterpret_cast<void**>(&m->dh), sizeof(float) * ND},
         {reinterpret_cast<void**>(&m->work), sizeof(float) * (2 * L + 1) * m->work_floats},
-        {reinterpret_cast<void**>(&m->splitk), sizeof(float) * 2 * m->splitk_floats},
+        {reinterpret_cast<void**>(&m->splitk), sizeof(float) * m->splitk_floats},
         {reinterpret_cast<void**>(&m->rope_cs), sizeof(float2) * m->T * (m->hd / 2)},
     };
     size_t total = 0;
@@ -678,11 +656,6 @@ LHIP_API int lhip_lm_create(const lhip_lm_config_t* cfg, void** model)
     m->fused_attn = lhip::attn_fused_ok(m->T, m->hd);
     m->fused_gemm = lhip::lm_fuse_ok(m->D, m->D, m->D) && m->F % 4 == 0;
     m->h_tgt.assign(static_cast<size_t>(N), 0);
-    if (int src = lhip::make_streams(*m)) {
-        lhip::release(*m);
-        delete m;
-        return src;
-    }
     *model = m;
     return LHIP_OK;
 }
@@ -694,7 +667,6 @@ LHIP_API int lhip_lm_destroy(void* model)
     auto* m = lhip::as_model(model);
     if (st().ready) {
         (void)hipStreamSynchronize(st().stream);
-        if (m->side) (void)hipStreamSynchronize(m->side);
         lhip::release(*m);
     }
     delete m;
