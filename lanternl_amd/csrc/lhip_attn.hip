@@ -53,6 +53,7 @@ struct AttnArgs {
     int B, H, T, hd, D, N;
     float scale;
     int causal;
+    int vec;              // T, hd, D % 4 == 0 and 16-byte aligned bases: float4 loads
 };
 
 __device__ __forceinline__ int round16(int x) { return (x + 15) & ~15; }
@@ -62,6 +63,8 @@ __device__ __forceinline__ int attn_lim(int i, int T, int causal) { return causa
 // side by side (independent accumulator chains); lane l reads
 // A(i0 + l%16, k0 + l/16) = a[(i0 + l%16) * kLd + k] and the B element
 // b_j[(j0 + l%16) * kLd + k] of block j (both operands stored k-contiguous).
+// (Reading every step's operands before the first MFMA was measured slower:
+// 10.8 -> 13.3 us for the C2 backward.)
 template <int NB>
 __device__ __forceinline__ void mfma_rows(floatx4 (&acc)[NB], const float* a, int i0, const float* b, int j0,
                                           int jstep, int nb, int k0, int k1)
@@ -122,6 +125,52 @@ __device__ __forceinline__ void load_qkv(const AttnArgs& a, int b, int h, float*
     }
 }
 
+// float4 form of load_qkv (AttnArgs::vec): a unit is (row t, 4-column group
+// g); its q, k, v and (cos, sin) pairs are one float4 load each, row-major
+// copies are float4 LDS stores.
+__device__ __forceinline__ void load_qkv4(const AttnArgs& a, int b, int h, float* q_rm, float* q_tr, float* k_rm,
+                                          float* k_tr, float* v_rm, float* v_tr)
+{
+    constexpr int U = kMax * (kMax / 4) / kAttnThreads;   // units per thread
+    const int T = a.T, hd = a.hd, D = a.D, pairs = hd >> 1;
+    const int T16 = round16(T), g16 = round16(hd) >> 2, gq = hd >> 2;
+    const long long ND = static_cast<long long>(a.N) * D;
+    float4 qv[U], kv[U], vv[U], cv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int idx = threadIdx.x + kAttnThreads * u;
+        const int t = idx / g16, g = idx - t * g16;
+        qv[u] = kv[u] = vv[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+        cv[u] = make_float4(1.f, 0.f, 1.f, 0.f);
+        if (t < T && g < gq) {
+            const long long off = static_cast<long long>(b * T + t) * D + h * hd + 4 * g;
+            qv[u] = *reinterpret_cast<const float4*>(a.qkv + off);
+            kv[u] = *reinterpret_cast<const float4*>(a.qkv + ND + off);
+            vv[u] = *reinterpret_cast<const float4*>(a.qkv + 2 * ND + off);
+            cv[u] = *reinterpret_cast<const float4*>(a.cs + t * pairs + 2 * g);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int idx = threadIdx.x + kAttnThreads * u;
+        const int t = idx / g16, g = idx - t * g16;
+        if (t < T16 && g < g16) {
+            const float4 c = cv[u], x = qv[u], y = kv[u], v = vv[u];
+            const float4 qr = make_float4(x.x * c.x - x.y * c.y, x.x * c.y + x.y * c.x,
+                                          x.z * c.z - x.w * c.w, x.z * c.w + x.w * c.z);
+            const float4 kr = make_float4(y.x * c.x - y.y * c.y, y.x * c.y + y.y * c.x,
+                                          y.z * c.z - y.w * c.w, y.z * c.w + y.w * c.z);
+            const int d = 4 * g;
+            if (q_rm) *reinterpret_cast<float4*>(q_rm + t * kLd + d) = qr;
+            if (k_rm) *reinterpret_cast<float4*>(k_rm + t * kLd + d) = kr;
+            if (v_rm) *reinterpret_cast<float4*>(v_rm + t * kLd + d) = v;
+            if (q_tr) { q_tr[d * kLd + t] = qr.x; q_tr[(d + 1) * kLd + t] = qr.y; q_tr[(d + 2) * kLd + t] = qr.z; q_tr[(d + 3) * kLd + t] = qr.w; }
+            if (k_tr) { k_tr[d * kLd + t] = kr.x; k_tr[(d + 1) * kLd + t] = kr.y; k_tr[(d + 2) * kLd + t] = kr.z; k_tr[(d + 3) * kLd + t] = kr.w; }
+            if (v_tr) { v_tr[d * kLd + t] = v.x; v_tr[(d + 1) * kLd + t] = v.y; v_tr[(d + 2) * kLd + t] = v.z; v_tr[(d + 3) * kLd + t] = v.w; }
+        }
+    }
+}
+
 // Forward.  Wave w: S = scale * qr kr^T for its 16 query rows against the key
 // blocks it can see (all, or blocks 0..w when causal), the row softmax in the
 // MFMA accumulators (each row's 16 columns of a block sit in one 16-lane DPP
@@ -136,7 +185,8 @@ __global__ void __launch_bounds__(kAttnThreads) attn_fwd_kernel(const AttnArgs a
     const int T = a.T, hd = a.hd;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r = lane & 15, q = lane >> 4;
     const int nbt = round16(T) >> 4, nbd = round16(hd) >> 4, hd4 = (hd + 3) & ~3, T4 = (T + 3) & ~3;
-    load_qkv(a, b, h, qs, nullptr, ks, nullptr, nullptr, vT);
+    if (a.vec) load_qkv4(a, b, h, qs, nullptr, ks, nullptr, nullptr, vT);
+    else load_qkv(a, b, h, qs, nullptr, ks, nullptr, nullptr, vT);
     __syncthreads();
     const int i0 = 16 * wave;
     const bool active = i0 < T;
@@ -249,17 +299,43 @@ __global__ void __launch_bounds__(kAttnThreads) attn_bwd_kernel(const AttnArgs a
     const bool active = i0 < T;
     const int nj = a.causal ? min(wave + 1, nbt) : nbt;
     const float* Pg = a.P + (static_cast<long long>(b) * a.H + h) * T * T;
-    // this wave's P rows in accumulator layout, loaded with everything else
-    float Pd[4][4];
+    if (a.vec) {
+        load_qkv4(a, b, h, nullptr, qT, nullptr, kT, vs, nullptr);
+        // P^T and dO, dO^T from float4 loads: a P unit is (row i, 4-column
+        // group c), a dO unit (row i, 4-column group g); zero padded to T16 / hd16
+        constexpr int UP = kMax * (kMax / 4) / kAttnThreads;
+        const int c16 = T16 >> 2, g16 = hd16 >> 2;
+        float4 pv[UP], ov[UP];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int i = i0 + 4 * q + e, c = 16 * j + r;
-            Pd[j][e] = (active && j < nj && i < T && c < T) ? Pg[i * T + c] : 0.f;
+        for (int u = 0; u < UP; ++u) {
+            const int idx = threadIdx.x + kAttnThreads * u;
+            const int i = idx / c16, c = idx - i * c16;
+            const int oi = idx / g16, og = idx - oi * g16;
+            pv[u] = (i < T && 4 * c < T) ? *reinterpret_cast<const float4*>(Pg + i * T + 4 * c)
+                                         : make_float4(0.f, 0.f, 0.f, 0.f);
+            ov[u] = (oi < T && 4 * og < hd)
+                        ? *reinterpret_cast<const float4*>(a.dctx + static_cast<long long>(b * T + oi) * D + h * hd + 4 * og)
+                        : make_float4(0.f, 0.f, 0.f, 0.f);
         }
-    load_qkv(a, b, h, nullptr, qT, nullptr, kT, vs, nullptr);
-    {
+#pragma unroll
+        for (int u = 0; u < UP; ++u) {
+            const int idx = threadIdx.x + kAttnThreads * u;
+            const int i = idx / c16, c = idx - i * c16;
+            const int oi = idx / g16, og = idx - oi * g16;
+            if (i < T16) {
+                const int j = 4 * c;
+                PT[j * kLd + i] = pv[u].x; PT[(j + 1) * kLd + i] = pv[u].y;
+                PT[(j + 2) * kLd + i] = pv[u].z; PT[(j + 3) * kLd + i] = pv[u].w;
+            }
+            if (oi < T16) {
+                const int d = 4 * og;
+                *reinterpret_cast<float4*>(dOs + oi * kLd + d) = ov[u];
+                dOT[d * kLd + oi] = ov[u].x; dOT[(d + 1) * kLd + oi] = ov[u].y;
+                dOT[(d + 2) * kLd + oi] = ov[u].z; dOT[(d + 3) * kLd + oi] = ov[u].w;
+            }
+        }
+    } else {
+        load_qkv(a, b, h, nullptr, qT, nullptr, kT, vs, nullptr);
         // P^T, dO and dO^T over [T16) x [T16) / [T16) x [hd16), zero padded
         constexpr int U = kMax * kMax / kAttnThreads;
         float pv[U], ov[U];
@@ -279,6 +355,15 @@ __global__ void __launch_bounds__(kAttnThreads) attn_bwd_kernel(const AttnArgs a
         }
     }
     __syncthreads();
+    // this wave's P rows in accumulator layout (P^T is zero padded past T)
+    float Pd[4][4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int i = i0 + 4 * q + e, c = 16 * j + r;
+            Pd[j][e] = (active && j < nj) ? PT[c * kLd + i] : 0.f;
+        }
     if (active) {
         // dP(i, j) = sum_d dO(i, d) v(j, d)
         floatx4 G[4];
@@ -346,6 +431,7 @@ int attn_fwd(const float* qkv, const float2* cs, float* P, float* ctx, int B, in
     a.qkv = qkv; a.cs = cs; a.P = P; a.ctx = ctx;
     a.B = B; a.H = H; a.T = T; a.hd = hd; a.D = H * hd; a.N = B * T;
     a.scale = scale; a.causal = causal;
+    a.vec = (hd % 4 == 0 && aligned16(qkv) && aligned16(cs)) ? 1 : 0;
     attn_fwd_kernel<<<B * H, kAttnThreads, 0, s>>>(a);
     return check_launch("attn_fwd");
 }
@@ -359,6 +445,7 @@ int attn_bwd(const float* qkv, const float2* cs, const float* P, const float* dc
     a.qkv = qkv; a.cs = cs; a.P = const_cast<float*>(P); a.dctx = dctx; a.dqkv = dqkv;
     a.B = B; a.H = H; a.T = T; a.hd = hd; a.D = H * hd; a.N = B * T;
     a.scale = scale; a.causal = causal;
+    a.vec = (hd % 4 == 0 && T % 4 == 0 && aligned16(qkv) && aligned16(cs) && aligned16(P) && aligned16(dctx)) ? 1 : 0;
     attn_bwd_kernel<<<B * H, kAttnThreads, 0, s>>>(a);
     return check_launch("attn_bwd");
 }

@@ -1283,13 +1283,17 @@ int launch_reduce(const GemmArgs& g, int batch, hipStream_t stream)
     return check_launch("sgemm: split-K reduce");
 }
 
-// Grouped transposed-A products (the weight gradients of one transformer
-// layer: dW = X^T . dY with X, dY row-major over the same B*T rows) in one
-// launch.  Workgroup id -> (group, tile) through the groups' first-tile table;
-// each tile is computed like sgemm_tiny_kernel<TA, !TB>: 16x16 outputs, four
-// waves over 16-deep K steps, lane l holding A^T[row][k0+4q..+3] (four scalar
-// loads down a column of the stored A, coalesced over the 16 rows) and
-// B[k0+4q..+3][col], partial tiles summed in LDS in wave order.
+// Grouped transposed-A products (the weight gradients of the LMTrain step:
+// dW = X^T . dY with X, dY row-major over the same B*T rows, every layer's and
+// the tied embedding's in one launch).  Workgroup id -> (group, tile) through
+// the groups' first-tile table; each 32x32 tile is computed like
+// sgemm_small_kernel<TA, !TB>: NW waves split K into 8-deep steps, lane l
+// (row or column l%32, half h = l/32) holding A^T[row][k0+4h..+3] (four loads
+// down a column of the stored A, coalesced over the 32 rows) and
+// B[k0+4h..+3][col], v_mfma_f32_32x32x2f32, partial tiles summed in LDS in
+// wave order.  (Fallback for operands that cannot take float4 loads.)
+constexpr int kGroupedTile = 32;
+
 struct GroupedTNArgs {
     GroupedTN e[kGroupedMax];
     int tile0[kGroupedMax + 1];
@@ -1297,10 +1301,17 @@ struct GroupedTNArgs {
     int ngroups, K;
 };
 
-__global__ void __launch_bounds__(256) sgemm_grouped_tn_kernel(const GroupedTNArgs ga)
+template <int NW>
+__global__ void __launch_bounds__(64 * NW) sgemm_grouped_tn_kernel(const GroupedTNArgs ga)
 {
-    __shared__ float red[4][4][64];
-    const int id = blockIdx.x;
+    __shared__ float red[NW][16][64];
+    // XCD-contiguous tiles: workgroups are dispatched round-robin over the 8
+    // XCDs, so id p runs on XCD p % 8; XCD x takes the tiles
+    // [x*G/8, (x+1)*G/8) (G padded to a multiple of 8), i.e. whole groups and
+    // row bands, whose operands then stay in that XCD's L2.
+    const int per_xcd = gridDim.x / 8;
+    const int id = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    if (id >= ga.tile0[ga.ngroups]) return;   // padding
     int gi = 0;
     for (int i = 1; i < ga.ngroups; ++i)
         if (id >= ga.tile0[i]) gi = i;
@@ -1308,37 +1319,132 @@ __global__ void __launch_bounds__(256) sgemm_grouped_tn_kernel(const GroupedTNAr
     const int local = id - ga.tile0[gi];
     const int tm = local / ga.tiles_n[gi], tn = local - tm * ga.tiles_n[gi];
     const int K = ga.K;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, lr = lane & 15, q = lane >> 4;
-    const int m0 = tm * 16, n0 = tn * 16;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, lr = lane & 31, h = lane >> 5;
+    const int m0 = tm * kGroupedTile, n0 = tn * kGroupedTile;
     const int row = m0 + lr, col = n0 + lr;
     const bool rok = row < e.M, cok = col < e.N;
-    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+    floatx16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
     constexpr int U = kSmallU;
-    for (int kp = 16 * wave; kp < K; kp += 64 * U) {
+    for (int kp = 8 * wave; kp < K; kp += 8 * NW * U) {
         float a[U][4], b[U][4];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int k = kp + 64 * u + 4 * q;
+            const int kl = kp + 8 * NW * u + 4 * h;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const bool kin = k + i < K;
-                a[u][i] = (rok && kin) ? e.A[static_cast<long long>(k + i) * e.lda + row] : 0.f;
-                b[u][i] = (cok && kin) ? e.B[static_cast<long long>(k + i) * e.ldb + col] : 0.f;
+                const bool kin = kl + i < K;
+                a[u][i] = (rok && kin) ? e.A[static_cast<long long>(kl + i) * e.lda + row] : 0.f;
+                b[u][i] = (cok && kin) ? e.B[static_cast<long long>(kl + i) * e.ldb + col] : 0.f;
             }
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            if (kp + 64 * u >= K) break;   // wave-uniform
+            if (kp + 8 * NW * u >= K) break;   // wave-uniform
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u][i], b[u][i], acc, 0, 0, 0);
+            for (int i = 0; i < 4; ++i) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[u][i], b[u][i], acc, 0, 0, 0);
         }
     }
 #pragma unroll
-    for (int r = 0; r < 4; ++r) red[wave][r][lane] = acc[r];
+    for (int r = 0; r < 16; ++r) red[wave][r][lane] = acc[r];
     __syncthreads();
-    const float v = ((red[0][wave][lane] + red[1][wave][lane]) + red[2][wave][lane]) + red[3][wave][lane];
-    const int orow = m0 + 4 * q + wave, ocol = n0 + lr;
-    if (orow < e.M && ocol < e.N) e.C[static_cast<long long>(orow) * e.ldc + ocol] = v;
+    // thread (wave w, lane l) finishes accumulator registers (16/NW)w .. of lane l
+    constexpr int RPW = 16 / NW;
+    const int ocol = n0 + (lane & 31);
+    const int lk = lane >> 5;
+#pragma unroll
+    for (int q = 0; q < RPW; ++q) {
+        const int r = RPW * wave + q;
+        float v = red[0][r][lane];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) v += red[w][r][lane];
+        const int orow = m0 + 8 * (r >> 2) + 4 * lk + (r & 3);
+        if (orow < e.M && ocol < e.N) e.C[static_cast<long long>(orow) * e.ldc + ocol] = v;
+    }
+}
+
+// LDS-staged form of the grouped kernel, for groups whose operands allow
+// float4 loads (leading dimensions % 4 == 0, 16-byte aligned bases).  Both
+// operands are stored K-major (A is K x M, B is K x N), so a 64-deep chunk of
+// each is copied into LDS unchanged with float4 loads (four per thread per
+// chunk), double-buffered; wave w then runs the 8 MFMA steps of chunk rows
+// 16w .. 16w+15 on the whole 32x32 tile, reading each operand fragment as one
+// conflict-free ds_read_b32 (lanes 0-31 row k, 32-63 row k+1).  The waves'
+// tiles are summed in LDS in wave order.
+constexpr int kGroupedBK = 64;
+
+__global__ void __launch_bounds__(256) sgemm_grouped_tn_lds_kernel(const GroupedTNArgs ga)
+{
+    constexpr int T = kGroupedTile, BK = kGroupedBK;
+    __shared__ float As[2][BK][T];
+    __shared__ float Bs[2][BK][T];
+    __shared__ float red[4][16][64];
+    const int per_xcd = gridDim.x / 8;
+    const int id = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    if (id >= ga.tile0[ga.ngroups]) return;   // padding
+    int gi = 0;
+    for (int i = 1; i < ga.ngroups; ++i)
+        if (id >= ga.tile0[i]) gi = i;
+    const GroupedTN& e = ga.e[gi];
+    const int local = id - ga.tile0[gi];
+    const int tm = local / ga.tiles_n[gi], tn = local - tm * ga.tiles_n[gi];
+    const int K = ga.K;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, lr = lane & 31, lk = lane >> 5;
+    const int m0 = tm * T, n0 = tn * T;
+    // chunk loader: thread t covers chunk rows t/8 and t/8 + 32, float4 column (t%8)*4
+    const int lrow = tid >> 3, lc4 = (tid & 7) * 4;
+    const bool am_ok = m0 + lc4 < e.M, bn_ok = n0 + lc4 < e.N;   // M, N % 4 == 0 (host check)
+    float4 ra[2], rb[2];
+    auto gload = [&](int k0) {
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            const int k = k0 + lrow + 32 * p;
+            const bool kin = k < K;
+            ra[p] = (kin && am_ok) ? *reinterpret_cast<const float4*>(e.A + static_cast<long long>(k) * e.lda + m0 + lc4)
+                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+            rb[p] = (kin && bn_ok) ? *reinterpret_cast<const float4*>(e.B + static_cast<long long>(k) * e.ldb + n0 + lc4)
+                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    auto lstore = [&](int buf) {
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            *reinterpret_cast<float4*>(&As[buf][lrow + 32 * p][lc4]) = ra[p];
+            *reinterpret_cast<float4*>(&Bs[buf][lrow + 32 * p][lc4]) = rb[p];
+        }
+    };
+    floatx16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+    const int nk = (K + BK - 1) / BK;
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+        const int cur = kt & 1;
+        const bool more = kt + 1 < nk;
+        if (more) gload((kt + 1) * BK);
+#pragma unroll
+        for (int st = 0; st < 8; ++st) {
+            const int kr = 16 * wave + 2 * st + lk;
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(As[cur][kr][lr], Bs[cur][kr][lr], acc, 0, 0, 0);
+        }
+        if (more) lstore(cur ^ 1);
+        __syncthreads();
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) red[wave][r][lane] = acc[r];
+    __syncthreads();
+    // thread (wave w, lane l) finishes accumulator registers 4w .. 4w+3 of lane l
+    const int ocol = n0 + lr;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int r = 4 * wave + q;
+        const float v = ((red[0][r][lane] + red[1][r][lane]) + red[2][r][lane]) + red[3][r][lane];
+        const int orow = m0 + 8 * (r >> 2) + 4 * lk + (r & 3);
+        if (orow < e.M && ocol < e.N) e.C[static_cast<long long>(orow) * e.ldc + ocol] = v;
+    }
 }
 
 }  // namespace
@@ -1358,14 +1464,23 @@ int sgemm_grouped_tn(const GroupedTN* g, int ngroups, int K, hipStream_t stream)
             return fail(LHIP_E_SHAPE, "sgemm_grouped_tn: group %d leading dimensions", i);
         ga.e[i] = e;
         ga.tile0[i] = static_cast<int>(tiles);
-        ga.tiles_n[i] = ceil_div(e.N, 16);
-        tiles += static_cast<long long>(ceil_div(e.M, 16)) * ga.tiles_n[i];
+        ga.tiles_n[i] = ceil_div(e.N, kGroupedTile);
+        tiles += static_cast<long long>(ceil_div(e.M, kGroupedTile)) * ga.tiles_n[i];
         if (tiles > 0x7fffffffLL) return fail(LHIP_E_CAPACITY, "sgemm_grouped_tn: too many tiles");
     }
     ga.tile0[ngroups] = static_cast<int>(tiles);
     ga.ngroups = ngroups;
     ga.K = K;
-    sgemm_grouped_tn_kernel<<<static_cast<unsigned>(tiles), 256, 0, stream>>>(ga);
+    const unsigned grid = static_cast<unsigned>((tiles + 7) / 8 * 8);   // whole XCD rounds
+    bool vec = true;
+    for (int i = 0; i < ngroups; ++i) {
+        const GroupedTN& e = g[i];
+        vec = vec && e.lda % 4 == 0 && e.ldb % 4 == 0 && e.M % 4 == 0 && e.N % 4 == 0 && aligned16(e.A) &&
+              aligned16(e.B);
+    }
+    if (vec) sgemm_grouped_tn_lds_kernel<<<grid, 256, 0, stream>>>(ga);
+    else if (K >= 256) sgemm_grouped_tn_kernel<8><<<grid, 512, 0, stream>>>(ga);
+    else sgemm_grouped_tn_kernel<4><<<grid, 256, 0, stream>>>(ga);
     return check_launch("sgemm_grouped_tn");
 }
 

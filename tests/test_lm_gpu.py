@@ -75,6 +75,27 @@ def test_lm_step_two_layers_clip_active():
     gpu.close()
 
 
+def test_lm_step_eight_layers_weight_gradient_batches():
+    """Eight layers: the deferred weight gradients (1 + 7 x 8 products, 17
+    norm-gain column sums) exceed one grouped launch and one column-sum launch,
+    so they are issued in several batches."""
+    announce("lm 8 layers")
+    gpu, res = _run_case(40, 16, 8, 2, 32, 2, 8, steps=2, lr=0.1, std=0.3, seed=6)
+    _check(res)
+    gpu.close()
+
+
+@pytest.mark.parametrize("D,H,T", [(12, 2, 7), (16, 2, 7), (24, 2, 12)])
+def test_lm_step_attention_load_paths(D, H, T):
+    """The fused attention's operand loads: float4 (head_dim and T multiples of
+    4), float4 forward with element-wise backward (T = 7), and element-wise
+    both ways (head_dim 6)."""
+    announce("lm attention loads", D, H, T)
+    gpu, res = _run_case(30, D, 1, H, 2 * D, 2, T, steps=1, lr=0.1, std=0.3, seed=7 + D + T)
+    _check(res)
+    gpu.close()
+
+
 def test_lm_step_config_c2():
     """Config C2: vocab 2000, dim 128, 4 layers, 8 heads (hd 16), ffn 256, batch 8 x seq 64,
     weights N(0, 0.02); one SGD step (lr 0.1, momentum 0.9, wd 0.01, clip 1)."""
