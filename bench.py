@@ -128,7 +128,7 @@ def cpu_baseline_gemm(n=512, reps=4):
 # library stream it runs on.
 # HBM bytes per launch of that kernel from rocprofv3 FETCH_SIZE / WRITE_SIZE
 # (scaled by the copy-kernel calibration): profiles/sgemm_batched_reduce_dh2.md.
-DOMINANT_C2_TRAFFIC_BYTES = 3_564_544
+DOMINANT_C2_TRAFFIC_BYTES = 3_562_496
 
 
 def dominant_kernel_c2(steps, warmup):
@@ -228,6 +228,29 @@ def run_gemm_workload(args):
     print(json.dumps(line), flush=True)
 
 
+def bench_host_gemm(m, k, n, op=0, reps=20):
+    """lhip_matmul_host (the flat-table adapter contract, luatl_adapter.lua:128-135):
+    double host arrays in, fp32 conversion, upload, GEMM, download, double host
+    array out, synchronous -- timed with the host clock around whole calls.
+    This is the PCIe-inclusive rate of the boundary; it is never `value`."""
+    from lanternl_amd._lib import call
+    rng = np.random.default_rng(0)
+    a = rng.uniform(-1, 1, m * k)
+    nb = k * n if op == 0 else (n * k if op == 1 else m * n)
+    b = rng.uniform(-1, 1, nb)
+    rows = k if op == 2 else m
+    c = np.empty(rows * n)
+    args = (op, a.ctypes.data, b.ctypes.data, c.ctypes.data, m, k, n, 0)
+    call("lhip_matmul_host", *args)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        call("lhip_matmul_host", *args)
+    dt = (time.perf_counter() - t0) / reps
+    nbytes = 8.0 * (m * k + nb + rows * n)
+    return {"suite": "gemm_host", "op": ["NN", "NT", "TN"][op], "m": m, "k": k, "n": n, "ms": dt * 1e3,
+            "tflops": 2.0 * m * k * n / dt / 1e12, "host_bytes": nbytes, "host_gbps": nbytes / dt / 1e9}
+
+
 def run_gemm_suite(args):
     from lanternl_amd import device
     device.init(0)
@@ -242,6 +265,10 @@ def run_gemm_suite(args):
         r = bench_gemm(m, n, k, ta, tb, steps=steps, warmup=args.warmup)
         r["hbm_gbps_algorithmic"] = r["bytes"] / (r["ms"] * 1e-3) / 1e9
         print(json.dumps({"suite": "gemm", **r}), flush=True)
+    # the host-table boundary (PCIe and fp64 <-> fp32 conversions included)
+    for m, k, n, op, reps in [(256, 128, 256, 0, 50), (256, 128, 256, 1, 50), (256, 128, 256, 2, 50),
+                              (1024, 1024, 1024, 0, 10), (4096, 4096, 4096, 0, 3)]:
+        print(json.dumps(bench_host_gemm(m, k, n, op, reps)), flush=True)
 
 
 # ------------------------------------------------------------ bandwidth kernels

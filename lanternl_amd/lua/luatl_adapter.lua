@@ -54,6 +54,10 @@ int lhip_ce_fused(const float* logits, const int* targets, float* losses, float*
                   int rows, int vocab, int ignore_index, float grad_scale);
 int lhip_argmax_rows(const float* x, int* out, int rows, int cols);
 int lhip_add(const float* a, const float* b, float* out, long long n);
+int lhip_program_begin(void);
+int lhip_program_end(void** program);
+int lhip_program_replay(void* program, int times);
+int lhip_program_free(void* program);
 ]]
 
 local STATUS = { [0] = "OK", [-1] = "NULL", [-2] = "SHAPE", [-3] = "DTYPE", [-4] = "DEVICE",
@@ -300,6 +304,37 @@ function M.add_inplace(A, B)
 end
 
 function M.sync() ck(C.lhip_sync(), "sync") end
+
+-- Program (luaTL.Program capture/replay, ai/gpu/luaTL_train.lua:327-627):
+-- fn() issues adapter calls, which are recorded rather than run; the result
+-- replays them as one graph launch.  Calls that synchronise or allocate fail
+-- while recording, so run fn() once eagerly first.
+local Program = {}
+Program.__index = Program
+
+function M.program(fn)
+    ck(C.lhip_program_begin(), "program")
+    local ok, err = pcall(fn)
+    if not ok then
+        C.lhip_program_end(nil)             -- discard the partial recording
+        error(err, 2)
+    end
+    local h = ffi.new("void*[1]")
+    ck(C.lhip_program_end(h), "program")
+    return setmetatable({ h = ffi.gc(h[0], C.lhip_program_free) }, Program)
+end
+
+function Program:replay(times)
+    ck(C.lhip_program_replay(self.h, times or 1), "program.replay")
+    return self
+end
+
+function Program:free()
+    if self.h ~= nil then
+        C.lhip_program_free(ffi.gc(self.h, nil))
+        self.h = nil
+    end
+end
 
 function M.shutdown()
     C.lhip_shutdown()
