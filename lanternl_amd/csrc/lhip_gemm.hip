@@ -1149,6 +1149,41 @@ sgemm_tiny_kernel(const GemmArgs g)
             }
         }
     };
+    // A pass whose U steps all lie inside [kbeg, kend), with float4-aligned
+    // contiguous operands (and, for batch-reduce, 16-deep steps that never
+    // straddle a block), loads with no selects and no branches: each load's
+    // register is final, so all 8U loads issue before the first wait.
+    const bool fast_ops = (TA || g.vecA) && (!TB || g.vecB) && (!BR || g.Kb % 16 == 0);
+    auto load_pass_full = [&](int kp, float (&a)[U][4], float (&b)[U][4]) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int ks = kp + 64 * u;
+            const int kl = ks + 4 * q;
+            int kb = kl;
+            const float* __restrict__ Ab = A;
+            const float* __restrict__ Bb = B;
+            if (BR) {
+                const int j = ks / g.Kb;
+                kb = kl - j * g.Kb;
+                Ab = A + j * g.sAk;
+                Bb = B + j * g.sBk;
+            }
+            if (!TA) {
+                const float4 v = *reinterpret_cast<const float4*>(Ab + static_cast<long long>(rowc) * g.lda + kb);
+                a[u][0] = v.x; a[u][1] = v.y; a[u][2] = v.z; a[u][3] = v.w;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) a[u][i] = Ab[static_cast<long long>(kb + i) * g.lda + rowc];
+            }
+            if (!TB) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) b[u][i] = Bb[static_cast<long long>(kb + i) * g.ldb + colc];
+            } else {
+                const float4 v = *reinterpret_cast<const float4*>(Bb + static_cast<long long>(colc) * g.ldb + kb);
+                b[u][0] = v.x; b[u][1] = v.y; b[u][2] = v.z; b[u][3] = v.w;
+            }
+        }
+    };
     auto mma_pass = [&](int kp, const float (&a)[U][4], const float (&b)[U][4]) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -1159,7 +1194,15 @@ sgemm_tiny_kernel(const GemmArgs g)
     };
     int kp = kbeg + 16 * wave;
     if (!PIPE) {   // K fits one pass: one register set
-        if (kp < kend) {
+        if (fast_ops && kp + 64 * (U - 1) + 16 <= kend) {
+            float a0[U][4], b0[U][4];
+            load_pass_full(kp, a0, b0);
+            __builtin_amdgcn_sched_barrier(0);   // keep every load ahead of the first MFMA
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a0[u][i], b0[u][i], acc, 0, 0, 0);
+        } else if (kp < kend) {
             float a0[U][4], b0[U][4];
             load_pass(kp, a0, b0);
             mma_pass(kp, a0, b0);
