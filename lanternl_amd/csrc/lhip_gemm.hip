@@ -1149,15 +1149,18 @@ sgemm_tiny_kernel(const GemmArgs g)
             }
         }
     };
-    // A pass whose U steps all lie inside [kbeg, kend), with float4-aligned
-    // contiguous operands (and, for batch-reduce, 16-deep steps that never
-    // straddle a block), loads with no selects and no branches: each load's
-    // register is final, so all 8U loads issue before the first wait.
+    // When every live step of the pass is a full 16-deep step (K a multiple
+    // of 64), the operands' contiguous loads are float4-aligned and, for
+    // batch-reduce, a step never straddles a block, the pass loads with no
+    // selects: each load's register is final, dead steps are skipped by
+    // wave-uniform branches, and all the pass's loads issue before the first
+    // wait.
     const bool fast_ops = (TA || g.vecA) && (!TB || g.vecB) && (!BR || g.Kb % 16 == 0);
     auto load_pass_full = [&](int kp, float (&a)[U][4], float (&b)[U][4]) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int ks = kp + 64 * u;
+            if (ks >= kend) break;
             const int kl = ks + 4 * q;
             int kb = kl;
             const float* __restrict__ Ab = A;
@@ -1194,14 +1197,16 @@ sgemm_tiny_kernel(const GemmArgs g)
     };
     int kp = kbeg + 16 * wave;
     if (!PIPE) {   // K fits one pass: one register set
-        if (fast_ops && kp + 64 * (U - 1) + 16 <= kend) {
+        if (fast_ops && (kend - kbeg) % 64 == 0 && kp < kend) {
             float a0[U][4], b0[U][4];
             load_pass_full(kp, a0, b0);
             __builtin_amdgcn_sched_barrier(0);   // keep every load ahead of the first MFMA
 #pragma unroll
-            for (int u = 0; u < U; ++u)
+            for (int u = 0; u < U; ++u) {
+                if (kp + 64 * u >= kend) break;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a0[u][i], b0[u][i], acc, 0, 0, 0);
+            }
         } else if (kp < kend) {
             float a0[U][4], b0[U][4];
             load_pass(kp, a0, b0);
@@ -1617,12 +1622,27 @@ int sgemm_grouped_tn(const GroupedTN* g, int ngroups, int K, hipStream_t stream)
 bool use_small_kernel(int m, int n, int k) { return k <= 2048 || m <= 64 || n <= 64; }
 
 
-int splitk_plan(int m, int n, int k, int batch, size_t ws_floats, int* kchunk_out)
+int splitk_plan(int m, int n, int k, int batch, size_t ws_floats, int* kchunk_out, bool unreduced)
 {
     const int cus = st().cu_count > 0 ? st().cu_count : 256;
     const long long tiles64 = static_cast<long long>(ceil_div(m, 64)) * ceil_div(n, 64) * batch;
     const long long big_tiles = static_cast<long long>(ceil_div(m, 128)) * ceil_div(n, 128) * batch;
     if (big_tiles >= cus || tiles64 >= cus) return 1;
+    const long long mnb = static_cast<long long>(m) * n * batch;
+    const long long tiles32 = static_cast<long long>(ceil_div(m, 32)) * ceil_div(n, 32) * batch;
+    const int pass = 64 * kSmallU;
+    if (unreduced && use_small_kernel(m, n, k) && tiles32 < cus && k > pass) {
+        // 16x16 tiles whose consumer sums the slices itself (no reduce
+        // launch): one software pass per slice, slices a multiple of 64 deep
+        long long s = std::min<long long>(ceil_div(k, pass), 64);
+        if (mnb > 0) s = std::min<long long>(s, static_cast<long long>(ws_floats / mnb));
+        if (s < 2) return 1;
+        const int kchunk = ceil_div(ceil_div(k, static_cast<int>(s)), 64) * 64;
+        const int splits = ceil_div(k, kchunk);
+        if (splits < 2) return 1;
+        *kchunk_out = kchunk;
+        return splits;
+    }
     long long tiles, min_k;
     int unit;
     if (use_small_kernel(m, n, k)) {
@@ -1645,7 +1665,6 @@ int splitk_plan(int m, int n, int k, int batch, size_t ws_floats, int* kchunk_ou
     long long s = (2LL * cus + tiles - 1) / tiles;          // aim at ~2 workgroups per CU
     s = std::min<long long>(s, k / min_k);
     s = std::min<long long>(s, 64);
-    const long long mnb = static_cast<long long>(m) * n * batch;
     if (mnb > 0) s = std::min<long long>(s, static_cast<long long>(ws_floats / mnb));
     if (s < 2) return 1;
     const int kchunk = ceil_div(ceil_div(k, s), unit) * unit;
@@ -1726,7 +1745,7 @@ int sgemm_run(int ta, int tb, int m, int n, int k, float alpha,
     if (big_tiles >= cus) return launch_cfg<128, 128, 32>(ta, tb, g, batch, stream);
     if (tiles64 >= cus) return launch_cfg<64, 64, 32>(ta, tb, g, batch, stream);
     const bool small = use_small_kernel(m, n, g.K);
-    g.splits = o.ws ? splitk_plan(m, n, g.K, batch, o.ws_floats, &g.kchunk) : 1;
+    g.splits = o.ws ? splitk_plan(m, n, g.K, batch, o.ws_floats, &g.kchunk, o.splits_out != nullptr) : 1;
     g.ws = o.ws;
     if (o.splits_out) {
         if (alpha != 1.f || beta != 0.f || batch != 1 || o.R)

@@ -71,7 +71,9 @@ __global__ void __launch_bounds__(256) lm_fused_gemm_kernel(const FuseArgs f)
     __shared__ float red2[DUAL ? 4 : 1][4][64];
     __shared__ float ssr[4][64];
     __shared__ float row_s[16];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, lr = lane & 15, q = lane >> 4;
+    const int lane = threadIdx.x & 63, lr = lane & 15, q = lane >> 4;
+    // wave-uniform (readfirstlane): the K-step bounds below are scalar branches
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     int tm, tn;
     xcd_tile(blockIdx.x, gridDim.x, f.tiles_n, tm, tn);
     const int m0 = tm * 16, n0 = tn * 16;
@@ -80,51 +82,87 @@ __global__ void __launch_bounds__(256) lm_fused_gemm_kernel(const FuseArgs f)
     const float* __restrict__ B = f.B + y * f.sB;
     const int row = m0 + lr, col = n0 + lr;
     const bool rok = row < f.M, cok = col < f.N;
+    // Rows past M and columns past N load from row / column 0 (valid
+    // addresses): they reach only outputs that are not stored, and their row
+    // statistics are masked below (inv, coef and r are 0 for them).
+    const int rowc = rok ? row : 0, colc = cok ? col : 0;
     const bool writer = y == 0 && tn == 0;   // writes the row-stage outputs (h/inv or dx/dw partials)
 
+    // Every operand loads unconditionally: a lane past K (the last step, when
+    // K % 16 != 0) reads the step start and its A element is zeroed after the
+    // loads.  With no select or masked load on a loaded value, all of the
+    // pass's loads issue before the first wait.
     float a[U][4], w[U][4], b[U][4], b2[DUAL ? U : 1][4], x[NB ? U : 1][4], rs[NB ? U : 1][4];
     float ss = 0.f;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        const int k = 16 * wave + 64 * u + 4 * q;   // K % 4 == 0: the four k are all in or all out
-        const bool kin = k < K;
-        const long long ro = static_cast<long long>(row) * f.lda + k;
-        const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
-        float4 av = (rok && kin) ? ld4(f.A + ro) : z4;
-        for (int p = 1; p < f.a_parts; ++p) {
-            if (rok && kin) {
-                const float4 t = ld4(f.A + p * f.a_pstride + ro);
-                av.x += t.x; av.y += t.y; av.z += t.z; av.w += t.w;
-            }
-        }
-        to4(a[u], av);
-        to4(w[u], ((NORM || NB) && kin) ? ld4(f.nw + k) : z4);
+        const int ks = 16 * wave + 64 * u;          // wave-uniform step start
+        if (ks >= K) break;
+        const int k = ks + 4 * q;                   // K % 4 == 0: the four k are all in or all out
+        const int kc = k < K ? k : ks;
+        const long long ro = static_cast<long long>(rowc) * f.lda + kc;
+        to4(a[u], ld4(f.A + ro));
+        if constexpr (NORM || NB) to4(w[u], ld4(f.nw + kc));
         if constexpr (NB) {
-            to4(x[u], (rok && kin) ? ld4(f.nbx + ro) : z4);
-            to4(rs[u], (f.nbres && rok && kin) ? ld4(f.nbres + ro) : z4);
+            to4(x[u], ld4(f.nbx + ro));
+            if (f.nbres) to4(rs[u], ld4(f.nbres + ro));
+            else to4(rs[u], make_float4(0.f, 0.f, 0.f, 0.f));
         }
         if constexpr (TB) {
-            to4(b[u], (cok && kin) ? ld4(B + static_cast<long long>(col) * f.ldb + k) : z4);
+            to4(b[u], ld4(B + static_cast<long long>(colc) * f.ldb + kc));
         } else {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) b[u][i] = (cok && kin) ? B[static_cast<long long>(k + i) * f.ldb + col] : 0.f;
+            for (int i = 0; i < 4; ++i) b[u][i] = B[static_cast<long long>(kc + i) * f.ldb + colc];
         }
         if constexpr (DUAL) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                b2[u][i] = (cok && kin) ? f.B2[static_cast<long long>(k + i) * f.ldb + col] : 0.f;
+            for (int i = 0; i < 4; ++i) b2[u][i] = f.B2[static_cast<long long>(kc + i) * f.ldb + colc];
+        }
+    }
+    // A = sum of a_parts slices (unreduced split-K of the producer), summed
+    // in slice order; each slice's loads cover every step before its adds
+    if (f.a_parts > 1) {
+        for (int p = 1; p < f.a_parts; ++p) {
+            float t[U][4];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int ks = 16 * wave + 64 * u;
+                if (ks >= K) break;
+                const int k = ks + 4 * q;
+                const int kc = k < K ? k : ks;
+                to4(t[u], ld4(f.A + p * f.a_pstride + static_cast<long long>(rowc) * f.lda + kc));
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                if (16 * wave + 64 * u >= K) break;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) a[u][i] += t[u][i];
+            }
+        }
+    }
+    if (K % 16 != 0) {   // the last step is partial: lanes past K contribute zero
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int ks = 16 * wave + 64 * u;
+            if (ks >= K) break;
+            if (ks + 16 > K && ks + 4 * q >= K) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) a[u][i] = 0.f;
+            }
         }
     }
     // Row statistic over the whole row (lanes l%16 = r of all q groups and
     // waves): sum x^2 (NORM) or sum dy w x (NB).
     if constexpr (NORM || NB) {
 #pragma unroll
-        for (int u = 0; u < U; ++u)
+        for (int u = 0; u < U; ++u) {
+            if (16 * wave + 64 * u >= K) break;   // dead steps hold no data
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 if constexpr (NORM) ss += a[u][i] * a[u][i];
                 else ss += a[u][i] * w[u][i] * x[u][i];
             }
+        }
         ssr[wave][lane] = ss;
         __syncthreads();
         if (threadIdx.x < 16) {
@@ -152,13 +190,14 @@ __global__ void __launch_bounds__(256) lm_fused_gemm_kernel(const FuseArgs f)
         const float coef = row_s[lr];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
+            if (16 * wave + 64 * u >= K) break;
             const int k = 16 * wave + 64 * u + 4 * q;
             float o[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 float v = a[u][i] * w[u][i] * r - x[u][i] * coef;
                 if (f.nbres) v = v + rs[u][i];
-                o[i] = v;
+                o[i] = k < K ? v : 0.f;   // lanes past K read real x / dres: keep them out of the product
             }
             if (writer) {
 #pragma unroll
@@ -195,6 +234,7 @@ __global__ void __launch_bounds__(256) lm_fused_gemm_kernel(const FuseArgs f)
             const float r = row_s[lr];
 #pragma unroll
             for (int u = 0; u < U; ++u) {
+                if (16 * wave + 64 * u >= K) break;
                 const int k = 16 * wave + 64 * u + 4 * q;
                 if (k < K)
                     *reinterpret_cast<float4*>(f.h + static_cast<long long>(row) * K + k) =
