@@ -183,12 +183,14 @@ int lm_fused_gemm(const FuseCall& c, hipStream_t s);
 // for cfg, through one pinned staging buffer.
 int lm_checkpoint_io(const lhip_lm_config_t& cfg, float* dev_params, const char* path, const lhip_ckpt_info_t* info,
                      lhip_ckpt_header_t* header, bool save);
-// Fused per-(window, head) attention of the LMTrain step (T <= 64, head_dim <= 64, even).
+// Fused attention of the LMTrain step (T <= 64, head_dim <= 64, even), one
+// workgroup per (window, head, 16-row block); the backward reads the forward's
+// ctx (O) for rowsum(dO o O).
 bool attn_fused_ok(int T, int hd);
 int attn_fwd(const float* qkv, const float2* cs, float* P, float* ctx, int B, int H, int T, int hd, float scale,
              int causal, hipStream_t s);
-int attn_bwd(const float* qkv, const float2* cs, const float* P, const float* dctx, float* dqkv, int B, int H, int T,
-             int hd, float scale, int causal, hipStream_t s);
+int attn_bwd(const float* qkv, const float2* cs, const float* P, const float* ctx, const float* dctx, float* dqkv, int B,
+             int H, int T, int hd, float scale, int causal, hipStream_t s);
 
 // Options of the GEMM launcher.
 //   inner / s?2 : second batch level -- blockIdx.y = outer * inner + i and operand

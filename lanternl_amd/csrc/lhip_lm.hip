@@ -370,7 +370,7 @@ int enqueue_step(LmModel& m, hipStream_t s, const Hyper& hp, bool device_hyper)
         }
         if (m.fused_attn) {
             // dP, dv, softmax backward, dq, dk and the inverse RoPE per (window, head)
-            LM_TRY(attn_bwd(qkv, m.rope_cs, P, m.dctx, dqkv, m.B, H, T, hd, scale, causal, s));
+            LM_TRY(attn_bwd(qkv, m.rope_cs, P, ctx, m.dctx, dqkv, m.B, H, T, hd, scale, causal, s));
         } else {
             // per (window, head): dP = dO . v^T ; dv = P^T . dO
             LM_TRY(q.hgemm(0, 1, T, T, hd, m.dctx, D, hd, TD, qkv + 2 * ND, D, hd, TD, m.dP, T, TT, HTT));

@@ -22,10 +22,10 @@ from tests.gpu_util import announce, rel_fro
 pytestmark = pytest.mark.gpu
 
 
-def _run_case(V, D, L, H, F, B, T, steps, lr, std, seed, graph=False, clip=1.0, mom=0.9, wd=0.01):
+def _run_case(V, D, L, H, F, B, T, steps, lr, std, seed, graph=False, clip=1.0, mom=0.9, wd=0.01, causal=True):
     rng = np.random.default_rng(seed)
-    cfg = O.lm_cfg(V, D, L, H, F)
-    gpu = lmtrain.GpuLMStep(V, D, L, H, F, B, T)
+    cfg = O.lm_cfg(V, D, L, H, F, causal=causal)
+    gpu = lmtrain.GpuLMStep(V, D, L, H, F, B, T, causal=causal)
     p32 = lmtrain.init_params(gpu.cfg, rng, std)
     gpu.set_params(p32)
     if graph:
@@ -92,6 +92,18 @@ def test_lm_step_attention_load_paths(D, H, T):
     both ways (head_dim 6)."""
     announce("lm attention loads", D, H, T)
     gpu, res = _run_case(30, D, 1, H, 2 * D, 2, T, steps=1, lr=0.1, std=0.3, seed=7 + D + T)
+    _check(res)
+    gpu.close()
+
+
+@pytest.mark.parametrize("D,H", [(32, 2), (12, 2)])
+def test_lm_step_non_causal(D, H):
+    """Non-causal attention over T = 40 (three 16-row blocks, the last ragged):
+    every key block is visible from every query block, so the backward's dq
+    and dk/dv jobs each sum shares from all three waves; float4 (head_dim 16)
+    and element-wise (head_dim 6) loads."""
+    announce("lm non-causal", D, H)
+    gpu, res = _run_case(30, D, 1, H, 2 * D, 2, 40, steps=1, lr=0.1, std=0.3, seed=11 + D, causal=False)
     _check(res)
     gpu.close()
 
