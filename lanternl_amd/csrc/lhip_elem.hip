@@ -357,9 +357,11 @@ __global__ void embed_fwd_kernel(const float* __restrict__ table, const int* __r
 
 // dtable[v] (+)= scale * sum over tokens i with ids[i] == v, added in token
 // order (the Lua loop order, tensor2.lua:592-607), one wave per vocabulary row:
-// the ids are scanned 64 at a time and matches found with a wave ballot.  No
-// atomics, so the result is deterministic.  Ids outside [0, vocab) are skipped.
+// the ids are loaded 1024 at a time (16 per lane, all issued before the first
+// compare) and matches found 64 at a time with a wave ballot.  No atomics, so
+// the result is deterministic.  Ids outside [0, vocab) are skipped.
 constexpr int kEmbedChunk = 512;  // columns per pass (8 per lane)
+constexpr int kEmbedIds = 16;     // id chunks of 64 per scan pass
 
 __global__ void __launch_bounds__(64)
 embed_bwd_kernel(const float* __restrict__ g, const int* __restrict__ ids, float* __restrict__ dtable,
@@ -375,18 +377,28 @@ embed_bwd_kernel(const float* __restrict__ g, const int* __restrict__ ids, float
             const int d = d0 + lane + 64 * k;
             a[k] = (acc && d < dim) ? row[d] : 0.f;
         }
-        for (int i0 = 0; i0 < n; i0 += 64) {
-            const int i = i0 + lane;
-            const bool hit = i < n && ids[i] == v;
-            unsigned long long mask = __ballot(hit);
-            while (mask) {
-                const int b = __ffsll(static_cast<long long>(mask)) - 1;
-                mask &= mask - 1;
-                const float* gr = g + static_cast<long long>(i0 + b) * dim;
+        for (int c0 = 0; c0 < n; c0 += 64 * kEmbedIds) {
+            int idv[kEmbedIds];
 #pragma unroll
-                for (int k = 0; k < kEmbedChunk / 64; ++k) {
-                    const int d = d0 + lane + 64 * k;
-                    if (d < dim) a[k] = a[k] + scale * gr[d];
+            for (int k = 0; k < kEmbedIds; ++k) {
+                if (c0 + 64 * k >= n) break;                  // uniform
+                const int i = c0 + 64 * k + lane;
+                idv[k] = ids[min(i, n - 1)];
+            }
+#pragma unroll
+            for (int k = 0; k < kEmbedIds; ++k) {
+                if (c0 + 64 * k >= n) break;
+                const int i0 = c0 + 64 * k;
+                unsigned long long mask = __ballot(i0 + lane < n && idv[k] == v);
+                while (mask) {
+                    const int b = __ffsll(static_cast<long long>(mask)) - 1;
+                    mask &= mask - 1;
+                    const float* gr = g + static_cast<long long>(i0 + b) * dim;
+#pragma unroll
+                    for (int j = 0; j < kEmbedChunk / 64; ++j) {
+                        const int d = d0 + lane + 64 * j;
+                        if (d < dim) a[j] = a[j] + scale * gr[d];
+                    }
                 }
             }
         }

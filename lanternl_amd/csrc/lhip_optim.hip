@@ -25,12 +25,23 @@ sumsq_stage1(const float* __restrict__ x, long long n, double* __restrict__ part
     const long long t0 = blockIdx.x * static_cast<long long>(kRedThreads) + threadIdx.x;
     double s = 0.0;
     if (vec) {
+        // four grid-stride float4 per pass, all loaded before the first add
+        // (the summation order is the plain grid-stride order)
         const float4* x4 = reinterpret_cast<const float4*>(x);
         const long long n4 = n >> 2;
-        for (long long i = t0; i < n4; i += stride) {
-            const float4 v = x4[i];
-            s += static_cast<double>(v.x) * v.x + static_cast<double>(v.y) * v.y +
-                 static_cast<double>(v.z) * v.z + static_cast<double>(v.w) * v.w;
+        for (long long base = t0; base < n4; base += 4 * stride) {
+            float4 v[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const long long i = base + k * stride;
+                v[k] = i < n4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                if (base + k * stride >= n4) break;
+                s += static_cast<double>(v[k].x) * v[k].x + static_cast<double>(v[k].y) * v[k].y +
+                     static_cast<double>(v[k].z) * v[k].z + static_cast<double>(v[k].w) * v[k].w;
+            }
         }
         for (long long i = 4 * n4 + t0; i < n; i += stride) s += static_cast<double>(x[i]) * x[i];
     } else {
@@ -55,60 +66,110 @@ __global__ void __launch_bounds__(64) sum_stage2(const double* __restrict__ part
     if (threadIdx.x == 0) out[0] = s;
 }
 
+// Global gradient norm from the stage-1 partials (nparts > 0; every block sums
+// them in sum_stage2's order, so all blocks, and the two-kernel form, agree bit
+// for bit) or from the finished total (nparts == 0).
+__device__ __forceinline__ double grad_total(const double* __restrict__ sumsq, int nparts)
+{
+    if (nparts <= 0) return sumsq[0];
+    __shared__ double tot;
+    if (threadIdx.x < 64) {
+        double s = 0.0;
+        for (int i = threadIdx.x; i < nparts; i += 64) s += sumsq[i];
+        s = wave_sum(s);
+        if (threadIdx.x == 0) tot = s;
+    }
+    __syncthreads();
+    return tot;
+}
+
+__device__ __forceinline__ float ld_lane(const float4& v, int k) { return k == 0 ? v.x : k == 1 ? v.y : k == 2 ? v.z : v.w; }
+__device__ __forceinline__ void st_lane(float4& v, int k, float x)
+{
+    if (k == 0) v.x = x; else if (k == 1) v.y = x; else if (k == 2) v.z = x; else v.w = x;
+}
+
+struct SgdHyper {
+    float lr, momentum, wd, grad_scale;
+    int nesterov;
+};
+
+// optim2.SGD on one element after scale and clip; g receives the gradient used
+__device__ __forceinline__ void sgd_elem(float& p, float& g, float& v, const SgdHyper& h, float clipf)
+{
+    float gk = g * h.grad_scale;
+    if (clipf != 1.0f) gk = gk * clipf;
+    g = gk;
+    if (h.wd != 0.f) gk = gk + h.wd * p;
+    if (h.momentum > 0.f) {
+        const float vk = h.momentum * v + gk;
+        v = vk;
+        p = h.nesterov ? p - h.lr * (gk + h.momentum * vk) : p - h.lr * vk;
+    } else {
+        p = p - h.lr * gk;
+    }
+}
+
 // One SGD step over n parameters with the LMTrain step logic.  sumsq is the
 // sum of squares of the RAW gradients; the norm of the scaled gradients is
 // grad_scale * sqrt(sumsq).  g is overwritten with the gradient actually used
 // (after scale and clip) so callers can inspect it, as optim2 mutates grads.
-//
-// With nparts > 0, `sumsq` holds the nparts stage-1 partials instead of the
-// total: every block sums them in sum_stage2's order (so all blocks, and the
-// two-kernel form, agree bit for bit), which saves the second reduction launch.
+// With vec (p, g, v 16-byte aligned) the body runs on float4; a thread's first
+// float4 is fetched before the norm is reduced, so the loads overlap it.
 __global__ void __launch_bounds__(256)
 sgd_step_kernel(float* __restrict__ p, float* __restrict__ g, float* __restrict__ v, long long n,
                 const double* __restrict__ sumsq, int nparts, float lr, float momentum, float wd,
                 float grad_scale, float clip_norm, int nesterov, float* __restrict__ gnorm_out,
-                int* __restrict__ applied_out, const float* __restrict__ hyper)
+                int* __restrict__ applied_out, const float* __restrict__ hyper, int vec)
 {
     if (hyper) {   // hyper-parameters resident on the device (graph replay)
         lr = hyper[0]; momentum = hyper[1]; wd = hyper[2]; clip_norm = hyper[3];
         nesterov = hyper[4] != 0.f;
     }
-    double total;
-    if (nparts > 0) {
-        __shared__ double tot;
-        if (threadIdx.x < 64) {
-            double s = 0.0;
-            for (int i = threadIdx.x; i < nparts; i += 64) s += sumsq[i];
-            s = wave_sum(s);
-            if (threadIdx.x == 0) tot = s;
-        }
-        __syncthreads();
-        total = tot;
-    } else {
-        total = sumsq[0];
-    }
-    const double norm = static_cast<double>(grad_scale) * sqrt(total);
-    const bool finite = isfinite(norm);
+    const SgdHyper hy{lr, momentum, wd, grad_scale, nesterov};
     const long long t0 = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
+    const long long stride = static_cast<long long>(gridDim.x) * blockDim.x;
+    const long long n4 = vec ? (n >> 2) : 0;
+    float4* p4 = reinterpret_cast<float4*>(p);
+    float4* g4 = reinterpret_cast<float4*>(g);
+    float4* v4 = reinterpret_cast<float4*>(v);
+    const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 pv = z4, gv = z4, vv = z4;
+    if (t0 < n4) {
+        gv = g4[t0];
+        pv = p4[t0];
+        if (momentum > 0.f) vv = v4[t0];
+    }
+    const double norm = static_cast<double>(grad_scale) * sqrt(grad_total(sumsq, nparts));
+    const bool finite = isfinite(norm);
     if (t0 == 0) {
         if (gnorm_out) gnorm_out[0] = static_cast<float>(norm);
         if (applied_out) applied_out[0] = finite ? 1 : 0;
     }
     if (!finite) return;   // lmtrain.lua:1214-1218: skip the step
     const float clipf = (clip_norm > 0.f && norm > clip_norm) ? static_cast<float>(clip_norm / norm) : 1.0f;
-    const long long stride = static_cast<long long>(gridDim.x) * blockDim.x;
-    for (long long i = t0; i < n; i += stride) {
-        float gk = g[i] * grad_scale;
-        if (clipf != 1.0f) gk = gk * clipf;
-        g[i] = gk;
-        if (wd != 0.f) gk = gk + wd * p[i];
-        if (momentum > 0.f) {
-            const float vk = momentum * v[i] + gk;
-            v[i] = vk;
-            p[i] = nesterov ? p[i] - lr * (gk + momentum * vk) : p[i] - lr * vk;
-        } else {
-            p[i] = p[i] - lr * gk;
+    for (long long i = t0; i < n4; i += stride) {
+        if (i != t0) {
+            gv = g4[i];
+            pv = p4[i];
+            if (momentum > 0.f) vv = v4[i];
         }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            float pk = ld_lane(pv, k), gk = ld_lane(gv, k), vk = ld_lane(vv, k);
+            sgd_elem(pk, gk, vk, hy, clipf);
+            st_lane(pv, k, pk); st_lane(gv, k, gk); st_lane(vv, k, vk);
+        }
+        g4[i] = gv;
+        if (momentum > 0.f) v4[i] = vv;
+        p4[i] = pv;
+    }
+    for (long long i = 4 * n4 + t0; i < n; i += stride) {
+        float pk = p[i], gk = g[i], vk = momentum > 0.f ? v[i] : 0.f;
+        sgd_elem(pk, gk, vk, hy, clipf);
+        g[i] = gk;
+        if (momentum > 0.f) v[i] = vk;
+        p[i] = pk;
     }
 }
 
@@ -132,21 +193,7 @@ adamw_step_kernel(float* __restrict__ p, float* __restrict__ g, float* __restric
         lr = hyper[0]; wd = hyper[2]; clip_norm = hyper[3];
         beta1 = hyper[5]; beta2 = hyper[6]; eps = hyper[7]; parity = hyper[8] != 0.f ? 1 : 0;
     }
-    double total;
-    if (nparts > 0) {
-        __shared__ double tot;
-        if (threadIdx.x < 64) {
-            double s = 0.0;
-            for (int i = threadIdx.x; i < nparts; i += 64) s += sumsq[i];
-            s = wave_sum(s);
-            if (threadIdx.x == 0) tot = s;
-        }
-        __syncthreads();
-        total = tot;
-    } else {
-        total = sumsq[0];
-    }
-    const double norm = static_cast<double>(grad_scale) * sqrt(total);
+    const double norm = static_cast<double>(grad_scale) * sqrt(grad_total(sumsq, nparts));
     const bool finite = isfinite(norm);
     const int t_old = tcount ? tcount[parity] : t_in - 1;
     const int t = t_old + 1;
@@ -237,10 +284,12 @@ int sgd_step(float* p, float* g, float* v, long long n, const double* sumsq_dev,
     const int cus = st().cu_count > 0 ? st().cu_count : 256;
     long long blocks = (n + 255) / 256;
     if (blocks > 4LL * cus) blocks = 4LL * cus;
+    const int vec = (aligned16(p) && aligned16(g) && (!v || aligned16(v))) ? 1 : 0;
+    if (vec) blocks = std::min<long long>((n / 4 + 255) / 256, 4LL * cus);
     if (blocks < 1) blocks = 1;
     sgd_step_kernel<<<static_cast<int>(blocks), 256, 0, s>>>(p, g, v, n, sumsq_dev, nparts, lr, momentum, wd,
                                                            grad_scale, clip_norm, nesterov, gnorm_out, applied_out,
-                                                           hyper_dev);
+                                                           hyper_dev, vec);
     return check_launch("sgd_step");
 }
 
