@@ -1149,8 +1149,10 @@ sgemm_tiny_kernel(const GemmArgs g)
             }
         }
     };
-    // When every live step of the pass is a full 16-deep step (K a multiple
-    // of 64), the operands' contiguous loads are float4-aligned and, for
+    // When every live step of the pass is a full 16-deep step (the slice
+    // length kend - kbeg a multiple of 16: steps start at kbeg + 16j, so a
+    // step that starts before kend also ends by it), the operands' contiguous
+    // loads are float4-aligned and, for
     // batch-reduce, a step never straddles a block, the pass loads with no
     // selects: each load's register is final, dead steps are skipped by
     // wave-uniform branches, and all the pass's loads issue before the first
@@ -1197,7 +1199,7 @@ sgemm_tiny_kernel(const GemmArgs g)
     };
     int kp = kbeg + 16 * wave;
     if (!PIPE) {   // K fits one pass: one register set
-        if (fast_ops && (kend - kbeg) % 64 == 0 && kp < kend) {
+        if (fast_ops && (kend - kbeg) % 16 == 0 && kp < kend) {
             float a0[U][4], b0[U][4];
             load_pass_full(kp, a0, b0);
             __builtin_amdgcn_sched_barrier(0);   // keep every load ahead of the first MFMA
