@@ -442,14 +442,18 @@ sgemm_256_kernel(const GemmArgs g)
     tile_coords(blockIdx.x, gridDim.x, g.tiles_m, g.tiles_n, tm, tn);
     const int m0 = tm * kBig, n0 = tn * kBig;
     const long long zo = blockIdx.y / g.inner, zi = blockIdx.y % g.inner;
-    const float* __restrict__ A = g.A + zo * g.sA2 + zi * g.sA;
-    const float* __restrict__ B = g.B + zo * g.sB2 + zi * g.sB;
+    // split-K: this workgroup takes k in [kbeg, kbeg + K); the operands are
+    // offset to the slice start (k runs along a stored row of A when !TA and
+    // of B when TB, down the stored columns otherwise)
+    const int kbeg = blockIdx.z * g.kchunk;
+    const int K = min(g.K, kbeg + g.kchunk) - kbeg;
+    const float* __restrict__ A = g.A + zo * g.sA2 + zi * g.sA + (TA ? static_cast<long long>(kbeg) * g.lda : kbeg);
+    const float* __restrict__ B = g.B + zo * g.sB2 + zi * g.sB + (TB ? kbeg : static_cast<long long>(kbeg) * g.ldb);
     const long long coff = zo * g.sC2 + zi * g.sC;
     const int wm = (wave >> 1) * 128, wn = (wave & 1) * 128;
 
     BigTileRegs<TA, FULL> ra;    // op(A): row m; stored M x K (!TA) or K x M (TA)
     BigTileRegs<!TB, FULL> rb;   // op(B): row n; stored N x K (TB) or K x N (!TB)
-    const int K = g.K;
     auto gload = [&](int s, int k0) {
         ra.load_slot(s, A, g.lda, m0, k0, M, K, g.vecA, tid);
         rb.load_slot(s, B, g.ldb, n0, k0, N, K, g.vecB, tid);
@@ -548,6 +552,25 @@ sgemm_256_kernel(const GemmArgs g)
         __builtin_amdgcn_sched_barrier(0);
     }
 
+    if (g.splits > 1) {
+        // raw slice sums, [slice][batch][M][N]; the ordered reduce applies
+        // alpha, beta and R
+        float* __restrict__ wz =
+            g.ws + (static_cast<long long>(blockIdx.z) * gridDim.y + blockIdx.y) * (static_cast<long long>(M) * N);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int col = n0 + wn + 32 * j + lr;
+                if (!FULL && col >= N) continue;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int row = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+                    if (FULL || row < M) wz[static_cast<long long>(row) * N + col] = acc[i][j][r];
+                }
+            }
+        return;
+    }
     float* __restrict__ C = g.C + coff;
     const float* R = g.R ? g.R + coff : C;
     const int ldr = g.R ? g.ldr : g.ldc;
@@ -575,15 +598,20 @@ sgemm_256_kernel(const GemmArgs g)
     else epilogue(std::false_type{});
 }
 
+int launch_reduce(const GemmArgs& g, int batch, hipStream_t stream);
+
 int launch_256(int ta, int tb, GemmArgs g, int batch, hipStream_t stream)
 {
     g.tiles_m = ceil_div(g.M, kBig);
     g.tiles_n = ceil_div(g.N, kBig);
     const long long nwg = static_cast<long long>(g.tiles_m) * g.tiles_n;
     if (nwg > 0x7fffffffLL) return fail(LHIP_E_CAPACITY, "sgemm: %lld workgroups exceed the grid limit", nwg);
-    g.splits = 1; g.kchunk = g.K; g.ws = nullptr;
-    dim3 grid(static_cast<unsigned>(nwg), batch, 1), block(kThreads, 1, 1);
-    const bool full = g.M % kBig == 0 && g.N % kBig == 0 && g.K % kBigK == 0 && (ta || g.vecA) && (!tb || g.vecB);
+    if (g.splits <= 1 || !g.ws) { g.splits = 1; g.kchunk = g.K; g.ws = nullptr; }
+    dim3 grid(static_cast<unsigned>(nwg), batch, g.splits), block(kThreads, 1, 1);
+    // FULL: every tile and every K slice whole (slices start at multiples of
+    // kchunk, itself a multiple of the 32-deep K tile)
+    const bool full = g.M % kBig == 0 && g.N % kBig == 0 && g.K % kBigK == 0 && g.kchunk % kBigK == 0 &&
+                      (ta || g.vecA) && (!tb || g.vecB);
     auto go = [&](auto fullc) {
         constexpr bool F = decltype(fullc)::value;
         if (!ta && !tb) sgemm_256_kernel<false, false, F><<<grid, block, 0, stream>>>(g);
@@ -593,7 +621,9 @@ int launch_256(int ta, int tb, GemmArgs g, int batch, hipStream_t stream)
     };
     if (full) go(std::true_type{});
     else go(std::false_type{});
-    return check_launch("sgemm (256): kernel launch");
+    const int rc = check_launch("sgemm (256): kernel launch");
+    if (rc != LHIP_OK || g.splits <= 1) return rc;
+    return launch_reduce(g, batch, stream);
 }
 
 // ---------------------------------------------------------------------------
@@ -1624,6 +1654,28 @@ int sgemm_grouped_tn(const GroupedTN* g, int ngroups, int K, hipStream_t stream)
 bool use_small_kernel(int m, int n, int k) { return k <= 2048 || m <= 64 || n <= 64; }
 
 
+// 256x256 tiles split over K (one batch): when the tiles alone would fill
+// between a quarter and all of the CUs (e.g. 2048^3: 64 tiles), each tile's K
+// is cut into slices of at least 512 so that tiles x slices covers the CUs;
+// the slices are summed in order by the reduce.  K % 32 == 0 keeps every
+// slice whole.  Returns the slice count (1: not this path).
+int split256_plan(int m, int n, int k, int batch, size_t ws_floats, int* kchunk_out)
+{
+    const int cus = st().cu_count > 0 ? st().cu_count : 256;
+    const long long tiles = static_cast<long long>(ceil_div(m, kBig)) * ceil_div(n, kBig);
+    if (batch != 1 || tiles >= cus || 4 * tiles < cus || k % kBigK != 0) return 1;
+    long long s = (cus + tiles - 1) / tiles;
+    s = std::min<long long>(s, k / 512);
+    const long long mn = static_cast<long long>(m) * n;
+    if (mn > 0) s = std::min<long long>(s, static_cast<long long>(ws_floats / mn));
+    if (s < 2) return 1;
+    const int kchunk = ceil_div(ceil_div(k, static_cast<int>(s)), kBigK) * kBigK;
+    const int splits = ceil_div(k, kchunk);
+    if (splits < 2) return 1;
+    *kchunk_out = kchunk;
+    return splits;
+}
+
 int splitk_plan(int m, int n, int k, int batch, size_t ws_floats, int* kchunk_out, bool unreduced)
 {
     const int cus = st().cu_count > 0 ? st().cu_count : 256;
@@ -1744,6 +1796,14 @@ int sgemm_run(int ta, int tb, int m, int n, int k, float alpha,
     }
     const long long tiles256 = static_cast<long long>(ceil_div(m, kBig)) * ceil_div(n, kBig) * batch;
     if (tiles256 >= cus) return launch_256(ta, tb, g, batch, stream);
+    if (!br && o.ws && !o.splits_out) {
+        int kc = 0;
+        const int s256 = split256_plan(m, n, k, batch, o.ws_floats, &kc);
+        if (s256 > 1) {
+            g.splits = s256; g.kchunk = kc; g.ws = o.ws;
+            return launch_256(ta, tb, g, batch, stream);
+        }
+    }
     if (big_tiles >= cus) return launch_cfg<128, 128, 32>(ta, tb, g, batch, stream);
     if (tiles64 >= cus) return launch_cfg<64, 64, 32>(ta, tb, g, batch, stream);
     const bool small = use_small_kernel(m, n, g.K);
@@ -1789,9 +1849,13 @@ static int sgemm_immediate(int transa, int transb, int m, int n, int k, float al
     int kchunk = 0;
     if (m > 0 && n > 0 && k > 0 && batch > 0) {
         const size_t cap = static_cast<size_t>(1) << 26;
-        const int splits = lhip::skinny_ok(transa, transb, m, n, batch, 1)
-                               ? lhip::skinny_plan(m, n, k, cap, &kchunk)
-                               : lhip::splitk_plan(m, n, k, batch, cap, &kchunk);
+        int splits = 1;
+        if (lhip::skinny_ok(transa, transb, m, n, batch, 1)) {
+            splits = lhip::skinny_plan(m, n, k, cap, &kchunk);
+        } else {
+            splits = lhip::split256_plan(m, n, k, batch, cap, &kchunk);
+            if (splits <= 1) splits = lhip::splitk_plan(m, n, k, batch, cap, &kchunk);
+        }
         if (splits > 1) {
             o.ws_floats = static_cast<size_t>(splits) * m * n * batch;
             int rc = lhip::workspace(o.ws_floats * sizeof(float), reinterpret_cast<void**>(&o.ws));

@@ -230,6 +230,7 @@ int sgemm_run(int transa, int transb, int m, int n, int k, float alpha,
               float* C, int ldc, long long sC, int batch, const GemmOpts& o, hipStream_t stream);
 // Number of K slices sgemm_run would use (1 = none); *kchunk receives the slice length.
 int splitk_plan(int m, int n, int k, int batch, size_t ws_floats, int* kchunk, bool unreduced = false);
+int split256_plan(int m, int n, int k, int batch, size_t ws_floats, int* kchunk);
 
 int sgemm_launch(int transa, int transb, int m, int n, int k, float alpha,
                  const float* A, int lda, const float* B, int ldb, float beta,

@@ -134,9 +134,10 @@ def test_gemm_strided_batched_per_head_qk():
             assert rel_fro(s[h], O.matmul_nt(qh, kh)) <= TOL
 
 
-@pytest.mark.parametrize("n", [1024, 4096])
+@pytest.mark.parametrize("n", [1024, 2048, 4096])
 def test_gemm_square_large(n):
-    """Config C5 square shapes (1024^3, 4096^3), all three products, vs numpy float64."""
+    """Config C5 square shapes (1024^3, 2048^3, 4096^3), all three products, vs
+    numpy float64.  2048^3 runs 64 256x256 tiles split four ways over K."""
     announce("gemm square", n)
     rng = np.random.default_rng(n)
     a = rng.uniform(-1, 1, (n, n)).astype(np.float32)
@@ -253,11 +254,11 @@ def test_gemm_c3_lm_head_shapes(ta, tb):
 
 @pytest.mark.parametrize("m,n,k,batch", [(512, 128, 2000, 1), (128, 128, 4096, 3), (64, 64, 1000, 2),
                                          (96, 64, 1100, 2), (512, 512, 2048, 1), (33, 70, 999, 1),
-                                         (1, 4096, 4096, 1)])
+                                         (1, 4096, 4096, 1), (2048, 2048, 1024, 1)])
 def test_gemm_split_k_alpha_beta_batched(m, n, k, batch):
-    """Long-K shapes with few output tiles: the 64x64 and 32x32 kernels split K
-    (alpha/beta apply once, after the ordered sum of the slices); the 16x16
-    kernel walks long K in software-pipelined passes."""
+    """Long-K shapes with few output tiles: the 256x256 (2048 x 2048), 64x64 and
+    32x32 kernels split K (alpha/beta apply once, after the ordered sum of the
+    slices); the 16x16 kernel walks long K in software-pipelined passes."""
     announce("gemm split-k", m, n, k, batch)
     rng = np.random.default_rng(m + n + k)
     a = f32(rng.uniform(-1, 1, (batch, m, k)))
