@@ -761,9 +761,9 @@ sgemm_small_kernel(const GemmArgs g)
 }
 
 // ---------------------------------------------------------------------------
-// Skinny products (M <= 16 rows of C, B stored K x N): the work is one
+// Skinny products (M <= 64 rows of C, B stored K x N): the work is one
 // streaming pass over B, HBM-bound.  With one or two rows of C this VALU form
-// streams B (2 to 4 FMAs per float4 of B); three to sixteen rows take the MFMA
+// streams B (2 to 4 FMAs per float4 of B); three to 64 rows take the MFMA
 // form below, since at 16 rows the 64 FMAs per float4 outrun the VALU (packed
 // fp32 is not used).  Each wave covers 256 columns with one float4 per lane.  The workgroup walks its K slice in chunks of kSkinnyKC
 // rows: the chunk of A is staged in LDS as [k][m] (zero past M and past the
@@ -772,7 +772,7 @@ sgemm_small_kernel(const GemmArgs g)
 // Waves 1..3 hand their sums to wave 0 through LDS, added in wave order.  A K
 // split over blockIdx.y writes [split][M][N] partials that splitk_reduce adds
 // in split order.
-constexpr int kSkinnyMax = 16;
+constexpr int kSkinnyMax = 64;
 constexpr int kSkinnyCols = 256;    // columns per workgroup (64 lanes x float4)
 constexpr int kSkinnyKC = 256;      // K rows of A staged per chunk
 
@@ -897,25 +897,27 @@ sgemm_skinny_kernel(const GemmArgs g)
     }
 }
 
-// Skinny products with 3..16 rows of C on the matrix cores.  The VALU form
+// Skinny products with 3..64 rows of C on the matrix cores.  The VALU form
 // above would spend up to 64 FMAs per float4 of B, more than the VALU issues at
-// HBM rate; v_mfma_f32_16x16x4f32 covers 16 rows at once.  Each wave covers 64
+// HBM rate; v_mfma_f32_16x16x4f32 covers 16 rows at once, and MG groups of 16
+// rows (MG = ceil(M / 16)) reuse each float4 of B for 4 * MG MFMAs.  Each wave covers 64
 // columns: lane (q = l/16, p = l%16) loads the float4 B[k][c0+4p .. c0+4p+3] of
 // row k = k0 + 4s + q of step s (four 256-byte row segments per step), and MFMA
 // e (e = 0..3) multiplies element e of it, so MFMA e computes the columns
 // c0 + 4p + e with A[p][k] as its A operand (zero for p >= M).  Accumulator
 // register r of MFMA e then holds C[4q + r][c0 + 4p + e]: each lane owns a 4x4
-// block, stored as four float4 rows.  Waves take the 4-row steps w, w+4, ...
+// block, stored as four float4 rows (per row group g: rows 16g + 4q + r).
+// Waves take the 4-row steps w, w+4, ...
 // of the workgroup's K slice, U steps in flight, and hand their sums to wave 0
 // through LDS (added in wave order).  Splits as in the VALU form.
 constexpr int kSkinnyMfmaCols = 64;
 
-template <bool TA, bool VEC>
+template <bool TA, bool VEC, int MG>
 __global__ void __launch_bounds__(256)
 sgemm_skinny_mfma_kernel(const GemmArgs g)
 {
     constexpr int U = 8;
-    __shared__ floatx4 red[3][4][64];
+    __shared__ floatx4 red[3][4 * MG][64];
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int p = lane & 15, q = lane >> 4;
@@ -924,19 +926,21 @@ sgemm_skinny_mfma_kernel(const GemmArgs g)
     const int k0 = blockIdx.y * g.kchunk;
     const int k1 = min(g.K, k0 + g.kchunk);
     const bool colfull = VEC && col + 3 < N;
-    const bool mok = p < M;
     const int nsteps = (k1 - k0 + 3) / 4;
-    floatx4 acc[4];
+    floatx4 acc[MG][4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) acc[e] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int gi = 0; gi < MG; ++gi)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[gi][e] = floatx4{0.f, 0.f, 0.f, 0.f};
     for (int s0 = wv; s0 < nsteps; s0 += 4 * U) {
         float4 b[U];
-        float a[U];
+        float a[MG][U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int kk = k0 + 4 * (s0 + 4 * u) + q;
             b[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-            a[u] = 0.f;
+#pragma unroll
+            for (int gi = 0; gi < MG; ++gi) a[gi][u] = 0.f;
             if (kk < k1) {
                 const float* src = g.B + static_cast<long long>(kk) * g.ldb + col;
                 if (colfull) {
@@ -948,40 +952,236 @@ sgemm_skinny_mfma_kernel(const GemmArgs g)
                     b[u].z = col + 2 < N ? src[2] : 0.f;
                     b[u].w = col + 3 < N ? src[3] : 0.f;
                 }
-                if (mok)
-                    a[u] = TA ? g.A[static_cast<long long>(kk) * g.lda + p] : g.A[static_cast<long long>(p) * g.lda + kk];
+#pragma unroll
+                for (int gi = 0; gi < MG; ++gi) {
+                    const int row = 16 * gi + p;
+                    if (row < M)
+                        a[gi][u] = TA ? g.A[static_cast<long long>(kk) * g.lda + row]
+                                      : g.A[static_cast<long long>(row) * g.lda + kk];
+                }
             }
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             if (s0 + 4 * u < nsteps) {     // uniform
-                acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u], b[u].x, acc[0], 0, 0, 0);
-                acc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u], b[u].y, acc[1], 0, 0, 0);
-                acc[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u], b[u].z, acc[2], 0, 0, 0);
-                acc[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u], b[u].w, acc[3], 0, 0, 0);
+#pragma unroll
+                for (int gi = 0; gi < MG; ++gi) {
+                    acc[gi][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[gi][u], b[u].x, acc[gi][0], 0, 0, 0);
+                    acc[gi][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[gi][u], b[u].y, acc[gi][1], 0, 0, 0);
+                    acc[gi][2] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[gi][u], b[u].z, acc[gi][2], 0, 0, 0);
+                    acc[gi][3] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[gi][u], b[u].w, acc[gi][3], 0, 0, 0);
+                }
             }
         }
     }
     if (wv > 0) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) red[wv - 1][e][lane] = acc[e];
+        for (int gi = 0; gi < MG; ++gi)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) red[wv - 1][4 * gi + e][lane] = acc[gi][e];
     }
     __syncthreads();
     if (wv != 0) return;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
+    for (int gi = 0; gi < MG; ++gi)
 #pragma unroll
-        for (int w = 0; w < 3; ++w) acc[e] += red[w][e][lane];
-    }
+        for (int e = 0; e < 4; ++e) {
+#pragma unroll
+            for (int w = 0; w < 3; ++w) acc[gi][e] += red[w][4 * gi + e][lane];
+        }
     const bool split = g.splits > 1;
     float* base = split ? g.ws + static_cast<long long>(blockIdx.y) * M * N : g.C;
     const int ld = split ? N : g.ldc;
     const bool vst = colfull && (split ? (N % 4 == 0) : (g.ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(g.C) & 15u) == 0));
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int row = 4 * q + r;
+    for (int gr = 0; gr < 4 * MG; ++gr) {
+        const int gi = gr >> 2, r = gr & 3;
+        const int row = 16 * gi + 4 * q + r;
         if (row >= M) continue;
-        float v[4] = {acc[0][r], acc[1][r], acc[2][r], acc[3][r]};
+        float v[4] = {acc[gi][0][r], acc[gi][1][r], acc[gi][2][r], acc[gi][3][r]};
+        float* dst = base + static_cast<long long>(row) * ld + col;
+        if (!split) {
+            const float* rr = g.R ? g.R + static_cast<long long>(row) * g.ldr + col : dst;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (col + e < N) v[e] = g.alpha * v[e] + (g.beta != 0.f ? g.beta * rr[e] : 0.f);
+        }
+        if (vst) {
+            *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (col + e < N) dst[e] = v[e];
+        }
+    }
+}
+
+// 17..64 rows (MG = 2..4 groups of 16): the same MFMA scheme with A staged in
+// LDS per chunk of KC K rows, since loading A per step (MG scalar loads a lane
+// per 4-row step, each touching 16 rows) outweighs the stream of B.  Eight
+// waves (two per SIMD) take the 4-row steps w, w + 8, ... of a chunk.  A chunk
+// is loaded as float4 along k (thread (m, k4): A[m][kc + 4k4 .. +3]) and written
+// k-major As[k][m] with row stride 80 (16k + m spreads a wave's writes and the
+// operand reads As[(4s + q) * 80 + 16g + p] over all 64 banks).  The next
+// chunk's A and B are loaded into a second register set before the current
+// chunk's MFMAs.  The waves' sums meet in two fixed rounds (waves 4..7 into
+// 0..3, then 1..3 into 0).
+constexpr int kSkinnyKCA = 128;
+constexpr int kSkinnyLdsA = 80;
+constexpr int kSkinnyLdsWaves = 8;
+
+template <bool TA, bool VEC, int MG>
+__global__ void __launch_bounds__(64 * kSkinnyLdsWaves)
+sgemm_skinny_mfma_lds_kernel(const GemmArgs g)
+{
+    constexpr int NW = kSkinnyLdsWaves;
+    constexpr int NT = 64 * NW;
+    constexpr int KC = kSkinnyKCA;
+    constexpr int U = KC / (4 * NW);                    // 4-row steps per wave per chunk
+    constexpr int UA = 16 * MG * (KC / 4) / NT;         // A float4 units per thread per chunk
+    static_assert(UA >= 1 && 16 * MG * (KC / 4) % NT == 0, "A chunk units must split evenly");
+    // one LDS region for the A chunks and, after the last chunk, the waves' sums
+    constexpr int kAs = KC * kSkinnyLdsA;               // floats
+    constexpr int kRed = 4 * 4 * MG * 64 * 4;           // floats: 4 waves' partial tiles
+    __shared__ floatx4 lds[(kAs > kRed ? kAs : kRed) / 4];
+    float* As = reinterpret_cast<float*>(lds);
+    floatx4 (*red)[4 * MG][64] = reinterpret_cast<floatx4 (*)[4 * MG][64]>(lds);
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int p = lane & 15, q = lane >> 4;
+    const int M = g.M, N = g.N;
+    const int col = blockIdx.x * kSkinnyMfmaCols + 4 * p;
+    const int k0 = blockIdx.y * g.kchunk;
+    const int k1 = min(g.K, k0 + g.kchunk);
+    const bool colfull = VEC && col + 3 < N;
+    floatx4 acc[MG][4];
+#pragma unroll
+    for (int gi = 0; gi < MG; ++gi)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[gi][e] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    struct Chunk { float4 b[U]; float a[UA][4]; };
+    auto load = [&](Chunk& c, int kc) {
+        const int kn = min(KC, k1 - kc);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int kl = 4 * (wv + NW * u) + q;
+            c.b[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (kl < kn) {
+                const float* src = g.B + static_cast<long long>(kc + kl) * g.ldb + col;
+                if (colfull) {
+                    const floatx4 v = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(src));
+                    c.b[u] = make_float4(v.x, v.y, v.z, v.w);
+                } else {
+                    c.b[u].x = col + 0 < N ? src[0] : 0.f;
+                    c.b[u].y = col + 1 < N ? src[1] : 0.f;
+                    c.b[u].z = col + 2 < N ? src[2] : 0.f;
+                    c.b[u].w = col + 3 < N ? src[3] : 0.f;
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < UA; ++j) {
+            const int idx = threadIdx.x + NT * j;
+            const int m = idx % (16 * MG), k4 = idx / (16 * MG);
+            if (!TA && g.vecA && m < M && 4 * k4 + 3 < kn) {   // kc is a multiple of 4
+                const float4 v = *reinterpret_cast<const float4*>(g.A + static_cast<long long>(m) * g.lda + kc + 4 * k4);
+                c.a[j][0] = v.x; c.a[j][1] = v.y; c.a[j][2] = v.z; c.a[j][3] = v.w;
+                continue;
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int kl = 4 * k4 + e;
+                c.a[j][e] = (m < M && kl < kn)
+                                ? (TA ? g.A[static_cast<long long>(kc + kl) * g.lda + m]
+                                      : g.A[static_cast<long long>(m) * g.lda + kc + kl])
+                                : 0.f;
+            }
+        }
+    };
+    auto consume = [&](const Chunk& c, int kc) {
+        const int kn = min(KC, k1 - kc);
+        __syncthreads();   // the previous chunk's operand reads are done
+#pragma unroll
+        for (int j = 0; j < UA; ++j) {
+            const int idx = threadIdx.x + NT * j;
+            const int m = idx % (16 * MG), k4 = idx / (16 * MG);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) As[(4 * k4 + e) * kSkinnyLdsA + m] = c.a[j][e];
+        }
+        __syncthreads();
+        return kn;
+    };
+    auto mma = [&](const Chunk& c, int kn) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int st = wv + NW * u;
+            if (4 * st >= kn) break;                     // uniform
+            const float* ar = As + (4 * st + q) * kSkinnyLdsA + p;
+#pragma unroll
+            for (int gi = 0; gi < MG; ++gi) {
+                const float a = ar[16 * gi];
+                acc[gi][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, c.b[u].x, acc[gi][0], 0, 0, 0);
+                acc[gi][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, c.b[u].y, acc[gi][1], 0, 0, 0);
+                acc[gi][2] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, c.b[u].z, acc[gi][2], 0, 0, 0);
+                acc[gi][3] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, c.b[u].w, acc[gi][3], 0, 0, 0);
+            }
+        }
+    };
+    // two register sets: chunk c + 1 is loaded while chunk c runs its MFMAs
+    if (k0 < k1) {
+        Chunk c0, c1;
+        load(c0, k0);
+        for (int kc = k0; kc < k1; kc += 2 * KC) {
+            int kn = consume(c0, kc);
+            if (kc + KC < k1) load(c1, kc + KC);
+            mma(c0, kn);
+            if (kc + KC >= k1) break;
+            kn = consume(c1, kc + KC);
+            if (kc + 2 * KC < k1) load(c0, kc + 2 * KC);
+            mma(c1, kn);
+        }
+    }
+    __syncthreads();   // the last chunk's operand reads are done: the region becomes the hand-off
+    if (wv >= 4) {
+#pragma unroll
+        for (int gi = 0; gi < MG; ++gi)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) red[wv - 4][4 * gi + e][lane] = acc[gi][e];
+    }
+    __syncthreads();
+    if (wv < 4) {
+#pragma unroll
+        for (int gi = 0; gi < MG; ++gi)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[gi][e] += red[wv][4 * gi + e][lane];
+    }
+    __syncthreads();
+    if (wv >= 1 && wv < 4) {
+#pragma unroll
+        for (int gi = 0; gi < MG; ++gi)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) red[wv - 1][4 * gi + e][lane] = acc[gi][e];
+    }
+    __syncthreads();
+    if (wv != 0) return;
+#pragma unroll
+    for (int gi = 0; gi < MG; ++gi)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+#pragma unroll
+            for (int w = 0; w < 3; ++w) acc[gi][e] += red[w][4 * gi + e][lane];
+        }
+    const bool split = g.splits > 1;
+    float* base = split ? g.ws + static_cast<long long>(blockIdx.y) * M * N : g.C;
+    const int ld = split ? N : g.ldc;
+    const bool vst = colfull && (split ? (N % 4 == 0) : (g.ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(g.C) & 15u) == 0));
+#pragma unroll
+    for (int gr = 0; gr < 4 * MG; ++gr) {
+        const int gi = gr >> 2, r = gr & 3;
+        const int row = 16 * gi + 4 * q + r;
+        if (row >= M) continue;
+        float v[4] = {acc[gi][0][r], acc[gi][1][r], acc[gi][2][r], acc[gi][3][r]};
         float* dst = base + static_cast<long long>(row) * ld + col;
         if (!split) {
             const float* rr = g.R ? g.R + static_cast<long long>(row) * g.ldr + col : dst;
@@ -1344,7 +1544,7 @@ int launch_small(int ta, int tb, GemmArgs g, int batch, hipStream_t stream)
     return launch_reduce(g, batch, stream);
 }
 
-// Skinny path: M <= 16, B not transposed, one product (no batch, no
+// Skinny path: M <= 64, B not transposed, one product (no batch, no
 // batch-reduce), at least one full wave of columns.
 bool skinny_ok(int ta, int tb, int m, int n, int batch, int kblocks)
 {
@@ -1352,7 +1552,7 @@ bool skinny_ok(int ta, int tb, int m, int n, int batch, int kblocks)
     return !tb && m >= 1 && m <= kSkinnyMax && n >= kSkinnyCols && batch == 1 && kblocks == 1;
 }
 
-// Rows of C up to which the VALU form is used; 3..16 rows take the MFMA form.
+// Rows of C up to which the VALU form is used; 3..64 rows take the MFMA form.
 constexpr int kSkinnyValuMax = 2;
 
 // K slices of the skinny path: about two workgroups per CU, at least 64 K rows
@@ -1362,7 +1562,9 @@ int skinny_plan(int m, int n, int k, size_t ws_floats, int* kchunk_out)
 {
     const int cus = st().cu_count > 0 ? st().cu_count : 256;
     const long long cb = ceil_div(n, m <= kSkinnyValuMax ? kSkinnyCols : kSkinnyMfmaCols);
-    long long s = (2LL * cus + cb - 1) / cb;
+    // about two workgroups per CU; one for the eight-wave 17..64-row kernel
+    const long long per_cu = m > 16 ? 1 : 2;
+    long long s = (per_cu * cus + cb - 1) / cb;
     s = std::min<long long>(s, k / 64);
     s = std::min<long long>(s, std::max<long long>(1, k / (8LL * m)));
     const long long mn = static_cast<long long>(m) * n;
@@ -1395,13 +1597,29 @@ int launch_skinny(int ta, GemmArgs g, hipStream_t stream)
         else { if (vec) launch_skinny_t<false, true>(g, grid, stream); else launch_skinny_t<false, false>(g, grid, stream); }
     } else {
         const dim3 grid(ceil_div(g.N, kSkinnyMfmaCols), g.splits);
-        if (ta) {
-            if (vec) sgemm_skinny_mfma_kernel<true, true><<<grid, 256, 0, stream>>>(g);
-            else sgemm_skinny_mfma_kernel<true, false><<<grid, 256, 0, stream>>>(g);
-        } else {
-            if (vec) sgemm_skinny_mfma_kernel<false, true><<<grid, 256, 0, stream>>>(g);
-            else sgemm_skinny_mfma_kernel<false, false><<<grid, 256, 0, stream>>>(g);
-        }
+        auto go = [&](auto mgc) {
+            constexpr int MG = decltype(mgc)::value;
+            constexpr int T = 64 * kSkinnyLdsWaves;
+            if (ta) {
+                if (vec) sgemm_skinny_mfma_lds_kernel<true, true, MG><<<grid, T, 0, stream>>>(g);
+                else sgemm_skinny_mfma_lds_kernel<true, false, MG><<<grid, T, 0, stream>>>(g);
+            } else {
+                if (vec) sgemm_skinny_mfma_lds_kernel<false, true, MG><<<grid, T, 0, stream>>>(g);
+                else sgemm_skinny_mfma_lds_kernel<false, false, MG><<<grid, T, 0, stream>>>(g);
+            }
+        };
+        const int mg = ceil_div(g.M, 16);
+        if (mg == 1) {
+            if (ta) {
+                if (vec) sgemm_skinny_mfma_kernel<true, true, 1><<<grid, 256, 0, stream>>>(g);
+                else sgemm_skinny_mfma_kernel<true, false, 1><<<grid, 256, 0, stream>>>(g);
+            } else {
+                if (vec) sgemm_skinny_mfma_kernel<false, true, 1><<<grid, 256, 0, stream>>>(g);
+                else sgemm_skinny_mfma_kernel<false, false, 1><<<grid, 256, 0, stream>>>(g);
+            }
+        } else if (mg == 2) go(std::integral_constant<int, 2>{});
+        else if (mg == 3) go(std::integral_constant<int, 3>{});
+        else go(std::integral_constant<int, 4>{});
     }
     int rc = check_launch("sgemm (skinny): kernel launch");
     if (rc != LHIP_OK || g.splits <= 1) return rc;

@@ -364,12 +364,14 @@ def test_gemm_256_tile_path(m, n, k, batch, ld_pad):
 
 
 # ------------------------------------------------------------ skinny products
-# M <= 16 with B stored K x N take the streaming kernel (one pass over B,
-# K split into slices summed in order); edge columns, unaligned leading
-# dimensions, transposed A, alpha/beta and K shorter than a slice are covered.
+# M <= 64 with B stored K x N take the streaming kernel (one pass over B,
+# K split into slices summed in order; 3..64 rows on the matrix cores in one to
+# four 16-row groups); edge columns, unaligned leading dimensions, transposed
+# A, alpha/beta and K shorter than a slice are covered.
 @pytest.mark.parametrize("m,k,n", [(1, 4096, 4096), (16, 4096, 4096), (1, 7, 256), (2, 64, 300),
                                    (3, 1000, 513), (5, 333, 1024), (8, 4097, 257), (13, 129, 777),
-                                   (16, 64, 256), (11, 2, 4096)])
+                                   (16, 64, 256), (11, 2, 4096), (17, 300, 257), (33, 512, 300),
+                                   (48, 1000, 1024), (64, 4096, 4096), (61, 77, 4097), (64, 3, 256)])
 def test_gemm_skinny_vs_oracle(m, k, n):
     announce("gemm skinny", m, k, n)
     rng = np.random.default_rng(7000 + m * 11 + k + n)
