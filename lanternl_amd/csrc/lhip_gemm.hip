@@ -32,6 +32,7 @@
 #include <type_traits>
 
 #include "lhip_internal.h"
+#include "lhip_reduce.h"
 
 namespace lhip {
 namespace {
@@ -1680,6 +1681,9 @@ struct GroupedTNArgs {
     int tile0[kGroupedMax + 1];
     int tiles_n[kGroupedMax];
     int ngroups, K;
+    ColsumSet cs;     // column sums run by the workgroups after the last tile
+    int cs_cb;        // 32-column blocks per column-sum job
+    int cs_blocks;    // cs.njobs * cs_cb
 };
 
 template <int NW>
@@ -1752,7 +1756,8 @@ __global__ void __launch_bounds__(64 * NW) sgemm_grouped_tn_kernel(const Grouped
 // chunk), double-buffered; wave w then runs the 8 MFMA steps of chunk rows
 // 16w .. 16w+15 on the whole 32x32 tile, reading each operand fragment as one
 // conflict-free ds_read_b32 (lanes 0-31 row k, 32-63 row k+1).  The waves'
-// tiles are summed in LDS in wave order.
+// tiles are summed in LDS in wave order.  Workgroups past the last tile run the
+// column-sum jobs of ga.cs, one 32-column block each (colsum4_block).
 constexpr int kGroupedBK = 64;
 
 __global__ void __launch_bounds__(256) sgemm_grouped_tn_lds_kernel(const GroupedTNArgs ga)
@@ -1763,7 +1768,14 @@ __global__ void __launch_bounds__(256) sgemm_grouped_tn_lds_kernel(const Grouped
     __shared__ float red[4][16][64];
     const int per_xcd = gridDim.x / 8;
     const int id = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
-    if (id >= ga.tile0[ga.ngroups]) return;   // padding
+    if (id >= ga.tile0[ga.ngroups]) {
+        const int cid = id - ga.tile0[ga.ngroups];
+        if (cid >= ga.cs_blocks) return;   // padding
+        const int job = cid / ga.cs_cb, cb = cid - job * ga.cs_cb;
+        colsum4_block(ga.cs.partial[job], ga.cs.nparts[job], ga.cs.out[job], ga.cs.cols, 32 * cb, ga.cs.acc,
+                      reinterpret_cast<float4 (*)[8]>(&red[0][0][0]));
+        return;
+    }
     int gi = 0;
     for (int i = 1; i < ga.ngroups; ++i)
         if (id >= ga.tile0[i]) gi = i;
@@ -1830,9 +1842,13 @@ __global__ void __launch_bounds__(256) sgemm_grouped_tn_lds_kernel(const Grouped
 
 }  // namespace
 
-int sgemm_grouped_tn(const GroupedTN* g, int ngroups, int K, hipStream_t stream)
+int sgemm_grouped_tn(const GroupedTN* g, int ngroups, int K, hipStream_t stream, const ColsumSet* cs)
 {
-    if (ngroups <= 0) return LHIP_OK;
+    if (ngroups <= 0) {
+        if (cs && cs->njobs > 0)
+            return rmsnorm_bwd_colsum_multi(cs->partial, cs->nparts, cs->out, cs->njobs, cs->cols, cs->acc, stream);
+        return LHIP_OK;
+    }
     if (ngroups > kGroupedMax) return fail(LHIP_E_ARG, "sgemm_grouped_tn: %d groups (at most %d)", ngroups, kGroupedMax);
     if (K <= 0) return fail(LHIP_E_SHAPE, "sgemm_grouped_tn: K=%d", K);
     GroupedTNArgs ga{};
@@ -1852,17 +1868,33 @@ int sgemm_grouped_tn(const GroupedTN* g, int ngroups, int K, hipStream_t stream)
     ga.tile0[ngroups] = static_cast<int>(tiles);
     ga.ngroups = ngroups;
     ga.K = K;
-    const unsigned grid = static_cast<unsigned>((tiles + 7) / 8 * 8);   // whole XCD rounds
     bool vec = true;
     for (int i = 0; i < ngroups; ++i) {
         const GroupedTN& e = g[i];
         vec = vec && e.lda % 4 == 0 && e.ldb % 4 == 0 && e.M % 4 == 0 && e.N % 4 == 0 && aligned16(e.A) &&
               aligned16(e.B);
     }
+    // column sums in the same launch when they take the float4 form too
+    bool cs_fused = false;
+    if (vec && cs && cs->njobs > 0) {
+        if (cs->njobs > kColsumJobs) return fail(LHIP_E_ARG, "sgemm_grouped_tn: %d column-sum jobs", cs->njobs);
+        cs_fused = cs->cols > 0 && cs->cols % 4 == 0;
+        for (int i = 0; i < cs->njobs && cs_fused; ++i)
+            cs_fused = cs->nparts[i] > 0 && cs->partial[i] && cs->out[i] && aligned16(cs->partial[i]) &&
+                       aligned16(cs->out[i]);
+        if (cs_fused) {
+            ga.cs = *cs;
+            ga.cs_cb = ceil_div(cs->cols, 32);
+            ga.cs_blocks = cs->njobs * ga.cs_cb;
+        }
+    }
+    const unsigned grid = static_cast<unsigned>((tiles + ga.cs_blocks + 7) / 8 * 8);   // whole XCD rounds
     if (vec) sgemm_grouped_tn_lds_kernel<<<grid, 256, 0, stream>>>(ga);
     else if (K >= 256) sgemm_grouped_tn_kernel<8><<<grid, 512, 0, stream>>>(ga);
     else sgemm_grouped_tn_kernel<4><<<grid, 256, 0, stream>>>(ga);
-    return check_launch("sgemm_grouped_tn");
+    int rc = check_launch("sgemm_grouped_tn");
+    if (rc != LHIP_OK || cs_fused || !cs || cs->njobs <= 0) return rc;
+    return rmsnorm_bwd_colsum_multi(cs->partial, cs->nparts, cs->out, cs->njobs, cs->cols, cs->acc, stream);
 }
 
 // Below the 64x64-tile threshold, the 32x32 small kernel is used unless K is

@@ -224,7 +224,17 @@ struct GroupedTN {
     float* C; int ldc;
     int M, N;
 };
-int sgemm_grouped_tn(const GroupedTN* g, int ngroups, int K, hipStream_t stream);
+// Column-sum jobs (the RMSNorm gains' dw from per-tile partials) that a
+// grouped launch can run in extra workgroups: out_j[c] (+)= sum_b partial_j[b][c].
+struct ColsumSet {
+    const float* partial[kColsumJobs];
+    int nparts[kColsumJobs];
+    float* out[kColsumJobs];
+    int njobs, cols, acc;
+};
+// cs (optional): column sums issued with the products -- in the same launch
+// when both take their float4 forms, otherwise as a second launch.
+int sgemm_grouped_tn(const GroupedTN* g, int ngroups, int K, hipStream_t stream, const ColsumSet* cs = nullptr);
 int sgemm_run(int transa, int transb, int m, int n, int k, float alpha,
               const float* A, int lda, long long sA, const float* B, int ldb, long long sB, float beta,
               float* C, int ldc, long long sC, int batch, const GemmOpts& o, hipStream_t stream);

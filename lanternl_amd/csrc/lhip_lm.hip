@@ -424,8 +424,13 @@ int enqueue_step(LmModel& m, hipStream_t s, const Hyper& hp, bool device_hyper)
         ncs = 0;
     }
     cs_p[ncs] = pend.part; cs_n[ncs] = pend.parts; cs_o[ncs] = pend.gw; ++ncs;
-    LM_TRY(sgemm_grouped_tn(dw_all, ndw, N, s));
-    LM_TRY(rmsnorm_bwd_colsum_multi(cs_p, cs_n, cs_o, ncs, D, 0, s));
+    {
+        // the last products and the gains' column sums in one launch
+        ColsumSet cs{};
+        for (int i = 0; i < ncs; ++i) { cs.partial[i] = cs_p[i]; cs.nparts[i] = cs_n[i]; cs.out[i] = cs_o[i]; }
+        cs.njobs = ncs; cs.cols = D; cs.acc = 0;
+        LM_TRY(sgemm_grouped_tn(dw_all, ndw, N, s, &cs));
+    }
     LM_TRY(embed_bwd(gxl(0), m.ids, m.grd(0), N, D, V, 1.f, 1, s));    // after gemb (same launch order)
 
     // ---------------- optimizer (lmtrain.lua:1212-1226) ----------------

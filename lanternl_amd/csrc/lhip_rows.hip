@@ -303,48 +303,8 @@ __global__ void __launch_bounds__(256)
 colsum4_kernel(const ColsumJobs jobs, int cols, int acc)
 {
     __shared__ float4 red[32][8];
-    const float* __restrict__ partial = jobs.partial[blockIdx.y];
-    float* __restrict__ out = jobs.out[blockIdx.y];
-    const int nparts = jobs.nparts[blockIdx.y];
-    const int q = threadIdx.x & 7, g = threadIdx.x >> 3;
-    const int c = blockIdx.x * 32 + 4 * q;
-    float4 s = f4zero();
-    if (c < cols) {
-        int b = g;
-        for (; b + 7 * 32 < nparts; b += 8 * 32) {
-            float4 t[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u)
-                t[u] = *reinterpret_cast<const float4*>(partial + static_cast<size_t>(b + u * 32) * cols + c);
-#pragma unroll
-            for (int u = 0; u < 8; ++u) { s.x += t[u].x; s.y += t[u].y; s.z += t[u].z; s.w += t[u].w; }
-        }
-        for (; b < nparts; b += 32) {
-            const float4 t = *reinterpret_cast<const float4*>(partial + static_cast<size_t>(b) * cols + c);
-            s.x += t.x; s.y += t.y; s.z += t.z; s.w += t.w;
-        }
-    }
-    red[g][q] = s;
-    __syncthreads();
-#pragma unroll
-    for (int half = 16; half > 0; half >>= 1) {
-        if (g < half) {
-            const float4 t = red[g + half][q];
-            float4 u = red[g][q];
-            u.x += t.x; u.y += t.y; u.z += t.z; u.w += t.w;
-            red[g][q] = u;
-        }
-        __syncthreads();
-    }
-    if (g == 0 && c < cols) {
-        float4 t = red[0][q];
-        float4* o = reinterpret_cast<float4*>(out + c);
-        if (acc) {
-            const float4 v = *o;
-            t.x += v.x; t.y += v.y; t.z += v.z; t.w += v.w;
-        }
-        *o = t;
-    }
+    colsum4_block(jobs.partial[blockIdx.y], jobs.nparts[blockIdx.y], jobs.out[blockIdx.y], cols, blockIdx.x * 32, acc,
+                  red);
 }
 
 __global__ void __launch_bounds__(256)
