@@ -82,6 +82,23 @@ LHIP_API const char* lhip_version(void);
  * (cuda/luaTL_core.cu:1841-1853, 2149-2151) with plain owned buffers. */
 LHIP_API int lhip_malloc(void** dptr, size_t bytes);
 LHIP_API int lhip_free(void* dptr);
+/* Device memory free / total in bytes (luaTL_mem_info, cuda/luaTL_core.cu:1765-1772). */
+LHIP_API int lhip_mem_info(unsigned long long* free_bytes, unsigned long long* total_bytes);
+/* Accounting of the library's device memory, the counterpart of the pool
+ * statistics the reference adapter's stats() reports (luaTL_pool_get_stats,
+ * cuda/luaTL_core.cu:1862-1869; fields luaTL_core.cu:218-234): there is no
+ * caching pool here, so every lhip_malloc is a hipMalloc and every lhip_free
+ * a hipFree of a buffer the caller owns. */
+typedef struct {
+    unsigned long long bytes_in_use;     /* live lhip_malloc buffers          */
+    unsigned long long peak_in_use;      /* high-water mark of bytes_in_use   */
+    unsigned long long live_buffers;
+    unsigned long long n_alloc;          /* lhip_malloc calls that succeeded  */
+    unsigned long long n_free;           /* lhip_free calls of live buffers   */
+    unsigned long long workspace_bytes;  /* library scratch (split-K, reductions) */
+    unsigned long long staging_bytes;    /* host-table path device staging    */
+} lhip_mem_stats_t;
+LHIP_API int lhip_mem_stats(lhip_mem_stats_t* out);
 /* Synchronous host<->device copies (replace luaTL_tensor_upload/download and
  * luaTL_to_gpu/to_cpu, cuda/luaTL_core.cu:2031-2094, 2153-2155). */
 LHIP_API int lhip_upload(void* dst_device, const void* src_host, size_t bytes);
@@ -237,6 +254,11 @@ LHIP_API int lhip_embed_bwd(const float* dout, const int* ids, float* dtable, in
 LHIP_API int lhip_fill(float* x, long long n, float value);
 /* out = a + b elementwise (the residual adds of ai/nn/transformer.lua:243-249). */
 LHIP_API int lhip_add(const float* a, const float* b, float* out, long long n);
+/* out = silu(x) = x * sigmoid(x) elementwise over n floats (in place allowed),
+ * sigmoid by sign as Tensor.silu (ai/core/tensor2.lua:272-291); the adapter's
+ * silu_inplace (ai/gpu/luatl_adapter.lua:168, Tensor:silu_inplace
+ * ai/gpu/luaTL.lua:669). */
+LHIP_API int lhip_silu(const float* x, float* out, long long n);
 /* *out (device double) = sum of x^2, deterministic two-stage reduction
  * (optim2.grad_norm squared, ai/optim/optim2.lua:27-38; replaces luaTL_l2_accum,
  * cuda/luaTL_train.cu:1215-1221). */

@@ -32,6 +32,12 @@ class DevInfo(ctypes.Structure):
     ]
 
 
+class MemStats(ctypes.Structure):
+    """lhip_mem_stats_t"""
+    _fields_ = [(n, ctypes.c_ulonglong) for n in ("bytes_in_use", "peak_in_use", "live_buffers", "n_alloc",
+                                                  "n_free", "workspace_bytes", "staging_bytes")]
+
+
 _i, _f, _d, _ll, _sz = ctypes.c_int, ctypes.c_float, ctypes.c_double, ctypes.c_longlong, ctypes.c_size_t
 _p = ctypes.c_void_p
 _pp = ctypes.POINTER(ctypes.c_void_p)
@@ -47,6 +53,8 @@ SIGNATURES = {
     "lhip_version": (ctypes.c_char_p, []),
     "lhip_malloc": (_i, [_pp, _sz]),
     "lhip_free": (_i, [_p]),
+    "lhip_mem_info": (_i, [ctypes.POINTER(ctypes.c_ulonglong), ctypes.POINTER(ctypes.c_ulonglong)]),
+    "lhip_mem_stats": (_i, [ctypes.POINTER(MemStats)]),
     "lhip_upload": (_i, [_p, _p, _sz]),
     "lhip_download": (_i, [_p, _p, _sz]),
     "lhip_copy": (_i, [_p, _p, _sz]),
@@ -80,6 +88,7 @@ SIGNATURES = {
     "lhip_embed_bwd": (_i, [_p, _p, _p, _i, _i, _i, _f, _i]),
     "lhip_fill": (_i, [_p, _ll, _f]),
     "lhip_add": (_i, [_p, _p, _p, _ll]),
+    "lhip_silu": (_i, [_p, _p, _ll]),
     "lhip_sumsq": (_i, [_p, _ll, _p]),
     "lhip_sum": (_i, [_p, _i, _f, _p]),
     "lhip_sgd_step": (_i, [_p, _p, _p, _ll, _p, _f, _f, _f, _f, _f, _i, _p, _p]),

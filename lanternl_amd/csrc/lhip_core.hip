@@ -171,6 +171,11 @@ LHIP_API int lhip_malloc(void** dptr, size_t bytes)
         (void)hipGetLastError();
         return fail(LHIP_E_OOM, "lhip_malloc: %zu bytes: %s", bytes, hipGetErrorString(e));
     }
+    auto& s = st();
+    s.live[*dptr] = bytes;
+    s.bytes_in_use += bytes;
+    if (s.bytes_in_use > s.peak_in_use) s.peak_in_use = s.bytes_in_use;
+    ++s.n_alloc;
     return LHIP_OK;
 }
 
@@ -182,6 +187,38 @@ LHIP_API int lhip_free(void* dptr)
     // Work already enqueued may still read the buffer.
     LHIP_CHECK_HIP(hipStreamSynchronize(st().stream), "lhip_free: stream sync");
     LHIP_CHECK_HIP(hipFree(dptr), "lhip_free: hipFree");
+    auto& s = st();
+    const auto it = s.live.find(dptr);
+    if (it != s.live.end()) {
+        s.bytes_in_use -= it->second;
+        ++s.n_free;
+        s.live.erase(it);
+    }
+    return LHIP_OK;
+}
+
+LHIP_API int lhip_mem_info(unsigned long long* free_bytes, unsigned long long* total_bytes)
+{
+    LHIP_REQUIRE_READY();
+    size_t f = 0, t = 0;
+    LHIP_CHECK_HIP(hipMemGetInfo(&f, &t), "lhip_mem_info: hipMemGetInfo");
+    if (free_bytes) *free_bytes = f;
+    if (total_bytes) *total_bytes = t;
+    return LHIP_OK;
+}
+
+LHIP_API int lhip_mem_stats(lhip_mem_stats_t* out)
+{
+    if (!out) return fail(LHIP_E_NULL, "lhip_mem_stats: out is NULL");
+    const auto& s = st();
+    std::memset(out, 0, sizeof(*out));
+    out->bytes_in_use = s.bytes_in_use;
+    out->peak_in_use = s.peak_in_use;
+    out->live_buffers = s.live.size();
+    out->n_alloc = s.n_alloc;
+    out->n_free = s.n_free;
+    out->workspace_bytes = s.work_bytes;
+    out->staging_bytes = s.d_stage_floats * sizeof(float);
     return LHIP_OK;
 }
 

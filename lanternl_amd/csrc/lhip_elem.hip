@@ -63,6 +63,34 @@ __global__ void fill_bytes_kernel(unsigned char* __restrict__ p, long long n)
         p[i] = 0;
 }
 
+// sigmoid evaluated by sign (tensor2.lua:272-291): 1/(1+e^-v) for v >= 0,
+// e^v/(1+e^v) below, so neither branch overflows
+__device__ __forceinline__ float silu_sign(float v)
+{
+    if (v >= 0.f) return v / (1.0f + expf(-v));
+    const float z = expf(v);
+    return v * z / (1.0f + z);
+}
+
+// out = silu(x) elementwise (in place allowed: each element is read, then written)
+__global__ void silu_kernel(const float* x, float* o, long long n, int vec)
+{
+    const long long stride = static_cast<long long>(gridDim.x) * blockDim.x;
+    const long long t0 = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
+    if (vec) {
+        const long long n4 = n >> 2;
+        const float4* x4 = reinterpret_cast<const float4*>(x);
+        float4* o4 = reinterpret_cast<float4*>(o);
+        for (long long i = t0; i < n4; i += stride) {
+            const float4 v = x4[i];
+            o4[i] = make_float4(silu_sign(v.x), silu_sign(v.y), silu_sign(v.z), silu_sign(v.w));
+        }
+        for (long long i = 4 * n4 + t0; i < n; i += stride) o[i] = silu_sign(x[i]);
+    } else {
+        for (long long i = t0; i < n; i += stride) o[i] = silu_sign(x[i]);
+    }
+}
+
 __global__ void add_kernel(const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ o,
                            long long n, int vec)
 {
@@ -442,6 +470,16 @@ int add(const float* a, const float* b, float* o, long long n, hipStream_t s)
     return check_launch("add");
 }
 
+int silu(const float* x, float* o, long long n, hipStream_t s)
+{
+    if (n < 0) return fail(LHIP_E_SHAPE, "silu: n < 0");
+    if (n == 0) return LHIP_OK;
+    if (!x || !o) return fail(LHIP_E_NULL, "silu: NULL pointer");
+    const int vec = aligned16(x) && aligned16(o);
+    silu_kernel<<<grid_for(vec ? (n + 3) / 4 : n, 256), 256, 0, s>>>(x, o, n, vec);
+    return check_launch("silu");
+}
+
 int swiglu_fwd(const float* g, int ldg, const float* u, int ldu, float* h, int ldh, int rows, int cols,
                hipStream_t s)
 {
@@ -544,6 +582,12 @@ LHIP_API int lhip_add(const float* a, const float* b, float* out, long long n)
 {
     LHIP_REQUIRE_READY();
     return lhip::add(a, b, out, n, st().stream);
+}
+
+LHIP_API int lhip_silu(const float* x, float* out, long long n)
+{
+    LHIP_REQUIRE_READY();
+    return lhip::silu(x, out, n, st().stream);
 }
 
 LHIP_API int lhip_swiglu_fwd(const float* gate, int ld_gate, const float* up, int ld_up, float* out, int ld_out,

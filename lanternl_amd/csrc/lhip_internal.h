@@ -6,6 +6,7 @@
 // message retrievable through lhip_last_error(), and returns a status code.
 #pragma once
 
+#include <unordered_map>
 #include <hip/hip_runtime.h>
 
 #include <cstddef>
@@ -36,6 +37,9 @@ struct State {
     size_t work_bytes = 0;
     // a program (stream capture of the library stream) is being recorded
     bool recording = false;
+    // accounting of lhip_malloc buffers (lhip_mem_stats)
+    std::unordered_map<void*, size_t> live;
+    unsigned long long bytes_in_use = 0, peak_in_use = 0, n_alloc = 0, n_free = 0;
 };
 
 State& st();
@@ -95,6 +99,7 @@ int workspace(size_t bytes, void** out);
 int fill(float* p, long long n, float v, hipStream_t s);
 int zero_bytes(void* p, size_t bytes, hipStream_t s);
 int add(const float* a, const float* b, float* o, long long n, hipStream_t s);
+int silu(const float* x, float* o, long long n, hipStream_t s);
 int rmsnorm_fwd(const float* x, const float* w, float* y, float* inv, int rows, int cols, float eps,
                 hipStream_t s);
 int rmsnorm_bwd_parts(int rows, int cols);

@@ -58,6 +58,27 @@ int lhip_program_begin(void);
 int lhip_program_end(void** program);
 int lhip_program_replay(void* program, int times);
 int lhip_program_free(void* program);
+int lhip_silu(const float* x, float* out, long long n);
+int lhip_mem_info(unsigned long long* free_bytes, unsigned long long* total_bytes);
+typedef struct {
+    unsigned long long bytes_in_use, peak_in_use, live_buffers, n_alloc, n_free,
+                       workspace_bytes, staging_bytes;
+} lhip_mem_stats_t;
+int lhip_mem_stats(lhip_mem_stats_t* out);
+typedef struct {
+    char name[256];
+    char arch[64];
+    int device;
+    int compute_units;
+    int clock_khz;
+    int wavefront_size;
+    long long total_mem;
+    long long lds_per_block;
+    int l2_bytes;
+    double peak_fp32_matrix_tflops;
+    double peak_hbm_gbps;
+} lhip_devinfo_t;
+int lhip_device_info(lhip_devinfo_t* out);
 ]]
 
 local STATUS = { [0] = "OK", [-1] = "NULL", [-2] = "SHAPE", [-3] = "DTYPE", [-4] = "DEVICE",
@@ -206,7 +227,10 @@ function Handle:toflat()
 end
 
 function Handle:zero() ck(C.lhip_zero(self.ptr, self.rows * self.cols * 4), "zero") return self end
-function Handle:free() if self.ptr then C.lhip_free(ffi.gc(self.ptr, nil)); self.ptr = nil end end
+function Handle:free()
+    if self.ptr and self.owned ~= false then C.lhip_free(ffi.gc(self.ptr, nil)) end
+    self.ptr = nil
+end
 function Handle:shape() return self.rows, self.cols end
 
 local function fp(h) return ffi.cast("float*", h.ptr) end
@@ -303,7 +327,101 @@ function M.add_inplace(A, B)
     return A
 end
 
+function M.silu_inplace(h)
+    ck(C.lhip_silu(fp(h), fp(h), h.rows * h.cols), "silu_inplace")
+    return h
+end
+
 function M.sync() ck(C.lhip_sync(), "sync") end
+
+--  Memory and device queries (luatl_adapter.lua:184-185,243-246).  There is
+--  no caching pool: stats() reports the library's own accounting of the
+--  buffers it allocated (lhip_mem_stats), under the reference's key names
+--  where they mean the same thing.
+local mstats = ffi.new("lhip_mem_stats_t")
+function M.stats()
+    ck(C.lhip_mem_stats(mstats), "stats")
+    local s = mstats
+    return {
+        in_use = tonumber(s.bytes_in_use), peak = tonumber(s.peak_in_use),
+        blocks = tonumber(s.live_buffers), allocs = tonumber(s.n_alloc), frees = tonumber(s.n_free),
+        workspace = tonumber(s.workspace_bytes), staging = tonumber(s.staging_bytes),
+        reserved = tonumber(s.bytes_in_use + s.workspace_bytes + s.staging_bytes),
+    }
+end
+
+local devinfo = ffi.new("lhip_devinfo_t")
+function M.hardware()
+    ck(C.lhip_device_info(devinfo), "hardware")
+    local d = devinfo
+    return {
+        name = ffi.string(d.name), arch = ffi.string(d.arch), device = d.device,
+        sm_count = d.compute_units, compute_units = d.compute_units, clock_mhz = d.clock_khz / 1000,
+        warp_size = d.wavefront_size, total_mem = tonumber(d.total_mem),
+        smem_per_block = tonumber(d.lds_per_block), l2_bytes = d.l2_bytes,
+        gflops_fp32_matrix = d.peak_fp32_matrix_tflops * 1000, hbm_gbps = d.peak_hbm_gbps,
+    }
+end
+
+local u64a, u64b = ffi.new("unsigned long long[1]"), ffi.new("unsigned long long[1]")
+function M.mem()
+    ck(C.lhip_mem_info(u64a, u64b), "mem")
+    return tonumber(u64a[0]), tonumber(u64b[0])
+end
+
+--  Resident-tensor toolkit (luatl_adapter.lua:188-241): allocation-free views
+--  over device memory.  A view is { ptr, rows, cols, rs, cs, bs } in
+--  elements; wrap() makes a non-owning Handle over a raw device pointer.
+local function base_ptr(t)
+    if is_handle(t) or (type(t) == "table" and t.ptr ~= nil) then return t.ptr end
+    return t
+end
+
+--- Element-offset pointer into a handle's (or view's) float32 storage.
+function M.offset(t, elems)
+    return ffi.cast("char*", base_ptr(t)) + elems * 4
+end
+
+--- Explicit stride view: rs = row stride, cs = column stride, bs = batch stride (elements).
+function M.view(ptr, rows, cols, rs, cs, bs)
+    return { ptr = ptr, rows = rows, cols = cols, rs = rs, cs = cs, bs = bs or 0 }
+end
+
+--- Column slice [col0, col0 + w) of a handle, keeping the parent's leading dimension.
+function M.cols(t, col0, w)
+    return M.view(M.offset(t, col0), t.rows, w, t.cols, 1, 0)
+end
+
+--- Non-owning handle over a raw device pointer (free() leaves the memory alone).
+function M.wrap(ptr, rows, cols)
+    return setmetatable({ rows = rows, cols = cols, ptr = ffi.cast("void*", ptr), owned = false }, Handle)
+end
+
+--- int32 index buffer (4 bytes per entry, as float32).
+function M.ids(n)
+    local h = M.alloc(n, 1)
+    h.is_ids = true
+    return h
+end
+
+function M.upload_i32(t, cbuf, n)
+    ck(C.lhip_upload(base_ptr(t), cbuf, n * 4), "upload_i32")
+end
+
+function M.download_i32(t, cbuf, n)
+    ck(C.lhip_download(cbuf, base_ptr(t), n * 4), "download_i32")
+end
+
+function M.download_f32(ptr, cbuf, n)
+    ck(C.lhip_download(cbuf, base_ptr(ptr), n * 4), "download_f32")
+end
+
+--- One float read back from device memory (the loss, the gradient norm).
+local one = ffi.new("float[1]")
+function M.scalar(t)
+    ck(C.lhip_download(one, base_ptr(t), 4), "scalar")
+    return one[0]
+end
 
 -- Program (luaTL.Program capture/replay, ai/gpu/luaTL_train.lua:327-627):
 -- fn() issues adapter calls, which are recorded rather than run; the result

@@ -445,3 +445,60 @@ def test_sum_and_fill_and_add():
     call("lhip_zero", Z.ptr + 4, 7)
     z = Z.download().view(np.uint8)
     assert (z[4:11] == 0).all() and z[11] != 0
+
+
+# ------------------------------------------------------------ silu, memory queries
+@pytest.mark.parametrize("n", [1, 7, 4096, 1_000_003])
+def test_silu_vs_closed_form_in_place_and_out(n):
+    """lhip_silu (the adapter's silu_inplace): x * sigmoid(x) with the sigmoid by
+    sign (tensor2.lua:272-291), against the float64 closed form, including large
+    |x|; in place and out of place, on an unaligned view."""
+    announce("silu", n)
+    rng = np.random.default_rng(n)
+    x = f32(rng.normal(0, 4, n))
+    # large |x| (exp(80) overflows the naive sigmoid's intermediate in fp32 only
+    # at ~89, but the sign form never forms it); silu(-80) ~ -1.4e-33 stays a
+    # normal fp32 number, so the relative bar applies
+    x[: min(n, 3)] = np.array([-80.0, 80.0, 0.0], np.float32)[: min(n, 3)]
+    xd = x.astype(np.float64)
+    ref = xd / (1.0 + np.exp(-np.clip(xd, -700, 700)))
+    X, Y = to_dev(x), device.Buffer((n,))
+    call("lhip_silu", X.ptr, Y.ptr, n)
+    assert rel_fro(dl(Y), ref) <= EW
+    call("lhip_silu", X.ptr, X.ptr, n)                       # in place
+    assert rel_fro(dl(X), ref) <= EW
+    if n > 1:                                                # unaligned view: scalar path
+        Z = to_dev(x)
+        call("lhip_silu", Z.offset(1), Z.offset(1), n - 1)
+        got = dl(Z)
+        assert got[0] == x[0]
+        assert rel_fro(got[1:], ref[1:]) <= EW
+
+
+def test_mem_info_and_allocation_accounting():
+    """lhip_mem_info (luaTL_mem_info) and lhip_mem_stats (the adapter's stats())."""
+    import ctypes
+    from lanternl_amd._lib import MemStats, lib
+    announce("mem info / stats")
+    L = lib()
+    free_b, total_b = ctypes.c_ulonglong(), ctypes.c_ulonglong()
+    call("lhip_mem_info", ctypes.byref(free_b), ctypes.byref(total_b))
+    assert 0 < free_b.value <= total_b.value
+    assert abs(total_b.value - device.info()["total_mem"]) <= 0.01 * device.info()["total_mem"]
+    before = MemStats()
+    call("lhip_mem_stats", ctypes.byref(before))
+    p = ctypes.c_void_p()
+    call("lhip_malloc", ctypes.byref(p), 3 << 20)
+    mid = MemStats()
+    call("lhip_mem_stats", ctypes.byref(mid))
+    assert mid.bytes_in_use == before.bytes_in_use + (3 << 20)
+    assert mid.live_buffers == before.live_buffers + 1
+    assert mid.n_alloc == before.n_alloc + 1
+    assert mid.peak_in_use >= mid.bytes_in_use
+    assert L.lhip_free(p) == 0
+    after = MemStats()
+    call("lhip_mem_stats", ctypes.byref(after))
+    assert after.bytes_in_use == before.bytes_in_use
+    assert after.live_buffers == before.live_buffers
+    assert after.n_free == before.n_free + 1
+    assert after.peak_in_use >= mid.bytes_in_use
