@@ -901,125 +901,19 @@ sgemm_skinny_kernel(const GemmArgs g)
 // Skinny products with 3..64 rows of C on the matrix cores.  The VALU form
 // above would spend up to 64 FMAs per float4 of B, more than the VALU issues at
 // HBM rate; v_mfma_f32_16x16x4f32 covers 16 rows at once, and MG groups of 16
-// rows (MG = ceil(M / 16)) reuse each float4 of B for 4 * MG MFMAs.  Each wave covers 64
-// columns: lane (q = l/16, p = l%16) loads the float4 B[k][c0+4p .. c0+4p+3] of
-// row k = k0 + 4s + q of step s (four 256-byte row segments per step), and MFMA
-// e (e = 0..3) multiplies element e of it, so MFMA e computes the columns
-// c0 + 4p + e with A[p][k] as its A operand (zero for p >= M).  Accumulator
-// register r of MFMA e then holds C[4q + r][c0 + 4p + e]: each lane owns a 4x4
-// block, stored as four float4 rows (per row group g: rows 16g + 4q + r).
-// Waves take the 4-row steps w, w+4, ...
-// of the workgroup's K slice, U steps in flight, and hand their sums to wave 0
-// through LDS (added in wave order).  Splits as in the VALU form.
+// rows (MG = ceil(M / 16)) reuse each float4 of B for 4 * MG MFMAs.  Each wave
+// covers 64 columns: lane (q = l/16, p = l%16) loads the float4
+// B[k][c0+4p .. c0+4p+3] of row k = k0 + 4s + q of step s (four 256-byte row
+// segments per step), and MFMA e (e = 0..3) multiplies element e of it, so MFMA
+// e computes the columns c0 + 4p + e with A[16g + p][k] as its A operand (zero
+// past M).  Accumulator register r of MFMA e then holds C[16g + 4q + r][c0 + 4p
+// + e]: each lane owns 4x4 blocks, stored as float4 rows.  Splits as in the
+// VALU form.
 constexpr int kSkinnyMfmaCols = 64;
 
-template <bool TA, bool VEC, int MG>
-__global__ void __launch_bounds__(256)
-sgemm_skinny_mfma_kernel(const GemmArgs g)
-{
-    constexpr int U = 8;
-    __shared__ floatx4 red[3][4 * MG][64];
-    const int lane = threadIdx.x & 63;
-    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int p = lane & 15, q = lane >> 4;
-    const int M = g.M, N = g.N;
-    const int col = blockIdx.x * kSkinnyMfmaCols + 4 * p;
-    const int k0 = blockIdx.y * g.kchunk;
-    const int k1 = min(g.K, k0 + g.kchunk);
-    const bool colfull = VEC && col + 3 < N;
-    const int nsteps = (k1 - k0 + 3) / 4;
-    floatx4 acc[MG][4];
-#pragma unroll
-    for (int gi = 0; gi < MG; ++gi)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) acc[gi][e] = floatx4{0.f, 0.f, 0.f, 0.f};
-    for (int s0 = wv; s0 < nsteps; s0 += 4 * U) {
-        float4 b[U];
-        float a[MG][U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int kk = k0 + 4 * (s0 + 4 * u) + q;
-            b[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-            for (int gi = 0; gi < MG; ++gi) a[gi][u] = 0.f;
-            if (kk < k1) {
-                const float* src = g.B + static_cast<long long>(kk) * g.ldb + col;
-                if (colfull) {
-                    const floatx4 v = __builtin_nontemporal_load(reinterpret_cast<const floatx4*>(src));
-                    b[u] = make_float4(v.x, v.y, v.z, v.w);
-                } else {
-                    b[u].x = col + 0 < N ? src[0] : 0.f;
-                    b[u].y = col + 1 < N ? src[1] : 0.f;
-                    b[u].z = col + 2 < N ? src[2] : 0.f;
-                    b[u].w = col + 3 < N ? src[3] : 0.f;
-                }
-#pragma unroll
-                for (int gi = 0; gi < MG; ++gi) {
-                    const int row = 16 * gi + p;
-                    if (row < M)
-                        a[gi][u] = TA ? g.A[static_cast<long long>(kk) * g.lda + row]
-                                      : g.A[static_cast<long long>(row) * g.lda + kk];
-                }
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            if (s0 + 4 * u < nsteps) {     // uniform
-#pragma unroll
-                for (int gi = 0; gi < MG; ++gi) {
-                    acc[gi][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[gi][u], b[u].x, acc[gi][0], 0, 0, 0);
-                    acc[gi][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[gi][u], b[u].y, acc[gi][1], 0, 0, 0);
-                    acc[gi][2] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[gi][u], b[u].z, acc[gi][2], 0, 0, 0);
-                    acc[gi][3] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[gi][u], b[u].w, acc[gi][3], 0, 0, 0);
-                }
-            }
-        }
-    }
-    if (wv > 0) {
-#pragma unroll
-        for (int gi = 0; gi < MG; ++gi)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) red[wv - 1][4 * gi + e][lane] = acc[gi][e];
-    }
-    __syncthreads();
-    if (wv != 0) return;
-#pragma unroll
-    for (int gi = 0; gi < MG; ++gi)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-#pragma unroll
-            for (int w = 0; w < 3; ++w) acc[gi][e] += red[w][4 * gi + e][lane];
-        }
-    const bool split = g.splits > 1;
-    float* base = split ? g.ws + static_cast<long long>(blockIdx.y) * M * N : g.C;
-    const int ld = split ? N : g.ldc;
-    const bool vst = colfull && (split ? (N % 4 == 0) : (g.ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(g.C) & 15u) == 0));
-#pragma unroll
-    for (int gr = 0; gr < 4 * MG; ++gr) {
-        const int gi = gr >> 2, r = gr & 3;
-        const int row = 16 * gi + 4 * q + r;
-        if (row >= M) continue;
-        float v[4] = {acc[gi][0][r], acc[gi][1][r], acc[gi][2][r], acc[gi][3][r]};
-        float* dst = base + static_cast<long long>(row) * ld + col;
-        if (!split) {
-            const float* rr = g.R ? g.R + static_cast<long long>(row) * g.ldr + col : dst;
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                if (col + e < N) v[e] = g.alpha * v[e] + (g.beta != 0.f ? g.beta * rr[e] : 0.f);
-        }
-        if (vst) {
-            *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
-        } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                if (col + e < N) dst[e] = v[e];
-        }
-    }
-}
-
-// 17..64 rows (MG = 2..4 groups of 16): the same MFMA scheme with A staged in
-// LDS per chunk of KC K rows, since loading A per step (MG scalar loads a lane
-// per 4-row step, each touching 16 rows) outweighs the stream of B.  Eight
+// A is staged in LDS per chunk of KC K rows (loading it per step, MG scalar
+// loads a lane per 4-row step each touching 16 rows, outweighed the stream of
+// B at 64 rows and measured 6% slower at 16).  Eight
 // waves (two per SIMD) take the 4-row steps w, w + 8, ... of a chunk.  A chunk
 // is loaded as float4 along k (thread (m, k4): A[m][kc + 4k4 .. +3]) and written
 // k-major As[k][m] with row stride 80 (16k + m spreads a wave's writes and the
@@ -1563,8 +1457,8 @@ int skinny_plan(int m, int n, int k, size_t ws_floats, int* kchunk_out)
 {
     const int cus = st().cu_count > 0 ? st().cu_count : 256;
     const long long cb = ceil_div(n, m <= kSkinnyValuMax ? kSkinnyCols : kSkinnyMfmaCols);
-    // about two workgroups per CU; one for the eight-wave 17..64-row kernel
-    const long long per_cu = m > 16 ? 1 : 2;
+    // about two workgroups per CU for the VALU form; one for the eight-wave MFMA form
+    const long long per_cu = m > kSkinnyValuMax ? 1 : 2;
     long long s = (per_cu * cus + cb - 1) / cb;
     s = std::min<long long>(s, k / 64);
     s = std::min<long long>(s, std::max<long long>(1, k / (8LL * m)));
@@ -1610,15 +1504,8 @@ int launch_skinny(int ta, GemmArgs g, hipStream_t stream)
             }
         };
         const int mg = ceil_div(g.M, 16);
-        if (mg == 1) {
-            if (ta) {
-                if (vec) sgemm_skinny_mfma_kernel<true, true, 1><<<grid, 256, 0, stream>>>(g);
-                else sgemm_skinny_mfma_kernel<true, false, 1><<<grid, 256, 0, stream>>>(g);
-            } else {
-                if (vec) sgemm_skinny_mfma_kernel<false, true, 1><<<grid, 256, 0, stream>>>(g);
-                else sgemm_skinny_mfma_kernel<false, false, 1><<<grid, 256, 0, stream>>>(g);
-            }
-        } else if (mg == 2) go(std::integral_constant<int, 2>{});
+        if (mg == 1) go(std::integral_constant<int, 1>{});
+        else if (mg == 2) go(std::integral_constant<int, 2>{});
         else if (mg == 3) go(std::integral_constant<int, 3>{});
         else go(std::integral_constant<int, 4>{});
     }
