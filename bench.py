@@ -128,7 +128,7 @@ def cpu_baseline_gemm(n=512, reps=4):
 # library stream it runs on.
 # HBM bytes per launch of that kernel from rocprofv3 FETCH_SIZE / WRITE_SIZE
 # (scaled by the copy-kernel calibration): profiles/sgemm_batched_reduce_dh2.md.
-DOMINANT_C2_TRAFFIC_BYTES = 3_506_176
+DOMINANT_C2_TRAFFIC_BYTES = 3_474_432
 
 
 def dominant_kernel_c2(steps, warmup):

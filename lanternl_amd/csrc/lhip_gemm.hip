@@ -1103,14 +1103,15 @@ sgemm_skinny_mfma_lds_kernel(const GemmArgs g)
 // K step at k0, lane l (row or column l%16, group q = l/16) holds
 // op(A)[row][k0+4q .. k0+4q+3] and op(B)[k0+4q .. k0+4q+3][col]; MFMA i of the
 // step multiplies element i of both, so its four k slots (one per lane group)
-// are k0+4q+i and the four MFMAs cover k0 .. k0+15 exactly once.  The four
-// waves take the 16-deep steps w, w+4, ...; their tiles are summed in LDS in
-// wave order.  Steps wholly past the end of K issue no MFMA.  BR as above.
-template <bool TA, bool TB, bool BR, bool PIPE>
-__global__ void __launch_bounds__(256)
+// are k0+4q+i and the four MFMAs cover k0 .. k0+15 exactly once.  The NW
+// waves (4, or 8 for one-pass slices deeper than 256) take the 16-deep steps
+// w, w+NW, ...; their tiles are summed in LDS in wave order.  Steps wholly
+// past the end of K issue no MFMA.  BR as above.
+template <bool TA, bool TB, bool BR, bool PIPE, int NW = 4>
+__global__ void __launch_bounds__(64 * NW)
 sgemm_tiny_kernel(const GemmArgs g)
 {
-    __shared__ float red[4][4][64];
+    __shared__ float red[NW][4][64];
     const int M = g.M, N = g.N;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -1145,7 +1146,7 @@ sgemm_tiny_kernel(const GemmArgs g)
     auto load_pass = [&](int kp, float (&a)[U][4], float (&b)[U][4]) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int ks = kp + 64 * u;                 // wave-uniform step start
+            const int ks = kp + 16 * NW * u;                 // wave-uniform step start
             const bool live = ks < kend;                // uniform
             // Without a second pass to overlap, steps past the end are skipped
             // by a scalar branch.  A pipelined pass keeps a fixed load count
@@ -1224,7 +1225,7 @@ sgemm_tiny_kernel(const GemmArgs g)
     auto load_pass_guarded = [&](int kp, float (&a)[U][4], float (&b)[U][4]) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int kl = kp + 64 * u + 4 * q;
+            const int kl = kp + 16 * NW * u + 4 * q;
             const bool kfull = kl + 3 < kend;
             const int kend_l = kend - kl;
             int kb = kl;
@@ -1235,7 +1236,7 @@ sgemm_tiny_kernel(const GemmArgs g)
                 // block, so the index is the wave-uniform step start's
                 int j;
                 if (g.Kb % 16 == 0) {
-                    const int ks = __builtin_amdgcn_readfirstlane(kp + 64 * u);
+                    const int ks = __builtin_amdgcn_readfirstlane(kp + 16 * NW * u);
                     j = ks / g.Kb;
                 } else {
                     j = kl / g.Kb;
@@ -1286,7 +1287,7 @@ sgemm_tiny_kernel(const GemmArgs g)
     auto load_pass_full = [&](int kp, float (&a)[U][4], float (&b)[U][4]) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int ks = kp + 64 * u;
+            const int ks = kp + 16 * NW * u;
             if (ks >= kend) break;
             const int kl = ks + 4 * q;
             int kb = kl;
@@ -1317,7 +1318,7 @@ sgemm_tiny_kernel(const GemmArgs g)
     auto mma_pass = [&](int kp, const float (&a)[U][4], const float (&b)[U][4]) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            if (kp + 64 * u >= kend) break;   // wave-uniform: nothing left in this pass
+            if (kp + 16 * NW * u >= kend) break;   // wave-uniform: nothing left in this pass
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u][i], b[u][i], acc, 0, 0, 0);
         }
@@ -1330,7 +1331,7 @@ sgemm_tiny_kernel(const GemmArgs g)
             __builtin_amdgcn_sched_barrier(0);   // keep every load ahead of the first MFMA
 #pragma unroll
             for (int u = 0; u < U; ++u) {
-                if (kp + 64 * u >= kend) break;
+                if (kp + 16 * NW * u >= kend) break;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a0[u][i], b0[u][i], acc, 0, 0, 0);
             }
@@ -1343,11 +1344,11 @@ sgemm_tiny_kernel(const GemmArgs g)
         float a0[U][4], b0[U][4], a1[U][4], b1[U][4];
         load_pass_guarded(kp, a0, b0);
         while (true) {
-            const int k1 = kp + 64 * U;
+            const int k1 = kp + 16 * NW * U;
             if (k1 < kend) load_pass_guarded(k1, a1, b1);
             mma_pass(kp, a0, b0);
             if (k1 >= kend) break;
-            const int k2 = k1 + 64 * U;
+            const int k2 = k1 + 16 * NW * U;
             if (k2 < kend) load_pass_guarded(k2, a0, b0);
             mma_pass(k1, a1, b1);
             if (k2 >= kend) break;
@@ -1355,11 +1356,15 @@ sgemm_tiny_kernel(const GemmArgs g)
         }
     }
 
-    // thread (wave w, lane l) finishes accumulator register w of lane l
+    // thread (wave w < 4, lane l) finishes accumulator register w of lane l,
+    // summing the NW waves' partial tiles in wave order
 #pragma unroll
     for (int r = 0; r < 4; ++r) red[wave][r][lane] = acc[r];
     __syncthreads();
-    const float v = ((red[0][wave][lane] + red[1][wave][lane]) + red[2][wave][lane]) + red[3][wave][lane];
+    if (wave >= 4) return;
+    float v = red[0][wave][lane];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) v += red[w][wave][lane];
     const int orow = m0 + 4 * q + wave;
     const int ocol = n0 + lr;
     if (orow >= M || ocol >= N) return;
@@ -1392,16 +1397,17 @@ void launch_small_t(const GemmArgs& g, dim3 grid, hipStream_t stream)
 int launch_reduce(const GemmArgs& g, int batch, hipStream_t stream);
 
 // PIPE: K needs more than one pass of the four waves (64 * kSmallU deep)
-template <bool PIPE>
-void launch_tiny_t(int ta, int tb, const GemmArgs& g, dim3 grid, dim3 block, hipStream_t stream)
+template <bool PIPE, int NW>
+void launch_tiny_t(int ta, int tb, const GemmArgs& g, dim3 grid, hipStream_t stream)
 {
+    const dim3 block(64 * NW);
     if (g.Kb != g.K) {
-        if (!tb) sgemm_tiny_kernel<false, false, true, PIPE><<<grid, block, 0, stream>>>(g);
-        else sgemm_tiny_kernel<false, true, true, PIPE><<<grid, block, 0, stream>>>(g);
-    } else if (!ta && !tb) sgemm_tiny_kernel<false, false, false, PIPE><<<grid, block, 0, stream>>>(g);
-    else if (ta && !tb) sgemm_tiny_kernel<true, false, false, PIPE><<<grid, block, 0, stream>>>(g);
-    else if (!ta && tb) sgemm_tiny_kernel<false, true, false, PIPE><<<grid, block, 0, stream>>>(g);
-    else sgemm_tiny_kernel<true, true, false, PIPE><<<grid, block, 0, stream>>>(g);
+        if (!tb) sgemm_tiny_kernel<false, false, true, PIPE, NW><<<grid, block, 0, stream>>>(g);
+        else sgemm_tiny_kernel<false, true, true, PIPE, NW><<<grid, block, 0, stream>>>(g);
+    } else if (!ta && !tb) sgemm_tiny_kernel<false, false, false, PIPE, NW><<<grid, block, 0, stream>>>(g);
+    else if (ta && !tb) sgemm_tiny_kernel<true, false, false, PIPE, NW><<<grid, block, 0, stream>>>(g);
+    else if (!ta && tb) sgemm_tiny_kernel<false, true, false, PIPE, NW><<<grid, block, 0, stream>>>(g);
+    else sgemm_tiny_kernel<true, true, false, PIPE, NW><<<grid, block, 0, stream>>>(g);
 }
 
 int launch_tiny(int ta, int tb, GemmArgs g, int batch, hipStream_t stream)
@@ -1411,9 +1417,12 @@ int launch_tiny(int ta, int tb, GemmArgs g, int batch, hipStream_t stream)
     const long long nwg = static_cast<long long>(g.tiles_m) * g.tiles_n;
     if (nwg > 0x7fffffffLL) return fail(LHIP_E_CAPACITY, "sgemm: %lld workgroups exceed the grid limit", nwg);
     if (g.splits <= 1) { g.splits = 1; g.kchunk = g.K; g.ws = nullptr; }
-    dim3 grid(static_cast<unsigned>(nwg), batch, g.splits), block(256);
-    if (g.kchunk > 64 * kSmallU) launch_tiny_t<true>(ta, tb, g, grid, block, stream);
-    else launch_tiny_t<false>(ta, tb, g, grid, block, stream);
+    dim3 grid(static_cast<unsigned>(nwg), batch, g.splits);
+    // one pass of four waves covers 64 * kSmallU of K; a one-pass slice deeper
+    // than 256 runs on eight waves (half the loads and MFMAs per wave)
+    if (g.kchunk > 64 * kSmallU) launch_tiny_t<true, 4>(ta, tb, g, grid, stream);
+    else if (g.kchunk > 256) launch_tiny_t<false, 8>(ta, tb, g, grid, stream);
+    else launch_tiny_t<false, 4>(ta, tb, g, grid, stream);
     int rc = check_launch("sgemm (tiny): kernel launch");
     if (rc != LHIP_OK || g.splits <= 1 || g.skip_reduce) return rc;
     return launch_reduce(g, batch, stream);
