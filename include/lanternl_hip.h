@@ -95,7 +95,7 @@ typedef struct {
     unsigned long long live_buffers;
     unsigned long long n_alloc;          /* lhip_malloc calls that succeeded  */
     unsigned long long n_free;           /* lhip_free calls of live buffers   */
-    unsigned long long workspace_bytes;  /* library scratch (split-K, reductions) */
+    unsigned long long workspace_bytes;  /* library scratch (split-K, reductions), incl. retired */
     unsigned long long staging_bytes;    /* host-table path device staging    */
 } lhip_mem_stats_t;
 LHIP_API int lhip_mem_stats(lhip_mem_stats_t* out);
@@ -129,8 +129,11 @@ LHIP_API int lhip_event_elapsed_ms(void* start, void* stop, float* ms);
  * to the host (upload, download, sync, malloc, free, event timing,
  * lhip_matmul_host, every lhip_lm_* call) fail with LHIP_E_UNSUPPORTED, and
  * so does a call whose library workspace would have to grow: issue the same
- * calls once before recording them.  lhip_program_end(NULL) discards the
- * recording.  Replaces the Program command buffer with its capture/replay
+ * calls once before recording them.  A program keeps the library workspace it
+ * was recorded with: when a later eager call grows the workspace while
+ * programs are live, the old one is retired, not freed, and released when the
+ * last program is freed (or at lhip_shutdown).  lhip_program_end(NULL)
+ * discards the recording.  Replaces the Program command buffer with its capture/replay
  * (ai/gpu/luaTL_train.lua:327-627; luaTL_prog_run / luaTL_prog_capture /
  * luaTL_prog_replay / luaTL_prog_graph_free, cuda/luaTL_train.cu:1505-1690). */
 LHIP_API int lhip_program_begin(void);

@@ -562,7 +562,9 @@ int attn_bwd(const float* qkv, const float2* cs, const float* P, const float* ct
     a.qkv = qkv; a.cs = cs; a.P = const_cast<float*>(P); a.ctx = const_cast<float*>(ctx); a.dctx = dctx; a.dqkv = dqkv;
     a.B = B; a.H = H; a.T = T; a.hd = hd; a.D = H * hd; a.N = B * T;
     a.scale = scale; a.causal = causal;
-    a.vec = (hd % 4 == 0 && aligned16(qkv) && aligned16(cs) && aligned16(dctx) && aligned16(dqkv)) ? 1 : 0;
+    // the float4 path also reads ctx (the forward's O, for rowsum(dO*O))
+    a.vec = (hd % 4 == 0 && aligned16(qkv) && aligned16(cs) && aligned16(ctx) && aligned16(dctx) &&
+             aligned16(dqkv)) ? 1 : 0;
     attn_bwd_kernel<<<B * H * ((T + 15) / 16), kAttnThreads, 0, s>>>(a);
     return check_launch("attn_bwd");
 }

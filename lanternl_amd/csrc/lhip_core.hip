@@ -51,8 +51,15 @@ int workspace(size_t bytes, void** out)
                         "workspace: %zu bytes needed (%zu held) while a program is being recorded; run the same "
                         "calls once before recording them", bytes, s.work_bytes);
         if (s.work) {
-            LHIP_CHECK_HIP(hipStreamSynchronize(s.stream), "workspace: stream sync");
-            LHIP_CHECK_HIP(hipFree(s.work), "workspace: hipFree");
+            if (s.live_programs > 0) {
+                // a live program may hold this pointer: keep it until the last
+                // program is freed (lhip_program_free) or shutdown
+                s.retired.push_back(s.work);
+                s.retired_bytes += s.work_bytes;
+            } else {
+                LHIP_CHECK_HIP(hipStreamSynchronize(s.stream), "workspace: stream sync");
+                LHIP_CHECK_HIP(hipFree(s.work), "workspace: hipFree");
+            }
             s.work = nullptr;
             s.work_bytes = 0;
         }
@@ -132,6 +139,7 @@ LHIP_API int lhip_shutdown(void)
     if (s.d_stage) (void)hipFree(s.d_stage);
     if (s.h_stage) (void)hipHostFree(s.h_stage);
     if (s.work) (void)hipFree(s.work);
+    for (void* p : s.retired) (void)hipFree(p);
     (void)hipStreamDestroy(s.stream);
     s = lhip::State();
     return LHIP_OK;
@@ -217,7 +225,7 @@ LHIP_API int lhip_mem_stats(lhip_mem_stats_t* out)
     out->live_buffers = s.live.size();
     out->n_alloc = s.n_alloc;
     out->n_free = s.n_free;
-    out->workspace_bytes = s.work_bytes;
+    out->workspace_bytes = s.work_bytes + s.retired_bytes;
     out->staging_bytes = s.d_stage_floats * sizeof(float);
     return LHIP_OK;
 }
@@ -349,6 +357,7 @@ LHIP_API int lhip_program_end(void** program)
     (void)hipGraphDestroy(g);
     if (e != hipSuccess) return lhip::hip_fail(e, "lhip_program_end: instantiate");
     *program = static_cast<void*>(x);
+    ++s.live_programs;
     return LHIP_OK;
 }
 
@@ -370,6 +379,15 @@ LHIP_API int lhip_program_free(void* program)
     // a replay still in flight uses the executable graph
     LHIP_CHECK_HIP(hipStreamSynchronize(st().stream), "lhip_program_free: stream sync");
     LHIP_CHECK_HIP(hipGraphExecDestroy(static_cast<hipGraphExec_t>(program)), "lhip_program_free");
+    auto& s = st();
+    if (s.live_programs > 0) --s.live_programs;
+    if (s.live_programs == 0 && !s.retired.empty()) {
+        // no program can reach the retired workspaces any more (the stream
+        // was synchronised above)
+        for (void* p : s.retired) LHIP_CHECK_HIP(hipFree(p), "lhip_program_free: retired workspace");
+        s.retired.clear();
+        s.retired_bytes = 0;
+    }
     return LHIP_OK;
 }
 

@@ -7,6 +7,7 @@
 #pragma once
 
 #include <unordered_map>
+#include <vector>
 #include <hip/hip_runtime.h>
 
 #include <cstddef>
@@ -35,6 +36,13 @@ struct State {
     // scratch for reductions of the immediate entry points (grown on demand)
     void* work = nullptr;
     size_t work_bytes = 0;
+    // workspaces replaced by a larger one while recorded programs were live:
+    // a program keeps the pointer it was recorded with, so these stay
+    // allocated until no program is live (or shutdown)
+    std::vector<void*> retired;
+    size_t retired_bytes = 0;
+    // executable programs made by lhip_program_end and not yet freed
+    int live_programs = 0;
     // a program (stream capture of the library stream) is being recorded
     bool recording = false;
     // accounting of lhip_malloc buffers (lhip_mem_stats)
@@ -91,7 +99,8 @@ __device__ __forceinline__ void xcd_tile(int pid, int nwg, int tiles_n, int& tm,
 
 // Library workspace of at least `bytes` (reused; growing it waits for the
 // stream, so while a program is being recorded a call that would grow it fails
-// with LHIP_E_UNSUPPORTED).
+// with LHIP_E_UNSUPPORTED).  While recorded programs are live, the workspace
+// they were recorded with is retired rather than freed when it grows.
 int workspace(size_t bytes, void** out);
 
 // Launchers shared by the immediate entry points and the LM step runner.  They

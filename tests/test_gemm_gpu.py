@@ -154,6 +154,47 @@ def test_gemm_square_large(n):
         assert rel_fro(C.download(), ref) <= TOL, (ta, tb)
 
 
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1)])
+def test_gemm_square_8192(ta, tb):
+    """Config C5's largest square shape, 8192^3, for A.B, A^T.B and A.B^T.
+
+    A full float64 product would take minutes on the host, so two checks
+    cover it:
+      * 256 whole rows of C, drawn at random over every row band, against
+        float64 (relative Frobenius <= 1e-4);
+      * a Freivalds check of every row of C: with two random vectors x,
+        C.x against op(A).(op(B).x) in float64, row by row, relative to
+        |C_i| |x|.  A single wrong element of size e in row i moves that row's
+        residual by about e |x_j|; fp32 rounding moves it by ~1e-8 of the
+        scale (2.3e-8 measured for numpy's fp32 product at 4096^3), so the
+        1e-6 bar catches any element wrong by more than ~0.5 (entries of C
+        are ~ sqrt(8192/9) = 30 in size).
+    """
+    n = 8192
+    announce("gemm square 8192", ta, tb)
+    rng = np.random.default_rng(8192 + 2 * ta + tb)
+    a = rng.uniform(-1, 1, (n, n)).astype(np.float32)     # stored operand (k x m when ta)
+    b = rng.uniform(-1, 1, (n, n)).astype(np.float32)     # stored operand (n x k when tb)
+    A, B, C = to_dev(a), to_dev(b), device.Buffer((n, n))
+    kernels.sgemm(A, B, C, transa=ta, transb=tb)
+    device.sync()
+    del A, B
+    c = C.download()
+    del C
+    opa = a.T if ta else a            # op(A), views
+    opb = b.T if tb else b
+    rows = np.sort(rng.choice(n, 256, replace=False))
+    ref_rows = opa[rows].astype(np.float64) @ opb.astype(np.float64)
+    assert rel_fro(c[rows], ref_rows) <= TOL
+    x = rng.standard_normal((n, 2))
+    bx = opb.astype(np.float64) @ x
+    abx = opa.astype(np.float64) @ bx
+    cx = c.astype(np.float64) @ x
+    scale = np.linalg.norm(c.astype(np.float64), axis=1)[:, None] * np.linalg.norm(x, axis=0)[None, :]
+    worst = float(np.max(np.abs(cx - abx) / scale))
+    assert worst <= 1e-6, worst
+
+
 @pytest.mark.parametrize("m", [1, 16, 64])
 def test_gemm_skinny(m):
     """Config C5 skinny shapes: M in {1,16,64}, K=N=4096."""

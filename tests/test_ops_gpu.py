@@ -356,8 +356,12 @@ def test_embed_out_of_range_ids_give_zero_rows():
 
 
 # ------------------------------------------------------------------ optimizer
-@pytest.mark.parametrize("clip,B,nan", [(1.0, 8, False), (1e6, 1, False), (1.0, 4, True)])
-def test_sumsq_and_sgd_step_vs_oracle(clip, B, nan):
+@pytest.mark.parametrize("clip,B,nan,mom,nest", [(1.0, 8, False, 0.9, 0), (1e6, 1, False, 0.9, 0),
+                                                  (1.0, 4, True, 0.9, 0), (1.0, 8, False, 0.9, 1),
+                                                  (1e6, 2, False, 0.0, 0)])
+def test_sumsq_and_sgd_step_vs_oracle(clip, B, nan, mom, nest):
+    """lhip_sgd_step: LMTrain's step logic around optim2.SGD (lmtrain.lua:1212-1226,
+    optim2.lua:72-99), with momentum (plain and Nesterov) and without."""
     rng = np.random.default_rng(17)
     n = 912_512
     p = f32(rng.standard_normal(n) * 0.02)
@@ -373,8 +377,8 @@ def test_sumsq_and_sgd_step_vs_oracle(clip, B, nan):
     ss = SS.download().view(np.float64)[0]
     if not nan:
         assert abs(ss - float(np.sum(g * g))) <= 1e-9 * ss
-    lr, mom, wd = 0.05, 0.9, 0.01
-    call("lhip_sgd_step", P.ptr, G.ptr, Vb.ptr, n, SS.ptr, lr, mom, wd, 1.0 / B, clip, 0, NORM.ptr, APP.ptr)
+    lr, wd = 0.05, 0.01
+    call("lhip_sgd_step", P.ptr, G.ptr, Vb.ptr, n, SS.ptr, lr, mom, wd, 1.0 / B, clip, nest, NORM.ptr, APP.ptr)
     device.sync()
     # oracle: scale_grads(1/B) (only when B > 1), norm, skip if non-finite, clip, SGD
     gg = g / B if B > 1 else g.copy()
@@ -385,7 +389,7 @@ def test_sumsq_and_sgd_step_vs_oracle(clip, B, nan):
     if applied:
         if norm > clip:
             gg = gg * (clip / norm)
-        O.sgd_step(pr, gg, vr, lr, mom, wd)
+        O.sgd_step(pr, gg, vr, lr, mom, wd, nesterov=bool(nest))
         assert abs(NORM.download()[0] - norm) <= 1e-6 * norm
         assert rel_fro(dl(G), gg) <= EW
     assert rel_fro(dl(P), pr) <= EW and rel_fro(dl(Vb), vr) <= EW

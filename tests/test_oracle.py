@@ -273,6 +273,27 @@ def test_grad_norm_and_sgd_closed_form():
     np.testing.assert_allclose(p, [0.949 - 0.096849, -2.023 - 0.043677], rtol=1e-14)
 
 
+def test_sgd_nesterov_and_plain_closed_form():
+    """optim2.lua:84-97: Nesterov steps by g' + momentum*v instead of v, and
+    momentum 0 is plain SGD on g' = g + wd*p (hand-computed values)."""
+    g = np.array([0.5, 0.25])
+    p = np.array([1.0, -2.0]); v = np.zeros(2)
+    O.sgd_step(p, g, v, lr=0.1, momentum=0.9, wd=0.01, nesterov=True)
+    # step 1: g' = [0.51, 0.23] = v; p -= 0.1 * (g' + 0.9 v) = 0.1 * 1.9 g'
+    np.testing.assert_allclose(v, [0.51, 0.23], rtol=1e-15)
+    np.testing.assert_allclose(p, [0.9031, -2.0437], rtol=1e-14)
+    O.sgd_step(p, g, v, lr=0.1, momentum=0.9, wd=0.01, nesterov=True)
+    # step 2: g' = g + 0.01 p = [0.509031, 0.229563]; v = 0.9 v + g' = [0.968031, 0.436563];
+    # p -= 0.1 * (g' + 0.9 v) = 0.1 * [1.3802589, 0.6224697]
+    np.testing.assert_allclose(v, [0.968031, 0.436563], rtol=1e-14)
+    np.testing.assert_allclose(p, [0.76507411, -2.10594697], rtol=1e-14)
+    # momentum 0: no velocity, p -= lr * (g + wd p); v untouched
+    p = np.array([1.0, -2.0]); v = np.array([7.0, 7.0])
+    O.sgd_step(p, g, v, lr=0.1, momentum=0.0, wd=0.01)
+    np.testing.assert_allclose(p, [1.0 - 0.051, -2.0 - 0.023], rtol=1e-15)
+    assert np.array_equal(v, [7.0, 7.0])
+
+
 def test_adamw_closed_forms():
     """optim2.lua:116-147.  No reference test holds AdamW vectors, so the
     restatement is pinned by what the algorithm fixes: with a constant

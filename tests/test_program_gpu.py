@@ -150,3 +150,53 @@ def test_discarded_recording_leaves_library_usable():
         call("lhip_program_end", None)               # nothing is being recorded
     with pytest.raises(LanternlHipError, match="NULL"):
         call("lhip_program_replay", None, 1)
+
+
+def test_program_survives_workspace_growth():
+    """A program keeps the workspace pointer it was recorded with.  An eager
+    call that grows the library workspace while the program is live must not
+    free that memory under it: the old workspace is retired until the last
+    program is freed, and the replay still matches the eager result."""
+    announce("program", "workspace growth between record and replay")
+    from lanternl_amd._lib import MemStats
+    rng = np.random.default_rng(9)
+
+    def ws_bytes():
+        s = MemStats()
+        call("lhip_mem_stats", ctypes.byref(s))
+        return s.workspace_bytes
+
+    m, n, k = 256, 128, 8192                       # split-K through the workspace
+    a, b = f32(rng.uniform(-1, 1, (m, k))), f32(rng.uniform(-1, 1, (k, n)))
+    A, B, Cp = to_dev(a), to_dev(b), device.Buffer((m, n))
+    call("lhip_sgemm", 0, 0, m, n, k, 1.0, A.ptr, k, B.ptr, n, 0.0, Cp.ptr, n)
+    eager = dl(Cp)
+    assert rel_fro(eager, O.mm(a, b)) <= 1e-4
+    prog = device.Program.record(
+        lambda: call("lhip_sgemm", 0, 0, m, n, k, 1.0, A.ptr, k, B.ptr, n, 0.0, Cp.ptr, n))
+    w0 = ws_bytes()
+    # 4096 x 3840 x 4096 splits K in two slices of 4096x3840 floats (126 MB of
+    # partials), more than any earlier call of this suite needs
+    gm, gn, gk = 4096, 3840, 4096
+    ga = to_dev(rng.uniform(-1, 1, (gm, gk)).astype(np.float32))
+    gb = to_dev(rng.uniform(-1, 1, (gk, gn)).astype(np.float32))
+    gc = device.Buffer((gm, gn))
+    call("lhip_sgemm", 0, 0, gm, gn, gk, 1.0, ga.ptr, gk, gb.ptr, gn, 0.0, gc.ptr, gn)
+    device.sync()
+    if ws_bytes() <= w0:
+        prog.free()
+        pytest.skip(f"workspace already {w0} bytes: the growing call did not grow it")
+    grown = ws_bytes()          # the new workspace, plus the retired one held for the program
+    assert grown > w0
+    del ga, gb, gc
+    for rep in range(3):
+        Cp.zero()
+        prog.replay()
+        got = dl(Cp)
+        assert np.array_equal(got, eager), f"replay {rep} after the workspace grew"
+        # the eager path on the grown workspace still agrees too
+        call("lhip_sgemm", 0, 0, m, n, k, 1.0, A.ptr, k, B.ptr, n, 0.0, Cp.ptr, n)
+        assert np.array_equal(dl(Cp), eager)
+    prog.free()
+    # the retired workspace is released with the last live program
+    assert ws_bytes() == grown - w0
