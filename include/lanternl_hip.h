@@ -170,6 +170,22 @@ LHIP_API int lhip_sgemm_batched_reduce(int transa, int transb, int m, int n, int
                                        const float* A, int lda, long long strideA,
                                        const float* B, int ldb, long long strideB, float beta,
                                        float* C, int ldc, int count);
+/* lhip_sgemm with no allocation of any kind: no counterpart in the reference.
+ * It is for callers that cannot allocate device memory (code under graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments, kernels and results as lhip_sgemm (bit-identical: the same K
+ * slices summed in the same order), but split-K partials go to a fixed 64 MiB
+ * device array that each GPU holds from lhip_init to process exit, never to
+ * the library workspace.  A shape whose partials would exceed 64 MiB is
+ * refused with LHIP_E_CAPACITY before anything is launched (e.g. 4096 x 3840
+ * x 4096, two slices of 63 MB each); every unsplit shape fits.  All calls on
+ * one GPU share the array and each overwrites what the previous left: they are
+ * ordered on the library stream, and work that overlapped them on one GPU
+ * (another stream replaying a recording of this call) would race.  Recordable
+ * into a program at any time. */
+LHIP_API int lhip_sgemm_noalloc(int transa, int transb, int m, int n, int k, float alpha,
+                                const float* A, int lda, const float* B, int ldb, float beta,
+                                float* C, int ldc);
 
 /* Host-table GEMM for the flat-table backend contract (matrix.lua:178-202 ->
  * luatl_adapter.lua:128-135).  a, b, c are HOST double arrays, row-major:

@@ -74,6 +74,7 @@ SIGNATURES = {
     "lhip_sgemm_strided_batched": (_i, [_i, _i, _i, _i, _i, _f, _p, _i, _ll, _p, _i, _ll, _f,
                                         _p, _i, _ll, _i]),
     "lhip_sgemm_batched_reduce": (_i, [_i, _i, _i, _i, _i, _f, _p, _i, _ll, _p, _i, _ll, _f, _p, _i, _i]),
+    "lhip_sgemm_noalloc": (_i, [_i, _i, _i, _i, _i, _f, _p, _i, _p, _i, _f, _p, _i]),
     "lhip_matmul_host": (_i, [_i, _p, _p, _p, _i, _i, _i, _i]),
     "lhip_rmsnorm_fwd": (_i, [_p, _p, _p, _p, _i, _i, _f]),
     "lhip_rmsnorm_bwd": (_i, [_p, _p, _p, _p, _p, _p, _i, _i, _i]),

@@ -112,6 +112,10 @@ LHIP_API int lhip_init(int device)
         return fail(LHIP_E_UNSUPPORTED, "lhip_init: device %d is %s; this library is built for gfx950 (MI355X) only",
                     device, p.gcnArchName);
     // Default-priority, non-blocking stream: independent of the null stream.
+    {
+        const int rc = lhip::noalloc_scratch_init(device);
+        if (rc != LHIP_OK) return rc;
+    }
     LHIP_CHECK_HIP(hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking), "lhip_init: hipStreamCreate");
     s.device = device;
     s.cu_count = p.multiProcessorCount;

@@ -1977,6 +1977,63 @@ int sgemm_launch(int ta, int tb, int m, int n, int k, float alpha,
     return sgemm_run(ta, tb, m, n, k, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC, batch, o, stream);
 }
 
+// Fixed split-K scratch of lhip_sgemm_noalloc (the array itself is below, at file scope).
+constexpr size_t kNoallocScratchBytes = static_cast<size_t>(64) << 20;   // 64 MiB
+constexpr int kNoallocMaxDevices = 64;
+
+}  // namespace lhip
+
+// ---- scratch of the allocation-free entry point (lhip_sgemm_noalloc) ----------
+// Split-K partials of lhip_sgemm_noalloc live in this file-scope device array
+// instead of the library workspace, so that call never allocates.  Each GPU
+// holds its own copy for the life of the process.  Host code never uses the
+// array's name as an address (on the host it is only a stand-in for the
+// symbol): lhip_init resolves its device address once per device with
+// hipGetSymbolAddress (noalloc_scratch_init) and every launch takes that
+// pointer.  The partials of a split are fully written before the reduce reads
+// them, so nothing in the array needs to start at zero.
+static __device__ __align__(256) float scratch[lhip::kNoallocScratchBytes / sizeof(float)];
+
+namespace lhip {
+
+static float* g_scratch_dev[kNoallocMaxDevices] = {};
+
+int noalloc_scratch_init(int device)
+{
+    if (device < 0 || device >= kNoallocMaxDevices)
+        return fail(LHIP_E_CAPACITY, "lhip_init: device %d beyond the %d devices the scratch table holds", device,
+                    kNoallocMaxDevices);
+    if (g_scratch_dev[device]) return LHIP_OK;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+        (void)hipGetLastError();
+        return fail(LHIP_E_DEVICE, "lhip_init: hipGetSymbolAddress(scratch) on device %d: %s", device,
+                    e != hipSuccess ? hipGetErrorString(e) : "null address");
+    }
+    g_scratch_dev[device] = static_cast<float*>(p);
+    return LHIP_OK;
+}
+
+// The split-K plan of an immediate product: the slice count (1 = unsplit) and
+// the partials it needs, in floats.  lhip_sgemm and lhip_sgemm_noalloc share
+// it, so both sum the same slices in the same order.
+static int immediate_plan(int transa, int transb, int m, int n, int k, int batch, size_t* need_floats)
+{
+    *need_floats = 0;
+    if (m <= 0 || n <= 0 || k <= 0 || batch <= 0) return 1;
+    const size_t cap = static_cast<size_t>(1) << 26;
+    int kchunk = 0, splits = 1;
+    if (skinny_ok(transa, transb, m, n, batch, 1)) {
+        splits = skinny_plan(m, n, k, cap, &kchunk);
+    } else {
+        splits = split256_plan(m, n, k, batch, cap, &kchunk);
+        if (splits <= 1) splits = splitk_plan(m, n, k, batch, cap, &kchunk);
+    }
+    if (splits > 1) *need_floats = static_cast<size_t>(splits) * m * n * batch;
+    return splits;
+}
+
 }  // namespace lhip
 
 using lhip::fail;
@@ -1992,23 +2049,34 @@ static int sgemm_immediate(int transa, int transb, int m, int n, int k, float al
 {
     lhip::GemmOpts o;
     o.inner = batch > 0 ? batch : 1;
-    int kchunk = 0;
-    if (m > 0 && n > 0 && k > 0 && batch > 0) {
-        const size_t cap = static_cast<size_t>(1) << 26;
-        int splits = 1;
-        if (lhip::skinny_ok(transa, transb, m, n, batch, 1)) {
-            splits = lhip::skinny_plan(m, n, k, cap, &kchunk);
-        } else {
-            splits = lhip::split256_plan(m, n, k, batch, cap, &kchunk);
-            if (splits <= 1) splits = lhip::splitk_plan(m, n, k, batch, cap, &kchunk);
-        }
-        if (splits > 1) {
-            o.ws_floats = static_cast<size_t>(splits) * m * n * batch;
-            int rc = lhip::workspace(o.ws_floats * sizeof(float), reinterpret_cast<void**>(&o.ws));
-            if (rc != LHIP_OK) return rc;
-        }
+    size_t need = 0;
+    if (lhip::immediate_plan(transa, transb, m, n, k, batch, &need) > 1) {
+        o.ws_floats = need;
+        int rc = lhip::workspace(o.ws_floats * sizeof(float), reinterpret_cast<void**>(&o.ws));
+        if (rc != LHIP_OK) return rc;
     }
     return lhip::sgemm_run(transa, transb, m, n, k, alpha, A, lda, sA, B, ldb, sB, beta, C, ldc, sC, batch, o,
+                           st().stream);
+}
+
+LHIP_API int lhip_sgemm_noalloc(int transa, int transb, int m, int n, int k, float alpha,
+                                const float* A, int lda, const float* B, int ldb, float beta,
+                                float* C, int ldc)
+{
+    LHIP_REQUIRE_READY();
+    float* const ptr = lhip::g_scratch_dev[st().device];
+    if (!ptr) return fail(LHIP_E_DEVICE, "lhip_sgemm_noalloc: scratch of device %d not resolved", st().device);
+    lhip::GemmOpts o;
+    size_t need = 0;
+    if (lhip::immediate_plan(transa, transb, m, n, k, 1, &need) > 1) {
+        if (need * sizeof(float) > lhip::kNoallocScratchBytes)
+            return fail(LHIP_E_CAPACITY,
+                        "lhip_sgemm_noalloc: m=%d n=%d k=%d needs %zu bytes of split-K scratch, beyond its fixed "
+                        "%zu bytes; use lhip_sgemm", m, n, k, need * sizeof(float), lhip::kNoallocScratchBytes);
+        o.ws = ptr;
+        o.ws_floats = need;
+    }
+    return lhip::sgemm_run(transa, transb, m, n, k, alpha, A, lda, 0, B, ldb, 0, beta, C, ldc, 0, 1, o,
                            st().stream);
 }
 

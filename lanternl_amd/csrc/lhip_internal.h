@@ -97,6 +97,10 @@ __device__ __forceinline__ void xcd_tile(int pid, int nwg, int tiles_n, int& tm,
     tn = pid - tm * tiles_n;
 }
 
+// Resolves, once per device, the device address of the fixed scratch array of
+// lhip_sgemm_noalloc (called by lhip_init with the device current).
+int noalloc_scratch_init(int device);
+
 // Library workspace of at least `bytes` (reused; growing it waits for the
 // stream, so while a program is being recorded a call that would grow it fails
 // with LHIP_E_UNSUPPORTED).  While recorded programs are live, the workspace
