@@ -311,6 +311,104 @@ LHIP_API int lhip_adamw_step(float* params, float* grads, float* m, float* v, lo
                              float weight_decay, float grad_scale, float clip_norm, int step,
                              float* grad_norm_out, int* applied_out);
 
+/* ---- the luaTL operation set ----------------------------------------------
+ * The calls behind the reference adapter's resident API
+ * (ai/gpu/luatl_adapter.lua:126-187) and luaTL.Program's op list
+ * (ai/gpu/luaTL_train.lua:365-606), with luaTL's semantics (fp32 only; every
+ * reduction deterministic).  Device pointers, asynchronous on the library
+ * stream like every compute call. */
+
+/* Post-GEMM activations and GEMM prologues: the values of luaTL's act/pre
+ * codes (cuda/luaTL_core.cu:76-90). */
+enum { LHIP_ACT_NONE = 0, LHIP_ACT_RELU = 1, LHIP_ACT_GELU = 2, LHIP_ACT_SILU = 3, LHIP_ACT_TANH = 4,
+       LHIP_ACT_SIGMOID = 5 };
+enum { LHIP_PRE_NONE = 0, LHIP_PRE_RMSNORM = 1, LHIP_PRE_GELU = 2, LHIP_PRE_SILU = 3, LHIP_PRE_RELU = 4 };
+
+/* C = act(alpha * pre(A) . B + bias) + beta * C over `batch` matrices, each
+ * operand a strided view: element (i, j) of A (M x K) at A[i*a_rs + j*a_cs]
+ * (+ b*a_bs for batch b), likewise B (K x N) and C (M x N).  pre RMSNORM
+ * scales row i of A by rowscale[i] (or, when rowscale is NULL, by
+ * 1/sqrt(mean_k A[i,k]^2 + eps)) and column k by gamma[k] (1 when NULL); the
+ * other prologues map A elementwise.  bias (N floats) and act may be
+ * NULL / NONE; beta == 0 never reads C.  Without a prologue each operand must
+ * be row- or column-major (one unit stride; anything else is
+ * LHIP_E_UNSUPPORTED); the product runs on the fp32 MFMA GEMM family, a
+ * prologue or epilogue as an extra streaming pass.  Replaces luaTL_gemm_ex
+ * (cuda/luaTL_train.cu:1075-1094; kernel semantics :127-234). */
+LHIP_API int lhip_gemm_ex(const float* A, const float* B, float* C, const float* bias, const float* gamma,
+                          const float* rowscale, int M, int N, int K, long long a_rs, long long a_cs,
+                          long long b_rs, long long b_cs, long long c_rs, long long c_cs, long long a_bs,
+                          long long b_bs, long long c_bs, int batch, float alpha, float beta, float eps,
+                          int pre_op, int post_op);
+
+/* Elementwise operators: the values of luaTL's EW codes (cuda/luaTL_core.cu:49-72). */
+enum { LHIP_EW_COPY = 0, LHIP_EW_ADD = 1, LHIP_EW_SUB = 2, LHIP_EW_MUL = 3, LHIP_EW_DIV = 4, LHIP_EW_SCALE = 5,
+       LHIP_EW_AXPY = 6, LHIP_EW_FILL = 7, LHIP_EW_RELU = 8, LHIP_EW_GELU = 9, LHIP_EW_SILU = 10,
+       LHIP_EW_TANH = 11, LHIP_EW_SIGMOID = 12, LHIP_EW_EXP = 13, LHIP_EW_SQRT = 14, LHIP_EW_RSQRT = 15,
+       LHIP_EW_NEG = 16, LHIP_EW_RECIP = 17, LHIP_EW_ABS = 18, LHIP_EW_CLAMP = 19, LHIP_EW_DRELU = 20,
+       LHIP_EW_DSILU = 21, LHIP_EW_DGELU = 22 };
+/* c[i] = op(a[i], b[i], alpha, beta) for i < n (a or b NULL reads as 0):
+ * ADD alpha*a+beta*b, SUB alpha*a-beta*b, MUL alpha*a*b, DIV alpha*a/(b+1e-20),
+ * SCALE alpha*a+beta, AXPY alpha*a+b, FILL alpha, CLAMP min(max(a,alpha),beta),
+ * DRELU b*(a>0), DSILU b*silu'(a), DGELU b*gelu'(a), the rest unary in a
+ * (GELU in its tanh form).  In place allowed.  Replaces luaTL_elementwise
+ * (cuda/luaTL_core.cu:2308; operators :909-934). */
+LHIP_API int lhip_elementwise(const float* a, const float* b, float* c, long long n, int op, float alpha, float beta);
+/* y = x * w / sqrt(mean_j x^2 + eps) per row, w NULL meaning gain 1 (up to
+ * 65536 columns), no 1/rms output.  Replaces luaTL_rmsnorm (cuda/luaTL_core.cu:
+ * 2329-2341, kernel :1092-1114). */
+LHIP_API int lhip_rmsnorm_ex(const float* x, const float* w, float* y, int rows, int cols, float eps);
+/* luaTL's RMSNorm backward: 1/rms recomputed from x and eps, dx overwritten,
+ * dw (may be NULL) accumulated (+=), w NULL meaning gain 1.  Replaces
+ * luaTL_rmsnorm_bwd (cuda/luaTL_train.cu:1096-1106, kernel :489-526). */
+LHIP_API int lhip_rmsnorm_bwd_ex(const float* x, const float* w, const float* dy, float* dx, float* dw, int rows,
+                                 int cols, float eps);
+/* out[r] = 1/sqrt(mean_k x[r*rs + k*cs]^2 + eps).  Replaces luaTL_row_rms
+ * (cuda/luaTL_train.cu:1261, kernel :355-369). */
+LHIP_API int lhip_row_rms(const float* x, float* out, int rows, int cols, long long rs, long long cs, float eps);
+/* luaTL's softmax: v = x*scale + bias[j] (bias NULL: none) over the columns
+ * j <= limit of row r, limit = ((group > 0 ? r % group : r) + mask_offset)
+ * when causal, else cols-1; masked entries 0, a row with nothing kept all 0.
+ * Replaces luaTL_softmax_ex (cuda/luaTL_train.cu:1108-1118, kernel :545-585). */
+LHIP_API int lhip_softmax_ex(const float* x, const float* bias, float* y, int rows, int cols, float scale, int causal,
+                             int group, int mask_offset);
+/* dx = scale * y * (dy - sum_{j<=limit} dy_j y_j) on the kept columns, 0 beyond
+ * (dx overwritten).  Replaces luaTL_softmax_bwd (cuda/luaTL_train.cu:1120-1129). */
+LHIP_API int lhip_softmax_bwd_ex(const float* y, const float* dy, float* dx, int rows, int cols, float scale,
+                                 int causal, int group, int mask_offset);
+/* luaTL's SwiGLU backward with either output optional: da = dout*b*silu'(a)
+ * (stored with lda), db = dout*silu(a) (stored with ldb).  Replaces
+ * luaTL_swiglu_bwd (cuda/luaTL_train.cu:1142-1152). */
+LHIP_API int lhip_swiglu_bwd_ex(const float* a, const float* b, const float* dout, float* da, float* db, int rows,
+                                int cols, int lda, int ldb, int ldo);
+/* out[c] = alpha * sum_r x[r*row_stride + c] + beta * out[c] (beta == 0 does
+ * not read out).  Replaces luaTL_reduce_cols (cuda/luaTL_train.cu:1203-1213). */
+LHIP_API int lhip_reduce_cols(const float* x, float* out, int rows, int cols, long long row_stride, float alpha,
+                              float beta);
+/* *acc (device float) += sum x^2.  Replaces luaTL_l2_accum (cuda/luaTL_train.cu:1215-1221). */
+LHIP_API int lhip_l2_accum(const float* x, long long n, float* acc);
+/* x *= max_norm / (sqrt(*nsq) + 1e-6) when sqrt(*nsq) > max_norm > 0 (nsq a
+ * device float), else unchanged.  Replaces luaTL_clip_by_nsq (cuda/luaTL_train.cu:1223-1231). */
+LHIP_API int lhip_clip_by_nsq(float* x, long long n, const float* nsq, float max_norm);
+/* *acc (device float) += scale * sum x.  The accumulating form of luaTL_sum_f32
+ * (cuda/luaTL_train.cu:1233-1239, kernel :969-979). */
+LHIP_API int lhip_sum_accum(const float* x, long long n, float scale, float* acc);
+/* out (cols x rows) = x (rows x cols)^T, out of place.  Replaces luaTL's
+ * transpose op (cuda/luaTL_core.cu:1036-1060). */
+LHIP_API int lhip_transpose(const float* x, float* out, int rows, int cols);
+/* out[r][c] = x[r][c] + alpha * v[c] (v NULL reads as 0).  Replaces luaTL's
+ * bcast_add (cuda/luaTL_core.cu:1018-1033). */
+LHIP_API int lhip_bcast_add(const float* x, const float* v, float* out, int rows, int cols, float alpha);
+/* luaTL's AdamW update: per-element gradient clamp to [-clip, clip] when
+ * clip > 0, m/v moments, decoupled decay, then w -= lr * m*bc1 / (sqrt(v*bc2)
+ * + eps) with bc = 1/(1 - beta^max(step,1)); w_mirror (may be NULL) gets a
+ * copy of w.  Replaces luaTL_adamw_kernel (cuda/luaTL_core.cu:1346-1380) as
+ * Program:adamw issues it (cuda/luaTL_train.cu:1427-1449).  The LMTrain
+ * step's AdamW is lhip_adamw_step, which follows optim2 instead. */
+LHIP_API int lhip_adamw_elementwise(float* w, const float* g, float* m, float* v, float* w_mirror, long long n,
+                                    int step, float lr, float beta1, float beta2, float eps, float weight_decay,
+                                    float clip);
+
 /* ---- the CPU LMTrain step, resident on the GPU ------------------------------
  * One optimizer step of LMTrain with optimizer = "sgd" over `batch` windows of
  * `seq` tokens, with the CPU path's model (ai/nn/transformer.lua:84-257:

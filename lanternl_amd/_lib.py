@@ -94,6 +94,23 @@ SIGNATURES = {
     "lhip_sum": (_i, [_p, _i, _f, _p]),
     "lhip_sgd_step": (_i, [_p, _p, _p, _ll, _p, _f, _f, _f, _f, _f, _i, _p, _p]),
     "lhip_adamw_step": (_i, [_p, _p, _p, _p, _ll, _p, _f, _f, _f, _f, _f, _f, _f, _i, _p, _p]),
+    # the luaTL operation set
+    "lhip_gemm_ex": (_i, [_p, _p, _p, _p, _p, _p, _i, _i, _i, _ll, _ll, _ll, _ll, _ll, _ll, _ll, _ll, _ll,
+                          _i, _f, _f, _f, _i, _i]),
+    "lhip_elementwise": (_i, [_p, _p, _p, _ll, _i, _f, _f]),
+    "lhip_rmsnorm_ex": (_i, [_p, _p, _p, _i, _i, _f]),
+    "lhip_rmsnorm_bwd_ex": (_i, [_p, _p, _p, _p, _p, _i, _i, _f]),
+    "lhip_row_rms": (_i, [_p, _p, _i, _i, _ll, _ll, _f]),
+    "lhip_softmax_ex": (_i, [_p, _p, _p, _i, _i, _f, _i, _i, _i]),
+    "lhip_softmax_bwd_ex": (_i, [_p, _p, _p, _i, _i, _f, _i, _i, _i]),
+    "lhip_swiglu_bwd_ex": (_i, [_p, _p, _p, _p, _p, _i, _i, _i, _i, _i]),
+    "lhip_reduce_cols": (_i, [_p, _p, _i, _i, _ll, _f, _f]),
+    "lhip_l2_accum": (_i, [_p, _ll, _p]),
+    "lhip_clip_by_nsq": (_i, [_p, _ll, _p, _f]),
+    "lhip_sum_accum": (_i, [_p, _ll, _f, _p]),
+    "lhip_transpose": (_i, [_p, _p, _i, _i]),
+    "lhip_bcast_add": (_i, [_p, _p, _p, _i, _i, _f]),
+    "lhip_adamw_elementwise": (_i, [_p, _p, _p, _p, _p, _ll, _i, _f, _f, _f, _f, _f, _f]),
 }
 
 class LmConfig(ctypes.Structure):

@@ -117,6 +117,25 @@ LHIP_API int lhip_init(int device)
         if (rc != LHIP_OK) return rc;
     }
     LHIP_CHECK_HIP(hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking), "lhip_init: hipStreamCreate");
+    {
+        hipError_t eo = hipMalloc(reinterpret_cast<void**>(&s.ones), lhip::kOnesMax * sizeof(float));
+        if (eo != hipSuccess) {
+            s.ones = nullptr;
+            (void)hipStreamDestroy(s.stream);
+            s.stream = nullptr;
+            return lhip::hip_fail(eo, "lhip_init: ones vector");
+        }
+        int rc = lhip::fill(s.ones, lhip::kOnesMax, 1.0f, s.stream);
+        if (rc == LHIP_OK && hipStreamSynchronize(s.stream) != hipSuccess)
+            rc = fail(LHIP_E_DEVICE, "lhip_init: filling the ones vector failed");
+        if (rc != LHIP_OK) {
+            (void)hipFree(s.ones);
+            s.ones = nullptr;
+            (void)hipStreamDestroy(s.stream);
+            s.stream = nullptr;
+            return rc;
+        }
+    }
     s.device = device;
     s.cu_count = p.multiProcessorCount;
     s.clock_khz = p.clockRate;
@@ -144,6 +163,7 @@ LHIP_API int lhip_shutdown(void)
     if (s.h_stage) (void)hipHostFree(s.h_stage);
     if (s.work) (void)hipFree(s.work);
     for (void* p : s.retired) (void)hipFree(p);
+    if (s.ones) (void)hipFree(s.ones);
     (void)hipStreamDestroy(s.stream);
     s = lhip::State();
     return LHIP_OK;

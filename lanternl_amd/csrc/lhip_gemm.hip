@@ -2018,7 +2018,7 @@ int noalloc_scratch_init(int device)
 // The split-K plan of an immediate product: the slice count (1 = unsplit) and
 // the partials it needs, in floats.  lhip_sgemm and lhip_sgemm_noalloc share
 // it, so both sum the same slices in the same order.
-static int immediate_plan(int transa, int transb, int m, int n, int k, int batch, size_t* need_floats)
+int immediate_plan(int transa, int transb, int m, int n, int k, int batch, size_t* need_floats)
 {
     *need_floats = 0;
     if (m <= 0 || n <= 0 || k <= 0 || batch <= 0) return 1;

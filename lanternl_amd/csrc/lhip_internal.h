@@ -43,6 +43,8 @@ struct State {
     size_t retired_bytes = 0;
     // executable programs made by lhip_program_end and not yet freed
     int live_programs = 0;
+    // kOnesMax ones (the gain of the gain-free luaTL row operations), filled at init
+    float* ones = nullptr;
     // a program (stream capture of the library stream) is being recorded
     bool recording = false;
     // accounting of lhip_malloc buffers (lhip_mem_stats)
@@ -50,7 +52,12 @@ struct State {
     unsigned long long bytes_in_use = 0, peak_in_use = 0, n_alloc = 0, n_free = 0;
 };
 
+constexpr int kOnesMax = 65536;
+
 State& st();
+
+// The device ones vector for a gain-free row operation of n columns.
+int ones_vector(int n, const float** out);
 
 // Record an error message (printf-style) and return `code`.
 int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
@@ -256,6 +263,9 @@ int sgemm_grouped_tn(const GroupedTN* g, int ngroups, int K, hipStream_t stream,
 int sgemm_run(int transa, int transb, int m, int n, int k, float alpha,
               const float* A, int lda, long long sA, const float* B, int ldb, long long sB, float beta,
               float* C, int ldc, long long sC, int batch, const GemmOpts& o, hipStream_t stream);
+// The split-K plan of an immediate product (lhip_sgemm's): slice count (1 =
+// unsplit) and, in *need_floats, the partials it needs.
+int immediate_plan(int transa, int transb, int m, int n, int k, int batch, size_t* need_floats);
 // Number of K slices sgemm_run would use (1 = none); *kchunk receives the slice length.
 int splitk_plan(int m, int n, int k, int batch, size_t ws_floats, int* kchunk, bool unreduced = false);
 int split256_plan(int m, int n, int k, int batch, size_t ws_floats, int* kchunk);

@@ -1,23 +1,39 @@
 --  luatl_adapter.lua -- lanternl's `luatl_adapter` backend, served by liblanternl_hip.so
 --  (MI355X / gfx950) through the LuaJIT FFI.
 --
---  Drop-in for ai/gpu/luatl_adapter.lua: ai/core/matrix.lua probes it by name
---  (BACKEND_NAMES, matrix.lua:25), requires `available == true` and a
---  `matmul` function (matrix.lua:28-48), and calls
---  matmul(a_flat, m, k, b_flat, n) -> new flat table (matrix.lua:178-202).
---  matmul_nt / matmul_tn serve the transposed products with the same calling
---  convention (a dispatch that matrix.lua gains with the patch shown in
---  INTEGRATION.md).  The resident-handle API below keeps the names of
---  luatl_adapter.lua:46-246 for the calls this backend implements.
+--  Drop-in for ai/gpu/luatl_adapter.lua, call for call: the same names, argument
+--  lists and return conventions.
+--    * Module contract (ai/core/matrix.lua:28-48,178-202): `available`,
+--      `reason`/`error`, and matmul(a, m, k, b, n), where a and b are flat
+--      tables or resident handles; two handles give a new handle, otherwise a
+--      NEW flat table (luatl_adapter.lua:102-135).  matmul_nt / matmul_tn serve
+--      the transposed products with the same convention (the dispatch that
+--      matrix.lua gains with the patch shown in INTEGRATION.md).
+--    * Legacy flat calls rmsnorm(x, rows, cols, w, eps), softmax(x, rows, cols),
+--      softmax_causal(x, rows, cols, scale, group) (:137-159).
+--    * Resident calls gemm(hA, hB, hC, opts), gemm_dx, gemm_dw, add_inplace,
+--      silu_inplace, gelu_inplace, scale_inplace, rope(h, o),
+--      swiglu(ha, hb, ho, o), rmsnorm_bwd(hx, hg, hdy, hdx, hdg, eps),
+--      softmax_bwd(hy, hdy, hdx, o), program(cap, timing), sync, stats,
+--      hardware, shutdown (:161-187), and the resident-tensor toolkit
+--      offset, view, cols, wrap, ids, upload_i32, download_i32, download_f32,
+--      scalar, mem (:188-246).
+--    * program(cap, timing) returns a Program with luaTL.Program's op list
+--      (ai/gpu/luaTL_train.lua:332-632): ops queue library calls; run() issues
+--      them on the library stream, capture() records them once into a hipGraph,
+--      replay() launches it.
+--  Handles and tensors carry .t.data / .data (the device address), rows and
+--  cols as the reference's do.  M.luaTL (the reference's own low-level module)
+--  has no counterpart here and stays nil.
 --
 --  Errors: every C status is checked; a failure raises
 --  "lanternl_hip[<what>]: <message> (<STATUS>)" (the reference's ck(),
 --  ai/gpu/luaTL.lua:240-246), which the registry counts (matrix.lua:169-176).
 
-local M = { name = "lanternl_hip", priority = 100, available = false, reason = "not loaded" }
+local M = { name = "luatl", priority = 100, available = false, reason = "not loaded" }
 
 local okffi, ffi = pcall(require, "ffi")
-if not okffi then M.reason = "LuaJIT FFI unavailable" return M end
+if not okffi then M.reason = "LuaJIT FFI unavailable" M.error = M.reason return M end
 
 ffi.cdef[[
 int lhip_init(int device);
@@ -29,36 +45,58 @@ int lhip_malloc(void** dptr, size_t bytes);
 int lhip_free(void* dptr);
 int lhip_upload(void* dst_device, const void* src_host, size_t bytes);
 int lhip_download(void* dst_host, const void* src_device, size_t bytes);
+int lhip_copy(void* dst_device, const void* src_device, size_t bytes);
 int lhip_zero(void* dptr, size_t bytes);
 int lhip_sync(void);
+int lhip_event_create(void** ev);
+int lhip_event_destroy(void* ev);
+int lhip_event_record(void* ev);
+int lhip_event_elapsed_ms(void* start, void* stop, float* ms);
 int lhip_sgemm(int transa, int transb, int m, int n, int k, float alpha,
                const float* A, int lda, const float* B, int ldb, float beta,
                float* C, int ldc);
 int lhip_matmul_host(int op, const double* a, const double* b, double* c,
                      int m, int k, int n, int acc);
-int lhip_rmsnorm_fwd(const float* x, const float* w, float* y, float* inv, int rows, int cols, float eps);
-int lhip_rmsnorm_bwd(const float* x, const float* w, const float* inv, const float* dy,
-                     float* dx, float* dw, int rows, int cols, int accumulate);
-int lhip_softmax_fwd(const float* x, float* y, int rows, int cols, float scale,
-                     int causal, int offset, int group);
-int lhip_softmax_bwd(const float* y, const float* dy, float* dx, int rows, int cols,
-                     float scale, int causal, int offset, int group, int accumulate);
+int lhip_gemm_ex(const float* A, const float* B, float* C, const float* bias, const float* gamma,
+                 const float* rowscale, int M, int N, int K, long long a_rs, long long a_cs,
+                 long long b_rs, long long b_cs, long long c_rs, long long c_cs, long long a_bs,
+                 long long b_bs, long long c_bs, int batch, float alpha, float beta, float eps,
+                 int pre_op, int post_op);
+int lhip_elementwise(const float* a, const float* b, float* c, long long n, int op, float alpha, float beta);
+int lhip_rmsnorm_ex(const float* x, const float* w, float* y, int rows, int cols, float eps);
+int lhip_rmsnorm_bwd_ex(const float* x, const float* w, const float* dy, float* dx, float* dw, int rows,
+                        int cols, float eps);
+int lhip_row_rms(const float* x, float* out, int rows, int cols, long long rs, long long cs, float eps);
+int lhip_softmax_ex(const float* x, const float* bias, float* y, int rows, int cols, float scale, int causal,
+                    int group, int mask_offset);
+int lhip_softmax_bwd_ex(const float* y, const float* dy, float* dx, int rows, int cols, float scale,
+                        int causal, int group, int mask_offset);
 int lhip_swiglu_fwd(const float* gate, int ld_gate, const float* up, int ld_up,
                     float* out, int ld_out, int rows, int cols);
-int lhip_swiglu_bwd(const float* gate, int ld_gate, const float* up, int ld_up,
-                    const float* dout, int ld_dout, float* dgate, int ld_dgate,
-                    float* dup, int ld_dup, int rows, int cols, int accumulate);
+int lhip_swiglu_bwd_ex(const float* a, const float* b, const float* dout, float* da, float* db, int rows,
+                       int cols, int lda, int ldb, int ldo);
 int lhip_rope(float* x, const int* pos_ids, int rows, int heads, int head_dim, int row_stride,
               int pos_offset, int pos_period, double base, int interleaved, int inverse);
 int lhip_ce_fused(const float* logits, const int* targets, float* losses, float* dlogits,
                   int rows, int vocab, int ignore_index, float grad_scale);
 int lhip_argmax_rows(const float* x, int* out, int rows, int cols);
-int lhip_add(const float* a, const float* b, float* out, long long n);
+int lhip_embed_fwd(const float* table, const int* ids, float* out, int n, int dim, int vocab);
+int lhip_embed_bwd(const float* dout, const int* ids, float* dtable, int n, int dim, int vocab,
+                   float scale, int accumulate);
+int lhip_reduce_cols(const float* x, float* out, int rows, int cols, long long row_stride, float alpha,
+                     float beta);
+int lhip_l2_accum(const float* x, long long n, float* acc);
+int lhip_clip_by_nsq(float* x, long long n, const float* nsq, float max_norm);
+int lhip_sum_accum(const float* x, long long n, float scale, float* acc);
+int lhip_transpose(const float* x, float* out, int rows, int cols);
+int lhip_bcast_add(const float* x, const float* v, float* out, int rows, int cols, float alpha);
+int lhip_adamw_elementwise(float* w, const float* g, float* m, float* v, float* w_mirror, long long n,
+                           int step, float lr, float beta1, float beta2, float eps, float weight_decay,
+                           float clip);
 int lhip_program_begin(void);
 int lhip_program_end(void** program);
 int lhip_program_replay(void* program, int times);
 int lhip_program_free(void* program);
-int lhip_silu(const float* x, float* out, long long n);
 int lhip_mem_info(unsigned long long* free_bytes, unsigned long long* total_bytes);
 typedef struct {
     unsigned long long bytes_in_use, peak_in_use, live_buffers, n_alloc, n_free,
@@ -106,7 +144,11 @@ for _, path in ipairs(candidates()) do
     if ok then C = lib break end
     load_err = tostring(lib)
 end
-if not C then M.reason = "liblanternl_hip.so not found (" .. tostring(load_err) .. ")" return M end
+if not C then
+    M.reason = "liblanternl_hip.so not found (" .. tostring(load_err) .. ")"
+    M.error = M.reason
+    return M
+end
 
 local function ck(rc, what)
     if rc ~= 0 then
@@ -117,11 +159,26 @@ local function ck(rc, what)
 end
 
 local okinit, initerr = pcall(function() ck(C.lhip_init(0), "init") end)
-if not okinit then M.reason = tostring(initerr) return M end
+if not okinit then M.reason = tostring(initerr) M.error = M.reason return M end
+
+local devinfo = ffi.new("lhip_devinfo_t")
+ck(C.lhip_device_info(devinfo), "device_info")
 
 M.available = true
 M.reason = "ready"
+M.device = ffi.string(devinfo.name)
 M.C = C
+M.luaTL = nil
+
+local F32 = 0
+M.F32 = F32
+-- luaTL.EW / act / pre codes (cuda/luaTL_core.cu:49-90) = LHIP_EW_* / LHIP_ACT_* / LHIP_PRE_*
+M.EW = { COPY = 0, ADD = 1, SUB = 2, MUL = 3, DIV = 4, SCALE = 5, AXPY = 6, FILL = 7, RELU = 8, GELU = 9,
+         SILU = 10, TANH = 11, SIGMOID = 12, EXP = 13, SQRT = 14, RSQRT = 15, NEG = 16, RECIP = 17,
+         ABS = 18, CLAMP = 19, DRELU = 20, DSILU = 21, DGELU = 22 }
+M.ACT = { NONE = 0, RELU = 1, GELU = 2, SILU = 3, TANH = 4, SIGMOID = 5 }
+M.PRE = { NONE = 0, RMSNORM = 1, GELU = 2, SILU = 3, RELU = 4 }
+local EW = M.EW
 
 local ok_tnew, tnew = pcall(require, "table.new")
 if not ok_tnew then tnew = function() return {} end end
@@ -132,37 +189,195 @@ local i32_ct = ffi.typeof("int32_t[?]")
 
 --  cached host staging (no per-call cdata churn, as luatl_adapter.lua:24-32)
 local stage, stage_n = {}, {}
-local function host_f64(slot, n)
-    if not stage[slot] or stage_n[slot] < n then
-        stage[slot] = f64_ct(n)
-        stage_n[slot] = n
+local function host_buf(ct, slot, n)
+    local key = slot .. tostring(ct)
+    if not stage[key] or stage_n[key] < n then
+        stage[key] = ct(n)
+        stage_n[key] = n
     end
-    return stage[slot]
+    return stage[key]
 end
 
-local function fill_f64(dst, src, n)
-    for i = 1, n do dst[i - 1] = src[i] end
+--  TENSORS: a device fp32 matrix { data, rows, cols, dtype, nelem, nbytes } --
+--  the role of a luaTL tensor.  Owning tensors free their memory from an FFI
+--  finaliser; wrap() makes non-owning ones.
+local Tensor = {}
+Tensor.__index = Tensor
+M.TensorClass = Tensor
+
+local function new_tensor(rows, cols)
+    local pp = ffi.new("void*[1]")
+    ck(C.lhip_malloc(pp, math.max(rows * cols, 1) * 4), "alloc")
+    local t = setmetatable({ rows = rows, cols = cols, dtype = F32, nelem = rows * cols,
+                             nbytes = rows * cols * 4 }, Tensor)
+    t.owner = ffi.gc(pp[0], function(p) C.lhip_free(p) end)
+    t.data = ffi.cast("float*", t.owner)
+    return t
 end
 
+--- Logical transpose as a stride view (luaTL_train.lua:120-122).
+function Tensor:t() return M.view(self.data, self.cols, self.rows, 1, self.cols, 0) end
+function Tensor:free()
+    if self.owner ~= nil then C.lhip_free(ffi.gc(self.owner, nil)) end
+    self.owner, self.data = nil, nil
+end
+
+--  HANDLES (luatl_adapter.lua:46-101): a persistent GPU tensor exposed to lanternl
+local Handle = {}
+Handle.__index = Handle
+M.HandleClass = Handle
+
+local function is_handle(x) return type(x) == "table" and getmetatable(x) == Handle end
+M.is_handle = is_handle
+
+local function new_handle(t, rows, cols)
+    return setmetatable({ t = t, rows = rows, cols = cols, __luatl_handle = true }, Handle)
+end
+M.new_handle = new_handle
+
+--- Upload a flat Lua array once and keep it resident (luatl_adapter.lua:63-73).
+function M.pin(flat, rows, cols)
+    local n = rows * cols
+    if #flat ~= n then
+        error(("luatl.pin: %d elements != %dx%d"):format(#flat, rows, cols), 2)
+    end
+    return new_handle(new_tensor(rows, cols), rows, cols):upload(flat)
+end
+
+--- A resident zero tensor (activations, grads, optimizer state) (:75-78).
+function M.alloc(rows, cols)
+    return new_handle(new_tensor(rows, cols), rows, cols):zero()
+end
+
+function Handle:toflat()
+    local n = self.rows * self.cols
+    local buf = host_buf(f32_ct, "dl", n)
+    ck(C.lhip_download(buf, self.t.data, n * 4), "download")
+    local out = tnew(n, 0)
+    for i = 1, n do out[i] = buf[i - 1] end
+    return out
+end
+
+function Handle:upload(flat)
+    local n = self.rows * self.cols
+    if #flat < n then error(("luatl.upload: %d elements < %dx%d"):format(#flat, self.rows, self.cols), 2) end
+    local buf = host_buf(f32_ct, "ul", n)
+    for i = 1, n do buf[i - 1] = flat[i] end
+    ck(C.lhip_upload(self.t.data, buf, n * 4), "upload")
+    return self
+end
+
+function Handle:zero() ck(C.lhip_zero(self.t.data, self.rows * self.cols * 4), "zero") return self end
+function Handle:free() if self.t then self.t:free() self.t = nil end end
+function Handle:tensor() return self.t end
+function Handle:shape() return self.rows, self.cols end
+
+--  device scratch for the flat-table calls, keyed by "slot:rows x cols" (:34-44)
+local scratch = {}
+local function dev_scratch(slot, rows, cols)
+    local key = slot .. ":" .. rows .. "x" .. cols
+    local t = scratch[key]
+    if not t then
+        t = new_tensor(rows, cols)
+        scratch[key] = t
+    end
+    return t
+end
+
+--  a handle's tensor, or a flat table uploaded to scratch (:102-114)
+local function as_tensor(x, rows, cols, slot)
+    if is_handle(x) then return x.t, true end
+    local n = rows * cols
+    if #x < n then
+        error(("luatl adapter: expected %d elements, got %d"):format(n, #x), 3)
+    end
+    local buf = host_buf(f32_ct, slot, n)
+    for i = 1, n do buf[i - 1] = x[i] end
+    local t = dev_scratch(slot, rows, cols)
+    ck(C.lhip_upload(t.data, buf, n * 4), "upload")
+    return t, false
+end
+
+--  a new handle over t, or a new flat table read back from it (:116-124)
+local function emit(t, rows, cols, resident)
+    if resident then return new_handle(t, rows, cols) end
+    local n = rows * cols
+    local buf = host_buf(f32_ct, "out", n)
+    ck(C.lhip_download(buf, t.data, n * 4), "download")
+    local out = tnew(n, 0)
+    for i = 1, n do out[i] = buf[i - 1] end
+    return out
+end
+
+--  the flat-table product through lhip_matmul_host (double in and out)
 local function host_gemm(op, a, m, k, b, n, na, nb, nc, what)
     if #a < na then error(("lanternl_hip: %s: a has %d elements, expected %d"):format(what, #a, na), 3) end
     if #b < nb then error(("lanternl_hip: %s: b has %d elements, expected %d"):format(what, #b, nb), 3) end
-    local A = host_f64("a", na)
-    local B = host_f64("b", nb)
-    local Cb = host_f64("c", nc)
-    fill_f64(A, a, na)
-    fill_f64(B, b, nb)
+    local A = host_buf(f64_ct, "a", na)
+    local B = host_buf(f64_ct, "b", nb)
+    local Cb = host_buf(f64_ct, "c", nc)
+    for i = 1, na do A[i - 1] = a[i] end
+    for i = 1, nb do B[i - 1] = b[i] end
     ck(C.lhip_matmul_host(op, A, B, Cb, m, k, n, 0), what)
     local out = tnew(nc, 0)
     for i = 1, nc do out[i] = Cb[i - 1] end
     return out
 end
 
---  LEGACY-COMPATIBLE ENTRY POINTS (matrix.lua's backend contract)
+--  STRIDE VIEWS AND gemm_ex (luaTL_train.lua:113-172)
+--- Explicit stride view: rs = row stride, cs = column stride, bs = batch stride (elements) (:200-203).
+function M.view(ptr, rows, cols, rs, cs, bs)
+    if type(ptr) == "table" then ptr = is_handle(ptr) and ptr.t.data or ptr.data end
+    return { data = ffi.cast("float*", ptr), rows = rows, cols = cols, rs = rs, cs = cs, bs = bs or 0,
+             dtype = F32, nelem = rows * cols }
+end
 
---  a(m x k) . b(k x n) -> new flat table of m*n numbers (luatl_adapter.lua:128-135)
+local function coerce(x)
+    if is_handle(x) then x = x.t end
+    if x.rs then return x end
+    return { data = x.data, rows = x.rows, cols = x.cols, rs = x.cols, cs = 1, bs = 0, dtype = F32 }
+end
+
+local function dptr(x)
+    if x == nil then return nil end
+    if is_handle(x) then return x.t.data end
+    if type(x) == "table" then return x.data end
+    return x
+end
+
+--- Cc = act(alpha * pre(A) @ B + bias) + beta*Cc on tensors, handles or stride views
+--- (luaTL.gemm_ex, luaTL_train.lua:154-172); opts alpha, beta, bias, gamma, rowscale,
+--- batch, eps, pre, act.
+function M.gemm_ex(A, B, Cc, o)
+    o = o or {}
+    local a, b, c = coerce(A), coerce(B), coerce(Cc)
+    if b.rows ~= a.cols then
+        error(("gemm_ex: inner dim mismatch %dx%d @ %dx%d"):format(a.rows, a.cols, b.rows, b.cols), 2)
+    end
+    ck(C.lhip_gemm_ex(a.data, b.data, c.data, dptr(o.bias), dptr(o.gamma), dptr(o.rowscale),
+                      a.rows, b.cols, a.cols, a.rs, a.cs, b.rs, b.cs, c.rs, c.cs, a.bs, b.bs, c.bs,
+                      o.batch or 1, o.alpha or 1.0, o.beta or 0.0, o.eps or 1e-5, o.pre or 0, o.act or 0),
+       "gemm_ex")
+    return Cc
+end
+
+local function tview(x)
+    if is_handle(x) then x = x.t end
+    return M.view(x.data, x.cols, x.rows, 1, x.cols, 0)
+end
+
+--  LEGACY-COMPATIBLE ENTRY POINTS (signatures unchanged, luatl_adapter.lua:126-159)
+
 function M.matmul(a, m, k, b, n)
-    return host_gemm(0, a, m, k, b, n, m * k, k * n, m * n, "matmul")
+    if not is_handle(a) and not is_handle(b) then
+        return host_gemm(0, a, m, k, b, n, m * k, k * n, m * n, "matmul")
+    end
+    local A, ah = as_tensor(a, m, k, "A")
+    local B, bh = as_tensor(b, k, n, "B")
+    local resident = ah and bh
+    local Cc = resident and new_tensor(m, n) or dev_scratch("C", m, n)
+    M.gemm_ex(A, B, Cc)
+    return emit(Cc, m, n, resident)
 end
 
 --  a(m x k) . b(n x k)^T -> m*n numbers (matrix.matmul_nt, matrix.lua:597-625)
@@ -175,191 +390,109 @@ function M.matmul_tn(a, m, k, b, n)
     return host_gemm(2, a, m, k, b, n, m * k, m * n, k * n, "matmul_tn")
 end
 
---  RESIDENT HANDLES (luatl_adapter.lua:46-101): a device fp32 matrix with a
---  finaliser; flat Lua tables cross the boundary only on pin/upload/toflat.
-local Handle = {}
-Handle.__index = Handle
-M.HandleClass = Handle
-
-local function is_handle(x) return type(x) == "table" and getmetatable(x) == Handle end
-M.is_handle = is_handle
-
-local function dev_alloc(bytes)
-    local pp = ffi.new("void*[1]")
-    ck(C.lhip_malloc(pp, bytes), "alloc")
-    return ffi.gc(pp[0], function(p) C.lhip_free(p) end)
+function M.rmsnorm(x, rows, cols, w, eps)
+    local X, xh = as_tensor(x, rows, cols, "A")
+    local W = nil
+    if w then W = (as_tensor(w, 1, cols, "B")) end
+    local O = xh and new_tensor(rows, cols) or dev_scratch("C", rows, cols)
+    ck(C.lhip_rmsnorm_ex(X.data, W and W.data or nil, O.data, rows, cols, eps or 1e-5), "rmsnorm")
+    return emit(O, rows, cols, xh)
 end
 
-local function new_handle(rows, cols)
-    local h = setmetatable({ rows = rows, cols = cols }, Handle)
-    h.ptr = dev_alloc(math.max(rows * cols, 1) * 4)
-    return h
+function M.softmax(x, rows, cols)
+    local X, xh = as_tensor(x, rows, cols, "A")
+    local O = xh and new_tensor(rows, cols) or dev_scratch("C", rows, cols)
+    ck(C.lhip_softmax_ex(X.data, nil, O.data, rows, cols, 1.0, 0, 0, 0), "softmax")
+    return emit(O, rows, cols, xh)
 end
 
-function M.alloc(rows, cols)
-    local h = new_handle(rows, cols)
-    ck(C.lhip_zero(h.ptr, math.max(rows * cols, 1) * 4), "zero")
-    return h
+function M.softmax_causal(x, rows, cols, scale, group)
+    local X, xh = as_tensor(x, rows, cols, "A")
+    local O = xh and new_tensor(rows, cols) or dev_scratch("C", rows, cols)
+    ck(C.lhip_softmax_ex(X.data, nil, O.data, rows, cols, scale or 1.0, 1, group or 0, 0), "softmax_causal")
+    return emit(O, rows, cols, xh)
 end
 
-function M.pin(flat, rows, cols)
-    local h = new_handle(rows, cols)
-    h:upload(flat)
-    return h
+--  RESIDENT-MODE PRIMITIVES (luatl_adapter.lua:161-187)
+
+function M.gemm(hA, hB, hC, opts) M.gemm_ex(hA.t, hB.t, hC.t, opts) return hC end
+--- dX = dY . W^T + beta*dX (luaTL.matmul_dx, luaTL_train.lua:174-177)
+function M.gemm_dx(hdY, hW, hdX, beta) M.gemm_ex(hdY.t, tview(hW), hdX.t, { beta = beta or 0.0 }) return hdX end
+--- dW = X^T . dY + beta*dW, beta defaulting to 1 (luaTL.matmul_dw, luaTL_train.lua:179-182)
+function M.gemm_dw(hX, hdY, hdW, beta)
+    M.gemm_ex(tview(hX), hdY.t, hdW.t, { beta = beta == nil and 1.0 or beta })
+    return hdW
 end
 
-function Handle:upload(flat)
-    local n = self.rows * self.cols
-    if #flat < n then error(("lanternl_hip.upload: %d elements < %dx%d"):format(#flat, self.rows, self.cols), 2) end
-    local buf = f32_ct(n)
-    for i = 1, n do buf[i - 1] = flat[i] end
-    ck(C.lhip_upload(self.ptr, buf, n * 4), "upload")
-    return self
+--- Tensor:add_inplace (luaTL.lua:633-638): the AXPY operator with a = dst,
+--- b = src, i.e. dst = alpha*dst + src.
+function M.add_inplace(hDst, hSrc, alpha)
+    ck(C.lhip_elementwise(hDst.t.data, hSrc.t.data, hDst.t.data, hDst.t.nelem, EW.AXPY, alpha or 1.0, 0.0),
+       "add_inplace")
+    return hDst
 end
-
-function Handle:toflat()
-    local n = self.rows * self.cols
-    local buf = f32_ct(n)
-    ck(C.lhip_download(buf, self.ptr, n * 4), "download")
-    local out = tnew(n, 0)
-    for i = 1, n do out[i] = buf[i - 1] end
-    return out
-end
-
-function Handle:zero() ck(C.lhip_zero(self.ptr, self.rows * self.cols * 4), "zero") return self end
-function Handle:free()
-    if self.ptr and self.owned ~= false then C.lhip_free(ffi.gc(self.ptr, nil)) end
-    self.ptr = nil
-end
-function Handle:shape() return self.rows, self.cols end
-
-local function fp(h) return ffi.cast("float*", h.ptr) end
-
---  C = A . B (+ beta C); gemm_dx: dY . W^T; gemm_dw: X^T . dY (+= with beta = 1),
---  the three products of luatl_adapter.lua:163-165 / luaTL_train.lua:154-182.
-function M.gemm(A, B, Cm, beta)
-    Cm = Cm or M.alloc(A.rows, B.cols)
-    ck(C.lhip_sgemm(0, 0, A.rows, B.cols, A.cols, 1.0, fp(A), A.cols, fp(B), B.cols, beta or 0.0,
-                    fp(Cm), Cm.cols), "gemm")
-    return Cm
-end
-
-function M.gemm_dx(dY, W, dX, beta)
-    dX = dX or M.alloc(dY.rows, W.rows)
-    ck(C.lhip_sgemm(0, 1, dY.rows, W.rows, dY.cols, 1.0, fp(dY), dY.cols, fp(W), W.cols, beta or 0.0,
-                    fp(dX), dX.cols), "gemm_dx")
-    return dX
-end
-
-function M.gemm_dw(X, dY, dW, beta)
-    dW = dW or M.alloc(X.cols, dY.cols)
-    ck(C.lhip_sgemm(1, 0, X.cols, dY.cols, X.rows, 1.0, fp(X), X.cols, fp(dY), dY.cols, beta or 1.0,
-                    fp(dW), dW.cols), "gemm_dw")
-    return dW
-end
-
-function M.rmsnorm(X, W, eps, Y, inv)
-    Y = Y or M.alloc(X.rows, X.cols)
-    inv = inv or M.alloc(X.rows, 1)
-    ck(C.lhip_rmsnorm_fwd(fp(X), fp(W), fp(Y), fp(inv), X.rows, X.cols, eps or 1e-5), "rmsnorm")
-    return Y, inv
-end
-
-function M.rmsnorm_bwd(X, W, inv, dY, dX, dW, accumulate)
-    dX = dX or M.alloc(X.rows, X.cols)
-    ck(C.lhip_rmsnorm_bwd(fp(X), fp(W), fp(inv), fp(dY), fp(dX), dW and fp(dW) or nil, X.rows, X.cols,
-                          accumulate and 1 or 0), "rmsnorm_bwd")
-    return dX, dW
-end
-
-function M.softmax(X, Y, scale)
-    Y = Y or M.alloc(X.rows, X.cols)
-    ck(C.lhip_softmax_fwd(fp(X), fp(Y), X.rows, X.cols, scale or 1.0, 0, 0, 0), "softmax")
-    return Y
-end
-
-function M.softmax_causal(X, Y, scale, offset, group)
-    Y = Y or M.alloc(X.rows, X.cols)
-    ck(C.lhip_softmax_fwd(fp(X), fp(Y), X.rows, X.cols, scale or 1.0, 1, offset or 0, group or 0),
-       "softmax_causal")
-    return Y
-end
-
-function M.softmax_bwd(Y, dY, dX, scale, causal, offset, group)
-    dX = dX or M.alloc(Y.rows, Y.cols)
-    ck(C.lhip_softmax_bwd(fp(Y), fp(dY), fp(dX), Y.rows, Y.cols, scale or 1.0, causal and 1 or 0,
-                          offset or 0, group or 0, 0), "softmax_bwd")
-    return dX
-end
-
-function M.swiglu(G, U, H)
-    H = H or M.alloc(G.rows, G.cols)
-    ck(C.lhip_swiglu_fwd(fp(G), G.cols, fp(U), U.cols, fp(H), H.cols, G.rows, G.cols), "swiglu")
-    return H
-end
-
---  in place; interleaved pairs (the CPU path's) unless opts.half_split
-function M.rope(X, heads, head_dim, opts)
-    opts = opts or {}
-    ck(C.lhip_rope(fp(X), nil, X.rows, heads, head_dim, X.cols, opts.pos_offset or 0, opts.period or 0,
-                   opts.base or 10000.0, opts.half_split and 0 or 1, opts.inverse and 1 or 0), "rope")
-    return X
-end
-
---  per-row CE losses and dlogits (written over the logits when dlogits == nil)
-function M.cross_entropy(logits, targets0, grad_scale)
-    local n = logits.rows
-    local tg = i32_ct(n)
-    for i = 1, n do tg[i - 1] = targets0[i] end
-    local dtg = dev_alloc(n * 4)
-    ck(C.lhip_upload(dtg, tg, n * 4), "cross_entropy: targets")
-    local losses = M.alloc(n, 1)
-    ck(C.lhip_ce_fused(fp(logits), ffi.cast("int*", dtg), fp(losses), fp(logits), n, logits.cols, -1,
-                       grad_scale or 1.0), "cross_entropy")
-    local l = losses:toflat()
-    local s = 0
-    for i = 1, n do s = s + l[i] end
-    return s / n
-end
-
-function M.add_inplace(A, B)
-    ck(C.lhip_add(fp(A), fp(B), fp(A), A.rows * A.cols), "add_inplace")
-    return A
-end
-
 function M.silu_inplace(h)
-    ck(C.lhip_silu(fp(h), fp(h), h.rows * h.cols), "silu_inplace")
+    ck(C.lhip_elementwise(h.t.data, nil, h.t.data, h.t.nelem, EW.SILU, 0.0, 0.0), "silu_inplace")
     return h
 end
+function M.gelu_inplace(h)
+    ck(C.lhip_elementwise(h.t.data, nil, h.t.data, h.t.nelem, EW.GELU, 0.0, 0.0), "gelu_inplace")
+    return h
+end
+function M.scale_inplace(h, a)
+    ck(C.lhip_elementwise(h.t.data, nil, h.t.data, h.t.nelem, EW.SCALE, a, 0.0), "scale_inplace")
+    return h
+end
+
+--  Tensor:rope (luaTL_train.lua:225-234): in place, half-split pairs unless o.interleaved
+local function rope_call(x, o)
+    o = o or {}
+    local heads = o.heads or 1
+    local hd = o.head_dim or (x.cols / heads)
+    local rs = o.row_stride or x.cols
+    ck(C.lhip_rope(x.data, o.pos_ids and ffi.cast("int*", dptr(o.pos_ids)) or nil, x.rows, heads, hd,
+                   rs > 0 and rs or heads * hd, o.pos_offset or 0, 0, o.theta or 10000.0,
+                   o.interleaved and 1 or 0, o.inverse and 1 or 0), "rope")
+end
+function M.rope(h, o) rope_call(h.t, o) return h end
+
+--  luaTL.swiglu (luaTL_train.lua:209-215): out = silu(a) * b
+local function swiglu_call(a, b, out, o)
+    o = o or {}
+    ck(C.lhip_swiglu_fwd(a.data, o.lda or a.cols, b.data, o.ldb or b.cols, out.data, o.ldo or out.cols,
+                         out.rows, out.cols), "swiglu")
+end
+function M.swiglu(ha, hb, ho, o) swiglu_call(ha.t, hb.t, ho.t, o) return ho end
+
+function M.rmsnorm_bwd(hx, hg, hdy, hdx, hdg, eps)
+    local x = hx.t
+    ck(C.lhip_rmsnorm_bwd_ex(x.data, hg and hg.t.data or nil, hdy.t.data, hdx.t.data,
+                             hdg and hdg.t.data or nil, x.rows, x.cols, eps or 1e-5), "rmsnorm_bwd")
+    return hdx
+end
+
+local function softmax_bwd_call(y, dy, dx, o)
+    o = o or {}
+    ck(C.lhip_softmax_bwd_ex(y.data, dy.data, dx.data, y.rows, y.cols, o.scale or 1.0, o.causal and 1 or 0,
+                             o.group or 0, o.mask_offset or 0), "softmax_bwd")
+end
+function M.softmax_bwd(hy, hdy, hdx, o) softmax_bwd_call(hy.t, hdy.t, hdx.t, o) return hdx end
 
 function M.sync() ck(C.lhip_sync(), "sync") end
 
---  Memory and device queries (luatl_adapter.lua:184-185,243-246).  There is
---  no caching pool: stats() reports the library's own accounting of the
---  buffers it allocated (lhip_mem_stats), under the reference's key names
---  where they mean the same thing.
+--- Memory statistics under the reference pool's keys (luaTL.pool_stats, luaTL.lua:308-325).
+--- There is no caching pool: every allocation is a hipMalloc.
 local mstats = ffi.new("lhip_mem_stats_t")
 function M.stats()
     ck(C.lhip_mem_stats(mstats), "stats")
     local s = mstats
     return {
-        in_use = tonumber(s.bytes_in_use), peak = tonumber(s.peak_in_use),
-        blocks = tonumber(s.live_buffers), allocs = tonumber(s.n_alloc), frees = tonumber(s.n_free),
-        workspace = tonumber(s.workspace_bytes), staging = tonumber(s.staging_bytes),
         reserved = tonumber(s.bytes_in_use + s.workspace_bytes + s.staging_bytes),
-    }
-end
-
-local devinfo = ffi.new("lhip_devinfo_t")
-function M.hardware()
-    ck(C.lhip_device_info(devinfo), "hardware")
-    local d = devinfo
-    return {
-        name = ffi.string(d.name), arch = ffi.string(d.arch), device = d.device,
-        sm_count = d.compute_units, compute_units = d.compute_units, clock_mhz = d.clock_khz / 1000,
-        warp_size = d.wavefront_size, total_mem = tonumber(d.total_mem),
-        smem_per_block = tonumber(d.lds_per_block), l2_bytes = d.l2_bytes,
-        gflops_fp32_matrix = d.peak_fp32_matrix_tflops * 1000, hbm_gbps = d.peak_hbm_gbps,
+        in_use = tonumber(s.bytes_in_use), peak = tonumber(s.peak_in_use), blocks = tonumber(s.live_buffers),
+        free_blocks = 0, allocs = tonumber(s.n_alloc), frees = tonumber(s.n_free),
+        cuda_malloc = tonumber(s.n_alloc), cuda_free = tonumber(s.n_free), cache_hit = 0,
+        cache_miss = tonumber(s.n_alloc), trims = 0,
+        workspace = tonumber(s.workspace_bytes), staging = tonumber(s.staging_bytes),
     }
 end
 
@@ -369,95 +502,317 @@ function M.mem()
     return tonumber(u64a[0]), tonumber(u64b[0])
 end
 
---  Resident-tensor toolkit (luatl_adapter.lua:188-241): allocation-free views
---  over device memory.  A view is { ptr, rows, cols, rs, cs, bs } in
---  elements; wrap() makes a non-owning Handle over a raw device pointer.
-local function base_ptr(t)
-    if is_handle(t) or (type(t) == "table" and t.ptr ~= nil) then return t.ptr end
-    return t
+--- Device description under the reference's keys (luaTL.hardware, luaTL.lua:279-305).
+function M.hardware()
+    ck(C.lhip_device_info(devinfo), "hardware")
+    local d = devinfo
+    local free, total = M.mem()
+    local cus = d.compute_units
+    return {
+        name = ffi.string(d.name), sm = ffi.string(d.arch):match("^[^:]*"), major = 9, minor = 5,
+        multiprocessors = cus, cores_per_sm = 64, cuda_cores = 64 * cus, warp_size = d.wavefront_size,
+        max_threads_block = 1024, max_threads_sm = 2048, shared_per_block = tonumber(d.lds_per_block),
+        shared_per_sm = 160 * 1024, total_vram = total, free_vram = free, l2_cache = d.l2_bytes,
+        bandwidth_gbs = d.peak_hbm_gbps, gflops_fp32 = d.peak_fp32_matrix_tflops * 1000,
+        gflops_fp16 = 0, tensor_cores = true, fp16 = false, bf16 = false,
+    }
 end
 
---- Element-offset pointer into a handle's (or view's) float32 storage.
+--  RESIDENT TENSOR TOOLKIT (luatl_adapter.lua:188-246)
+
+--- Element-offset pointer into a tensor's (or handle's, or view's) f32 storage.
 function M.offset(t, elems)
-    return ffi.cast("char*", base_ptr(t)) + elems * 4
+    return ffi.cast("char*", dptr(t)) + elems * 4
 end
 
---- Explicit stride view: rs = row stride, cs = column stride, bs = batch stride (elements).
-function M.view(ptr, rows, cols, rs, cs, bs)
-    return { ptr = ptr, rows = rows, cols = cols, rs = rs, cs = cs, bs = bs or 0 }
-end
-
---- Column slice [col0, col0 + w) of a handle, keeping the parent's leading dimension.
+--- Column slice [col0, col0 + w) keeping the parent's leading dimension.
 function M.cols(t, col0, w)
+    if is_handle(t) then t = t.t end
     return M.view(M.offset(t, col0), t.rows, w, t.cols, 1, 0)
 end
 
---- Non-owning handle over a raw device pointer (free() leaves the memory alone).
+--- Non-owning tensor over a raw device pointer.
 function M.wrap(ptr, rows, cols)
-    return setmetatable({ rows = rows, cols = cols, ptr = ffi.cast("void*", ptr), owned = false }, Handle)
+    return setmetatable({ data = ffi.cast("float*", ptr), rows = rows, cols = cols, dtype = F32,
+                          nelem = rows * cols, nbytes = rows * cols * 4 }, Tensor)
 end
 
---- int32 index buffer (4 bytes per entry, as float32).
+--- int32 index buffer backed by f32-sized storage (4 bytes either way).
 function M.ids(n)
     local h = M.alloc(n, 1)
     h.is_ids = true
     return h
 end
 
-function M.upload_i32(t, cbuf, n)
-    ck(C.lhip_upload(base_ptr(t), cbuf, n * 4), "upload_i32")
-end
+function M.upload_i32(t, cbuf, n) ck(C.lhip_upload(dptr(t), cbuf, n * 4), "adapter.upload_i32") end
+function M.download_i32(t, cbuf, n) ck(C.lhip_download(cbuf, dptr(t), n * 4), "adapter.download_i32") end
+function M.download_f32(ptr, cbuf, n) ck(C.lhip_download(cbuf, dptr(ptr), n * 4), "adapter.download_f32") end
 
-function M.download_i32(t, cbuf, n)
-    ck(C.lhip_download(cbuf, base_ptr(t), n * 4), "download_i32")
-end
-
-function M.download_f32(ptr, cbuf, n)
-    ck(C.lhip_download(cbuf, base_ptr(ptr), n * 4), "download_f32")
-end
-
---- One float read back from device memory (the loss, the gradient norm).
+--- One float read back from a device tensor (the loss / grad norm).
 local one = ffi.new("float[1]")
 function M.scalar(t)
-    ck(C.lhip_download(one, base_ptr(t), 4), "scalar")
+    ck(C.lhip_download(one, dptr(t), 4), "adapter.scalar")
     return one[0]
 end
 
--- Program (luaTL.Program capture/replay, ai/gpu/luaTL_train.lua:327-627):
--- fn() issues adapter calls, which are recorded rather than run; the result
--- replays them as one graph launch.  Calls that synchronise or allocate fail
--- while recording, so run fn() once eagerly first.
-local Program = {}
-Program.__index = Program
+--  PROGRAM: luaTL.Program's op list (ai/gpu/luaTL_train.lua:332-632) over this
+--  library.  Each op method queues one library call; run(keep) issues the
+--  queue on the library stream (then, unless async(true), waits and, with
+--  timing, reads the elapsed time) and clears it unless keep; capture()
+--  records the queue once into a hipGraph (run it first: a recording cannot
+--  allocate); replay() launches the graph, or runs the queue when nothing is
+--  captured.  barrier() waits for the stream when run and is skipped in a
+--  capture, as luaTL_prog_capture skips SYNC ops (luaTL_train.cu:1614-1660).
+local Prog = {}
+Prog.__index = Prog
+M.ProgramClass = Prog
 
-function M.program(fn)
-    ck(C.lhip_program_begin(), "program")
-    local ok, err = pcall(fn)
-    if not ok then
-        C.lhip_program_end(nil)             -- discard the partial recording
-        error(err, 2)
-    end
-    local h = ffi.new("void*[1]")
-    ck(C.lhip_program_end(h), "program")
-    return setmetatable({ h = ffi.gc(h[0], C.lhip_program_free) }, Program)
+local function new_event()
+    local pp = ffi.new("void*[1]")
+    ck(C.lhip_event_create(pp), "event")
+    return ffi.gc(pp[0], C.lhip_event_destroy)
 end
 
-function Program:replay(times)
-    ck(C.lhip_program_replay(self.h, times or 1), "program.replay")
+function M.program(cap, timing)
+    local p = setmetatable({ ops = {}, capacity = (cap and cap > 0) and cap or 4096, timing = timing and true,
+                             flags = 1, last_ms = -1.0, total_runs = 0 }, Prog)
+    if p.timing then p.ev0, p.ev1 = new_event(), new_event() end
+    return p
+end
+
+function Prog:reset() self.ops = {} return self end
+function Prog:size() return #self.ops end
+function Prog:async(on) self.flags = on and 0 or 1 return self end
+
+function Prog:push(fn, is_sync)
+    local n = #self.ops
+    if n >= self.capacity then error("luaTL.Program full (" .. self.capacity .. ")", 3) end
+    self.ops[n + 1] = { fn = fn, sync = is_sync }
     return self
 end
 
-function Program:free()
-    if self.h ~= nil then
-        C.lhip_program_free(ffi.gc(self.h, nil))
-        self.h = nil
+function Prog:gemm(A, B, Cc, o) return self:push(function() M.gemm_ex(A, B, Cc, o) end) end
+function Prog:matmul(A, B, Cc, o) return self:gemm(A, B, Cc, o) end
+function Prog:dx(dY, W, dX, beta) return self:gemm(dY, tview(W), dX, { beta = beta or 0.0 }) end
+function Prog:dw(X, dY, dW, beta) return self:gemm(tview(X), dY, dW, { beta = beta == nil and 1.0 or beta }) end
+
+function Prog:ew(op, A, B, out, alpha, beta)
+    return self:push(function()
+        ck(C.lhip_elementwise(dptr(A), dptr(B), dptr(out), out.nelem or out.rows * out.cols, op, alpha or 1.0,
+                              beta or 0.0), "prog.ew")
+    end)
+end
+function Prog:add(A, B, out) return self:ew(EW.ADD, A, B, out, 1, 1) end
+function Prog:axpy(dst, B, a) return self:ew(EW.AXPY, dst, B, dst, a or 1, 0) end
+function Prog:scale(dst, a) return self:ew(EW.SCALE, dst, nil, dst, a, 0) end
+function Prog:dsilu(x, dy, out) return self:ew(EW.DSILU, x, dy, out, 1, 0) end
+function Prog:dgelu(x, dy, out) return self:ew(EW.DGELU, x, dy, out, 1, 0) end
+
+function Prog:rmsnorm(x, w, out, eps)
+    return self:push(function()
+        ck(C.lhip_rmsnorm_ex(x.data, dptr(w), out.data, x.rows, x.cols, eps or 1e-5), "prog.rmsnorm")
+    end)
+end
+
+function Prog:rmsnorm_bwd(x, gamma, dy, dx, dgamma, eps)
+    return self:push(function()
+        ck(C.lhip_rmsnorm_bwd_ex(x.data, dptr(gamma), dy.data, dx.data, dptr(dgamma), x.rows, x.cols, eps or 1e-5),
+           "prog.rmsnorm_bwd")
+    end)
+end
+
+function Prog:softmax(x, out, o)
+    o = o or {}
+    return self:push(function()
+        ck(C.lhip_softmax_ex(x.data, dptr(o.bias), out.data, x.rows, x.cols, o.scale or 1.0, o.causal and 1 or 0,
+                             o.group or 0, o.mask_offset or 0), "prog.softmax")
+    end)
+end
+
+function Prog:softmax_bwd(y, dy, dx, o) return self:push(function() softmax_bwd_call(y, dy, dx, o) end) end
+function Prog:swiglu(a, b, out, o) return self:push(function() swiglu_call(a, b, out, o) end) end
+
+function Prog:swiglu_bwd(a, b, dout, da, db, o)
+    o = o or {}
+    return self:push(function()
+        ck(C.lhip_swiglu_bwd_ex(a.data, b.data, dout.data, dptr(da), dptr(db), dout.rows, dout.cols,
+                                o.lda or a.cols, o.ldb or b.cols, o.ldo or dout.cols), "prog.swiglu_bwd")
+    end)
+end
+
+function Prog:rope(x, o) return self:push(function() rope_call(x, o) end) end
+
+function Prog:embed(ids, tbl, out)
+    return self:push(function()
+        ck(C.lhip_embed_fwd(tbl.data, ffi.cast("int*", dptr(ids)), out.data, out.rows, out.cols, tbl.rows),
+           "prog.embed")
+    end)
+end
+
+function Prog:embed_bwd(ids, dout, dtable, scale)
+    return self:push(function()
+        ck(C.lhip_embed_bwd(dout.data, ffi.cast("int*", dptr(ids)), dtable.data, dout.rows, dout.cols,
+                            dtable.rows, scale or 1.0, 1), "prog.embed_bwd")
+    end)
+end
+
+function Prog:cross_entropy(logits, targets, losses, dlogits, o)
+    o = o or {}
+    return self:push(function()
+        ck(C.lhip_ce_fused(logits.data, ffi.cast("int*", dptr(targets)), dptr(losses), dptr(dlogits), logits.rows,
+                           logits.cols, o.ignore_index or -1, o.grad_scale or (1.0 / logits.rows)),
+           "prog.cross_entropy")
+    end)
+end
+
+function Prog:reduce_cols(x, out, alpha, beta, rs)
+    return self:push(function()
+        ck(C.lhip_reduce_cols(x.data, dptr(out), x.rows, x.cols, rs or x.cols, alpha or 1.0, beta or 0.0),
+           "prog.reduce_cols")
+    end)
+end
+
+function Prog:l2(x, acc)
+    return self:push(function() ck(C.lhip_l2_accum(x.data, x.nelem, dptr(acc)), "prog.l2") end)
+end
+
+function Prog:clip(x, nsq, max_norm)
+    return self:push(function() ck(C.lhip_clip_by_nsq(x.data, x.nelem, dptr(nsq), max_norm), "prog.clip") end)
+end
+
+function Prog:adamw(w, g, m, v, w_lp, o)
+    o = o or {}
+    return self:push(function()
+        ck(C.lhip_adamw_elementwise(w.data, g.data, m.data, v.data, dptr(w_lp), w.nelem, o.step or 1,
+                                    o.lr or 1e-3, o.beta1 or 0.9, o.beta2 or 0.999, o.eps or 1e-8, o.wd or 0.0,
+                                    o.clip or 0.0), "prog.adamw")
+    end)
+end
+
+function Prog:zero(t) return self:push(function() ck(C.lhip_zero(t.data, t.nbytes), "prog.zero") end) end
+function Prog:copy(src, dst)
+    return self:push(function() ck(C.lhip_copy(dst.data, src.data, src.nbytes), "prog.copy") end)
+end
+function Prog:cast(src, dst)
+    if (src.dtype or F32) ~= F32 or (dst.dtype or F32) ~= F32 then
+        error("luaTL.Program:cast: this build holds fp32 only", 2)
     end
+    return self:copy(src, dst)
+end
+
+function Prog:transpose(x, out)
+    return self:push(function() ck(C.lhip_transpose(x.data, out.data, x.rows, x.cols), "prog.transpose") end)
+end
+
+function Prog:bcast_add(x, vec, out, alpha)
+    return self:push(function()
+        ck(C.lhip_bcast_add(x.data, dptr(vec), out.data, x.rows, x.cols, alpha or 1.0), "prog.bcast_add")
+    end)
+end
+
+function Prog:barrier() return self:push(function() ck(C.lhip_sync(), "prog.barrier") end, true) end
+
+function Prog:argmax(x, out)
+    return self:push(function()
+        ck(C.lhip_argmax_rows(x.data, ffi.cast("int*", dptr(out)), x.rows, x.cols), "prog.argmax")
+    end)
+end
+
+function Prog:sum(x, acc, scale)
+    return self:push(function() ck(C.lhip_sum_accum(x.data, x.nelem, scale or 1.0, dptr(acc)), "prog.sum") end)
+end
+
+function Prog:gather(src, idx, dst)
+    return self:push(function()
+        ck(C.lhip_embed_fwd(src.data, ffi.cast("int*", dptr(idx)), dst.data, dst.rows, dst.cols, src.rows),
+           "prog.gather")
+    end)
+end
+
+function Prog:row_rms(x, out, eps, rs, cs)
+    return self:push(function()
+        ck(C.lhip_row_rms(x.data, dptr(out), x.rows, x.cols, rs or x.cols, cs or 1, eps or 1e-5), "prog.row_rms")
+    end)
+end
+
+local ms_buf = ffi.new("float[1]")
+function Prog:finish()
+    if self.flags == 1 then
+        if self.ev1 then
+            ck(C.lhip_event_elapsed_ms(self.ev0, self.ev1, ms_buf), "prog.elapsed")
+            self.last_ms = ms_buf[0]
+        else
+            ck(C.lhip_sync(), "prog.sync")
+        end
+    end
+    self.total_runs = self.total_runs + 1
+end
+
+function Prog:run(keep)
+    if #self.ops == 0 then return self end
+    if self.ev0 then ck(C.lhip_event_record(self.ev0), "prog.event") end
+    for i = 1, #self.ops do self.ops[i].fn() end
+    if self.ev1 then ck(C.lhip_event_record(self.ev1), "prog.event") end
+    self:finish()
+    if not keep then self.ops = {} end
+    return self
+end
+
+--- Record the current op list as a hipGraph (barriers skipped).  Run it once first.
+function Prog:capture()
+    if #self.ops == 0 then error("Program:capture: the op list is empty (ARG)", 2) end
+    self:free_graph()
+    ck(C.lhip_sync(), "prog.capture")
+    ck(C.lhip_program_begin(), "prog.capture")
+    local ok, err = pcall(function()
+        for i = 1, #self.ops do
+            if not self.ops[i].sync then self.ops[i].fn() end
+        end
+    end)
+    if not ok then
+        C.lhip_program_end(nil)              -- discard the partial recording
+        error(err, 2)
+    end
+    local h = ffi.new("void*[1]")
+    ck(C.lhip_program_end(h), "prog.capture")
+    self.graph = ffi.gc(h[0], C.lhip_program_free)
+    return self
+end
+
+function Prog:replay()
+    if not self.graph then return self:run(true) end
+    if self.ev0 then ck(C.lhip_event_record(self.ev0), "prog.event") end
+    ck(C.lhip_program_replay(self.graph, 1), "prog.replay")
+    if self.ev1 then ck(C.lhip_event_record(self.ev1), "prog.event") end
+    self:finish()
+    return self
+end
+
+function Prog:wait()
+    ck(C.lhip_sync(), "prog.wait")
+    if self.ev1 then
+        ck(C.lhip_event_elapsed_ms(self.ev0, self.ev1, ms_buf), "prog.elapsed")
+        self.last_ms = ms_buf[0]
+    end
+    return self
+end
+
+function Prog:elapsed_ms() return self.last_ms end
+function Prog:is_captured() return self.graph ~= nil end
+function Prog:free_graph()
+    if self.graph ~= nil then
+        C.lhip_program_free(ffi.gc(self.graph, nil))
+        self.graph = nil
+    end
+    return self
 end
 
 function M.shutdown()
+    for k in pairs(scratch) do scratch[k] = nil end
     C.lhip_shutdown()
     M.available = false
     M.reason = "shut down"
+    M.error = M.reason
 end
 
 return M

@@ -787,3 +787,233 @@ int or_lm_step_sgd(const or_lm_cfg* c, double* params, double* vel,
     or_sgd_step(params, grads, vel, or_lm_num_params(c), lr, momentum, wd, 0);
     return 1;
 }
+
+
+/* ======================================================================
+ * The luaTL operation set: the reference GPU path's kernels in double.
+ * ====================================================================== */
+
+/* 1/(1+e^-v) by sign (no overflow on either side) */
+static double or_sigmoid(double v)
+{
+    if (v >= 0) return 1.0 / (1.0 + exp(-v));
+    const double z = exp(v);
+    return z / (1.0 + z);
+}
+
+/* cuda/luaTL_core.cu:370-383: the tanh-form GELU and its derivative */
+static double or_gelu(double x)
+{
+    const double c0 = sqrt(2.0 / 3.14159265358979323846), c1 = 0.044715;
+    return 0.5 * x * (1.0 + tanh(c0 * (x + c1 * x * x * x)));
+}
+
+static double or_gelu_grad(double x)
+{
+    const double c0 = sqrt(2.0 / 3.14159265358979323846), c1 = 0.044715;
+    const double th = tanh(c0 * (x + c1 * x * x * x));
+    const double dt = c0 * (1.0 + 3.0 * c1 * x * x);
+    return 0.5 * (1.0 + th) + 0.5 * x * (1.0 - th * th) * dt;
+}
+
+static double or_silu_grad(double x)
+{
+    const double s = or_sigmoid(x);
+    return s * (1.0 + x * (1.0 - s));
+}
+
+/* cuda/luaTL_core.cu:909-934 */
+static double or_ew1(int op, double a, double b, double alpha, double beta)
+{
+    switch (op) {
+    case 0: return a;
+    case 1: return alpha * a + beta * b;
+    case 2: return alpha * a - beta * b;
+    case 3: return alpha * a * b;
+    case 4: return alpha * a / (b + 1e-20);
+    case 5: return alpha * a + beta;
+    case 6: return alpha * a + b;
+    case 7: return alpha;
+    case 8: return a > 0 ? a : 0.0;
+    case 9: return or_gelu(a);
+    case 10: return a * or_sigmoid(a);
+    case 11: return tanh(a);
+    case 12: return or_sigmoid(a);
+    case 13: return exp(a);
+    case 14: return sqrt(a > 0 ? a : 0.0);
+    case 15: return 1.0 / sqrt(a > 1e-20 ? a : 1e-20);
+    case 16: return -a;
+    case 17: return 1.0 / (a + 1e-20);
+    case 18: return fabs(a);
+    case 19: { double v = a > alpha ? a : alpha; return v < beta ? v : beta; }
+    case 20: return a > 0 ? b : 0.0;
+    case 21: return b * or_silu_grad(a);
+    case 22: return b * or_gelu_grad(a);
+    default: return a;
+    }
+}
+
+void or_ew(int op, const double* a, const double* b, double* c, long n, double alpha, double beta)
+{
+    for (long i = 0; i < n; ++i) c[i] = or_ew1(op, a ? a[i] : 0.0, b ? b[i] : 0.0, alpha, beta);
+}
+
+static double or_act(int act, double v)
+{
+    switch (act) {
+    case 1: return v > 0 ? v : 0.0;
+    case 2: return or_gelu(v);
+    case 3: return v * or_sigmoid(v);
+    case 4: return tanh(v);
+    case 5: return or_sigmoid(v);
+    default: return v;
+    }
+}
+
+/* cuda/luaTL_train.cu:127-234 (luaTL_gemm_ex_kernel), one output at a time */
+void or_gemm_ex(const double* A, const double* B, double* C, const double* bias, const double* gamma,
+                const double* rowscale, int M, int N, int K, long a_rs, long a_cs, long b_rs, long b_cs,
+                long c_rs, long c_cs, long a_bs, long b_bs, long c_bs, int batch, double alpha, double beta,
+                double eps, int pre_op, int post_op)
+{
+    if (batch < 1) batch = 1;
+    for (int z = 0; z < batch; ++z) {
+        const double* Az = A + (long)z * a_bs;
+        const double* Bz = B + (long)z * b_bs;
+        double* Cz = C + (long)z * c_bs;
+        for (int i = 0; i < M; ++i) {
+            double rsc = 1.0;
+            if (pre_op == 1) {
+                if (rowscale) {
+                    rsc = rowscale[i];
+                } else {
+                    double ss = 0;
+                    for (int k = 0; k < K; ++k) {
+                        const double a = Az[i * a_rs + k * a_cs];
+                        ss += a * a;
+                    }
+                    rsc = 1.0 / sqrt(ss / K + eps);
+                }
+            }
+            for (int j = 0; j < N; ++j) {
+                double acc = 0;
+                for (int k = 0; k < K; ++k) {
+                    double a = Az[i * a_rs + k * a_cs];
+                    if (pre_op == 1) a = a * rsc * (gamma ? gamma[k] : 1.0);
+                    else if (pre_op == 2) a = or_gelu(a);
+                    else if (pre_op == 3) a = a * or_sigmoid(a);
+                    else if (pre_op == 4) a = a > 0 ? a : 0.0;
+                    acc += a * Bz[k * b_rs + j * b_cs];
+                }
+                double v = alpha * acc;
+                if (bias) v += bias[j];
+                v = or_act(post_op, v);
+                double* cp = Cz + i * c_rs + j * c_cs;
+                if (beta != 0) v += beta * *cp;
+                *cp = v;
+            }
+        }
+    }
+}
+
+/* cuda/luaTL_train.cu:545-585 */
+void or_softmax_ex(const double* x, const double* bias, double* y, int rows, int cols, double scale,
+                   int causal, int group, int moff)
+{
+    for (int r = 0; r < rows; ++r) {
+        const int lrow = group > 0 ? r % group : r;
+        const int limit = causal ? lrow + moff : cols - 1;
+        const double* xr = x + (long)r * cols;
+        double* yr = y + (long)r * cols;
+        double mx = -INFINITY;
+        for (int i = 0; i < cols && i <= limit; ++i) {
+            double v = xr[i] * scale + (bias ? bias[i] : 0.0);
+            if (v > mx) mx = v;
+        }
+        const double base = mx == -INFINITY ? 0.0 : mx;
+        double sum = 0;
+        for (int i = 0; i < cols; ++i) {
+            double e = 0;
+            if (i <= limit) e = exp(xr[i] * scale + (bias ? bias[i] : 0.0) - base);
+            yr[i] = e;
+            sum += e;
+        }
+        const double inv = sum > 0 ? 1.0 / sum : 0.0;
+        for (int i = 0; i < cols; ++i) yr[i] *= inv;
+    }
+}
+
+/* cuda/luaTL_train.cu:589-619 */
+void or_softmax_bwd_ex(const double* y, const double* dy, double* dx, int rows, int cols, double scale,
+                       int causal, int group, int moff)
+{
+    for (int r = 0; r < rows; ++r) {
+        const int lrow = group > 0 ? r % group : r;
+        const int limit = causal ? lrow + moff : cols - 1;
+        const long o = (long)r * cols;
+        double dot = 0;
+        for (int i = 0; i < cols && i <= limit; ++i) dot += dy[o + i] * y[o + i];
+        for (int i = 0; i < cols; ++i) dx[o + i] = i <= limit ? scale * y[o + i] * (dy[o + i] - dot) : 0.0;
+    }
+}
+
+/* cuda/luaTL_train.cu:489-526 */
+void or_rmsnorm_bwd_luatl(const double* x, const double* g, const double* dy, double* dx, double* dgamma,
+                          int rows, int cols, double eps)
+{
+    for (int r = 0; r < rows; ++r) {
+        const double* xr = x + (long)r * cols;
+        const double* dyr = dy + (long)r * cols;
+        double ss = 0;
+        for (int i = 0; i < cols; ++i) ss += xr[i] * xr[i];
+        const double s = 1.0 / sqrt(ss / cols + eps);
+        double dot = 0;
+        for (int i = 0; i < cols; ++i) dot += dyr[i] * (g ? g[i] : 1.0) * xr[i];
+        const double c = (s * s * s / cols) * dot;
+        for (int i = 0; i < cols; ++i) {
+            dx[(long)r * cols + i] = s * (g ? g[i] : 1.0) * dyr[i] - c * xr[i];
+            if (dgamma) dgamma[i] += dyr[i] * xr[i] * s;
+        }
+    }
+}
+
+/* cuda/luaTL_core.cu:1346-1380 with the corrections of cuda/luaTL_train.cu:1427-1449 */
+void or_adamw_luatl(double* w, const double* g, double* m, double* v, long n, int step, double lr,
+                    double b1, double b2, double eps, double wd, double clip)
+{
+    const int t = step < 1 ? 1 : step;
+    const double bc1 = 1.0 / (1.0 - pow(b1, t));
+    const double bc2 = 1.0 / (1.0 - pow(b2, t));
+    for (long i = 0; i < n; ++i) {
+        double gr = g[i];
+        if (clip > 0) gr = gr < -clip ? -clip : (gr > clip ? clip : gr);
+        const double mi = b1 * m[i] + (1 - b1) * gr;
+        const double vi = b2 * v[i] + (1 - b2) * gr * gr;
+        m[i] = mi;
+        v[i] = vi;
+        double wi = w[i];
+        wi -= lr * wd * wi;
+        wi -= lr * (mi * bc1) / (sqrt(vi * bc2) + eps);
+        w[i] = wi;
+    }
+}
+
+/* cuda/luaTL_train.cu:895-906 */
+void or_reduce_cols(const double* x, double* out, int rows, int cols, long rs, double alpha, double beta)
+{
+    for (int c = 0; c < cols; ++c) {
+        double acc = 0;
+        for (int r = 0; r < rows; ++r) acc += x[(long)r * rs + c];
+        out[c] = alpha * acc + beta * out[c];
+    }
+}
+
+/* cuda/luaTL_train.cu:947-965 */
+void or_clip_by_nsq(double* x, long n, double nsq, double max_norm)
+{
+    const double nrm = sqrt(nsq > 0 ? nsq : 0.0);
+    double f = 1.0;
+    if (max_norm > 0 && nrm > max_norm) f = max_norm / (nrm + 1e-6);
+    if (f == 1.0) return;
+    for (long i = 0; i < n; ++i) x[i] *= f;
+}

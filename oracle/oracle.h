@@ -39,6 +39,26 @@
  *   or_lm_*           : float64 torch.autograd of the same model (independent
  *                       derivative), finite differences on a tiny model, ln V at
  *                       near-uniform logits.
+ *   or_ew             : sigmoid against scipy's expit, tanh/exp/sqrt against
+ *                       numpy, silu'/gelu' against central differences of
+ *                       silu/gelu, the tanh-form GELU within 1e-3 of x*Phi(x)
+ *                       (its published accuracy), each binary operator on
+ *                       hand-picked values.
+ *   or_gemm_ex        : numpy float64 products of explicitly transposed,
+ *                       batched copies; the RMSNorm prologue against
+ *                       or_rmsnorm_fwd then '@'; activations against
+ *                       scipy/numpy; beta == 0 with NaN in C.
+ *   or_softmax_ex / or_softmax_bwd_ex : scipy softmax of the kept prefix,
+ *                       all-zero rows when nothing is kept, equality with
+ *                       or_softmax_fwd/bwd where their contracts coincide,
+ *                       central differences for the backward.
+ *   or_rmsnorm_bwd_luatl : or_rmsnorm_bwd with 1/rms recomputed (pinned
+ *                       above), dgamma accumulation, gamma NULL = ones.
+ *   or_adamw_luatl    : constant-gradient closed form (every step is
+ *                       w(1-lr*wd) - lr*g/(|g|+eps)), the clamp, moments vs
+ *                       their recurrences.
+ *   or_reduce_cols / or_clip_by_nsq : numpy column sums; the clip's fixed
+ *                       point (norm after = max_norm*nrm/(nrm+1e-6)).
  */
 #ifndef LANTERNL_ORACLE_H
 #define LANTERNL_ORACLE_H
@@ -165,6 +185,41 @@ int or_lm_step_adamw(const or_lm_cfg* c, double* params, double* m, double* v, i
                      const int* ids, const int* tgt, int B, int T,
                      double lr, double b1, double b2, double eps, double wd, double clip_norm,
                      double* losses, double* gnorm, int* correct, double* grads);
+
+/* ---- the luaTL operation set (the reference GPU path's kernels, restated
+ *      in double for the adapter's resident calls and Program ops) ------- */
+/* c[i] = op(a[i], b[i], alpha, beta) with luaTL's operator table
+ * (cuda/luaTL_core.cu:49-72, 909-934); a or b NULL read as 0; GELU in the
+ * tanh form of cuda/luaTL_core.cu:370-383. */
+void or_ew(int op, const double* a, const double* b, double* c, long n, double alpha, double beta);
+/* luaTL_gemm_ex_kernel (cuda/luaTL_train.cu:127-234): strided, batched,
+ * C = act(alpha * pre(A).B + bias) + beta*C; pre 1 = RMSNorm of A's rows
+ * (rowscale given, else 1/sqrt(mean a^2 + eps)) times gamma[k]; pre 2-4 =
+ * gelu/silu/relu of a; beta == 0 does not read C. */
+void or_gemm_ex(const double* A, const double* B, double* C, const double* bias, const double* gamma,
+                const double* rowscale, int M, int N, int K, long a_rs, long a_cs, long b_rs, long b_cs,
+                long c_rs, long c_cs, long a_bs, long b_bs, long c_bs, int batch, double alpha, double beta,
+                double eps, int pre_op, int post_op);
+/* luaTL_softmax_ex_kernel (cuda/luaTL_train.cu:545-585): v = x*scale + bias[j]
+ * over j <= limit, limit = (group>0 ? r%group : r) + moff when causal, else
+ * cols-1; masked 0; nothing kept -> all 0. */
+void or_softmax_ex(const double* x, const double* bias, double* y, int rows, int cols, double scale,
+                   int causal, int group, int moff);
+/* luaTL_softmax_bwd_kernel (cuda/luaTL_train.cu:589-619), dx overwritten. */
+void or_softmax_bwd_ex(const double* y, const double* dy, double* dx, int rows, int cols, double scale,
+                       int causal, int group, int moff);
+/* luaTL_rmsnorm_bwd_kernel (cuda/luaTL_train.cu:489-526): s from x and eps,
+ * dx overwritten, dgamma (may be NULL) accumulated, gamma NULL = 1. */
+void or_rmsnorm_bwd_luatl(const double* x, const double* g, const double* dy, double* dx, double* dgamma,
+                          int rows, int cols, double eps);
+/* luaTL_adamw_kernel (cuda/luaTL_core.cu:1346-1380) with bc1 = 1/(1-b1^t),
+ * bc2 = 1/(1-b2^t), t = max(step, 1) (cuda/luaTL_train.cu:1427-1449). */
+void or_adamw_luatl(double* w, const double* g, double* m, double* v, long n, int step, double lr,
+                    double b1, double b2, double eps, double wd, double clip);
+/* out[c] = alpha * sum_r x[r*rs + c] + beta * out[c] (cuda/luaTL_train.cu:895-906) */
+void or_reduce_cols(const double* x, double* out, int rows, int cols, long rs, double alpha, double beta);
+/* x *= max_norm/(sqrt(nsq)+1e-6) when sqrt(nsq) > max_norm > 0 (cuda/luaTL_train.cu:947-965) */
+void or_clip_by_nsq(double* x, long n, double nsq, double max_norm);
 
 #ifdef __cplusplus
 }

@@ -68,6 +68,17 @@ def _declare(L):
         "or_sgd_step": (None, [_D, _D, _D, c_long, c_double, c_double, c_double, c_int]),
         "or_adamw_step": (None, [_D, _D, _D, _D, c_long, c_double, c_double, c_double, c_double,
                                  c_double, c_int]),
+        "or_ew": (None, [c_int, _D, _D, _D, c_long, c_double, c_double]),
+        "or_gemm_ex": (None, [_D, _D, _D, _D, _D, _D, c_int, c_int, c_int, c_long, c_long, c_long, c_long,
+                              c_long, c_long, c_long, c_long, c_long, c_int, c_double, c_double, c_double,
+                              c_int, c_int]),
+        "or_softmax_ex": (None, [_D, _D, _D, c_int, c_int, c_double, c_int, c_int, c_int]),
+        "or_softmax_bwd_ex": (None, [_D, _D, _D, c_int, c_int, c_double, c_int, c_int, c_int]),
+        "or_rmsnorm_bwd_luatl": (None, [_D, _D, _D, _D, _D, c_int, c_int, c_double]),
+        "or_adamw_luatl": (None, [_D, _D, _D, _D, c_long, c_int, c_double, c_double, c_double, c_double,
+                                  c_double, c_double]),
+        "or_reduce_cols": (None, [_D, _D, c_int, c_int, c_long, c_double, c_double]),
+        "or_clip_by_nsq": (None, [_D, c_long, c_double, c_double]),
         "or_lm_num_params": (c_long, [ctypes.POINTER(LmCfg)]),
         "or_lm_param_offsets": (c_int, [ctypes.POINTER(LmCfg), ctypes.POINTER(c_long), _I, _I]),
         "or_lm_window": (c_double, [ctypes.POINTER(LmCfg), _D, _I, _I, c_int, _D, _D, _I]),
@@ -379,3 +390,110 @@ def lm_step_adamw(cfg, params, m, v, t, ids, tgt, lr, beta1=0.9, beta2=0.95, eps
                                      ctypes.byref(gn), ctypes.byref(corr), grads.ctypes.data_as(_D))
     return dict(losses=losses, gnorm=gn.value, correct=corr.value, grads=grads,
                 applied=bool(applied), t=tc.value)
+
+
+# ---------------------------------------------------------------- luaTL operation set
+# The reference GPU path's kernels restated in double (oracle.c, "The luaTL
+# operation set"); the adapter's resident calls and Program ops are checked
+# against these.
+EW = {"COPY": 0, "ADD": 1, "SUB": 2, "MUL": 3, "DIV": 4, "SCALE": 5, "AXPY": 6, "FILL": 7, "RELU": 8,
+      "GELU": 9, "SILU": 10, "TANH": 11, "SIGMOID": 12, "EXP": 13, "SQRT": 14, "RSQRT": 15, "NEG": 16,
+      "RECIP": 17, "ABS": 18, "CLAMP": 19, "DRELU": 20, "DSILU": 21, "DGELU": 22}
+
+
+def ew(op, a, b, alpha=1.0, beta=0.0, n=None):
+    """luaTL_elementwise's operator table (cuda/luaTL_core.cu:909-934); a/b may be None."""
+    if isinstance(op, str):
+        op = EW[op]
+    ref = a if a is not None else b
+    n = int(np.size(ref)) if n is None else n
+    pa = pb = _nul(_D)
+    if a is not None:
+        a, pa = _d(a)
+    if b is not None:
+        b, pb = _d(b)
+    c = np.empty(n)
+    lib().or_ew(op, pa, pb, c.ctypes.data_as(_D), n, alpha, beta)
+    return c if ref is None else c.reshape(np.shape(ref))
+
+
+def gemm_ex(A, B, C, M, N, K, strides, batch=1, alpha=1.0, beta=0.0, eps=1e-5, pre=0, act=0, bias=None,
+            gamma=None, rowscale=None):
+    """luaTL_gemm_ex_kernel (cuda/luaTL_train.cu:127-234) on flat float64 buffers;
+    strides = (a_rs, a_cs, b_rs, b_cs, c_rs, c_cs, a_bs, b_bs, c_bs).  C is updated in place."""
+    A, pA = _d(A); B, pB = _d(B)
+    assert C.dtype == np.float64 and C.flags.c_contiguous
+    keep, ptrs = [], []
+    for v in (bias, gamma, rowscale):
+        if v is None:
+            ptrs.append(_nul(_D))
+        else:
+            v, p = _d(v)
+            keep.append(v)
+            ptrs.append(p)
+    lib().or_gemm_ex(pA, pB, C.ctypes.data_as(_D), ptrs[0], ptrs[1], ptrs[2], M, N, K, *strides, batch, alpha,
+                     beta, eps, pre, act)
+    return C
+
+
+def softmax_ex(x, bias=None, scale=1.0, causal=False, group=0, moff=0):
+    """luaTL_softmax_ex_kernel (cuda/luaTL_train.cu:545-585)."""
+    x, px = _d(x)
+    rows, cols = x.shape
+    y = np.empty_like(x)
+    pb = _nul(_D)
+    if bias is not None:
+        bias, pb = _d(bias)
+    lib().or_softmax_ex(px, pb, y.ctypes.data_as(_D), rows, cols, scale, int(causal), group, moff)
+    return y
+
+
+def softmax_bwd_ex(y, dy, scale=1.0, causal=False, group=0, moff=0):
+    """luaTL_softmax_bwd_kernel (cuda/luaTL_train.cu:589-619)."""
+    y, py = _d(y); dy, pdy = _d(dy)
+    rows, cols = y.shape
+    dx = np.empty_like(y)
+    lib().or_softmax_bwd_ex(py, pdy, dx.ctypes.data_as(_D), rows, cols, scale, int(causal), group, moff)
+    return dx
+
+
+def rmsnorm_bwd_luatl(x, g, dy, eps, dgamma=None):
+    """luaTL_rmsnorm_bwd_kernel (cuda/luaTL_train.cu:489-526): returns dx; dgamma (float64,
+    may be None) accumulates."""
+    x, px = _d(x); dy, pdy = _d(dy)
+    rows, cols = x.shape
+    pg = _nul(_D)
+    if g is not None:
+        g, pg = _d(g)
+    dx = np.empty_like(x)
+    pdg = _nul(_D)
+    if dgamma is not None:
+        assert dgamma.dtype == np.float64 and dgamma.flags.c_contiguous
+        pdg = dgamma.ctypes.data_as(_D)
+    lib().or_rmsnorm_bwd_luatl(px, pg, pdy, dx.ctypes.data_as(_D), pdg, rows, cols, eps)
+    return dx
+
+
+def adamw_luatl(w, g, m, v, step, lr=1e-3, b1=0.9, b2=0.999, eps=1e-8, wd=0.0, clip=0.0):
+    """luaTL_adamw_kernel (cuda/luaTL_core.cu:1346-1380), in place on float64 w, m, v."""
+    for a in (w, m, v):
+        assert a.dtype == np.float64 and a.flags.c_contiguous
+    g, pg = _d(g)
+    lib().or_adamw_luatl(w.ctypes.data_as(_D), pg, m.ctypes.data_as(_D), v.ctypes.data_as(_D), w.size, step,
+                         lr, b1, b2, eps, wd, clip)
+
+
+def reduce_cols(x, out, alpha=1.0, beta=0.0, rs=None):
+    """luaTL_reduce_cols_kernel (cuda/luaTL_train.cu:895-906), out updated in place."""
+    x, px = _d(x)
+    rows, cols = x.shape
+    assert out.dtype == np.float64 and out.flags.c_contiguous
+    lib().or_reduce_cols(px, out.ctypes.data_as(_D), rows, cols, cols if rs is None else rs, alpha, beta)
+    return out
+
+
+def clip_by_nsq(x, nsq, max_norm):
+    """luaTL_clip_kernel (cuda/luaTL_train.cu:947-965), in place on float64 x."""
+    assert x.dtype == np.float64 and x.flags.c_contiguous
+    lib().or_clip_by_nsq(x.ctypes.data_as(_D), x.size, nsq, max_norm)
+    return x

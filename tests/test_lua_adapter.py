@@ -1,13 +1,25 @@
 """CPU checks of lanternl_amd/lua/luatl_adapter.lua, which cannot run here (no
-LuaJIT in this image): its ffi.cdef must declare exactly the C ABI of
-include/lanternl_hip.h, and it must define the module surface of the
-reference adapter (ai/gpu/luatl_adapter.lua:63-246) that this backend serves."""
+LuaJIT in this image or on the GPU box):
+  * its ffi.cdef declares exactly the C ABI of include/lanternl_hip.h;
+  * every function of the reference adapter (ai/gpu/luatl_adapter.lua), every
+    Handle method and every luaTL.Program method (ai/gpu/luaTL_train.lua:
+    332-632) exists with the reference's parameter list, name for name, and the
+    module sets the reference's fields -- the reference's signatures come from
+    tests/golden/adapter_signatures.json (tests/golden/make_adapter_signatures.py);
+  * the Python mirror (lanternl_amd/backend.py), which the GPU tests drive,
+    has the same functions with the same parameter counts."""
+import inspect
+import json
 import os
 import re
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 ADAPTER = os.path.join(ROOT, "lanternl_amd", "lua", "luatl_adapter.lua")
 HEADER = os.path.join(ROOT, "include", "lanternl_hip.h")
+SIGS = json.load(open(os.path.join(ROOT, "tests", "golden", "adapter_signatures.json")))
+# Prog:slot hands out the next slot of the reference's C op array; ops here are
+# queued closures, so there is no slot to hand out (Prog:push plays that part)
+PROGRAM_INTERNAL = {"slot"}
 
 
 def _params(decl):
@@ -23,12 +35,17 @@ def _decls(text, prefix=""):
     return out
 
 
+def _lua_sigs(text, owner):
+    pat = re.compile(r"^function\s+" + re.escape(owner) + r"[.:](\w+)\s*\(([^)]*)\)", re.M)
+    return {m.group(1): [p.strip() for p in m.group(2).split(",") if p.strip()] for m in pat.finditer(text)}
+
+
 def test_cdef_functions_match_the_header():
     lua = open(ADAPTER).read()
     cdef = lua[lua.index("ffi.cdef[["): lua.index("]]", lua.index("ffi.cdef[["))]
     mine = _decls(cdef)
     header = _decls(open(HEADER).read(), prefix=r"LHIP_API\s+")
-    assert len(mine) >= 30
+    assert len(mine) >= 45
     missing = sorted(set(mine) - set(header))
     assert not missing, f"cdef declares functions the header does not: {missing}"
     wrong = {f: (mine[f], header[f]) for f in mine if mine[f] != header[f]}
@@ -46,20 +63,56 @@ def test_library_exports_every_cdef_function():
     assert not missing, missing
 
 
-# module contract (matrix.lua:28-48,178-202) and the resident-mode surface of
-# ai/gpu/luatl_adapter.lua:63-246 (gelu_inplace and scale_inplace are not on
-# the hot path: neither the CPU LMTrain step nor this backend uses them)
-SURFACE = ["matmul", "matmul_nt", "matmul_tn", "pin", "alloc", "gemm", "gemm_dx", "gemm_dw", "rmsnorm",
-           "rmsnorm_bwd", "softmax", "softmax_causal", "softmax_bwd", "swiglu", "rope", "add_inplace",
-           "silu_inplace", "program", "sync", "stats", "hardware", "shutdown", "offset", "view", "cols", "wrap",
-           "ids", "upload_i32", "download_i32", "download_f32", "scalar", "mem"]
-HANDLE = ["toflat", "upload", "zero", "free", "shape"]
+def test_every_reference_adapter_function_has_its_parameter_list():
+    mine = _lua_sigs(open(ADAPTER).read(), "M")
+    ref = SIGS["module"]
+    assert len(ref) >= 30
+    missing = sorted(set(ref) - set(mine))
+    assert not missing, f"reference adapter functions missing: {missing}"
+    wrong = {f: (mine[f], ref[f]) for f in ref if mine[f] != ref[f]}
+    assert not wrong, f"parameter lists differ (mine, reference): {wrong}"
+    # the transposed products this backend adds, with matmul's convention
+    assert mine["matmul_nt"] == mine["matmul_tn"] == ref["matmul"]
 
 
-def test_adapter_defines_the_reference_surface():
+def test_handle_methods_and_program_methods_match():
     lua = open(ADAPTER).read()
-    have = set(re.findall(r"^function M\.(\w+)\s*\(", lua, re.M))
-    assert not [f for f in SURFACE if f not in have], [f for f in SURFACE if f not in have]
-    hmeth = set(re.findall(r"^function Handle:(\w+)\s*\(", lua, re.M))
-    assert not [f for f in HANDLE if f not in hmeth]
-    assert re.search(r"available\s*=", lua) and re.search(r"reason\s*=", lua)
+    mine = _lua_sigs(lua, "Handle")
+    wrong = {f: (mine.get(f), p) for f, p in SIGS["handle"].items() if mine.get(f) != p}
+    assert not wrong, wrong
+    prog = _lua_sigs(lua, "Prog")
+    want = {k: v for k, v in SIGS["program"].items() if k not in PROGRAM_INTERNAL}
+    assert len(want) >= 40
+    wrong = {f: (prog.get(f), p) for f, p in want.items() if prog.get(f) != p}
+    assert not wrong, f"Program methods differ (mine, reference): {wrong}"
+
+
+def test_module_sets_the_reference_fields():
+    lua = open(ADAPTER).read()
+    ctor = re.search(r"local M\s*=\s*\{([^}]*)\}", lua).group(1)
+    fields = set(re.findall(r"\bM\.(\w+)\s*=[^=]", lua)) | set(re.findall(r"(\w+)\s*=", ctor))
+    missing = sorted(set(SIGS["fields"]) - fields)
+    assert not missing, missing
+    assert "reason" in fields      # matrix.lua:39-40 reads mod.reason
+    assert re.search(r'name\s*=\s*"luatl"', ctor) and re.search(r"priority\s*=\s*100", ctor)
+
+
+def test_python_mirror_has_the_same_calls():
+    """lanternl_amd/backend.py is what the GPU tests drive: same functions, same arity."""
+    from lanternl_amd import backend as B
+    for f, params in SIGS["module"].items():
+        fn = getattr(B, f, None)
+        assert callable(fn), f
+        sig = inspect.signature(fn)
+        assert len(sig.parameters) == len(params), (f, list(sig.parameters), params)
+    for f, params in SIGS["handle"].items():
+        assert len(inspect.signature(getattr(B.Handle, f)).parameters) == len(params) + 1, f
+    for f, params in SIGS["program"].items():
+        if f in PROGRAM_INTERNAL:
+            continue
+        meth = getattr(B.Program, "async_" if f == "async" else f)
+        assert len(inspect.signature(meth).parameters) == len(params) + 1, (f, params)
+    for field in ("name", "priority", "available", "reason", "error", "C", "luaTL", "HandleClass",
+                  "is_handle", "new_handle"):
+        assert hasattr(B, field), field
+    assert B.name == "luatl" and B.priority == 100

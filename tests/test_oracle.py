@@ -450,3 +450,195 @@ def test_lm_step_adamw_semantics():
     out = O.lm_step_adamw(cfg, bad, mb, vb, 1, ids, tgt, lr=1e-2)
     assert not out["applied"] and out["t"] == 1
     assert np.array_equal(mb, m) and np.array_equal(vb, v)
+
+
+# ------------------------------------------------- luaTL operation set (GPU reference path)
+def test_ew_unary_operators_against_libraries():
+    """cuda/luaTL_core.cu:909-934, unary half: each against a library routine."""
+    x = np.linspace(-40, 40, 801)
+    assert np.allclose(O.ew("SIGMOID", x, None), sps.expit(x), rtol=1e-14, atol=1e-300)
+    assert np.allclose(O.ew("SILU", x, None), x * sps.expit(x), rtol=1e-14, atol=1e-300)
+    assert np.allclose(O.ew("TANH", x, None), np.tanh(x), rtol=1e-14)
+    xs = np.linspace(-5, 5, 101)
+    assert np.allclose(O.ew("EXP", xs, None), np.exp(xs), rtol=1e-14)
+    assert np.array_equal(O.ew("RELU", x, None), np.maximum(x, 0))
+    assert np.array_equal(O.ew("ABS", x, None), np.abs(x))
+    assert np.array_equal(O.ew("NEG", x, None), -x)
+    assert np.array_equal(O.ew("COPY", x, None), x)
+    assert np.allclose(O.ew("SQRT", x, None), np.sqrt(np.maximum(x, 0)), rtol=1e-15)
+    assert O.ew("RSQRT", np.array([4.0]), None)[0] == 0.5 and O.ew("RECIP", np.array([4.0]), None)[0] == 0.25
+    # the tanh form approximates x * Phi(x) to within 1e-3 everywhere (its
+    # published accuracy); a wrong coefficient or a missing 0.5 breaks this
+    xg = np.linspace(-8, 8, 3201)
+    assert np.max(np.abs(O.ew("GELU", xg, None) - xg * sps.ndtr(xg))) < 1e-3
+
+
+def test_ew_derivative_operators_against_central_differences():
+    """DSILU / DGELU / DRELU: b times the derivative of the unary operator."""
+    a = np.linspace(-6, 6, 241)
+    b = RNG.uniform(-2, 2, a.size)
+    h = 1e-6
+    for dop, op in (("DSILU", "SILU"), ("DGELU", "GELU")):
+        fd = (O.ew(op, a + h, None) - O.ew(op, a - h, None)) / (2 * h)
+        assert np.allclose(O.ew(dop, a, b), b * fd, atol=1e-8), dop
+    assert np.array_equal(O.ew("DRELU", a, b), np.where(a > 0, b, 0.0))
+
+
+def test_ew_binary_operators_hand_values():
+    """The binary rows of luaTL's table on hand-picked values.  AXPY is
+    alpha*a + b (luaTL_core.cu:921): Tensor:add_inplace(B, alpha) runs it with
+    a = self, b = B (luaTL.lua:634-638), so it computes alpha*self + B."""
+    one = lambda op, a, b, al, be: O.ew(op, np.array([a]), np.array([b]), al, be)[0]  # noqa: E731
+    assert one("ADD", 2, 3, 2.0, 0.5) == 5.5
+    assert one("SUB", 2, 3, 2.0, 0.5) == 2.5
+    assert one("MUL", 2, 3, 0.5, 9.0) == 3.0
+    assert abs(one("DIV", 3, 4, 2.0, 9.0) - 1.5) < 1e-15
+    assert one("SCALE", 3, 99, 2.0, 1.0) == 7.0
+    assert one("AXPY", 3, 4, 2.0, 9.0) == 10.0
+    assert one("FILL", 3, 4, 2.5, 9.0) == 2.5
+    assert one("CLAMP", 5, 0, -1.0, 2.0) == 2.0 and one("CLAMP", -5, 0, -1.0, 2.0) == -1.0
+    # a missing operand reads as 0
+    assert O.ew("ADD", np.array([2.0]), None, 1.0, 1.0)[0] == 2.0
+
+
+def _np_gemm_ref(a, b, c0, alpha, beta, bias=None, act=None):
+    v = alpha * (a @ b)
+    if bias is not None:
+        v = v + bias[None, :]
+    if act is not None:
+        v = act(v)
+    return v + beta * c0 if beta != 0 else v
+
+
+def test_gemm_ex_strides_batches_and_epilogue():
+    """cuda/luaTL_train.cu:127-234 against numpy products of explicit copies."""
+    M, N, K = 7, 5, 6
+    # A given transposed (stored K x M: a_rs = 1, a_cs = M), C column-major
+    at = RNG.standard_normal((K, M))
+    b = RNG.standard_normal((K, N))
+    c0 = RNG.standard_normal((N, M))                 # C^T stored
+    C = c0.copy().ravel()
+    O.gemm_ex(at.ravel(), b.ravel(), C, M, N, K, (1, M, N, 1, 1, M, 0, 0, 0), alpha=0.5, beta=2.0)
+    ref = _np_gemm_ref(at.T, b, c0.T, 0.5, 2.0)
+    assert np.allclose(C.reshape(N, M).T, ref, rtol=1e-13)
+    # bias + GELU + beta, row-major; beta == 0 never reads C
+    a = RNG.standard_normal((M, K))
+    bias = RNG.standard_normal(N)
+    c1 = RNG.standard_normal((M, N))
+    C = c1.copy().ravel()
+    O.gemm_ex(a.ravel(), b.ravel(), C, M, N, K, (K, 1, N, 1, N, 1, 0, 0, 0), alpha=1.5, beta=-1.0, act=2,
+              bias=bias)
+    gelu = lambda v: O.ew("GELU", v, None)  # noqa: E731 (pinned above)
+    assert np.allclose(C.reshape(M, N), _np_gemm_ref(a, b, c1, 1.5, -1.0, bias, gelu), rtol=1e-12)
+    C = np.full(M * N, np.nan)
+    O.gemm_ex(a.ravel(), b.ravel(), C, M, N, K, (K, 1, N, 1, N, 1, 0, 0, 0), act=5)
+    assert np.allclose(C.reshape(M, N), sps.expit(a @ b), rtol=1e-13)
+    # batched per-head views: q (T x H*hd) . k^T per head into S (H x T x T)
+    T, H, hd = 5, 3, 4
+    q = RNG.standard_normal((T, H * hd)); k = RNG.standard_normal((T, H * hd))
+    S = np.zeros(H * T * T)
+    O.gemm_ex(q.ravel(), k.ravel(), S, T, T, hd, (H * hd, 1, 1, H * hd, T, 1, hd, hd, T * T), batch=H)
+    S = S.reshape(H, T, T)
+    for h in range(H):
+        qs, ks = q[:, h * hd:(h + 1) * hd], k[:, h * hd:(h + 1) * hd]
+        assert np.allclose(S[h], qs @ ks.T, rtol=1e-13)
+
+
+def test_gemm_ex_prologues():
+    """pre RMSNORM equals or_rmsnorm_fwd's rows (pinned by finite differences)
+    times B, with rowscale computed or given; pre SILU/RELU map A elementwise."""
+    M, N, K = 6, 4, 8
+    a = RNG.standard_normal((M, K)); b = RNG.standard_normal((K, N)); g = RNG.normal(1, 0.1, K)
+    eps = 1e-5
+    y, inv = O.rmsnorm_fwd(a, g, eps)
+    C = np.zeros(M * N)
+    O.gemm_ex(a.ravel(), b.ravel(), C, M, N, K, (K, 1, N, 1, N, 1, 0, 0, 0), pre=1, gamma=g, eps=eps)
+    assert np.allclose(C.reshape(M, N), y @ b, rtol=1e-12)
+    rs = RNG.uniform(0.5, 2, M)
+    C = np.zeros(M * N)
+    O.gemm_ex(a.ravel(), b.ravel(), C, M, N, K, (K, 1, N, 1, N, 1, 0, 0, 0), pre=1, rowscale=rs)
+    assert np.allclose(C.reshape(M, N), (a * rs[:, None]) @ b, rtol=1e-12)
+    for pre, f in ((3, lambda v: v * sps.expit(v)), (4, lambda v: np.maximum(v, 0))):
+        C = np.zeros(M * N)
+        O.gemm_ex(a.ravel(), b.ravel(), C, M, N, K, (K, 1, N, 1, N, 1, 0, 0, 0), pre=pre)
+        assert np.allclose(C.reshape(M, N), f(a) @ b, rtol=1e-12)
+
+
+def _kept_softmax(v, lim):
+    out = np.zeros_like(v)
+    if lim > 0:
+        out[:lim] = sps.softmax(v[:lim])
+    return out
+
+
+def test_softmax_ex_against_scipy_and_the_cpu_form():
+    rows, cols = 9, 7
+    x = RNG.standard_normal((rows, cols)) * 2
+    bias = RNG.standard_normal(cols)
+    for causal, group, moff, scale, bb in ((False, 0, 0, 0.5, None), (True, 3, 0, 1.0, None),
+                                           (True, 0, 2, 0.7, bias), (True, 4, -2, 1.0, None)):
+        y = O.softmax_ex(x, bb, scale, causal, group, moff)
+        for r in range(rows):
+            lrow = r % group if group > 0 else r
+            lim = min(max(lrow + moff + 1, 0), cols) if causal else cols
+            v = x[r] * scale + (bb if bb is not None else 0)
+            assert np.allclose(y[r], _kept_softmax(v, lim), rtol=1e-13, atol=1e-300)
+    # a negative offset masks whole rows: all zero
+    y = O.softmax_ex(x, None, 1.0, True, 0, -3)
+    assert not y[:3].any() and np.allclose(y[3:].sum(1), 1)
+    # where the contracts coincide (offset >= 0, group = rows) it equals the
+    # CPU path's or_softmax_fwd
+    assert np.allclose(O.softmax_ex(x, None, 1.0, True, 0, 1), O.softmax_fwd(x, causal=True, offset=1), rtol=1e-14)
+
+
+def test_softmax_bwd_ex_by_central_differences():
+    rows, cols = 5, 6
+    x = RNG.standard_normal((rows, cols))
+    dy = RNG.standard_normal((rows, cols))
+    for causal, group, moff, scale in ((False, 0, 0, 0.8), (True, 2, 1, 1.3), (True, 0, -2, 1.0)):
+        y = O.softmax_ex(x, None, scale, causal, group, moff)
+        dx = O.softmax_bwd_ex(y, dy, scale, causal, group, moff)
+        f = lambda xx: float(np.sum(dy * O.softmax_ex(xx, None, scale, causal, group, moff)))  # noqa: E731
+        assert np.allclose(dx, fd_grad(f, x), atol=1e-8)
+
+
+def test_rmsnorm_bwd_luatl_matches_the_cpu_form():
+    rows, cols, eps = 6, 10, 1e-5
+    x = RNG.standard_normal((rows, cols)); g = RNG.normal(1, 0.1, cols); dy = RNG.standard_normal((rows, cols))
+    _, inv = O.rmsnorm_fwd(x, g, eps)
+    dx_ref, dg_ref = O.rmsnorm_bwd(x, g, inv, dy)
+    dg = np.zeros(cols)
+    dx = O.rmsnorm_bwd_luatl(x, g, dy, eps, dg)
+    assert np.allclose(dx, dx_ref, rtol=1e-12) and np.allclose(dg, dg_ref, rtol=1e-12)
+    O.rmsnorm_bwd_luatl(x, g, dy, eps, dg)            # dgamma accumulates
+    assert np.allclose(dg, 2 * dg_ref, rtol=1e-12)
+    assert np.allclose(O.rmsnorm_bwd_luatl(x, None, dy, eps), O.rmsnorm_bwd_luatl(x, np.ones(cols), dy, eps))
+
+
+def test_adamw_luatl_closed_forms():
+    """Constant gradient: m*bc1 = g and v*bc2 = g^2 at every t, so each step is
+    w(1 - lr*wd) - lr*g/(|g| + eps); clip clamps g first."""
+    lr, b1, b2, eps, wd = 0.05, 0.9, 0.999, 1e-8, 0.01
+    g = np.array([2.0, -0.5, 1e-3, 0.0, 7.0])
+    w = RNG.standard_normal(5); m = np.zeros(5); v = np.zeros(5)
+    wexp = w.copy()
+    gc = np.clip(g, -3.0, 3.0)
+    for t in range(1, 6):
+        O.adamw_luatl(w, g, m, v, t, lr, b1, b2, eps, wd, clip=3.0)
+        wexp = wexp * (1 - lr * wd) - lr * gc / (np.abs(gc) + eps)
+    assert np.allclose(w, wexp, rtol=1e-12, atol=1e-15)
+    assert np.allclose(m, (1 - b1 ** 5) * gc, rtol=1e-12) and np.allclose(v, (1 - b2 ** 5) * gc ** 2, rtol=1e-12)
+
+
+def test_reduce_cols_and_clip():
+    x = RNG.standard_normal((11, 6))
+    out = RNG.standard_normal(6)
+    ref = 0.5 * x.sum(0) + 2.0 * out
+    assert np.allclose(O.reduce_cols(x, out.copy(), 0.5, 2.0), ref, rtol=1e-13)
+    wide = RNG.standard_normal((4, 10))           # row stride 10, 6 columns summed
+    assert np.allclose(O.reduce_cols(wide[:, :6].copy(), np.zeros(6)), wide[:, :6].sum(0))
+    y = RNG.standard_normal(50)
+    nsq = float(np.sum(y * y)); nrm = math.sqrt(nsq)
+    z = O.clip_by_nsq(y.copy(), nsq, nrm / 4)
+    assert abs(np.linalg.norm(z) - (nrm / 4) * nrm / (nrm + 1e-6)) < 1e-12
+    assert np.array_equal(O.clip_by_nsq(y.copy(), nsq, 2 * nrm), y)     # below the bound: unchanged
