@@ -432,10 +432,10 @@ typedef struct {
 } lhip_lm_config_t;
 
 typedef struct {
-    float loss;          /* mean over windows of each window's mean CE */
+    float loss;          /* sum_w len_w * (window w's mean CE) / sum_w len_w (LMTrain's batch loss) */
     float grad_norm;     /* global norm of the 1/batch-scaled grads, before clipping */
     int applied;         /* 1 when the update ran (finite norm), else 0 */
-    int correct;         /* argmax hits over the batch*seq targets */
+    int correct;         /* argmax hits over the batch's tokens */
     int steps;           /* steps enqueued since creation */
 } lhip_lm_stats_t;
 
@@ -451,8 +451,21 @@ LHIP_API int lhip_lm_get_params(void* model, float* host, long long n);
 LHIP_API int lhip_lm_get_grads(void* model, float* host, long long n);
 LHIP_API int lhip_lm_set_velocity(void* model, const float* host, long long n);
 LHIP_API int lhip_lm_get_velocity(void* model, float* host, long long n);
-/* Token ids and next-token targets, batch*seq each, 0-based, row b*seq + t. */
+/* Token ids and next-token targets, batch*seq each, 0-based, row b*seq + t:
+ * `batch` full windows of `seq` tokens. */
 LHIP_API int lhip_lm_set_batch(void* model, const int* ids, const int* targets);
+/* The same with LMTrain's ragged batches: n_windows (1..batch) windows, window
+ * b holding lengths[b] (1..seq) tokens at rows b*seq .. b*seq+lengths[b]-1
+ * (the rest of its rows, and the slots past n_windows, are ignored);
+ * lengths NULL means full windows.  Each window's loss is the mean CE over
+ * its own tokens, the summed gradients are scaled by 1/n_windows when
+ * n_windows > 1, and lhip_lm_stats reports LMTrain's token-weighted batch
+ * loss: build_windows' short last window and the short last batch of the
+ * batch loop (ai/optim/lmtrain.lua:535-558,1183-1212; tensor2.lua:845-857).
+ * A non-causal model whose seq or head_dim exceeds the fused attention's
+ * limit (64) takes only full windows (LHIP_E_UNSUPPORTED otherwise). */
+LHIP_API int lhip_lm_set_batch_ex(void* model, const int* ids, const int* targets, const int* lengths,
+                                  int n_windows);
 /* Capture the step into a hipGraph on the next call and replay it afterwards. */
 LHIP_API int lhip_lm_use_graph(void* model, int on);
 /* Enqueue one step (asynchronous). */
@@ -468,7 +481,8 @@ LHIP_API int lhip_lm_step_adamw(void* model, float lr, float beta1, float beta2,
  * step count: set (e.g. on resume) and get (synchronous). */
 LHIP_API int lhip_lm_set_adam_state(void* model, const float* m, const float* v, long long n, int step);
 LHIP_API int lhip_lm_get_adam_state(void* model, float* m, float* v, long long n, int* step);
-/* Wait and report the last step; window_losses (may be NULL) gets `batch` values. */
+/* Wait and report the last step; window_losses (may be NULL) gets `batch`
+ * values, each window's mean CE (0 for empty slots). */
 LHIP_API int lhip_lm_stats(void* model, lhip_lm_stats_t* out, float* window_losses, int nwin);
 /* Row argmax of the last step's logits (batch*seq int32). */
 LHIP_API int lhip_lm_get_argmax(void* model, int* host, int n);

@@ -154,6 +154,7 @@ SIGNATURES.update({
     "lhip_lm_set_velocity": (_i, [_p, _p, _ll]),
     "lhip_lm_get_velocity": (_i, [_p, _p, _ll]),
     "lhip_lm_set_batch": (_i, [_p, _p, _p]),
+    "lhip_lm_set_batch_ex": (_i, [_p, _p, _p, _p, _i]),
     "lhip_lm_use_graph": (_i, [_p, _i]),
     "lhip_lm_step_sgd": (_i, [_p, _f, _f, _f, _f, _i]),
     "lhip_lm_step_adamw": (_i, [_p, _f, _f, _f, _f, _f, _f]),

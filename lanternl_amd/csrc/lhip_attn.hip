@@ -56,10 +56,13 @@ struct AttnArgs {
     float scale;
     int causal;
     int vec;              // T, hd, D % 4 == 0 and 16-byte aligned bases: float4 loads
+    const int* wlen;      // [B] keys of each window (NULL: T); keys past it are masked
 };
 
 __device__ __forceinline__ int round16(int x) { return (x + 15) & ~15; }
-__device__ __forceinline__ int attn_lim(int i, int T, int causal) { return causal ? (i + 1 < T ? i + 1 : T) : T; }
+// keys visible to query row i: those below kl (the window's length, or T),
+// and at most i when causal; a row with none gets a zero P row
+__device__ __forceinline__ int attn_lim(int i, int kl, int causal) { return causal ? (i + 1 < kl ? i + 1 : kl) : kl; }
 
 // One 16x16 block C(i, j) = sum_{0 <= k < K4} A(i, k) B(k, j) (K4 % 4 == 0,
 // wave-uniform): lane l supplies A(l%16, k + l/16) = a[(l%16) * ars +
@@ -239,6 +242,7 @@ __global__ void __launch_bounds__(kAttnThreads) attn_fwd_kernel(const AttnArgs a
     const int nj = a.causal ? c + 1 : nbt;
     const bool act = wave < nj;
     const int col = 16 * wave + r;
+    const int kl = a.wlen ? min(T, a.wlen[b]) : T;
     if (a.vec) {
         Qkv4 x;
         qkv_fetch(a, b, h, x);
@@ -254,7 +258,7 @@ __global__ void __launch_bounds__(kAttnThreads) attn_fwd_kernel(const AttnArgs a
         const floatx4 S = mfma_block(qs + i0 * kLd, kLd, 1, ks + 16 * wave * kLd, kLd, 1, hd4);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            v[e] = col < attn_lim(i0 + 4 * q + e, T, a.causal) ? S[e] * a.scale : -INFINITY;
+            v[e] = col < attn_lim(i0 + 4 * q + e, kl, a.causal) ? S[e] * a.scale : -INFINITY;
             const float m = row16_max(v[e]);
             if (r == 0) rmax[wave][4 * q + e] = m;
         }
@@ -266,7 +270,7 @@ __global__ void __launch_bounds__(kAttnThreads) attn_fwd_kernel(const AttnArgs a
             float m = -INFINITY;
             for (int w = 0; w < nj; ++w) m = fmaxf(m, rmax[w][4 * q + e]);
             const float mx = (m == -INFINITY || m != m) ? 0.f : m;
-            p[e] = col < attn_lim(i0 + 4 * q + e, T, a.causal) ? expf(v[e] - mx) : 0.f;
+            p[e] = col < attn_lim(i0 + 4 * q + e, kl, a.causal) ? expf(v[e] - mx) : 0.f;
             const float s = row16_sum(p[e]);
             if (r == 0) rsum[wave][4 * q + e] = s;
         }
@@ -539,14 +543,14 @@ __global__ void __launch_bounds__(kAttnThreads) attn_bwd_kernel(const AttnArgs a
 bool attn_fused_ok(int T, int hd) { return T >= 1 && T <= kMax && hd >= 2 && hd <= kMax && hd % 2 == 0; }
 
 int attn_fwd(const float* qkv, const float2* cs, float* P, float* ctx, int B, int H, int T, int hd, float scale,
-             int causal, hipStream_t s)
+             int causal, hipStream_t s, const int* wlen)
 {
     if (!attn_fused_ok(T, hd)) return fail(LHIP_E_UNSUPPORTED, "attn_fwd: T=%d hd=%d outside the fused limits", T, hd);
     if (!qkv || !cs || !P || !ctx) return fail(LHIP_E_NULL, "attn_fwd: NULL argument");
     AttnArgs a{};
     a.qkv = qkv; a.cs = cs; a.P = P; a.ctx = ctx;
     a.B = B; a.H = H; a.T = T; a.hd = hd; a.D = H * hd; a.N = B * T;
-    a.scale = scale; a.causal = causal;
+    a.scale = scale; a.causal = causal; a.wlen = wlen;
     a.vec = (hd % 4 == 0 && aligned16(qkv) && aligned16(cs)) ? 1 : 0;
     a.vec = a.vec && aligned16(ctx);
     attn_fwd_kernel<<<B * H * ((T + 15) / 16), kAttnThreads, 0, s>>>(a);

@@ -141,8 +141,11 @@ int softmax_fwd(const float* x, float* y, int rows, int cols, float scale, int c
 int softmax_bwd(const float* y, const float* dy, float* dx, int rows, int cols, float scale, int causal,
                 int offset, int group, int accumulate, hipStream_t s);
 // amax (optional): first index of each row's maximum logit, written in the same pass
+// row_len (may be NULL): per-window row counts, window = row / period; a
+// counted row's gradient scale is then gscale / row_len[window]
 int ce_fused(const float* logits, const int* tgt, float* losses, float* dlogits, int rows, int V,
-             int ignore_index, float gscale, hipStream_t s, int* amax = nullptr);
+             int ignore_index, float gscale, hipStream_t s, int* amax = nullptr, const int* row_len = nullptr,
+             int period = 0);
 int argmax_rows(const float* x, int* out, int rows, int cols, hipStream_t s);
 int swiglu_fwd(const float* g, int ldg, const float* u, int ldu, float* h, int ldh, int rows, int cols,
                hipStream_t s);
@@ -212,8 +215,10 @@ int lm_checkpoint_io(const lhip_lm_config_t& cfg, float* dev_params, const char*
 // workgroup per (window, head, 16-row block); the backward reads the forward's
 // ctx (O) for rowsum(dO o O).
 bool attn_fused_ok(int T, int hd);
+// wlen (may be NULL): keys of each window; keys at or past it are masked (the
+// backward reads the masked P, so it needs no limit of its own)
 int attn_fwd(const float* qkv, const float2* cs, float* P, float* ctx, int B, int H, int T, int hd, float scale,
-             int causal, hipStream_t s);
+             int causal, hipStream_t s, const int* wlen = nullptr);
 int attn_bwd(const float* qkv, const float2* cs, const float* P, const float* ctx, const float* dctx, float* dqkv, int B,
              int H, int T, int hd, float scale, int causal, hipStream_t s);
 

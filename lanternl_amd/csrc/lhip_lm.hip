@@ -40,10 +40,11 @@ enum { OPT_SGD = 0, OPT_ADAMW = 1 };
 
 // Optimizer hyper-parameters of one step.  Eager launches pass them by value;
 // a captured step reads them from the device copy m.hyper, laid out as
-// {lr, momentum, wd, clip, nesterov, beta1, beta2, eps, parity}, which
-// set_hyper_kernel refreshes before each replay.
+// {lr, momentum, wd, clip, nesterov, beta1, beta2, eps, parity, gscale}, which
+// set_hyper_kernel refreshes before each replay.  gscale is the batch's
+// scale_grads factor, 1/n for n > 1 windows (lmtrain.lua:1211).
 struct Hyper {
-    float lr, momentum, wd, clip, nesterov, beta1, beta2, eps, parity;
+    float lr, momentum, wd, clip, nesterov, beta1, beta2, eps, parity, gscale;
     int opt;
 };
 
@@ -51,7 +52,7 @@ __global__ void set_hyper_kernel(float* hp, const Hyper h)
 {
     if (threadIdx.x == 0) {
         hp[0] = h.lr; hp[1] = h.momentum; hp[2] = h.wd; hp[3] = h.clip; hp[4] = h.nesterov;
-        hp[5] = h.beta1; hp[6] = h.beta2; hp[7] = h.eps; hp[8] = h.parity;
+        hp[5] = h.beta1; hp[6] = h.beta2; hp[7] = h.eps; hp[8] = h.parity; hp[9] = h.gscale;
     }
 }
 
@@ -64,6 +65,7 @@ struct LmModel {
     size_t arena_bytes = 0;
     float *params = nullptr, *grads = nullptr, *vel = nullptr;
     int *ids = nullptr, *tgt = nullptr, *amax = nullptr, *applied = nullptr;
+    int* wlen = nullptr;          // tokens of each window slot (0: empty slot)
     float *losses = nullptr, *gnorm = nullptr, *hyper = nullptr;
     float *adam_m = nullptr, *adam_v = nullptr;   // AdamW moments
     int* tcount = nullptr;                         // AdamW step count, two parity slots
@@ -92,7 +94,9 @@ struct LmModel {
     hipGraphExec_t exec = nullptr;
     int steps = 0;
     bool have_batch = false;
-    std::vector<int> h_tgt;
+    std::vector<int> h_tgt;       // targets per row, -1 past a window's length
+    std::vector<int> h_len;       // window lengths (0 for empty slots)
+    int nwin = 0;                 // windows in the batch (slots 0 .. nwin-1)
 
     const float* prm(int tensor) const { return params + off[tensor]; }
     float* grd(int tensor) const { return grads + off[tensor]; }
@@ -239,7 +243,7 @@ int enqueue_step(LmModel& m, hipStream_t s, const Hyper& hp, bool device_hyper)
         if (m.fused_attn) {
             // RoPE, scores, causal softmax and P.v per (window, head) in one launch;
             // qkv keeps the unrotated q, k (the backward rotates again)
-            LM_TRY(attn_fwd(qkv, m.rope_cs, P, ctx, m.B, H, T, hd, scale, causal, s));
+            LM_TRY(attn_fwd(qkv, m.rope_cs, P, ctx, m.B, H, T, hd, scale, causal, s, m.wlen));
         } else {
             // RoPE on q and k (2N rows, positions row % T), interleaved pairs
             LM_TRY(rope(qkv, nullptr, 2 * N, H, hd, D, 0, T, base, 1, 0, s));
@@ -273,8 +277,9 @@ int enqueue_step(LmModel& m, hipStream_t s, const Hyper& hp, bool device_hyper)
     LM_TRY(rmsnorm_fwd(xL, lnf, m.xf, m.invf, N, D, eps, s));
     // tied head: logits = xf . emb^T
     LM_TRY(q.gemm(0, 1, N, V, D, m.xf, D, emb, D, 0.f, m.logits, V));
-    // per-row losses; dlogits = (softmax - onehot) / T written over the logits
-    LM_TRY(ce_fused(m.logits, m.tgt, m.losses, m.logits, N, V, -1, 1.0f / T, s, m.amax));
+    // per-row losses; dlogits = (softmax - onehot) / len(window) written over
+    // the logits; rows past a window's length (target -1) give 0 and 0
+    LM_TRY(ce_fused(m.logits, m.tgt, m.losses, m.logits, N, V, -1, 1.0f, s, m.amax, m.wlen, T));
 
     // ---------------- backward ----------------
     // The chain dlogits -> dx_L -> ... -> dx_0 first, then the weight gradients.
@@ -436,7 +441,7 @@ int enqueue_step(LmModel& m, hipStream_t s, const Hyper& hp, bool device_hyper)
     // ---------------- optimizer (lmtrain.lua:1212-1226) ----------------
     // squared-norm partials; the optimizer kernel finishes the sum itself
     LM_TRY(sumsq_partials(m.grads, m.nparam, m.ss_part, m.ss_blocks, s));
-    const float gscale = m.B > 1 ? 1.0f / m.B : 1.0f;
+    const float gscale = hp.gscale;
     const float* hdev = device_hyper ? m.hyper : nullptr;
     if (hp.opt == OPT_ADAMW)
         LM_TRY(adamw_step(m.params, m.grads, m.adam_m, m.adam_v, m.nparam, m.ss_part, m.ss_blocks, hp.lr, hp.beta1,
@@ -480,9 +485,10 @@ int capture_step(LmModel& m, hipStream_t s, const Hyper& hp)
 
 // One step with the given optimizer: graph replay (capturing first when
 // needed) or eager launches.
-int run_step(LmModel& m, const Hyper& hp)
+int run_step(LmModel& m, Hyper hp)
 {
     hipStream_t s = st().stream;
+    hp.gscale = m.nwin > 1 ? 1.0f / static_cast<float>(m.nwin) : 1.0f;   // optim2.scale_grads(1/n)
     if (m.use_graph) {
         set_hyper_kernel<<<1, 64, 0, s>>>(m.hyper, hp);
         if (int rc = check_launch("lm step: hyper")) return rc;
@@ -576,6 +582,7 @@ LHIP_API int lhip_lm_create(const lhip_lm_config_t* cfg, void** model)
         {reinterpret_cast<void**>(&m->ids), sizeof(int) * N},
         {reinterpret_cast<void**>(&m->tgt), sizeof(int) * N},
         {reinterpret_cast<void**>(&m->amax), sizeof(int) * N},
+        {reinterpret_cast<void**>(&m->wlen), sizeof(int) * m->B},
         {reinterpret_cast<void**>(&m->applied), sizeof(int) * 4},
         {reinterpret_cast<void**>(&m->losses), sizeof(float) * N},
         {reinterpret_cast<void**>(&m->gnorm), sizeof(float) * 4},
@@ -661,6 +668,7 @@ LHIP_API int lhip_lm_create(const lhip_lm_config_t* cfg, void** model)
     m->fused_attn = lhip::attn_fused_ok(m->T, m->hd);
     m->fused_gemm = lhip::lm_fuse_ok(m->D, m->D, m->D) && m->F % 4 == 0;
     m->h_tgt.assign(static_cast<size_t>(N), 0);
+    m->h_len.assign(static_cast<size_t>(m->B), 0);
     *model = m;
     return LHIP_OK;
 }
@@ -710,26 +718,60 @@ LHIP_API int lhip_lm_set_velocity(void* model, const float* host, long long n)
 
 LHIP_API int lhip_lm_get_velocity(void* model, float* host, long long n) { return lm_copy(model, host, n, 2, 0); }
 
-LHIP_API int lhip_lm_set_batch(void* model, const int* ids, const int* targets)
+LHIP_API int lhip_lm_set_batch_ex(void* model, const int* ids, const int* targets, const int* lengths,
+                                  int n_windows)
 {
     LHIP_REQUIRE_READY();
     LHIP_REFUSE_RECORDING();
     if (!model || !ids || !targets) return fail(LHIP_E_NULL, "lhip_lm_set_batch: NULL argument");
     auto* m = lhip::as_model(model);
-    for (int i = 0; i < m->N; ++i) {
-        if (ids[i] < 0 || ids[i] >= m->V)
-            return fail(LHIP_E_ARG, "lhip_lm_set_batch: ids[%d] = %d outside [0, %d)", i, ids[i], m->V);
-        if (targets[i] < 0 || targets[i] >= m->V)
-            return fail(LHIP_E_ARG, "lhip_lm_set_batch: targets[%d] = %d outside [0, %d)", i, targets[i], m->V);
+    if (n_windows < 1 || n_windows > m->B)
+        return fail(LHIP_E_SHAPE, "lhip_lm_set_batch: %d windows for %d slots", n_windows, m->B);
+    std::vector<int> len(static_cast<size_t>(m->B), 0);
+    bool short_batch = n_windows < m->B;
+    for (int b = 0; b < n_windows; ++b) {
+        len[b] = lengths ? lengths[b] : m->T;
+        if (len[b] < 1 || len[b] > m->T)
+            return fail(LHIP_E_SHAPE, "lhip_lm_set_batch: window %d has %d tokens, outside [1, %d]", b, len[b], m->T);
+        short_batch = short_batch || len[b] < m->T;
+    }
+    // Rows past a window's length (and empty slots) carry id 0, which keeps
+    // their forward finite, and target -1, which the CE turns into a zero
+    // loss and a zero gradient; with the causal mask, or the key limit of the
+    // fused attention, no counted row sees them.
+    if (short_batch && !m->c.causal && !m->fused_attn)
+        return fail(LHIP_E_UNSUPPORTED, "lhip_lm_set_batch: short windows in a non-causal model with seq %d or "
+                    "head_dim %d past the fused attention's limits", m->T, m->hd);
+    std::vector<int> hid(static_cast<size_t>(m->N), 0), htg(static_cast<size_t>(m->N), -1);
+    for (int b = 0; b < n_windows; ++b) {
+        for (int t = 0; t < len[b]; ++t) {
+            const size_t i = static_cast<size_t>(b) * m->T + t;
+            if (ids[i] < 0 || ids[i] >= m->V)
+                return fail(LHIP_E_ARG, "lhip_lm_set_batch: ids[%zu] = %d outside [0, %d)", i, ids[i], m->V);
+            if (targets[i] < 0 || targets[i] >= m->V)
+                return fail(LHIP_E_ARG, "lhip_lm_set_batch: targets[%zu] = %d outside [0, %d)", i, targets[i], m->V);
+            hid[i] = ids[i];
+            htg[i] = targets[i];
+        }
     }
     const size_t bytes = static_cast<size_t>(m->N) * sizeof(int);
-    LHIP_CHECK_HIP(hipMemcpyAsync(m->ids, ids, bytes, hipMemcpyHostToDevice, st().stream), "lhip_lm_set_batch: ids");
-    LHIP_CHECK_HIP(hipMemcpyAsync(m->tgt, targets, bytes, hipMemcpyHostToDevice, st().stream),
-                   "lhip_lm_set_batch: targets");
-    LHIP_CHECK_HIP(hipStreamSynchronize(st().stream), "lhip_lm_set_batch: sync");
-    std::memcpy(m->h_tgt.data(), targets, bytes);
+    hipStream_t s = st().stream;
+    LHIP_CHECK_HIP(hipMemcpyAsync(m->ids, hid.data(), bytes, hipMemcpyHostToDevice, s), "lhip_lm_set_batch: ids");
+    LHIP_CHECK_HIP(hipMemcpyAsync(m->tgt, htg.data(), bytes, hipMemcpyHostToDevice, s), "lhip_lm_set_batch: targets");
+    LHIP_CHECK_HIP(hipMemcpyAsync(m->wlen, len.data(), sizeof(int) * m->B, hipMemcpyHostToDevice, s),
+                   "lhip_lm_set_batch: lengths");
+    LHIP_CHECK_HIP(hipStreamSynchronize(s), "lhip_lm_set_batch: sync");
+    m->h_tgt = htg;
+    m->h_len = len;
+    m->nwin = n_windows;
     m->have_batch = true;
     return LHIP_OK;
+}
+
+LHIP_API int lhip_lm_set_batch(void* model, const int* ids, const int* targets)
+{
+    if (!model) return fail(LHIP_E_NULL, "lhip_lm_set_batch: NULL argument");
+    return lhip_lm_set_batch_ex(model, ids, targets, nullptr, lhip::as_model(model)->B);
 }
 
 LHIP_API int lhip_lm_use_graph(void* model, int on)
@@ -861,19 +903,23 @@ LHIP_API int lhip_lm_stats(void* model, lhip_lm_stats_t* out, float* window_loss
     LHIP_CHECK_HIP(hipMemcpyAsync(&applied, m->applied, sizeof(int), hipMemcpyDeviceToHost, s),
                    "lhip_lm_stats: applied");
     LHIP_CHECK_HIP(hipStreamSynchronize(s), "lhip_lm_stats: sync");
-    // per-window mean of the row losses (Tensor.cross_entropy's mean over T),
-    // then the mean over windows
+    // each window's mean over its own tokens (Tensor.cross_entropy), then the
+    // batch loss LMTrain reports: sum_w loss_w * len_w / sum_w len_w
+    // (lmtrain.lua:1197-1198,1233-1234); empty slots report 0
     double total = 0.0;
+    long long tokens = 0;
     for (int b = 0; b < m->B; ++b) {
+        const int len = m->h_len[b];
         double w = 0.0;
-        for (int t = 0; t < m->T; ++t) w += losses[static_cast<size_t>(b) * m->T + t];
-        w /= m->T;
+        for (int t = 0; t < len; ++t) w += losses[static_cast<size_t>(b) * m->T + t];
+        if (len > 0) w /= len;
         if (window_losses) window_losses[b] = static_cast<float>(w);
-        total += w;
+        total += w * len;
+        tokens += len;
     }
     int correct = 0;
     for (int i = 0; i < m->N; ++i) correct += am[i] == m->h_tgt[i];
-    out->loss = static_cast<float>(total / m->B);
+    out->loss = static_cast<float>(tokens > 0 ? total / tokens : 0.0);
     out->grad_norm = gn;
     out->applied = applied;
     out->correct = correct;

@@ -124,7 +124,7 @@ sgd_step_kernel(float* __restrict__ p, float* __restrict__ g, float* __restrict_
 {
     if (hyper) {   // hyper-parameters resident on the device (graph replay)
         lr = hyper[0]; momentum = hyper[1]; wd = hyper[2]; clip_norm = hyper[3];
-        nesterov = hyper[4] != 0.f;
+        nesterov = hyper[4] != 0.f; grad_scale = hyper[9];
     }
     const SgdHyper hy{lr, momentum, wd, grad_scale, nesterov};
     const long long t0 = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
@@ -181,7 +181,7 @@ sgd_step_kernel(float* __restrict__ p, float* __restrict__ g, float* __restrict_
 // (advanced only when the step applies) to tcount[parity ^ 1], so no block
 // can read a half-updated counter; the caller alternates parity per call.
 // Device hyper-parameters (graph replay): {lr, -, wd, clip, -, beta1, beta2,
-// eps, parity}.
+// eps, parity, grad_scale}.
 __global__ void __launch_bounds__(256)
 adamw_step_kernel(float* __restrict__ p, float* __restrict__ g, float* __restrict__ m, float* __restrict__ v,
                   long long n, const double* __restrict__ sumsq, int nparts, float lr, float beta1, float beta2,
@@ -192,6 +192,7 @@ adamw_step_kernel(float* __restrict__ p, float* __restrict__ g, float* __restric
     if (hyper) {
         lr = hyper[0]; wd = hyper[2]; clip_norm = hyper[3];
         beta1 = hyper[5]; beta2 = hyper[6]; eps = hyper[7]; parity = hyper[8] != 0.f ? 1 : 0;
+        grad_scale = hyper[9];
     }
     const double norm = static_cast<double>(grad_scale) * sqrt(grad_total(sumsq, nparts));
     const bool finite = isfinite(norm);

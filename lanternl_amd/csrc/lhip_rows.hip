@@ -497,11 +497,15 @@ softmax_bwd_generic(const float* __restrict__ y, const float* __restrict__ dy, f
 // Per row r with target t: rows with t < 0, t >= V or t == ignore_index give
 // loss 0 and dlogits 0; otherwise loss[r] = logsumexp(x) - x[t] and
 // dlogits = gscale * (softmax(x) - onehot(t)).  dlogits may alias logits.
+// With row_len (the LM step's windows of `period` rows), a counted row's scale
+// is gscale / row_len[row / period]: each window's CE is the mean over its
+// own length (tensor2.lua:845-857).
 // (tensor2.lua:809-882 per row; cuda/luaTL_train.cu:837-878 contract.)
 template <int NT, int NV, bool PF>
 __global__ void __launch_bounds__(NT)
 ce_fused_vec(const float* logits, const int* __restrict__ tgt, float* __restrict__ losses,
-             float* dlogits, int* __restrict__ amax, int rows, int V, int ignore_index, float gscale)
+             float* dlogits, int* __restrict__ amax, int rows, int V, int ignore_index, float gscale,
+             const int* __restrict__ row_len, int period)
 {
     // One workgroup per row at a time.  With PF, rows are walked block-stride
     // and the next row is prefetched into registers while the current one is
@@ -565,6 +569,7 @@ ce_fused_vec(const float* logits, const int* __restrict__ tgt, float* __restrict
         if (losses && threadIdx.x == 0) losses[row] = (mx + logf(sum)) - xt;
         if (dlogits) {
             const float is = 1.0f / sum;
+            const float gs = row_len ? gscale / static_cast<float>(row_len[row / period]) : gscale;
             float4* dr = reinterpret_cast<float4*>(dlogits + base);
 #pragma unroll
             for (int i = 0; i < NV; ++i) {
@@ -575,7 +580,7 @@ ce_fused_vec(const float* logits, const int* __restrict__ tgt, float* __restrict
                     for (int e = 0; e < 4; ++e) {
                         float p = f4get(v[i], e) * is;
                         if (4 * c + e == t) p -= 1.f;
-                        f4set(o, e, gscale * p);
+                        f4set(o, e, gs * p);
                     }
                     st_stream(dr + c, o);
                 }
@@ -608,7 +613,8 @@ ce_fused_vec(const float* logits, const int* __restrict__ tgt, float* __restrict
 
 __global__ void __launch_bounds__(256)
 ce_fused_generic(const float* logits, const int* __restrict__ tgt, float* __restrict__ losses,
-                 float* dlogits, int* __restrict__ amax, int rows, int V, int ignore_index, float gscale)
+                 float* dlogits, int* __restrict__ amax, int rows, int V, int ignore_index, float gscale,
+                 const int* __restrict__ row_len, int period)
 {
     __shared__ float red[4];
     __shared__ float redv[4];
@@ -639,11 +645,12 @@ ce_fused_generic(const float* logits, const int* __restrict__ tgt, float* __rest
     if (losses && threadIdx.x == 0) losses[row] = (mx + logf(sum)) - xt;
     if (dlogits) {
         const float is = 1.0f / sum;
+        const float gs = row_len ? gscale / static_cast<float>(row_len[row / period]) : gscale;
         // every element is read before the same thread overwrites it
         for (int c = threadIdx.x; c < V; c += 256) {
             float p = expf(logits[base + c] - mx) * is;
             if (c == t) p -= 1.f;
-            dlogits[base + c] = gscale * p;
+            dlogits[base + c] = gs * p;
         }
     }
 }
@@ -846,23 +853,28 @@ int softmax_bwd(const float* y, const float* dy, float* dx, int rows, int cols, 
 }
 
 int ce_fused(const float* logits, const int* tgt, float* losses, float* dlogits, int rows, int V,
-             int ignore_index, float gscale, hipStream_t s, int* amax)
+             int ignore_index, float gscale, hipStream_t s, int* amax, const int* row_len, int period)
 {
     if (rows < 0 || V <= 0) return fail(LHIP_E_SHAPE, "ce_fused: rows=%d vocab=%d", rows, V);
     if (rows == 0) return LHIP_OK;
     if (!logits || !tgt) return fail(LHIP_E_NULL, "ce_fused: NULL logits/targets");
+    if (row_len && period <= 0) return fail(LHIP_E_ARG, "ce_fused: window period %d must be > 0", period);
     const bool vec = V % 4 == 0 && aligned16(logits) && (!dlogits || aligned16(dlogits));
     const int cus = st().cu_count > 0 ? st().cu_count : 256;
     // rows walked block-stride: about 2 rows per workgroup once rows exceed the CUs
     const int nb_small = rows < 4 * cus ? rows : 4 * cus;
     if (vec && V <= 256 * 4 * 2)
-        ce_fused_vec<256, 2, true><<<nb_small, 256, 0, s>>>(logits, tgt, losses, dlogits, amax, rows, V, ignore_index, gscale);
+        ce_fused_vec<256, 2, true><<<nb_small, 256, 0, s>>>(logits, tgt, losses, dlogits, amax, rows, V, ignore_index, gscale,
+                                                          row_len, period);
     else if (vec && V <= 256 * 4 * 8)
-        ce_fused_vec<256, 8, true><<<nb_small, 256, 0, s>>>(logits, tgt, losses, dlogits, amax, rows, V, ignore_index, gscale);
+        ce_fused_vec<256, 8, true><<<nb_small, 256, 0, s>>>(logits, tgt, losses, dlogits, amax, rows, V, ignore_index, gscale,
+                                                          row_len, period);
     else if (vec && V <= 1024 * 4 * 8)
-        ce_fused_vec<1024, 8, false><<<rows, 1024, 0, s>>>(logits, tgt, losses, dlogits, amax, rows, V, ignore_index, gscale);
+        ce_fused_vec<1024, 8, false><<<rows, 1024, 0, s>>>(logits, tgt, losses, dlogits, amax, rows, V, ignore_index, gscale,
+                                                          row_len, period);
     else
-        ce_fused_generic<<<rows, 256, 0, s>>>(logits, tgt, losses, dlogits, amax, rows, V, ignore_index, gscale);
+        ce_fused_generic<<<rows, 256, 0, s>>>(logits, tgt, losses, dlogits, amax, rows, V, ignore_index, gscale,
+                                                          row_len, period);
     return check_launch("ce_fused");
 }
 

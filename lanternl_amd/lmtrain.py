@@ -10,8 +10,12 @@ all on the device.  ``save_checkpoint`` / ``load_checkpoint`` and
 ``GpuLMStep.save`` / ``load`` read and write the lmio v3 checkpoint format
 (ai/optim/lmio.lua).  Ids are 0-based here (Lua's are 1-based).
 
-Windows must be full (``seq`` tokens each); the reference's shorter trailing
-window of a sequence is not supported by the device step.
+Batches may be ragged as LMTrain's are: ``pack_windows`` lays out up to
+``batch`` windows of up to ``seq`` tokens each (the short trailing window that
+build_windows cuts at a sequence's end, and the short last batch of an epoch)
+for ``GpuLMStep.set_batch``.  Each window's loss is the mean over its own
+tokens and the summed gradients are scaled by 1/n_in_batch, as in
+lmtrain.lua:1183-1212.
 """
 import ctypes
 
@@ -40,6 +44,24 @@ def build_windows(sequences, max_seq, stride=None):
                 break
             start += stride
     return windows
+
+
+def pack_windows(windows, batch, seq):
+    """Lay out up to `batch` windows [(inp, tgt, n)] (build_windows' tuples) as
+    (ids, targets, lengths, n_windows) for GpuLMStep.set_batch: window b at row
+    b, its n tokens first, the rest of the row and the unused rows zero."""
+    if not 1 <= len(windows) <= batch:
+        raise ValueError(f"{len(windows)} windows for a batch of {batch}")
+    ids = np.zeros((batch, seq), np.int32)
+    tgt = np.zeros((batch, seq), np.int32)
+    lens = np.zeros(batch, np.int32)
+    for b, (inp, out, n) in enumerate(windows):
+        if not 1 <= n <= seq or len(inp) < n or len(out) < n:
+            raise ValueError(f"window {b}: {n} tokens, expected 1..{seq}")
+        ids[b, :n] = inp[:n]
+        tgt[b, :n] = out[:n]
+        lens[b] = n
+    return ids, tgt, lens, len(windows)
 
 
 def config(vocab, dim, layers, heads, ffn, batch, seq, causal=True, eps=1e-5, rope_base=10000.0):
@@ -147,12 +169,23 @@ class GpuLMStep:
     def velocity(self):
         return self._vec("lhip_lm_get_velocity")
 
-    def set_batch(self, ids, targets):
+    def set_batch(self, ids, targets, lengths=None, n_windows=None):
+        """(batch, seq) ids and targets; optionally each window's token count
+        (`lengths`, tokens first in its row) and the number of windows used
+        (`n_windows`), for LMTrain's short last window and short last batch."""
         ids = np.ascontiguousarray(ids, dtype=np.int32).reshape(-1)
         tgt = np.ascontiguousarray(targets, dtype=np.int32).reshape(-1)
         if ids.size != self.batch * self.seq or tgt.size != ids.size:
             raise ValueError(f"expected {self.batch}x{self.seq} ids and targets")
-        call("lhip_lm_set_batch", self._h, ids.ctypes.data, tgt.ctypes.data)
+        if lengths is None and n_windows is None:
+            call("lhip_lm_set_batch", self._h, ids.ctypes.data, tgt.ctypes.data)
+            return
+        nw = self.batch if n_windows is None else int(n_windows)
+        lens = None if lengths is None else np.ascontiguousarray(lengths, dtype=np.int32).reshape(-1)
+        if lens is not None and lens.size < nw:
+            raise ValueError(f"{lens.size} lengths for {nw} windows")
+        call("lhip_lm_set_batch_ex", self._h, ids.ctypes.data, tgt.ctypes.data,
+             None if lens is None else lens.ctypes.data, nw)
 
     def use_graph(self, on=True):
         call("lhip_lm_use_graph", self._h, int(bool(on)))

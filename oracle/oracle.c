@@ -743,20 +743,26 @@ double or_lm_window(const or_lm_cfg* c, const double* params, const int* ids, co
 /* the batch part of lmtrain.lua:1183-1222 shared by both optimizers: zero
  * grads, every window, scale 1/B, norm, finite check, clip.  Returns 1 when
  * the optimizer step is to be applied. */
+/* lmtrain.lua:1183-1226: windows b < nwin, window b holding lens[b] tokens
+ * (lens NULL: T) at ids/tgt + b*T (build_windows' short last window,
+ * lmtrain.lua:535-558); each window's loss is its own mean
+ * (tensor2.lua:845-857); gradients summed, then scaled by 1/nwin when nwin > 1
+ * (the short last batch runs n_in_batch windows). */
 static int lm_batch_grads(const or_lm_cfg* c, const double* params, const int* ids, const int* tgt,
-                          int B, int T, double clip_norm, double* losses, double* gnorm, int* correct,
-                          double* grads)
+                          int nwin, int T, const int* lens, double clip_norm, double* losses, double* gnorm,
+                          int* correct, double* grads)
 {
     const long n = or_lm_num_params(c);
     for (long e = 0; e < n; ++e) grads[e] = 0;                       /* opt.zero_grad() */
     int corr = 0;
-    for (int b = 0; b < B; ++b) {
-        const double l = or_lm_window(c, params, ids + (long)b * T, tgt + (long)b * T, T,
+    for (int b = 0; b < nwin; ++b) {
+        const int len = lens ? lens[b] : T;
+        const double l = or_lm_window(c, params, ids + (long)b * T, tgt + (long)b * T, len,
                                       grads, NULL, &corr);
         if (losses) losses[b] = l;
     }
     if (correct) *correct = corr;
-    if (B > 1) or_scale(grads, n, 1.0 / B);                          /* scale_grads */
+    if (nwin > 1) or_scale(grads, n, 1.0 / nwin);                    /* scale_grads */
     const double norm = or_grad_norm(grads, n);
     if (gnorm) *gnorm = norm;
     if (!(norm == norm) || norm == HUGE_VAL || norm == -HUGE_VAL) return 0;
@@ -771,7 +777,16 @@ int or_lm_step_adamw(const or_lm_cfg* c, double* params, double* m, double* v, i
                      double lr, double b1, double b2, double eps, double wd, double clip_norm,
                      double* losses, double* gnorm, int* correct, double* grads)
 {
-    if (!lm_batch_grads(c, params, ids, tgt, B, T, clip_norm, losses, gnorm, correct, grads)) return 0;
+    return or_lm_step_adamw_ex(c, params, m, v, t, ids, tgt, B, T, NULL, lr, b1, b2, eps, wd, clip_norm,
+                               losses, gnorm, correct, grads);
+}
+
+int or_lm_step_adamw_ex(const or_lm_cfg* c, double* params, double* m, double* v, int* t,
+                        const int* ids, const int* tgt, int nwin, int T, const int* lens,
+                        double lr, double b1, double b2, double eps, double wd, double clip_norm,
+                        double* losses, double* gnorm, int* correct, double* grads)
+{
+    if (!lm_batch_grads(c, params, ids, tgt, nwin, T, lens, clip_norm, losses, gnorm, correct, grads)) return 0;
     *t = *t + 1;
     or_adamw_step(params, grads, m, v, or_lm_num_params(c), lr, b1, b2, eps, wd, *t);
     return 1;
@@ -783,7 +798,16 @@ int or_lm_step_sgd(const or_lm_cfg* c, double* params, double* vel,
                    double lr, double momentum, double wd, double clip_norm,
                    double* losses, double* gnorm, int* correct, double* grads)
 {
-    if (!lm_batch_grads(c, params, ids, tgt, B, T, clip_norm, losses, gnorm, correct, grads)) return 0;
+    return or_lm_step_sgd_ex(c, params, vel, ids, tgt, B, T, NULL, lr, momentum, wd, clip_norm, losses, gnorm,
+                             correct, grads);
+}
+
+int or_lm_step_sgd_ex(const or_lm_cfg* c, double* params, double* vel,
+                      const int* ids, const int* tgt, int nwin, int T, const int* lens,
+                      double lr, double momentum, double wd, double clip_norm,
+                      double* losses, double* gnorm, int* correct, double* grads)
+{
+    if (!lm_batch_grads(c, params, ids, tgt, nwin, T, lens, clip_norm, losses, gnorm, correct, grads)) return 0;
     or_sgd_step(params, grads, vel, or_lm_num_params(c), lr, momentum, wd, 0);
     return 1;
 }

@@ -179,6 +179,19 @@ int or_lm_step_sgd(const or_lm_cfg* c, double* params, double* vel,
                    double lr, double momentum, double wd, double clip_norm,
                    double* losses, double* gnorm, int* correct, double* grads);
 
+/* The same over a ragged batch: windows b < nwin (nwin <= B; the short last
+ * batch), window b holding lens[b] <= T tokens at ids/tgt + b*T (lens NULL:
+ * T each; build_windows' short last window, lmtrain.lua:535-558); each
+ * window's loss is its own mean and the summed grads are scaled by 1/nwin. */
+int or_lm_step_sgd_ex(const or_lm_cfg* c, double* params, double* vel,
+                      const int* ids, const int* tgt, int nwin, int T, const int* lens,
+                      double lr, double momentum, double wd, double clip_norm,
+                      double* losses, double* gnorm, int* correct, double* grads);
+int or_lm_step_adamw_ex(const or_lm_cfg* c, double* params, double* m, double* v, int* t,
+                        const int* ids, const int* tgt, int nwin, int T, const int* lens,
+                        double lr, double b1, double b2, double eps, double wd, double clip_norm,
+                        double* losses, double* gnorm, int* correct, double* grads);
+
 /* The same step with optimizer="adamw": *t (the AdamW step count) is advanced
  * and the AdamW update applied only when the norm is finite.  m, v: moments. */
 int or_lm_step_adamw(const or_lm_cfg* c, double* params, double* m, double* v, int* t,

@@ -87,6 +87,11 @@ def _declare(L):
         "or_lm_step_adamw": (c_int, [ctypes.POINTER(LmCfg), _D, _D, _D, _I, _I, _I, c_int, c_int,
                                      c_double, c_double, c_double, c_double, c_double, c_double,
                                      _D, _D, _I, _D]),
+        "or_lm_step_sgd_ex": (c_int, [ctypes.POINTER(LmCfg), _D, _D, _I, _I, c_int, c_int, _I,
+                                      c_double, c_double, c_double, c_double, _D, _D, _I, _D]),
+        "or_lm_step_adamw_ex": (c_int, [ctypes.POINTER(LmCfg), _D, _D, _D, _I, _I, _I, c_int, c_int, _I,
+                                        c_double, c_double, c_double, c_double, c_double, c_double,
+                                        _D, _D, _I, _D]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -355,39 +360,54 @@ def lm_window(cfg, params, ids, tgt, grads=None):
     return loss, grads, logits, corr.value
 
 
-def lm_step_sgd(cfg, params, vel, ids, tgt, lr, momentum=0.9, wd=0.01, clip_norm=1.0):
+def _ragged(ids, lens, nwin):
+    B, T = ids.shape
+    nwin = B if nwin is None else int(nwin)
+    assert 1 <= nwin <= B
+    if lens is None:
+        return nwin, None, _nul(_I)
+    lens, pl = _i(lens)
+    assert lens.size >= nwin and np.all((lens[:nwin] >= 1) & (lens[:nwin] <= T))
+    return nwin, lens, pl
+
+
+def lm_step_sgd(cfg, params, vel, ids, tgt, lr, momentum=0.9, wd=0.01, clip_norm=1.0, lens=None, nwin=None):
     """One LMTrain batch step (optimizer="sgd"); params/vel float64 updated in place.
 
-    ids/tgt are (B, T) 0-based.  Returns dict(losses, gnorm, correct, grads, applied).
+    ids/tgt are (B, T) 0-based; windows b < nwin (default B), window b holding
+    lens[b] tokens (default T).  Returns dict(losses, gnorm, correct, grads, applied).
     """
     assert params.dtype == np.float64 and vel.dtype == np.float64
     ids, pi = _i(ids); tgt, pt = _i(tgt)
     B, T = ids.shape
+    nwin, lens_keep, pl = _ragged(ids, lens, nwin)
     losses = np.zeros(B); grads = np.zeros(params.size)
     gn = ctypes.c_double(0); corr = ctypes.c_int(0)
-    applied = lib().or_lm_step_sgd(ctypes.byref(cfg), params.ctypes.data_as(_D),
-                                   vel.ctypes.data_as(_D), pi, pt, B, T, lr, momentum, wd,
-                                   clip_norm, losses.ctypes.data_as(_D), ctypes.byref(gn),
-                                   ctypes.byref(corr), grads.ctypes.data_as(_D))
+    applied = lib().or_lm_step_sgd_ex(ctypes.byref(cfg), params.ctypes.data_as(_D),
+                                      vel.ctypes.data_as(_D), pi, pt, nwin, T, pl, lr, momentum, wd,
+                                      clip_norm, losses.ctypes.data_as(_D), ctypes.byref(gn),
+                                      ctypes.byref(corr), grads.ctypes.data_as(_D))
     return dict(losses=losses, gnorm=gn.value, correct=corr.value, grads=grads,
                 applied=bool(applied))
 
 
 def lm_step_adamw(cfg, params, m, v, t, ids, tgt, lr, beta1=0.9, beta2=0.95, eps=1e-8, wd=0.01,
-                  clip_norm=1.0):
+                  clip_norm=1.0, lens=None, nwin=None):
     """One LMTrain batch step (optimizer="adamw"); params, m, v float64 updated in
-    place.  t is the AdamW step count before the call.  Returns dict(losses,
-    gnorm, correct, grads, applied, t) with t advanced when the step applied."""
+    place.  t is the AdamW step count before the call; lens/nwin as lm_step_sgd.
+    Returns dict(losses, gnorm, correct, grads, applied, t) with t advanced when
+    the step applied."""
     for a in (params, m, v):
         assert a.dtype == np.float64
     ids, pi = _i(ids); tgt, pt = _i(tgt)
     B, T = ids.shape
+    nwin, lens_keep, pl = _ragged(ids, lens, nwin)
     losses = np.zeros(B); grads = np.zeros(params.size)
     gn = ctypes.c_double(0); corr = ctypes.c_int(0); tc = ctypes.c_int(int(t))
-    applied = lib().or_lm_step_adamw(ctypes.byref(cfg), params.ctypes.data_as(_D), m.ctypes.data_as(_D),
-                                     v.ctypes.data_as(_D), ctypes.byref(tc), pi, pt, B, T, lr, beta1,
-                                     beta2, eps, wd, clip_norm, losses.ctypes.data_as(_D),
-                                     ctypes.byref(gn), ctypes.byref(corr), grads.ctypes.data_as(_D))
+    applied = lib().or_lm_step_adamw_ex(ctypes.byref(cfg), params.ctypes.data_as(_D), m.ctypes.data_as(_D),
+                                        v.ctypes.data_as(_D), ctypes.byref(tc), pi, pt, nwin, T, pl, lr, beta1,
+                                        beta2, eps, wd, clip_norm, losses.ctypes.data_as(_D),
+                                        ctypes.byref(gn), ctypes.byref(corr), grads.ctypes.data_as(_D))
     return dict(losses=losses, gnorm=gn.value, correct=corr.value, grads=grads,
                 applied=bool(applied), t=tc.value)
 

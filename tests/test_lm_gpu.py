@@ -377,3 +377,96 @@ def test_lm_checkpoint_save_load_device(tmp_path):
     with pytest.raises(Exception):
         lmtrain.GpuLMStep(V, 48, L, H, F, B, T).load(tmp_path / "dev.bin")
     a.close(); b.close()
+
+
+# ------------------------------------------------- ragged batches (LMTrain's last window / last batch)
+def _ragged_case(V, D, L, H, F, B, T, plan, graph, causal=True, opt="sgd", seed=77):
+    """plan: per step (lengths, n_windows) or None for a full batch."""
+    rng = np.random.default_rng(seed)
+    cfg = O.lm_cfg(V, D, L, H, F, causal=causal)
+    gpu = lmtrain.GpuLMStep(V, D, L, H, F, B, T, causal=causal)
+    gpu.set_params(lmtrain.init_params(gpu.cfg, rng, 0.02))
+    if graph:
+        gpu.use_graph(True)
+    t = 0
+    for k, item in enumerate(plan):
+        announce("lm ragged", k, item, "graph" if graph else "eager", opt, "causal" if causal else "full")
+        ids = rng.integers(0, V, (B, T)).astype(np.int32)
+        tgt = rng.integers(0, V, (B, T)).astype(np.int32)
+        if item is None:
+            lens, nw = np.full(B, T, np.int32), B
+            gpu.set_batch(ids, tgt)
+        else:
+            lens = np.zeros(B, np.int32)
+            lens[:len(item)] = item
+            nw = len(item)
+            # junk past each window's length and in the unused slots must not matter
+            gpu.set_batch(ids, tgt, lens, nw)
+        p_before = gpu.params().astype(np.float64)
+        if opt == "sgd":
+            v_before = gpu.velocity().astype(np.float64)
+            gpu.step(0.05, 0.9, 0.01, 1.0)
+            ref_p, ref_v = p_before.copy(), v_before.copy()
+            ref = O.lm_step_sgd(cfg, ref_p, ref_v, ids, tgt, 0.05, 0.9, 0.01, 1.0, lens=lens, nwin=nw)
+        else:
+            m0, v0, t0 = gpu.adam_state()
+            gpu.step_adamw(1e-3, 0.9, 0.95, 1e-8, 0.01, 1.0)
+            ref_p, ref_m, ref_v = p_before.copy(), m0.astype(np.float64), v0.astype(np.float64)
+            ref = O.lm_step_adamw(cfg, ref_p, ref_m, ref_v, t0, ids, tgt, 1e-3, lens=lens, nwin=nw)
+        st = gpu.stats()
+        wl = st["window_losses"]
+        assert np.max(np.abs(wl[:nw] - ref["losses"][:nw])) <= 1e-5
+        assert np.all(wl[nw:] == 0)
+        tok = lens[:nw].astype(np.float64)
+        assert abs(st["loss"] - float(np.sum(ref["losses"][:nw] * tok) / tok.sum())) <= 1e-5
+        assert st["applied"] == ref["applied"] and st["correct"] == ref["correct"]
+        assert abs(st["grad_norm"] - ref["gnorm"]) <= 1e-5 * ref["gnorm"]
+        assert rel_fro(gpu.grads(), ref["grads"]) <= 1e-4
+        after = gpu.params().astype(np.float64)
+        if opt == "sgd":
+            assert rel_fro(after - p_before, ref_p - p_before) <= 1e-4
+            assert rel_fro(gpu.velocity(), ref_v) <= 1e-4
+        else:
+            assert rel_fro(after - p_before, ref_p - p_before) <= 1e-3
+            m1, v1, t1 = gpu.adam_state()
+            assert t1 == ref["t"] and rel_fro(m1, ref_m) <= 1e-4 and rel_fro(v1, ref_v) <= 1e-4
+        t += 1
+    gpu.close()
+
+
+RAGGED = [None, [64, 64, 64, 64, 17], None, [17], [64, 3, 64, 40, 64, 64, 64, 1]]
+
+
+@pytest.mark.parametrize("graph", [False, True])
+def test_lm_step_ragged_batches_c2(graph):
+    """Config C2 (B=8, T=64) with LMTrain's ragged batches: 5 windows of
+    {64, 64, 64, 64, 17} tokens, one 17-token window, 8 windows with short
+    ones, between full batches, eager and replayed from the captured graph."""
+    _ragged_case(2000, 128, 4, 8, 256, 8, 64, RAGGED, graph)
+
+
+def test_lm_step_ragged_adamw_and_noncausal():
+    _ragged_case(2000, 128, 2, 8, 256, 8, 64, [None, [64, 64, 64, 64, 17]], False, opt="adamw", seed=78)
+    # a non-causal model: the fused attention masks keys past each window's length
+    _ragged_case(64, 32, 1, 2, 48, 4, 16, [None, [16, 5, 9]], True, causal=False, seed=79)
+    # the unfused attention path (seq > 64), causal
+    _ragged_case(64, 32, 1, 2, 48, 2, 80, [[80, 33]], False, seed=80)
+
+
+def test_lm_set_batch_rejects_bad_windows():
+    from lanternl_amd._lib import LanternlHipError
+    gpu = lmtrain.GpuLMStep(64, 32, 1, 2, 48, 4, 16)
+    ids = np.zeros((4, 16), np.int32)
+    for lens, nw in (([16, 0], 2), ([17], 1), ([16] * 5, 5), ([4], 0)):
+        with pytest.raises(LanternlHipError):
+            gpu.set_batch(ids, ids, np.array(lens + [0] * (5 - len(lens)), np.int32), nw)
+    bad = ids.copy(); bad[0, 3] = 99                       # a counted id outside the vocabulary
+    with pytest.raises(LanternlHipError, match="ids"):
+        gpu.set_batch(bad, ids, np.array([8, 0, 0, 0], np.int32), 1)
+    bad[0, 3] = 0; bad[0, 12] = 99                         # past the window's length: ignored
+    gpu.set_batch(bad, ids, np.array([8, 0, 0, 0], np.int32), 1)
+    ncg = lmtrain.GpuLMStep(64, 32, 1, 2, 48, 2, 80, causal=False)   # unfused and non-causal
+    with pytest.raises(LanternlHipError, match="UNSUPPORTED"):
+        ncg.set_batch(np.zeros((2, 80), np.int32), np.zeros((2, 80), np.int32), np.array([80, 7], np.int32), 2)
+    ncg.set_batch(np.zeros((2, 80), np.int32), np.zeros((2, 80), np.int32))   # full windows are fine
+    gpu.close(); ncg.close()

@@ -642,3 +642,47 @@ def test_reduce_cols_and_clip():
     z = O.clip_by_nsq(y.copy(), nsq, nrm / 4)
     assert abs(np.linalg.norm(z) - (nrm / 4) * nrm / (nrm + 1e-6)) < 1e-12
     assert np.array_equal(O.clip_by_nsq(y.copy(), nsq, 2 * nrm), y)     # below the bound: unchanged
+
+
+def test_lm_ragged_batch_vs_torch_autograd():
+    """lmtrain.lua:535-558 (a short last window) and :1183-1212 (a short last
+    batch): each window's loss is the mean over its own tokens, the gradients
+    of the n_in_batch windows are summed and scaled by 1/n_in_batch.  Checked
+    against float64 torch autograd of each truncated window; the content past
+    a window's length and in the unused slots must not matter."""
+    pytest.importorskip("torch")
+    from tests import lm_torch_ref as ref
+    cfg = O.lm_cfg(**TINY)
+    p0, tab = _tiny_params(cfg)
+    rng = np.random.default_rng(21)
+    B, T = 4, 8
+    ids = rng.integers(0, cfg.vocab, (B, T)); tgt = rng.integers(0, cfg.vocab, (B, T))
+    lens, nwin = np.array([8, 3, 5, 8]), 3
+    gsum = np.zeros(p0.size); losses = []; corr = 0
+    for b in range(nwin):
+        tl, tg, tlog = ref.window_grad(cfg, p0, tab, ids[b, :lens[b]], tgt[b, :lens[b]])
+        gsum += tg
+        losses.append(tl)
+        corr += int((np.argmax(tlog, 1) == tgt[b, :lens[b]]).sum())
+    gexp = gsum / nwin
+    p = p0.copy(); v = np.zeros_like(p)
+    out = O.lm_step_sgd(cfg, p, v, ids, tgt, lr=0.0, momentum=0.0, wd=0.0, clip_norm=1e9, lens=lens, nwin=nwin)
+    np.testing.assert_allclose(out["losses"][:nwin], losses, rtol=1e-12)
+    np.testing.assert_allclose(out["grads"], gexp, rtol=1e-9, atol=1e-12)
+    assert out["correct"] == corr
+    # padding and unused slots do not matter
+    ids2, tgt2 = ids.copy(), tgt.copy()
+    ids2[1, 3:] = (ids2[1, 3:] + 5) % cfg.vocab; tgt2[2, 5:] = 0; ids2[3] = 1
+    p2 = p0.copy(); v2 = np.zeros_like(p2)
+    out2 = O.lm_step_sgd(cfg, p2, v2, ids2, tgt2, lr=0.0, momentum=0.0, wd=0.0, clip_norm=1e9, lens=lens, nwin=nwin)
+    assert np.array_equal(out2["grads"], out["grads"]) and np.array_equal(out2["losses"], out["losses"])
+    # one window in the batch: no scaling (lmtrain.lua:1211 scales only when n_in_batch > 1)
+    out1 = O.lm_step_sgd(cfg, p0.copy(), np.zeros_like(p0), ids, tgt, lr=0.0, momentum=0.0, wd=0.0,
+                         clip_norm=1e9, lens=lens, nwin=1)
+    np.testing.assert_allclose(out1["grads"], ref.window_grad(cfg, p0, tab, ids[0], tgt[0])[1], rtol=1e-9,
+                               atol=1e-12)
+    # full lengths are the full-window step
+    pa, pb = p0.copy(), p0.copy()
+    fa = O.lm_step_sgd(cfg, pa, np.zeros_like(pa), ids, tgt, lr=0.05)
+    fb = O.lm_step_sgd(cfg, pb, np.zeros_like(pb), ids, tgt, lr=0.05, lens=np.full(B, T), nwin=B)
+    assert np.array_equal(pa, pb) and np.array_equal(fa["grads"], fb["grads"])
