@@ -1580,6 +1580,8 @@ struct GroupedTNArgs {
     ColsumSet cs;     // column sums run by the workgroups after the last tile
     int cs_cb;        // 32-column blocks per column-sum job
     int cs_blocks;    // cs.njobs * cs_cb
+    int tp, cp;       // 64x64 kernel: tiles, column-sum workgroups per XCD
+    int cs_per_wg;    // 64x64 kernel: column-sum blocks per workgroup
 };
 
 template <int NW>
@@ -1736,6 +1738,120 @@ __global__ void __launch_bounds__(256) sgemm_grouped_tn_lds_kernel(const Grouped
     }
 }
 
+// 64x64 tiles for the same float4-loadable groups.  The tile's 32x32
+// quadrants belong to four waves, and with KS = 2 a second set of four waves
+// takes every other 64-deep K chunk (each set with its own double-buffered
+// LDS), so each chain of dependent chunk loads is half as long; the two
+// partial quadrants are added in LDS in a fixed order.  At the LM step's
+// shapes (K = batch*seq rows) this is about one workgroup per CU, each chunk
+// holding 32 MFMA steps per wave while the next chunk's loads are in flight,
+// and nothing is re-read by a neighbouring tile as often as with 32x32 tiles.
+// Placement: XCD x (blocks b with b % 8 == x) takes tiles [x*tp, (x+1)*tp)
+// first and then cp workgroups of column-sum jobs, each running up to
+// cs_per_wg 32-column blocks in turn, so no XCD holds more tiles than CUs.
+template <int KS>
+__global__ void __launch_bounds__(256 * KS) sgemm_grouped_tn_lds64_kernel(const GroupedTNArgs ga)
+{
+    constexpr int T = 64, BK = kGroupedBK, P = BK / 16;
+    __shared__ __align__(16) float As[KS][2][BK][T];
+    __shared__ __align__(16) float Bs[KS][2][BK][T];
+    const int xcd = blockIdx.x % 8, j = blockIdx.x / 8;
+    const int ntiles = ga.tile0[ga.ngroups];
+    if (j >= ga.tp) {
+        const int w = xcd * ga.cp + (j - ga.tp);
+        for (int q = 0; q < ga.cs_per_wg; ++q) {
+            const int cid = w * ga.cs_per_wg + q;
+            if (cid >= ga.cs_blocks) break;   // uniform
+            const int job = cid / ga.cs_cb, cb = cid - job * ga.cs_cb;
+            colsum4_block<256 * KS>(ga.cs.partial[job], ga.cs.nparts[job], ga.cs.out[job], ga.cs.cols, 32 * cb,
+                                    ga.cs.acc, reinterpret_cast<float4 (*)[8]>(&As[0][0][0][0]));
+            __syncthreads();   // red is reused by the next block
+        }
+        return;
+    }
+    const int id = xcd * ga.tp + j;
+    if (id >= ntiles) return;   // padding
+    int gi = 0;
+    for (int i = 1; i < ga.ngroups; ++i)
+        if (id >= ga.tile0[i]) gi = i;
+    const GroupedTN& e = ga.e[gi];
+    const int local = id - ga.tile0[gi];
+    const int tm = local / ga.tiles_n[gi], tn = local - tm * ga.tiles_n[gi];
+    const int K = ga.K;
+    const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, lk = lane >> 5;
+    const int grp = __builtin_amdgcn_readfirstlane(tid >> 8), gt = tid & 255;
+    const int wave = __builtin_amdgcn_readfirstlane((tid >> 6) & 3);
+    const int wm = 32 * (wave & 1), wn = 32 * (wave >> 1);
+    const int m0 = tm * T, n0 = tn * T;
+    // chunk loader of a set: thread t covers chunk rows t/16 + 16p (p < 4), float4 column (t%16)*4
+    const int lrow = gt >> 4, lc4 = (gt & 15) * 4;
+    const bool am_ok = m0 + lc4 < e.M, bn_ok = n0 + lc4 < e.N;   // M, N % 4 == 0 (host check)
+    float4 ra[P], rb[P];
+    auto gload = [&](int k0) {
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            const int k = k0 + lrow + 16 * p;
+            const bool kin = k < K;
+            ra[p] = (kin && am_ok) ? *reinterpret_cast<const float4*>(e.A + static_cast<long long>(k) * e.lda + m0 + lc4)
+                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+            rb[p] = (kin && bn_ok) ? *reinterpret_cast<const float4*>(e.B + static_cast<long long>(k) * e.ldb + n0 + lc4)
+                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    auto lstore = [&](int buf) {
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            *reinterpret_cast<float4*>(&As[grp][buf][lrow + 16 * p][lc4]) = ra[p];
+            *reinterpret_cast<float4*>(&Bs[grp][buf][lrow + 16 * p][lc4]) = rb[p];
+        }
+    };
+    floatx16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+    const int nk = (K + BK - 1) / BK;
+    const int iters = (nk + KS - 1) / KS;   // every set passes the same barriers
+    gload(grp * BK);
+    lstore(0);
+    __syncthreads();
+    for (int it = 0; it < iters; ++it) {
+        const int cur = it & 1;
+        const int kt = it * KS + grp;
+        const bool more = it + 1 < iters;
+        if (more) gload((kt + KS) * BK);
+        if (kt < nk) {
+#pragma unroll
+            for (int st = 0; st < BK / 2; ++st) {
+                const int kr = 2 * st + lk;   // lanes 0-31 read row k, 32-63 row k+1
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(As[grp][cur][kr][wm + lr], Bs[grp][cur][kr][wn + lr], acc,
+                                                           0, 0, 0);
+            }
+        }
+        if (more) lstore(cur ^ 1);
+        __syncthreads();
+    }
+    if (KS == 2) {   // set 1's partial quadrants added to set 0's
+        float* red = &As[0][0][0][0];
+        if (grp == 1) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) red[(wave * 16 + r) * 64 + lane] = acc[r];
+        }
+        __syncthreads();
+        if (grp == 1) return;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] += red[(wave * 16 + r) * 64 + lane];
+    }
+    // the wave's quadrant straight from its accumulators: register r of lane l
+    // is C(8(r/4) + 4(l/32) + r%4, l%32)
+    const int ocol = n0 + wn + lr;
+    if (ocol < e.N) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int orow = m0 + wm + 8 * (r >> 2) + 4 * lk + (r & 3);
+            if (orow < e.M) e.C[static_cast<long long>(orow) * e.ldc + ocol] = acc[r];
+        }
+    }
+}
+
 }  // namespace
 
 int sgemm_grouped_tn(const GroupedTN* g, int ngroups, int K, hipStream_t stream, const ColsumSet* cs)
@@ -1748,28 +1864,35 @@ int sgemm_grouped_tn(const GroupedTN* g, int ngroups, int K, hipStream_t stream,
     if (ngroups > kGroupedMax) return fail(LHIP_E_ARG, "sgemm_grouped_tn: %d groups (at most %d)", ngroups, kGroupedMax);
     if (K <= 0) return fail(LHIP_E_SHAPE, "sgemm_grouped_tn: K=%d", K);
     GroupedTNArgs ga{};
-    long long tiles = 0;
+    bool vec = true;
+    long long tiles64 = 0;
     for (int i = 0; i < ngroups; ++i) {
         const GroupedTN& e = g[i];
         if (e.M <= 0 || e.N <= 0) return fail(LHIP_E_SHAPE, "sgemm_grouped_tn: group %d is %dx%d", i, e.M, e.N);
         if (!e.A || !e.B || !e.C) return fail(LHIP_E_NULL, "sgemm_grouped_tn: group %d has a NULL operand", i);
         if (e.lda < e.M || e.ldb < e.N || e.ldc < e.N)
             return fail(LHIP_E_SHAPE, "sgemm_grouped_tn: group %d leading dimensions", i);
+        vec = vec && e.lda % 4 == 0 && e.ldb % 4 == 0 && e.M % 4 == 0 && e.N % 4 == 0 && aligned16(e.A) &&
+              aligned16(e.B);
+        tiles64 += static_cast<long long>(ceil_div(e.M, 64)) * ceil_div(e.N, 64);
+    }
+    // 64x64 tiles once they give a quarter of the CUs work and fit one
+    // workgroup per CU; 32x32 otherwise
+    const int cus = st().cu_count > 0 ? st().cu_count : 256;
+    const bool wide = vec && 4 * tiles64 >= cus && tiles64 <= cus;
+    const int tile = wide ? 64 : kGroupedTile;
+    long long tiles = 0;
+    for (int i = 0; i < ngroups; ++i) {
+        const GroupedTN& e = g[i];
         ga.e[i] = e;
         ga.tile0[i] = static_cast<int>(tiles);
-        ga.tiles_n[i] = ceil_div(e.N, kGroupedTile);
-        tiles += static_cast<long long>(ceil_div(e.M, kGroupedTile)) * ga.tiles_n[i];
+        ga.tiles_n[i] = ceil_div(e.N, tile);
+        tiles += static_cast<long long>(ceil_div(e.M, tile)) * ga.tiles_n[i];
         if (tiles > 0x7fffffffLL) return fail(LHIP_E_CAPACITY, "sgemm_grouped_tn: too many tiles");
     }
     ga.tile0[ngroups] = static_cast<int>(tiles);
     ga.ngroups = ngroups;
     ga.K = K;
-    bool vec = true;
-    for (int i = 0; i < ngroups; ++i) {
-        const GroupedTN& e = g[i];
-        vec = vec && e.lda % 4 == 0 && e.ldb % 4 == 0 && e.M % 4 == 0 && e.N % 4 == 0 && aligned16(e.A) &&
-              aligned16(e.B);
-    }
     // column sums in the same launch when they take the float4 form too
     bool cs_fused = false;
     if (vec && cs && cs->njobs > 0) {
@@ -1784,8 +1907,21 @@ int sgemm_grouped_tn(const GroupedTN* g, int ngroups, int K, hipStream_t stream,
             ga.cs_blocks = cs->njobs * ga.cs_cb;
         }
     }
-    const unsigned grid = static_cast<unsigned>((tiles + ga.cs_blocks + 7) / 8 * 8);   // whole XCD rounds
-    if (vec) sgemm_grouped_tn_lds_kernel<<<grid, 256, 0, stream>>>(ga);
+    unsigned grid = static_cast<unsigned>((tiles + ga.cs_blocks + 7) / 8 * 8);   // whole XCD rounds
+    if (wide) {
+        // per XCD: its tiles, then column-sum workgroups on the CUs left over
+        ga.tp = static_cast<int>((tiles + 7) / 8);
+        ga.cp = 0;
+        ga.cs_per_wg = 1;
+        if (ga.cs_blocks > 0) {
+            ga.cp = std::max(1, cus / 8 - ga.tp);
+            ga.cp = std::min(ga.cp, (ga.cs_blocks + 7) / 8);
+            ga.cs_per_wg = (ga.cs_blocks + 8 * ga.cp - 1) / (8 * ga.cp);
+        }
+        grid = static_cast<unsigned>(8 * (ga.tp + ga.cp));
+        sgemm_grouped_tn_lds64_kernel<2><<<grid, 512, 0, stream>>>(ga);
+    }
+    else if (vec) sgemm_grouped_tn_lds_kernel<<<grid, 256, 0, stream>>>(ga);
     else if (K >= 256) sgemm_grouped_tn_kernel<8><<<grid, 512, 0, stream>>>(ga);
     else sgemm_grouped_tn_kernel<4><<<grid, 256, 0, stream>>>(ga);
     int rc = check_launch("sgemm_grouped_tn");

@@ -183,28 +183,31 @@ __device__ __forceinline__ int block_argmax(float bv, int bi, float* redv, int* 
 
 }  // namespace lhip
 
-// Column sums of one 32-column block over 256 threads: out[c] (+)= sum_b
-// partial[b][c] for c in [c0, c0 + 32) (cols % 4 == 0, 16-byte aligned rows).
-// Thread (g, q) sums column quad q over the partial rows g, g + 32, ... (eight
-// loads in flight at a time); the 32 group sums are then added in a fixed tree
-// through red (32 x 8 float4 of LDS).  Deterministic.
+// Column sums of one 32-column block over the NT threads of a workgroup:
+// out[c] (+)= sum_b partial[b][c] for c in [c0, c0 + 32) (cols % 4 == 0,
+// 16-byte aligned rows).  Thread (g, q) sums column quad q over the partial
+// rows g, g + G, ... (G = NT/8 groups; eight loads in flight at a time); the G
+// group sums are then added in a fixed tree through red (G x 8 float4 of
+// LDS).  Deterministic.
+template <int NT = 256>
 __device__ inline void colsum4_block(const float* __restrict__ partial, int nparts, float* __restrict__ out, int cols,
                                      int c0, int acc, float4 (*red)[8])
 {
+    constexpr int G = NT / 8;
     const int q = threadIdx.x & 7, g = threadIdx.x >> 3;
     const int c = c0 + 4 * q;
     float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
     if (c < cols) {
         int b = g;
-        for (; b + 7 * 32 < nparts; b += 8 * 32) {
+        for (; b + 7 * G < nparts; b += 8 * G) {
             float4 t[8];
 #pragma unroll
             for (int u = 0; u < 8; ++u)
-                t[u] = *reinterpret_cast<const float4*>(partial + static_cast<size_t>(b + u * 32) * cols + c);
+                t[u] = *reinterpret_cast<const float4*>(partial + static_cast<size_t>(b + u * G) * cols + c);
 #pragma unroll
             for (int u = 0; u < 8; ++u) { s.x += t[u].x; s.y += t[u].y; s.z += t[u].z; s.w += t[u].w; }
         }
-        for (; b < nparts; b += 32) {
+        for (; b < nparts; b += G) {
             const float4 t = *reinterpret_cast<const float4*>(partial + static_cast<size_t>(b) * cols + c);
             s.x += t.x; s.y += t.y; s.z += t.z; s.w += t.w;
         }
@@ -212,7 +215,7 @@ __device__ inline void colsum4_block(const float* __restrict__ partial, int npar
     red[g][q] = s;
     __syncthreads();
 #pragma unroll
-    for (int half = 16; half > 0; half >>= 1) {
+    for (int half = G / 2; half > 0; half >>= 1) {
         if (g < half) {
             const float4 t = red[g + half][q];
             float4 u = red[g][q];
