@@ -1582,6 +1582,8 @@ struct GroupedTNArgs {
     int cs_blocks;    // cs.njobs * cs_cb
     int tp, cp;       // 64x64 kernel: tiles, column-sum workgroups per XCD
     int cs_per_wg;    // 64x64 kernel: column-sum blocks per workgroup
+    int do_sc;        // 64x64 kernel: run the groups' scatters
+    double* ss_out;   // 64x64 kernel: per-workgroup sums of squares of the stored values (or NULL)
 };
 
 template <int NW>
@@ -1738,6 +1740,22 @@ __global__ void __launch_bounds__(256) sgemm_grouped_tn_lds_kernel(const Grouped
     }
 }
 
+// Sum over the workgroup of each thread's double (wave order, then wave 0's
+// thread 0 adds the waves in order) into ss_out[blockIdx.x].
+template <int NW>
+__device__ __forceinline__ void block_sumsq_out(double v, double* ss_out, double* red)
+{
+    v = wave_sum(v);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double t = 0.0;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) t += red[w];
+        ss_out[blockIdx.x] = t;
+    }
+}
+
 // 64x64 tiles for the same float4-loadable groups.  The tile's 32x32
 // quadrants belong to four waves, and with KS = 2 a second set of four waves
 // takes every other 64-deep K chunk (each set with its own double-buffered
@@ -1755,22 +1773,32 @@ __global__ void __launch_bounds__(256 * KS) sgemm_grouped_tn_lds64_kernel(const 
     constexpr int T = 64, BK = kGroupedBK, P = BK / 16;
     __shared__ __align__(16) float As[KS][2][BK][T];
     __shared__ __align__(16) float Bs[KS][2][BK][T];
+    __shared__ double ssred[4 * KS];
+    __shared__ int sclst[4][1024];   // per wave of set 0: a scatter round's (token, row) list
     const int xcd = blockIdx.x % 8, j = blockIdx.x / 8;
     const int ntiles = ga.tile0[ga.ngroups];
     if (j >= ga.tp) {
         const int w = xcd * ga.cp + (j - ga.tp);
+        double sq = 0.0;
         for (int q = 0; q < ga.cs_per_wg; ++q) {
             const int cid = w * ga.cs_per_wg + q;
             if (cid >= ga.cs_blocks) break;   // uniform
             const int job = cid / ga.cs_cb, cb = cid - job * ga.cs_cb;
-            colsum4_block<256 * KS>(ga.cs.partial[job], ga.cs.nparts[job], ga.cs.out[job], ga.cs.cols, 32 * cb,
-                                    ga.cs.acc, reinterpret_cast<float4 (*)[8]>(&As[0][0][0][0]));
+            const float4 t = colsum4_block<256 * KS>(ga.cs.partial[job], ga.cs.nparts[job], ga.cs.out[job],
+                                                     ga.cs.cols, 32 * cb, ga.cs.acc,
+                                                     reinterpret_cast<float4 (*)[8]>(&As[0][0][0][0]));
+            sq += static_cast<double>(t.x) * t.x + static_cast<double>(t.y) * t.y +
+                  static_cast<double>(t.z) * t.z + static_cast<double>(t.w) * t.w;
             __syncthreads();   // red is reused by the next block
         }
+        if (ga.ss_out) block_sumsq_out<4 * KS>(sq, ga.ss_out, ssred);
         return;
     }
     const int id = xcd * ga.tp + j;
-    if (id >= ntiles) return;   // padding
+    if (id >= ntiles) {   // padding
+        if (ga.ss_out && threadIdx.x == 0) ga.ss_out[blockIdx.x] = 0.0;
+        return;
+    }
     int gi = 0;
     for (int i = 1; i < ga.ngroups; ++i)
         if (id >= ga.tile0[i]) gi = i;
@@ -1808,9 +1836,79 @@ __global__ void __launch_bounds__(256 * KS) sgemm_grouped_tn_lds64_kernel(const 
     floatx16 acc;
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+    // Scatter C[id_i] += scale * rows[i] over the tokens i whose id falls in
+    // this wave's 32 rows, in token order.  A round lists the matches among 512
+    // tokens in LDS (slot = rank in token order).  The first SC matches of the
+    // first round are fetched before the products start, so their loads
+    // overlap the chunk loads, and added after the products; any others are
+    // fetched after the products, eight at a time.
+    constexpr int SC = 24;
+    const bool scat = ga.do_sc && e.sc_n > 0 && grp == 0;
+    const int ocol = n0 + wn + lr;
+    const int rlo = m0 + wm;
+    int* lst = &sclst[wave][0];
+    int idpre[8];
+    if (scat) {
+        // unconditional loads (clamped index) keep the memory-count waits of
+        // the chunk loads exact
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int i = 64 * u + lane;
+            const int v = e.sc_ids[min(i, e.sc_n - 1)];
+            idpre[u] = i < e.sc_n ? v : -1;
+        }
+    }
+    auto build_list = [&](int base) -> int {   // wave-uniform match count
+        int total = 0;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int i = base + 64 * u + lane;
+            const int idv = base == 0 ? idpre[u] : (i < e.sc_n ? e.sc_ids[i] : -1);
+            const int rel = idv - rlo;
+            const bool hit = i < e.sc_n && rel >= 0 && rel < 32 && idv < e.M;
+            const unsigned long long mask = __ballot(hit);
+            if (hit) {
+                const int slot = total + __popcll(mask & ((1ull << lane) - 1ull));
+                lst[2 * slot] = i;
+                lst[2 * slot + 1] = rel;
+            }
+            total += __popcll(mask);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        return total;
+    };
+    const float scl = e.sc_scale;
     const int nk = (K + BK - 1) / BK;
     const int iters = (nk + KS - 1) / KS;   // every set passes the same barriers
     gload(grp * BK);
+    float sv[SC];             // rows of the first SC matches, fetched during the products
+    unsigned srel[SC / 4];    // their rows within the wave's 32, 8 bits each (0xff: none)
+    int first_total = 0;
+    if (scat) {
+        first_total = build_list(0);
+        const int ccol = min(ocol, e.N - 1);
+        int2 ent[SC];   // (token, row) pairs, read unconditionally so the reads batch
+#pragma unroll
+        for (int c = 0; c < SC; ++c) ent[c] = reinterpret_cast<const int2*>(lst)[c];
+#pragma unroll
+        for (int c = 0; c < SC; ++c) {
+            const int tok = c < first_total ? ent[c].x : 0;   // row 0 stands in (its value is not used)
+            sv[c] = e.sc_rows[static_cast<long long>(tok) * e.sc_ld + ccol];
+        }
+#pragma unroll
+        for (int q = 0; q < SC / 4; ++q) {
+            unsigned w = 0;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const int c = 4 * q + b;
+                w |= static_cast<unsigned>(c < first_total ? ent[c].y : 0xff) << (8 * b);
+            }
+            srel[q] = w;
+        }
+        __builtin_amdgcn_wave_barrier();   // the list is rewritten after the products
+    }
     lstore(0);
     __syncthreads();
     for (int it = 0; it < iters; ++it) {
@@ -1836,26 +1934,69 @@ __global__ void __launch_bounds__(256 * KS) sgemm_grouped_tn_lds64_kernel(const 
             for (int r = 0; r < 16; ++r) red[(wave * 16 + r) * 64 + lane] = acc[r];
         }
         __syncthreads();
-        if (grp == 1) return;
+        if (grp == 0) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[r] += red[(wave * 16 + r) * 64 + lane];
+            for (int r = 0; r < 16; ++r) acc[r] += red[(wave * 16 + r) * 64 + lane];
+        }
     }
-    // the wave's quadrant straight from its accumulators: register r of lane l
-    // is C(8(r/4) + 4(l/32) + r%4, l%32)
-    const int ocol = n0 + wn + lr;
-    if (ocol < e.N) {
+    if (scat) {
+        // register r of lane l holds C(8(r/4) + 4(l/32) + r%4, l%32) of the
+        // wave's quadrant: listed row rel (wave-uniform) lands in register
+        // 4(rel/8) + rel%4 of the lanes with l/32 == (rel/4)%2
+        auto add_row = [&](int rel, float v) {
+            const int rr = ((rel >> 3) << 2) | (rel & 3);
+            const float a = v * scl;
+            acc[rr] += lk == ((rel >> 2) & 1) ? a : 0.f;   // uniform index: one relative move
+        };
+#pragma unroll
+        for (int q = 0; q < SC / 4; ++q) {
+            const unsigned w = __builtin_amdgcn_readfirstlane(srel[q]);
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+                if (4 * q + b < first_total) add_row((w >> (8 * b)) & 0xff, sv[4 * q + b]);
+        }
+        if (e.sc_n > 512 || first_total > SC) {
+            for (int base = 0; base < e.sc_n; base += 512) {
+                const int total = build_list(base);
+                for (int c0 = base == 0 ? SC : 0; c0 < total; c0 += 8) {
+                    float v[8];
+#pragma unroll
+                    for (int c = 0; c < 8; ++c) {
+                        const int tok = lst[2 * (c0 + c)];
+                        v[c] = c0 + c < total && ocol < e.N ? e.sc_rows[static_cast<long long>(tok) * e.sc_ld + ocol]
+                                                           : 0.f;
+                    }
+#pragma unroll
+                    for (int c = 0; c < 8; ++c)
+                        if (c0 + c < total) add_row(__builtin_amdgcn_readfirstlane(lst[2 * (c0 + c) + 1]), v[c]);
+                }
+                __builtin_amdgcn_wave_barrier();   // the list is rewritten by the next round
+            }
+        }
+    }
+    double sq = 0.0;
+    if (grp == 0 && ocol < e.N) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int orow = m0 + wm + 8 * (r >> 2) + 4 * lk + (r & 3);
-            if (orow < e.M) e.C[static_cast<long long>(orow) * e.ldc + ocol] = acc[r];
+            if (orow < e.M) {
+                e.C[static_cast<long long>(orow) * e.ldc + ocol] = acc[r];
+                sq += static_cast<double>(acc[r]) * acc[r];
+            }
         }
     }
+    if (ga.ss_out) block_sumsq_out<4 * KS>(sq, ga.ss_out, ssred);
 }
 
 }  // namespace
 
-int sgemm_grouped_tn(const GroupedTN* g, int ngroups, int K, hipStream_t stream, const ColsumSet* cs)
+int sgemm_grouped_tn(const GroupedTN* g, int ngroups, int K, hipStream_t stream, const ColsumSet* cs,
+                     GroupedExtras* ex)
 {
+    if (ex) {
+        ex->fused = 0;
+        ex->ss_parts = 0;
+    }
     if (ngroups <= 0) {
         if (cs && cs->njobs > 0)
             return rmsnorm_bwd_colsum_multi(cs->partial, cs->nparts, cs->out, cs->njobs, cs->cols, cs->acc, stream);
@@ -1919,6 +2060,17 @@ int sgemm_grouped_tn(const GroupedTN* g, int ngroups, int K, hipStream_t stream,
             ga.cs_per_wg = (ga.cs_blocks + 8 * ga.cp - 1) / (8 * ga.cp);
         }
         grid = static_cast<unsigned>(8 * (ga.tp + ga.cp));
+        // the scatters and the per-workgroup sums of squares, when the column
+        // sums run here too (every stored value then passes through this launch)
+        if (ex && ex->ss_out && static_cast<int>(grid) <= ex->ss_cap && (!cs || cs->njobs == 0 || cs_fused)) {
+            for (int i = 0; i < ngroups; ++i)
+                if (g[i].sc_n > 0 && (!g[i].sc_ids || !g[i].sc_rows || g[i].sc_ld < g[i].N))
+                    return fail(LHIP_E_ARG, "sgemm_grouped_tn: group %d scatter arguments", i);
+            ga.do_sc = 1;
+            ga.ss_out = ex->ss_out;
+            ex->fused = 1;
+            ex->ss_parts = static_cast<int>(grid);
+        }
         sgemm_grouped_tn_lds64_kernel<2><<<grid, 512, 0, stream>>>(ga);
     }
     else if (vec) sgemm_grouped_tn_lds_kernel<<<grid, 256, 0, stream>>>(ga);
@@ -2087,6 +2239,8 @@ int sgemm_run(int ta, int tb, int m, int n, int k, float alpha,
         }
     }
     if (big_tiles >= cus) return launch_cfg<128, 128, 32>(ta, tb, g, batch, stream);
+    // short K (e.g. the LM head, K = dim): the whole K range in one LDS tile,
+    // so a workgroup waits on one load round trip instead of one per 32-deep chunk
     if (tiles64 >= cus) return launch_cfg<64, 64, 32>(ta, tb, g, batch, stream);
     const bool small = use_small_kernel(m, n, g.K);
     g.splits = o.ws ? splitk_plan(m, n, g.K, batch, o.ws_floats, &g.kchunk, o.splits_out != nullptr) : 1;

@@ -253,6 +253,25 @@ struct GroupedTN {
     const float* B; int ldb;
     float* C; int ldc;
     int M, N;
+    // optional scatter into this product's rows, in token order:
+    // C[sc_ids[i]] += sc_scale * sc_rows[i] (row stride sc_ld) for i < sc_n,
+    // ids outside [0, M) skipped (the tied table's embedding backward); done
+    // only when the launch reports GroupedExtras::fused
+    const int* sc_ids = nullptr;
+    const float* sc_rows = nullptr;
+    int sc_ld = 0, sc_n = 0;
+    float sc_scale = 1.f;
+};
+// Work a grouped launch can fold in on its 64x64-tile path: the groups'
+// scatters, and one sum of squares (in double) of every value the launch
+// stores per workgroup, into ss_out[0 .. ss_parts) (capacity ss_cap).  On
+// return `fused` says whether that happened; if not, the caller runs the
+// scatters and the norm itself.
+struct GroupedExtras {
+    double* ss_out = nullptr;
+    int ss_cap = 0;
+    int fused = 0;      // out
+    int ss_parts = 0;   // out
 };
 // Column-sum jobs (the RMSNorm gains' dw from per-tile partials) that a
 // grouped launch can run in extra workgroups: out_j[c] (+)= sum_b partial_j[b][c].
@@ -264,7 +283,8 @@ struct ColsumSet {
 };
 // cs (optional): column sums issued with the products -- in the same launch
 // when both take their float4 forms, otherwise as a second launch.
-int sgemm_grouped_tn(const GroupedTN* g, int ngroups, int K, hipStream_t stream, const ColsumSet* cs = nullptr);
+int sgemm_grouped_tn(const GroupedTN* g, int ngroups, int K, hipStream_t stream, const ColsumSet* cs = nullptr,
+                     GroupedExtras* ex = nullptr);
 int sgemm_run(int transa, int transb, int m, int n, int k, float alpha,
               const float* A, int lda, long long sA, const float* B, int ldb, long long sB, float beta,
               float* C, int ldc, long long sC, int batch, const GemmOpts& o, hipStream_t stream);

@@ -71,7 +71,8 @@ struct LmModel {
     int* tcount = nullptr;                         // AdamW step count, two parity slots
     long long adam_calls = 0;                      // AdamW steps enqueued (slot parity)
     double *ss = nullptr, *ss_part = nullptr;
-    int ss_blocks = 0;
+    int ss_blocks = 0;   // the stand-alone partial kernel's block count
+    int ss_cap = 0;      // ss_part's length (also holds the grouped launch's per-workgroup partials)
     // saved activations
     float *x = nullptr, *h = nullptr, *inv1 = nullptr, *qkv = nullptr, *P = nullptr, *ctx = nullptr;
     float *xmid = nullptr, *h2 = nullptr, *inv2 = nullptr, *zu = nullptr, *a = nullptr;
@@ -317,7 +318,11 @@ int enqueue_step(LmModel& m, hipStream_t s, const Hyper& hp, bool device_hyper)
     int cs_n[kColsumJobs];
     float* cs_o[kColsumJobs];
     int ncs = 0;
-    const GroupedTN gemb{dlg, V, m.xf, D, m.grd(0), D, V, D};                     // gemb = dlogits^T . xf
+    bool flushed = false;   // some products or column sums were issued before the final launch
+    GroupedTN gemb{dlg, V, m.xf, D, m.grd(0), D, V, D};                           // gemb = dlogits^T . xf
+    // the tied table's second term, dx_0 scattered to the token rows (gemb[id_i] += dx_0[i]),
+    // when the final launch can fold it in
+    gemb.sc_ids = m.ids; gemb.sc_rows = gxl(0); gemb.sc_ld = D; gemb.sc_n = N; gemb.sc_scale = 1.f;
     dw_all[ndw++] = gemb;
     // dxf = dlogits . emb; with fused GEMMs its split-K slices are left
     // unreduced and summed by the norm-backward prologue that consumes dxf
@@ -409,10 +414,12 @@ int enqueue_step(LmModel& m, hipStream_t s, const Hyper& hp, bool device_hyper)
             if (ndw + 7 > kGroupedMax) {
                 LM_TRY(sgemm_grouped_tn(dw_all, ndw, N, s));
                 ndw = 0;
+                flushed = true;
             }
             if (ncs + 2 > kColsumJobs) {
                 LM_TRY(rmsnorm_bwd_colsum_multi(cs_p, cs_n, cs_o, ncs, D, 0, s));
                 ncs = 0;
+                flushed = true;
             }
             for (int i = 0; i < 7; ++i) dw_all[ndw++] = gw[i];
             for (int i = 0; i < 2; ++i) { cs_p[ncs] = parts_p[i]; cs_n[ncs] = parts_n[i]; cs_o[ncs] = parts_o[i]; ++ncs; }
@@ -427,29 +434,41 @@ int enqueue_step(LmModel& m, hipStream_t s, const Hyper& hp, bool device_hyper)
     if (ncs + 1 > kColsumJobs) {
         LM_TRY(rmsnorm_bwd_colsum_multi(cs_p, cs_n, cs_o, ncs, D, 0, s));
         ncs = 0;
+        flushed = true;
     }
     cs_p[ncs] = pend.part; cs_n[ncs] = pend.parts; cs_o[ncs] = pend.gw; ++ncs;
+    int ss_parts = 0;   // squared-norm partials the optimizer sums
     {
         // the last products and the gains' column sums in one launch
         ColsumSet cs{};
         for (int i = 0; i < ncs; ++i) { cs.partial[i] = cs_p[i]; cs.nparts[i] = cs_n[i]; cs.out[i] = cs_o[i]; }
         cs.njobs = ncs; cs.cols = D; cs.acc = 0;
-        LM_TRY(sgemm_grouped_tn(dw_all, ndw, N, s, &cs));
+        // with every gradient stored by this launch (nothing issued earlier),
+        // it also runs the scatter and leaves the squared-norm partials
+        GroupedExtras ex;
+        if (!flushed) {
+            ex.ss_out = m.ss_part;
+            ex.ss_cap = m.ss_cap;
+        }
+        LM_TRY(sgemm_grouped_tn(dw_all, ndw, N, s, &cs, &ex));
+        ss_parts = ex.fused ? ex.ss_parts : 0;
     }
-    LM_TRY(embed_bwd(gxl(0), m.ids, m.grd(0), N, D, V, 1.f, 1, s));    // after gemb (same launch order)
-
     // ---------------- optimizer (lmtrain.lua:1212-1226) ----------------
-    // squared-norm partials; the optimizer kernel finishes the sum itself
-    LM_TRY(sumsq_partials(m.grads, m.nparam, m.ss_part, m.ss_blocks, s));
+    if (ss_parts == 0) {
+        LM_TRY(embed_bwd(gxl(0), m.ids, m.grd(0), N, D, V, 1.f, 1, s));    // after gemb (same launch order)
+        // squared-norm partials; the optimizer kernel finishes the sum itself
+        LM_TRY(sumsq_partials(m.grads, m.nparam, m.ss_part, m.ss_blocks, s));
+        ss_parts = m.ss_blocks;
+    }
     const float gscale = hp.gscale;
     const float* hdev = device_hyper ? m.hyper : nullptr;
     if (hp.opt == OPT_ADAMW)
-        LM_TRY(adamw_step(m.params, m.grads, m.adam_m, m.adam_v, m.nparam, m.ss_part, m.ss_blocks, hp.lr, hp.beta1,
+        LM_TRY(adamw_step(m.params, m.grads, m.adam_m, m.adam_v, m.nparam, m.ss_part, ss_parts, hp.lr, hp.beta1,
                           hp.beta2, hp.eps, hp.wd, gscale, hp.clip, 0, m.tcount, hp.parity != 0.f ? 1 : 0, m.gnorm,
                           m.applied, s, hdev));
     else
         LM_TRY(sgd_step(m.params, m.grads, m.vel, m.nparam, m.ss_part, hp.lr, hp.momentum, hp.wd, gscale, hp.clip,
-                        hp.nesterov != 0.f ? 1 : 0, m.gnorm, m.applied, s, hdev, m.ss_blocks));
+                        hp.nesterov != 0.f ? 1 : 0, m.gnorm, m.applied, s, hdev, ss_parts));
     return LHIP_OK;
 }
 
@@ -569,6 +588,7 @@ LHIP_API int lhip_lm_create(const lhip_lm_config_t* cfg, void** model)
     const long long N = m->N, D = m->D, F = m->F, V = m->V, L = m->L;
     const long long ND = N * D, NF = N * F, PL = static_cast<long long>(m->B) * m->H * m->T * m->T;
     m->ss_blocks = lhip::sumsq_blocks(m->nparam);
+    m->ss_cap = std::max(m->ss_blocks, 4096);
     // dw partials of one norm backward: the stand-alone kernel's, or one row per 16-row tile when fused
     m->work_floats = static_cast<size_t>(std::max(lhip::rmsnorm_bwd_parts(m->N, m->D), lhip::ceil_div(m->N, 16))) *
                      m->D;
@@ -591,7 +611,7 @@ LHIP_API int lhip_lm_create(const lhip_lm_config_t* cfg, void** model)
         {reinterpret_cast<void**>(&m->adam_v), sizeof(float) * m->nparam},
         {reinterpret_cast<void**>(&m->tcount), sizeof(int) * 4},
         {reinterpret_cast<void**>(&m->ss), sizeof(double) * 2},
-        {reinterpret_cast<void**>(&m->ss_part), sizeof(double) * m->ss_blocks},
+        {reinterpret_cast<void**>(&m->ss_part), sizeof(double) * m->ss_cap},
         {reinterpret_cast<void**>(&m->x), sizeof(float) * (L + 1) * ND},
         {reinterpret_cast<void**>(&m->h), sizeof(float) * L * ND},
         {reinterpret_cast<void**>(&m->inv1), sizeof(float) * L * N},

@@ -188,10 +188,11 @@ __device__ __forceinline__ int block_argmax(float bv, int bi, float* redv, int* 
 // 16-byte aligned rows).  Thread (g, q) sums column quad q over the partial
 // rows g, g + G, ... (G = NT/8 groups; eight loads in flight at a time); the G
 // group sums are then added in a fixed tree through red (G x 8 float4 of
-// LDS).  Deterministic.
+// LDS).  Deterministic.  Returns the float4 this thread stored (zeros for
+// threads that store nothing).
 template <int NT = 256>
-__device__ inline void colsum4_block(const float* __restrict__ partial, int nparts, float* __restrict__ out, int cols,
-                                     int c0, int acc, float4 (*red)[8])
+__device__ inline float4 colsum4_block(const float* __restrict__ partial, int nparts, float* __restrict__ out,
+                                       int cols, int c0, int acc, float4 (*red)[8])
 {
     constexpr int G = NT / 8;
     const int q = threadIdx.x & 7, g = threadIdx.x >> 3;
@@ -224,8 +225,9 @@ __device__ inline void colsum4_block(const float* __restrict__ partial, int npar
         }
         __syncthreads();
     }
+    float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
     if (g == 0 && c < cols) {
-        float4 t = red[0][q];
+        t = red[0][q];
         float4* o = reinterpret_cast<float4*>(out + c);
         if (acc) {
             const float4 v = *o;
@@ -233,4 +235,5 @@ __device__ inline void colsum4_block(const float* __restrict__ partial, int npar
         }
         *o = t;
     }
+    return t;
 }

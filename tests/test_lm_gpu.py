@@ -22,7 +22,8 @@ from tests.gpu_util import announce, rel_fro
 pytestmark = pytest.mark.gpu
 
 
-def _run_case(V, D, L, H, F, B, T, steps, lr, std, seed, graph=False, clip=1.0, mom=0.9, wd=0.01, causal=True):
+def _run_case(V, D, L, H, F, B, T, steps, lr, std, seed, graph=False, clip=1.0, mom=0.9, wd=0.01, causal=True,
+              id_hi=None):
     rng = np.random.default_rng(seed)
     cfg = O.lm_cfg(V, D, L, H, F, causal=causal)
     gpu = lmtrain.GpuLMStep(V, D, L, H, F, B, T, causal=causal)
@@ -32,7 +33,7 @@ def _run_case(V, D, L, H, F, B, T, steps, lr, std, seed, graph=False, clip=1.0, 
         gpu.use_graph(True)
     results = []
     for _ in range(steps):
-        ids = rng.integers(0, V, (B, T)).astype(np.int32)
+        ids = rng.integers(0, id_hi or V, (B, T)).astype(np.int32)
         tgt = rng.integers(0, V, (B, T)).astype(np.int32)
         gpu.set_batch(ids, tgt)
         # the oracle starts every step from the GPU's own state (no drift between the sides)
@@ -118,6 +119,20 @@ def test_lm_step_config_c2():
     # near-uniform logits at init: loss ~ ln V
     assert abs(st["loss"] - np.log(2000)) < 0.05
     assert ref["applied"]
+    gpu.close()
+
+
+@pytest.mark.parametrize("B,id_hi", [(16, 40), (8, 2000), (16, 2000)])
+def test_lm_step_c2_embedding_scatter(B, id_hi):
+    """C2's dimensions, where the last grouped weight-gradient launch also
+    scatters dx_0 into the tied table's rows and leaves the squared-norm
+    partials: ids crowded into 40 rows (hundreds of tokens per 32-row block,
+    past the first batch of matches) and 16 windows (1024 tokens, two listing
+    rounds), as well as spread ids at 512 and 1024 tokens."""
+    announce("lm C2 scatter", B, id_hi)
+    gpu, res = _run_case(2000, 128, 4, 8, 256, B, 64, steps=2, lr=0.1, std=0.02, seed=31 + B + id_hi,
+                         id_hi=id_hi)
+    _check(res)
     gpu.close()
 
 
