@@ -6,12 +6,16 @@ forward, cross-entropy, backward and the SGD update -- for vocab 2000, dim 128,
 4 layers, 8 heads, ffn 256, 8 windows x 64 tokens, resident on the GPU,
 launched eagerly on the library stream (`--graph`: replayed from a captured
 hipGraph instead).  Prints ONE JSON line: steps/s, a `roofline` object
-for the step's dominant kernel (timed live with hipEvents on the library
-stream), and a `cpu_baseline` object (the CPU oracle -- a single-threaded C
+for the step's dominant kernel (timed live on the library stream with the
+library's kernel timer), a `gemm4096` object (the 4096^3 NN GEMM measured in the same run)
+and a `cpu_baseline` object (the CPU oracle -- a single-threaded C
 restatement of lanternl's pure-Lua loops in double -- timed on this host).
+Kernel times (`kernel_ms`, `ms`) are dispatch start-to-end, as a kernel trace
+reports them; `*_events` figures are hipEvents around back-to-back launches.
 
   python bench.py [--steps K] [--warmup W]
   python bench.py --workload gemm4096      # the 4096^3 fp32 GEMM (C5) instead
+  python bench.py --workload dh2           # only the step's dominant kernel (counter passes)
   python bench.py --suite gemm             # C1/C3/C5 GEMM shapes, one JSON line each
   python bench.py --suite bandwidth        # C3/C4 bandwidth kernels, one JSON line each
   python bench.py --suite copy             # plain streaming kernel of known bytes (counter calibration)
@@ -82,24 +86,68 @@ def time_launches(fn, steps, warmup, recorded=False):
     return t.ms() / steps
 
 
+def kernel_ms(fn, calls, warmup=1):
+    """Kernel time per call of fn(i) the way a kernel trace (rocprofv3
+    --kernel-trace) reports it: the library's kernel timer records each
+    dispatch's start and end timestamps (lhip_ktimer_*), and a call's time is
+    the sum over the kernels it launched.  Launch gaps are not included.
+    Returns (ms per call, kernels per call)."""
+    from lanternl_amd import device
+    for i in range(warmup):
+        fn(i)
+    device.sync()
+    times = []
+    for i in range(calls):   # one call at a time: no launch waits behind another in the queue
+        times += device.kernel_times(lambda: fn(i), capacity=64)
+    if not times or len(times) % calls:
+        raise RuntimeError(f"kernel timer: {len(times)} dispatches for {calls} calls")
+    return sum(times) / calls, len(times) // calls
+
+
+def profile_figure(name, key):
+    """A figure recorded in a committed profile (profiles/<name>), on a line
+    `key: value` (the profile says how and at which commit it was measured)."""
+    import re
+    path = os.path.join(ROOT, "profiles", name)
+    if not os.path.exists(path):
+        return None, f"profiles/{name} is missing"
+    with open(path) as f:
+        text = f.read()
+    m = re.search(r"^" + re.escape(key) + r":\s*([0-9.]+)", text, re.M)
+    c = re.search(r"^measured_at_commit:\s*(\w+)", text, re.M)
+    if not m:
+        return None, f"profiles/{name} has no `{key}:` line"
+    return float(m.group(1)), f"profiles/{name}" + (f" (commit {c.group(1)})" if c else "")
+
+
 # ----------------------------------------------------------------------- GEMM
-def bench_gemm(m, n, k, ta=False, tb=False, steps=20, warmup=3, seed=0):
+def bench_gemm(m, n, k, ta=False, tb=False, steps=20, warmup=3, seed=0, rotate=False):
+    """fp32 GEMM timed with the kernel timer (`ms`, the kernel-trace figure
+    that `frac` uses) and with hipEvents around a recorded replay (`ms_events`).
+    rotate=True cycles over enough operand sets that one pass exceeds twice the
+    256 MB Infinity Cache, so an HBM-bound shape reads HBM, not the cache."""
     from lanternl_amd import device, kernels
     rng = np.random.default_rng(seed)
     a_shape = (k, m) if ta else (m, k)
     b_shape = (n, k) if tb else (k, n)
-    A = device.Buffer.from_numpy(rng.uniform(-1, 1, a_shape).astype(np.float32))
-    B = device.Buffer.from_numpy(rng.uniform(-1, 1, b_shape).astype(np.float32))
-    C = device.Buffer((m, n))
+    nbytes = 4.0 * (m * k + k * n + m * n)
+    nsets = max(1, -(-2 * MALL_BYTES // int(nbytes))) if rotate else 1
+    sets = []
+    for _ in range(nsets):
+        A = device.Buffer.from_numpy(rng.uniform(-1, 1, a_shape).astype(np.float32))
+        B = device.Buffer.from_numpy(rng.uniform(-1, 1, b_shape).astype(np.float32))
+        sets.append((A, B, device.Buffer((m, n))))
 
-    def run(_):
+    def run(i):
+        A, B, C = sets[i % nsets]
         kernels.sgemm(A, B, C, transa=ta, transb=tb)
-    ms = time_launches(run, steps, warmup, recorded=True)
+    ms_events = time_launches(run, steps, warmup, recorded=True)
+    ms, kpc = kernel_ms(run, steps)
     flops = 2.0 * m * n * k
     tflops = flops / (ms * 1e-3) / 1e12
     return {"m": m, "n": n, "k": k, "op": ("T" if ta else "N") + ("T" if tb else "N"),
-            "ms": ms, "tflops": tflops, "frac": tflops / PEAK_FP32_MFMA_TFLOPS,
-            "bytes": 4.0 * (m * k + k * n + m * n)}
+            "ms": ms, "ms_events": ms_events, "kernels_per_call": kpc, "tflops": tflops,
+            "frac": tflops / PEAK_FP32_MFMA_TFLOPS, "bytes": nbytes, "buffer_sets": nsets}
 
 
 def cpu_baseline_gemm(n=512, reps=4):
@@ -126,9 +174,9 @@ def cpu_baseline_gemm(n=512, reps=4):
 # [B*T, dim] output.  It is timed alone, with the step's shapes and layout
 # (the two gradients and the two weights adjacent), with hipEvents on the
 # library stream it runs on.
-# HBM bytes per launch of that kernel from rocprofv3 FETCH_SIZE / WRITE_SIZE
-# (scaled by the copy-kernel calibration): profiles/sgemm_batched_reduce_dh2.md.
-DOMINANT_C2_TRAFFIC_BYTES = 3_474_432
+# HBM bytes per launch come from that kernel's rocprofv3 FETCH_SIZE /
+# WRITE_SIZE passes (scaled by the copy-kernel calibration), read from
+# profiles/sgemm_batched_reduce_dh2.md.
 
 
 def dominant_kernel_c2(steps, warmup):
@@ -141,11 +189,13 @@ def dominant_kernel_c2(steps, warmup):
 
     def run(_):
         kernels.sgemm_batched_reduce(0, 1, N, D, F, 1.0, dzu.ptr, F, N * F, w13.ptr, F, D * F, 0.0, out.ptr, D, 2)
-    ms = time_launches(run, max(steps, 50), warmup, recorded=True)
+    calls = max(steps, 50)
+    ms_events = time_launches(run, calls, warmup, recorded=True)
+    ms, kpc = kernel_ms(run, calls)
     flops = 2.0 * N * D * (2 * F)
     tflops = flops / (ms * 1e-3) / 1e12
-    return {"ms": ms, "tflops": tflops, "frac": tflops / PEAK_FP32_MFMA_TFLOPS, "m": N, "n": D, "k": 2 * F,
-            "flops": flops}
+    return {"ms": ms, "ms_events": ms_events, "kernels_per_call": kpc, "tflops": tflops,
+            "frac": tflops / PEAK_FP32_MFMA_TFLOPS, "m": N, "n": D, "k": 2 * F, "flops": flops}
 
 
 def cpu_baseline_lm(nsteps=5):
@@ -184,6 +234,8 @@ def run_lm_workload(args):
     if not np.isfinite(st["loss"]):
         raise RuntimeError(f"non-finite loss after the timed steps: {st}")
     dom = dominant_kernel_c2(args.steps, args.warmup)
+    dom_traffic, dom_src = profile_figure("sgemm_batched_reduce_dh2.md", "traffic_bytes_per_launch")
+    g4 = gemm4096_object(args)
     flops = 3 * 1_000_341_504 * 1.0   # GEMM flops of one fwd+bwd step (forward x 3)
     line = {
         "metric": METRIC, "value": 1000.0 / ms, "unit": "steps/s", "n_gpus": 1,
@@ -196,25 +248,38 @@ def run_lm_workload(args):
         "step_gemm_tflops": flops / (ms * 1e-3) / 1e12,
         "last_step": {"loss": st["loss"], "grad_norm": st["grad_norm"], "applied": st["applied"]},
         "roofline": {"bound": "mfma", "achieved": dom["tflops"], "peak": PEAK_FP32_MFMA_TFLOPS,
-                     "unit": "TFLOP/s", "frac": dom["frac"], "traffic": DOMINANT_C2_TRAFFIC_BYTES,
+                     "unit": "TFLOP/s", "frac": dom["frac"], "traffic": dom_traffic,
+                     "traffic_source": dom_src,
                      "kernel": f"batch-reduce sgemm NT {dom['m']}x{dom['n']}x(2x{dom['k'] // 2}) "
                                f"(dh2 = dz1 . W1^T + du . W3^T), {dom['flops']:.0f} flop per launch",
-                     "kernel_ms": dom["ms"]},
+                     "kernel_ms": dom["ms"], "kernel_ms_events": dom["ms_events"],
+                     "kernel_ms_method": "kernel_ms: dispatch start-to-end timestamps per launch (library "
+                                         "kernel timer), as rocprofv3 --kernel-trace reports; kernel_ms_events: "
+                                         "hipEvents around a recorded replay of back-to-back launches "
+                                         "(includes launch gaps)"},
+        "gemm4096": g4,
         "cpu_baseline": cpu_baseline_lm(),
     }
     gpu.close()
     print(json.dumps(line), flush=True)
 
 
-# HBM bytes per 4096^3 NN launch from FETCH_SIZE / WRITE_SIZE with the copy
-# calibration: 2 x 196,747 + 65,536 = 459,030 KiB (profiles/sgemm_nn_4096.md).
-GEMM4096_TRAFFIC_BYTES = 459_030 * 1024
+def gemm4096_object(args):
+    """NN 4096^3 (config C5) in the same run: kernel-trace time, TFLOP/s and
+    fraction of the fp32 MFMA peak; HBM bytes per launch from the committed
+    FETCH_SIZE / WRITE_SIZE passes (profiles/sgemm_nn_4096.md)."""
+    r = bench_gemm(4096, 4096, 4096, steps=min(max(args.steps, 5), 20), warmup=min(args.warmup, 3) or 1)
+    traffic, src = profile_figure("sgemm_nn_4096.md", "traffic_bytes_per_launch")
+    return {"op": "NN", "m": 4096, "n": 4096, "k": 4096, "ms": r["ms"], "ms_events": r["ms_events"],
+            "tflops": r["tflops"], "frac": r["frac"], "peak": PEAK_FP32_MFMA_TFLOPS, "traffic": traffic,
+            "traffic_source": src}
 
 
 def run_gemm_workload(args):
     from lanternl_amd import device
     device.init(0)
     r = bench_gemm(4096, 4096, 4096, steps=args.steps, warmup=args.warmup)
+    traffic, src = profile_figure("sgemm_nn_4096.md", "traffic_bytes_per_launch")
     line = {
         "metric": METRIC, "value": r["tflops"], "unit": "TFLOP/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": r["ms"],
@@ -222,9 +287,11 @@ def run_gemm_workload(args):
         "data": "synthetic uniform[-1,1] seeded",
         "config": {"workload": "gemm_nn_4096^3 (config C5)", "m": 4096, "n": 4096, "k": 4096},
         "roofline": {"bound": "mfma", "achieved": r["tflops"], "peak": PEAK_FP32_MFMA_TFLOPS,
-                     "unit": "TFLOP/s", "frac": r["frac"], "traffic": GEMM4096_TRAFFIC_BYTES},
-        "cpu_baseline": cpu_baseline_gemm(),
+                     "unit": "TFLOP/s", "frac": r["frac"], "traffic": traffic, "traffic_source": src,
+                     "kernel_ms": r["ms"], "kernel_ms_events": r["ms_events"]},
     }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline_gemm()
     print(json.dumps(line), flush=True)
 
 
@@ -262,8 +329,12 @@ def run_gemm_suite(args):
     cases += [(512, 32000, 128, False, False), (128, 32000, 512, True, False), (512, 128, 32000, False, True)]
     for m, n, k, ta, tb in cases:
         steps = max(5, min(args.steps, int(4e12 / (2.0 * m * n * k)) + 5))
-        r = bench_gemm(m, n, k, ta, tb, steps=steps, warmup=args.warmup)
+        # the HBM-bound shapes (skinny M, C3's 32000-wide operands) rotate
+        # operand sets past the Infinity Cache
+        hbm = m <= 64 or max(m, n, k) == 32000
+        r = bench_gemm(m, n, k, ta, tb, steps=max(steps, 20) if hbm else steps, warmup=args.warmup, rotate=hbm)
         r["hbm_gbps_algorithmic"] = r["bytes"] / (r["ms"] * 1e-3) / 1e9
+        r["hbm_frac"] = r["hbm_gbps_algorithmic"] / PEAK_HBM_GBPS
         print(json.dumps({"suite": "gemm", **r}), flush=True)
     # the host-table boundary (PCIe and fp64 <-> fp32 conversions included)
     for m, k, n, op, reps in [(256, 128, 256, 0, 50), (256, 128, 256, 1, 50), (256, 128, 256, 2, 50),
@@ -282,10 +353,11 @@ def bench_bandwidth(name, nbytes, make_set, launch, steps, warmup, only=None):
 
     def run(i):
         launch(sets[i % nsets])
-    ms = time_launches(run, steps, warmup, recorded=True)
+    ms_events = time_launches(run, steps, warmup, recorded=True)
+    ms, kpc = kernel_ms(run, steps)
     gbps = nbytes / (ms * 1e-3) / 1e9
-    return {"suite": "bandwidth", "kernel": name, "ms": ms, "bytes": nbytes, "gbps": gbps,
-            "frac": gbps / PEAK_HBM_GBPS, "buffer_sets": nsets}
+    return {"suite": "bandwidth", "kernel": name, "ms": ms, "ms_events": ms_events, "kernels_per_call": kpc,
+            "bytes": nbytes, "gbps": gbps, "frac": gbps / PEAK_HBM_GBPS, "buffer_sets": nsets}
 
 
 def run_bandwidth_suite(args):
@@ -385,7 +457,9 @@ def main():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=10)
-    p.add_argument("--workload", default="lmtrain_c2", choices=["lmtrain_c2", "gemm4096"])
+    p.add_argument("--workload", default="lmtrain_c2", choices=["lmtrain_c2", "gemm4096", "dh2"],
+                   help="dh2: only the step's dominant kernel (for counter passes)")
+    p.add_argument("--no-cpu", action="store_true", help="gemm4096: skip the CPU baseline (counter passes)")
     p.add_argument("--graph", action="store_true",
                    help="replay the LM step from a captured hipGraph (default: eager launches on the library "
                         "stream)")
@@ -405,6 +479,10 @@ def main():
         run_copy_suite(args)
     elif args.workload == "gemm4096":
         run_gemm_workload(args)
+    elif args.workload == "dh2":
+        from lanternl_amd import device
+        device.init(0)
+        print(json.dumps({"workload": "dh2", **dominant_kernel_c2(args.steps, args.warmup)}), flush=True)
     else:
         run_lm_workload(args)
 

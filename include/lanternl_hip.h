@@ -142,6 +142,18 @@ LHIP_API int lhip_program_replay(void* program, int times);
 LHIP_API int lhip_program_free(void* program);
 LHIP_API int lhip_is_recording(void);
 
+/* Kernel timer.  No counterpart in the reference (the reference's
+ * luaTL.Program `timing` flag, ai/gpu/luaTL_train.lua:332-333, times a whole
+ * program run; this times each kernel).  For benchmarks that must agree with
+ * a kernel trace: between start and stop, each of the first `capacity` kernel
+ * launches records its dispatch's start and end timestamps (launch gaps
+ * excluded).  stop synchronises the stream, writes the durations in launch
+ * order to ms[0 .. min(count, capacity)) and the number of timed launches to
+ * *count.  Not allowed while a program is being recorded (and
+ * lhip_program_begin refuses while the timer is on). */
+LHIP_API int lhip_ktimer_start(int capacity);
+LHIP_API int lhip_ktimer_stop(float* ms, int capacity, int* count);
+
 /* ---- GEMM family (fp32 on v_mfma_f32_32x32x2f32) ---------------------------
  * C(m x n) = alpha * op(A)(m x k) * op(B)(k x n) + beta * C, row-major.
  *   transa == 0: A is m x k, lda >= k;   transa != 0: A is stored k x m, lda >= m

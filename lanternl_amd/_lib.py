@@ -70,6 +70,8 @@ SIGNATURES = {
     "lhip_program_replay": (_i, [_p, _i]),
     "lhip_program_free": (_i, [_p]),
     "lhip_is_recording": (_i, []),
+    "lhip_ktimer_start": (_i, [_i]),
+    "lhip_ktimer_stop": (_i, [ctypes.POINTER(_f), _i, ctypes.POINTER(_i)]),
     "lhip_sgemm": (_i, [_i, _i, _i, _i, _i, _f, _p, _i, _p, _i, _f, _p, _i]),
     "lhip_sgemm_strided_batched": (_i, [_i, _i, _i, _i, _i, _f, _p, _i, _ll, _p, _i, _ll, _f,
                                         _p, _i, _ll, _i]),

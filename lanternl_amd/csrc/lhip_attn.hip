@@ -553,7 +553,7 @@ int attn_fwd(const float* qkv, const float2* cs, float* P, float* ctx, int B, in
     a.scale = scale; a.causal = causal; a.wlen = wlen;
     a.vec = (hd % 4 == 0 && aligned16(qkv) && aligned16(cs)) ? 1 : 0;
     a.vec = a.vec && aligned16(ctx);
-    attn_fwd_kernel<<<B * H * ((T + 15) / 16), kAttnThreads, 0, s>>>(a);
+    klaunch(attn_fwd_kernel, B * H * ((T + 15) / 16), kAttnThreads, 0, s, a);
     return check_launch("attn_fwd");
 }
 
@@ -569,7 +569,7 @@ int attn_bwd(const float* qkv, const float2* cs, const float* P, const float* ct
     // the float4 path also reads ctx (the forward's O, for rowsum(dO*O))
     a.vec = (hd % 4 == 0 && aligned16(qkv) && aligned16(cs) && aligned16(ctx) && aligned16(dctx) &&
              aligned16(dqkv)) ? 1 : 0;
-    attn_bwd_kernel<<<B * H * ((T + 15) / 16), kAttnThreads, 0, s>>>(a);
+    klaunch(attn_bwd_kernel, B * H * ((T + 15) / 16), kAttnThreads, 0, s, a);
     return check_launch("attn_bwd");
 }
 

@@ -15,9 +15,11 @@
 namespace lhip {
 
 static State g_state;
+static KTimer g_ktimer;
 static thread_local char t_err[1024] = {0};
 
 State& st() { return g_state; }
+KTimer& ktimer() { return g_ktimer; }
 
 int fail(int code, const char* fmt, ...)
 {
@@ -164,6 +166,8 @@ LHIP_API int lhip_shutdown(void)
     if (s.work) (void)hipFree(s.work);
     for (void* p : s.retired) (void)hipFree(p);
     if (s.ones) (void)hipFree(s.ones);
+    for (hipEvent_t e : lhip::ktimer().ev) (void)hipEventDestroy(e);
+    lhip::ktimer() = lhip::KTimer();
     (void)hipStreamDestroy(s.stream);
     s = lhip::State();
     return LHIP_OK;
@@ -354,6 +358,7 @@ LHIP_API int lhip_program_begin(void)
     LHIP_REQUIRE_READY();
     auto& s = st();
     if (s.recording) return fail(LHIP_E_ARG, "lhip_program_begin: a program is already being recorded");
+    if (lhip::ktimer().on) return fail(LHIP_E_UNSUPPORTED, "lhip_program_begin: the kernel timer is on");
     LHIP_CHECK_HIP(hipStreamBeginCapture(s.stream, hipStreamCaptureModeRelaxed), "lhip_program_begin");
     s.recording = true;
     return LHIP_OK;
@@ -416,5 +421,43 @@ LHIP_API int lhip_program_free(void* program)
 }
 
 LHIP_API int lhip_is_recording(void) { return st().recording ? 1 : 0; }
+
+// ---- kernel timer ----
+// Each kernel launched while the timer is on gets its dispatch's start and
+// end timestamps recorded (hipExtLaunchKernel with an event pair), which is
+// what a kernel trace reports as its duration; launch gaps are not included.
+
+LHIP_API int lhip_ktimer_start(int capacity)
+{
+    LHIP_REQUIRE_READY();
+    LHIP_REFUSE_RECORDING();
+    auto& kt = lhip::ktimer();
+    if (kt.on) return fail(LHIP_E_ARG, "lhip_ktimer_start: the timer is already on");
+    if (capacity < 1 || capacity > (1 << 16))
+        return fail(LHIP_E_ARG, "lhip_ktimer_start: capacity %d outside [1, 65536]", capacity);
+    while (kt.ev.size() < static_cast<size_t>(2 * capacity)) {
+        hipEvent_t e = nullptr;
+        LHIP_CHECK_HIP(hipEventCreate(&e), "lhip_ktimer_start: hipEventCreate");
+        kt.ev.push_back(e);
+    }
+    kt.cap = capacity;
+    kt.used = 0;
+    kt.on = true;
+    return LHIP_OK;
+}
+
+LHIP_API int lhip_ktimer_stop(float* ms, int capacity, int* count)
+{
+    LHIP_REQUIRE_READY();
+    auto& kt = lhip::ktimer();
+    if (!kt.on) return fail(LHIP_E_ARG, "lhip_ktimer_stop: the timer is not on");
+    kt.on = false;
+    if (count) *count = kt.used;
+    LHIP_CHECK_HIP(hipStreamSynchronize(st().stream), "lhip_ktimer_stop: stream sync");
+    if (ms && capacity > 0)
+        for (int i = 0; i < kt.used && i < capacity; ++i)
+            LHIP_CHECK_HIP(hipEventElapsedTime(&ms[i], kt.ev[2 * i], kt.ev[2 * i + 1]), "lhip_ktimer_stop: elapsed");
+    return LHIP_OK;
+}
 
 }  // extern "C"

@@ -446,7 +446,7 @@ int fill(float* p, long long n, float v, hipStream_t s)
     if (n <= 0) return LHIP_OK;
     if (!p) return fail(LHIP_E_NULL, "fill: NULL pointer");
     if (!aligned16(p)) return fail(LHIP_E_ARG, "fill: pointer must be 16-byte aligned");
-    fill_kernel<<<grid_for((n + 3) / 4, 256), 256, 0, s>>>(p, n, v);
+    klaunch(fill_kernel, grid_for((n + 3) / 4, 256), 256, 0, s, p, n, v);
     return check_launch("fill");
 }
 
@@ -455,7 +455,7 @@ int zero_bytes(void* p, size_t bytes, hipStream_t s)
     if (bytes == 0) return LHIP_OK;
     if (!p) return fail(LHIP_E_NULL, "zero: NULL pointer");
     if (aligned16(p) && bytes % 4 == 0) return fill(static_cast<float*>(p), static_cast<long long>(bytes / 4), 0.f, s);
-    fill_bytes_kernel<<<grid_for(static_cast<long long>(bytes), 256), 256, 0, s>>>(static_cast<unsigned char*>(p),
+    klaunch(fill_bytes_kernel, grid_for(static_cast<long long>(bytes), 256), 256, 0, s, static_cast<unsigned char*>(p),
                                                                                   static_cast<long long>(bytes));
     return check_launch("zero");
 }
@@ -466,7 +466,7 @@ int add(const float* a, const float* b, float* o, long long n, hipStream_t s)
     if (n == 0) return LHIP_OK;
     if (!a || !b || !o) return fail(LHIP_E_NULL, "add: NULL pointer");
     const int vec = aligned16(a) && aligned16(b) && aligned16(o);
-    add_kernel<<<grid_for(vec ? (n + 3) / 4 : n, 256), 256, 0, s>>>(a, b, o, n, vec);
+    klaunch(add_kernel, grid_for(vec ? (n + 3) / 4 : n, 256), 256, 0, s, a, b, o, n, vec);
     return check_launch("add");
 }
 
@@ -476,7 +476,7 @@ int silu(const float* x, float* o, long long n, hipStream_t s)
     if (n == 0) return LHIP_OK;
     if (!x || !o) return fail(LHIP_E_NULL, "silu: NULL pointer");
     const int vec = aligned16(x) && aligned16(o);
-    silu_kernel<<<grid_for(vec ? (n + 3) / 4 : n, 256), 256, 0, s>>>(x, o, n, vec);
+    klaunch(silu_kernel, grid_for(vec ? (n + 3) / 4 : n, 256), 256, 0, s, x, o, n, vec);
     return check_launch("silu");
 }
 
@@ -491,7 +491,7 @@ int swiglu_fwd(const float* g, int ldg, const float* u, int ldu, float* h, int l
                     aligned16(u) && aligned16(h) &&
                     static_cast<long long>(rows) * (cols / 4) < (1LL << 31);
     const long long units = static_cast<long long>(rows) * (vec ? cols / 4 : cols);
-    swiglu_fwd_kernel<<<grid_for(units, 256), 256, 0, s>>>(g, ldg, u, ldu, h, ldh, rows, cols, vec);
+    klaunch(swiglu_fwd_kernel, grid_for(units, 256), 256, 0, s, g, ldg, u, ldu, h, ldh, rows, cols, vec);
     return check_launch("swiglu_fwd");
 }
 
@@ -507,7 +507,7 @@ int swiglu_bwd(const float* g, int ldg, const float* u, int ldu, const float* dh
                     lddu % 4 == 0 && aligned16(g) && aligned16(u) && aligned16(dh) && aligned16(dg) && aligned16(du) &&
                     static_cast<long long>(rows) * (cols / 4) < (1LL << 31);
     const long long units = static_cast<long long>(rows) * (vec ? cols / 4 : cols);
-    swiglu_bwd_kernel<<<grid_for(units, 256), 256, 0, s>>>(g, ldg, u, ldu, dh, lddh, dg, lddg, du, lddu, rows,
+    klaunch(swiglu_bwd_kernel, grid_for(units, 256), 256, 0, s, g, ldg, u, ldu, dh, lddh, dg, lddg, du, lddu, rows,
                                                            cols, acc, vec);
     return check_launch("swiglu_bwd");
 }
@@ -535,7 +535,7 @@ int rope(float* x, const int* pos_ids, int rows, int heads, int hd, int row_stri
     const bool hs2 = !interleaved && pairs % 2 == 0 && row_stride % 2 == 0 &&
                      (reinterpret_cast<uintptr_t>(x) & 7u) == 0;
     const dim3 grid(ceil_div(rows, kRopeRowsPerBlock));
-#define LHIP_ROPE(M_) rope_kernel<M_><<<grid, 256, 0, s>>>(x, pos_ids, rows, heads, hd, row_stride, pos_offset, \
+#define LHIP_ROPE(M_) klaunch(rope_kernel<M_>, grid, 256, 0, s, x, pos_ids, rows, heads, hd, row_stride, pos_offset, \
                                                            period, interleaved, inverse, fr)
     if (il4) LHIP_ROPE(ROPE_IL4);
     else if (hs4) LHIP_ROPE(ROPE_HS4);
@@ -552,7 +552,7 @@ int embed_fwd(const float* table, const int* ids, float* out, int n, int dim, in
     if (!table || !ids || !out) return fail(LHIP_E_NULL, "embed_fwd: NULL pointer");
     const int vec = dim % 4 == 0 && aligned16(table) && aligned16(out);
     const long long units = static_cast<long long>(n) * (vec ? dim / 4 : dim);
-    embed_fwd_kernel<<<grid_for(units, 256), 256, 0, s>>>(table, ids, out, n, dim, vocab, vec);
+    klaunch(embed_fwd_kernel, grid_for(units, 256), 256, 0, s, table, ids, out, n, dim, vocab, vec);
     return check_launch("embed_fwd");
 }
 
@@ -562,7 +562,7 @@ int embed_bwd(const float* g, const int* ids, float* dtable, int n, int dim, int
     if (n < 0 || dim <= 0 || vocab <= 0) return fail(LHIP_E_SHAPE, "embed_bwd: n=%d dim=%d vocab=%d", n, dim, vocab);
     if (!dtable) return fail(LHIP_E_NULL, "embed_bwd: dtable is NULL");
     if (n > 0 && (!g || !ids)) return fail(LHIP_E_NULL, "embed_bwd: NULL g/ids");
-    embed_bwd_kernel<<<vocab, 64, 0, s>>>(g, ids, dtable, n, dim, vocab, scale, acc);
+    klaunch(embed_bwd_kernel, vocab, 64, 0, s, g, ids, dtable, n, dim, vocab, scale, acc);
     return check_launch("embed_bwd");
 }
 

@@ -615,10 +615,10 @@ int launch_256(int ta, int tb, GemmArgs g, int batch, hipStream_t stream)
                       (ta || g.vecA) && (!tb || g.vecB);
     auto go = [&](auto fullc) {
         constexpr bool F = decltype(fullc)::value;
-        if (!ta && !tb) sgemm_256_kernel<false, false, F><<<grid, block, 0, stream>>>(g);
-        else if (ta && !tb) sgemm_256_kernel<true, false, F><<<grid, block, 0, stream>>>(g);
-        else if (!ta && tb) sgemm_256_kernel<false, true, F><<<grid, block, 0, stream>>>(g);
-        else sgemm_256_kernel<true, true, F><<<grid, block, 0, stream>>>(g);
+        if (!ta && !tb) klaunch(sgemm_256_kernel<false, false, F>, grid, block, 0, stream, g);
+        else if (ta && !tb) klaunch(sgemm_256_kernel<true, false, F>, grid, block, 0, stream, g);
+        else if (!ta && tb) klaunch(sgemm_256_kernel<false, true, F>, grid, block, 0, stream, g);
+        else klaunch(sgemm_256_kernel<true, true, F>, grid, block, 0, stream, g);
     };
     if (full) go(std::true_type{});
     else go(std::false_type{});
@@ -1389,9 +1389,9 @@ template <bool TA, bool TB, bool BR>
 void launch_small_t(const GemmArgs& g, dim3 grid, hipStream_t stream)
 {
     if (small_long_k(g))
-        sgemm_small_kernel<TA, TB, BR, kSmallWavesLongK><<<grid, dim3(64 * kSmallWavesLongK), 0, stream>>>(g);
+        klaunch(sgemm_small_kernel<TA, TB, BR, kSmallWavesLongK>, grid, dim3(64 * kSmallWavesLongK), 0, stream, g);
     else
-        sgemm_small_kernel<TA, TB, BR, 4><<<grid, dim3(256), 0, stream>>>(g);
+        klaunch(sgemm_small_kernel<TA, TB, BR, 4>, grid, dim3(256), 0, stream, g);
 }
 
 int launch_reduce(const GemmArgs& g, int batch, hipStream_t stream);
@@ -1402,12 +1402,12 @@ void launch_tiny_t(int ta, int tb, const GemmArgs& g, dim3 grid, hipStream_t str
 {
     const dim3 block(64 * NW);
     if (g.Kb != g.K) {
-        if (!tb) sgemm_tiny_kernel<false, false, true, PIPE, NW><<<grid, block, 0, stream>>>(g);
-        else sgemm_tiny_kernel<false, true, true, PIPE, NW><<<grid, block, 0, stream>>>(g);
-    } else if (!ta && !tb) sgemm_tiny_kernel<false, false, false, PIPE, NW><<<grid, block, 0, stream>>>(g);
-    else if (ta && !tb) sgemm_tiny_kernel<true, false, false, PIPE, NW><<<grid, block, 0, stream>>>(g);
-    else if (!ta && tb) sgemm_tiny_kernel<false, true, false, PIPE, NW><<<grid, block, 0, stream>>>(g);
-    else sgemm_tiny_kernel<true, true, false, PIPE, NW><<<grid, block, 0, stream>>>(g);
+        if (!tb) klaunch(sgemm_tiny_kernel<false, false, true, PIPE, NW>, grid, block, 0, stream, g);
+        else klaunch(sgemm_tiny_kernel<false, true, true, PIPE, NW>, grid, block, 0, stream, g);
+    } else if (!ta && !tb) klaunch(sgemm_tiny_kernel<false, false, false, PIPE, NW>, grid, block, 0, stream, g);
+    else if (ta && !tb) klaunch(sgemm_tiny_kernel<true, false, false, PIPE, NW>, grid, block, 0, stream, g);
+    else if (!ta && tb) klaunch(sgemm_tiny_kernel<false, true, false, PIPE, NW>, grid, block, 0, stream, g);
+    else klaunch(sgemm_tiny_kernel<true, true, false, PIPE, NW>, grid, block, 0, stream, g);
 }
 
 int launch_tiny(int ta, int tb, GemmArgs g, int batch, hipStream_t stream)
@@ -1485,8 +1485,8 @@ int skinny_plan(int m, int n, int k, size_t ws_floats, int* kchunk_out)
 template <bool TA, bool VEC>
 void launch_skinny_t(const GemmArgs& g, dim3 grid, hipStream_t stream)
 {
-    if (g.M == 1) sgemm_skinny_kernel<1, TA, VEC><<<grid, 256, 0, stream>>>(g);
-    else sgemm_skinny_kernel<2, TA, VEC><<<grid, 256, 0, stream>>>(g);
+    if (g.M == 1) klaunch(sgemm_skinny_kernel<1, TA, VEC>, grid, 256, 0, stream, g);
+    else klaunch(sgemm_skinny_kernel<2, TA, VEC>, grid, 256, 0, stream, g);
 }
 
 int launch_skinny(int ta, GemmArgs g, hipStream_t stream)
@@ -1505,11 +1505,11 @@ int launch_skinny(int ta, GemmArgs g, hipStream_t stream)
             constexpr int MG = decltype(mgc)::value;
             constexpr int T = 64 * kSkinnyLdsWaves;
             if (ta) {
-                if (vec) sgemm_skinny_mfma_lds_kernel<true, true, MG><<<grid, T, 0, stream>>>(g);
-                else sgemm_skinny_mfma_lds_kernel<true, false, MG><<<grid, T, 0, stream>>>(g);
+                if (vec) klaunch(sgemm_skinny_mfma_lds_kernel<true, true, MG>, grid, T, 0, stream, g);
+                else klaunch(sgemm_skinny_mfma_lds_kernel<true, false, MG>, grid, T, 0, stream, g);
             } else {
-                if (vec) sgemm_skinny_mfma_lds_kernel<false, true, MG><<<grid, T, 0, stream>>>(g);
-                else sgemm_skinny_mfma_lds_kernel<false, false, MG><<<grid, T, 0, stream>>>(g);
+                if (vec) klaunch(sgemm_skinny_mfma_lds_kernel<false, true, MG>, grid, T, 0, stream, g);
+                else klaunch(sgemm_skinny_mfma_lds_kernel<false, false, MG>, grid, T, 0, stream, g);
             }
         };
         const int mg = ceil_div(g.M, 16);
@@ -1532,10 +1532,10 @@ int launch_cfg(int ta, int tb, GemmArgs g, int batch, hipStream_t stream)
     if (nwg > 0x7fffffffLL) return fail(LHIP_E_CAPACITY, "sgemm: %lld workgroups exceed the grid limit", nwg);
     if (g.splits <= 1) { g.splits = 1; g.kchunk = g.K; g.ws = nullptr; }
     dim3 grid(static_cast<unsigned>(nwg), batch, g.splits), block(kThreads, 1, 1);
-    if (!ta && !tb) sgemm_mfma_kernel<BM, BN, BK, false, false><<<grid, block, 0, stream>>>(g);
-    else if (ta && !tb) sgemm_mfma_kernel<BM, BN, BK, true, false><<<grid, block, 0, stream>>>(g);
-    else if (!ta && tb) sgemm_mfma_kernel<BM, BN, BK, false, true><<<grid, block, 0, stream>>>(g);
-    else sgemm_mfma_kernel<BM, BN, BK, true, true><<<grid, block, 0, stream>>>(g);
+    if (!ta && !tb) klaunch(sgemm_mfma_kernel<BM, BN, BK, false, false>, grid, block, 0, stream, g);
+    else if (ta && !tb) klaunch(sgemm_mfma_kernel<BM, BN, BK, true, false>, grid, block, 0, stream, g);
+    else if (!ta && tb) klaunch(sgemm_mfma_kernel<BM, BN, BK, false, true>, grid, block, 0, stream, g);
+    else klaunch(sgemm_mfma_kernel<BM, BN, BK, true, true>, grid, block, 0, stream, g);
     int rc = check_launch("sgemm: kernel launch");
     if (rc != LHIP_OK || g.splits <= 1 || g.skip_reduce) return rc;
     return launch_reduce(g, batch, stream);
@@ -1550,14 +1550,14 @@ int launch_reduce(const GemmArgs& g, int batch, hipStream_t stream)
         long long rg = (total4 + 255) / 256;
         const long long cap = static_cast<long long>(st().cu_count > 0 ? st().cu_count : 256) * 4;
         if (rg > cap) rg = cap;
-        splitk_reduce4<<<static_cast<int>(rg), 256, 0, stream>>>(g);
+        klaunch(splitk_reduce4, static_cast<int>(rg), 256, 0, stream, g);
         return check_launch("sgemm: split-K reduce");
     }
     const long long total = static_cast<long long>(g.M) * g.N * batch;
     long long rg = (total + 255) / 256;
     const long long cap = static_cast<long long>(st().cu_count > 0 ? st().cu_count : 256) * 4;
     if (rg > cap) rg = cap;
-    splitk_reduce<<<static_cast<int>(rg), 256, 0, stream>>>(g, batch);
+    klaunch(splitk_reduce, static_cast<int>(rg), 256, 0, stream, g, batch);
     return check_launch("sgemm: split-K reduce");
 }
 
@@ -2071,11 +2071,11 @@ int sgemm_grouped_tn(const GroupedTN* g, int ngroups, int K, hipStream_t stream,
             ex->fused = 1;
             ex->ss_parts = static_cast<int>(grid);
         }
-        sgemm_grouped_tn_lds64_kernel<2><<<grid, 512, 0, stream>>>(ga);
+        klaunch(sgemm_grouped_tn_lds64_kernel<2>, grid, 512, 0, stream, ga);
     }
-    else if (vec) sgemm_grouped_tn_lds_kernel<<<grid, 256, 0, stream>>>(ga);
-    else if (K >= 256) sgemm_grouped_tn_kernel<8><<<grid, 512, 0, stream>>>(ga);
-    else sgemm_grouped_tn_kernel<4><<<grid, 256, 0, stream>>>(ga);
+    else if (vec) klaunch(sgemm_grouped_tn_lds_kernel, grid, 256, 0, stream, ga);
+    else if (K >= 256) klaunch(sgemm_grouped_tn_kernel<8>, grid, 512, 0, stream, ga);
+    else klaunch(sgemm_grouped_tn_kernel<4>, grid, 256, 0, stream, ga);
     int rc = check_launch("sgemm_grouped_tn");
     if (rc != LHIP_OK || cs_fused || !cs || cs->njobs <= 0) return rc;
     return rmsnorm_bwd_colsum_multi(cs->partial, cs->nparts, cs->out, cs->njobs, cs->cols, cs->acc, stream);

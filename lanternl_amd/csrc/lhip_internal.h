@@ -6,7 +6,10 @@
 // message retrievable through lhip_last_error(), and returns a status code.
 #pragma once
 
+#include <tuple>
+#include <type_traits>
 #include <unordered_map>
+#include <utility>
 #include <vector>
 #include <hip/hip_runtime.h>
 
@@ -55,6 +58,41 @@ struct State {
 constexpr int kOnesMax = 65536;
 
 State& st();
+
+// Kernel timer (lhip_ktimer_start/stop): while it is on, every launch made
+// through klaunch records its dispatch's start and end on an event pair, the
+// timestamps a kernel trace reports, for up to `cap` launches.
+struct KTimer {
+    bool on = false;
+    int cap = 0, used = 0;
+    std::vector<hipEvent_t> ev;   // 2 per launch
+};
+KTimer& ktimer();
+
+template <typename K, typename Tup, size_t... I>
+inline void klaunch_packed(K k, dim3 g, dim3 b, unsigned sh, hipStream_t s, Tup& t, std::index_sequence<I...>)
+{
+    void* argv[] = {static_cast<void*>(&std::get<I>(t))...};
+    KTimer& kt = ktimer();
+    if (kt.on && kt.used < kt.cap) {
+        hipEvent_t e0 = kt.ev[2 * kt.used], e1 = kt.ev[2 * kt.used + 1];
+        ++kt.used;
+        (void)hipExtLaunchKernel(reinterpret_cast<const void*>(k), g, b, argv, sh, s, e0, e1, 0);
+    } else {
+        (void)hipLaunchKernel(reinterpret_cast<const void*>(k), g, b, argv, sh, s);
+    }
+}
+
+// Launch kernel k on stream s: the same as k<<<g, b, sh, s>>>(args...) (the
+// arguments are converted to k's parameter types first); launch errors are
+// read by check_launch as usual.
+template <typename... KArgs, typename... Args>
+inline void klaunch(void (*k)(KArgs...), dim3 g, dim3 b, unsigned sh, hipStream_t s, Args&&... args)
+{
+    static_assert(sizeof...(KArgs) == sizeof...(Args), "klaunch: argument count differs from the kernel's");
+    std::tuple<std::decay_t<KArgs>...> t(std::forward<Args>(args)...);
+    klaunch_packed(k, g, b, sh, s, t, std::index_sequence_for<KArgs...>{});
+}
 
 // The device ones vector for a gain-free row operation of n columns.
 int ones_vector(int n, const float** out);

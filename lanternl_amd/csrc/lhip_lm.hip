@@ -509,7 +509,7 @@ int run_step(LmModel& m, Hyper hp)
     hipStream_t s = st().stream;
     hp.gscale = m.nwin > 1 ? 1.0f / static_cast<float>(m.nwin) : 1.0f;   // optim2.scale_grads(1/n)
     if (m.use_graph) {
-        set_hyper_kernel<<<1, 64, 0, s>>>(m.hyper, hp);
+        klaunch(set_hyper_kernel, 1, 64, 0, s, m.hyper, hp);
         if (int rc = check_launch("lm step: hyper")) return rc;
         if (!m.exec || m.graph_opt != hp.opt)
             if (int rc = capture_step(m, s, hp)) return rc;

@@ -309,11 +309,11 @@ int lm_fused_gemm(const FuseCall& c, hipStream_t s)
     if (nwg > 0x7fffffffLL || c.batch > 65535) return fail(LHIP_E_CAPACITY, "lm_fused_gemm: grid too large");
     dim3 grid(static_cast<unsigned>(nwg), c.batch);
     switch (mode) {
-    case FUSE_NORM: lm_fused_gemm_kernel<FUSE_NORM><<<grid, 256, 0, s>>>(f); break;
-    case FUSE_NORM_SWIGLU: lm_fused_gemm_kernel<FUSE_NORM_SWIGLU><<<grid, 256, 0, s>>>(f); break;
-    case FUSE_SWIGLU_BWD: lm_fused_gemm_kernel<FUSE_SWIGLU_BWD><<<grid, 256, 0, s>>>(f); break;
-    case FUSE_NB_SWIGLU_BWD: lm_fused_gemm_kernel<FUSE_NB_SWIGLU_BWD><<<grid, 256, 0, s>>>(f); break;
-    case FUSE_NB_NT: lm_fused_gemm_kernel<FUSE_NB_NT><<<grid, 256, 0, s>>>(f); break;
+    case FUSE_NORM: klaunch(lm_fused_gemm_kernel<FUSE_NORM>, grid, 256, 0, s, f); break;
+    case FUSE_NORM_SWIGLU: klaunch(lm_fused_gemm_kernel<FUSE_NORM_SWIGLU>, grid, 256, 0, s, f); break;
+    case FUSE_SWIGLU_BWD: klaunch(lm_fused_gemm_kernel<FUSE_SWIGLU_BWD>, grid, 256, 0, s, f); break;
+    case FUSE_NB_SWIGLU_BWD: klaunch(lm_fused_gemm_kernel<FUSE_NB_SWIGLU_BWD>, grid, 256, 0, s, f); break;
+    case FUSE_NB_NT: klaunch(lm_fused_gemm_kernel<FUSE_NB_NT>, grid, 256, 0, s, f); break;
     default: return fail(LHIP_E_ARG, "lm_fused_gemm: mode %d", mode);
     }
     return check_launch("lm_fused_gemm");

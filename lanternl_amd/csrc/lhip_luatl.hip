@@ -161,7 +161,7 @@ template <int OP>
 void launch_ew(const float* a, const float* b, float* c, long long n, float alpha, float beta, hipStream_t s)
 {
     const int vec = (!a || aligned16(a)) && (!b || aligned16(b)) && aligned16(c);
-    ew_kernel<OP><<<grid_for(vec ? (n + 3) / 4 : n, kThreads), kThreads, 0, s>>>(a, b, c, n, alpha, beta, vec);
+    klaunch(ew_kernel<OP>, grid_for(vec ? (n + 3) / 4 : n, kThreads), kThreads, 0, s, a, b, c, n, alpha, beta, vec);
 }
 
 // ------------------------------------------------------------ strided rows
@@ -509,7 +509,7 @@ LHIP_API int lhip_row_rms(const float* x, float* out, int rows, int cols, long l
     if (rows == 0) return LHIP_OK;
     if (!x || !out) return fail(LHIP_E_NULL, "lhip_row_rms: NULL pointer");
     const int vec = cs == 1 && rs % 4 == 0 && cols % 4 == 0 && lhip::aligned16(x);
-    lhip::row_rms_kernel<<<lhip::waves_grid(rows), lhip::kThreads, 0, st().stream>>>(x, out, rows, cols, rs, cs, eps,
+    lhip::klaunch(lhip::row_rms_kernel, lhip::waves_grid(rows), lhip::kThreads, 0, st().stream, x, out, rows, cols, rs, cs, eps,
                                                                                     vec);
     return lhip::check_launch("lhip_row_rms");
 }
@@ -544,7 +544,7 @@ LHIP_API int lhip_rmsnorm_bwd_ex(const float* x, const float* w, const float* dy
     if (rc != LHIP_OK) return rc;
     hipStream_t s = st().stream;
     float* inv = work;
-    lhip::row_rms_kernel<<<lhip::waves_grid(rows), lhip::kThreads, 0, s>>>(x, inv, rows, cols, cols, 1, eps,
+    lhip::klaunch(lhip::row_rms_kernel, lhip::waves_grid(rows), lhip::kThreads, 0, s, x, inv, rows, cols, cols, 1, eps,
                                                                           cols % 4 == 0 && lhip::aligned16(x));
     rc = lhip::check_launch("lhip_rmsnorm_bwd_ex: 1/rms");
     if (rc != LHIP_OK) return rc;
@@ -567,7 +567,7 @@ LHIP_API int lhip_softmax_ex(const float* x, const float* bias, float* y, int ro
     // the register-resident row kernel has the same semantics
     if (!bias && (!causal || mask_offset >= 0))
         return lhip::softmax_fwd(x, y, rows, cols, scale, causal, mask_offset, group, st().stream);
-    lhip::softmax_ex_kernel<<<lhip::waves_grid(rows), lhip::kThreads, 0, st().stream>>>(x, bias, y, rows, cols, scale,
+    lhip::klaunch(lhip::softmax_ex_kernel, lhip::waves_grid(rows), lhip::kThreads, 0, st().stream, x, bias, y, rows, cols, scale,
                                                                                        causal, group, mask_offset);
     return lhip::check_launch("lhip_softmax_ex");
 }
@@ -581,7 +581,7 @@ LHIP_API int lhip_softmax_bwd_ex(const float* y, const float* dy, float* dx, int
     if (!y || !dy || !dx) return fail(LHIP_E_NULL, "lhip_softmax_bwd_ex: NULL y/dy/dx");
     if (!causal || mask_offset >= 0)
         return lhip::softmax_bwd(y, dy, dx, rows, cols, scale, causal, mask_offset, group, 0, st().stream);
-    lhip::softmax_bwd_ex_kernel<<<lhip::waves_grid(rows), lhip::kThreads, 0, st().stream>>>(
+    lhip::klaunch(lhip::softmax_bwd_ex_kernel, lhip::waves_grid(rows), lhip::kThreads, 0, st().stream, 
         y, dy, dx, rows, cols, scale, causal, group, mask_offset);
     return lhip::check_launch("lhip_softmax_bwd_ex");
 }
@@ -598,7 +598,7 @@ LHIP_API int lhip_swiglu_bwd_ex(const float* a, const float* b, const float* dou
         return lhip::swiglu_bwd(a, lda, b, ldb, dout, ldo, da, lda, db, ldb, rows, cols, 0, st().stream);
     if (!da && !db) return LHIP_OK;
     const long long n = static_cast<long long>(rows) * cols;
-    lhip::swiglu_bwd_one_kernel<<<lhip::grid_for(n, lhip::kThreads), lhip::kThreads, 0, st().stream>>>(
+    lhip::klaunch(lhip::swiglu_bwd_one_kernel, lhip::grid_for(n, lhip::kThreads), lhip::kThreads, 0, st().stream, 
         a, lda, b, ldb, dout, ldo, da, db, rows, cols);
     return lhip::check_launch("lhip_swiglu_bwd_ex");
 }
@@ -611,7 +611,7 @@ LHIP_API int lhip_reduce_cols(const float* x, float* out, int rows, int cols, lo
         return fail(LHIP_E_SHAPE, "lhip_reduce_cols: rows=%d cols=%d row_stride=%lld", rows, cols, row_stride);
     if (cols == 0) return LHIP_OK;
     if (!out || (rows > 0 && !x)) return fail(LHIP_E_NULL, "lhip_reduce_cols: NULL pointer");
-    lhip::reduce_cols_kernel<<<lhip::ceil_div(cols, 64), lhip::kThreads, 0, st().stream>>>(x, out, rows, cols,
+    lhip::klaunch(lhip::reduce_cols_kernel, lhip::ceil_div(cols, 64), lhip::kThreads, 0, st().stream, x, out, rows, cols,
                                                                                           row_stride, alpha, beta);
     return lhip::check_launch("lhip_reduce_cols");
 }
@@ -628,7 +628,7 @@ LHIP_API int lhip_l2_accum(const float* x, long long n, float* acc)
     if (rc != LHIP_OK) return rc;
     rc = lhip::sumsq_partials(x, n, partial, nb, st().stream);
     if (rc != LHIP_OK) return rc;
-    lhip::l2_finish_kernel<<<1, 64, 0, st().stream>>>(partial, nb, acc);
+    lhip::klaunch(lhip::l2_finish_kernel, 1, 64, 0, st().stream, partial, nb, acc);
     return lhip::check_launch("lhip_l2_accum");
 }
 
@@ -638,7 +638,7 @@ LHIP_API int lhip_clip_by_nsq(float* x, long long n, const float* nsq, float max
     if (n < 0) return fail(LHIP_E_SHAPE, "lhip_clip_by_nsq: n < 0");
     if (n == 0) return LHIP_OK;
     if (!x || !nsq) return fail(LHIP_E_NULL, "lhip_clip_by_nsq: NULL pointer");
-    lhip::clip_kernel<<<lhip::grid_for(n, lhip::kThreads), lhip::kThreads, 0, st().stream>>>(x, n, nsq, max_norm);
+    lhip::klaunch(lhip::clip_kernel, lhip::grid_for(n, lhip::kThreads), lhip::kThreads, 0, st().stream, x, n, nsq, max_norm);
     return lhip::check_launch("lhip_clip_by_nsq");
 }
 
@@ -648,7 +648,7 @@ LHIP_API int lhip_sum_accum(const float* x, long long n, float scale, float* acc
     if (n < 0) return fail(LHIP_E_SHAPE, "lhip_sum_accum: n < 0");
     if (!acc || (n > 0 && !x)) return fail(LHIP_E_NULL, "lhip_sum_accum: NULL pointer");
     if (n == 0) return LHIP_OK;
-    lhip::sum_accum_kernel<<<1, lhip::kThreads, 0, st().stream>>>(x, n, scale, acc);
+    lhip::klaunch(lhip::sum_accum_kernel, 1, lhip::kThreads, 0, st().stream, x, n, scale, acc);
     return lhip::check_launch("lhip_sum_accum");
 }
 
@@ -661,7 +661,7 @@ LHIP_API int lhip_transpose(const float* x, float* out, int rows, int cols)
     if (x == out) return fail(LHIP_E_ARG, "lhip_transpose: in place is not supported");
     if (lhip::ceil_div(rows, 64) > 65535) return fail(LHIP_E_CAPACITY, "lhip_transpose: rows=%d", rows);
     const dim3 grid(lhip::ceil_div(cols, 64), lhip::ceil_div(rows, 64));
-    lhip::transpose_kernel<<<grid, lhip::kThreads, 0, st().stream>>>(x, out, rows, cols);
+    lhip::klaunch(lhip::transpose_kernel, grid, lhip::kThreads, 0, st().stream, x, out, rows, cols);
     return lhip::check_launch("lhip_transpose");
 }
 
@@ -672,7 +672,7 @@ LHIP_API int lhip_bcast_add(const float* x, const float* v, float* out, int rows
     if (rows == 0 || cols == 0) return LHIP_OK;
     if (!x || !out) return fail(LHIP_E_NULL, "lhip_bcast_add: NULL pointer");
     const long long n = static_cast<long long>(rows) * cols;
-    lhip::bcast_add_kernel<<<lhip::grid_for(n, lhip::kThreads), lhip::kThreads, 0, st().stream>>>(x, v, out, rows, cols,
+    lhip::klaunch(lhip::bcast_add_kernel, lhip::grid_for(n, lhip::kThreads), lhip::kThreads, 0, st().stream, x, v, out, rows, cols,
                                                                                                alpha);
     return lhip::check_launch("lhip_bcast_add");
 }
@@ -690,7 +690,7 @@ LHIP_API int lhip_adamw_elementwise(float* w, const float* g, float* m, float* v
     const int t = step < 1 ? 1 : step;
     const float bc1 = 1.0f / (1.0f - powf(beta1, static_cast<float>(t)));
     const float bc2 = 1.0f / (1.0f - powf(beta2, static_cast<float>(t)));
-    lhip::adamw_ew_kernel<<<lhip::grid_for(n, lhip::kThreads), lhip::kThreads, 0, st().stream>>>(
+    lhip::klaunch(lhip::adamw_ew_kernel, lhip::grid_for(n, lhip::kThreads), lhip::kThreads, 0, st().stream, 
         w, g, m, v, w_mirror, n, lr, beta1, beta2, eps, weight_decay, bc1, bc2, clip);
     return lhip::check_launch("lhip_adamw_elementwise");
 }
@@ -740,7 +740,7 @@ LHIP_API int lhip_gemm_ex(const float* A, const float* B, float* C, const float*
     long long sa = a_bs;
     if (pre) {
         float* ap = work;
-        lhip::gemm_pre_kernel<<<lhip::waves_grid(static_cast<long long>(M) * batch), lhip::kThreads, 0, s>>>(
+        lhip::klaunch(lhip::gemm_pre_kernel, lhip::waves_grid(static_cast<long long>(M) * batch), lhip::kThreads, 0, s, 
             A, a_rs, a_cs, a_bs, gamma, rowscale, ap, M, K, batch, eps, pre_op);
         int rc = lhip::check_launch("lhip_gemm_ex: prologue");
         if (rc != LHIP_OK) return rc;
@@ -761,7 +761,7 @@ LHIP_API int lhip_gemm_ex(const float* A, const float* B, float* C, const float*
                                  static_cast<long long>(M) * N, batch, o, s);
         if (rc != LHIP_OK) return rc;
         const long long total = static_cast<long long>(M) * N * batch;
-        lhip::gemm_post_kernel<<<lhip::grid_for(total, lhip::kThreads), lhip::kThreads, 0, s>>>(
+        lhip::klaunch(lhip::gemm_post_kernel, lhip::grid_for(total, lhip::kThreads), lhip::kThreads, 0, s, 
             T, bias, C, c_rs, c_cs, c_bs, M, N, batch, beta, post_op);
         return lhip::check_launch("lhip_gemm_ex: epilogue");
     }

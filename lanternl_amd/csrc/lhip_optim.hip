@@ -258,8 +258,8 @@ int sumsq(const float* x, long long n, double* out, double* partial, int partial
     if (n > 0 && !x) return fail(LHIP_E_NULL, "sumsq: x is NULL");
     const int nb = sumsq_blocks(n);
     if (nb > partial_len) return fail(LHIP_E_CAPACITY, "sumsq: workspace %d < %d blocks", partial_len, nb);
-    sumsq_stage1<<<nb, kRedThreads, 0, s>>>(x, n, partial, aligned16(x) ? 1 : 0);
-    sum_stage2<<<1, 64, 0, s>>>(partial, nb, out);
+    klaunch(sumsq_stage1, nb, kRedThreads, 0, s, x, n, partial, aligned16(x) ? 1 : 0);
+    klaunch(sum_stage2, 1, 64, 0, s, partial, nb, out);
     return check_launch("sumsq");
 }
 
@@ -269,7 +269,7 @@ int sumsq_partials(const float* x, long long n, double* partial, int partial_len
     if (n > 0 && !x) return fail(LHIP_E_NULL, "sumsq: x is NULL");
     const int nb = sumsq_blocks(n);
     if (nb > partial_len) return fail(LHIP_E_CAPACITY, "sumsq: workspace %d < %d blocks", partial_len, nb);
-    sumsq_stage1<<<nb, kRedThreads, 0, s>>>(x, n, partial, aligned16(x) ? 1 : 0);
+    klaunch(sumsq_stage1, nb, kRedThreads, 0, s, x, n, partial, aligned16(x) ? 1 : 0);
     return check_launch("sumsq");
 }
 
@@ -288,7 +288,7 @@ int sgd_step(float* p, float* g, float* v, long long n, const double* sumsq_dev,
     const int vec = (aligned16(p) && aligned16(g) && (!v || aligned16(v))) ? 1 : 0;
     if (vec) blocks = std::min<long long>((n / 4 + 255) / 256, 4LL * cus);
     if (blocks < 1) blocks = 1;
-    sgd_step_kernel<<<static_cast<int>(blocks), 256, 0, s>>>(p, g, v, n, sumsq_dev, nparts, lr, momentum, wd,
+    klaunch(sgd_step_kernel, static_cast<int>(blocks), 256, 0, s, p, g, v, n, sumsq_dev, nparts, lr, momentum, wd,
                                                            grad_scale, clip_norm, nesterov, gnorm_out, applied_out,
                                                            hyper_dev, vec);
     return check_launch("sgd_step");
@@ -306,7 +306,7 @@ int adamw_step(float* p, float* g, float* m, float* v, long long n, const double
     long long blocks = (n + 255) / 256;
     if (blocks > 4LL * cus) blocks = 4LL * cus;
     if (blocks < 1) blocks = 1;
-    adamw_step_kernel<<<static_cast<int>(blocks), 256, 0, s>>>(p, g, m, v, n, sumsq_dev, nparts, lr, beta1, beta2,
+    klaunch(adamw_step_kernel, static_cast<int>(blocks), 256, 0, s, p, g, m, v, n, sumsq_dev, nparts, lr, beta1, beta2,
                                                              eps, wd, grad_scale, clip_norm, t_in, tcount, parity,
                                                              gnorm_out, applied_out, hyper_dev);
     return check_launch("adamw_step");
@@ -316,7 +316,7 @@ int sum_f32(const float* x, int n, float scale, float* out, hipStream_t s)
 {
     if (n < 0) return fail(LHIP_E_SHAPE, "sum_f32: n < 0");
     if (!out || (n > 0 && !x)) return fail(LHIP_E_NULL, "sum_f32: NULL pointer");
-    sum_f32_kernel<<<1, 256, 0, s>>>(x, n, scale, out);
+    klaunch(sum_f32_kernel, 1, 256, 0, s, x, n, scale, out);
     return check_launch("sum_f32");
 }
 

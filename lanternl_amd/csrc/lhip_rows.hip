@@ -702,12 +702,12 @@ int rmsnorm_fwd(const float* x, const float* w, float* y, float* inv, int rows, 
     const int nv = nv_for(cols);
     const bool vec = nv && cols % 4 == 0 && aligned16(x) && aligned16(w) && aligned16(y);
     dim3 g(vec ? row_wave_blocks(rows) : row_blocks(rows)), b(kRowThreads);
-    if (!vec) rmsnorm_fwd_generic<<<g, b, 0, s>>>(x, w, y, inv, rows, cols, eps);
-    else if (nv == 1) rmsnorm_fwd_vec<1><<<g, b, 0, s>>>(x, w, y, inv, rows, cols, eps);
-    else if (nv == 2) rmsnorm_fwd_vec<2><<<g, b, 0, s>>>(x, w, y, inv, rows, cols, eps);
-    else if (nv == 4) rmsnorm_fwd_vec<4><<<g, b, 0, s>>>(x, w, y, inv, rows, cols, eps);
-    else if (nv == 8) rmsnorm_fwd_vec<8><<<g, b, 0, s>>>(x, w, y, inv, rows, cols, eps);
-    else rmsnorm_fwd_vec<16><<<g, b, 0, s>>>(x, w, y, inv, rows, cols, eps);
+    if (!vec) klaunch(rmsnorm_fwd_generic, g, b, 0, s, x, w, y, inv, rows, cols, eps);
+    else if (nv == 1) klaunch(rmsnorm_fwd_vec<1>, g, b, 0, s, x, w, y, inv, rows, cols, eps);
+    else if (nv == 2) klaunch(rmsnorm_fwd_vec<2>, g, b, 0, s, x, w, y, inv, rows, cols, eps);
+    else if (nv == 4) klaunch(rmsnorm_fwd_vec<4>, g, b, 0, s, x, w, y, inv, rows, cols, eps);
+    else if (nv == 8) klaunch(rmsnorm_fwd_vec<8>, g, b, 0, s, x, w, y, inv, rows, cols, eps);
+    else klaunch(rmsnorm_fwd_vec<16>, g, b, 0, s, x, w, y, inv, rows, cols, eps);
     return check_launch("rmsnorm_fwd");
 }
 
@@ -760,8 +760,8 @@ int rmsnorm_bwd_rows(const float* x, const float* w, const float* inv, const flo
     const dim3 g(blocks);
     const size_t lds = static_cast<size_t>(nw) * cols * sizeof(float);
 #define LHIP_RBV(NV_, NW_) \
-    rmsnorm_bwd_vec<NV_, NW_><<<g, 64 * NW_, lds, s>>>(x, w, inv, dy, dx, dres, partial, rows, cols)
-    if (!vec) rmsnorm_bwd_generic<<<g, kRowThreads, 0, s>>>(x, w, inv, dy, dx, dres, partial, rows, cols);
+    klaunch(rmsnorm_bwd_vec<NV_, NW_>, g, 64 * NW_, lds, s, x, w, inv, dy, dx, dres, partial, rows, cols)
+    if (!vec) klaunch(rmsnorm_bwd_generic, g, kRowThreads, 0, s, x, w, inv, dy, dx, dres, partial, rows, cols);
     else if (nv == 1) LHIP_RBV(1, 8);
     else if (nv == 2) LHIP_RBV(2, 8);
     else if (nv == 4) LHIP_RBV(4, 8);
@@ -794,8 +794,8 @@ int rmsnorm_bwd_colsum_multi(const float* const* partials, const int* parts, flo
     if (n == 0) return LHIP_OK;
     bool vec = cols % 4 == 0;
     for (int i = 0; i < n; ++i) vec = vec && aligned16(jobs.partial[i]) && aligned16(jobs.out[i]);
-    if (vec) colsum4_kernel<<<dim3(ceil_div(cols, 32), n), 256, 0, s>>>(jobs, cols, accumulate);
-    else colsum_kernel<<<dim3(ceil_div(cols, 32), n), 256, 0, s>>>(jobs, cols, accumulate);
+    if (vec) klaunch(colsum4_kernel, dim3(ceil_div(cols, 32), n), 256, 0, s, jobs, cols, accumulate);
+    else klaunch(colsum_kernel, dim3(ceil_div(cols, 32), n), 256, 0, s, jobs, cols, accumulate);
     return check_launch("rmsnorm_bwd: dw reduce");
 }
 
@@ -820,8 +820,8 @@ int softmax_fwd(const float* x, float* y, int rows, int cols, float scale, int c
     const int nv = nv_for(cols);
     const bool vec = nv && cols % 4 == 0 && aligned16(x) && aligned16(y);
     dim3 g(vec ? row_wave_blocks(rows) : row_blocks(rows)), b(kRowThreads);
-#define LHIP_SMF(NV_) softmax_fwd_vec<NV_><<<g, b, 0, s>>>(x, y, rows, cols, scale, causal, offset, group)
-    if (!vec) softmax_fwd_generic<<<g, b, 0, s>>>(x, y, rows, cols, scale, causal, offset, group);
+#define LHIP_SMF(NV_) klaunch(softmax_fwd_vec<NV_>, g, b, 0, s, x, y, rows, cols, scale, causal, offset, group)
+    if (!vec) klaunch(softmax_fwd_generic, g, b, 0, s, x, y, rows, cols, scale, causal, offset, group);
     else if (nv == 1) LHIP_SMF(1);
     else if (nv == 2) LHIP_SMF(2);
     else if (nv == 4) LHIP_SMF(4);
@@ -841,8 +841,8 @@ int softmax_bwd(const float* y, const float* dy, float* dx, int rows, int cols, 
     const int nv = nv_for(cols);
     const bool vec = nv && cols % 4 == 0 && aligned16(y) && aligned16(dy) && aligned16(dx);
     dim3 g(vec ? row_wave_blocks(rows) : row_blocks(rows)), b(kRowThreads);
-#define LHIP_SMB(NV_) softmax_bwd_vec<NV_><<<g, b, 0, s>>>(y, dy, dx, rows, cols, scale, causal, offset, group, accumulate)
-    if (!vec) softmax_bwd_generic<<<g, b, 0, s>>>(y, dy, dx, rows, cols, scale, causal, offset, group, accumulate);
+#define LHIP_SMB(NV_) klaunch(softmax_bwd_vec<NV_>, g, b, 0, s, y, dy, dx, rows, cols, scale, causal, offset, group, accumulate)
+    if (!vec) klaunch(softmax_bwd_generic, g, b, 0, s, y, dy, dx, rows, cols, scale, causal, offset, group, accumulate);
     else if (nv == 1) LHIP_SMB(1);
     else if (nv == 2) LHIP_SMB(2);
     else if (nv == 4) LHIP_SMB(4);
@@ -864,16 +864,16 @@ int ce_fused(const float* logits, const int* tgt, float* losses, float* dlogits,
     // rows walked block-stride: about 2 rows per workgroup once rows exceed the CUs
     const int nb_small = rows < 4 * cus ? rows : 4 * cus;
     if (vec && V <= 256 * 4 * 2)
-        ce_fused_vec<256, 2, true><<<nb_small, 256, 0, s>>>(logits, tgt, losses, dlogits, amax, rows, V, ignore_index, gscale,
+        klaunch(ce_fused_vec<256, 2, true>, nb_small, 256, 0, s, logits, tgt, losses, dlogits, amax, rows, V, ignore_index, gscale,
                                                           row_len, period);
     else if (vec && V <= 256 * 4 * 8)
-        ce_fused_vec<256, 8, true><<<nb_small, 256, 0, s>>>(logits, tgt, losses, dlogits, amax, rows, V, ignore_index, gscale,
+        klaunch(ce_fused_vec<256, 8, true>, nb_small, 256, 0, s, logits, tgt, losses, dlogits, amax, rows, V, ignore_index, gscale,
                                                           row_len, period);
     else if (vec && V <= 1024 * 4 * 8)
-        ce_fused_vec<1024, 8, false><<<rows, 1024, 0, s>>>(logits, tgt, losses, dlogits, amax, rows, V, ignore_index, gscale,
+        klaunch(ce_fused_vec<1024, 8, false>, rows, 1024, 0, s, logits, tgt, losses, dlogits, amax, rows, V, ignore_index, gscale,
                                                           row_len, period);
     else
-        ce_fused_generic<<<rows, 256, 0, s>>>(logits, tgt, losses, dlogits, amax, rows, V, ignore_index, gscale,
+        klaunch(ce_fused_generic, rows, 256, 0, s, logits, tgt, losses, dlogits, amax, rows, V, ignore_index, gscale,
                                                           row_len, period);
     return check_launch("ce_fused");
 }
@@ -883,7 +883,7 @@ int argmax_rows(const float* x, int* out, int rows, int cols, hipStream_t s)
     if (rows < 0 || cols <= 0) return fail(LHIP_E_SHAPE, "argmax_rows: rows=%d cols=%d", rows, cols);
     if (rows == 0) return LHIP_OK;
     if (!x || !out) return fail(LHIP_E_NULL, "argmax_rows: NULL x/out");
-    argmax_rows_kernel<<<row_blocks(rows), kRowThreads, 0, s>>>(x, out, rows, cols);
+    klaunch(argmax_rows_kernel, row_blocks(rows), kRowThreads, 0, s, x, out, rows, cols);
     return check_launch("argmax_rows");
 }
 

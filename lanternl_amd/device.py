@@ -140,6 +140,20 @@ class Timer:
             pass
 
 
+def kernel_times(fn, capacity=4096):
+    """Run fn() with the library's kernel timer on and return the duration
+    (ms) of each kernel it launched, in launch order: dispatch start to end,
+    as a kernel trace reports them (lhip_ktimer_start / lhip_ktimer_stop)."""
+    call("lhip_ktimer_start", capacity)
+    try:
+        fn()
+    finally:
+        buf = (ctypes.c_float * capacity)()
+        n = ctypes.c_int()
+        call("lhip_ktimer_stop", buf, capacity, ctypes.byref(n))
+    return [float(buf[i]) for i in range(min(n.value, capacity))]
+
+
 class Program:
     """A recorded sequence of library calls, replayed as one hipGraph launch.
 
