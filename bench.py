@@ -91,17 +91,20 @@ def kernel_ms(fn, calls, warmup=1):
     --kernel-trace) reports it: the library's kernel timer records each
     dispatch's start and end timestamps (lhip_ktimer_*), and a call's time is
     the sum over the kernels it launched.  Launch gaps are not included.
-    Returns (ms per call, kernels per call)."""
+    Returns (median ms per call, kernels per call)."""
     from lanternl_amd import device
     for i in range(warmup):
         fn(i)
     device.sync()
-    times = []
+    per_call, kpc = [], None
     for i in range(calls):   # one call at a time: no launch waits behind another in the queue
-        times += device.kernel_times(lambda: fn(i), capacity=64)
-    if not times or len(times) % calls:
-        raise RuntimeError(f"kernel timer: {len(times)} dispatches for {calls} calls")
-    return sum(times) / calls, len(times) // calls
+        t = device.kernel_times(lambda: fn(i), capacity=64)
+        if not t or (kpc is not None and len(t) != kpc):
+            raise RuntimeError(f"kernel timer: call {i} timed {len(t)} dispatches")
+        kpc = len(t)
+        per_call.append(sum(t))
+    # the median: a call that lands on a clock or power-state change is an outlier
+    return float(np.median(per_call)), kpc
 
 
 def profile_figure(name, key):
@@ -253,10 +256,10 @@ def run_lm_workload(args):
                      "kernel": f"batch-reduce sgemm NT {dom['m']}x{dom['n']}x(2x{dom['k'] // 2}) "
                                f"(dh2 = dz1 . W1^T + du . W3^T), {dom['flops']:.0f} flop per launch",
                      "kernel_ms": dom["ms"], "kernel_ms_events": dom["ms_events"],
-                     "kernel_ms_method": "kernel_ms: dispatch start-to-end timestamps per launch (library "
-                                         "kernel timer), as rocprofv3 --kernel-trace reports; kernel_ms_events: "
-                                         "hipEvents around a recorded replay of back-to-back launches "
-                                         "(includes launch gaps)"},
+                     "kernel_ms_method": "kernel_ms: median over calls of the dispatch start-to-end timestamps "
+                                         "(library kernel timer), as rocprofv3 --kernel-trace reports them; "
+                                         "kernel_ms_events: hipEvents around a recorded replay of back-to-back "
+                                         "launches (includes launch gaps)"},
         "gemm4096": g4,
         "cpu_baseline": cpu_baseline_lm(),
     }
