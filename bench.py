@@ -430,6 +430,22 @@ def run_bandwidth_suite(args):
                                lambda s: call("lhip_ce_fused", s[0].ptr, labels.ptr, s[2].ptr, s[1].ptr, R, V, -1,
                                               1.0 / R),
                                steps, warm, args.only))
+    # size-matched streaming references: what a kernel with no arithmetic and
+    # the same number of read and written streams reaches at these sizes
+    for rows, cols in ((T, Dm), (T, Fm)):
+        n = rows * cols
+        out.append(bench_bandwidth(f"reference silu {rows}x{cols} (1 read + 1 write)", 4 * 2 * n,
+                                   lambda i, n_=n: (B((n_,)).zero(), B((n_,))),
+                                   lambda s, n_=n: call("lhip_silu", s[0].ptr, s[1].ptr, n_),
+                                   steps, warm, args.only))
+        out.append(bench_bandwidth(f"reference silu in place {rows}x{cols} (1 read + 1 write)", 4 * 2 * n,
+                                   lambda i, n_=n: (B((n_,)).zero(),),
+                                   lambda s, n_=n: call("lhip_silu", s[0].ptr, s[0].ptr, n_),
+                                   steps, warm, args.only))
+        out.append(bench_bandwidth(f"reference add {rows}x{cols} (2 reads + 1 write)", 4 * 3 * n,
+                                   lambda i, n_=n: (B((n_,)).zero(), B((n_,)).zero(), B((n_,))),
+                                   lambda s, n_=n: call("lhip_add", s[0].ptr, s[1].ptr, s[2].ptr, n_),
+                                   steps, warm, args.only))
     for r in out:
         if r is not None:
             print(json.dumps(r), flush=True)

@@ -83,7 +83,8 @@ __global__ void silu_kernel(const float* x, float* o, long long n, int vec)
         float4* o4 = reinterpret_cast<float4*>(o);
         for (long long i = t0; i < n4; i += stride) {
             const float4 v = x4[i];
-            o4[i] = make_float4(silu_sign(v.x), silu_sign(v.y), silu_sign(v.z), silu_sign(v.w));
+            st_stream(reinterpret_cast<float*>(o4 + i),
+                      make_float4(silu_sign(v.x), silu_sign(v.y), silu_sign(v.z), silu_sign(v.w)));
         }
         for (long long i = 4 * n4 + t0; i < n; i += stride) o[i] = silu_sign(x[i]);
     } else {
@@ -103,7 +104,7 @@ __global__ void add_kernel(const float* __restrict__ a, const float* __restrict_
         float4* o4 = reinterpret_cast<float4*>(o);
         for (long long i = t0; i < n4; i += stride) {
             const float4 x = a4[i], y = b4[i];
-            o4[i] = make_float4(x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w);
+            st_stream(reinterpret_cast<float*>(o4 + i), make_float4(x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w));
         }
         for (long long i = 4 * n4 + t0; i < n; i += stride) o[i] = a[i] + b[i];
     } else {
