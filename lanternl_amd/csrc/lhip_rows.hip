@@ -400,6 +400,66 @@ softmax_fwd_vec(const float* __restrict__ x, float* __restrict__ y, int rows, in
     walk_rows<Row1<NV>>(rows, load, body);
 }
 
+// Long rows (2048 < cols <= 4096, cols % 1024 == 0): one 256-thread workgroup
+// per row, NPT float4 per thread (column c4 = thread + 256 i), the row max and
+// sum meeting in LDS in wave order.  A workgroup per row puts many more rows'
+// loads in flight than a wave per row (two rows per wave, two workgroups per
+// CU) at the same register cost per byte.
+template <int NPT>
+__global__ void __launch_bounds__(256)
+softmax_fwd_blk(const float* __restrict__ x, float* __restrict__ y, int rows, int cols, float scale,
+                int causal, int offset, int group)
+{
+    __shared__ float red[2][4];
+    const int row = blockIdx.x;
+    const int t = threadIdx.x, wv = t >> 6;
+    const int lim = softmax_lim(row, cols, causal, offset, group);
+    const float4* xr = reinterpret_cast<const float4*>(x + static_cast<size_t>(row) * cols);
+    float4 v[NPT];
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) {
+        const int c = t + 256 * i;
+        v[i] = 4 * c < lim ? ld_row(xr + c) : f4zero();
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) {
+        const int c = t + 256 * i;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float sv = (4 * c + e < lim) ? scale * f4get(v[i], e) : -INFINITY;
+            f4set(v[i], e, sv);
+            mx = fmaxf(mx, sv);
+        }
+    }
+    mx = wave_max(mx);
+    if ((t & 63) == 0) red[0][wv] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+    if (mx == -INFINITY || mx != mx) mx = 0.f;
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) {
+        const int c = t + 256 * i;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float ev = (4 * c + e < lim) ? expf(f4get(v[i], e) - mx) : 0.f;
+            f4set(v[i], e, ev);
+            sum += ev;
+        }
+    }
+    sum = wave_sum(sum);
+    if ((t & 63) == 0) red[1][wv] = sum;
+    __syncthreads();
+    sum = ((red[1][0] + red[1][1]) + red[1][2]) + red[1][3];
+    if (!(sum > 0.f)) sum = 1.f;
+    const float is = 1.0f / sum;
+    float4* yr = reinterpret_cast<float4*>(y + static_cast<size_t>(row) * cols);
+#pragma unroll
+    for (int i = 0; i < NPT; ++i)
+        st_stream(yr + t + 256 * i, make_float4(v[i].x * is, v[i].y * is, v[i].z * is, v[i].w * is));
+}
+
 __global__ void __launch_bounds__(kRowThreads)
 softmax_fwd_generic(const float* __restrict__ x, float* __restrict__ y, int rows, int cols, float scale,
                     int causal, int offset, int group)
@@ -473,6 +533,55 @@ softmax_bwd_vec(const float* __restrict__ y, const float* __restrict__ dy, float
         }
     };
     walk_rows<Row2<NV>>(rows, load, body);
+}
+
+// Long rows as softmax_fwd_blk: one 256-thread workgroup per row.
+template <int NPT>
+__global__ void __launch_bounds__(256)
+softmax_bwd_blk(const float* __restrict__ y, const float* __restrict__ dy, float* __restrict__ dx,
+                int rows, int cols, float scale, int causal, int offset, int group, int acc)
+{
+    __shared__ float red[4];
+    const int row = blockIdx.x;
+    const int t = threadIdx.x, wv = t >> 6;
+    const int lim = softmax_lim(row, cols, causal, offset, group);
+    const size_t base = static_cast<size_t>(row) * cols;
+    const float4* yr = reinterpret_cast<const float4*>(y + base);
+    const float4* gr = reinterpret_cast<const float4*>(dy + base);
+    float4 v[NPT], g[NPT];
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) {
+        const int c = t + 256 * i;
+        const bool in = 4 * c < lim;
+        v[i] = in ? ld_stream(yr + c) : f4zero();
+        g[i] = in ? ld_stream(gr + c) : f4zero();
+    }
+    float dot = 0.f;
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) {
+        const int c = t + 256 * i;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (4 * c + e < lim) dot += f4get(g[i], e) * f4get(v[i], e);
+    }
+    dot = wave_sum(dot);
+    if ((t & 63) == 0) red[wv] = dot;
+    __syncthreads();
+    dot = ((red[0] + red[1]) + red[2]) + red[3];
+    float4* dr = reinterpret_cast<float4*>(dx + base);
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) {
+        const int c = t + 256 * i;
+        float4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            f4set(o, e, (4 * c + e < lim) ? scale * (f4get(v[i], e) * (f4get(g[i], e) - dot)) : 0.f);
+        if (acc) {
+            const float4 old = dr[c];
+            o.x += old.x; o.y += old.y; o.z += old.z; o.w += old.w;
+        }
+        st_stream(dr + c, o);
+    }
 }
 
 __global__ void __launch_bounds__(kRowThreads)
@@ -821,7 +930,11 @@ int softmax_fwd(const float* x, float* y, int rows, int cols, float scale, int c
     const bool vec = nv && cols % 4 == 0 && aligned16(x) && aligned16(y);
     dim3 g(vec ? row_wave_blocks(rows) : row_blocks(rows)), b(kRowThreads);
 #define LHIP_SMF(NV_) klaunch(softmax_fwd_vec<NV_>, g, b, 0, s, x, y, rows, cols, scale, causal, offset, group)
-    if (!vec) klaunch(softmax_fwd_generic, g, b, 0, s, x, y, rows, cols, scale, causal, offset, group);
+    if (vec && cols > 2048 && cols <= 4096 && cols % 1024 == 0) {
+        if (cols == 3072) klaunch(softmax_fwd_blk<3>, dim3(rows), dim3(256), 0, s, x, y, rows, cols, scale, causal, offset, group);
+        else klaunch(softmax_fwd_blk<4>, dim3(rows), dim3(256), 0, s, x, y, rows, cols, scale, causal, offset, group);
+    }
+    else if (!vec) klaunch(softmax_fwd_generic, g, b, 0, s, x, y, rows, cols, scale, causal, offset, group);
     else if (nv == 1) LHIP_SMF(1);
     else if (nv == 2) LHIP_SMF(2);
     else if (nv == 4) LHIP_SMF(4);
@@ -842,7 +955,13 @@ int softmax_bwd(const float* y, const float* dy, float* dx, int rows, int cols, 
     const bool vec = nv && cols % 4 == 0 && aligned16(y) && aligned16(dy) && aligned16(dx);
     dim3 g(vec ? row_wave_blocks(rows) : row_blocks(rows)), b(kRowThreads);
 #define LHIP_SMB(NV_) klaunch(softmax_bwd_vec<NV_>, g, b, 0, s, y, dy, dx, rows, cols, scale, causal, offset, group, accumulate)
-    if (!vec) klaunch(softmax_bwd_generic, g, b, 0, s, y, dy, dx, rows, cols, scale, causal, offset, group, accumulate);
+    if (vec && cols > 2048 && cols <= 4096 && cols % 1024 == 0) {
+        if (cols == 3072) klaunch(softmax_bwd_blk<3>, dim3(rows), dim3(256), 0, s, y, dy, dx, rows, cols, scale, causal,
+                                  offset, group, accumulate);
+        else klaunch(softmax_bwd_blk<4>, dim3(rows), dim3(256), 0, s, y, dy, dx, rows, cols, scale, causal, offset, group,
+                     accumulate);
+    }
+    else if (!vec) klaunch(softmax_bwd_generic, g, b, 0, s, y, dy, dx, rows, cols, scale, causal, offset, group, accumulate);
     else if (nv == 1) LHIP_SMB(1);
     else if (nv == 2) LHIP_SMB(2);
     else if (nv == 4) LHIP_SMB(4);

@@ -34,7 +34,8 @@ def dl(buf):
 
 # ------------------------------------------------------------------ RMSNorm
 @pytest.mark.parametrize("rows,cols,eps", [(64, 128, 1e-5), (512, 128, 1e-5), (4096, 1024, 1e-6),
-                                           (7, 13, 1e-5), (3, 5000, 1e-6), (5, 4100, 1e-5), (9, 2048, 1e-6)])
+                                           (7, 13, 1e-5), (3, 5000, 1e-6), (5, 4100, 1e-5), (9, 2048, 1e-6),
+                                          (11, 3072, 1e-6), (6, 4096, 1e-5)])
 def test_rmsnorm_fwd_bwd(rows, cols, eps):
     announce("rmsnorm", rows, cols)
     rng = np.random.default_rng(rows * 31 + cols)
@@ -111,6 +112,8 @@ def softmax_bwd_ref(y, g, scale, causal, offset=0, group=None):
     (37, 53, 1.0, 1, 2, 0),              # generic path (cols % 4 != 0), offset
     (5, 5000, 0.5, 0, 0, 0),             # generic path (row too long for registers)
     (16, 20, 1.0, 1, -3, 8),             # negative offset: lim clamps to 1
+    (96, 3072, 0.5, 1, 5, 40),           # workgroup-per-row forward (3 float4 per thread), group-causal
+    (64, 4096, 1.0, 1, 0, 0),            # workgroup-per-row forward, causal prefix of a long row
 ])
 def test_softmax_fwd_bwd(rows, cols, scale, causal, offset, group):
     announce("softmax", rows, cols, causal, group)
@@ -128,6 +131,9 @@ def test_softmax_fwd_bwd(rows, cols, scale, causal, offset, group):
     G, DX = to_dev(g), device.Buffer((rows, cols))
     call("lhip_softmax_bwd", Y.ptr, G.ptr, DX.ptr, rows, cols, scale, causal, offset, group, 0)
     assert rel_fro(dl(DX), dx_ref) <= EW
+    # accumulate: a second call adds the same gradient
+    call("lhip_softmax_bwd", Y.ptr, G.ptr, DX.ptr, rows, cols, scale, causal, offset, group, 1)
+    assert rel_fro(dl(DX), 2 * dx_ref) <= EW
 
 
 def test_softmax_equal_logits_known_answer():
