@@ -19,6 +19,7 @@ reports them; `*_events` figures are hipEvents around back-to-back launches.
   python bench.py --suite gemm             # C1/C3/C5 GEMM shapes, one JSON line each
   python bench.py --suite bandwidth        # C3/C4 bandwidth kernels, one JSON line each
   python bench.py --suite copy             # plain streaming kernel of known bytes (counter calibration)
+  python bench.py --suite cpu              # CPU baselines: C1, C3, C4 and C5 1024^3 on the oracle (no GPU)
 
 Only one GPU is used; --gpus above 1 exits with a message.
 """
@@ -41,6 +42,27 @@ PEAK_HBM_GBPS = 8000.0          # MI355X HBM3E, published
 METRIC = "fp32 GEMM TFLOP/s and % of MFMA peak; LMTrain steps/sec at 1 MI355X"
 C2 = dict(vocab=2000, dim=128, layers=4, heads=8, ffn=256, batch=8, seq=64)
 MALL_BYTES = 256 << 20          # Infinity Cache: rotate working sets past it
+
+
+def _lscpu():
+    """Host CPU facts from lscpu: model name and total core count (sockets x
+    cores per socket) with the logical CPU count."""
+    import subprocess
+    info = {}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if ":" in line:
+                k, v = line.split(":", 1)
+                info[k.strip()] = v.strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        cores = int(info.get("Socket(s)", "0")) * int(info.get("Core(s) per socket", "0"))
+    except ValueError:
+        cores = 0
+    return {"model": info.get("Model name", _cpu_model()), "cores": cores or None,
+            "logical_cpus": int(info["CPU(s)"]) if info.get("CPU(s)", "").isdigit() else os.cpu_count()}
 
 
 def _cpu_model():
@@ -451,6 +473,77 @@ def run_bandwidth_suite(args):
             print(json.dumps(r), flush=True)
 
 
+def run_cpu_suite(args):
+    """CPU baselines of the stand-in for the reference's pure-Lua path (the
+    oracle: single-threaded C restatements of its loops in double; LuaJIT is
+    not installed): C1's three GEMM variants, each C4 kernel, C3's fused CE and
+    C5 1024^3, each a bounded sample timed on this host, one JSON line each."""
+    import oracle as O
+    host = _lscpu()
+    rng = np.random.default_rng(0)
+
+    def timed(fn, min_s=0.5, max_reps=50):
+        fn()
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            reps += 1
+            dt = time.perf_counter() - t0
+            if dt >= min_s or reps >= max_reps:
+                return dt / reps, reps
+
+    def line(case, dt, reps, value, unit, sample, gpu_ref):
+        print(json.dumps({"suite": "cpu", "case": case, "value": value, "unit": unit, "s_per_call": dt,
+                          "reps": reps, "cores": 1, "kind": "port", "sample": sample,
+                          "host_cpu": host["model"], "host_cores": host["cores"],
+                          "host_logical_cpus": host["logical_cpus"], "gpu_line": gpu_ref}), flush=True)
+
+    u = lambda *sh: rng.uniform(-1, 1, sh)   # noqa: E731
+    # C1: 256x128 . 128x256 and the transposed variants at matching shapes
+    a, b, at, bt = u(256, 128), u(128, 256), u(128, 256), u(256, 128)
+    for name, fn in (("C1 NN 256x128 . 128x256", lambda: O.mm(a, b)),
+                     ("C1 TN (128x256)^T . 128x256", lambda: O.matmul_tn(at, b)),
+                     ("C1 NT 256x128 . (256x128)^T", lambda: O.matmul_nt(a, bt))):
+        dt, reps = timed(fn)
+        line(name, dt, reps, 2.0 * 256 * 128 * 256 / dt / 1e9, "GFLOP/s", f"{reps} calls, double", "--suite gemm C1")
+    # C5 1024^3
+    a, b = u(1024, 1024), u(1024, 1024)
+    dt, reps = timed(lambda: O.mm(a, b), min_s=1.0, max_reps=3)
+    line("C5 NN 1024^3", dt, reps, 2.0 * 1024 ** 3 / dt / 1e9, "GFLOP/s", f"{reps} calls, double",
+         "--suite gemm NN 1024")
+    # C4 kernels on a 512-row sample of the 4096-row shapes (GB/s of the fp32
+    # bytes the GPU kernel moves for the same rows, so the two lines compare)
+    R, D, F = 512, 1024, 4096
+    x, w = rng.standard_normal((R, D)), rng.normal(1, 0.1, D)
+    y, inv = O.rmsnorm_fwd(x, w, 1e-6)
+    g = rng.standard_normal((R, D))
+    cases = [
+        ("C4 rmsnorm_fwd 512x1024 (of 4096x1024)", lambda: O.rmsnorm_fwd(x, w, 1e-6), 4 * (2 * R * D + D + R)),
+        ("C4 rmsnorm_bwd 512x1024 (of 4096x1024)", lambda: O.rmsnorm_bwd(x, w, inv, g), 4 * (3 * R * D + 2 * D + R)),
+        ("C4 rope_fwd 512x16x64 interleaved (of 4096)",
+         lambda: O.rope_heads(x, 16, 64, interleaved=True), 4 * 2 * R * D),
+        ("C4 rope_bwd 512x16x64 interleaved (of 4096)",
+         lambda: O.rope_heads(x, 16, 64, interleaved=True, inverse=True), 4 * 2 * R * D),
+    ]
+    gt, up, dh = rng.standard_normal((R, F)), rng.standard_normal((R, F)), rng.standard_normal((R, F))
+    sc = rng.normal(0, 2, (R, F))
+    sm = O.softmax_fwd(sc)
+    cases += [
+        ("C4 swiglu_fwd 512x4096 (of 4096x4096)", lambda: O.swiglu_fwd(gt, up), 4 * 3 * R * F),
+        ("C4 swiglu_bwd 512x4096 (of 4096x4096)", lambda: O.swiglu_bwd(gt, up, dh), 4 * 5 * R * F),
+        ("C4 softmax_fwd 512x4096 (of 4096x4096)", lambda: O.softmax_fwd(sc), 4 * 2 * R * F),
+        ("C4 softmax_bwd 512x4096 (of 4096x4096)", lambda: O.softmax_bwd(sm, dh), 4 * 3 * R * F),
+    ]
+    lg = rng.standard_normal((64, 32000))
+    tg = rng.integers(0, 32000, 64).astype(np.int32)
+    cases += [("C3 ce_fused 64x32000 (of 512x32000)", lambda: O.ce_fused(lg, tg, -1, 1.0 / 64),
+               4 * (2 * 64 * 32000 + 2 * 64))]
+    for name, fn, nbytes in cases:
+        dt, reps = timed(fn)
+        line(name, dt, reps, nbytes / dt / 1e9, "GB/s", f"{reps} calls, double arithmetic, fp32-equivalent bytes",
+             "--suite bandwidth")
+
+
 def run_copy_suite(args):
     """out = a + b over 64 Mi floats (768 MiB of traffic per launch: two 256 MiB
     reads, one 256 MiB write), the reference for scaling FETCH_SIZE/WRITE_SIZE."""
@@ -482,7 +575,7 @@ def main():
     p.add_argument("--graph", action="store_true",
                    help="replay the LM step from a captured hipGraph (default: eager launches on the library "
                         "stream)")
-    p.add_argument("--suite", default=None, choices=["gemm", "bandwidth", "copy"])
+    p.add_argument("--suite", default=None, choices=["gemm", "bandwidth", "copy", "cpu"])
     p.add_argument("--only", default=None, help="bandwidth suite: run only kernels whose name contains this")
     args = p.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -496,6 +589,8 @@ def main():
         run_bandwidth_suite(args)
     elif args.suite == "copy":
         run_copy_suite(args)
+    elif args.suite == "cpu":
+        run_cpu_suite(args)
     elif args.workload == "gemm4096":
         run_gemm_workload(args)
     elif args.workload == "dh2":
