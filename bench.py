@@ -320,7 +320,30 @@ def run_gemm_workload(args):
     print(json.dumps(line), flush=True)
 
 
-def bench_host_gemm(m, k, n, op=0, reps=20):
+def pcie_rates(nbytes=64 << 20, reps=10):
+    """Pinned-host <-> device copy rates (GB/s) on this box, through the HIP
+    runtime directly: the floor of the host-table path's transfers."""
+    hip = ctypes.CDLL("libamdhip64.so")
+    h, d = ctypes.c_void_p(), ctypes.c_void_p()
+    if hip.hipHostMalloc(ctypes.byref(h), ctypes.c_size_t(nbytes), 0) or hip.hipMalloc(ctypes.byref(d),
+                                                                                       ctypes.c_size_t(nbytes)):
+        raise RuntimeError("pcie_rates: allocation failed")
+    out = {}
+    try:
+        for name, dst, src, kind in (("h2d", d, h, 1), ("d2h", h, d, 2)):
+            for _ in range(2):
+                hip.hipMemcpy(dst, src, ctypes.c_size_t(nbytes), kind)
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                hip.hipMemcpy(dst, src, ctypes.c_size_t(nbytes), kind)
+            out[name] = nbytes * reps / (time.perf_counter() - t0) / 1e9
+    finally:
+        hip.hipFree(d)
+        hip.hipHostFree(h)
+    return out
+
+
+def bench_host_gemm(m, k, n, op=0, reps=20, rates=None, gemm_ms=None):
     """lhip_matmul_host (the flat-table adapter contract, luatl_adapter.lua:128-135):
     double host arrays in, fp32 conversion, upload, GEMM, download, double host
     array out, synchronous -- timed with the host clock around whole calls.
@@ -339,8 +362,16 @@ def bench_host_gemm(m, k, n, op=0, reps=20):
         call("lhip_matmul_host", *args)
     dt = (time.perf_counter() - t0) / reps
     nbytes = 8.0 * (m * k + nb + rows * n)
-    return {"suite": "gemm_host", "op": ["NN", "NT", "TN"][op], "m": m, "k": k, "n": n, "ms": dt * 1e3,
-            "tflops": 2.0 * m * k * n / dt / 1e12, "host_bytes": nbytes, "host_gbps": nbytes / dt / 1e9}
+    r = {"suite": "gemm_host", "op": ["NN", "NT", "TN"][op], "m": m, "k": k, "n": n, "ms": dt * 1e3,
+         "tflops": 2.0 * m * k * n / dt / 1e12, "host_bytes": nbytes, "host_gbps": nbytes / dt / 1e9}
+    if rates:
+        # the fp32 bytes that must cross PCIe (A and B up, C down) at the pinned rates
+        floor = 4.0 * (m * k + nb) / (rates["h2d"] * 1e9) + 4.0 * rows * n / (rates["d2h"] * 1e9)
+        r["pcie_floor_ms"] = floor * 1e3
+        if gemm_ms is not None:
+            r["gemm_ms"] = gemm_ms
+            r["vs_floor_plus_gemm"] = r["ms"] / (r["pcie_floor_ms"] + gemm_ms)
+    return r
 
 
 def run_gemm_suite(args):
@@ -361,10 +392,20 @@ def run_gemm_suite(args):
         r["hbm_gbps_algorithmic"] = r["bytes"] / (r["ms"] * 1e-3) / 1e9
         r["hbm_frac"] = r["hbm_gbps_algorithmic"] / PEAK_HBM_GBPS
         print(json.dumps({"suite": "gemm", **r}), flush=True)
-    # the host-table boundary (PCIe and fp64 <-> fp32 conversions included)
-    for m, k, n, op, reps in [(256, 128, 256, 0, 50), (256, 128, 256, 1, 50), (256, 128, 256, 2, 50),
-                              (1024, 1024, 1024, 0, 10), (4096, 4096, 4096, 0, 3)]:
-        print(json.dumps(bench_host_gemm(m, k, n, op, reps)), flush=True)
+    # the host-table boundary (PCIe and fp64 <-> fp32 conversions included),
+    # against the PCIe floor of its fp32 bytes plus the device GEMM
+    rates = pcie_rates()
+    print(json.dumps({"suite": "pcie", "h2d_gbps": rates["h2d"], "d2h_gbps": rates["d2h"],
+                      "bytes": 64 << 20, "memory": "pinned host"}), flush=True)
+    dev = {}
+    for m, k, n, op, reps in [(256, 128, 256, 0, 200), (256, 128, 256, 1, 200), (256, 128, 256, 2, 200),
+                              (1024, 1024, 1024, 0, 20), (4096, 4096, 4096, 0, 5)]:
+        key = (m, k, n, op)
+        if key not in dev:
+            ta, tb = op == 2, op == 1
+            gm, gn, gk = (k, n, m) if op == 2 else (m, n, k)
+            dev[key] = bench_gemm(gm, gn, gk, ta, tb, steps=10, warmup=2)["ms"]
+        print(json.dumps(bench_host_gemm(m, k, n, op, reps, rates, dev[key])), flush=True)
 
 
 # ------------------------------------------------------------ bandwidth kernels

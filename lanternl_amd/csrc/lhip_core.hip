@@ -161,6 +161,7 @@ LHIP_API int lhip_shutdown(void)
         s.recording = false;
     }
     (void)hipStreamSynchronize(s.stream);
+    lhip::host_pool_shutdown();
     if (s.d_stage) (void)hipFree(s.d_stage);
     if (s.h_stage) (void)hipHostFree(s.h_stage);
     if (s.work) (void)hipFree(s.work);

@@ -2414,67 +2414,5 @@ LHIP_API int lhip_sgemm_batched_reduce(int transa, int transb, int m, int n, int
     return lhip::sgemm_run(transa, transb, m, n, k, alpha, A, lda, 0, B, ldb, 0, beta, C, ldc, 0, 1, o, st().stream);
 }
 
-LHIP_API int lhip_matmul_host(int op, const double* a, const double* b, double* c,
-                              int m, int k, int n, int acc)
-{
-    LHIP_REQUIRE_READY();
-    LHIP_REFUSE_RECORDING();
-    if (op < 0 || op > 2) return fail(LHIP_E_ARG, "lhip_matmul_host: op %d not in {0,1,2}", op);
-    if (m < 0 || k < 0 || n < 0) return fail(LHIP_E_SHAPE, "lhip_matmul_host: negative size");
-    // Result shape and operand sizes per op.
-    const long long rows = (op == 2) ? k : m;
-    const long long inner = (op == 2) ? m : k;
-    const long long na = static_cast<long long>(m) * k;
-    const long long nb = (op == 0) ? static_cast<long long>(k) * n
-                                   : (op == 1 ? static_cast<long long>(n) * k : static_cast<long long>(m) * n);
-    const long long nc = rows * n;
-    if (nc == 0) return LHIP_OK;
-    if (!c) return fail(LHIP_E_NULL, "lhip_matmul_host: c is NULL");
-    if (inner == 0) {
-        if (!acc) for (long long i = 0; i < nc; ++i) c[i] = 0.0;
-        return LHIP_OK;
-    }
-    if (!a || !b) return fail(LHIP_E_NULL, "lhip_matmul_host: a or b is NULL");
-    auto& s = st();
-    // Staging: [A | B | C] in fp32, each section padded to 64 floats so every
-    // operand starts 256-byte aligned.
-    auto pad = [](long long x) { return (x + 63) / 64 * 64; };
-    const size_t need = static_cast<size_t>(pad(na) + pad(nb) + pad(nc));
-    if (need > s.d_stage_floats) {
-        if (s.d_stage) { hipStreamSynchronize(s.stream); hipFree(s.d_stage); s.d_stage = nullptr; s.d_stage_floats = 0; }
-        LHIP_CHECK_HIP(hipMalloc(&s.d_stage, need * sizeof(float)), "lhip_matmul_host: device staging");
-        s.d_stage_floats = need;
-    }
-    if (need > s.h_stage_floats) {
-        if (s.h_stage) { hipStreamSynchronize(s.stream); hipHostFree(s.h_stage); s.h_stage = nullptr; s.h_stage_floats = 0; }
-        LHIP_CHECK_HIP(hipHostMalloc(&s.h_stage, need * sizeof(float), hipHostMallocDefault),
-                       "lhip_matmul_host: pinned staging");
-        s.h_stage_floats = need;
-    }
-    float* ha = s.h_stage;
-    float* hb = ha + pad(na);
-    float* hc = hb + pad(nb);
-    for (long long i = 0; i < na; ++i) ha[i] = static_cast<float>(a[i]);
-    for (long long i = 0; i < nb; ++i) hb[i] = static_cast<float>(b[i]);
-    float* da = s.d_stage;
-    float* db = da + pad(na);
-    float* dc = db + pad(nb);
-    LHIP_CHECK_HIP(hipMemcpyAsync(da, ha, (pad(na) + nb) * sizeof(float), hipMemcpyHostToDevice, s.stream),
-                   "lhip_matmul_host: upload");
-    int rc;
-    if (op == 0)       // c(m x n) = a(m x k) b(k x n)
-        rc = lhip::sgemm_launch(0, 0, m, n, k, 1.f, da, k, db, n, 0.f, dc, n, 1, 0, 0, 0, s.stream);
-    else if (op == 1)  // c(m x n) = a(m x k) b(n x k)^T
-        rc = lhip::sgemm_launch(0, 1, m, n, k, 1.f, da, k, db, k, 0.f, dc, n, 1, 0, 0, 0, s.stream);
-    else               // c(k x n) = a(m x k)^T b(m x n)
-        rc = lhip::sgemm_launch(1, 0, k, n, m, 1.f, da, k, db, n, 0.f, dc, n, 1, 0, 0, 0, s.stream);
-    if (rc != LHIP_OK) return rc;
-    LHIP_CHECK_HIP(hipMemcpyAsync(hc, dc, nc * sizeof(float), hipMemcpyDeviceToHost, s.stream),
-                   "lhip_matmul_host: download");
-    LHIP_CHECK_HIP(hipStreamSynchronize(s.stream), "lhip_matmul_host: sync");
-    if (acc) for (long long i = 0; i < nc; ++i) c[i] += static_cast<double>(hc[i]);
-    else     for (long long i = 0; i < nc; ++i) c[i] = static_cast<double>(hc[i]);
-    return LHIP_OK;
-}
 
 }  // extern "C"

@@ -1,0 +1,345 @@
+// lhip_host.hip -- the host-table GEMM of the flat-table backend contract
+// (lhip_matmul_host): host double arrays in and out, fp32 on the GPU.
+//
+// Replaces the reference adapter's flat-table matmul (ai/gpu/luatl_adapter.lua:
+// 103-135: as_tensor rounds each Lua double to fp32 into a device tensor, the
+// GEMM runs, the result is read back and widened).  Here the fp64 <-> fp32
+// conversions run on a pool of host threads straight into / out of pinned
+// staging, in chunks: each chunk's upload (or download) is queued on the
+// library stream as soon as it is converted (or waited for just before it is
+// widened), so conversion overlaps the PCIe copies and the GEMM.  Small calls
+// (the C1 shapes) skip the pool: one vectorised pass per operand, one upload,
+// one download.
+#include <atomic>
+#include <condition_variable>
+#include <functional>
+#include <mutex>
+#include <thread>
+
+#include "lhip_internal.h"
+
+namespace lhip {
+namespace {
+
+// ---------------------------------------------------------------- conversions
+// The same loops compiled twice: for AVX2 hosts (4 doubles per conversion
+// instruction) and for the x86-64 baseline; the AVX2 form is chosen at run time.
+__attribute__((target("avx2"))) void f64_to_f32_avx2(const double* __restrict__ s, float* __restrict__ d,
+                                                     long long n)
+{
+    for (long long i = 0; i < n; ++i) d[i] = static_cast<float>(s[i]);
+}
+void f64_to_f32_base(const double* __restrict__ s, float* __restrict__ d, long long n)
+{
+    for (long long i = 0; i < n; ++i) d[i] = static_cast<float>(s[i]);
+}
+__attribute__((target("avx2"))) void f32_to_f64_avx2(const float* __restrict__ s, double* __restrict__ d,
+                                                     long long n, int acc)
+{
+    if (acc) for (long long i = 0; i < n; ++i) d[i] += static_cast<double>(s[i]);
+    else for (long long i = 0; i < n; ++i) d[i] = static_cast<double>(s[i]);
+}
+void f32_to_f64_base(const float* __restrict__ s, double* __restrict__ d, long long n, int acc)
+{
+    if (acc) for (long long i = 0; i < n; ++i) d[i] += static_cast<double>(s[i]);
+    else for (long long i = 0; i < n; ++i) d[i] = static_cast<double>(s[i]);
+}
+
+bool host_avx2()
+{
+    static const bool v = __builtin_cpu_supports("avx2");
+    return v;
+}
+
+void narrow(const double* s, float* d, long long n)
+{
+    if (host_avx2()) f64_to_f32_avx2(s, d, n);
+    else f64_to_f32_base(s, d, n);
+}
+
+void widen(const float* s, double* d, long long n, int acc)
+{
+    if (host_avx2()) f32_to_f64_avx2(s, d, n, acc);
+    else f32_to_f64_base(s, d, n, acc);
+}
+
+// ---------------------------------------------------------------- thread pool
+// Workers sleep on a condition variable.  run(parts, fn) publishes fn under a
+// new generation number, hands out part indices 0..parts-1 through an atomic
+// counter (the calling thread takes parts too) and returns once every worker
+// has finished with that generation, so no worker can still hold fn (or touch
+// the counter) when run returns.  Started on the first large call, joined by
+// lhip_shutdown.
+class HostPool {
+public:
+    ~HostPool() { stop(); }
+
+    int threads() const { return static_cast<int>(workers_.size()) + 1; }
+
+    void start()
+    {
+        if (!workers_.empty()) return;
+        unsigned hw = std::thread::hardware_concurrency();
+        int n = static_cast<int>(hw > 0 ? hw : 4);
+        if (n > kMaxThreads) n = kMaxThreads;
+        unsigned long long g0;
+        {
+            std::lock_guard<std::mutex> g(mu_);
+            quit_ = false;
+            g0 = gen_;   // a new worker waits for the next generation
+        }
+        for (int i = 1; i < n; ++i) workers_.emplace_back([this, g0] { loop(g0); });
+    }
+
+    void stop()
+    {
+        {
+            std::lock_guard<std::mutex> g(mu_);
+            quit_ = true;
+            ++gen_;
+        }
+        cv_.notify_all();
+        for (auto& t : workers_) t.join();
+        workers_.clear();
+    }
+
+    void run(int parts, const std::function<void(int)>& fn)
+    {
+        if (workers_.empty() || parts <= 1) {
+            for (int p = 0; p < parts; ++p) fn(p);
+            return;
+        }
+        {
+            std::lock_guard<std::mutex> g(mu_);
+            fn_ = &fn;
+            parts_ = parts;
+            next_.store(0);
+            finished_ = 0;
+            ++gen_;
+        }
+        cv_.notify_all();
+        work(&fn, parts);
+        std::unique_lock<std::mutex> g(mu_);
+        done_cv_.wait(g, [&] { return finished_ == static_cast<int>(workers_.size()); });
+        fn_ = nullptr;
+    }
+
+private:
+    static constexpr int kMaxThreads = 16;
+
+    void work(const std::function<void(int)>* fn, int parts)
+    {
+        for (int p; (p = next_.fetch_add(1)) < parts;) (*fn)(p);
+    }
+
+    void loop(unsigned long long seen)
+    {
+        while (true) {
+            const std::function<void(int)>* fn;
+            int parts;
+            {
+                std::unique_lock<std::mutex> g(mu_);
+                cv_.wait(g, [&] { return gen_ != seen; });
+                seen = gen_;
+                if (quit_) return;
+                fn = fn_;
+                parts = parts_;
+            }
+            if (!fn) continue;
+            work(fn, parts);
+            {
+                std::lock_guard<std::mutex> g(mu_);
+                ++finished_;
+            }
+            done_cv_.notify_one();
+        }
+    }
+
+    std::vector<std::thread> workers_;
+    std::mutex mu_;
+    std::condition_variable cv_, done_cv_;
+    const std::function<void(int)>* fn_ = nullptr;
+    int parts_ = 0, finished_ = 0;
+    std::atomic<int> next_{0};
+    unsigned long long gen_ = 0;
+    bool quit_ = false;
+};
+
+HostPool g_pool;
+
+// Copy n floats from pinned host memory into device memory with the GPU's own
+// loads (one float4 per thread): for a small call this costs a kernel launch
+// instead of a DMA transfer's ~11 us of fixed latency.
+__global__ void __launch_bounds__(256) stage_in_kernel(const float* __restrict__ src, float* __restrict__ dst,
+                                                       long long n)
+{
+    const long long i = (static_cast<long long>(blockIdx.x) * 256 + threadIdx.x) * 4;
+    if (i + 3 < n) {
+        *reinterpret_cast<float4*>(dst + i) = *reinterpret_cast<const float4*>(src + i);
+    } else {
+        for (long long j = i; j < n; ++j) dst[j] = src[j];
+    }
+}
+
+// Below this many elements in all three operands together a call converts on
+// the calling thread (waking the pool costs more than it saves).
+constexpr long long kPoolMin = 1LL << 20;
+// Elements per pipelined chunk (16 MiB of fp32).
+constexpr long long kChunk = 1LL << 22;
+
+// Convert [0, n) with the pool, in slices of at least 64 Ki elements.
+void par_narrow(const double* s, float* d, long long n)
+{
+    const int parts = static_cast<int>(std::min<long long>(g_pool.threads(), (n + 65535) / 65536));
+    const long long per = (n + parts - 1) / parts;
+    g_pool.run(parts, [&](int p) {
+        const long long b = p * per, e = std::min(n, b + per);
+        if (b < e) narrow(s + b, d + b, e - b);
+    });
+}
+
+void par_widen(const float* s, double* d, long long n, int acc)
+{
+    const int parts = static_cast<int>(std::min<long long>(g_pool.threads(), (n + 65535) / 65536));
+    const long long per = (n + parts - 1) / parts;
+    g_pool.run(parts, [&](int p) {
+        const long long b = p * per, e = std::min(n, b + per);
+        if (b < e) widen(s + b, d + b, e - b, acc);
+    });
+}
+
+}  // namespace
+
+void host_pool_shutdown() { g_pool.stop(); }
+
+}  // namespace lhip
+
+using lhip::fail;
+using lhip::st;
+
+extern "C" {
+
+LHIP_API int lhip_matmul_host(int op, const double* a, const double* b, double* c,
+                              int m, int k, int n, int acc)
+{
+    LHIP_REQUIRE_READY();
+    LHIP_REFUSE_RECORDING();
+    if (op < 0 || op > 2) return fail(LHIP_E_ARG, "lhip_matmul_host: op %d not in {0,1,2}", op);
+    if (m < 0 || k < 0 || n < 0) return fail(LHIP_E_SHAPE, "lhip_matmul_host: negative size");
+    // Result shape and operand sizes per op.
+    const long long rows = (op == 2) ? k : m;
+    const long long inner = (op == 2) ? m : k;
+    const long long na = static_cast<long long>(m) * k;
+    const long long nb = (op == 0) ? static_cast<long long>(k) * n
+                                   : (op == 1 ? static_cast<long long>(n) * k : static_cast<long long>(m) * n);
+    const long long nc = rows * n;
+    if (nc == 0) return LHIP_OK;
+    if (!c) return fail(LHIP_E_NULL, "lhip_matmul_host: c is NULL");
+    if (inner == 0) {
+        if (!acc) for (long long i = 0; i < nc; ++i) c[i] = 0.0;
+        return LHIP_OK;
+    }
+    if (!a || !b) return fail(LHIP_E_NULL, "lhip_matmul_host: a or b is NULL");
+    auto& s = st();
+    // Staging: [A | B | C] in fp32, each section padded to 64 floats so every
+    // operand starts 256-byte aligned.
+    auto pad = [](long long x) { return (x + 63) / 64 * 64; };
+    const size_t need = static_cast<size_t>(pad(na) + pad(nb) + pad(nc));
+    if (need > s.d_stage_floats) {
+        if (s.d_stage) {
+            LHIP_CHECK_HIP(hipStreamSynchronize(s.stream), "lhip_matmul_host: sync");
+            LHIP_CHECK_HIP(hipFree(s.d_stage), "lhip_matmul_host: free device staging");
+            s.d_stage = nullptr;
+            s.d_stage_floats = 0;
+        }
+        LHIP_CHECK_HIP(hipMalloc(&s.d_stage, need * sizeof(float)), "lhip_matmul_host: device staging");
+        s.d_stage_floats = need;
+    }
+    if (need > s.h_stage_floats) {
+        if (s.h_stage) {
+            LHIP_CHECK_HIP(hipStreamSynchronize(s.stream), "lhip_matmul_host: sync");
+            LHIP_CHECK_HIP(hipHostFree(s.h_stage), "lhip_matmul_host: free pinned staging");
+            s.h_stage = nullptr;
+            s.h_stage_floats = 0;
+        }
+        LHIP_CHECK_HIP(hipHostMalloc(&s.h_stage, need * sizeof(float), hipHostMallocDefault),
+                       "lhip_matmul_host: pinned staging");
+        s.h_stage_floats = need;
+    }
+    float* ha = s.h_stage;
+    float* hb = ha + pad(na);
+    float* hc = hb + pad(nb);
+    float* da = s.d_stage;
+    float* db = da + pad(na);
+    float* dc = db + pad(nb);
+    const bool pooled = na + nb + nc >= lhip::kPoolMin;
+    if (pooled) lhip::g_pool.start();
+
+    // upload: convert a chunk, queue its copy, convert the next meanwhile
+    auto upload = [&](const double* src, float* h, float* d, long long cnt) -> int {
+        if (!pooled) {
+            lhip::narrow(src, h, cnt);
+            return LHIP_OK;
+        }
+        for (long long off = 0; off < cnt; off += lhip::kChunk) {
+            const long long len = std::min(lhip::kChunk, cnt - off);
+            lhip::par_narrow(src + off, h + off, len);
+            LHIP_CHECK_HIP(hipMemcpyAsync(d + off, h + off, len * sizeof(float), hipMemcpyHostToDevice, s.stream),
+                           "lhip_matmul_host: upload");
+        }
+        return LHIP_OK;
+    };
+    if (int rc = upload(a, ha, da, na)) return rc;
+    if (int rc = upload(b, hb, db, nb)) return rc;
+    if (!pooled) {   // A and B (adjacent in the staging) in one kernel-side copy
+        const long long cnt = pad(na) + nb;
+        lhip::klaunch(lhip::stage_in_kernel, dim3(static_cast<unsigned>((cnt + 1023) / 1024)), dim3(256), 0, s.stream,
+                      ha, da, cnt);
+        if (int rc = lhip::check_launch("lhip_matmul_host: upload")) return rc;
+    }
+    // A small call's product is stored by the GEMM straight into the pinned
+    // staging (the GPU writes host memory over PCIe): no download copy, whose
+    // fixed cost (~11 us) is most of such a call.
+    float* cout = pooled ? dc : hc;
+    int rc;
+    if (op == 0)       // c(m x n) = a(m x k) b(k x n)
+        rc = lhip::sgemm_launch(0, 0, m, n, k, 1.f, da, k, db, n, 0.f, cout, n, 1, 0, 0, 0, s.stream);
+    else if (op == 1)  // c(m x n) = a(m x k) b(n x k)^T
+        rc = lhip::sgemm_launch(0, 1, m, n, k, 1.f, da, k, db, k, 0.f, cout, n, 1, 0, 0, 0, s.stream);
+    else               // c(k x n) = a(m x k)^T b(m x n)
+        rc = lhip::sgemm_launch(1, 0, k, n, m, 1.f, da, k, db, n, 0.f, cout, n, 1, 0, 0, 0, s.stream);
+    if (rc != LHIP_OK) return rc;
+    if (!pooled) {
+        LHIP_CHECK_HIP(hipStreamSynchronize(s.stream), "lhip_matmul_host: sync");
+        lhip::widen(hc, c, nc, acc);
+        return LHIP_OK;
+    }
+    // download: queue every chunk's copy with an event behind it, then widen
+    // each chunk as soon as its event has fired
+    const int nch = static_cast<int>((nc + lhip::kChunk - 1) / lhip::kChunk);
+    std::vector<hipEvent_t> ev(nch, nullptr);
+    int err = LHIP_OK;
+    for (int i = 0; i < nch && err == LHIP_OK; ++i) {
+        const long long off = i * lhip::kChunk, len = std::min(lhip::kChunk, nc - off);
+        hipError_t e = hipEventCreateWithFlags(&ev[i], hipEventDisableTiming);
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(hc + off, dc + off, len * sizeof(float), hipMemcpyDeviceToHost, s.stream);
+        if (e == hipSuccess) e = hipEventRecord(ev[i], s.stream);
+        if (e != hipSuccess) err = lhip::hip_fail(e, "lhip_matmul_host: download");
+    }
+    for (int i = 0; i < nch && err == LHIP_OK; ++i) {
+        const long long off = i * lhip::kChunk, len = std::min(lhip::kChunk, nc - off);
+        const hipError_t e = hipEventSynchronize(ev[i]);
+        if (e != hipSuccess) {
+            err = lhip::hip_fail(e, "lhip_matmul_host: download wait");
+            break;
+        }
+        lhip::par_widen(hc + off, c + off, len, acc);
+    }
+    if (err != LHIP_OK) (void)hipStreamSynchronize(s.stream);   // no copy may still target the staging
+    for (hipEvent_t e : ev)
+        if (e) (void)hipEventDestroy(e);
+    return err;
+}
+
+}  // extern "C"

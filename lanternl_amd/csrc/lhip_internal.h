@@ -145,6 +145,8 @@ __device__ __forceinline__ void xcd_tile(int pid, int nwg, int tiles_n, int& tm,
 // Resolves, once per device, the device address of the fixed scratch array of
 // lhip_sgemm_noalloc (called by lhip_init with the device current).
 int noalloc_scratch_init(int device);
+// Join the host conversion threads of lhip_matmul_host (lhip_shutdown).
+void host_pool_shutdown();
 
 // Library workspace of at least `bytes` (reused; growing it waits for the
 // stream, so while a program is being recorded a call that would grow it fails

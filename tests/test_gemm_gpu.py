@@ -274,6 +274,30 @@ def test_matmul_host_accumulate_in_double():
     assert rel_fro(out, expect) <= TOL
 
 
+@pytest.mark.parametrize("op,m,k,n,acc", [(0, 2048, 2304, 2048, 0), (1, 1500, 1024, 1300, 1), (2, 2100, 1000, 900, 0)])
+def test_matmul_host_threaded_chunks(op, m, k, n, acc):
+    """Calls large enough for the threaded, chunked host path (conversions on
+    the host pool, 16 MiB chunks: op 0 has two upload chunks per operand and
+    two download chunks) against float64 products of the fp32-rounded inputs."""
+    announce("matmul_host threaded", op, m, k, n, acc)
+    from lanternl_amd._lib import call
+    rng = np.random.default_rng(40 + op)
+    a = rng.uniform(-1, 1, (m, k))
+    b = rng.uniform(-1, 1, {0: (k, n), 1: (n, k), 2: (m, n)}[op])
+    a32, b32 = a.astype(np.float32).astype(np.float64), b.astype(np.float32).astype(np.float64)
+    ref = {0: lambda: a32 @ b32, 1: lambda: a32 @ b32.T, 2: lambda: a32.T @ b32}[op]()
+    c0 = rng.uniform(-1, 1, ref.shape)
+    out = c0.copy()
+    call("lhip_matmul_host", op, a.ctypes.data_as(ctypes.c_void_p), b.ctypes.data_as(ctypes.c_void_p),
+         out.ctypes.data_as(ctypes.c_void_p), m, k, n, acc)
+    assert rel_fro(out, ref + c0 if acc else ref) <= TOL
+    # a second call reuses the staging and the pool
+    out2 = np.zeros_like(ref)
+    call("lhip_matmul_host", op, a.ctypes.data_as(ctypes.c_void_p), b.ctypes.data_as(ctypes.c_void_p),
+         out2.ctypes.data_as(ctypes.c_void_p), m, k, n, 0)
+    assert rel_fro(out2, ref) <= TOL
+
+
 @pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1)])
 def test_gemm_c3_lm_head_shapes(ta, tb):
     """Config C3: logits = hidden(512x128) . W(128x32000); dW = hidden^T . dlogits;
