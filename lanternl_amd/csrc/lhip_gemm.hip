@@ -332,6 +332,149 @@ sgemm_mfma_kernel(const GemmArgs g)
         }
 }
 
+// sgemm_mfma_kernel with two wave sets per workgroup (KS = 2, 512 threads):
+// set s takes the K chunks s, s+2, ... with its own double-buffered LDS, so
+// each SIMD holds two waves and the chain of dependent chunk loads per set is
+// half as long; set 1's partial tiles are added to set 0's in LDS (fixed
+// order) before set 0 stores.  For long K on one 64x64 tile per CU (1024^3:
+// 35.7 -> 29.6 us).
+template <int BM, int BN, int BK, bool TA, bool TB, int KS>
+__global__ void __launch_bounds__(kThreads * KS)
+sgemm_mfma_ks_kernel(const GemmArgs g)
+{
+    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int FM = WM / 32, FN = WN / 32;
+    constexpr int LDA = TA ? BM + 4 : BM + 1;
+    constexpr int LDB = TB ? BN + 1 : BN + 4;
+    __shared__ float As[KS][2][BK * LDA];
+    __shared__ float Bs[KS][2][BK * LDB];
+    const int M = g.M, N = g.N;
+    const int tid = threadIdx.x;
+    const int grp = __builtin_amdgcn_readfirstlane(tid >> 8), gt = tid & 255;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((tid >> 6) & 3);
+    const int lr = lane & 31, lk = lane >> 5;
+    int tm, tn;
+    tile_coords(blockIdx.x, gridDim.x, g.tiles_m, g.tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const long long zo = blockIdx.y / g.inner, zi = blockIdx.y % g.inner;
+    const float* __restrict__ A = g.A + zo * g.sA2 + zi * g.sA;
+    const float* __restrict__ B = g.B + zo * g.sB2 + zi * g.sB;
+    const long long coff = zo * g.sC2 + zi * g.sC;
+    const int wm = (wave >> 1) * WM, wn = (wave & 1) * WN;
+    TileRegs<TA ? BK : BM, TA ? BM : BK> ra;
+    TileRegs<TB ? BN : BK, TB ? BK : BN> rb;
+    const int kbeg = blockIdx.z * g.kchunk;
+    const int kend = min(g.K, kbeg + g.kchunk);
+    auto gload = [&](int k0) {
+        if (TA) ra.load(A, g.lda, k0, m0, kend, M, g.vecA, gt);
+        else    ra.load(A, g.lda, m0, k0, M, kend, g.vecA, gt);
+        if (TB) rb.load(B, g.ldb, n0, k0, N, kend, g.vecB, gt);
+        else    rb.load(B, g.ldb, k0, n0, kend, N, g.vecB, gt);
+    };
+    auto lstore = [&](int buf) {
+        if (TA) ra.template store_direct<LDA>(As[grp][buf], gt);
+        else    ra.template store_transposed<LDA>(As[grp][buf], gt);
+        if (TB) rb.template store_transposed<LDB>(Bs[grp][buf], gt);
+        else    rb.template store_direct<LDB>(Bs[grp][buf], gt);
+    };
+    floatx16 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+    const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
+    const int iters = (nk + KS - 1) / KS;
+    if (grp < nk) gload(kbeg + grp * BK);
+    else { ra = decltype(ra){}; rb = decltype(rb){}; }
+    lstore(0);
+    __syncthreads();
+    for (int it = 0; it < iters; ++it) {
+        const int cur = it & 1;
+        const int kt = it * KS + grp;
+        const bool more = it + 1 < iters;
+        const bool next_in = kt + KS < nk;
+        if (more && next_in) gload(kbeg + (kt + KS) * BK);
+        if (kt < nk) {
+            const float* as = As[grp][cur];
+            const float* bs = Bs[grp][cur];
+#pragma unroll
+            for (int kk = 0; kk < BK; kk += 2) {
+                float a[FM], b[FN];
+#pragma unroll
+                for (int i = 0; i < FM; ++i) a[i] = as[(kk + lk) * LDA + wm + 32 * i + lr];
+#pragma unroll
+                for (int j = 0; j < FN; ++j) b[j] = bs[(kk + lk) * LDB + wn + 32 * j + lr];
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
+            }
+        }
+        if (more && next_in) lstore(cur ^ 1);
+        __syncthreads();
+    }
+    static_assert(KS == 2 && 4 * FM * FN * 1024 <= KS * 2 * BK * LDA, "reduction area");
+    float* red = &As[0][0][0];   // set 1's partial tiles, FM*FN*16*64 floats per wave
+    if (grp == 1) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) red[((wave * FM + i) * FN + j) * 1024 + r * 64 + lane] = acc[i][j][r];
+    }
+    __syncthreads();
+    if (grp == 1) return;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] += red[((wave * FM + i) * FN + j) * 1024 + r * 64 + lane];
+    // Accumulator layout of a 32x32 block: element r of lane l sits at
+    // row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+    if (g.splits > 1) {   // split-K partial of this slice, summed by splitk_reduce
+        float* wz = g.ws + (static_cast<long long>(blockIdx.z) * gridDim.y + blockIdx.y) *
+                               (static_cast<long long>(M) * N);
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                const int col = n0 + wn + 32 * j + lr;
+                if (col >= N) continue;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int row = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * lk + (r & 3);
+                    if (row < M) wz[static_cast<long long>(row) * N + col] = acc[i][j][r];
+                }
+            }
+        return;
+    }
+    float* __restrict__ C = g.C + coff;
+    const float* R = g.R ? g.R + coff : C;
+    const int ldr = g.R ? g.ldr : g.ldc;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int col = n0 + wn + 32 * j + lr;
+            if (col >= N) continue;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * lk + (r & 3);
+                if (row < M) {
+                    const float v = g.alpha * acc[i][j][r];
+                    C[static_cast<long long>(row) * g.ldc + col] =
+                        (g.beta != 0.f) ? v + g.beta * R[static_cast<long long>(row) * ldr + col] : v;
+                }
+            }
+        }
+}
+
 // ---------------------------------------------------------------------------
 // Large problems (at least one 256x256 tile per CU): 256x256 output tiles,
 // four waves of 128x128 (16 v_mfma_f32_32x32x2f32 accumulators each, 256
@@ -1524,6 +1667,24 @@ int launch_skinny(int ta, GemmArgs g, hipStream_t stream)
 }
 
 template <int BM, int BN, int BK>
+int launch_cfg_ks(int ta, int tb, GemmArgs g, int batch, hipStream_t stream)
+{
+    g.tiles_m = ceil_div(g.M, BM);
+    g.tiles_n = ceil_div(g.N, BN);
+    const long long nwg = static_cast<long long>(g.tiles_m) * g.tiles_n;
+    if (nwg > 0x7fffffffLL) return fail(LHIP_E_CAPACITY, "sgemm: %lld workgroups exceed the grid limit", nwg);
+    if (g.splits <= 1) { g.splits = 1; g.kchunk = g.K; g.ws = nullptr; }
+    dim3 grid(static_cast<unsigned>(nwg), batch, g.splits), block(2 * kThreads, 1, 1);
+    if (!ta && !tb) klaunch(sgemm_mfma_ks_kernel<BM, BN, BK, false, false, 2>, grid, block, 0, stream, g);
+    else if (ta && !tb) klaunch(sgemm_mfma_ks_kernel<BM, BN, BK, true, false, 2>, grid, block, 0, stream, g);
+    else if (!ta && tb) klaunch(sgemm_mfma_ks_kernel<BM, BN, BK, false, true, 2>, grid, block, 0, stream, g);
+    else klaunch(sgemm_mfma_ks_kernel<BM, BN, BK, true, true, 2>, grid, block, 0, stream, g);
+    int rc = check_launch("sgemm: kernel launch");
+    if (rc != LHIP_OK || g.splits <= 1 || g.skip_reduce) return rc;
+    return launch_reduce(g, batch, stream);
+}
+
+template <int BM, int BN, int BK>
 int launch_cfg(int ta, int tb, GemmArgs g, int batch, hipStream_t stream)
 {
     g.tiles_m = ceil_div(g.M, BM);
@@ -2241,7 +2402,11 @@ int sgemm_run(int ta, int tb, int m, int n, int k, float alpha,
     if (big_tiles >= cus) return launch_cfg<128, 128, 32>(ta, tb, g, batch, stream);
     // short K (e.g. the LM head, K = dim): the whole K range in one LDS tile,
     // so a workgroup waits on one load round trip instead of one per 32-deep chunk
-    if (tiles64 >= cus) return launch_cfg<64, 64, 32>(ta, tb, g, batch, stream);
+    if (tiles64 >= cus) {
+        // long K: two wave sets per 64x64 tile
+        if (g.K >= 512 && tiles64 <= 2 * cus) return launch_cfg_ks<64, 64, 64>(ta, tb, g, batch, stream);
+        return launch_cfg<64, 64, 32>(ta, tb, g, batch, stream);
+    }
     const bool small = use_small_kernel(m, n, g.K);
     g.splits = o.ws ? splitk_plan(m, n, g.K, batch, o.ws_floats, &g.kchunk, o.splits_out != nullptr) : 1;
     g.ws = o.ws;

@@ -52,6 +52,25 @@ def test_gemm_family_vs_oracle(m, k, n):
     assert rel_fro(_gemm(True, True, at, bt), ref) <= TOL
 
 
+@pytest.mark.parametrize("m,k,n", [(1024, 1024, 1024), (1000, 777, 1030)])
+def test_gemm_two_wave_set_tiles(m, k, n):
+    """Mid-size products with long K on one 64x64 tile per CU (the two-wave-set
+    kernel: odd and even K chunks on separate wave sets, K = 777 ragged with an
+    odd chunk count), all four transposition variants, and alpha / beta."""
+    announce("gemm two wave sets", m, k, n)
+    rng = np.random.default_rng(m + k + n)
+    a = f32(rng.uniform(-1, 1, (m, k)))
+    b = f32(rng.uniform(-1, 1, (k, n)))
+    ref = a.astype(np.float64) @ b.astype(np.float64)
+    at, bt = np.ascontiguousarray(a.T), np.ascontiguousarray(b.T)
+    for ta, tb in ((0, 0), (1, 0), (0, 1), (1, 1)):
+        got = _gemm(bool(ta), bool(tb), at if ta else a, bt if tb else b)
+        assert rel_fro(got, ref) <= TOL, (ta, tb)
+    c0 = f32(rng.uniform(-1, 1, (m, n)))
+    got = _gemm(False, False, a, b, alpha=0.5, beta=-2.0, c0=c0)
+    assert rel_fro(got, 0.5 * ref - 2.0 * c0.astype(np.float64)) <= TOL
+
+
 def test_gemm_c1_all_variants_bitwise_stable():
     """Config C1: A 256x128, B 128x256; the three products agree with the oracle
     and with each other (A.B = (A^T)^T.B = A.(B^T)^T) to fp32 rounding."""
