@@ -1975,8 +1975,10 @@ __global__ void __launch_bounds__(256 * KS) sgemm_grouped_tn_lds64_kernel(const 
     // chunk loader of a set: thread t covers chunk rows t/16 + 16p (p < 4), float4 column (t%16)*4
     const int lrow = gt >> 4, lc4 = (gt & 15) * 4;
     const bool am_ok = m0 + lc4 < e.M, bn_ok = n0 + lc4 < e.N;   // M, N % 4 == 0 (host check)
-    float4 ra[P], rb[P];
-    auto gload = [&](int k0) {
+    // two register sets: a set's next-but-one chunk is in flight while the
+    // current chunk's MFMAs run and the next chunk goes to LDS
+    float4 ra0[P], rb0[P], ra1[P], rb1[P];
+    auto gload = [&](int k0, float4 (&ra)[P], float4 (&rb)[P]) {
 #pragma unroll
         for (int p = 0; p < P; ++p) {
             const int k = k0 + lrow + 16 * p;
@@ -1987,7 +1989,7 @@ __global__ void __launch_bounds__(256 * KS) sgemm_grouped_tn_lds64_kernel(const 
                                    : make_float4(0.f, 0.f, 0.f, 0.f);
         }
     };
-    auto lstore = [&](int buf) {
+    auto lstore = [&](int buf, const float4 (&ra)[P], const float4 (&rb)[P]) {
 #pragma unroll
         for (int p = 0; p < P; ++p) {
             *reinterpret_cast<float4*>(&As[grp][buf][lrow + 16 * p][lc4]) = ra[p];
@@ -2043,7 +2045,8 @@ __global__ void __launch_bounds__(256 * KS) sgemm_grouped_tn_lds64_kernel(const 
     const float scl = e.sc_scale;
     const int nk = (K + BK - 1) / BK;
     const int iters = (nk + KS - 1) / KS;   // every set passes the same barriers
-    gload(grp * BK);
+    gload(grp * BK, ra0, rb0);
+    if (iters > 1) gload((grp + KS) * BK, ra1, rb1);
     float sv[SC];             // rows of the first SC matches, fetched during the products
     unsigned srel[SC / 4];    // their rows within the wave's 32, 8 bits each (0xff: none)
     int first_total = 0;
@@ -2070,22 +2073,30 @@ __global__ void __launch_bounds__(256 * KS) sgemm_grouped_tn_lds64_kernel(const 
         }
         __builtin_amdgcn_wave_barrier();   // the list is rewritten after the products
     }
-    lstore(0);
+    lstore(0, ra0, rb0);
     __syncthreads();
-    for (int it = 0; it < iters; ++it) {
-        const int cur = it & 1;
-        const int kt = it * KS + grp;
-        const bool more = it + 1 < iters;
-        if (more) gload((kt + KS) * BK);
+    auto chunk_mfma = [&](int buf, int kt) {
         if (kt < nk) {
 #pragma unroll
             for (int st = 0; st < BK / 2; ++st) {
                 const int kr = 2 * st + lk;   // lanes 0-31 read row k, 32-63 row k+1
-                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(As[grp][cur][kr][wm + lr], Bs[grp][cur][kr][wn + lr], acc,
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(As[grp][buf][kr][wm + lr], Bs[grp][buf][kr][wn + lr], acc,
                                                            0, 0, 0);
             }
         }
-        if (more) lstore(cur ^ 1);
+    };
+    // iteration it computes the set's chunk it*KS + grp from LDS buffer it%2,
+    // stores chunk it+1 (loaded an iteration earlier) into the other buffer
+    // and issues the loads of chunk it+2
+    for (int it = 0; it < iters; it += 2) {
+        if (it + 2 < iters) gload(((it + 2) * KS + grp) * BK, ra0, rb0);
+        chunk_mfma(0, it * KS + grp);
+        if (it + 1 < iters) lstore(1, ra1, rb1);
+        __syncthreads();
+        if (it + 1 >= iters) break;
+        if (it + 3 < iters) gload(((it + 3) * KS + grp) * BK, ra1, rb1);
+        chunk_mfma(1, (it + 1) * KS + grp);
+        if (it + 2 < iters) lstore(0, ra0, rb0);
         __syncthreads();
     }
     if (KS == 2) {   // set 1's partial quadrants added to set 0's
