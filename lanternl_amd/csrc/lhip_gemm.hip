@@ -332,12 +332,12 @@ sgemm_mfma_kernel(const GemmArgs g)
         }
 }
 
-// sgemm_mfma_kernel with two wave sets per workgroup (KS = 2, 512 threads):
-// set s takes the K chunks s, s+2, ... with its own double-buffered LDS, so
-// each SIMD holds two waves and the chain of dependent chunk loads per set is
-// half as long; set 1's partial tiles are added to set 0's in LDS (fixed
-// order) before set 0 stores.  For long K on one 64x64 tile per CU (1024^3:
-// 35.7 -> 29.6 us).
+// sgemm_mfma_kernel with KS wave sets per workgroup (KS * 256 threads): set
+// s takes the K chunks s, s+KS, ... with its own double-buffered LDS, so each
+// SIMD holds KS waves and each set's chain of dependent chunk loads is KS
+// times shorter; the sets' partial tiles meet in LDS (fixed order).  For long
+// K on one or two 64x64 tiles per CU (1024^3: 35.7 us on one wave set, 28.2
+// on four).
 template <int BM, int BN, int BK, bool TA, bool TB, int KS>
 __global__ void __launch_bounds__(kThreads * KS)
 sgemm_mfma_ks_kernel(const GemmArgs g)
@@ -417,24 +417,29 @@ sgemm_mfma_ks_kernel(const GemmArgs g)
         if (more && next_in) lstore(cur ^ 1);
         __syncthreads();
     }
-    static_assert(KS == 2 && 4 * FM * FN * 1024 <= KS * 2 * BK * LDA, "reduction area");
-    float* red = &As[0][0][0];   // set 1's partial tiles, FM*FN*16*64 floats per wave
-    if (grp == 1) {
+    constexpr int SZ = 4 * FM * FN * 1024;   // one set's partial tiles (floats)
+    static_assert(KS >= 2 && (KS - 1) * SZ <= KS * 2 * BK * LDA, "reduction area");
+    float* red = &As[0][0][0];   // sets 1..KS-1 leave their partial tiles here
+    if (grp > 0) {
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
             for (int j = 0; j < FN; ++j)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) red[((wave * FM + i) * FN + j) * 1024 + r * 64 + lane] = acc[i][j][r];
+                for (int r = 0; r < 16; ++r)
+                    red[(grp - 1) * SZ + ((wave * FM + i) * FN + j) * 1024 + r * 64 + lane] = acc[i][j][r];
     }
     __syncthreads();
-    if (grp == 1) return;
+    if (grp > 0) return;
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+    for (int t = 1; t < KS; ++t)   // in set order
 #pragma unroll
-        for (int j = 0; j < FN; ++j)
+        for (int i = 0; i < FM; ++i)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] += red[((wave * FM + i) * FN + j) * 1024 + r * 64 + lane];
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    acc[i][j][r] += red[(t - 1) * SZ + ((wave * FM + i) * FN + j) * 1024 + r * 64 + lane];
     // Accumulator layout of a 32x32 block: element r of lane l sits at
     // row 8*(r/4) + 4*(l/32) + r%4, column l%32.
     if (g.splits > 1) {   // split-K partial of this slice, summed by splitk_reduce
@@ -1599,6 +1604,30 @@ bool skinny_ok(int ta, int tb, int m, int n, int batch, int kblocks)
     return !tb && m >= 1 && m <= kSkinnyMax && n >= kSkinnyCols && batch == 1 && kblocks == 1;
 }
 
+// 33..64 rows with long K and wide N: one 64-row tile band of 64x64 tiles on
+// four wave sets, split over K so that tiles x slices fill the CUs (M = 64,
+// K = N = 4096: 64 tiles x 4 slices, 31.8 us against 45 us on the skinny MFMA
+// form and its reduce).
+bool ks_split_ok(int m, int n, int k, int batch)
+{
+    return batch == 1 && m > 32 && m <= 64 && n >= 1024 && k >= 2048;
+}
+
+int ks_split_plan(int m, int n, int k, size_t ws_floats, int* kchunk_out)
+{
+    const int cus = st().cu_count > 0 ? st().cu_count : 256;
+    const long long tiles = ceil_div(n, 64);
+    long long s = std::max<long long>(1, cus / tiles);
+    s = std::min<long long>(s, k / 512);
+    s = std::min<long long>(s, 16);
+    const long long mn = static_cast<long long>(m) * n;
+    s = std::min<long long>(s, static_cast<long long>(ws_floats / mn));
+    if (s < 2) return 1;
+    const int kchunk = ceil_div(ceil_div(k, static_cast<int>(s)), 32) * 32;
+    *kchunk_out = kchunk;
+    return ceil_div(k, kchunk);
+}
+
 // Rows of C up to which the VALU form is used; 3..64 rows take the MFMA form.
 constexpr int kSkinnyValuMax = 2;
 
@@ -1666,7 +1695,7 @@ int launch_skinny(int ta, GemmArgs g, hipStream_t stream)
     return launch_reduce(g, 1, stream);
 }
 
-template <int BM, int BN, int BK>
+template <int BM, int BN, int BK, int KS>
 int launch_cfg_ks(int ta, int tb, GemmArgs g, int batch, hipStream_t stream)
 {
     g.tiles_m = ceil_div(g.M, BM);
@@ -1674,11 +1703,11 @@ int launch_cfg_ks(int ta, int tb, GemmArgs g, int batch, hipStream_t stream)
     const long long nwg = static_cast<long long>(g.tiles_m) * g.tiles_n;
     if (nwg > 0x7fffffffLL) return fail(LHIP_E_CAPACITY, "sgemm: %lld workgroups exceed the grid limit", nwg);
     if (g.splits <= 1) { g.splits = 1; g.kchunk = g.K; g.ws = nullptr; }
-    dim3 grid(static_cast<unsigned>(nwg), batch, g.splits), block(2 * kThreads, 1, 1);
-    if (!ta && !tb) klaunch(sgemm_mfma_ks_kernel<BM, BN, BK, false, false, 2>, grid, block, 0, stream, g);
-    else if (ta && !tb) klaunch(sgemm_mfma_ks_kernel<BM, BN, BK, true, false, 2>, grid, block, 0, stream, g);
-    else if (!ta && tb) klaunch(sgemm_mfma_ks_kernel<BM, BN, BK, false, true, 2>, grid, block, 0, stream, g);
-    else klaunch(sgemm_mfma_ks_kernel<BM, BN, BK, true, true, 2>, grid, block, 0, stream, g);
+    dim3 grid(static_cast<unsigned>(nwg), batch, g.splits), block(KS * kThreads, 1, 1);
+    if (!ta && !tb) klaunch(sgemm_mfma_ks_kernel<BM, BN, BK, false, false, KS>, grid, block, 0, stream, g);
+    else if (ta && !tb) klaunch(sgemm_mfma_ks_kernel<BM, BN, BK, true, false, KS>, grid, block, 0, stream, g);
+    else if (!ta && tb) klaunch(sgemm_mfma_ks_kernel<BM, BN, BK, false, true, KS>, grid, block, 0, stream, g);
+    else klaunch(sgemm_mfma_ks_kernel<BM, BN, BK, true, true, KS>, grid, block, 0, stream, g);
     int rc = check_launch("sgemm: kernel launch");
     if (rc != LHIP_OK || g.splits <= 1 || g.skip_reduce) return rc;
     return launch_reduce(g, batch, stream);
@@ -2395,6 +2424,14 @@ int sgemm_run(int ta, int tb, int m, int n, int k, float alpha,
     // small (fewer 64x64 tiles than CUs): 32x32 tiles with K shared by the
     // four waves of a workgroup, split over workgroups when K is very long
     // (split-K partials in o.ws).
+    if (!br && !o.splits_out && o.ws && ks_split_ok(m, n, k, batch)) {
+        int kc = 0;
+        const int s = ks_split_plan(m, n, k, o.ws_floats, &kc);
+        if (s > 1) {
+            g.splits = s; g.kchunk = kc; g.ws = o.ws;
+            return launch_cfg_ks<64, 64, 32, 4>(ta, tb, g, batch, stream);
+        }
+    }
     if (skinny_ok(ta, tb, m, n, batch, br ? o.kblocks : 1) && !o.splits_out && k > 0) {
         g.ws = o.ws;
         g.ws_floats_avail = o.ws ? o.ws_floats : 0;
@@ -2414,8 +2451,9 @@ int sgemm_run(int ta, int tb, int m, int n, int k, float alpha,
     // short K (e.g. the LM head, K = dim): the whole K range in one LDS tile,
     // so a workgroup waits on one load round trip instead of one per 32-deep chunk
     if (tiles64 >= cus) {
-        // long K: two wave sets per 64x64 tile
-        if (g.K >= 512 && tiles64 <= 2 * cus) return launch_cfg_ks<64, 64, 64>(ta, tb, g, batch, stream);
+        // long K at one or two 64x64 tiles per CU: four or two wave sets per tile
+        if (g.K >= 512 && tiles64 <= cus) return launch_cfg_ks<64, 64, 32, 4>(ta, tb, g, batch, stream);
+        if (g.K >= 512 && tiles64 <= 2 * cus) return launch_cfg_ks<64, 64, 32, 2>(ta, tb, g, batch, stream);
         return launch_cfg<64, 64, 32>(ta, tb, g, batch, stream);
     }
     const bool small = use_small_kernel(m, n, g.K);
@@ -2490,7 +2528,10 @@ int immediate_plan(int transa, int transb, int m, int n, int k, int batch, size_
     if (m <= 0 || n <= 0 || k <= 0 || batch <= 0) return 1;
     const size_t cap = static_cast<size_t>(1) << 26;
     int kchunk = 0, splits = 1;
-    if (skinny_ok(transa, transb, m, n, batch, 1)) {
+    if (ks_split_ok(m, n, k, batch)) {
+        splits = ks_split_plan(m, n, k, cap, &kchunk);
+        if (splits <= 1 && skinny_ok(transa, transb, m, n, batch, 1)) splits = skinny_plan(m, n, k, cap, &kchunk);
+    } else if (skinny_ok(transa, transb, m, n, batch, 1)) {
         splits = skinny_plan(m, n, k, cap, &kchunk);
     } else {
         splits = split256_plan(m, n, k, batch, cap, &kchunk);

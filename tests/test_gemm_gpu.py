@@ -52,11 +52,28 @@ def test_gemm_family_vs_oracle(m, k, n):
     assert rel_fro(_gemm(True, True, at, bt), ref) <= TOL
 
 
-@pytest.mark.parametrize("m,k,n", [(1024, 1024, 1024), (1000, 777, 1030)])
+@pytest.mark.parametrize("m,k,n", [(64, 4096, 4096), (40, 2500, 1100)])
+def test_gemm_split_band_on_four_wave_sets(m, k, n):
+    """33..64 rows with long K: one band of 64x64 tiles on four wave sets,
+    split over K (slices summed in order by the reduce), all four
+    transposition variants, ragged M, N and K."""
+    announce("gemm split band", m, k, n)
+    rng = np.random.default_rng(m * 3 + k + n)
+    a = f32(rng.uniform(-1, 1, (m, k)))
+    b = f32(rng.uniform(-1, 1, (k, n)))
+    ref = a.astype(np.float64) @ b.astype(np.float64)
+    at, bt = np.ascontiguousarray(a.T), np.ascontiguousarray(b.T)
+    for ta, tb in ((0, 0), (1, 0), (0, 1), (1, 1)):
+        got = _gemm(bool(ta), bool(tb), at if ta else a, bt if tb else b)
+        assert rel_fro(got, ref) <= TOL, (ta, tb)
+
+
+@pytest.mark.parametrize("m,k,n", [(1024, 1024, 1024), (1000, 777, 1030), (2048, 1024, 1024)])
 def test_gemm_two_wave_set_tiles(m, k, n):
-    """Mid-size products with long K on one 64x64 tile per CU (the two-wave-set
-    kernel: odd and even K chunks on separate wave sets, K = 777 ragged with an
-    odd chunk count), all four transposition variants, and alpha / beta."""
+    """Mid-size products with long K on one or two 64x64 tiles per CU (four or
+    two wave sets taking every fourth or second K chunk; K = 777 ragged with a
+    chunk count that is not a multiple of the set count), all four
+    transposition variants, and alpha / beta."""
     announce("gemm two wave sets", m, k, n)
     rng = np.random.default_rng(m + k + n)
     a = f32(rng.uniform(-1, 1, (m, k)))

@@ -45,6 +45,7 @@ def _run(name, ta, tb, m, n, k, A, B, C, alpha=1.0, beta=0.0):
 SEQUENCE = [
     (2048, 2048, 2048, 0, 0),   # 256x256 tiles, 4 K slices: 64 MiB of partials
     (256, 256, 8192, 1, 0),     # 64x64 tiles, 32 K slices (Aᵀ.B)
+    (64, 4096, 4096, 0, 0),     # one band of 64x64 tiles on four wave sets, 4 K slices
     (16, 4096, 4096, 0, 0),     # skinny rows, K slices
     (96, 80, 3000, 0, 1),       # A.Bᵀ, ragged edges
     (64, 64, 64, 0, 0),         # unsplit
