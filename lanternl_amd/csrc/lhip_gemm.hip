@@ -2311,6 +2311,9 @@ int split256_plan(int m, int n, int k, int batch, size_t ws_floats, int* kchunk_
     return splits;
 }
 
+// K per split slice from which a split 64x64-tile product runs on four wave sets.
+constexpr int kKsSliceMin = 1024;
+
 int splitk_plan(int m, int n, int k, int batch, size_t ws_floats, int* kchunk_out, bool unreduced)
 {
     const int cus = st().cu_count > 0 ? st().cu_count : 256;
@@ -2350,6 +2353,21 @@ int splitk_plan(int m, int n, int k, int batch, size_t ws_floats, int* kchunk_ou
         tiles = tiles64;
         unit = 32;
         min_k = 128;
+        // slices of 1024 or more K at one workgroup per CU run on four wave
+        // sets (ks_slices), which beats two single-set workgroups per CU
+        const long long s1 = (cus + tiles - 1) / tiles;
+        if (k / s1 >= kKsSliceMin) {
+            long long s = std::min<long long>(s1, 64);
+            if (mnb > 0) s = std::min<long long>(s, static_cast<long long>(ws_floats / mnb));
+            if (s >= 2) {
+                const int kchunk = ceil_div(ceil_div(k, s), 32) * 32;
+                const int splits = ceil_div(k, kchunk);
+                if (splits >= 2) {
+                    *kchunk_out = kchunk;
+                    return splits;
+                }
+            }
+        }
     }
     long long s = (2LL * cus + tiles - 1) / tiles;          // aim at ~2 workgroups per CU
     s = std::min<long long>(s, k / min_k);
@@ -2468,6 +2486,7 @@ int sgemm_run(int ta, int tb, int m, int n, int k, float alpha,
     const long long tiles32 = static_cast<long long>(ceil_div(m, 32)) * ceil_div(n, 32) * batch;
     if (small && tiles32 < cus) return launch_tiny(ta, tb, g, batch, stream);
     if (small) return launch_small(ta, tb, g, batch, stream);
+    if (g.splits > 1 && g.kchunk >= kKsSliceMin) return launch_cfg_ks<64, 64, 32, 4>(ta, tb, g, batch, stream);
     return launch_cfg<64, 64, 32>(ta, tb, g, batch, stream);
 }
 

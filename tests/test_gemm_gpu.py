@@ -52,10 +52,11 @@ def test_gemm_family_vs_oracle(m, k, n):
     assert rel_fro(_gemm(True, True, at, bt), ref) <= TOL
 
 
-@pytest.mark.parametrize("m,k,n", [(64, 4096, 4096), (40, 2500, 1100)])
+@pytest.mark.parametrize("m,k,n", [(64, 4096, 4096), (40, 2500, 1100), (300, 20000, 200)])
 def test_gemm_split_band_on_four_wave_sets(m, k, n):
-    """33..64 rows with long K: one band of 64x64 tiles on four wave sets,
-    split over K (slices summed in order by the reduce), all four
+    """Few 64x64 tiles with long K, split over K into slices of 1024 or more
+    on four wave sets (33..64 rows: one tile band; 300 x 200 x 20000: 20
+    tiles in 13 slices), slices summed in order by the reduce, all four
     transposition variants, ragged M, N and K."""
     announce("gemm split band", m, k, n)
     rng = np.random.default_rng(m * 3 + k + n)
