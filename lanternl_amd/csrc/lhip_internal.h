@@ -244,6 +244,9 @@ struct FuseCall {
     const float* nbx = nullptr; const float* nbres = nullptr; const float* nbinv = nullptr;
     float* nbout = nullptr; float* nbpart = nullptr;
     int a_parts = 1; long long a_pstride = 0;   // A = sum of a_parts slices a_pstride apart (in order)
+    // A row r = A row gather[r] (an embedding lookup; gather_rows rows in A),
+    // and with FB_NORM the gathered rows are also written to xout (ld K)
+    const int* gather = nullptr; int gather_rows = 0; float* xout = nullptr;
 };
 bool lm_fuse_ok(int K, int lda, int ldb_nt);
 int lm_fused_gemm(const FuseCall& c, hipStream_t s);

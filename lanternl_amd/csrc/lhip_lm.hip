@@ -214,7 +214,8 @@ int enqueue_step(LmModel& m, hipStream_t s, const Hyper& hp, bool device_hyper)
     // the backward overwrites it (beta = 0 GEMMs, accumulate = 0 column sums)
 
     // ---------------- forward (transformer.lua:228-257) ----------------
-    LM_TRY(embed_fwd(emb, m.ids, m.x, N, D, V, s));
+    // x_0 = emb[ids]: with fused GEMMs, gathered by layer 0's norm + q/k/v GEMM
+    if (!m.fused_gemm) LM_TRY(embed_fwd(emb, m.ids, m.x, N, D, V, s));
     for (int l = 0; l < L; ++l) {
         const float* xl = m.x + l * ND;
         float* h = m.h + l * ND;
@@ -233,6 +234,7 @@ int enqueue_step(LmModel& m, hipStream_t s, const Hyper& hp, bool device_hyper)
             FuseCall c;
             c.mode = FUSE_NORM; c.M = N; c.N = D; c.K = D; c.batch = 3;
             c.A = xl; c.lda = D; c.B = m.prm(m.lt(l, P_WQ)); c.ldb = D; c.sB = static_cast<long long>(D) * D;
+            if (l == 0) { c.A = emb; c.gather = m.ids; c.gather_rows = V; c.xout = m.x; }
             c.C = qkv; c.ldc = D; c.sC = ND;
             c.nw = m.prm(m.lt(l, P_LN1)); c.eps = eps; c.h = h; c.inv = inv1;
             LM_TRY(lm_fused_gemm(c, s));

@@ -7,6 +7,10 @@
 //   FUSE_SWIGLU_BWD   G = X . B^T, then dZ, dU = the SwiGLU backward of
 //                     (Z, U) with upstream G               (f = a . w2 backward)
 //
+// With a gather table the A rows are embedding rows (A row r = table row
+// ids[r], transformer.lua:228-231 with Tensor.embed), and the writer also
+// stores them (x_0, the residual stream's start).
+//
 // RMSNorm (ai/core/tensor2.lua:609-634): out(r, k) = x(r, k) * inv(r) * w(k),
 // inv(r) = 1 / sqrt(sum_k x(r, k)^2 / K + eps).  inv(r) does not depend on k,
 // so it factors out of the product: C(r, n) = inv(r) * sum_k (x(r, k) w(k))
@@ -46,6 +50,7 @@ struct FuseArgs {
     const float* Z; const float* U; float* dZ; float* dU; // SwiGLU backward epilogue (ld ldc)
     const float* nbx; const float* nbres; const float* nbinv; float* nbout; float* nbpart;  // norm-backward prologue
     int a_parts; long long a_pstride;   // A = sum of a_parts slices (split-K partials), summed in order
+    const int* gather; int gather_rows; float* xout;   // gathered A rows (embedding), written to xout
 };
 
 __device__ __forceinline__ float sigmoid_sign(float v)
@@ -86,6 +91,9 @@ __global__ void __launch_bounds__(256) lm_fused_gemm_kernel(const FuseArgs f)
     // addresses): they reach only outputs that are not stored, and their row
     // statistics are masked below (inv, coef and r are 0 for them).
     const int rowc = rok ? row : 0, colc = cok ? col : 0;
+    // the A row this lane loads: its own, or the table row its id names
+    // (clamped into the table; ids are validated before the step)
+    const int arow = f.gather ? min(max(f.gather[rowc], 0), f.gather_rows - 1) : rowc;
     const bool writer = y == 0 && tn == 0;   // writes the row-stage outputs (h/inv or dx/dw partials)
 
     // Every operand loads unconditionally: a lane past K (the last step, when
@@ -101,7 +109,7 @@ __global__ void __launch_bounds__(256) lm_fused_gemm_kernel(const FuseArgs f)
         const int k = ks + 4 * q;                   // K % 4 == 0: the four k are all in or all out
         const int kc = k < K ? k : ks;
         const long long ro = static_cast<long long>(rowc) * f.lda + kc;
-        to4(a[u], ld4(f.A + ro));
+        to4(a[u], ld4(f.A + static_cast<long long>(arow) * f.lda + kc));
         if constexpr (NORM || NB) to4(w[u], ld4(f.nw + kc));
         if constexpr (NB) {
             to4(x[u], ld4(f.nbx + ro));
@@ -236,10 +244,14 @@ __global__ void __launch_bounds__(256) lm_fused_gemm_kernel(const FuseArgs f)
             for (int u = 0; u < U; ++u) {
                 if (16 * wave + 64 * u >= K) break;
                 const int k = 16 * wave + 64 * u + 4 * q;
-                if (k < K)
+                if (k < K) {
                     *reinterpret_cast<float4*>(f.h + static_cast<long long>(row) * K + k) =
                         make_float4(a[u][0] * r * w[u][0], a[u][1] * r * w[u][1], a[u][2] * r * w[u][2],
                                     a[u][3] * r * w[u][3]);
+                    if (f.xout)
+                        *reinterpret_cast<float4*>(f.xout + static_cast<long long>(row) * K + k) =
+                            make_float4(a[u][0], a[u][1], a[u][2], a[u][3]);
+                }
             }
         }
     }
@@ -296,6 +308,9 @@ int lm_fused_gemm(const FuseCall& c, hipStream_t s)
     if ((mode & FB_SWIGLU_BWD) && (!c.Z || !c.U || !c.dZ || !c.dU))
         return fail(LHIP_E_ARG, "lm_fused_gemm: swiglu backward operands");
     if (!(mode & (FB_DUAL | FB_SWIGLU_BWD)) && !c.C) return fail(LHIP_E_NULL, "lm_fused_gemm: C is NULL");
+    if (c.gather && (!(mode & FB_NORM) || (mode & FB_NORMBWD) || c.gather_rows <= 0 || c.a_parts > 1 ||
+                     (c.xout && !aligned16(c.xout))))
+        return fail(LHIP_E_ARG, "lm_fused_gemm: gathered A rows need the norm prologue and a table");
     FuseArgs f{};
     f.M = c.M; f.N = c.N; f.K = c.K;
     f.A = c.A; f.lda = c.lda; f.B = c.B; f.ldb = c.ldb; f.sB = c.sB; f.C = c.C; f.ldc = c.ldc; f.sC = c.sC;
@@ -305,6 +320,7 @@ int lm_fused_gemm(const FuseCall& c, hipStream_t s)
     f.Z = c.Z; f.U = c.U; f.dZ = c.dZ; f.dU = c.dU;
     f.nbx = c.nbx; f.nbres = c.nbres; f.nbinv = c.nbinv; f.nbout = c.nbout; f.nbpart = c.nbpart;
     f.a_parts = c.a_parts > 0 ? c.a_parts : 1; f.a_pstride = c.a_pstride;
+    f.gather = c.gather; f.gather_rows = c.gather_rows; f.xout = c.xout;
     const long long nwg = static_cast<long long>(ceil_div(c.M, 16)) * f.tiles_n;
     if (nwg > 0x7fffffffLL || c.batch > 65535) return fail(LHIP_E_CAPACITY, "lm_fused_gemm: grid too large");
     dim3 grid(static_cast<unsigned>(nwg), c.batch);
