@@ -1947,20 +1947,23 @@ __device__ __forceinline__ void block_sumsq_out(double v, double* ss_out, double
 }
 
 // 64x64 tiles for the same float4-loadable groups.  The tile's 32x32
-// quadrants belong to four waves, and with KS = 2 a second set of four waves
-// takes every other 64-deep K chunk (each set with its own double-buffered
-// LDS), so each chain of dependent chunk loads is half as long; the two
-// partial quadrants are added in LDS in a fixed order.  At the LM step's
-// shapes (K = batch*seq rows) this is about one workgroup per CU, each chunk
-// holding 32 MFMA steps per wave while the next chunk's loads are in flight,
-// and nothing is re-read by a neighbouring tile as often as with 32x32 tiles.
+// quadrants belong to four waves, and KS sets of four waves take the BK-deep
+// K chunks in turn (set s: chunks s, s+KS, ..., each set with its own
+// double-buffered LDS), so each chain of dependent chunk loads is 1/KS as
+// long; the partial quadrants are added in LDS in set order.  KS = 2 with
+// 64-deep chunks for short K; KS = 4 with 32-deep chunks from K = 512 on
+// (four waves per SIMD: the C2 step's launch, K = 512, 19.3 -> 18.1 us).  At
+// the LM step's shapes (K = batch*seq rows) this is about one workgroup per
+// CU, and nothing is re-read by a neighbouring tile as often as with 32x32
+// tiles.
 // Placement: XCD x (blocks b with b % 8 == x) takes tiles [x*tp, (x+1)*tp)
 // first and then cp workgroups of column-sum jobs, each running up to
 // cs_per_wg 32-column blocks in turn, so no XCD holds more tiles than CUs.
-template <int KS>
+template <int KS, int BK>
 __global__ void __launch_bounds__(256 * KS) sgemm_grouped_tn_lds64_kernel(const GroupedTNArgs ga)
 {
-    constexpr int T = 64, BK = kGroupedBK, P = BK / 16;
+    constexpr int T = 64, P = BK / 16;
+    static_assert(BK % 16 == 0 && (KS - 1) * 4096 <= KS * 2 * BK * T, "reduction area");
     __shared__ __align__(16) float As[KS][2][BK][T];
     __shared__ __align__(16) float Bs[KS][2][BK][T];
     __shared__ double ssred[4 * KS];
@@ -2128,16 +2131,18 @@ __global__ void __launch_bounds__(256 * KS) sgemm_grouped_tn_lds64_kernel(const 
         if (it + 2 < iters) lstore(0, ra0, rb0);
         __syncthreads();
     }
-    if (KS == 2) {   // set 1's partial quadrants added to set 0's
+    if (KS > 1) {   // sets 1..KS-1's partial quadrants added to set 0's, in set order
         float* red = &As[0][0][0][0];
-        if (grp == 1) {
+        if (grp > 0) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) red[(wave * 16 + r) * 64 + lane] = acc[r];
+            for (int r = 0; r < 16; ++r) red[((grp - 1) * 64 + wave * 16 + r) * 64 + lane] = acc[r];
         }
         __syncthreads();
         if (grp == 0) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[r] += red[(wave * 16 + r) * 64 + lane];
+            for (int t = 0; t < KS - 1; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[r] += red[(t * 64 + wave * 16 + r) * 64 + lane];
         }
     }
     if (scat) {
@@ -2272,7 +2277,8 @@ int sgemm_grouped_tn(const GroupedTN* g, int ngroups, int K, hipStream_t stream,
             ex->fused = 1;
             ex->ss_parts = static_cast<int>(grid);
         }
-        klaunch(sgemm_grouped_tn_lds64_kernel<2>, grid, 512, 0, stream, ga);
+        if (K >= 512) klaunch(sgemm_grouped_tn_lds64_kernel<4, 32>, grid, 1024, 0, stream, ga);
+        else klaunch(sgemm_grouped_tn_lds64_kernel<2, kGroupedBK>, grid, 512, 0, stream, ga);
     }
     else if (vec) klaunch(sgemm_grouped_tn_lds_kernel, grid, 256, 0, stream, ga);
     else if (K >= 256) klaunch(sgemm_grouped_tn_kernel<8>, grid, 512, 0, stream, ga);
