@@ -516,15 +516,19 @@ constexpr int kBigLds = kBig * kLd256;
 
 __device__ __forceinline__ int big_swz(int row) { return (row ^ (row >> 3)) & 7; }
 
-template <bool KMAJOR, bool FULL>
+template <bool KMAJOR, bool FULL, int ROWS = kBig>
 struct BigTileRegs {
-    // 256 rows (m or n) x kBigK k of one operand: kBigQ float4 per thread
-    float4 v[kBigQ];
+    // ROWS rows (m or n) x kBigK k of one operand: NS float4 per thread
+    static constexpr int NS = ROWS * kBigK / 4 / kThreads;
+    static constexpr int CQ = ROWS / 4;              // KMAJOR: column quads of a k row
+    static constexpr int KQS = kThreads / CQ;        // KMAJOR: k quads per slot block
+    static_assert(NS % 4 == 0 && kThreads % CQ == 0, "tile rows");
+    float4 v[NS];
 
     // stored: element (row, k) at X[row * ld + k] (!KMAJOR) or X[k * ld + row] (KMAJOR).
-    // Slot s (0 .. kBigQ-1) is one float4 load:
+    // Slot s (0 .. NS-1) is one float4 load:
     // !KMAJOR: row tid/8 + 32s, k quad tid%8;
-    // KMAJOR: k row 4kq + s%4 of block (columns 4(tid%64) .. +3, k quad kq = tid/64 + 4(s/4)).
+    // KMAJOR: k row 4kq + s%4 of block (columns 4(tid%CQ) .. +3, k quad kq = tid/CQ + KQS(s/4)).
     // The slots are loaded and stored one at a time so that the main loop can
     // spread them between MFMA groups; a KMAJOR store slot needs the four
     // load slots of its block.
@@ -538,8 +542,8 @@ struct BigTileRegs {
             gk = k0 + 4 * (tid % kBigQ);
             src = X + static_cast<long long>(gr) * ld + gk;
         } else {
-            gr = r0 + 4 * (tid & 63);
-            gk = k0 + 4 * ((tid >> 6) + 4 * (s >> 2)) + (s & 3);
+            gr = r0 + 4 * (tid % CQ);
+            gk = k0 + 4 * (tid / CQ + KQS * (s >> 2)) + (s & 3);
             src = X + static_cast<long long>(gk) * ld + gr;
         }
         // the 4 contiguous elements: (row gr, k gk..gk+3) or (k gk, columns gr..gr+3)
@@ -562,10 +566,10 @@ struct BigTileRegs {
             const int row = tid / kBigQ + (kThreads / kBigQ) * s;
             *reinterpret_cast<float4*>(lds + row * kLd256 + 4 * ((tid % kBigQ) ^ big_swz(row))) = v[s];
         } else {
-            // column 4(tid%64) + s%4 of block s/4: its four k from the block's four loads
+            // column 4(tid%CQ) + s%4 of block s/4: its four k from the block's four loads
             const int b = s >> 2, c = s & 3;
-            const int row = 4 * (tid & 63) + c;
-            const int kq = (tid >> 6) + 4 * b;
+            const int row = 4 * (tid % CQ) + c;
+            const int kq = tid / CQ + KQS * b;
             const float4 t = make_float4(f4get(v[4 * b + 0], c), f4get(v[4 * b + 1], c), f4get(v[4 * b + 2], c),
                                          f4get(v[4 * b + 3], c));
             *reinterpret_cast<float4*>(lds + row * kLd256 + 4 * (kq ^ big_swz(row))) = t;
@@ -573,14 +577,19 @@ struct BigTileRegs {
     }
 };
 
-// FULL: M and N multiples of 256, K of kBigK, k-contiguous operands 16-byte
-// aligned -- every tile load is in bounds and unconditional.
-template <bool TA, bool TB, bool FULL>
+// FULL: M and N multiples of TILE, K of kBigK, k-contiguous operands 16-byte
+// aligned -- every tile load is in bounds and unconditional.  TILE = 128 is
+// the same kernel on 128x128 tiles (four waves of 64x64, 4 accumulators each,
+// 64 KB of LDS: two workgroups per CU), for problems with fewer 256x256 tiles
+// than CUs but many 128x128 ones.
+template <bool TA, bool TB, bool FULL, int TILE = kBig>
 __global__ void __launch_bounds__(kThreads)
 sgemm_256_kernel(const GemmArgs g)
 {
-    __shared__ float As[2][kBigLds];
-    __shared__ float Bs[2][kBigLds];
+    constexpr int F = TILE / 64;   // 32x32 blocks per wave and dimension
+    constexpr int LDS = TILE * kLd256;
+    __shared__ float As[2][LDS];
+    __shared__ float Bs[2][LDS];
     const int M = g.M, N = g.N;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -589,7 +598,7 @@ sgemm_256_kernel(const GemmArgs g)
     const int h = lane >> 5;
     int tm, tn;
     tile_coords(blockIdx.x, gridDim.x, g.tiles_m, g.tiles_n, tm, tn);
-    const int m0 = tm * kBig, n0 = tn * kBig;
+    const int m0 = tm * TILE, n0 = tn * TILE;
     const long long zo = blockIdx.y / g.inner, zi = blockIdx.y % g.inner;
     // split-K: this workgroup takes k in [kbeg, kbeg + K); the operands are
     // offset to the slice start (k runs along a stored row of A when !TA and
@@ -599,10 +608,11 @@ sgemm_256_kernel(const GemmArgs g)
     const float* __restrict__ A = g.A + zo * g.sA2 + zi * g.sA + (TA ? static_cast<long long>(kbeg) * g.lda : kbeg);
     const float* __restrict__ B = g.B + zo * g.sB2 + zi * g.sB + (TB ? kbeg : static_cast<long long>(kbeg) * g.ldb);
     const long long coff = zo * g.sC2 + zi * g.sC;
-    const int wm = (wave >> 1) * 128, wn = (wave & 1) * 128;
+    const int wm = (wave >> 1) * (TILE / 2), wn = (wave & 1) * (TILE / 2);
 
-    BigTileRegs<TA, FULL> ra;    // op(A): row m; stored M x K (!TA) or K x M (TA)
-    BigTileRegs<!TB, FULL> rb;   // op(B): row n; stored N x K (TB) or K x N (!TB)
+    BigTileRegs<TA, FULL, TILE> ra;    // op(A): row m; stored M x K (!TA) or K x M (TA)
+    BigTileRegs<!TB, FULL, TILE> rb;   // op(B): row n; stored N x K (TB) or K x N (!TB)
+    constexpr int NS = BigTileRegs<TA, FULL, TILE>::NS;
     auto gload = [&](int s, int k0) {
         ra.load_slot(s, A, g.lda, m0, k0, M, K, g.vecA, tid);
         rb.load_slot(s, B, g.ldb, n0, k0, N, K, g.vecB, tid);
@@ -612,59 +622,60 @@ sgemm_256_kernel(const GemmArgs g)
         rb.store_slot(s, Bs[buf], tid);
     };
 
-    floatx16 acc[4][4];
+    floatx16 acc[F][F];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < F; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < F; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
     // Fragments of one 8-deep step: a[i] = op(A) rows wm+32i+lr, b[j] = op(B)
     // columns wn+32j+lr, k = k0+4h .. k0+4h+3 each.
     // Quad k0/4 + h of row wm + 32i + lr sits at position (k0/4 + h) ^ swz, with
-    // swz = (lr ^ (lr >> 3) ^ 4(i & 1)) & 7 (wm, wn are multiples of 128);
+    // swz = (lr ^ (lr >> 3) ^ 4(i & 1)) & 7 (wm, wn are multiples of 64);
     // k0/4 is even, so the position is (k0/4) ^ g with g = h ^ swz.
-    struct Frag { float4 a[4], b[4]; };
+    struct Frag { float4 a[F], b[F]; };
     const int g_even = (h ^ lr ^ (lr >> 3)) & 7;
     auto read_frag = [&](Frag& f, int buf, int k0) {
         const float* as = As[buf] + (wm + lr) * kLd256;
         const float* bs = Bs[buf] + (wn + lr) * kLd256;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < F; ++i)
             f.a[i] = *reinterpret_cast<const float4*>(as + 32 * i * kLd256 + 4 * ((k0 / 4) ^ g_even ^ (4 * (i & 1))));
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < F; ++j)
             f.b[j] = *reinterpret_cast<const float4*>(bs + 32 * j * kLd256 + 4 * ((k0 / 4) ^ g_even ^ (4 * (j & 1))));
     };
     auto mma_t = [&](const Frag& f, int t) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < F; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < F; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(f4get(f.a[i], t), f4get(f.b[j], t), acc[i][j],
                                                                 0, 0, 0);
     };
 
     // Software pipeline over the four 8-deep steps of a K tile:
-    //   steps 0-2: read the next step's fragments, then four groups of 16
+    //   steps 0-2: read the next step's fragments, then four groups of F*F
     //     MFMAs; after each group, steps 0-1 issue one slot of the next tile's
-    //     global loads (8 slots), step 2 writes two slots to the other LDS
-    //     buffer (so the loads have had two steps to land);
+    //     global loads (8 slots; with TILE = 128, 4 slots in step 0), step 2
+    //     writes two slots (one) to the other LDS buffer (so the loads have
+    //     had two steps to land);
     //   barrier; read the next tile's step-0 fragments; step 3's MFMAs.
     // Spreading the loads and LDS writes keeps the MFMA pipe fed (a CU's
     // address path takes 64 B/clk: a whole tile's 64 KB issued at once stalls
     // the waves for ~1K cycles).  All reads of an LDS buffer are issued before
     // the barrier that precedes its next write.
     constexpr int kSteps = kBigK / 8;
-    static_assert(kSteps == 4 && kBigQ == 8, "the load/store schedule assumes 32-deep K tiles");
+    static_assert(kSteps == 4 && kBigQ == 8 && (NS == 8 || NS == 4), "the load/store schedule assumes 32-deep K tiles");
     const int nk = (K + kBigK - 1) / kBigK;
     Frag f[2];
     if (nk > 0) {
 #pragma unroll
-        for (int sl = 0; sl < kBigQ; ++sl) gload(sl, 0);
+        for (int sl = 0; sl < NS; ++sl) gload(sl, 0);
 #pragma unroll
-        for (int sl = 0; sl < kBigQ; ++sl) lstore(sl, 0);
+        for (int sl = 0; sl < NS; ++sl) lstore(sl, 0);
         __syncthreads();
         read_frag(f[0], 0, 0);
     }
@@ -682,11 +693,16 @@ sgemm_256_kernel(const GemmArgs g)
                 __builtin_amdgcn_sched_barrier(0);
                 mma_t(f[st & 1], t);
                 __builtin_amdgcn_sched_barrier(0);
-                if (st < 2) {
-                    gload(4 * st + t, kn);
+                if (NS == 8) {
+                    if (st < 2) {
+                        gload(4 * st + t, kn);
+                    } else {
+                        lstore(2 * t, cur ^ 1);
+                        lstore(2 * t + 1, cur ^ 1);
+                    }
                 } else {
-                    lstore(2 * t, cur ^ 1);
-                    lstore(2 * t + 1, cur ^ 1);
+                    if (st == 0) gload(t, kn);
+                    else if (st == 2) lstore(t, cur ^ 1);
                 }
             }
         }
@@ -707,9 +723,9 @@ sgemm_256_kernel(const GemmArgs g)
         float* __restrict__ wz =
             g.ws + (static_cast<long long>(blockIdx.z) * gridDim.y + blockIdx.y) * (static_cast<long long>(M) * N);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < F; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
+            for (int j = 0; j < F; ++j) {
                 const int col = n0 + wn + 32 * j + lr;
                 if (!FULL && col >= N) continue;
 #pragma unroll
@@ -727,9 +743,9 @@ sgemm_256_kernel(const GemmArgs g)
     auto epilogue = [&](auto use_rc) {
         constexpr bool USE_R = decltype(use_rc)::value;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < F; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
+            for (int j = 0; j < F; ++j) {
                 const int col = n0 + wn + 32 * j + lr;
                 if (!FULL && col >= N) continue;
 #pragma unroll
@@ -749,30 +765,36 @@ sgemm_256_kernel(const GemmArgs g)
 
 int launch_reduce(const GemmArgs& g, int batch, hipStream_t stream);
 
-int launch_256(int ta, int tb, GemmArgs g, int batch, hipStream_t stream)
+template <int TILE>
+int launch_big(int ta, int tb, GemmArgs g, int batch, hipStream_t stream)
 {
-    g.tiles_m = ceil_div(g.M, kBig);
-    g.tiles_n = ceil_div(g.N, kBig);
+    g.tiles_m = ceil_div(g.M, TILE);
+    g.tiles_n = ceil_div(g.N, TILE);
     const long long nwg = static_cast<long long>(g.tiles_m) * g.tiles_n;
     if (nwg > 0x7fffffffLL) return fail(LHIP_E_CAPACITY, "sgemm: %lld workgroups exceed the grid limit", nwg);
     if (g.splits <= 1 || !g.ws) { g.splits = 1; g.kchunk = g.K; g.ws = nullptr; }
     dim3 grid(static_cast<unsigned>(nwg), batch, g.splits), block(kThreads, 1, 1);
     // FULL: every tile and every K slice whole (slices start at multiples of
     // kchunk, itself a multiple of the 32-deep K tile)
-    const bool full = g.M % kBig == 0 && g.N % kBig == 0 && g.K % kBigK == 0 && g.kchunk % kBigK == 0 &&
+    const bool full = g.M % TILE == 0 && g.N % TILE == 0 && g.K % kBigK == 0 && g.kchunk % kBigK == 0 &&
                       (ta || g.vecA) && (!tb || g.vecB);
     auto go = [&](auto fullc) {
         constexpr bool F = decltype(fullc)::value;
-        if (!ta && !tb) klaunch(sgemm_256_kernel<false, false, F>, grid, block, 0, stream, g);
-        else if (ta && !tb) klaunch(sgemm_256_kernel<true, false, F>, grid, block, 0, stream, g);
-        else if (!ta && tb) klaunch(sgemm_256_kernel<false, true, F>, grid, block, 0, stream, g);
-        else klaunch(sgemm_256_kernel<true, true, F>, grid, block, 0, stream, g);
+        if (!ta && !tb) klaunch(sgemm_256_kernel<false, false, F, TILE>, grid, block, 0, stream, g);
+        else if (ta && !tb) klaunch(sgemm_256_kernel<true, false, F, TILE>, grid, block, 0, stream, g);
+        else if (!ta && tb) klaunch(sgemm_256_kernel<false, true, F, TILE>, grid, block, 0, stream, g);
+        else klaunch(sgemm_256_kernel<true, true, F, TILE>, grid, block, 0, stream, g);
     };
     if (full) go(std::true_type{});
     else go(std::false_type{});
     const int rc = check_launch("sgemm (256): kernel launch");
     if (rc != LHIP_OK || g.splits <= 1) return rc;
     return launch_reduce(g, batch, stream);
+}
+
+int launch_256(int ta, int tb, GemmArgs g, int batch, hipStream_t stream)
+{
+    return launch_big<kBig>(ta, tb, g, batch, stream);
 }
 
 // ---------------------------------------------------------------------------
@@ -2317,6 +2339,20 @@ int split256_plan(int m, int n, int k, int batch, size_t ws_floats, int* kchunk_
     return splits;
 }
 
+// The 256x256-tile kernel on 128x128 tiles: when there are fewer 256x256
+// tiles than CUs but at least ~3/4 of a CU's worth of 128x128 tiles, unless
+// the 256x256 tiles split over K into slices of 1024 or more (long K: the
+// big tiles' 84% beat the small ones' 79% at 2048x2048x8192).  Measured:
+// 2048^3 151.8 (256x256 in 4 slices of 512) -> 143.1 us; the C3 logits
+// 512x32000x128 57.3 -> 51.0 us; C3 dW 128x32000x512 52.4 -> 45.7 us.
+bool big128_ok(int m, int n, int batch, int s256, int kc256)
+{
+    const int cus = st().cu_count > 0 ? st().cu_count : 256;
+    const long long t256 = static_cast<long long>(ceil_div(m, kBig)) * ceil_div(n, kBig) * batch;
+    const long long t128 = static_cast<long long>(ceil_div(m, 128)) * ceil_div(n, 128) * batch;
+    return t256 < cus && 4 * t128 >= 3LL * cus && !(s256 > 1 && kc256 >= 1024);
+}
+
 // K per split slice from which a split 64x64-tile product runs on four wave sets.
 constexpr int kKsSliceMin = 1024;
 
@@ -2463,13 +2499,12 @@ int sgemm_run(int ta, int tb, int m, int n, int k, float alpha,
     }
     const long long tiles256 = static_cast<long long>(ceil_div(m, kBig)) * ceil_div(n, kBig) * batch;
     if (tiles256 >= cus) return launch_256(ta, tb, g, batch, stream);
-    if (!br && o.ws && !o.splits_out) {
-        int kc = 0;
-        const int s256 = split256_plan(m, n, k, batch, o.ws_floats, &kc);
-        if (s256 > 1) {
-            g.splits = s256; g.kchunk = kc; g.ws = o.ws;
-            return launch_256(ta, tb, g, batch, stream);
-        }
+    int kc256 = 0;
+    const int s256 = (!br && o.ws && !o.splits_out) ? split256_plan(m, n, k, batch, o.ws_floats, &kc256) : 1;
+    if (!br && big128_ok(m, n, batch, s256, kc256)) return launch_big<128>(ta, tb, g, batch, stream);
+    if (s256 > 1) {
+        g.splits = s256; g.kchunk = kc256; g.ws = o.ws;
+        return launch_256(ta, tb, g, batch, stream);
     }
     if (big_tiles >= cus) return launch_cfg<128, 128, 32>(ta, tb, g, batch, stream);
     // short K (e.g. the LM head, K = dim): the whole K range in one LDS tile,
@@ -2560,7 +2595,8 @@ int immediate_plan(int transa, int transb, int m, int n, int k, int batch, size_
         splits = skinny_plan(m, n, k, cap, &kchunk);
     } else {
         splits = split256_plan(m, n, k, batch, cap, &kchunk);
-        if (splits <= 1) splits = splitk_plan(m, n, k, batch, cap, &kchunk);
+        if (big128_ok(m, n, batch, splits, kchunk)) splits = 1;
+        else if (splits <= 1) splits = splitk_plan(m, n, k, batch, cap, &kchunk);
     }
     if (splits > 1) *need_floats = static_cast<size_t>(splits) * m * n * batch;
     return splits;

@@ -434,10 +434,18 @@ def test_gemm_batched_reduce_rejects_bad_count():
 @pytest.mark.parametrize("m,n,k,batch,ld_pad", [(4096, 4096, 96, 1, 0),     # every tile full
                                                 (4000, 4100, 203, 1, 0),   # ragged M, N and K
                                                 (4096, 4096, 64, 1, 1),    # ld % 4 != 0: scalar loads
-                                                (1024, 1024, 80, 16, 0)])  # 16 x 16 tiles per batch
+                                                (1024, 1024, 80, 16, 0),   # 16 x 16 tiles per batch
+                                                # 128x128 tiles on the same kernel
+                                                (2048, 2048, 96, 1, 0),    # every tile full
+                                                (2000, 2100, 203, 1, 0),   # ragged M, N and K
+                                                (2048, 2048, 64, 1, 1),    # scalar loads
+                                                (512, 512, 80, 16, 0),     # 4 x 4 tiles per batch
+                                                (128, 32000, 96, 1, 0)])   # one row of tiles (C3 dW shape)
 def test_gemm_256_tile_path(m, n, k, batch, ld_pad):
-    """Problems with at least one 256x256 output tile per CU: all four operand
-    layouts, alpha/beta, vs numpy float64 on each batch entry."""
+    """Problems with at least one 256x256 output tile per CU, and those with
+    fewer but about one 128x128 tile per CU or more (the same kernel on
+    128x128 tiles): all four operand layouts, alpha/beta, vs numpy float64 on
+    each batch entry."""
     announce("gemm 256 tiles", m, n, k, batch, ld_pad)
     rng = np.random.default_rng(m + n + k + batch + ld_pad)
     a = rng.uniform(-1, 1, (batch, m, k)).astype(np.float32)
