@@ -2345,6 +2345,25 @@ int split256_plan(int m, int n, int k, int batch, size_t ws_floats, int* kchunk_
 // big tiles' 84% beat the small ones' 79% at 2048x2048x8192).  Measured:
 // 2048^3 151.8 (256x256 in 4 slices of 512) -> 143.1 us; the C3 logits
 // 512x32000x128 57.3 -> 51.0 us; C3 dW 128x32000x512 52.4 -> 45.7 us.
+// Few 128x128 tiles (at most an eighth of the CUs) over a long K: the same
+// kernel split over K into one slice per CU's worth of tiles, slices of 448+
+// (C3 dhidden 512x128x32000: 4 tiles x 64 slices of 512, 53-57 -> 48 us; a
+// split count that leaves CUs idle or doubles up measured slower).  Batch 1.
+int big128_split_plan(int m, int n, int k, size_t ws_floats, int* kchunk_out)
+{
+    const int cus = st().cu_count > 0 ? st().cu_count : 256;
+    if (m <= 64 || n <= 64) return 1;
+    const long long t128 = static_cast<long long>(ceil_div(m, 128)) * ceil_div(n, 128);
+    if (8 * t128 > cus) return 1;
+    const long long s = cus / t128;
+    const int kchunk = static_cast<int>(ceil_div(ceil_div(static_cast<long long>(k), s), 32LL) * 32);
+    if (kchunk < 448) return 1;
+    const int splits = ceil_div(k, kchunk);
+    if (splits < 2 || static_cast<size_t>(splits) * m * n > ws_floats) return 1;
+    *kchunk_out = kchunk;
+    return splits;
+}
+
 bool big128_ok(int m, int n, int batch, int s256, int kc256)
 {
     const int cus = st().cu_count > 0 ? st().cu_count : 256;
@@ -2506,6 +2525,14 @@ int sgemm_run(int ta, int tb, int m, int n, int k, float alpha,
         g.splits = s256; g.kchunk = kc256; g.ws = o.ws;
         return launch_256(ta, tb, g, batch, stream);
     }
+    if (!br && o.ws && !o.splits_out && batch == 1) {
+        int kc128 = 0;
+        const int s128 = big128_split_plan(m, n, k, o.ws_floats, &kc128);
+        if (s128 > 1) {
+            g.splits = s128; g.kchunk = kc128; g.ws = o.ws;
+            return launch_big<128>(ta, tb, g, 1, stream);
+        }
+    }
     if (big_tiles >= cus) return launch_cfg<128, 128, 32>(ta, tb, g, batch, stream);
     // short K (e.g. the LM head, K = dim): the whole K range in one LDS tile,
     // so a workgroup waits on one load round trip instead of one per 32-deep chunk
@@ -2596,7 +2623,10 @@ int immediate_plan(int transa, int transb, int m, int n, int k, int batch, size_
     } else {
         splits = split256_plan(m, n, k, batch, cap, &kchunk);
         if (big128_ok(m, n, batch, splits, kchunk)) splits = 1;
-        else if (splits <= 1) splits = splitk_plan(m, n, k, batch, cap, &kchunk);
+        else if (splits <= 1) {
+            splits = batch == 1 ? big128_split_plan(m, n, k, cap, &kchunk) : 1;
+            if (splits <= 1) splits = splitk_plan(m, n, k, batch, cap, &kchunk);
+        }
     }
     if (splits > 1) *need_floats = static_cast<size_t>(splits) * m * n * batch;
     return splits;

@@ -52,11 +52,11 @@ def test_gemm_family_vs_oracle(m, k, n):
     assert rel_fro(_gemm(True, True, at, bt), ref) <= TOL
 
 
-@pytest.mark.parametrize("m,k,n", [(64, 4096, 4096), (40, 2500, 1100), (300, 20000, 200)])
+@pytest.mark.parametrize("m,k,n", [(64, 4096, 4096), (40, 2500, 1100), (1000, 8192, 600)])
 def test_gemm_split_band_on_four_wave_sets(m, k, n):
     """Few 64x64 tiles with long K, split over K into slices of 1024 or more
-    on four wave sets (33..64 rows: one tile band; 300 x 200 x 20000: 20
-    tiles in 13 slices), slices summed in order by the reduce, all four
+    on four wave sets (33..64 rows: one tile band; 1000 x 600 x 8192: 160
+    tiles in 2 slices), slices summed in order by the reduce, all four
     transposition variants, ragged M, N and K."""
     announce("gemm split band", m, k, n)
     rng = np.random.default_rng(m * 3 + k + n)
@@ -86,6 +86,26 @@ def test_gemm_two_wave_set_tiles(m, k, n):
         assert rel_fro(got, ref) <= TOL, (ta, tb)
     c0 = f32(rng.uniform(-1, 1, (m, n)))
     got = _gemm(False, False, a, b, alpha=0.5, beta=-2.0, c0=c0)
+    assert rel_fro(got, 0.5 * ref - 2.0 * c0.astype(np.float64)) <= TOL
+
+
+@pytest.mark.parametrize("m,k,n", [(512, 32000, 128), (500, 20000, 130), (300, 20000, 200)])
+def test_gemm_big_tiles_split_over_k(m, k, n):
+    """Few 128x128 tiles over a long K (C3 dhidden 512x128x32000): the big-tile
+    kernel split over K into one slice per CU's worth of tiles, the slices
+    summed in order by the reduce; all four transposition variants, ragged M,
+    N and K, and alpha / beta."""
+    announce("gemm big tiles split", m, k, n)
+    rng = np.random.default_rng(m + 7 * k + n)
+    a = f32(rng.uniform(-1, 1, (m, k)))
+    b = f32(rng.uniform(-1, 1, (k, n)))
+    ref = a.astype(np.float64) @ b.astype(np.float64)
+    at, bt = np.ascontiguousarray(a.T), np.ascontiguousarray(b.T)
+    for ta, tb in ((0, 0), (1, 0), (0, 1), (1, 1)):
+        got = _gemm(bool(ta), bool(tb), at if ta else a, bt if tb else b)
+        assert rel_fro(got, ref) <= TOL, (ta, tb)
+    c0 = f32(rng.uniform(-1, 1, (m, n)))
+    got = _gemm(False, True, a, bt, alpha=0.5, beta=-2.0, c0=c0)
     assert rel_fro(got, 0.5 * ref - 2.0 * c0.astype(np.float64)) <= TOL
 
 
