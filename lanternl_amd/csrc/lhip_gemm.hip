@@ -2539,6 +2539,9 @@ int sgemm_run(int ta, int tb, int m, int n, int k, float alpha,
     if (tiles64 >= cus) {
         // long K at one or two 64x64 tiles per CU: four or two wave sets per tile
         if (g.K >= 512 && tiles64 <= cus) return launch_cfg_ks<64, 64, 32, 4>(ta, tb, g, batch, stream);
+        // shorter K at exactly one tile per CU (the C2 tied head, 512x2000x128:
+        // 1 us less per step): two wave sets, one 32-deep chunk in two each
+        if (g.K >= 64 && tiles64 <= cus) return launch_cfg_ks<64, 64, 32, 2>(ta, tb, g, batch, stream);
         if (g.K >= 512 && tiles64 <= 2 * cus) return launch_cfg_ks<64, 64, 32, 2>(ta, tb, g, batch, stream);
         return launch_cfg<64, 64, 32>(ta, tb, g, batch, stream);
     }

@@ -69,12 +69,14 @@ def test_gemm_split_band_on_four_wave_sets(m, k, n):
         assert rel_fro(got, ref) <= TOL, (ta, tb)
 
 
-@pytest.mark.parametrize("m,k,n", [(1024, 1024, 1024), (1000, 777, 1030), (2048, 1024, 1024)])
+@pytest.mark.parametrize("m,k,n", [(1024, 1024, 1024), (1000, 777, 1030), (2048, 1024, 1024), (512, 128, 2000),
+                                   (500, 100, 2040)])
 def test_gemm_two_wave_set_tiles(m, k, n):
     """Mid-size products with long K on one or two 64x64 tiles per CU (four or
     two wave sets taking every fourth or second K chunk; K = 777 ragged with a
-    chunk count that is not a multiple of the set count), all four
-    transposition variants, and alpha / beta."""
+    chunk count that is not a multiple of the set count), short K at one tile
+    per CU on two wave sets (the C2 tied head 512x2000x128; K = 100 ragged),
+    all four transposition variants, and alpha / beta."""
     announce("gemm two wave sets", m, k, n)
     rng = np.random.default_rng(m + k + n)
     a = f32(rng.uniform(-1, 1, (m, k)))
