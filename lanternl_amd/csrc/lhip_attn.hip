@@ -10,8 +10,11 @@
 //   dqr = dS . kr, dkr = dS^T . qr, dq, dk = inverse RoPE of dqr, dkr.
 // Each direction is one launch instead of five or six (RoPE, scores GEMM,
 // softmax, PV GEMM / dP and dv GEMMs, softmax backward, dq and dk GEMMs, RoPE
-// backward).  A (window, head) is split over one workgroup (4 wave64s) per
-// 16-row block, so a C2 layer runs 256 workgroups (one per CU) instead of 64:
+// backward).  The forward runs one wave per (window, head, 16-row query
+// block) with no LDS when the float4 forms apply (attn_fwd_wave_kernel);
+// otherwise, and in the backward, a (window, head) is split over one
+// workgroup (4 wave64s) per 16-row block, so a C2 layer runs 256 workgroups
+// (one per CU) instead of 64:
 // the step is latency-bound and a wave's VALU work is what it waits on, so the
 // work is spread over CUs, one 16x16 block per wave.  The backward uses
 // rowsum(dP o P) = rowsum(dO o O) (O = ctx), which makes each dS block
@@ -321,6 +324,140 @@ __global__ void __launch_bounds__(kAttnThreads) attn_fwd_kernel(const AttnArgs a
     }
 }
 
+// Forward on one wave per (window b, head h, query block c), with no LDS and
+// no barrier.  The wave forms S^T = kr . qr^T block by block (keys as rows:
+// lane (r, q) supplies kr(j0 + r, k) and qr(i0 + r, k) for k = 16u + 4q + e
+// with MFMA e of a step taking element e of each float4, and receives
+// S(i0 + r, j0 + 4q + e) in element e), so a query row's scores sit in the 4
+// lanes r, r+16, r+32, r+48: its max and sum of exp are an in-lane reduction
+// over blocks and elements, then two lane exchanges.  The same registers are
+// then the A operand of P . v (k = key j0 + 4q + e), with v(j0 + 4q + e,
+// 16db + r) loaded per lane as B, and P goes to global as float4 rows.  All
+// global loads (q, k, v, the (cos, sin) pairs) issue before the first use,
+// at clamped addresses.  Requires hd % 4 == 0, T % 4 == 0 and 16-byte aligned
+// qkv, cs, P and ctx.
+constexpr int kWaveJobs = 1;   // waves (jobs) per workgroup
+template <int U>   // float4 groups of 16 head dims: hd <= 16 U
+__global__ void __launch_bounds__(64 * kWaveJobs) attn_fwd_wave_kernel(const AttnArgs a)
+{
+    const int T = a.T, hd = a.hd, D = a.D, pairs = hd >> 1;
+    const int nbt = (T + 15) >> 4;
+    const int job = blockIdx.x * kWaveJobs + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (job >= a.B * a.H * nbt) return;
+    const int c = job % nbt, bh = job / nbt, b = bh / a.H, h = bh - b * a.H;
+    const int lane = threadIdx.x & 63, r = lane & 15, q = lane >> 4;
+    const int i0 = 16 * c;
+    const int nj = a.causal ? c + 1 : nbt;
+    const int kl = a.wlen ? min(T, a.wlen[b]) : T;
+    const long long ND = static_cast<long long>(a.N) * D;
+    const float* __restrict__ base = a.qkv + static_cast<long long>(b * T) * D + h * hd;
+    // query row i0 + r and key rows j0 + r: U float4 of dims 16u + 4q .. +3
+    const int qi = min(i0 + r, T - 1);
+    float4 qv[U], qc[U], kv[4][U], kc[4][U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int g = 4 * u + q;                       // float4 index within the head
+        const int gc = 4 * g < hd ? g : 0;             // past hd: loaded from column 0, zeroed below
+        qv[u] = *reinterpret_cast<const float4*>(base + static_cast<long long>(qi) * D + 4 * gc);
+        qc[u] = *reinterpret_cast<const float4*>(a.cs + qi * pairs + 2 * gc);
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) {
+            const int kj = min(16 * jb + r, T - 1);
+            kv[jb][u] = *reinterpret_cast<const float4*>(base + ND + static_cast<long long>(kj) * D + 4 * gc);
+            kc[jb][u] = *reinterpret_cast<const float4*>(a.cs + kj * pairs + 2 * gc);
+        }
+    }
+    // v(j0 + 4q + e, 16 db + r) for the output's 16-column blocks db
+    float vv[4][U][4];
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+        for (int db = 0; db < U; ++db)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int j = min(16 * jb + 4 * q + e, T - 1), d = 16 * db + r;
+                vv[jb][db][e] = base[2 * ND + static_cast<long long>(j) * D + (d < hd ? d : 0)];
+            }
+    auto rot = [](float4 x, float4 c) {
+        return make_float4(x.x * c.x - x.y * c.y, x.x * c.y + x.y * c.x, x.z * c.z - x.w * c.w, x.z * c.w + x.w * c.z);
+    };
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const bool in = 4 * (4 * u + q) < hd;
+        qv[u] = in ? rot(qv[u], qc[u]) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) kv[jb][u] = in ? rot(kv[jb][u], kc[jb][u]) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    // scores of query row i0 + r against keys j0 + 4q + e, masked
+    const int lim = attn_lim(i0 + r, kl, a.causal);
+    float sv[4][4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) {
+        floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+        if (jb < nj) {   // wave-uniform
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[jb][u].x, qv[u].x, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[jb][u].y, qv[u].y, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[jb][u].z, qv[u].z, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[jb][u].w, qv[u].w, acc, 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int j = 16 * jb + 4 * q + e;
+            sv[jb][e] = (jb < nj && j < lim) ? acc[e] * a.scale : -INFINITY;
+            mx = fmaxf(mx, sv[jb][e]);
+        }
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m0 = (mx == -INFINITY || mx != mx) ? 0.f : mx;
+    float sum = 0.f;
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int j = 16 * jb + 4 * q + e;
+            sv[jb][e] = (jb < nj && j < lim) ? expf(sv[jb][e] - m0) : 0.f;
+            sum += sv[jb][e];
+        }
+    sum += __shfl_xor(sum, 16);
+    sum += __shfl_xor(sum, 32);
+    const float is = sum > 0.f ? 1.0f / sum : 1.0f;
+    // P rows i0 .. i0+15 (zeros past the causal edge), float4 per lane and block
+    const int row = i0 + r;
+    float* Pg = a.P + (static_cast<long long>(b) * a.H + h) * T * T + static_cast<long long>(row) * T;
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sv[jb][e] *= is;
+        const int j = 16 * jb + 4 * q;
+        if (jb < nbt && row < T && j < T)
+            *reinterpret_cast<float4*>(Pg + j) = make_float4(sv[jb][0], sv[jb][1], sv[jb][2], sv[jb][3]);
+    }
+    // ctx(i0 + 4q + e, 16 db + r) = sum_j P(i0 + 4q + e, j) v(j, 16 db + r): A = P with
+    // rows r (query) and k = key, B = v
+#pragma unroll
+    for (int db = 0; db < U; ++db) {
+        if (16 * db >= hd) break;   // uniform
+        floatx4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) {
+            if (jb >= nj) break;   // uniform
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o = __builtin_amdgcn_mfma_f32_16x16x4f32(sv[jb][e], vv[jb][db][e], o, 0, 0, 0);
+        }
+        const int d = 16 * db + r;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int orow = i0 + 4 * q + e;
+            if (orow < T && d < hd) a.ctx[static_cast<long long>(b * T + orow) * D + h * hd + d] = o[e];
+        }
+    }
+}
+
 // Backward.  Workgroup (window b, head h, block c).  With D_i = rowsum(dO o O)
 // (O the forward's ctx; it equals rowsum(dP o P)), a block
 // dS(i, j) = scale * P(i, j) o (dP(i, j) - D_i) needs only dP(i, j) =
@@ -553,7 +690,16 @@ int attn_fwd(const float* qkv, const float2* cs, float* P, float* ctx, int B, in
     a.scale = scale; a.causal = causal; a.wlen = wlen;
     a.vec = (hd % 4 == 0 && aligned16(qkv) && aligned16(cs)) ? 1 : 0;
     a.vec = a.vec && aligned16(ctx);
-    klaunch(attn_fwd_kernel, B * H * ((T + 15) / 16), kAttnThreads, 0, s, a);
+    const int jobs = B * H * ((T + 15) / 16);
+    if (a.vec && T % 4 == 0 && aligned16(P)) {   // one wave per (window, head, query block)
+        const unsigned grid = static_cast<unsigned>((jobs + kWaveJobs - 1) / kWaveJobs);
+        if (hd <= 16) klaunch(attn_fwd_wave_kernel<1>, grid, 64 * kWaveJobs, 0, s, a);
+        else if (hd <= 32) klaunch(attn_fwd_wave_kernel<2>, grid, 64 * kWaveJobs, 0, s, a);
+        else if (hd <= 48) klaunch(attn_fwd_wave_kernel<3>, grid, 64 * kWaveJobs, 0, s, a);
+        else klaunch(attn_fwd_wave_kernel<4>, grid, 64 * kWaveJobs, 0, s, a);
+        return check_launch("attn_fwd");
+    }
+    klaunch(attn_fwd_kernel, jobs, kAttnThreads, 0, s, a);
     return check_launch("attn_fwd");
 }
 

@@ -86,11 +86,12 @@ def test_lm_step_eight_layers_weight_gradient_batches():
     gpu.close()
 
 
-@pytest.mark.parametrize("D,H,T", [(12, 2, 7), (16, 2, 7), (24, 2, 12)])
+@pytest.mark.parametrize("D,H,T", [(12, 2, 7), (16, 2, 7), (24, 2, 12), (64, 2, 20), (96, 2, 36), (128, 2, 64)])
 def test_lm_step_attention_load_paths(D, H, T):
     """The fused attention's operand loads: float4 (head_dim and T multiples of
     4), float4 forward with element-wise backward (T = 7), and element-wise
-    both ways (head_dim 6)."""
+    both ways (head_dim 6); the one-wave forward over one to four 16-wide
+    head-dimension groups (head_dim 12 (partial group), 32, 48 and 64)."""
     announce("lm attention loads", D, H, T)
     gpu, res = _run_case(30, D, 1, H, 2 * D, 2, T, steps=1, lr=0.1, std=0.3, seed=7 + D + T)
     _check(res)
