@@ -441,11 +441,11 @@ __global__ void __launch_bounds__(64 * kWaveJobs) attn_fwd_wave_kernel(const Att
     // rows r (query) and k = key, B = v
 #pragma unroll
     for (int db = 0; db < U; ++db) {
-        if (16 * db >= hd) break;   // uniform
+        if (16 * db >= hd) continue;   // uniform (no break: the loops must unroll fully)
         floatx4 o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int jb = 0; jb < 4; ++jb) {
-            if (jb >= nj) break;   // uniform
+            if (jb >= nj) continue;   // uniform
 #pragma unroll
             for (int e = 0; e < 4; ++e) o = __builtin_amdgcn_mfma_f32_16x16x4f32(sv[jb][e], vv[jb][db][e], o, 0, 0, 0);
         }
