@@ -1660,8 +1660,11 @@ int skinny_plan(int m, int n, int k, size_t ws_floats, int* kchunk_out)
 {
     const int cus = st().cu_count > 0 ? st().cu_count : 256;
     const long long cb = ceil_div(n, m <= kSkinnyValuMax ? kSkinnyCols : kSkinnyMfmaCols);
-    // about two workgroups per CU for the VALU form; one for the eight-wave MFMA form
-    const long long per_cu = m > kSkinnyValuMax ? 1 : 2;
+    // about two workgroups per CU for the VALU form and the one-group (M <= 16)
+    // MFMA form; one for the eight-wave MFMA form on 2-4 groups (M = 4, 8, 16
+    // at K = N = 4096: 24.1, 24.5, 21.1 us on one per CU, 19.6, 19.6, 19.3 on
+    // two; M = 32: 29.2 on one, 30.7 on two)
+    const long long per_cu = m <= 16 ? 2 : 1;
     long long s = (per_cu * cus + cb - 1) / cb;
     s = std::min<long long>(s, k / 64);
     s = std::min<long long>(s, std::max<long long>(1, k / (8LL * m)));
