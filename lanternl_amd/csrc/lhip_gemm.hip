@@ -337,8 +337,9 @@ sgemm_mfma_kernel(const GemmArgs g)
 // SIMD holds KS waves and each set's chain of dependent chunk loads is KS
 // times shorter; the sets' partial tiles meet in LDS (fixed order).  For long
 // K on one or two 64x64 tiles per CU (1024^3: 35.7 us on one wave set, 28.2
-// on four).
-template <int BM, int BN, int BK, bool TA, bool TB, int KS>
+// on four).  PF = 2: two register sets per wave set, so chunk kt + 2 KS is in
+// flight while chunk kt runs and chunk kt + KS goes to LDS.
+template <int BM, int BN, int BK, bool TA, bool TB, int KS, int PF = 1>
 __global__ void __launch_bounds__(kThreads * KS)
 sgemm_mfma_ks_kernel(const GemmArgs g)
 {
@@ -362,22 +363,24 @@ sgemm_mfma_ks_kernel(const GemmArgs g)
     const float* __restrict__ B = g.B + zo * g.sB2 + zi * g.sB;
     const long long coff = zo * g.sC2 + zi * g.sC;
     const int wm = (wave >> 1) * WM, wn = (wave & 1) * WN;
-    TileRegs<TA ? BK : BM, TA ? BM : BK> ra;
-    TileRegs<TB ? BN : BK, TB ? BK : BN> rb;
+    TileRegs<TA ? BK : BM, TA ? BM : BK> ra, ra2;
+    TileRegs<TB ? BN : BK, TB ? BK : BN> rb, rb2;
     const int kbeg = blockIdx.z * g.kchunk;
     const int kend = min(g.K, kbeg + g.kchunk);
-    auto gload = [&](int k0) {
-        if (TA) ra.load(A, g.lda, k0, m0, kend, M, g.vecA, gt);
-        else    ra.load(A, g.lda, m0, k0, M, kend, g.vecA, gt);
-        if (TB) rb.load(B, g.ldb, n0, k0, N, kend, g.vecB, gt);
-        else    rb.load(B, g.ldb, k0, n0, kend, N, g.vecB, gt);
+    auto gload_to = [&](auto& xa, auto& xb, int k0) {
+        if (TA) xa.load(A, g.lda, k0, m0, kend, M, g.vecA, gt);
+        else    xa.load(A, g.lda, m0, k0, M, kend, g.vecA, gt);
+        if (TB) xb.load(B, g.ldb, n0, k0, N, kend, g.vecB, gt);
+        else    xb.load(B, g.ldb, k0, n0, kend, N, g.vecB, gt);
     };
-    auto lstore = [&](int buf) {
-        if (TA) ra.template store_direct<LDA>(As[grp][buf], gt);
-        else    ra.template store_transposed<LDA>(As[grp][buf], gt);
-        if (TB) rb.template store_transposed<LDB>(Bs[grp][buf], gt);
-        else    rb.template store_direct<LDB>(Bs[grp][buf], gt);
+    auto lstore_from = [&](const auto& xa, const auto& xb, int buf) {
+        if (TA) xa.template store_direct<LDA>(As[grp][buf], gt);
+        else    xa.template store_transposed<LDA>(As[grp][buf], gt);
+        if (TB) xb.template store_transposed<LDB>(Bs[grp][buf], gt);
+        else    xb.template store_direct<LDB>(Bs[grp][buf], gt);
     };
+    auto gload = [&](int k0) { gload_to(ra, rb, k0); };
+    auto lstore = [&](int buf) { lstore_from(ra, rb, buf); };
     floatx16 acc[FM][FN];
 #pragma unroll
     for (int i = 0; i < FM; ++i)
@@ -387,35 +390,56 @@ sgemm_mfma_ks_kernel(const GemmArgs g)
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
     const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
     const int iters = (nk + KS - 1) / KS;
+    auto mma = [&](int cur) {
+        const float* as = As[grp][cur];
+        const float* bs = Bs[grp][cur];
+#pragma unroll
+        for (int kk = 0; kk < BK; kk += 2) {
+            float a[FM], b[FN];
+#pragma unroll
+            for (int i = 0; i < FM; ++i) a[i] = as[(kk + lk) * LDA + wm + 32 * i + lr];
+#pragma unroll
+            for (int j = 0; j < FN; ++j) b[j] = bs[(kk + lk) * LDB + wn + 32 * j + lr];
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+    };
     if (grp < nk) gload(kbeg + grp * BK);
     else { ra = decltype(ra){}; rb = decltype(rb){}; }
-    lstore(0);
-    __syncthreads();
-    for (int it = 0; it < iters; ++it) {
-        const int cur = it & 1;
-        const int kt = it * KS + grp;
-        const bool more = it + 1 < iters;
-        const bool next_in = kt + KS < nk;
-        if (more && next_in) gload(kbeg + (kt + KS) * BK);
-        if (kt < nk) {
-            const float* as = As[grp][cur];
-            const float* bs = Bs[grp][cur];
-#pragma unroll
-            for (int kk = 0; kk < BK; kk += 2) {
-                float a[FM], b[FN];
-#pragma unroll
-                for (int i = 0; i < FM; ++i) a[i] = as[(kk + lk) * LDA + wm + 32 * i + lr];
-#pragma unroll
-                for (int j = 0; j < FN; ++j) b[j] = bs[(kk + lk) * LDB + wn + 32 * j + lr];
-#pragma unroll
-                for (int i = 0; i < FM; ++i)
-#pragma unroll
-                    for (int j = 0; j < FN; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
-            }
-        }
-        if (more && next_in) lstore(cur ^ 1);
+    if constexpr (PF == 2) {
+        // two register sets: chunk kt + 2 KS is loaded while chunk kt runs its
+        // MFMAs and chunk kt + KS (loaded one iteration earlier) goes to LDS
+        if (grp + KS < nk) gload_to(ra2, rb2, kbeg + (grp + KS) * BK);
+        lstore(0);
         __syncthreads();
+        auto body = [&](int it, auto& la, auto& lb, const auto& sa, const auto& sb) {
+            const int cur = it & 1;
+            const int kt = it * KS + grp;
+            if (kt + 2 * KS < nk) gload_to(la, lb, kbeg + (kt + 2 * KS) * BK);
+            if (kt < nk) mma(cur);
+            if (kt + KS < nk) lstore_from(sa, sb, cur ^ 1);
+            __syncthreads();
+        };
+        for (int it = 0; it < iters; it += 2) {
+            body(it, ra, rb, ra2, rb2);
+            if (it + 1 < iters) body(it + 1, ra2, rb2, ra, rb);
+        }
+    } else {
+        lstore(0);
+        __syncthreads();
+        for (int it = 0; it < iters; ++it) {
+            const int cur = it & 1;
+            const int kt = it * KS + grp;
+            const bool more = it + 1 < iters;
+            const bool next_in = kt + KS < nk;
+            if (more && next_in) gload(kbeg + (kt + KS) * BK);
+            if (kt < nk) mma(cur);
+            if (more && next_in) lstore(cur ^ 1);
+            __syncthreads();
+        }
     }
     constexpr int SZ = 4 * FM * FN * 1024;   // one set's partial tiles (floats)
     static_assert(KS >= 2 && (KS - 1) * SZ <= KS * 2 * BK * LDA, "reduction area");
@@ -1729,7 +1753,11 @@ int launch_cfg_ks(int ta, int tb, GemmArgs g, int batch, hipStream_t stream)
     if (nwg > 0x7fffffffLL) return fail(LHIP_E_CAPACITY, "sgemm: %lld workgroups exceed the grid limit", nwg);
     if (g.splits <= 1) { g.splits = 1; g.kchunk = g.K; g.ws = nullptr; }
     dim3 grid(static_cast<unsigned>(nwg), batch, g.splits), block(KS * kThreads, 1, 1);
-    if (!ta && !tb) klaunch(sgemm_mfma_ks_kernel<BM, BN, BK, false, false, KS>, grid, block, 0, stream, g);
+    // NN (A's 32-deep chunk is 64 row segments of 128 bytes) loads two chunks
+    // ahead: 1024^3 32.3 -> 30.8 us and 2048x1024x512 31.9 -> 31.3 (medians of
+    // six alternating rounds on one box); TN and NT measured 0.4-0.5 us slower
+    // that way
+    if (!ta && !tb) klaunch(sgemm_mfma_ks_kernel<BM, BN, BK, false, false, KS, 2>, grid, block, 0, stream, g);
     else if (ta && !tb) klaunch(sgemm_mfma_ks_kernel<BM, BN, BK, true, false, KS>, grid, block, 0, stream, g);
     else if (!ta && tb) klaunch(sgemm_mfma_ks_kernel<BM, BN, BK, false, true, KS>, grid, block, 0, stream, g);
     else klaunch(sgemm_mfma_ks_kernel<BM, BN, BK, true, true, KS>, grid, block, 0, stream, g);
