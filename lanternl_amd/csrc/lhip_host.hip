@@ -8,15 +8,11 @@
 // staging, in chunks: each chunk's upload (or download) is queued on the
 // library stream as soon as it is converted (or waited for just before it is
 // widened), so conversion overlaps the PCIe copies and the GEMM.  Small calls
-// (the C1 shapes) skip the pool: one vectorised pass per operand, one upload,
-// one download.
-#include <atomic>
-#include <condition_variable>
-#include <functional>
-#include <mutex>
-#include <thread>
-
+// (the C1 shapes) convert each operand in one pass split over the calling
+// thread and the pool's spinning workers, copy A and B in with one kernel and
+// have the GEMM store the product straight into pinned memory.
 #include "lhip_internal.h"
+#include "lhip_pool.h"
 
 namespace lhip {
 namespace {
@@ -63,109 +59,7 @@ void widen(const float* s, double* d, long long n, int acc)
     else f32_to_f64_base(s, d, n, acc);
 }
 
-// ---------------------------------------------------------------- thread pool
-// Workers sleep on a condition variable.  run(parts, fn) publishes fn under a
-// new generation number, hands out part indices 0..parts-1 through an atomic
-// counter (the calling thread takes parts too) and returns once every worker
-// has finished with that generation, so no worker can still hold fn (or touch
-// the counter) when run returns.  Started on the first large call, joined by
-// lhip_shutdown.
-class HostPool {
-public:
-    ~HostPool() { stop(); }
-
-    int threads() const { return static_cast<int>(workers_.size()) + 1; }
-
-    void start()
-    {
-        if (!workers_.empty()) return;
-        unsigned hw = std::thread::hardware_concurrency();
-        int n = static_cast<int>(hw > 0 ? hw : 4);
-        if (n > kMaxThreads) n = kMaxThreads;
-        unsigned long long g0;
-        {
-            std::lock_guard<std::mutex> g(mu_);
-            quit_ = false;
-            g0 = gen_;   // a new worker waits for the next generation
-        }
-        for (int i = 1; i < n; ++i) workers_.emplace_back([this, g0] { loop(g0); });
-    }
-
-    void stop()
-    {
-        {
-            std::lock_guard<std::mutex> g(mu_);
-            quit_ = true;
-            ++gen_;
-        }
-        cv_.notify_all();
-        for (auto& t : workers_) t.join();
-        workers_.clear();
-    }
-
-    void run(int parts, const std::function<void(int)>& fn)
-    {
-        if (workers_.empty() || parts <= 1) {
-            for (int p = 0; p < parts; ++p) fn(p);
-            return;
-        }
-        {
-            std::lock_guard<std::mutex> g(mu_);
-            fn_ = &fn;
-            parts_ = parts;
-            next_.store(0);
-            finished_ = 0;
-            ++gen_;
-        }
-        cv_.notify_all();
-        work(&fn, parts);
-        std::unique_lock<std::mutex> g(mu_);
-        done_cv_.wait(g, [&] { return finished_ == static_cast<int>(workers_.size()); });
-        fn_ = nullptr;
-    }
-
-private:
-    static constexpr int kMaxThreads = 16;
-
-    void work(const std::function<void(int)>* fn, int parts)
-    {
-        for (int p; (p = next_.fetch_add(1)) < parts;) (*fn)(p);
-    }
-
-    void loop(unsigned long long seen)
-    {
-        while (true) {
-            const std::function<void(int)>* fn;
-            int parts;
-            {
-                std::unique_lock<std::mutex> g(mu_);
-                cv_.wait(g, [&] { return gen_ != seen; });
-                seen = gen_;
-                if (quit_) return;
-                fn = fn_;
-                parts = parts_;
-            }
-            if (!fn) continue;
-            work(fn, parts);
-            {
-                std::lock_guard<std::mutex> g(mu_);
-                ++finished_;
-            }
-            done_cv_.notify_one();
-        }
-    }
-
-    std::vector<std::thread> workers_;
-    std::mutex mu_;
-    std::condition_variable cv_, done_cv_;
-    const std::function<void(int)>* fn_ = nullptr;
-    int parts_ = 0, finished_ = 0;
-    std::atomic<int> next_{0};
-    unsigned long long gen_ = 0;
-    bool quit_ = false;
-};
-
-HostPool g_pool;
+HostPool g_pool;   // three spinning workers
 
 // Copy n floats from pinned host memory into device memory with the GPU's own
 // loads (one float4 per thread): for a small call this costs a kernel launch
@@ -181,16 +75,26 @@ __global__ void __launch_bounds__(256) stage_in_kernel(const float* __restrict__
     }
 }
 
-// Below this many elements in all three operands together a call converts on
-// the calling thread (waking the pool costs more than it saves).
+// Below this many elements in all three operands together a call is small:
+// one conversion pass per operand (split over the calling thread and the
+// spinning workers), one upload kernel, the product stored into pinned memory.
 constexpr long long kPoolMin = 1LL << 20;
 // Elements per pipelined chunk (16 MiB of fp32).
 constexpr long long kChunk = 1LL << 22;
 
-// Convert [0, n) with the pool, in slices of at least 64 Ki elements.
-void par_narrow(const double* s, float* d, long long n)
+// Convert [0, n) with the pool: slices of at least 64 Ki elements over every
+// thread, or (small calls) of at least 8 Ki over the calling thread and the
+// spinning workers.
+int conv_parts(long long n, bool small)
 {
-    const int parts = static_cast<int>(std::min<long long>(g_pool.threads(), (n + 65535) / 65536));
+    const long long unit = small ? 8192 : 65536;
+    const int cap = small ? g_pool.spinners() + 1 : g_pool.threads();
+    return static_cast<int>(std::max<long long>(1, std::min<long long>(cap, (n + unit - 1) / unit)));
+}
+
+void par_narrow(const double* s, float* d, long long n, bool small = false)
+{
+    const int parts = conv_parts(n, small);
     const long long per = (n + parts - 1) / parts;
     g_pool.run(parts, [&](int p) {
         const long long b = p * per, e = std::min(n, b + per);
@@ -198,9 +102,23 @@ void par_narrow(const double* s, float* d, long long n)
     });
 }
 
-void par_widen(const float* s, double* d, long long n, int acc)
+// A and B of a small call in one run: the parts split the two arrays as one
+// index range (A's elements, then B's).
+void par_narrow2(const double* a, float* ha, long long na, const double* b, float* hb, long long nb)
 {
-    const int parts = static_cast<int>(std::min<long long>(g_pool.threads(), (n + 65535) / 65536));
+    const long long n = na + nb;
+    const int parts = conv_parts(n, true);
+    const long long per = (n + parts - 1) / parts;
+    g_pool.run(parts, [&](int p) {
+        const long long lo = p * per, hi = std::min(n, lo + per);
+        if (lo < std::min(hi, na)) narrow(a + lo, ha + lo, std::min(hi, na) - lo);
+        if (std::max(lo, na) < hi) narrow(b + (std::max(lo, na) - na), hb + (std::max(lo, na) - na), hi - std::max(lo, na));
+    });
+}
+
+void par_widen(const float* s, double* d, long long n, int acc, bool small = false)
+{
+    const int parts = conv_parts(n, small);
     const long long per = (n + parts - 1) / parts;
     g_pool.run(parts, [&](int p) {
         const long long b = p * per, e = std::min(n, b + per);
@@ -273,14 +191,10 @@ LHIP_API int lhip_matmul_host(int op, const double* a, const double* b, double* 
     float* db = da + pad(na);
     float* dc = db + pad(nb);
     const bool pooled = na + nb + nc >= lhip::kPoolMin;
-    if (pooled) lhip::g_pool.start();
+    lhip::g_pool.start();
 
     // upload: convert a chunk, queue its copy, convert the next meanwhile
     auto upload = [&](const double* src, float* h, float* d, long long cnt) -> int {
-        if (!pooled) {
-            lhip::narrow(src, h, cnt);
-            return LHIP_OK;
-        }
         for (long long off = 0; off < cnt; off += lhip::kChunk) {
             const long long len = std::min(lhip::kChunk, cnt - off);
             lhip::par_narrow(src + off, h + off, len);
@@ -289,8 +203,12 @@ LHIP_API int lhip_matmul_host(int op, const double* a, const double* b, double* 
         }
         return LHIP_OK;
     };
-    if (int rc = upload(a, ha, da, na)) return rc;
-    if (int rc = upload(b, hb, db, nb)) return rc;
+    if (!pooled) {
+        lhip::par_narrow2(a, ha, na, b, hb, nb);
+    } else {
+        if (int rc = upload(a, ha, da, na)) return rc;
+        if (int rc = upload(b, hb, db, nb)) return rc;
+    }
     if (!pooled) {   // A and B (adjacent in the staging) in one kernel-side copy
         const long long cnt = pad(na) + nb;
         lhip::klaunch(lhip::stage_in_kernel, dim3(static_cast<unsigned>((cnt + 1023) / 1024)), dim3(256), 0, s.stream,
@@ -311,7 +229,7 @@ LHIP_API int lhip_matmul_host(int op, const double* a, const double* b, double* 
     if (rc != LHIP_OK) return rc;
     if (!pooled) {
         LHIP_CHECK_HIP(hipStreamSynchronize(s.stream), "lhip_matmul_host: sync");
-        lhip::widen(hc, c, nc, acc);
+        lhip::par_widen(hc, c, nc, acc, true);
         return LHIP_OK;
     }
     // download: queue every chunk's copy with an event behind it, then widen
