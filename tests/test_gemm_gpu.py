@@ -333,6 +333,32 @@ def test_matmul_host_accumulate_in_double():
     assert rel_fro(out, expect) <= TOL
 
 
+def test_matmul_host_small_calls_back_to_back():
+    """Small calls (under 1 Mi elements) convert on the calling thread and the
+    pool's spinning workers: 240 calls of random shapes (one to four parts per
+    conversion), ops and accumulate flags, with pauses past the workers' spin
+    window every 40 calls, each against the float64 product of the
+    fp32-rounded inputs."""
+    announce("matmul_host small calls")
+    import time
+    from lanternl_amd._lib import call
+    rng = np.random.default_rng(77)
+    for i in range(240):
+        op, acc = int(rng.integers(0, 3)), int(rng.integers(0, 2))
+        m, k, n = (int(x) for x in rng.integers(1, 300, 3))
+        a = rng.uniform(-1, 1, (m, k))
+        b = rng.uniform(-1, 1, {0: (k, n), 1: (n, k), 2: (m, n)}[op])
+        a32, b32 = a.astype(np.float32).astype(np.float64), b.astype(np.float32).astype(np.float64)
+        ref = {0: lambda: a32 @ b32, 1: lambda: a32 @ b32.T, 2: lambda: a32.T @ b32}[op]()
+        c0 = rng.uniform(-1, 1, ref.shape)
+        out = c0.copy()
+        call("lhip_matmul_host", op, a.ctypes.data_as(ctypes.c_void_p), b.ctypes.data_as(ctypes.c_void_p),
+             out.ctypes.data_as(ctypes.c_void_p), m, k, n, acc)
+        assert rel_fro(out, ref + c0 if acc else ref) <= TOL, (i, op, m, k, n, acc)
+        if i % 40 == 39:
+            time.sleep(0.003)
+
+
 @pytest.mark.parametrize("op,m,k,n,acc", [(0, 2048, 2304, 2048, 0), (1, 1500, 1024, 1300, 1), (2, 2100, 1000, 900, 0)])
 def test_matmul_host_threaded_chunks(op, m, k, n, acc):
     """Calls large enough for the threaded, chunked host path (conversions on
