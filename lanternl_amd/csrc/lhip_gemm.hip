@@ -75,6 +75,21 @@ struct TileRegs {
         }
     }
 
+    // Every element in bounds and the stored rows 16-byte aligned: one
+    // unconditional float4 load per pass (no branch for a wait to be
+    // conservative about).
+    __device__ __forceinline__ void load_full(const float* __restrict__ g, int ld, int r0, int c0, int tid)
+    {
+        const int cq = tid % CQ;
+        const int rr = tid / CQ;
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+            const float4 t = *reinterpret_cast<const float4*>(g + static_cast<long long>(r0 + rr + p * RPP) * ld + c0 +
+                                                              4 * cq);
+            v[p].x = t.x; v[p].y = t.y; v[p].z = t.z; v[p].w = t.w;   // per component: stays in VGPRs
+        }
+    }
+
     // Store as lds[row][col] (tile orientation kept; LD % 4 == 0).
     template <int LD>
     __device__ __forceinline__ void store_direct(float* lds, int tid) const
@@ -339,7 +354,7 @@ sgemm_mfma_kernel(const GemmArgs g)
 // K on one or two 64x64 tiles per CU (1024^3: 35.7 us on one wave set, 28.2
 // on four).  PF = 2: two register sets per wave set, so chunk kt + 2 KS is in
 // flight while chunk kt runs and chunk kt + KS goes to LDS.
-template <int BM, int BN, int BK, bool TA, bool TB, int KS, int PF = 1>
+template <int BM, int BN, int BK, bool TA, bool TB, int KS, int PF = 1, bool FULL = false>
 __global__ void __launch_bounds__(kThreads * KS)
 sgemm_mfma_ks_kernel(const GemmArgs g)
 {
@@ -368,10 +383,17 @@ sgemm_mfma_ks_kernel(const GemmArgs g)
     const int kbeg = blockIdx.z * g.kchunk;
     const int kend = min(g.K, kbeg + g.kchunk);
     auto gload_to = [&](auto& xa, auto& xb, int k0) {
-        if (TA) xa.load(A, g.lda, k0, m0, kend, M, g.vecA, gt);
-        else    xa.load(A, g.lda, m0, k0, M, kend, g.vecA, gt);
-        if (TB) xb.load(B, g.ldb, n0, k0, N, kend, g.vecB, gt);
-        else    xb.load(B, g.ldb, k0, n0, kend, N, g.vecB, gt);
+        if constexpr (FULL) {
+            if (TA) xa.load_full(A, g.lda, k0, m0, gt);
+            else    xa.load_full(A, g.lda, m0, k0, gt);
+            if (TB) xb.load_full(B, g.ldb, n0, k0, gt);
+            else    xb.load_full(B, g.ldb, k0, n0, gt);
+        } else {
+            if (TA) xa.load(A, g.lda, k0, m0, kend, M, g.vecA, gt);
+            else    xa.load(A, g.lda, m0, k0, M, kend, g.vecA, gt);
+            if (TB) xb.load(B, g.ldb, n0, k0, N, kend, g.vecB, gt);
+            else    xb.load(B, g.ldb, k0, n0, kend, N, g.vecB, gt);
+        }
     };
     auto lstore_from = [&](const auto& xa, const auto& xb, int buf) {
         if (TA) xa.template store_direct<LDA>(As[grp][buf], gt);
@@ -407,25 +429,39 @@ sgemm_mfma_ks_kernel(const GemmArgs g)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
         }
     };
-    if (grp < nk) gload(kbeg + grp * BK);
+    // FULL: every chunk load is unconditional (past the last chunk a set
+    // reloads the last one, which it never stores), so the wait before an LDS
+    // store counts only the loads of the chunk being stored; a set with no
+    // chunk stores and reads only its own LDS, and adds a zero tile
+    if (FULL) gload(kbeg + min(grp, nk - 1) * BK);
+    else if (grp < nk) gload(kbeg + grp * BK);
     else { ra = decltype(ra){}; rb = decltype(rb){}; }
     if constexpr (PF == 2) {
         // two register sets: chunk kt + 2 KS is loaded while chunk kt runs its
         // MFMAs and chunk kt + KS (loaded one iteration earlier) goes to LDS
-        if (grp + KS < nk) gload_to(ra2, rb2, kbeg + (grp + KS) * BK);
+        if (FULL) gload_to(ra2, rb2, kbeg + min(grp + KS, nk - 1) * BK);
+        else if (grp + KS < nk) gload_to(ra2, rb2, kbeg + (grp + KS) * BK);
         lstore(0);
         __syncthreads();
-        auto body = [&](int it, auto& la, auto& lb, const auto& sa, const auto& sb) {
+        // the register sets are picked at compile time (a run-time choice
+        // between them would put both in scratch memory)
+        auto body = [&](int it, auto setc) {
+            constexpr int L = decltype(setc)::value;   // the set loaded; the other is stored
+            auto& la = L == 0 ? ra : ra2;
+            auto& lb = L == 0 ? rb : rb2;
+            const auto& sa = L == 0 ? ra2 : ra;
+            const auto& sb = L == 0 ? rb2 : rb;
             const int cur = it & 1;
             const int kt = it * KS + grp;
-            if (kt + 2 * KS < nk) gload_to(la, lb, kbeg + (kt + 2 * KS) * BK);
+            if (FULL) gload_to(la, lb, kbeg + min(kt + 2 * KS, nk - 1) * BK);
+            else if (kt + 2 * KS < nk) gload_to(la, lb, kbeg + (kt + 2 * KS) * BK);
             if (kt < nk) mma(cur);
             if (kt + KS < nk) lstore_from(sa, sb, cur ^ 1);
             __syncthreads();
         };
         for (int it = 0; it < iters; it += 2) {
-            body(it, ra, rb, ra2, rb2);
-            if (it + 1 < iters) body(it + 1, ra2, rb2, ra, rb);
+            body(it, std::integral_constant<int, 0>{});
+            if (it + 1 < iters) body(it + 1, std::integral_constant<int, 1>{});
         }
     } else {
         lstore(0);
@@ -435,7 +471,8 @@ sgemm_mfma_ks_kernel(const GemmArgs g)
             const int kt = it * KS + grp;
             const bool more = it + 1 < iters;
             const bool next_in = kt + KS < nk;
-            if (more && next_in) gload(kbeg + (kt + KS) * BK);
+            if (FULL) gload(kbeg + min(kt + KS, nk - 1) * BK);
+            else if (more && next_in) gload(kbeg + (kt + KS) * BK);
             if (kt < nk) mma(cur);
             if (more && next_in) lstore(cur ^ 1);
             __syncthreads();
@@ -1757,7 +1794,19 @@ int launch_cfg_ks(int ta, int tb, GemmArgs g, int batch, hipStream_t stream)
     // ahead: 1024^3 32.3 -> 30.8 us and 2048x1024x512 31.9 -> 31.3 (medians of
     // six alternating rounds on one box); TN and NT measured 0.4-0.5 us slower
     // that way
-    if (!ta && !tb) klaunch(sgemm_mfma_ks_kernel<BM, BN, BK, false, false, KS, 2>, grid, block, 0, stream, g);
+    // Whole tiles and chunks with float4-loadable operands: unconditional
+    // loads two chunks ahead (1024^3 NN 29.5 -> 26.6 us, NT 26.9 -> 24.2, TN
+    // 27.5 -> 26.0, 2048x1024x512 30.6 -> 25.8, the M = 64 band 29.4 -> 27.3;
+    // with the loads behind a branch each LDS store waited for every load in
+    // flight, the chunk two ahead included)
+    const bool full = g.M % BM == 0 && g.N % BN == 0 && g.K % BK == 0 && g.kchunk % BK == 0 && g.vecA && g.vecB &&
+                      g.Kb == g.K;
+    if (full) {
+        if (!ta && !tb) klaunch(sgemm_mfma_ks_kernel<BM, BN, BK, false, false, KS, 2, true>, grid, block, 0, stream, g);
+        else if (ta && !tb) klaunch(sgemm_mfma_ks_kernel<BM, BN, BK, true, false, KS, 2, true>, grid, block, 0, stream, g);
+        else if (!ta && tb) klaunch(sgemm_mfma_ks_kernel<BM, BN, BK, false, true, KS, 2, true>, grid, block, 0, stream, g);
+        else klaunch(sgemm_mfma_ks_kernel<BM, BN, BK, true, true, KS, 2, true>, grid, block, 0, stream, g);
+    } else if (!ta && !tb) klaunch(sgemm_mfma_ks_kernel<BM, BN, BK, false, false, KS, 2>, grid, block, 0, stream, g);
     else if (ta && !tb) klaunch(sgemm_mfma_ks_kernel<BM, BN, BK, true, false, KS>, grid, block, 0, stream, g);
     else if (!ta && tb) klaunch(sgemm_mfma_ks_kernel<BM, BN, BK, false, true, KS>, grid, block, 0, stream, g);
     else klaunch(sgemm_mfma_ks_kernel<BM, BN, BK, true, true, KS>, grid, block, 0, stream, g);
