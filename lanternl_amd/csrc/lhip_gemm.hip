@@ -78,14 +78,18 @@ struct TileRegs {
     // Every element in bounds and the stored rows 16-byte aligned: one
     // unconditional float4 load per pass (no branch for a wait to be
     // conservative about).
-    __device__ __forceinline__ void load_full(const float* __restrict__ g, int ld, int r0, int c0, int tid)
+    // Rows past rmax and columns past cmax (cmax % 4 == 0) are clamped into
+    // the operand: they only reach outputs that are not stored.
+    __device__ __forceinline__ void load_full(const float* __restrict__ g, int ld, int r0, int c0, int rmax, int cmax,
+                                              int tid)
     {
         const int cq = tid % CQ;
         const int rr = tid / CQ;
+        const int c = min(c0 + 4 * cq, cmax - 4);
 #pragma unroll
         for (int p = 0; p < PASSES; ++p) {
-            const float4 t = *reinterpret_cast<const float4*>(g + static_cast<long long>(r0 + rr + p * RPP) * ld + c0 +
-                                                              4 * cq);
+            const int r = min(r0 + rr + p * RPP, rmax - 1);
+            const float4 t = *reinterpret_cast<const float4*>(g + static_cast<long long>(r) * ld + c);
             v[p].x = t.x; v[p].y = t.y; v[p].z = t.z; v[p].w = t.w;   // per component: stays in VGPRs
         }
     }
@@ -384,10 +388,12 @@ sgemm_mfma_ks_kernel(const GemmArgs g)
     const int kend = min(g.K, kbeg + g.kchunk);
     auto gload_to = [&](auto& xa, auto& xb, int k0) {
         if constexpr (FULL) {
-            if (TA) xa.load_full(A, g.lda, k0, m0, gt);
-            else    xa.load_full(A, g.lda, m0, k0, gt);
-            if (TB) xb.load_full(B, g.ldb, n0, k0, gt);
-            else    xb.load_full(B, g.ldb, k0, n0, gt);
+            // K is whole chunks; M and N are clamped (M % 4 == 0 when A is
+            // stored K-major, N % 4 == 0 when B is)
+            if (TA) xa.load_full(A, g.lda, k0, m0, kend, M, gt);
+            else    xa.load_full(A, g.lda, m0, k0, M, kend, gt);
+            if (TB) xb.load_full(B, g.ldb, n0, k0, N, kend, gt);
+            else    xb.load_full(B, g.ldb, k0, n0, kend, N, gt);
         } else {
             if (TA) xa.load(A, g.lda, k0, m0, kend, M, g.vecA, gt);
             else    xa.load(A, g.lda, m0, k0, M, kend, g.vecA, gt);
@@ -1794,13 +1800,17 @@ int launch_cfg_ks(int ta, int tb, GemmArgs g, int batch, hipStream_t stream)
     // ahead: 1024^3 32.3 -> 30.8 us and 2048x1024x512 31.9 -> 31.3 (medians of
     // six alternating rounds on one box); TN and NT measured 0.4-0.5 us slower
     // that way
-    // Whole tiles and chunks with float4-loadable operands: unconditional
+    // Whole chunks with float4-loadable operands: unconditional
     // loads two chunks ahead (1024^3 NN 29.5 -> 26.6 us, NT 26.9 -> 24.2, TN
     // 27.5 -> 26.0, 2048x1024x512 30.6 -> 25.8, the M = 64 band 29.4 -> 27.3;
     // with the loads behind a branch each LDS store waited for every load in
     // flight, the chunk two ahead included)
-    const bool full = g.M % BM == 0 && g.N % BN == 0 && g.K % BK == 0 && g.kchunk % BK == 0 && g.vecA && g.vecB &&
-                      g.Kb == g.K;
+    // (M and N need not be whole tiles: rows and columns past them are
+    // clamped into the operands; M % 4 == 0 when A is stored K-major and
+    // N % 4 == 0 when B is.  The tied head of the C2 step, 512x2000x128 NT,
+    // 7.2 -> 6.8 us; a 60x4000x4096 band 31.5 -> 27.8.)
+    const bool full = (!ta || g.M % 4 == 0) && (tb || g.N % 4 == 0) && g.K % BK == 0 && g.kchunk % BK == 0 &&
+                      g.vecA && g.vecB && g.Kb == g.K;
     if (full) {
         if (!ta && !tb) klaunch(sgemm_mfma_ks_kernel<BM, BN, BK, false, false, KS, 2, true>, grid, block, 0, stream, g);
         else if (ta && !tb) klaunch(sgemm_mfma_ks_kernel<BM, BN, BK, true, false, KS, 2, true>, grid, block, 0, stream, g);
