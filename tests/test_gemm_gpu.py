@@ -70,13 +70,17 @@ def test_gemm_split_band_on_four_wave_sets(m, k, n):
 
 
 @pytest.mark.parametrize("m,k,n", [(1024, 1024, 1024), (1000, 777, 1030), (2048, 1024, 1024), (512, 128, 2000),
-                                   (500, 100, 2040)])
+                                   (500, 100, 2040), (500, 1024, 2000), (510, 512, 2044), (60, 2048, 2000)])
 def test_gemm_two_wave_set_tiles(m, k, n):
     """Mid-size products with long K on one or two 64x64 tiles per CU (four or
     two wave sets taking every fourth or second K chunk; K = 777 ragged with a
     chunk count that is not a multiple of the set count), short K at one tile
     per CU on two wave sets (the C2 tied head 512x2000x128; K = 100 ragged),
-    all four transposition variants, and alpha / beta."""
+    all four transposition variants, and alpha / beta.  Whole 32-deep chunks
+    take the unconditional-load form with rows and columns past M and N
+    clamped: 500x1024x2000 (edge tiles in M and N), 510x512x2044 (M % 4 != 0:
+    the K-major-A variants keep the guarded loads), 60x2048x2000 (the split
+    64-row band)."""
     announce("gemm two wave sets", m, k, n)
     rng = np.random.default_rng(m + k + n)
     a = f32(rng.uniform(-1, 1, (m, k)))
