@@ -95,6 +95,26 @@ def test_gemm_two_wave_set_tiles(m, k, n):
     assert rel_fro(got, 0.5 * ref - 2.0 * c0.astype(np.float64)) <= TOL
 
 
+@pytest.mark.parametrize("m,k,n", [(1536, 1536, 1536), (1500, 777, 1700), (1536, 256, 1536), (1600, 800, 1600)])
+def test_gemm_one_wave_set_tiles(m, k, n):
+    """Products with more 64x64 tiles than two per CU below the big-tile sizes
+    (or short K) on the wave-set kernel with one set: whole-chunk loads two
+    chunks ahead, or the guarded loads for K = 777; all four transposition
+    variants and alpha / beta, against float64."""
+    announce("gemm one wave set", m, k, n)
+    rng = np.random.default_rng(m + 3 * k + n)
+    a = f32(rng.uniform(-1, 1, (m, k)))
+    b = f32(rng.uniform(-1, 1, (k, n)))
+    ref = a.astype(np.float64) @ b.astype(np.float64)
+    at, bt = np.ascontiguousarray(a.T), np.ascontiguousarray(b.T)
+    for ta, tb in ((0, 0), (1, 0), (0, 1), (1, 1)):
+        got = _gemm(bool(ta), bool(tb), at if ta else a, bt if tb else b)
+        assert rel_fro(got, ref) <= TOL, (ta, tb)
+    c0 = f32(rng.uniform(-1, 1, (m, n)))
+    got = _gemm(False, False, a, b, alpha=0.5, beta=-2.0, c0=c0)
+    assert rel_fro(got, 0.5 * ref - 2.0 * c0.astype(np.float64)) <= TOL
+
+
 @pytest.mark.parametrize("m,k,n", [(512, 32000, 128), (500, 20000, 130), (300, 20000, 200)])
 def test_gemm_big_tiles_split_over_k(m, k, n):
     """Few 128x128 tiles over a long K (C3 dhidden 512x128x32000): the big-tile
