@@ -147,10 +147,15 @@ LHIP_API int lhip_is_recording(void);
  * program run; this times each kernel).  For benchmarks that must agree with
  * a kernel trace: between start and stop, each of the first `capacity` kernel
  * launches records its dispatch's start and end timestamps (launch gaps
- * excluded).  stop synchronises the stream, writes the durations in launch
- * order to ms[0 .. min(count, capacity)) and the number of timed launches to
- * *count.  Not allowed while a program is being recorded (and
- * lhip_program_begin refuses while the timer is on). */
+ * excluded).  stop synchronises the stream, writes the durations of the
+ * timed launches in launch order to ms[0 .. min(timed, capacity)) and the
+ * number of kernels launched while the timer was on (timed or not) to
+ * *count.  When ms is given and some launch went untimed (past either
+ * capacity, or made into a stream capture, where nothing is dispatched),
+ * stop still fills ms but returns LHIP_E_CAPACITY, so a caller cannot
+ * under-report silently.  Not allowed while a program is being recorded
+ * (lhip_program_begin refuses while the timer is on, and so does a
+ * graph-mode lhip_lm_step_*). */
 LHIP_API int lhip_ktimer_start(int capacity);
 LHIP_API int lhip_ktimer_stop(float* ms, int capacity, int* count);
 

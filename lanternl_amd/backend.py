@@ -3,9 +3,13 @@
 The Python mirror of ``lanternl_amd/lua/luatl_adapter.lua``, which is the Lua
 module itself (the LuaJIT FFI binding that ai/core/matrix.lua requires).  Both
 follow the reference adapter, ai/gpu/luatl_adapter.lua, call for call: the
-same names, the same argument lists and the same return conventions, so a
-reference caller (tests/test.lua:436-475, ai/optim/lmtrain_gpu.lua:94-104,
-ai/benchmarks/bench_gpu_transformer.lua) reads the same here.
+same names, the same argument lists and the same return conventions.  A
+reference caller that uses only the adapter's own functions (the registry,
+tests/test.lua:436-475) reads the same here.  Callers that reach past the
+adapter into the reference's low-level module (``adapter.luaTL``:
+ai/gpu/gpu_transformer.lua:58-60, ai/benchmarks/bench_gpu_transformer.lua:41,
+and ai/optim/lmtrain_gpu.lua through gpu_transformer) do not: that field has
+no counterpart here and is None.
 
 * Module contract (matrix.lua:28-48): ``available``, ``reason``/``error`` and
   ``matmul(a, m, k, b, n)``.  ``a`` and ``b`` are flat row-major sequences or
@@ -16,6 +20,11 @@ ai/benchmarks/bench_gpu_transformer.lua) reads the same here.
       matmul_nt(a, m, k, b, n) -> a(m x k) . b(n x k)^T   (m*n numbers)
       matmul_tn(a, m, k, b, n) -> a(m x k)^T . b(m x n)   (k*n numbers)
 
+  ``matmul_into(op, a, m, k, b, n, rd, acc)`` serves the products that write
+  into a caller's flat sequence (matrix.multiply / matmul_nt / matmul_tn with
+  ``out``, which the autograd backward passes with ``acc = true``,
+  tensor2.lua:206-211,222-227): ``rd`` receives the product, or has it added
+  in double with ``acc``, after the device call has succeeded.
 * Legacy flat calls (luatl_adapter.lua:137-159): ``rmsnorm(x, rows, cols, w,
   eps)``, ``softmax(x, rows, cols)``, ``softmax_causal(x, rows, cols, scale,
   group)``, each taking a flat table or a handle.
@@ -89,13 +98,12 @@ class Tensor:
     address, ``rows``/``cols``/``nelem``/``nbytes``/``dtype``).  Owning tensors
     hold a device.Buffer; ``wrap`` makes non-owning ones."""
 
-    __slots__ = ("data", "rows", "cols", "dtype", "_buf", "is_ids")
+    __slots__ = ("data", "rows", "cols", "dtype", "_buf")
 
     def __init__(self, rows, cols, data=None, buf=None):
         self.rows, self.cols, self.dtype = int(rows), int(cols), F32
         self._buf = buf
         self.data = int(data) if data is not None else (buf.ptr if buf is not None else 0)
-        self.is_ids = False
 
     @property
     def nelem(self):
@@ -121,6 +129,22 @@ class Tensor:
         self.data = 0
 
 
+def _fetch_f32(ptr, n):
+    """n fp32 values at a device address, as a new list of floats."""
+    buf = np.empty(n, np.float32)
+    call("lhip_download", buf.ctypes.data, ptr, 4 * n)
+    return buf.astype(np.float64).tolist()
+
+
+def _put_f32(ptr, seq, n, what):
+    """The first n numbers of a flat sequence, rounded to fp32, to a device address."""
+    vals = np.asarray(seq, dtype=np.float32).reshape(-1)
+    if vals.size < n:
+        raise ValueError(f"lanternl_hip: {what} needs {n} numbers, the table holds {vals.size}")
+    vals = np.ascontiguousarray(vals[:n])
+    call("lhip_upload", ptr, vals.ctypes.data, 4 * n)
+
+
 class Handle:
     """A resident GPU matrix exposed to lanternl (luatl_adapter.lua:46-101)."""
 
@@ -128,18 +152,10 @@ class Handle:
         self.t, self.rows, self.cols = t, rows, cols
 
     def toflat(self):
-        n = self.rows * self.cols
-        out = np.empty(n, np.float32)
-        call("lhip_download", out.ctypes.data, self.t.data, 4 * n)
-        return out.astype(np.float64).tolist()
+        return _fetch_f32(self.t.data, self.rows * self.cols)
 
     def upload(self, flat):
-        n = self.rows * self.cols
-        a = np.asarray(flat, dtype=np.float32).reshape(-1)
-        if a.size < n:
-            raise ValueError(f"luatl.upload: {a.size} elements < {self.rows}x{self.cols}")
-        a = np.ascontiguousarray(a[:n])
-        call("lhip_upload", self.t.data, a.ctypes.data, 4 * n)
+        _put_f32(self.t.data, flat, self.rows * self.cols, f"Handle:upload into {self.rows}x{self.cols}")
         return self
 
     def zero(self):
@@ -147,9 +163,9 @@ class Handle:
         return self
 
     def free(self):
-        if self.t is not None:
-            self.t.free()
-            self.t = None
+        t, self.t = self.t, None
+        if t is not None:
+            t.free()
 
     def tensor(self):
         return self.t
@@ -170,12 +186,16 @@ def new_handle(t, rows, cols):
 
 
 def pin(flat, rows, cols):
-    """Upload a flat sequence once and keep it resident (luatl_adapter.lua:63-73)."""
+    """Upload a flat sequence once and keep it resident (luatl_adapter.lua:63-73):
+    it must hold exactly rows*cols numbers."""
     _require()
     n = rows * cols
     if len(flat) != n:
-        raise ValueError(f"luatl.pin: {len(flat)} elements != {rows}x{cols}")
-    return Handle(Tensor.new(rows, cols), rows, cols).upload(flat)
+        raise ValueError(f"lanternl_hip.pin: a {rows}x{cols} matrix takes exactly {n} numbers, "
+                         f"the table holds {len(flat)}")
+    h = Handle(Tensor.new(rows, cols), rows, cols)
+    _put_f32(h.t.data, flat, n, "pin")
+    return h
 
 
 def alloc(rows, cols):
@@ -184,58 +204,78 @@ def alloc(rows, cols):
     return Handle(Tensor.new(rows, cols), rows, cols).zero()
 
 
-# scratch for the flat-table calls, keyed by slot and shape (luatl_adapter.lua:34-44)
-_scratch = {}
+# Device lanes for the flat-table calls: one grow-only buffer per operand lane
+# (0 = first operand, 1 = second, 2 = result), sized to the next power of two
+# that fits; each call gets a non-owning tensor shaped for it.
+LANE_A, LANE_B, LANE_C = 0, 1, 2
+_lanes = {}
 
 
-def _dev_scratch(slot, rows, cols):
-    key = (slot, rows, cols)
-    t = _scratch.get(key)
-    if t is None:
-        t = Tensor.new(rows, cols)
-        _scratch[key] = t
-    return t
+def _pow2_at_least(n):
+    c = 256
+    while c < n:
+        c *= 2
+    return c
 
 
-def _as_tensor(x, rows, cols, slot):
-    """A handle's tensor, or a flat sequence uploaded to scratch (luatl_adapter.lua:102-114)."""
+def _dev_lane(lane, rows, cols):
+    need = max(rows * cols, 1)
+    store = _lanes.get(lane)
+    if store is None or store.nelem < need:
+        if store is not None:
+            store.free()
+        store = Tensor.new(_pow2_at_least(need), 1)
+        _lanes[lane] = store
+    return Tensor(rows, cols, data=store.data)
+
+
+def _operand(x, rows, cols, lane):
+    """(tensor, resident): a handle's tensor, or a flat sequence copied into a device lane."""
     if is_handle(x):
         return x.t, True
-    n = rows * cols
-    a = np.asarray(x, dtype=np.float32).reshape(-1)
-    if a.size < n:
-        raise ValueError(f"luatl adapter: expected {n} elements, got {a.size}")
-    a = np.ascontiguousarray(a[:n])
-    t = _dev_scratch(slot, rows, cols)
-    call("lhip_upload", t.data, a.ctypes.data, 4 * n)
+    t = _dev_lane(lane, rows, cols)
+    _put_f32(t.data, x, rows * cols, f"a {rows}x{cols} operand")
     return t, False
 
 
-def _emit(t, rows, cols, resident):
-    """A new handle over t, or a new flat list read back from it (luatl_adapter.lua:116-124)."""
-    if resident:
-        return Handle(t, rows, cols)
-    n = rows * cols
-    out = np.empty(n, np.float32)
-    call("lhip_download", out.ctypes.data, t.data, 4 * n)
-    return out.astype(np.float64).tolist()
+def _deliver(t, rows, cols, resident):
+    """A new handle over t for resident inputs, otherwise a new flat list read back from t."""
+    return Handle(t, rows, cols) if resident else _fetch_f32(t.data, rows * cols)
 
 
-def _flat64(x, n, what):
-    a = np.ascontiguousarray(np.asarray(x, dtype=np.float64).reshape(-1))
-    if a.size < n:
-        raise ValueError(f"luatl adapter: {what}: expected {n} elements, got {a.size}")
-    return a
+def _row_call(x, rows, cols, launch):
+    """launch(X, O) on a flat sequence or a handle; the output takes the input's form."""
+    X, resident = _operand(x, rows, cols, LANE_A)
+    O = Tensor.new(rows, cols) if resident else _dev_lane(LANE_C, rows, cols)
+    launch(X, O)
+    return _deliver(O, rows, cols, resident)
 
 
-def _host(op, a, m, k, b, n, rows, nb):
-    """lhip_matmul_host: the flat-table product, double in and out."""
-    ad = _flat64(a, m * k, "a")
-    bd = _flat64(b, nb, "b")
-    out = np.empty(rows * n, dtype=np.float64)
-    call("lhip_matmul_host", op, ad.ctypes.data_as(ctypes.c_void_p), bd.ctypes.data_as(ctypes.c_void_p),
-         out.ctypes.data_as(ctypes.c_void_p), m, k, n, 0)
-    return out.tolist()
+# the flat-table products through lhip_matmul_host (double in and out)
+_OPCODE = {"nn": 0, "nt": 1, "tn": 2}
+_OPNAME = ("matmul", "matmul_nt", "matmul_tn")
+
+
+def _extents(code, m, k, n):
+    return ((m * k, k * n, m * n), (m * k, n * k, m * n), (m * k, m * n, k * n))[code]
+
+
+def _doubles(x, need, what):
+    vals = np.ascontiguousarray(np.asarray(x, dtype=np.float64).reshape(-1))
+    if vals.size < need:
+        raise ValueError(f"lanternl_hip: {what} needs {need} numbers, the table holds {vals.size}")
+    return vals
+
+
+def _host_product(code, a, m, k, b, n):
+    """The product as a float64 array of its rows*cols numbers."""
+    na, nb, nc = _extents(code, m, k, n)
+    ad = _doubles(a, na, f"{_OPNAME[code]} operand a")
+    bd = _doubles(b, nb, f"{_OPNAME[code]} operand b")
+    res = np.empty(nc, dtype=np.float64)
+    call("lhip_matmul_host", code, ad.ctypes.data_as(ctypes.c_void_p), bd.ctypes.data_as(ctypes.c_void_p),
+         res.ctypes.data_as(ctypes.c_void_p), m, k, n, 0)
+    return res
 
 
 # ------------------------------------------------------------------ legacy entry points
@@ -243,55 +283,74 @@ def matmul(a, m, k, b, n):
     """a(m x k) . b(k x n) (luatl_adapter.lua:128-135): flat tables -> new flat
     list; two handles -> new handle; a handle and a table -> flat list."""
     _require()
-    if not is_handle(a) and not is_handle(b):
-        return _host(0, a, m, k, b, n, m, k * n)
-    A, ah = _as_tensor(a, m, k, "A")
-    B, bh = _as_tensor(b, k, n, "B")
-    resident = ah and bh
-    Cc = Tensor.new(m, n) if resident else _dev_scratch("C", m, n)
-    gemm_ex(A, B, Cc)
-    return _emit(Cc, m, n, resident)
+    if not (is_handle(a) or is_handle(b)):
+        return _host_product(0, a, m, k, b, n).tolist()
+    A, ra = _operand(a, m, k, LANE_A)
+    B, rb = _operand(b, k, n, LANE_B)
+    resident = ra and rb
+    out = Tensor.new(m, n) if resident else _dev_lane(LANE_C, m, n)
+    gemm_ex(A, B, out)
+    return _deliver(out, m, n, resident)
 
 
 def matmul_nt(a, m, k, b, n):
     """a(m x k) . b(n x k)^T -> new flat list of m*n (matrix.lua:597-625 semantics)."""
     _require()
-    return _host(1, a, m, k, b, n, m, n * k)
+    return _host_product(1, a, m, k, b, n).tolist()
 
 
 def matmul_tn(a, m, k, b, n):
     """a(m x k)^T . b(m x n) -> new flat list of k*n (matrix.lua:627-660 semantics)."""
     _require()
-    return _host(2, a, m, k, b, n, k, m * n)
+    return _host_product(2, a, m, k, b, n).tolist()
+
+
+def matmul_into(op, a, m, k, b, n, rd, acc):
+    """The product `op` ("nn", "nt", "tn"; shapes as in matmul / matmul_nt /
+    matmul_tn) of two flat sequences, written into the caller's flat sequence
+    ``rd``: the product itself, or ``rd + product`` in double when ``acc``.
+    ``rd`` is written only after the device call has succeeded.  Returns rd."""
+    _require()
+    code = _OPCODE.get(op)
+    if code is None:
+        raise ValueError(f'lanternl_hip.matmul_into: op must be "nn", "nt" or "tn", got {op!r}')
+    nc = _extents(code, m, k, n)[2]
+    if len(rd) < nc:
+        raise ValueError(f"lanternl_hip.matmul_into: rd holds {len(rd)} numbers, the product {nc}")
+    res = _host_product(code, a, m, k, b, n)
+    if isinstance(rd, np.ndarray):
+        if acc:
+            rd[:nc] += res
+        else:
+            rd[:nc] = res
+    else:
+        prev = np.asarray(rd[:nc], dtype=np.float64) if acc else 0.0
+        rd[:nc] = (prev + res).tolist()
+    return rd
 
 
 def rmsnorm(x, rows, cols, w=None, eps=None):
     """luatl_adapter.lua:137-145: y = x * w / rms(x) per row (w None: gain 1)."""
     _require()
-    X, xh = _as_tensor(x, rows, cols, "A")
-    W = _as_tensor(w, 1, cols, "B")[0] if w is not None else None
-    O = Tensor.new(rows, cols) if xh else _dev_scratch("C", rows, cols)
-    call("lhip_rmsnorm_ex", X.data, W.data if W else None, O.data, rows, cols, 1e-5 if eps is None else eps)
-    return _emit(O, rows, cols, xh)
+    gain = _operand(w, 1, cols, LANE_B)[0] if w is not None else None
+    e = 1e-5 if eps is None else eps
+    return _row_call(x, rows, cols, lambda X, O: call("lhip_rmsnorm_ex", X.data, gain.data if gain else None,
+                                                      O.data, rows, cols, e))
 
 
 def softmax(x, rows, cols):
     """luatl_adapter.lua:147-152: row softmax, no mask."""
     _require()
-    X, xh = _as_tensor(x, rows, cols, "A")
-    O = Tensor.new(rows, cols) if xh else _dev_scratch("C", rows, cols)
-    call("lhip_softmax_ex", X.data, None, O.data, rows, cols, 1.0, 0, 0, 0)
-    return _emit(O, rows, cols, xh)
+    return _row_call(x, rows, cols, lambda X, O: call("lhip_softmax_ex", X.data, None, O.data, rows, cols,
+                                                      1.0, 0, 0, 0))
 
 
 def softmax_causal(x, rows, cols, scale=None, group=None):
     """luatl_adapter.lua:154-159: causal row softmax of scale*x, mask restarting every `group` rows."""
     _require()
-    X, xh = _as_tensor(x, rows, cols, "A")
-    O = Tensor.new(rows, cols) if xh else _dev_scratch("C", rows, cols)
-    call("lhip_softmax_ex", X.data, None, O.data, rows, cols, 1.0 if scale is None else scale, 1,
-         group or 0, 0)
-    return _emit(O, rows, cols, xh)
+    sc = 1.0 if scale is None else scale
+    return _row_call(x, rows, cols, lambda X, O: call("lhip_softmax_ex", X.data, None, O.data, rows, cols,
+                                                      sc, 1, group or 0, 0))
 
 
 # ------------------------------------------------------------------ views and gemm_ex
@@ -479,7 +538,8 @@ def hardware():
 
 def shutdown():
     global available, reason
-    _scratch.clear()
+    for lane in list(_lanes):
+        _lanes.pop(lane).free()
     call("lhip_shutdown")
     available, reason = False, "shut down"
 
@@ -496,10 +556,9 @@ def view(ptr, rows, cols, rs, cs, bs=0):
 
 
 def cols(t, col0, w):
-    """Column slice keeping the parent's leading dimension (luatl_adapter.lua:206-209)."""
-    if is_handle(t):
-        t = t.t
-    return view(offset(t, col0), t.rows, w, t.cols, 1, 0)
+    """Column slice [col0, col0 + w) keeping the parent's leading dimension (luatl_adapter.lua:206-209)."""
+    base = t.t if is_handle(t) else t
+    return View(_base(base) + 4 * int(col0), base.rows, w, base.cols, 1, 0)
 
 
 def wrap(ptr, rows, cols_):
@@ -508,10 +567,9 @@ def wrap(ptr, rows, cols_):
 
 
 def ids(n):
-    """An int32 index buffer in f32-sized storage (luatl_adapter.lua:215-219)."""
-    h = alloc(n, 1)
-    h.is_ids = True
-    return h
+    """A zeroed device buffer for n int32 ids: an n x 1 tensor, since ids and
+    fp32 values are both 4 bytes wide (luatl_adapter.lua:215-219)."""
+    return alloc(n, 1)
 
 
 def upload_i32(t, cbuf, n):
@@ -534,10 +592,8 @@ def download_f32(ptr, cbuf, n):
 
 
 def scalar(t):
-    """One float read back from device memory (luatl_adapter.lua:236-241)."""
-    out = np.empty(1, np.float32)
-    call("lhip_download", out.ctypes.data, _base(t), 4)
-    return float(out[0])
+    """The first fp32 value of a device tensor, handle or view (a loss, a norm) (luatl_adapter.lua:236-241)."""
+    return _fetch_f32(_base(t), 1)[0]
 
 
 def mem():

@@ -6,6 +6,7 @@
 // here buffers are plain hipMalloc allocations owned by the caller (the LuaJIT
 // side frees them from an ffi.gc finaliser), and all compute work is ordered
 // on one library-owned stream.
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -443,6 +444,7 @@ LHIP_API int lhip_ktimer_start(int capacity)
     }
     kt.cap = capacity;
     kt.used = 0;
+    kt.total = 0;
     kt.on = true;
     return LHIP_OK;
 }
@@ -453,11 +455,16 @@ LHIP_API int lhip_ktimer_stop(float* ms, int capacity, int* count)
     auto& kt = lhip::ktimer();
     if (!kt.on) return fail(LHIP_E_ARG, "lhip_ktimer_stop: the timer is not on");
     kt.on = false;
-    if (count) *count = kt.used;
+    if (count) *count = kt.total;
     LHIP_CHECK_HIP(hipStreamSynchronize(st().stream), "lhip_ktimer_stop: stream sync");
-    if (ms && capacity > 0)
-        for (int i = 0; i < kt.used && i < capacity; ++i)
-            LHIP_CHECK_HIP(hipEventElapsedTime(&ms[i], kt.ev[2 * i], kt.ev[2 * i + 1]), "lhip_ktimer_stop: elapsed");
+    const int filled = (ms && capacity > 0) ? std::min(kt.used, capacity) : 0;
+    for (int i = 0; i < filled; ++i)
+        LHIP_CHECK_HIP(hipEventElapsedTime(&ms[i], kt.ev[2 * i], kt.ev[2 * i + 1]), "lhip_ktimer_stop: elapsed");
+    if (ms && kt.total > filled)
+        return fail(LHIP_E_CAPACITY,
+                    "lhip_ktimer_stop: %d kernels were launched but only %d timed (timer capacity %d, "
+                    "caller capacity %d; launches into a graph capture are never timed)",
+                    kt.total, filled, kt.cap, capacity);
     return LHIP_OK;
 }
 

@@ -61,10 +61,13 @@ State& st();
 
 // Kernel timer (lhip_ktimer_start/stop): while it is on, every launch made
 // through klaunch records its dispatch's start and end on an event pair, the
-// timestamps a kernel trace reports, for up to `cap` launches.
+// timestamps a kernel trace reports, for up to `cap` launches.  `total`
+// counts every launch made while it is on, timed or not (past the capacity,
+// or into a stream capture, where a launch is recorded, not dispatched), so
+// that stop can report launches that went untimed.
 struct KTimer {
     bool on = false;
-    int cap = 0, used = 0;
+    int cap = 0, used = 0, total = 0;
     std::vector<hipEvent_t> ev;   // 2 per launch
 };
 KTimer& ktimer();
@@ -74,7 +77,13 @@ inline void klaunch_packed(K k, dim3 g, dim3 b, unsigned sh, hipStream_t s, Tup&
 {
     void* argv[] = {static_cast<void*>(&std::get<I>(t))...};
     KTimer& kt = ktimer();
-    if (kt.on && kt.used < kt.cap) {
+    bool timed = false;
+    if (kt.on) {
+        ++kt.total;
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        timed = kt.used < kt.cap && hipStreamIsCapturing(s, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone;
+    }
+    if (timed) {
         hipEvent_t e0 = kt.ev[2 * kt.used], e1 = kt.ev[2 * kt.used + 1];
         ++kt.used;
         (void)hipExtLaunchKernel(reinterpret_cast<const void*>(k), g, b, argv, sh, s, e0, e1, 0);

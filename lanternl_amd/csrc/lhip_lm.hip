@@ -511,6 +511,10 @@ int run_step(LmModel& m, Hyper hp)
     hipStream_t s = st().stream;
     hp.gscale = m.nwin > 1 ? 1.0f / static_cast<float>(m.nwin) : 1.0f;   // optim2.scale_grads(1/n)
     if (m.use_graph) {
+        // a graph replay's kernels are not launched through klaunch, so the
+        // kernel timer could not time them (lhip_program_begin refuses too)
+        if (ktimer().on)
+            return fail(LHIP_E_UNSUPPORTED, "lm step: graph mode while the kernel timer is on");
         klaunch(set_hyper_kernel, 1, 64, 0, s, m.hyper, hp);
         if (int rc = check_launch("lm step: hyper")) return rc;
         if (!m.exec || m.graph_opt != hp.opt)

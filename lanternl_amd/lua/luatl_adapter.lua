@@ -7,8 +7,10 @@
 --      `reason`/`error`, and matmul(a, m, k, b, n), where a and b are flat
 --      tables or resident handles; two handles give a new handle, otherwise a
 --      NEW flat table (luatl_adapter.lua:102-135).  matmul_nt / matmul_tn serve
---      the transposed products with the same convention (the dispatch that
---      matrix.lua gains with the patch shown in INTEGRATION.md).
+--      the transposed products with the same convention, and
+--      matmul_into(op, a, m, k, b, n, rd, acc) serves every product that
+--      writes into a caller's table (`out`, with or without `acc`): the
+--      dispatch that matrix.lua gains with the patch shown in INTEGRATION.md.
 --    * Legacy flat calls rmsnorm(x, rows, cols, w, eps), softmax(x, rows, cols),
 --      softmax_causal(x, rows, cols, scale, group) (:137-159).
 --    * Resident calls gemm(hA, hB, hC, opts), gemm_dx, gemm_dw, add_inplace,
@@ -23,8 +25,16 @@
 --      them on the library stream, capture() records them once into a hipGraph,
 --      replay() launches it.
 --  Handles and tensors carry .t.data / .data (the device address), rows and
---  cols as the reference's do.  M.luaTL (the reference's own low-level module)
---  has no counterpart here and stays nil.
+--  cols as the reference's do.  One reference field has no counterpart:
+--  M.luaTL, the reference's own low-level module, stays nil, so callers that
+--  reach past the adapter into it (ai/gpu/gpu_transformer.lua:58-60,
+--  ai/optim/lmtrain_gpu.lua, ai/benchmarks/bench_gpu_transformer.lua:41-44)
+--  do not run on this backend.
+--
+--  Marshaling: flat tables reach the device through grow-only host lanes
+--  (cdata arrays, one per element type and operand) and grow-only device
+--  lanes (one buffer per operand), both sized to the next power of two that
+--  fits; handles are used in place.
 --
 --  Errors: every C status is checked; a failure raises
 --  "lanternl_hip[<what>]: <message> (<STATUS>)" (the reference's ck(),
@@ -185,17 +195,53 @@ if not ok_tnew then tnew = function() return {} end end
 
 local f64_ct = ffi.typeof("double[?]")
 local f32_ct = ffi.typeof("float[?]")
-local i32_ct = ffi.typeof("int32_t[?]")
 
---  cached host staging (no per-call cdata churn, as luatl_adapter.lua:24-32)
-local stage, stage_n = {}, {}
-local function host_buf(ct, slot, n)
-    local key = slot .. tostring(ct)
-    if not stage[key] or stage_n[key] < n then
-        stage[key] = ct(n)
-        stage_n[key] = n
+--  HOST LANES.  Marshaling goes through one grow-only cdata array per element
+--  type and operand lane (LANE_A / LANE_B first and second operand, LANE_C the
+--  result).  A lane grows to the next power of two that fits and never
+--  shrinks, so calls of varied shapes settle on a handful of allocations.
+local LANE_A, LANE_B, LANE_C = 1, 2, 3
+
+local function pow2_at_least(n)
+    local c = 256
+    while c < n do c = c * 2 end
+    return c
+end
+
+local HostLane = {}
+HostLane.__index = HostLane
+local function host_lane(ct) return setmetatable({ ct = ct, cap = 0, buf = nil }, HostLane) end
+function HostLane:reserve(n)
+    if n > self.cap then
+        self.cap = pow2_at_least(n)
+        self.buf = self.ct(self.cap)
     end
-    return stage[key]
+    return self.buf
+end
+
+local lanes = {
+    f64 = { host_lane(f64_ct), host_lane(f64_ct), host_lane(f64_ct) },
+    f32 = { host_lane(f32_ct), host_lane(f32_ct), host_lane(f32_ct) },
+}
+
+-- numbers [1..n] of a Lua table into elements [0..n-1] of a cdata array
+local function pack(dst, src, n)
+    for i = 0, n - 1 do dst[i] = src[i + 1] end
+    return dst
+end
+
+-- elements [0..n-1] of a cdata array as a new 1-based Lua table
+local function unpack_new(src, n)
+    local t = tnew(n, 0)
+    for i = 1, n do t[i] = src[i - 1] end
+    return t
+end
+
+local function count_or_fail(tbl, need, what, level)
+    local have = type(tbl) == "table" and #tbl or -1
+    if have < need then
+        error(("lanternl_hip: %s needs %d numbers, the table holds %d"):format(what, need, have), level + 1)
+    end
 end
 
 --  TENSORS: a device fp32 matrix { data, rows, cols, dtype, nelem, nbytes } --
@@ -222,6 +268,34 @@ function Tensor:free()
     self.owner, self.data = nil, nil
 end
 
+-- device <-> Lua table, fp32 on the device, through a host lane
+local function put_f32(dptr_, src, n, lane)
+    local buf = pack(lanes.f32[lane]:reserve(n), src, n)
+    ck(C.lhip_upload(dptr_, buf, n * 4), "upload")
+end
+
+local function fetch_f32(dptr_, n, lane)
+    local buf = lanes.f32[lane]:reserve(n)
+    ck(C.lhip_download(buf, dptr_, n * 4), "download")
+    return unpack_new(buf, n)
+end
+
+--  DEVICE LANES: the flat-table calls' device operands, one grow-only buffer
+--  per lane (the same policy as the host lanes).  Each call gets a
+--  non-owning tensor shaped for it over its lane's buffer.
+local dev_lanes = {}
+local function dev_lane(lane, rows, cols)
+    local need = math.max(rows * cols, 1)
+    local store = dev_lanes[lane]
+    if store == nil or store.nelem < need then
+        if store ~= nil then store:free() end
+        store = new_tensor(pow2_at_least(need), 1)
+        dev_lanes[lane] = store
+    end
+    return setmetatable({ data = store.data, rows = rows, cols = cols, dtype = F32, nelem = rows * cols,
+                          nbytes = rows * cols * 4 }, Tensor)
+end
+
 --  HANDLES (luatl_adapter.lua:46-101): a persistent GPU tensor exposed to lanternl
 local Handle = {}
 Handle.__index = Handle
@@ -235,13 +309,17 @@ local function new_handle(t, rows, cols)
 end
 M.new_handle = new_handle
 
---- Upload a flat Lua array once and keep it resident (luatl_adapter.lua:63-73).
+--- Upload a flat Lua array once and keep it resident (luatl_adapter.lua:63-73):
+--- the table must hold exactly rows*cols numbers.
 function M.pin(flat, rows, cols)
     local n = rows * cols
-    if #flat ~= n then
-        error(("luatl.pin: %d elements != %dx%d"):format(#flat, rows, cols), 2)
+    if type(flat) ~= "table" or #flat ~= n then
+        error(("lanternl_hip.pin: a %dx%d matrix takes exactly %d numbers, the table holds %s")
+              :format(rows, cols, n, type(flat) == "table" and tostring(#flat) or type(flat)), 2)
     end
-    return new_handle(new_tensor(rows, cols), rows, cols):upload(flat)
+    local h = new_handle(new_tensor(rows, cols), rows, cols)
+    put_f32(h.t.data, flat, n, LANE_A)
+    return h
 end
 
 --- A resident zero tensor (activations, grads, optimizer state) (:75-78).
@@ -249,79 +327,70 @@ function M.alloc(rows, cols)
     return new_handle(new_tensor(rows, cols), rows, cols):zero()
 end
 
-function Handle:toflat()
-    local n = self.rows * self.cols
-    local buf = host_buf(f32_ct, "dl", n)
-    ck(C.lhip_download(buf, self.t.data, n * 4), "download")
-    local out = tnew(n, 0)
-    for i = 1, n do out[i] = buf[i - 1] end
-    return out
-end
+function Handle:toflat() return fetch_f32(self.t.data, self.rows * self.cols, LANE_C) end
 
 function Handle:upload(flat)
     local n = self.rows * self.cols
-    if #flat < n then error(("luatl.upload: %d elements < %dx%d"):format(#flat, self.rows, self.cols), 2) end
-    local buf = host_buf(f32_ct, "ul", n)
-    for i = 1, n do buf[i - 1] = flat[i] end
-    ck(C.lhip_upload(self.t.data, buf, n * 4), "upload")
+    count_or_fail(flat, n, ("Handle:upload into %dx%d"):format(self.rows, self.cols), 2)
+    put_f32(self.t.data, flat, n, LANE_A)
     return self
 end
 
 function Handle:zero() ck(C.lhip_zero(self.t.data, self.rows * self.cols * 4), "zero") return self end
-function Handle:free() if self.t then self.t:free() self.t = nil end end
+function Handle:free()
+    local t = self.t
+    self.t = nil
+    if t ~= nil then t:free() end
+end
 function Handle:tensor() return self.t end
 function Handle:shape() return self.rows, self.cols end
 
---  device scratch for the flat-table calls, keyed by "slot:rows x cols" (:34-44)
-local scratch = {}
-local function dev_scratch(slot, rows, cols)
-    local key = slot .. ":" .. rows .. "x" .. cols
-    local t = scratch[key]
-    if not t then
-        t = new_tensor(rows, cols)
-        scratch[key] = t
-    end
-    return t
-end
-
---  a handle's tensor, or a flat table uploaded to scratch (:102-114)
-local function as_tensor(x, rows, cols, slot)
+-- a handle's tensor (resident), or a flat table copied into a device lane
+local function operand(x, rows, cols, lane)
     if is_handle(x) then return x.t, true end
     local n = rows * cols
-    if #x < n then
-        error(("luatl adapter: expected %d elements, got %d"):format(n, #x), 3)
-    end
-    local buf = host_buf(f32_ct, slot, n)
-    for i = 1, n do buf[i - 1] = x[i] end
-    local t = dev_scratch(slot, rows, cols)
-    ck(C.lhip_upload(t.data, buf, n * 4), "upload")
+    count_or_fail(x, n, ("a %dx%d operand"):format(rows, cols), 2)
+    local t = dev_lane(lane, rows, cols)
+    put_f32(t.data, x, n, lane)
     return t, false
 end
 
---  a new handle over t, or a new flat table read back from it (:116-124)
-local function emit(t, rows, cols, resident)
+-- the call's result: a new handle over t when the inputs were resident,
+-- otherwise a new flat table read back from t
+local function deliver(t, rows, cols, resident)
     if resident then return new_handle(t, rows, cols) end
-    local n = rows * cols
-    local buf = host_buf(f32_ct, "out", n)
-    ck(C.lhip_download(buf, t.data, n * 4), "download")
-    local out = tnew(n, 0)
-    for i = 1, n do out[i] = buf[i - 1] end
-    return out
+    return fetch_f32(t.data, rows * cols, LANE_C)
 end
 
---  the flat-table product through lhip_matmul_host (double in and out)
-local function host_gemm(op, a, m, k, b, n, na, nb, nc, what)
-    if #a < na then error(("lanternl_hip: %s: a has %d elements, expected %d"):format(what, #a, na), 3) end
-    if #b < nb then error(("lanternl_hip: %s: b has %d elements, expected %d"):format(what, #b, nb), 3) end
-    local A = host_buf(f64_ct, "a", na)
-    local B = host_buf(f64_ct, "b", nb)
-    local Cb = host_buf(f64_ct, "c", nc)
-    for i = 1, na do A[i - 1] = a[i] end
-    for i = 1, nb do B[i - 1] = b[i] end
-    ck(C.lhip_matmul_host(op, A, B, Cb, m, k, n, 0), what)
-    local out = tnew(nc, 0)
-    for i = 1, nc do out[i] = Cb[i - 1] end
-    return out
+-- run `launch(X, O)` on a flat table or a handle; the output takes the input's form
+local function row_call(x, rows, cols, launch)
+    local X, resident = operand(x, rows, cols, LANE_A)
+    local O = resident and new_tensor(rows, cols) or dev_lane(LANE_C, rows, cols)
+    launch(X, O)
+    return deliver(O, rows, cols, resident)
+end
+
+--  THE FLAT-TABLE PRODUCTS through lhip_matmul_host (double in and out).
+--  op 0 = a(m x k).b(k x n), 1 = a(m x k).b(n x k)^T, 2 = a(m x k)^T.b(m x n)
+local OPCODE = { nn = 0, nt = 1, tn = 2 }
+local OPNAME = { [0] = "matmul", [1] = "matmul_nt", [2] = "matmul_tn" }
+
+local function extents(code, m, k, n)
+    if code == 0 then return m * k, k * n, m * n end
+    if code == 1 then return m * k, n * k, m * n end
+    return m * k, m * n, k * n
+end
+
+-- the product in the result lane (a cdata double array) and its element count
+local function host_product(code, a, m, k, b, n)
+    local na, nb, nc = extents(code, m, k, n)
+    count_or_fail(a, na, OPNAME[code] .. " operand a", 3)
+    count_or_fail(b, nb, OPNAME[code] .. " operand b", 3)
+    local A = pack(lanes.f64[LANE_A]:reserve(na), a, na)
+    local B = pack(lanes.f64[LANE_B]:reserve(nb), b, nb)
+    local R = lanes.f64[LANE_C]:reserve(nc)
+    ck(C.lhip_matmul_host(code, A, B, R, m, k, n, 0), OPNAME[code])
+    return R, nc
 end
 
 --  STRIDE VIEWS AND gemm_ex (luaTL_train.lua:113-172)
@@ -368,49 +437,69 @@ end
 
 --  LEGACY-COMPATIBLE ENTRY POINTS (signatures unchanged, luatl_adapter.lua:126-159)
 
+--- a(m x k) . b(k x n): two flat tables -> a new flat table of m*n numbers
+--- (the registry's contract, matrix.lua:178-202); two handles -> a new handle;
+--- a handle and a table -> a new flat table.
 function M.matmul(a, m, k, b, n)
-    if not is_handle(a) and not is_handle(b) then
-        return host_gemm(0, a, m, k, b, n, m * k, k * n, m * n, "matmul")
+    if not (is_handle(a) or is_handle(b)) then
+        return unpack_new(host_product(0, a, m, k, b, n))
     end
-    local A, ah = as_tensor(a, m, k, "A")
-    local B, bh = as_tensor(b, k, n, "B")
-    local resident = ah and bh
-    local Cc = resident and new_tensor(m, n) or dev_scratch("C", m, n)
-    M.gemm_ex(A, B, Cc)
-    return emit(Cc, m, n, resident)
+    local A, ra = operand(a, m, k, LANE_A)
+    local B, rb = operand(b, k, n, LANE_B)
+    local resident = ra and rb
+    local out = resident and new_tensor(m, n) or dev_lane(LANE_C, m, n)
+    M.gemm_ex(A, B, out)
+    return deliver(out, m, n, resident)
 end
 
---  a(m x k) . b(n x k)^T -> m*n numbers (matrix.matmul_nt, matrix.lua:597-625)
-function M.matmul_nt(a, m, k, b, n)
-    return host_gemm(1, a, m, k, b, n, m * k, n * k, m * n, "matmul_nt")
-end
+--- a(m x k) . b(n x k)^T -> a new flat table of m*n numbers (matrix.matmul_nt, matrix.lua:597-625)
+function M.matmul_nt(a, m, k, b, n) return unpack_new(host_product(1, a, m, k, b, n)) end
 
---  a(m x k)^T . b(m x n) -> k*n numbers (matrix.matmul_tn, matrix.lua:627-660)
-function M.matmul_tn(a, m, k, b, n)
-    return host_gemm(2, a, m, k, b, n, m * k, m * n, k * n, "matmul_tn")
+--- a(m x k)^T . b(m x n) -> a new flat table of k*n numbers (matrix.matmul_tn, matrix.lua:627-660)
+function M.matmul_tn(a, m, k, b, n) return unpack_new(host_product(2, a, m, k, b, n)) end
+
+--- The product `op` ("nn", "nt" or "tn", shapes as in matmul / matmul_nt /
+--- matmul_tn) of two flat tables, written into the caller's flat table rd:
+--- rd = product when acc is false, rd = rd + product (in double) when acc is
+--- true.  This is what matrix.multiply / matmul_nt / matmul_tn call when they
+--- are given `out` (the autograd backward's grad_of(x) with acc = true,
+--- tensor2.lua:206-211,222-227).  rd is written only after the device call
+--- has succeeded, so an error leaves it untouched.  Returns rd.
+function M.matmul_into(op, a, m, k, b, n, rd, acc)
+    local code = OPCODE[op]
+    if code == nil then
+        error(("lanternl_hip.matmul_into: op must be \"nn\", \"nt\" or \"tn\", got %s"):format(tostring(op)), 2)
+    end
+    local nc = select(3, extents(code, m, k, n))
+    if type(rd) ~= "table" or #rd < nc then
+        error(("lanternl_hip.matmul_into: rd must be a flat table of %d numbers"):format(nc), 2)
+    end
+    local R = host_product(code, a, m, k, b, n)
+    if acc then
+        for i = 1, nc do rd[i] = rd[i] + R[i - 1] end
+    else
+        for i = 1, nc do rd[i] = R[i - 1] end
+    end
+    return rd
 end
 
 function M.rmsnorm(x, rows, cols, w, eps)
-    local X, xh = as_tensor(x, rows, cols, "A")
-    local W = nil
-    if w then W = (as_tensor(w, 1, cols, "B")) end
-    local O = xh and new_tensor(rows, cols) or dev_scratch("C", rows, cols)
-    ck(C.lhip_rmsnorm_ex(X.data, W and W.data or nil, O.data, rows, cols, eps or 1e-5), "rmsnorm")
-    return emit(O, rows, cols, xh)
+    local gain = w and (operand(w, 1, cols, LANE_B)) or nil
+    return row_call(x, rows, cols, function(X, O)
+        ck(C.lhip_rmsnorm_ex(X.data, gain and gain.data or nil, O.data, rows, cols, eps or 1e-5), "rmsnorm")
+    end)
 end
 
 function M.softmax(x, rows, cols)
-    local X, xh = as_tensor(x, rows, cols, "A")
-    local O = xh and new_tensor(rows, cols) or dev_scratch("C", rows, cols)
-    ck(C.lhip_softmax_ex(X.data, nil, O.data, rows, cols, 1.0, 0, 0, 0), "softmax")
-    return emit(O, rows, cols, xh)
+    return row_call(x, rows, cols, function(X, O)
+        ck(C.lhip_softmax_ex(X.data, nil, O.data, rows, cols, 1.0, 0, 0, 0), "softmax")
+    end)
 end
 
 function M.softmax_causal(x, rows, cols, scale, group)
-    local X, xh = as_tensor(x, rows, cols, "A")
-    local O = xh and new_tensor(rows, cols) or dev_scratch("C", rows, cols)
-    ck(C.lhip_softmax_ex(X.data, nil, O.data, rows, cols, scale or 1.0, 1, group or 0, 0), "softmax_causal")
-    return emit(O, rows, cols, xh)
+    return row_call(x, rows, cols, function(X, O)
+        ck(C.lhip_softmax_ex(X.data, nil, O.data, rows, cols, scale or 1.0, 1, group or 0, 0), "softmax_causal")
+    end)
 end
 
 --  RESIDENT-MODE PRIMITIVES (luatl_adapter.lua:161-187)
@@ -527,8 +616,8 @@ end
 
 --- Column slice [col0, col0 + w) keeping the parent's leading dimension.
 function M.cols(t, col0, w)
-    if is_handle(t) then t = t.t end
-    return M.view(M.offset(t, col0), t.rows, w, t.cols, 1, 0)
+    local base = is_handle(t) and t.t or t
+    return M.view(ffi.cast("float*", base.data) + col0, base.rows, w, base.cols, 1, 0)
 end
 
 --- Non-owning tensor over a raw device pointer.
@@ -537,23 +626,16 @@ function M.wrap(ptr, rows, cols)
                           nelem = rows * cols, nbytes = rows * cols * 4 }, Tensor)
 end
 
---- int32 index buffer backed by f32-sized storage (4 bytes either way).
-function M.ids(n)
-    local h = M.alloc(n, 1)
-    h.is_ids = true
-    return h
-end
+--- A zeroed device buffer for n int32 ids: an n x 1 tensor, since ids and
+--- fp32 values are both 4 bytes wide.
+function M.ids(n) return M.alloc(n, 1) end
 
 function M.upload_i32(t, cbuf, n) ck(C.lhip_upload(dptr(t), cbuf, n * 4), "adapter.upload_i32") end
 function M.download_i32(t, cbuf, n) ck(C.lhip_download(cbuf, dptr(t), n * 4), "adapter.download_i32") end
 function M.download_f32(ptr, cbuf, n) ck(C.lhip_download(cbuf, dptr(ptr), n * 4), "adapter.download_f32") end
 
---- One float read back from a device tensor (the loss / grad norm).
-local one = ffi.new("float[1]")
-function M.scalar(t)
-    ck(C.lhip_download(one, dptr(t), 4), "adapter.scalar")
-    return one[0]
-end
+--- The first fp32 value of a device tensor, handle or view (a loss, a norm).
+function M.scalar(t) return fetch_f32(dptr(t), 1, LANE_C)[1] end
 
 --  PROGRAM: luaTL.Program's op list (ai/gpu/luaTL_train.lua:332-632) over this
 --  library.  Each op method queues one library call; run(keep) issues the
@@ -808,7 +890,10 @@ function Prog:free_graph()
 end
 
 function M.shutdown()
-    for k in pairs(scratch) do scratch[k] = nil end
+    for lane, store in pairs(dev_lanes) do
+        store:free()
+        dev_lanes[lane] = nil
+    end
     C.lhip_shutdown()
     M.available = false
     M.reason = "shut down"

@@ -6,12 +6,27 @@ backends :127-135, reset_backends :137-142, use :144-167, backend_failed
 three products ``multiply`` (:541-595), ``matmul_nt`` (:597-625) and
 ``matmul_tn`` (:627-660).
 
-What is new relative to the reference: ``matmul_nt`` and ``matmul_tn`` are
-offloaded too, under the same gate as ``multiply`` (no ``out``, no ``acc``,
-accel enabled, not forced to "lua", and m*k*n >= threshold or a forced
-backend), trying each backend's ``matmul_nt`` / ``matmul_tn``.  The CPU loops
-below the threshold keep the reference's order (i-p-j with the a==0 skip for
-multiply and matmul_tn; a p-ordered dot product for matmul_nt).
+What is new relative to the reference: every product is offloaded above
+the threshold, including the calls that write into a caller's matrix.
+  * ``out`` absent, ``acc`` off: the backend entry ``matmul`` / ``matmul_nt`` /
+    ``matmul_tn`` returns a NEW flat table, adopted as the result's data
+    (``multiply``'s rule, matrix.lua:571-585, carried over to the transposed
+    products, which are pure Lua in the reference, matrix.lua:597-660).
+  * ``out`` given (the autograd backward, tensor2.lua:206-211,222-227, passes
+    ``grad_of(x)`` and ``acc = true``): the backend entry
+    ``matmul_into(op, a, m, k, b, n, rd, acc)`` computes the product on the
+    device and then, on the host in double, stores it into ``rd = out.data``
+    (acc off) or adds it to ``rd`` (acc on), the Lua-side add of the Lua
+    loops.  ``rd`` is touched only after the device call has succeeded, so a
+    failed call leaves it as it was and the Lua loop that follows does the
+    whole product once.
+  * ``out`` absent with ``acc`` on targets a fresh zero matrix, so it is the
+    plain product and takes the first rule.
+A backend without the entry a call needs is skipped for that call, not
+counted as failed.  The gate is otherwise the reference's: accel enabled,
+not forced to "lua", and m*k*n >= threshold or a forced backend.  The CPU
+loops below the threshold keep the reference's order (i-p-j with the a==0
+skip for multiply and matmul_tn; a p-ordered dot product for matmul_nt).
 
 Matrices are ``Matrix(rows, cols, data)`` with ``data`` a flat row-major
 sequence (a list or a 1-D float64 numpy array); 0-based, unlike Lua.
@@ -129,12 +144,13 @@ def _is_number(v):
     return isinstance(v, (int, float, np.floating, np.integer)) and not isinstance(v, bool)
 
 
-def _try_backend(entry, fn_name, ad, m, k, bd, n, last):
+def _try_backend(entry, fn_name, args, last):
+    """pcall one backend entry and validate its flat result (matrix.lua:178-202)."""
     fn = getattr(entry["module"], fn_name, None)
     if not callable(fn):
-        return None  # backend does not serve this product: not a failure
+        return None  # backend does not serve this call: not a failure
     try:
-        res = fn(ad, m, k, bd, n)
+        res = fn(*args)
     except Exception as e:  # noqa: BLE001 -- counted, as the Lua pcall does
         msg = str(e).splitlines()[0] if str(e) else type(e).__name__
         _backend_failed(entry, msg)
@@ -153,18 +169,29 @@ def _try_backend(entry, fn_name, ad, m, k, bd, n, last):
     return res
 
 
+# op names of the into-entry, per product
+_OPS = {"matmul": "nn", "matmul_nt": "nt", "matmul_tn": "tn"}
+
+
 def _dispatch(fn_name, who, ad, m, k, bd, n, last, out, acc):
-    """Shared gate of matrix.lua:571-590; returns the backend result or None."""
+    """The gate of matrix.lua:571-590, extended to every product and to `out`.
+
+    Returns the flat data the result adopts (a new table, or ``out.data``
+    written in place by ``matmul_into``), or None for the Lua loops."""
     global last_backend
     if not _backends:
         reset_backends()
     force = accel.get("force")
-    if out is None and not acc and accel.get("enabled") and force != "lua":
+    if accel.get("enabled") and force != "lua":
         work = m * k * n
         if force is not None or work >= (accel.get("threshold") or 0):
+            if out is None:
+                name, args = fn_name, (ad, m, k, bd, n)
+            else:
+                name, args = "matmul_into", (_OPS[fn_name], ad, m, k, bd, n, out.data, bool(acc))
             for e in _backends:
                 if e["available"] and (force is None or force == e["name"]):
-                    res = _try_backend(e, fn_name, ad, m, k, bd, n, last)
+                    res = _try_backend(e, name, args, last)
                     if res is not None:
                         last_backend = e["name"]
                         return res

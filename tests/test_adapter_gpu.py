@@ -77,8 +77,18 @@ def test_reference_adapter_test_replayed():
 
 
 def test_pin_rejects_a_wrong_element_count():
-    with pytest.raises(ValueError, match="elements"):
+    """luatl_adapter.lua:63-67: pin takes exactly rows*cols numbers; short and
+    long tables are both refused, and so is a short operand of a flat call."""
+    with pytest.raises(ValueError, match="takes exactly 4 numbers, the table holds 3"):
         ad.pin([1, 2, 3], 2, 2)
+    with pytest.raises(ValueError, match="takes exactly 4 numbers, the table holds 5"):
+        ad.pin([1, 2, 3, 4, 5], 2, 2)
+    with pytest.raises(ValueError, match="needs 6 numbers, the table holds 4"):
+        ad.matmul([1, 2, 3, 4], 2, 3, [1, 0, 0, 1, 1, 1], 2)
+    h = ad.pin([1.0, 2.0, 3.0, 4.0], 2, 2)
+    with pytest.raises(ValueError, match="needs 4 numbers"):
+        h.upload([1.0])
+    h.free()
 
 
 # ----------------------------------------------------------- legacy flat calls

@@ -37,7 +37,9 @@ def test_one_duration_per_kernel_in_launch_order():
     assert t[1] > 8 * max(t[0], t[2])
 
 
-def test_capacity_limits_the_timed_launches_and_count_reports_them():
+def test_capacity_limits_the_timed_launches_and_stop_reports_the_rest():
+    """Launches past the capacity run untimed; stop counts them all and returns
+    LHIP_E_CAPACITY, so a caller cannot sum a partial list unknowingly."""
     announce("ktimer capacity")
     a = device.Buffer.from_numpy(np.ones((32, 32), np.float32))
     c = device.Buffer((32, 32))
@@ -46,9 +48,37 @@ def test_capacity_limits_the_timed_launches_and_count_reports_them():
         kernels.sgemm(a, a, c)
     ms = (ctypes.c_float * 2)()
     n = ctypes.c_int()
-    call("lhip_ktimer_stop", ms, 2, ctypes.byref(n))
-    assert n.value == 2 and ms[0] > 0 and ms[1] > 0
+    with pytest.raises(LanternlHipError, match="5 kernels were launched but only 2 timed"):
+        call("lhip_ktimer_stop", ms, 2, ctypes.byref(n))
+    assert n.value == 5 and ms[0] > 0 and ms[1] > 0
     np.testing.assert_array_equal(c.download(), np.full((32, 32), 32, np.float32))
+    # the Python wrapper raises instead of returning a short list
+    with pytest.raises(LanternlHipError, match="only 3 timed"):
+        device.kernel_times(lambda: [kernels.sgemm(a, a, c) for _ in range(4)], capacity=3)
+    # within the capacity: one entry per launch, stop returns OK
+    assert len(device.kernel_times(lambda: [kernels.sgemm(a, a, c) for _ in range(3)], capacity=3)) == 3
+
+
+def test_graph_mode_lm_step_refused_while_the_timer_is_on():
+    """A graph replay's kernels cannot be timed, so a graph-mode step is refused
+    (as lhip_program_begin is) rather than leaving the timer to count captured
+    launches as dispatches."""
+    announce("ktimer vs lm graph step")
+    from lanternl_amd import lmtrain
+    step = lmtrain.GpuLMStep(vocab=32, dim=16, layers=1, heads=2, ffn=32, batch=2, seq=8)
+    rng = np.random.default_rng(0)
+    step.set_params(rng.normal(0, 0.02, step.n).astype(np.float32))
+    step.set_batch(rng.integers(0, 32, (2, 8)), rng.integers(0, 32, (2, 8)))
+    step.use_graph(True)
+    call("lhip_ktimer_start", 64)
+    try:
+        with pytest.raises(LanternlHipError, match="graph mode while the kernel timer is on"):
+            step.step(lr=0.1)
+    finally:
+        call("lhip_ktimer_stop", None, 0, None)
+    step.step(lr=0.1)          # timer off: the graph step runs
+    device.sync()
+    step.close()
 
 
 def test_timer_and_program_recording_exclude_each_other():

@@ -87,14 +87,34 @@ def test_handle_methods_and_program_methods_match():
     assert not wrong, f"Program methods differ (mine, reference): {wrong}"
 
 
+# Reference module fields with no counterpart here.  `luaTL` is the reference's
+# own low-level CUDA module (luatl_adapter.lua:17); callers that reach into it
+# (gpu_transformer.lua:58-60, bench_gpu_transformer.lua:41) are not served.
+ABSENT_FIELDS = {"luaTL"}
+
+
 def test_module_sets_the_reference_fields():
     lua = open(ADAPTER).read()
     ctor = re.search(r"local M\s*=\s*\{([^}]*)\}", lua).group(1)
-    fields = set(re.findall(r"\bM\.(\w+)\s*=[^=]", lua)) | set(re.findall(r"(\w+)\s*=", ctor))
-    missing = sorted(set(SIGS["fields"]) - fields)
+    # only assignments of a value count: `M.x = nil` does not set the field
+    fields = set(re.findall(r"\bM\.(\w+)\s*=(?!=)[ \t]*(?![ \t]|nil\b)", lua)) | set(re.findall(r"(\w+)\s*=", ctor))
+    missing = sorted(set(SIGS["fields"]) - ABSENT_FIELDS - fields)
     assert not missing, missing
+    assert ABSENT_FIELDS <= set(SIGS["fields"])
+    header = lua[:lua.index("local M =")]
+    for f in ABSENT_FIELDS:
+        assert f not in fields
+        assert f"M.{f}" in header and "no counterpart" in header, f"absent field {f} is not documented"
     assert "reason" in fields      # matrix.lua:39-40 reads mod.reason
     assert re.search(r'name\s*=\s*"luatl"', ctor) and re.search(r"priority\s*=\s*100", ctor)
+
+
+def test_matmul_into_entry_declared_in_both_modules():
+    """The entry the registry's out=/acc dispatch calls (matrix.lua patch in INTEGRATION.md)."""
+    mine = _lua_sigs(open(ADAPTER).read(), "M")
+    assert mine["matmul_into"] == ["op", "a", "m", "k", "b", "n", "rd", "acc"]
+    from lanternl_amd import backend as B
+    assert list(inspect.signature(B.matmul_into).parameters) == mine["matmul_into"]
 
 
 def test_python_mirror_has_the_same_calls():

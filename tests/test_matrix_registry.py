@@ -58,11 +58,99 @@ def test_threshold_gate_and_fallback_equals_lua_loops():
     big_a, big_b = rng.uniform(-1, 1, (16, 16)), rng.uniform(-1, 1, (16, 16))   # 4096 >= 4096
     MX.multiply(M(big_a), M(big_b))
     assert MX.last_backend == "luatl_adapter" and seen == [(16, 16, 16)]
-    # out= or acc= never offloads
+    # a backend without matmul_into is skipped (not failed) for out=: the Lua loop runs
     out = M(np.ones((16, 16)))
     MX.multiply(M(big_a), M(big_b), out=out, acc=True)
-    assert MX.last_backend == "lua" and len(seen) == 1
+    assert MX.last_backend == "lua" and len(seen) == 1 and MX.backends()[0]["errors"] == 0
     np.testing.assert_array_equal(out.to_numpy(), O.mm(big_a, big_b, out=np.ones((16, 16)), acc=True))
+
+
+def _into_stub(log):
+    """A backend whose matmul_into computes in float64 and follows the contract:
+    rd = product, or rd += product with acc, written in place; returns rd."""
+    def into(op, a, m, k, b, n, rd, acc):
+        log.append((op, m, k, n, acc))
+        A = np.asarray(a, dtype=np.float64).reshape(m, k)
+        if op == "nn":
+            P = A @ np.asarray(b, dtype=np.float64).reshape(k, n)
+        elif op == "nt":
+            P = A @ np.asarray(b, dtype=np.float64).reshape(n, k).T
+        else:
+            P = A.T @ np.asarray(b, dtype=np.float64).reshape(m, n)
+        P = P.reshape(-1)
+        if acc:
+            rd[:] = np.asarray(rd) + P
+        else:
+            rd[:] = P
+        return rd
+    return stub(matmul=lambda *a: None, matmul_into=into)
+
+
+@pytest.mark.parametrize("acc", [True, False])
+def test_out_and_acc_offload_through_matmul_into(acc):
+    """The backward's calls (tensor2.lua:206-211,222-227) pass out=grad_of(x), acc=true:
+    above the threshold all three products go to the backend's matmul_into and land
+    in out.data; the result equals the Lua loops on the same operands."""
+    log = []
+    MX.reset_backends({"luatl_adapter": _into_stub(log)})
+    rng = np.random.default_rng(3)
+    g = rng.uniform(-1, 1, (16, 24)); w = rng.uniform(-1, 1, (20, 24)); x = rng.uniform(-1, 1, (16, 20))
+    base_x = rng.uniform(-1, 1, (16, 20)); base_w = rng.uniform(-1, 1, (20, 24))
+    # BACKWARD.matmul for y = x.w: gx += g.w^T, gw += x^T.g
+    gx, gw = M(base_x), M(base_w)
+    data_x = gx.data
+    MX.matmul_nt(M(g), M(w), out=gx, acc=acc)
+    assert MX.last_backend == "luatl_adapter" and gx.data is data_x     # written in place
+    MX.matmul_tn(M(x), M(g), out=gw, acc=acc)
+    assert MX.last_backend == "luatl_adapter"
+    # BACKWARD.matmul_nt for s = x.w^T (w 24x20 here): gx += g.w, gw += g^T.x
+    s_g = rng.uniform(-1, 1, (16, 24)); w2 = rng.uniform(-1, 1, (24, 20))
+    gx2 = M(base_x)
+    MX.multiply(M(s_g), M(w2), out=gx2, acc=acc)
+    assert MX.last_backend == "luatl_adapter"
+    assert [e[0] for e in log] == ["nt", "tn", "nn"] and all(e[4] == acc for e in log)
+    MX.use("lua")
+    try:
+        rx, rw, rx2 = M(base_x), M(base_w), M(base_x)
+        MX.matmul_nt(M(g), M(w), out=rx, acc=acc)
+        MX.matmul_tn(M(x), M(g), out=rw, acc=acc)
+        MX.multiply(M(s_g), M(w2), out=rx2, acc=acc)
+    finally:
+        MX.use("auto")
+    for got, want in ((gx, rx), (gw, rw), (gx2, rx2)):
+        np.testing.assert_allclose(got.to_numpy(), want.to_numpy(), rtol=1e-12, atol=1e-12)
+
+
+def test_matmul_into_failure_falls_back_once_and_counts():
+    """A failing matmul_into is counted like a failing matmul; the Lua loop then
+    does the whole product once into out (the backend leaves rd untouched on error)."""
+    def boom(*a):
+        raise RuntimeError("into exploded")
+    MX.reset_backends({"luatl_adapter": stub(matmul=lambda *a: None, matmul_into=boom)})
+    a = np.ones((16, 16)); out = M(np.full((16, 16), 2.0))
+    MX.multiply(M(a), M(a), out=out, acc=True)
+    assert MX.last_backend == "lua"
+    np.testing.assert_array_equal(out.to_numpy(), np.full((16, 16), 18.0))
+    e = MX.backends()[0]
+    assert e["errors"] == 1 and e["last_error"] == "into exploded"
+
+
+def test_below_threshold_out_stays_in_lua_and_acc_without_out_is_plain():
+    log, seen = [], []
+    st = _into_stub(log)
+
+    def mm(a, m, k, b, n):
+        seen.append((m, k, n))
+        return list((np.asarray(a).reshape(m, k) @ np.asarray(b).reshape(k, n)).ravel())
+    st.matmul = mm
+    MX.reset_backends({"luatl_adapter": st})
+    small = np.ones((4, 8)); out = M(np.zeros((4, 4)))
+    MX.matmul_nt(M(small), M(small), out=out, acc=True)            # 4*8*4 < 4096
+    assert MX.last_backend == "lua" and not log
+    big = np.ones((16, 16))
+    r = MX.multiply(M(big), M(big), acc=True)                       # out=nil: fresh zeros, plain entry
+    assert MX.last_backend == "luatl_adapter" and seen == [(16, 16, 16)] and not log
+    np.testing.assert_array_equal(r.to_numpy(), np.full((16, 16), 16.0))
 
 
 def test_transposed_cpu_loops_match_oracle_exactly():

@@ -82,12 +82,20 @@ def test_noalloc_matches_sgemm_on_shrinking_calls():
 def test_noalloc_refuses_oversized_split_before_launch():
     device.init(0)
     # 4096 x 3840 x 4096: 240 tiles of 256x256, split in two K slices of
-    # 4096x3840 floats each (126 MB of partials) -- beyond the 64 MiB array.
-    # Refused on the host: the operand pointers are never dereferenced.
-    dummy = device.Buffer((4,))
-    rc = lib().lhip_sgemm_noalloc(0, 0, 4096, 3840, 4096, 1.0, dummy.ptr, 4096, dummy.ptr, 3840, 0.0,
-                                  dummy.ptr, 3840)
-    assert rc == -7, rc
+    # 4096x3840 floats each (126 MB of partials) on 256 CUs -- beyond the
+    # 64 MiB array, so the host refuses it before anything launches.  The
+    # operands are allocated at their real sizes (A 64 MiB, B and C 60 MiB),
+    # so that if a plan on another CU count needs no split (nothing to
+    # refuse), the call still runs in bounds and the assertion fails on the
+    # return code instead of a memory fault.
+    m, n, k = 4096, 3840, 4096
+    A, B, Cc = device.Buffer((m, k)), device.Buffer((k, n)), device.Buffer((m, n))
+    for buf in (A, B, Cc):
+        buf.zero()
+    device.sync()
+    rc = lib().lhip_sgemm_noalloc(0, 0, m, n, k, 1.0, A.ptr, k, B.ptr, n, 0.0, Cc.ptr, n)
+    device.sync()
+    assert rc == -7, f"expected LHIP_E_CAPACITY (-7), got {rc} on {device.info()['compute_units']} CUs"
     msg = _lib.last_error()
     assert "scratch" in msg and str(SCRATCH_BYTES) in msg, msg
     lib().lhip_clear_error()
