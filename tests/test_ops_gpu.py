@@ -35,7 +35,10 @@ def dl(buf):
 # ------------------------------------------------------------------ RMSNorm
 @pytest.mark.parametrize("rows,cols,eps", [(64, 128, 1e-5), (512, 128, 1e-5), (4096, 1024, 1e-6),
                                            (7, 13, 1e-5), (3, 5000, 1e-6), (5, 4100, 1e-5), (9, 2048, 1e-6),
-                                          (11, 3072, 1e-6), (6, 4096, 1e-5)])
+                                          (11, 3072, 1e-6), (6, 4096, 1e-5),
+                                          # two rows per wave (rows >= 4096): a last wave with one row,
+                                          # and rows shorter than a wave's float4 lanes (clamped loads)
+                                          (4099, 100, 1e-5), (4101, 1024, 1e-6)])
 def test_rmsnorm_fwd_bwd(rows, cols, eps):
     announce("rmsnorm", rows, cols)
     rng = np.random.default_rng(rows * 31 + cols)
@@ -114,6 +117,7 @@ def softmax_bwd_ref(y, g, scale, causal, offset=0, group=None):
     (16, 20, 1.0, 1, -3, 8),             # negative offset: lim clamps to 1
     (96, 3072, 0.5, 1, 5, 40),           # workgroup-per-row forward (3 float4 per thread), group-causal
     (64, 4096, 1.0, 1, 0, 0),            # workgroup-per-row forward, causal prefix of a long row
+    (32, 3072, 0.7, 0, 0, 0),            # workgroup-per-row, no mask (unconditional loads), 3 float4 per thread
 ])
 def test_softmax_fwd_bwd(rows, cols, scale, causal, offset, group):
     announce("softmax", rows, cols, causal, group)
@@ -147,7 +151,7 @@ def test_softmax_equal_logits_known_answer():
 
 
 # ------------------------------------------------------------------ SwiGLU
-@pytest.mark.parametrize("rows,cols", [(64, 256), (4096, 4096), (17, 33)])
+@pytest.mark.parametrize("rows,cols", [(64, 256), (4096, 4096), (17, 33), (3, 20), (7, 1028)])
 def test_swiglu_fwd_bwd(rows, cols):
     announce("swiglu", rows, cols)
     rng = np.random.default_rng(rows * 3 + cols)
@@ -162,6 +166,10 @@ def test_swiglu_fwd_bwd(rows, cols):
     call("lhip_swiglu_bwd", GT.ptr, cols, UP.ptr, cols, DH.ptr, cols, DG.ptr, cols, DU.ptr, cols, rows, cols, 0)
     assert rel_fro(dl(DG), dg_ref) <= EW
     assert rel_fro(dl(DU), du_ref) <= EW
+    # accumulate: a second call adds the same gradients
+    call("lhip_swiglu_bwd", GT.ptr, cols, UP.ptr, cols, DH.ptr, cols, DG.ptr, cols, DU.ptr, cols, rows, cols, 1)
+    assert rel_fro(dl(DG), 2 * dg_ref) <= EW
+    assert rel_fro(dl(DU), 2 * du_ref) <= EW
 
 
 def test_swiglu_strided_fused_w13_layout():
