@@ -7,7 +7,8 @@ forward, cross-entropy, backward and the SGD update -- for vocab 2000, dim 128,
 launched eagerly on the library stream (`--graph`: replayed from a captured
 hipGraph instead).  Prints ONE JSON line: steps/s, a `roofline` object
 for the step's dominant kernel (timed live on the library stream with the
-library's kernel timer), a `gemm4096` object (the 4096^3 NN GEMM measured in the same run)
+library's kernel timer), a `gemm4096` object (the 4096^3 NN GEMM measured in the same run),
+a `bandwidth` object (the C3/C4 bandwidth kernels measured in the same run)
 and a `cpu_baseline` object (the CPU oracle -- a single-threaded C
 restatement of lanternl's pure-Lua loops in double -- timed on this host).
 Kernel times (`kernel_ms`, `ms`) are dispatch start-to-end, as a kernel trace
@@ -236,10 +237,13 @@ def cpu_baseline_lm(nsteps=5):
     for _ in range(nsteps):
         O.lm_step_sgd(cfg, p, v, ids, tgt, 0.1)
     dt = (time.perf_counter() - t0) / nsteps
+    host = _lscpu()
     return {"value": 1.0 / dt, "unit": "steps/s", "cores": 1, "kind": "port",
+            "host_cpu": host["model"], "host_cores": host["cores"], "host_logical_cpus": host["logical_cpus"],
             "sample": f"{nsteps} full C2 LMTrain SGD steps (8 windows x 64 tokens, fwd+bwd+update) of the "
                       f"double-precision C restatement of the Lua CPU path (not LuaJIT: LuaJIT is not "
-                      f"installed), {_cpu_model()}"}
+                      f"installed), single-threaded on 1 of the host's {host['cores']} cores "
+                      f"({host['logical_cpus']} logical CPUs), {host['model']}"}
 
 
 def run_lm_workload(args):
@@ -283,6 +287,7 @@ def run_lm_workload(args):
                                          "kernel_ms_events: hipEvents around a recorded replay of back-to-back "
                                          "launches (includes launch gaps)"},
         "gemm4096": g4,
+        "bandwidth": bandwidth_object(args),
         "cpu_baseline": cpu_baseline_lm(),
     }
     gpu.close()
@@ -422,38 +427,49 @@ def bench_bandwidth(name, nbytes, make_set, launch, steps, warmup, only=None):
     ms_events = time_launches(run, steps, warmup, recorded=True)
     ms, kpc = kernel_ms(run, steps)
     gbps = nbytes / (ms * 1e-3) / 1e9
+    for st_ in sets:
+        for buf in st_:
+            buf.free()
     return {"suite": "bandwidth", "kernel": name, "ms": ms, "ms_events": ms_events, "kernels_per_call": kpc,
             "bytes": nbytes, "gbps": gbps, "frac": gbps / PEAK_HBM_GBPS, "buffer_sets": nsets}
 
 
-def run_bandwidth_suite(args):
+def bandwidth_cases(steps, warmup, only=None, references=True):
+    """The C3/C4 bandwidth kernels (and, with `references`, the library's
+    plainest streaming kernels at the same sizes and stream counts), each
+    timed with bench_bandwidth; returns their result dicts.  Inputs are
+    seeded N(0, 1)-shaped host arrays (one per shape, uploaded into every
+    buffer set: the timing needs non-zero data, not distinct data)."""
     from lanternl_amd import device
     from lanternl_amd._lib import call
     device.init(0)
     rng = np.random.default_rng(0)
     B = device.Buffer
     T, Dm, Fm = 4096, 1024, 4096
+    host = {}
 
     def arr(*shape, scale=1.0, loc=0.0):
-        return B.from_numpy((rng.standard_normal(shape) * scale + loc).astype(np.float32))
+        key = (shape, scale, loc)
+        if key not in host:
+            host[key] = (rng.standard_normal(shape) * scale + loc).astype(np.float32)
+        return B.from_numpy(host[key])
 
     out = []
-    steps, warm = max(args.steps, 20), args.warmup
     # RMSNorm 4096 x 1024 (eps 1e-6, gain N(1, 0.1))
     w = arr(Dm, scale=0.1, loc=1.0)
     nb = 4 * (2 * T * Dm + Dm + T)
     out.append(bench_bandwidth("rmsnorm_fwd 4096x1024", nb,
                                lambda i: (arr(T, Dm), B((T, Dm)), B((T,))),
                                lambda s: call("lhip_rmsnorm_fwd", s[0].ptr, w.ptr, s[1].ptr, s[2].ptr, T, Dm, 1e-6),
-                               steps, warm, args.only))
+                               steps, warmup, only))
     nb = 4 * (3 * T * Dm + 2 * Dm + T)
     inv = B.from_numpy(np.ones(T, np.float32))
     dw = B((Dm,))
     out.append(bench_bandwidth("rmsnorm_bwd 4096x1024", nb,
-                               lambda i: (arr(T, Dm), arr(T, Dm), B((T, Dm))),
+                               lambda i: (arr(T, Dm), arr(T, Dm, scale=0.5), B((T, Dm))),
                                lambda s: call("lhip_rmsnorm_bwd", s[0].ptr, w.ptr, inv.ptr, s[1].ptr, s[2].ptr,
                                               dw.ptr, T, Dm, 0),
-                               steps, warm, args.only))
+                               steps, warmup, only))
     # RoPE 4096 tokens x 16 heads x 64, base 1e4, in place (fwd and inverse),
     # interleaved pairs (the CPU path's layout) and half-split pairs
     nb = 4 * 2 * T * 16 * 64
@@ -464,27 +480,28 @@ def run_bandwidth_suite(args):
                                        lambda i: (arr(T, 16 * 64),),
                                        lambda s, inv_=inverse, il_=il: call("lhip_rope", s[0].ptr, None, T, 16, 64,
                                                                             16 * 64, 0, 0, 10000.0, il_, inv_),
-                                       steps, warm, args.only))
+                                       steps, warmup, only))
     # SwiGLU 4096 x 4096
     n = T * Fm
     out.append(bench_bandwidth("swiglu_fwd 4096x4096", 4 * 3 * n,
-                               lambda i: (arr(T, Fm), arr(T, Fm), B((T, Fm))),
+                               lambda i: (arr(T, Fm), arr(T, Fm, scale=0.5), B((T, Fm))),
                                lambda s: call("lhip_swiglu_fwd", s[0].ptr, Fm, s[1].ptr, Fm, s[2].ptr, Fm, T, Fm),
-                               steps, warm, args.only))
+                               steps, warmup, only))
     out.append(bench_bandwidth("swiglu_bwd 4096x4096", 4 * 5 * n,
-                               lambda i: (arr(T, Fm), arr(T, Fm), arr(T, Fm), B((T, Fm)), B((T, Fm))),
+                               lambda i: (arr(T, Fm), arr(T, Fm, scale=0.5), arr(T, Fm, scale=0.25), B((T, Fm)),
+                                          B((T, Fm))),
                                lambda s: call("lhip_swiglu_bwd", s[0].ptr, Fm, s[1].ptr, Fm, s[2].ptr, Fm, s[3].ptr,
                                               Fm, s[4].ptr, Fm, T, Fm, 0),
-                               steps, warm, args.only))
-    # row softmax 4096 x 4096, scores N(0, 4)
+                               steps, warmup, only))
+    # row softmax 4096 x 4096, scores N(0, 4) (sigma 2)
     out.append(bench_bandwidth("softmax_fwd 4096x4096", 4 * 2 * n,
                                lambda i: (arr(T, T, scale=2.0), B((T, T))),
                                lambda s: call("lhip_softmax_fwd", s[0].ptr, s[1].ptr, T, T, 1.0, 0, 0, 0),
-                               steps, warm, args.only))
+                               steps, warmup, only))
     out.append(bench_bandwidth("softmax_bwd 4096x4096", 4 * 3 * n,
-                               lambda i: (arr(T, T), arr(T, T), B((T, T))),
+                               lambda i: (arr(T, T, scale=0.01, loc=1.0 / T), arr(T, T), B((T, T))),
                                lambda s: call("lhip_softmax_bwd", s[0].ptr, s[1].ptr, s[2].ptr, T, T, 1.0, 0, 0, 0, 0),
-                               steps, warm, args.only))
+                               steps, warmup, only))
     # C3 fused softmax + CE: 512 x 32000 logits, labels uniform
     R, V = 512, 32000
     labels = B.from_numpy(rng.integers(0, V, R).astype(np.int32), np.int32)
@@ -492,26 +509,45 @@ def run_bandwidth_suite(args):
                                lambda i: (arr(R, V), B((R, V)), B((R,))),
                                lambda s: call("lhip_ce_fused", s[0].ptr, labels.ptr, s[2].ptr, s[1].ptr, R, V, -1,
                                               1.0 / R),
-                               steps, warm, args.only))
-    # size-matched streaming references: what a kernel with no arithmetic and
-    # the same number of read and written streams reaches at these sizes
-    for rows, cols in ((T, Dm), (T, Fm)):
-        n = rows * cols
-        out.append(bench_bandwidth(f"reference silu {rows}x{cols} (1 read + 1 write)", 4 * 2 * n,
-                                   lambda i, n_=n: (B((n_,)).zero(), B((n_,))),
-                                   lambda s, n_=n: call("lhip_silu", s[0].ptr, s[1].ptr, n_),
-                                   steps, warm, args.only))
-        out.append(bench_bandwidth(f"reference silu in place {rows}x{cols} (1 read + 1 write)", 4 * 2 * n,
-                                   lambda i, n_=n: (B((n_,)).zero(),),
-                                   lambda s, n_=n: call("lhip_silu", s[0].ptr, s[0].ptr, n_),
-                                   steps, warm, args.only))
-        out.append(bench_bandwidth(f"reference add {rows}x{cols} (2 reads + 1 write)", 4 * 3 * n,
-                                   lambda i, n_=n: (B((n_,)).zero(), B((n_,)).zero(), B((n_,))),
-                                   lambda s, n_=n: call("lhip_add", s[0].ptr, s[1].ptr, s[2].ptr, n_),
-                                   steps, warm, args.only))
-    for r in out:
-        if r is not None:
-            print(json.dumps(r), flush=True)
+                               steps, warmup, only))
+    if references:
+        # size-matched streaming references: what a kernel with no arithmetic
+        # to speak of and the same number of read and written streams reaches
+        for rows, cols in ((T, Dm), (T, Fm)):
+            n = rows * cols
+            out.append(bench_bandwidth(f"reference silu {rows}x{cols} (1 read + 1 write)", 4 * 2 * n,
+                                       lambda i, r_=rows, c_=cols: (arr(r_, c_), B((r_ * c_,))),
+                                       lambda s, n_=n: call("lhip_silu", s[0].ptr, s[1].ptr, n_),
+                                       steps, warmup, only))
+            out.append(bench_bandwidth(f"reference silu in place {rows}x{cols} (1 read + 1 write)", 4 * 2 * n,
+                                       lambda i, r_=rows, c_=cols: (arr(r_, c_),),
+                                       lambda s, n_=n: call("lhip_silu", s[0].ptr, s[0].ptr, n_),
+                                       steps, warmup, only))
+            out.append(bench_bandwidth(f"reference add {rows}x{cols} (2 reads + 1 write)", 4 * 3 * n,
+                                       lambda i, r_=rows, c_=cols: (arr(r_, c_), arr(r_, c_, scale=0.5),
+                                                                    B((r_ * c_,))),
+                                       lambda s, n_=n: call("lhip_add", s[0].ptr, s[1].ptr, s[2].ptr, n_),
+                                       steps, warmup, only))
+    return [r for r in out if r is not None]
+
+
+def bandwidth_object(args):
+    """The C3/C4 bandwidth kernels measured in the default run: kernel-timer
+    ms, GB/s and fraction of the 8 TB/s HBM peak per kernel (buffer sets
+    rotated past the Infinity Cache), 20 timed calls each."""
+    t0 = time.perf_counter()
+    res = bandwidth_cases(steps=20, warmup=5, references=False)
+    kernels = {r["kernel"]: {"ms": round(r["ms"], 6), "bytes": r["bytes"], "gbps": round(r["gbps"], 1),
+                             "frac": round(r["frac"], 4), "kernels_per_call": r["kernels_per_call"]} for r in res}
+    return {"peak_gbps": PEAK_HBM_GBPS, "method": "kernel timer (dispatch start to end, median of 20 calls each "
+            "launched alone), buffer sets rotated past the 256 MB Infinity Cache; bytes = each input read once "
+            "plus each output written once (fp32)", "seconds": round(time.perf_counter() - t0, 2),
+            "kernels": kernels}
+
+
+def run_bandwidth_suite(args):
+    for r in bandwidth_cases(max(args.steps, 20), args.warmup, args.only):
+        print(json.dumps(r), flush=True)
 
 
 def run_cpu_suite(args):
