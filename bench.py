@@ -379,6 +379,53 @@ def bench_host_gemm(m, k, n, op=0, reps=20, rates=None, gemm_ms=None):
     return r
 
 
+def bench_host_spin(m=256, k=128, n=256, reps=200, gap_us=200.0):
+    """The C1 host-table call with the conversion workers spinning between
+    calls (lhip_set_host_spin 1000 us, the default) and sleeping at once (0),
+    back to back and with `gap_us` of single-threaded host work between calls
+    (a LuaJIT host's own work).  Reports the call's wall time and the process
+    CPU time it costs per call (all threads; the gap's own work excluded)."""
+    import ctypes as ct
+    from lanternl_amd._lib import call
+    rng = np.random.default_rng(1)
+    a, b = rng.uniform(-1, 1, m * k), rng.uniform(-1, 1, k * n)
+    c = np.empty(m * n)
+    args_ = (0, a.ctypes.data, b.ctypes.data, c.ctypes.data, m, k, n, 0)
+    prev = ct.c_int()
+    call("lhip_set_host_spin", 1000, ct.byref(prev))
+
+    def gap():
+        t_end = time.perf_counter() + gap_us * 1e-6
+        while time.perf_counter() < t_end:
+            pass
+    out = []
+    try:
+        for spin in (1000, 0):
+            call("lhip_set_host_spin", spin, None)
+            for with_gap in (False, True):
+                for _ in range(5):
+                    call("lhip_matmul_host", *args_)
+                wall, cpu0, g_cpu = 0.0, time.process_time(), 0.0
+                for _ in range(reps):
+                    if with_gap:
+                        g0 = time.thread_time()          # the calling thread's own work only
+                        gap()
+                        g_cpu += time.thread_time() - g0
+                    t0 = time.perf_counter()
+                    call("lhip_matmul_host", *args_)
+                    wall += time.perf_counter() - t0
+                cpu = time.process_time() - cpu0 - g_cpu
+                out.append({"suite": "gemm_host_spin", "op": "NN", "m": m, "k": k, "n": n, "spin_us": spin,
+                            "host_work_between_calls_us": gap_us if with_gap else 0.0,
+                            "ms": wall / reps * 1e3, "cpu_ms_per_call": cpu / reps * 1e3,
+                            "note": "cpu_ms_per_call: process CPU time (every thread) per call, the calling "
+                                    "thread's host work between calls excluded (workers spinning through the "
+                                    "gaps are counted)"})
+    finally:
+        call("lhip_set_host_spin", prev.value, None)
+    return out
+
+
 def run_gemm_suite(args):
     from lanternl_amd import device
     device.init(0)
@@ -411,6 +458,8 @@ def run_gemm_suite(args):
             gm, gn, gk = (k, n, m) if op == 2 else (m, n, k)
             dev[key] = bench_gemm(gm, gn, gk, ta, tb, steps=10, warmup=2)["ms"]
         print(json.dumps(bench_host_gemm(m, k, n, op, reps, rates, dev[key])), flush=True)
+    for r in bench_host_spin():
+        print(json.dumps(r), flush=True)
 
 
 # ------------------------------------------------------------ bandwidth kernels

@@ -215,6 +215,15 @@ LHIP_API int lhip_sgemm_noalloc(int transa, int transb, int m, int n, int k, flo
 LHIP_API int lhip_matmul_host(int op, const double* a, const double* b, double* c,
                               int m, int k, int n, int acc);
 
+/* How long, in microseconds, the host threads of lhip_matmul_host spin after
+ * a call before they sleep (and how long a call spins waiting for their
+ * parts before it sleeps).  No counterpart in the reference.  The default,
+ * 1000, keeps three workers awake between back-to-back small calls, each
+ * busy on a core while it spins; 0 puts them to sleep at once, for hosts that
+ * need those cores (a small call then pays their wake-up).  *previous (may be
+ * NULL) receives the old value.  Range [0, 100000]. */
+LHIP_API int lhip_set_host_spin(int spin_us, int* previous);
+
 /* ---- bandwidth-bound kernels (device pointers, fp32 rows, async) ----------
  * `accumulate` != 0 adds into the output(s) instead of overwriting them, the
  * way the CPU path's BACKWARD.* functions add into grad buffers. */

@@ -78,6 +78,7 @@ SIGNATURES = {
     "lhip_sgemm_batched_reduce": (_i, [_i, _i, _i, _i, _i, _f, _p, _i, _ll, _p, _i, _ll, _f, _p, _i, _i]),
     "lhip_sgemm_noalloc": (_i, [_i, _i, _i, _i, _i, _f, _p, _i, _p, _i, _f, _p, _i]),
     "lhip_matmul_host": (_i, [_i, _p, _p, _p, _i, _i, _i, _i]),
+    "lhip_set_host_spin": (_i, [_i, ctypes.POINTER(_i)]),
     "lhip_rmsnorm_fwd": (_i, [_p, _p, _p, _p, _i, _i, _f]),
     "lhip_rmsnorm_bwd": (_i, [_p, _p, _p, _p, _p, _p, _i, _i, _i]),
     "lhip_softmax_fwd": (_i, [_p, _p, _i, _i, _f, _i, _i, _i]),

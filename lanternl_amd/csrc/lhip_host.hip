@@ -260,4 +260,13 @@ LHIP_API int lhip_matmul_host(int op, const double* a, const double* b, double* 
     return err;
 }
 
+LHIP_API int lhip_set_host_spin(int spin_us, int* previous)
+{
+    if (spin_us < 0 || spin_us > 100000)
+        return fail(LHIP_E_ARG, "lhip_set_host_spin: spin_us %d outside [0, 100000]", spin_us);
+    if (previous) *previous = lhip::g_pool.spin_us();
+    lhip::g_pool.set_spin_us(spin_us);
+    return LHIP_OK;
+}
+
 }  // extern "C"

@@ -69,18 +69,28 @@ __global__ void __launch_bounds__(64) sum_stage2(const double* __restrict__ part
 // Global gradient norm from the stage-1 partials (nparts > 0; every block sums
 // them in sum_stage2's order, so all blocks, and the two-kernel form, agree bit
 // for bit) or from the finished total (nparts == 0).
+// The squared gradient norm from the producers' per-workgroup partials, the
+// same value in every block (every block sums them in the same order).  All
+// 256 threads load: up to 4 partials each, every load issued before the
+// first add (indices clamped, masked in the sum), so a block waits for one
+// load round trip instead of one per 64 partials; then the four waves' sums
+// meet in LDS in wave order.  Called by every thread of a 256-thread block.
 __device__ __forceinline__ double grad_total(const double* __restrict__ sumsq, int nparts)
 {
     if (nparts <= 0) return sumsq[0];
-    __shared__ double tot;
-    if (threadIdx.x < 64) {
-        double s = 0.0;
-        for (int i = threadIdx.x; i < nparts; i += 64) s += sumsq[i];
-        s = wave_sum(s);
-        if (threadIdx.x == 0) tot = s;
-    }
+    __shared__ double part[4];
+    constexpr int kPer = 4;
+    double t[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) t[j] = sumsq[min(static_cast<int>(threadIdx.x) + 256 * j, nparts - 1)];
+    double s = 0.0;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) s += static_cast<int>(threadIdx.x) + 256 * j < nparts ? t[j] : 0.0;
+    for (int i = static_cast<int>(threadIdx.x) + 256 * kPer; i < nparts; i += 256) s += sumsq[i];
+    s = wave_sum(s);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
     __syncthreads();
-    return tot;
+    return ((part[0] + part[1]) + part[2]) + part[3];
 }
 
 __device__ __forceinline__ float ld_lane(const float4& v, int k) { return k == 0 ? v.x : k == 1 ? v.y : k == 2 ? v.z : v.w; }

@@ -36,6 +36,12 @@ namespace lhip {
 class HostPool {
 public:
     explicit HostPool(int spinners = 3, int spin_us = 1000) : spinners_(spinners), spin_us_(spin_us) {}
+
+    // How long the spinners (and a caller waiting for workers' parts) spin
+    // before they block; 0 makes them block at once.  Takes effect from the
+    // next wait of each thread.
+    void set_spin_us(int us) { spin_us_.store(us < 0 ? 0 : us, std::memory_order_relaxed); }
+    int spin_us() const { return spin_us_.load(std::memory_order_relaxed); }
     ~HostPool() { stop(); }
     HostPool(const HostPool&) = delete;
     HostPool& operator=(const HostPool&) = delete;
@@ -81,7 +87,7 @@ public:
         const auto t0 = std::chrono::steady_clock::now();
         for (int it = 1; remaining_.load(std::memory_order_acquire) > 0; ++it) {
             cpu_pause();
-            if ((it & 255) == 0 && std::chrono::steady_clock::now() - t0 > std::chrono::microseconds(spin_us_)) {
+            if ((it & 255) == 0 && std::chrono::steady_clock::now() - t0 > std::chrono::microseconds(spin_us())) {
                 std::unique_lock<std::mutex> g(mu_);
                 caller_waits_.store(true);
                 done_cv_.wait(g, [&] { return remaining_.load() == 0; });
@@ -171,7 +177,7 @@ private:
                     if (gen_.load(std::memory_order_acquire) != seen) { moved = true; break; }
                     cpu_pause();
                     if ((it & 255) == 0 &&
-                        std::chrono::steady_clock::now() - t0 > std::chrono::microseconds(spin_us_))
+                        std::chrono::steady_clock::now() - t0 > std::chrono::microseconds(spin_us()))
                         break;
                 }
             }
@@ -190,7 +196,8 @@ private:
         }
     }
 
-    const int spinners_, spin_us_;
+    const int spinners_;
+    std::atomic<int> spin_us_;
     std::vector<std::thread> workers_;
     std::mutex mu_;
     std::condition_variable cv_, spin_cv_, done_cv_;   // other workers, spinners, the caller

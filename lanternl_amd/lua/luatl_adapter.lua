@@ -67,6 +67,7 @@ int lhip_sgemm(int transa, int transb, int m, int n, int k, float alpha,
                float* C, int ldc);
 int lhip_matmul_host(int op, const double* a, const double* b, double* c,
                      int m, int k, int n, int acc);
+int lhip_set_host_spin(int spin_us, int* previous);
 int lhip_gemm_ex(const float* A, const float* B, float* C, const float* bias, const float* gamma,
                  const float* rowscale, int M, int N, int K, long long a_rs, long long a_cs,
                  long long b_rs, long long b_cs, long long c_rs, long long c_cs, long long a_bs,

@@ -1,8 +1,9 @@
 // Stress check of lhip::HostPool (lanternl_amd/csrc/lhip_pool.h), built and run
 // by tests/test_host_pool.py (also under ThreadSanitizer).  Every run() must
 // call each part exactly once and return only after all of them returned;
-// workers are let fall asleep between some runs (short and long pauses), and
-// the pool is stopped and restarted.
+// workers are let fall asleep between some runs (short and long pauses), the
+// spin window is switched between 0 and 200 us while they run, and the pool
+// is stopped and restarted.
 #include <atomic>
 #include <chrono>
 #include <cstdio>
@@ -39,6 +40,9 @@ int main(int argc, char** argv)
             const unsigned r = rng() % 100;
             if (r < 3) std::this_thread::sleep_for(std::chrono::microseconds(400));   // past the spin window
             else if (r < 8) std::this_thread::sleep_for(std::chrono::microseconds(50));
+            // the spin window changed while workers spin or sleep (0: block at once)
+            if (r == 50) pool.set_spin_us(0);
+            else if (r == 51) pool.set_spin_us(200);
         }
         pool.stop();
         pool.start(4);   // restart, then let the destructor join

@@ -357,6 +357,38 @@ def test_matmul_host_accumulate_in_double():
     assert rel_fro(out, expect) <= TOL
 
 
+def test_matmul_host_with_workers_not_spinning():
+    """lhip_set_host_spin(0): the conversion workers sleep at once after each
+    call; results are unchanged (C1, all three products), the old value comes
+    back, and out-of-range values are refused."""
+    announce("matmul_host spin 0")
+    from lanternl_amd._lib import LanternlHipError, call
+    prev = ctypes.c_int()
+    call("lhip_set_host_spin", 0, ctypes.byref(prev))
+    try:
+        rng = np.random.default_rng(21)
+        a = f32(rng.uniform(-1, 1, (256, 128)))
+        b = f32(rng.uniform(-1, 1, (128, 256)))
+        for op, bb, ref in ((0, b, O.mm(a, b)), (1, np.ascontiguousarray(b.T), O.mm(a, b)),
+                            (2, f32(rng.uniform(-1, 1, (256, 256))), None)):
+            if op == 2:
+                ref = O.matmul_tn(a, bb)
+            rows, n = (128, 256) if op == 2 else (256, 256)
+            out = np.empty((rows, n))
+            for _ in range(3):    # back to back: the workers sleep and wake each time
+                call("lhip_matmul_host", op, a.ctypes.data_as(ctypes.c_void_p), bb.ctypes.data_as(ctypes.c_void_p),
+                     out.ctypes.data_as(ctypes.c_void_p), 256, 128, 256, 0)
+                assert rel_fro(out, ref) <= TOL
+        with pytest.raises(LanternlHipError, match="outside"):
+            call("lhip_set_host_spin", -1, None)
+        got = ctypes.c_int()
+        call("lhip_set_host_spin", 0, ctypes.byref(got))
+        assert got.value == 0
+    finally:
+        call("lhip_set_host_spin", prev.value, None)
+    assert prev.value == 1000
+
+
 def test_matmul_host_small_calls_back_to_back():
     """Small calls (under 1 Mi elements) convert on the calling thread and the
     pool's spinning workers: 240 calls of random shapes (one to four parts per
