@@ -224,6 +224,17 @@ def dominant_kernel_c2(steps, warmup):
             "frac": tflops / PEAK_FP32_MFMA_TFLOPS, "m": N, "n": D, "k": 2 * F, "flops": flops}
 
 
+def dispatch_floor_ms(calls=50):
+    """Kernel-timer duration of a kernel that does almost nothing (a one-
+    workgroup fill of 16 bytes): the floor under every launch of the step."""
+    from lanternl_amd import device
+    from lanternl_amd._lib import call
+    buf = device.Buffer((4,))
+    ms, _ = kernel_ms(lambda _: call("lhip_zero", buf.ptr, 16), calls)
+    buf.free()
+    return ms
+
+
 def cpu_baseline_lm(nsteps=5):
     import oracle as O
     cfg = O.lm_cfg(C2["vocab"], C2["dim"], C2["layers"], C2["heads"], C2["ffn"])
@@ -263,6 +274,7 @@ def run_lm_workload(args):
     if not np.isfinite(st["loss"]):
         raise RuntimeError(f"non-finite loss after the timed steps: {st}")
     dom = dominant_kernel_c2(args.steps, args.warmup)
+    floor_ms = dispatch_floor_ms()
     dom_traffic, dom_src = profile_figure("sgemm_batched_reduce_dh2.md", "traffic_bytes_per_launch")
     g4 = gemm4096_object(args)
     flops = 3 * 1_000_341_504 * 1.0   # GEMM flops of one fwd+bwd step (forward x 3)
@@ -282,6 +294,10 @@ def run_lm_workload(args):
                      "kernel": f"batch-reduce sgemm NT {dom['m']}x{dom['n']}x(2x{dom['k'] // 2}) "
                                f"(dh2 = dz1 . W1^T + du . W3^T), {dom['flops']:.0f} flop per launch",
                      "kernel_ms": dom["ms"], "kernel_ms_events": dom["ms_events"],
+                     "dispatch_floor_ms": floor_ms,
+                     "dispatch_floor_method": "the same kernel timer on a one-workgroup fill of 16 bytes "
+                                              "(lhip_zero), launched alone: what any kernel costs on this "
+                                              "timer before it does work",
                      "kernel_ms_method": "kernel_ms: median over calls of the dispatch start-to-end timestamps "
                                          "(library kernel timer), as rocprofv3 --kernel-trace reports them; "
                                          "kernel_ms_events: hipEvents around a recorded replay of back-to-back "
