@@ -10,7 +10,7 @@
 --      the transposed products with the same convention, and
 --      matmul_into(op, a, m, k, b, n, rd, acc) serves every product that
 --      writes into a caller's table (`out`, with or without `acc`): the
---      dispatch that matrix.lua gains with the patch shown in INTEGRATION.md.
+--      dispatch that matrix.lua gains with lanternl_amd/lua/matrix_patch.lua.
 --    * Legacy flat calls rmsnorm(x, rows, cols, w, eps), softmax(x, rows, cols),
 --      softmax_causal(x, rows, cols, scale, group) (:137-159).
 --    * Resident calls gemm(hA, hB, hC, opts), gemm_dx, gemm_dw, add_inplace,

@@ -33,7 +33,9 @@ UNARY_PRI = 8
 
 
 def tokenize(text):
-    """[(kind, value, line)]: kind is 'name', 'kw', 'num', 'str', 'op' or 'eof'."""
+    """[(kind, value, line)]: kind is 'name', 'kw', 'num', 'str', 'op' or 'eof'.
+    A 'str' token carries a fourth field: True for a long bracket string (its
+    text raw), False for a quoted one (its text with the escapes unprocessed)."""
     toks, i, line, n = [], 0, 1, len(text)
     while i < n:
         c = text[i]
@@ -63,7 +65,7 @@ def tokenize(text):
             j = text.find(close, i + m.end())
             if j < 0:
                 raise LuaSyntaxError(f"line {line}: unfinished long string")
-            toks.append(("str", text[i + m.end():j], line))
+            toks.append(("str", text[i + m.end():j], line, True))
             line += text.count("\n", i, j)
             i = j + len(close)
             continue
@@ -80,7 +82,7 @@ def tokenize(text):
                 if text[j] == c:
                     break
                 j += 1
-            toks.append(("str", text[i + 1:j], line))
+            toks.append(("str", text[i + 1:j], line, False))
             i = j + 1
             continue
         m = re.match(r"0[xX][0-9a-fA-F]+(?:[uU]?[lL][lL])?|(?:\d+\.?\d*|\.\d+)(?:[eE][+-]?\d+)?(?:[uU]?[lL][lL]|i)?",

@@ -110,7 +110,7 @@ def test_module_sets_the_reference_fields():
 
 
 def test_matmul_into_entry_declared_in_both_modules():
-    """The entry the registry's out=/acc dispatch calls (matrix.lua patch in INTEGRATION.md)."""
+    """The entry the registry's out=/acc dispatch calls (lanternl_amd/lua/matrix_patch.lua)."""
     mine = _lua_sigs(open(ADAPTER).read(), "M")
     assert mine["matmul_into"] == ["op", "a", "m", "k", "b", "n", "rd", "acc"]
     from lanternl_amd import backend as B

@@ -1,10 +1,10 @@
 """The Lua side, checked without a Lua runtime (none exists in this image or on
-the GPU box): lanternl_amd/lua/luatl_adapter.lua and the matrix.lua patch in
-INTEGRATION.md must parse as Lua 5.1 / LuaJIT, and every name they use must be
-a local in scope or a Lua builtin (a misspelt local, or a local function used
-above its declaration, would otherwise only fail when LuaJIT runs it).  The
-parser itself (tests/lua_lint.py) is checked on constructs it must accept and
-mistakes it must reject."""
+the GPU box): lanternl_amd/lua/luatl_adapter.lua and the matrix.lua patch
+(lanternl_amd/lua/matrix_patch.lua) must parse as Lua 5.1 / LuaJIT, and every
+name they use must be a local in scope or a Lua builtin (a misspelt local, or
+a local function used above its declaration, would otherwise only fail when
+LuaJIT runs it).  The parser itself (tests/lua_lint.py) is checked on
+constructs it must accept and mistakes it must reject."""
 import os
 import re
 
@@ -81,19 +81,31 @@ def test_adapter_parses_and_uses_only_locals_and_builtins():
     assert not unknown, f"names used as globals in luatl_adapter.lua (first line): {unknown}"
 
 
-def test_integration_matrix_lua_patch_parses():
-    """The helper and the three call sites INTEGRATION.md adds to matrix.lua."""
-    text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
-    blocks = re.findall(r"```lua\n(.*?)```", text, re.S)
-    assert len(blocks) >= 2
-    helper = next(b for b in blocks if "local function try_offload" in b)
+def test_matrix_lua_patch_parses():
+    """The helper and the three call sites the patch adds to matrix.lua."""
+    from tests.lua_registry import PATCH, patch_parts
+    text = open(PATCH).read()
+    L.parse(text)                                    # the file as a whole is valid Lua
+    helper, sites = patch_parts(text)
     # matrix.lua's own locals the helper relies on (ai/core/matrix.lua:1-25,169-176)
     matrix_locals = {"matrix", "backends", "backend_failed", "sformat"}
     free = L.free_names(helper)
     assert set(free) <= LUA_BUILTINS | matrix_locals, free
-    sites = next(b for b in blocks if 'try_offload("matmul", "multiply"' in b)
     # the call sites are statements inside the three functions: wrap them in one
     wrapped = ("local function try_offload(...) end\nlocal function body(a, b, ad, bd, m, k, n, result, out, acc)\n"
-               + sites + "\nend")
+               + "\n".join(sites.values()) + "\nend")
     free = L.free_names(wrapped)
     assert not free, free
+
+
+def test_integration_notes_show_the_patch_file_verbatim():
+    """The ```lua blocks the integration notes give maintainers are the patch
+    file's two parts, character for character."""
+    from tests.lua_registry import PATCH
+    text = open(PATCH).read()
+    helper = text.split("-- [helper]\n", 1)[1].split("-- [call sites]\n", 1)[0]
+    sites = text.split("-- [call sites]\n", 1)[1]
+    notes = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    blocks = re.findall(r"```lua\n(.*?)```", notes, re.S)
+    assert helper.rstrip("\n") + "\n" in [b for b in blocks]
+    assert sites in blocks
