@@ -130,6 +130,15 @@ def kernel_ms(fn, calls, warmup=1):
     return float(np.median(per_call)), kpc
 
 
+def xcd_traffic_floor(m, n, k, xcds=8):
+    """Least bytes an m x n x k fp32 product moves between the XCDs' L2s and
+    memory when each XCD computes a block of the output: an XCD taking 1/q of
+    the rows and 1/p of the columns (p*q = xcds) fetches A/q and B/p, so A is
+    fetched p times and B q times in all; C is written once."""
+    a, b, c = 4 * m * k, 4 * n * k, 4 * m * n
+    return min(p * a + (xcds // p) * b for p in (1, 2, 4, 8) if xcds % p == 0) + c
+
+
 def profile_figure(name, key):
     """A figure recorded in a committed profile (profiles/<name>), on a line
     `key: value` (the profile says how and at which commit it was measured)."""
@@ -276,6 +285,7 @@ def run_lm_workload(args):
     dom = dominant_kernel_c2(args.steps, args.warmup)
     floor_ms = dispatch_floor_ms()
     dom_traffic, dom_src = profile_figure("sgemm_batched_reduce_dh2.md", "traffic_bytes_per_launch")
+    xcd_floor = xcd_traffic_floor(dom["m"], dom["n"], dom["k"])
     g4 = gemm4096_object(args)
     flops = 3 * 1_000_341_504 * 1.0   # GEMM flops of one fwd+bwd step (forward x 3)
     line = {
@@ -291,6 +301,11 @@ def run_lm_workload(args):
         "roofline": {"bound": "mfma", "achieved": dom["tflops"], "peak": PEAK_FP32_MFMA_TFLOPS,
                      "unit": "TFLOP/s", "frac": dom["frac"], "traffic": dom_traffic,
                      "traffic_source": dom_src,
+                     "traffic_floor_8xcd": xcd_floor,
+                     "traffic_floor_method": "least L2-miss bytes any placement of the output tiles over the "
+                                             "8 XCDs (each with its own L2) can reach: min over p*q = 8 of "
+                                             "p*A + q*B + C, an XCD taking 1/q of the rows and 1/p of the "
+                                             "columns; algorithmic bytes assume one shared cache",
                      "kernel": f"batch-reduce sgemm NT {dom['m']}x{dom['n']}x(2x{dom['k'] // 2}) "
                                f"(dh2 = dz1 . W1^T + du . W3^T), {dom['flops']:.0f} flop per launch",
                      "kernel_ms": dom["ms"], "kernel_ms_events": dom["ms_events"],
