@@ -641,7 +641,12 @@ class CData:
             if ftype is None:
                 raise LuaError(f"cdata<{self.ct.name}> has no field '{k}'")
             if ftype is ctypes.c_void_p:
-                setattr(st, k, _to_addr(v))
+                if isinstance(v, str):          # LuaJIT points the field at the string's bytes
+                    buf = ctypes.create_string_buffer(v.encode())
+                    self.__dict__.setdefault("_strings", {})[k] = buf
+                    setattr(st, k, ctypes.addressof(buf))
+                else:
+                    setattr(st, k, _to_addr(v))
             elif issubclass(ftype, ctypes.Array):
                 setattr(st, k, v.encode() if isinstance(v, str) else v)
             else:
@@ -730,6 +735,8 @@ class FFI:
                     nm = nm.strip()
                     t = self.parse_type(head + ("*" * nm.count("*")))
                     fields.append((nm.replace("*", "").strip(), t.scalar_ctype()))
+            if m.group(2) in self.types:
+                raise LuaError(f"attempt to redefine '{m.group(2)}'")
             self.types[m.group(2)] = type(m.group(2), (ctypes.Structure,), {"_fields_": fields})
         body = re.sub(r"typedef\s+struct\s*\{.*?\}\s*\w+\s*;", "", text, flags=re.S)
         for m in re.finditer(r"([\w\s\*]+?)\b(\w+)\s*\(([^;]*?)\)\s*;", body, re.S):
@@ -740,6 +747,8 @@ class FFI:
                     prm = " ".join(prm.split())
                     pm = re.match(r"^(.*?[\s\*])(\w+)$", prm)
                     args.append(self.parse_type(pm.group(1) if pm else prm))
+            if name in self.funcs:
+                raise LuaError(f"attempt to redefine '{name}'")
             self.funcs[name] = (self.parse_type(ret), args)
 
     # -- objects
@@ -832,9 +841,13 @@ class CLib:
         def call(*vals):
             if len(vals) != len(args):
                 raise LuaError(f"wrong number of arguments for function '{name}'")
-            conv = []
+            conv, keep = [], []
             for a, v in zip(args, vals):
-                if a.ptr:
+                if a.ptr and isinstance(v, str):     # const char*: the string's bytes for the call
+                    buf = ctypes.create_string_buffer(v.encode())
+                    keep.append(buf)
+                    conv.append(ctypes.addressof(buf))
+                elif a.ptr:
                     conv.append(_to_addr(v))
                 else:
                     n = tonum(v)

@@ -1,6 +1,6 @@
 """The Lua side, checked without a Lua runtime (none exists in this image or on
-the GPU box): lanternl_amd/lua/luatl_adapter.lua and the matrix.lua patch
-(lanternl_amd/lua/matrix_patch.lua) must parse as Lua 5.1 / LuaJIT, and every
+the GPU box): lanternl_amd/lua/luatl_adapter.lua, lanternl_amd/lua/lanternl_lm.lua
+and the matrix.lua patch (lanternl_amd/lua/matrix_patch.lua) must parse as Lua 5.1 / LuaJIT, and every
 name they use must be a local in scope or a Lua builtin (a misspelt local, or
 a local function used above its declaration, would otherwise only fail when
 LuaJIT runs it).  The parser itself (tests/lua_lint.py) is checked on
@@ -74,11 +74,12 @@ def test_resolver_finds_use_before_local_and_misspelt_locals():
     assert L.free_names("local function f(p) end return p") == {"p": 1}
 
 
-def test_adapter_parses_and_uses_only_locals_and_builtins():
-    text = open(ADAPTER).read()
+@pytest.mark.parametrize("name", ["luatl_adapter.lua", "lanternl_lm.lua"])
+def test_module_parses_and_uses_only_locals_and_builtins(name):
+    text = open(os.path.join(os.path.dirname(ADAPTER), name)).read()
     free = L.free_names(text)
     unknown = {k: v for k, v in free.items() if k not in LUA_BUILTINS}
-    assert not unknown, f"names used as globals in luatl_adapter.lua (first line): {unknown}"
+    assert not unknown, f"names used as globals in {name} (first line): {unknown}"
 
 
 def test_matrix_lua_patch_parses():

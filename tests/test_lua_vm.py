@@ -274,24 +274,63 @@ def _sig(ct):
     return (ct.base.__name__ if ct.base is not None else "void", ct.ptr)
 
 
-def test_adapter_cdef_matches_the_header_and_the_library():
-    vm, M = run_module(ADAPTER)
+LUA_MODULES = [ADAPTER, os.path.join(ROOT, "lanternl_amd", "lua", "lanternl_lm.lua")]
+
+
+@pytest.mark.parametrize("path", LUA_MODULES, ids=os.path.basename)
+def test_module_cdef_matches_the_header_and_the_library(path):
+    """Each module's ffi.cdef, declared as the module declares it, against the
+    C header: every function's argument and return types, every struct's
+    field names, types and offsets; and every symbol resolves in the library."""
+    text = open(path).read()
+    blocks = re.findall(r"ffi\.cdef\[\[(.*?)\]\]", text, re.S)
+    assert len(blocks) == 1
+    mf = FFI()
+    mf.cdef(blocks[0])
+    _compare_with_header(mf)
+
+
+def _compare_with_header(mf):
     hf = _header_ffi()
-    assert len(vm.ffi.funcs) >= 40
-    for name, (ret, args) in vm.ffi.funcs.items():
+    assert len(mf.funcs) >= 15
+    for name, (ret, args) in mf.funcs.items():
         assert name in hf.funcs, f"{name} is declared in the adapter but not in lanternl_hip.h"
         hret, hargs = hf.funcs[name]
         assert _sig(ret) == _sig(hret), name
         assert [_sig(a) for a in args] == [_sig(a) for a in hargs], name
     def layout(cls):
         return [(f, t.__name__, getattr(cls, f).offset, getattr(cls, f).size) for f, t in cls._fields_]
-    for tname, cls in vm.ffi.types.items():
+    for tname, cls in mf.types.items():
         hcls = hf.types[tname]
         assert ctypes.sizeof(cls) == ctypes.sizeof(hcls), tname
         assert layout(cls) == layout(hcls), tname
     lib = ctypes.CDLL(LIB)
-    for name in vm.ffi.funcs:
+    for name in mf.funcs:
         assert hasattr(lib, name), name
+
+
+def test_the_two_modules_declare_nothing_twice():
+    """LuaJIT's C namespace is global: a second declaration of a name raises
+    "attempt to redefine", so the modules loaded together must not overlap."""
+    decls = []
+    for path in LUA_MODULES:
+        mf = FFI()
+        mf.cdef(re.search(r"ffi\.cdef\[\[(.*?)\]\]", open(path).read(), re.S).group(1))
+        decls.append(set(mf.funcs) | set(mf.types))
+    assert not (decls[0] & decls[1])
+    with pytest.raises(LuaError, match="attempt to redefine 'f'"):
+        FFI().cdef("int f(int x);\nint f(int x);")
+
+
+def test_lm_module_is_unavailable_with_the_adapter():
+    vm = LuaVM()
+    vm.search_dirs.append(os.path.dirname(ADAPTER))
+    lm = vm.call(vm.G.rawget("require"), "lanternl_lm")[0]
+    ad = vm.call(vm.G.rawget("require"), "luatl_adapter")[0]
+    if ad.rawget("available"):
+        pytest.skip("a GPU is visible: the GPU tests cover the available module")
+    assert lm.rawget("available") is False and lm.rawget("reason") == ad.rawget("reason")
+    assert lm.rawget("new") is None
 
 
 def test_adapter_module_loads_and_reports_availability():
