@@ -42,6 +42,9 @@ class LuaTable:
     def key(k):
         if isinstance(k, float) and k.is_integer():
             return int(k)
+        if isinstance(k, CInt64):
+            raise LuaError("a 64-bit integer cdata used as a table key (LuaJIT keys cdata by identity); "
+                           "convert it with tonumber()")
         if isinstance(k, bool):
             return k
         return k
@@ -71,6 +74,21 @@ class LuaTable:
 
     def to_list(self):
         return [self.d[i] for i in range(1, self.length() + 1)]
+
+
+class CInt64:
+    """A 64-bit integer cdata.  LuaJIT boxes every int64_t / uint64_t value it
+    reads from C (a return value, an array element, a struct field): tonumber()
+    converts it, arithmetic with numbers stays 64-bit, comparisons work; here
+    math functions, 'for' limits, concatenation and use as a table key refuse
+    it, so a missing tonumber() in the Lua under test fails."""
+    __slots__ = ("v", "unsigned")
+
+    def __init__(self, v, unsigned=False):
+        v = int(v) % (1 << 64)
+        if not unsigned and v >= 1 << 63:
+            v -= 1 << 64
+        self.v, self.unsigned = v, unsigned
 
 
 class LuaFunction:
@@ -443,6 +461,8 @@ def tostr(v):
         return v
     if isinstance(v, CData):
         return f"cdata<{v.ct.name}>: 0x{v.address():x}"
+    if isinstance(v, CInt64):
+        return f"{v.v}{'ULL' if v.unsigned else 'LL'}"
     return f"{type(v).__name__}: 0x{id(v):x}"
 
 
@@ -477,7 +497,7 @@ def lua_type(v):
         return "string"
     if isinstance(v, LuaTable):
         return "table"
-    if isinstance(v, CData) or isinstance(v, CType):
+    if isinstance(v, (CData, CType, CInt64)):
         return "cdata"
     if callable(v):
         return "function"
@@ -623,7 +643,7 @@ class CData:
             st = self._struct()
             if st is None or k not in {f[0] for f in type(st)._fields_}:
                 raise LuaError(f"cdata<{self.ct.name}> has no field '{k}'")
-            return _from_c(getattr(st, k))
+            return _from_c(getattr(st, k), dict(type(st)._fields_)[k])
         et = self.ct.elem()
         i = int(k)
         if not self.is_pointer():
@@ -632,7 +652,7 @@ class CData:
             v = et.scalar_ctype().from_address(self.addr + i * et.size()).value
         if et.ptr:
             return CData(et, addr=v or 0)
-        return _from_c(v)
+        return _from_c(v, et.base)
 
     def setindex(self, k, v):
         if isinstance(k, str):
@@ -650,7 +670,7 @@ class CData:
             elif issubclass(ftype, ctypes.Array):
                 setattr(st, k, v.encode() if isinstance(v, str) else v)
             else:
-                n = tonum(v)
+                n = v.v if isinstance(v, CInt64) else tonum(v)
                 if n is None:
                     raise LuaError(f"cannot convert {lua_type(v)} to field '{k}'")
                 setattr(st, k, n if ftype in _FLOATS else int(n))
@@ -660,7 +680,7 @@ class CData:
         if et.ptr:
             val = _to_addr(v)
         else:
-            n = tonum(v)
+            n = v.v if isinstance(v, CInt64) else tonum(v)
             if n is None:
                 raise LuaError(f"cannot convert {lua_type(v)} to '{et.name}'")
             val = n if et.base in _FLOATS else int(n)
@@ -676,7 +696,13 @@ class CData:
         return CData(pt, addr=self.address() + int(n) * et.size())
 
 
-def _from_c(v):
+_INT64_SIGNED = (ctypes.c_longlong, ctypes.c_int64, ctypes.c_long)
+_INT64_UNSIGNED = (ctypes.c_ulonglong, ctypes.c_uint64, ctypes.c_ulong, ctypes.c_size_t)
+
+
+def _from_c(v, ctype=None):
+    if ctype is not None and ctypes.sizeof(ctype) == 8 and ctype in _INT64_SIGNED + _INT64_UNSIGNED:
+        return CInt64(v, ctype in _INT64_UNSIGNED)
     if isinstance(v, bytes):
         return v.decode(errors="replace")
     if isinstance(v, (int, float)) and not isinstance(v, bool):
@@ -764,6 +790,8 @@ class FFI:
         if isinstance(ct, str):
             ct = self.parse_type(ct)
         if ct.ptr and not ct.is_array():
+            if isinstance(v, CInt64):
+                return CData(ct, addr=v.v % (1 << 64))
             if isinstance(v, (int, float)) and not isinstance(v, bool):
                 return CData(ct, addr=int(v))
             return CData(ct, addr=_to_addr(v))
@@ -850,7 +878,7 @@ class CLib:
                 elif a.ptr:
                     conv.append(_to_addr(v))
                 else:
-                    n = tonum(v)
+                    n = v.v if isinstance(v, CInt64) else tonum(v)
                     if n is None:
                         raise LuaError(f"bad argument to '{name}': cannot convert {lua_type(v)} to a number")
                     conv.append(n if a.base in _FLOATS else int(n))
@@ -859,7 +887,7 @@ class CLib:
                 return None
             if ret.ptr:
                 return CData(ret, addr=r or 0)
-            return float(r)
+            return _from_c(r, ret.base)
         self.cache[name] = call
         return call
 
@@ -1149,6 +1177,8 @@ class LuaVM:
             v = self.eval(e[2], scopes)
             if e[1] == "not":
                 return not truthy(v)
+            if e[1] == "-" and isinstance(v, CInt64):
+                return CInt64(-v.v, v.unsigned)
             if e[1] == "-":
                 n = tonum(v)
                 if n is None:
@@ -1195,6 +1225,8 @@ class LuaVM:
             return lua_eq(a, b)
         if op == "~=":
             return not lua_eq(a, b)
+        if isinstance(a, CInt64) or isinstance(b, CInt64):
+            return self.int64_op(op, a, b, line)
         if op in ("<", ">", "<=", ">="):
             if isinstance(a, str) and isinstance(b, str):
                 pass
@@ -1225,6 +1257,31 @@ class LuaVM:
         if op == "^":
             return math.pow(x, y)
         raise LuaError(self._at(line) + f"unsupported operator {op}")
+
+    def int64_op(self, op, a, b, line):
+        """+ - * and comparisons with a 64-bit integer cdata operand (the other
+        a number or one too): the result is 64-bit, unsigned if either is."""
+        def val(x):
+            if isinstance(x, CInt64):
+                return x.v
+            if isinstance(x, (int, float)) and not isinstance(x, bool):
+                return int(x)
+            raise LuaError(self._at(line) + f"attempt to perform arithmetic on a {lua_type(x)} value")
+        if isinstance(a, CData):      # pointer + int64
+            if op == "+":
+                return a.add(val(b))
+            raise LuaError(self._at(line) + "attempt to perform arithmetic on a cdata value")
+        x, y = val(a), val(b)
+        uns = any(isinstance(t, CInt64) and t.unsigned for t in (a, b))
+        if op in ("<", ">", "<=", ">="):
+            return {"<": x < y, ">": x > y, "<=": x <= y, ">=": x >= y}[op]
+        if op == "+":
+            return CInt64(x + y, uns)
+        if op == "-":
+            return CInt64(x - y, uns)
+        if op == "*":
+            return CInt64(x * y, uns)
+        raise LuaError(self._at(line) + f"operator {op} on a 64-bit integer cdata is not supported here")
 
     # -- standard library (the parts the files use)
     def _install_stdlib(self):
@@ -1304,6 +1361,8 @@ class LuaVM:
             return tostr(v)
 
         def lua_tonumber(v, base=None):
+            if isinstance(v, CInt64):
+                return [float(v.v)]
             if base is not None:
                 try:
                     return [float(int(str(v).strip(), int(base)))]
@@ -1364,7 +1423,7 @@ class LuaVM:
                 v = args[ai] if ai < len(args) else None
                 ai += 1
                 if conv in "dioxXuc":
-                    n = tonum(v)
+                    n = v.v if isinstance(v, CInt64) else tonum(v)
                     if n is None:
                         raise LuaError(f"bad argument #{ai} to 'format' (number expected, got {lua_type(v)})")
                     out.append(("%" + spec + ("d" if conv in "iu" else conv)) % int(n) if conv != "c"
@@ -1516,6 +1575,13 @@ def lua_eq(a, b):
         return a is b
     if isinstance(a, (int, float)) and isinstance(b, (int, float)):
         return float(a) == float(b)
+    if isinstance(a, CInt64) or isinstance(b, CInt64):
+        def iv(x):
+            if isinstance(x, CInt64):
+                return x.v
+            return x if isinstance(x, (int, float)) else None
+        x, y = iv(a), iv(b)
+        return x is not None and y is not None and x == y
     if isinstance(a, str) and isinstance(b, str):
         return a == b
     if isinstance(a, CData) and isinstance(b, CData) and a.is_pointer() and b.is_pointer():

@@ -209,12 +209,36 @@ def test_ffi_arrays_structs_pointers():
     local f = ffi.new("float[3]", 1, 2, 3)
     local cp = ffi.cast("char*", arr) + 8
     local dp = ffi.cast("double*", cp)
-    return p[0], p[1], r.a, r.b, r.big, pp[0] == nil, f[2], dp[0], ffi.sizeof == nil
+    return p[0], p[1], r.a, r.b, tonumber(r.big), pp[0] == nil, f[2], dp[0], ffi.sizeof == nil
     '''
     with pytest.raises(LuaError, match="ffi.sizeof is not supported"):
         run(src)
     r = run(src.replace(", ffi.sizeof == nil", ""))
     assert r == [3.0, 4.5, 7.0, 0.25, 2.0 ** 40, True, 3.0, 1.5]
+
+
+def test_ffi_64bit_integers_are_boxed_as_luajit_does():
+    """A long long read from C is an int64 cdata: tonumber() converts it;
+    arithmetic with numbers stays 64-bit; math, 'for' limits, concatenation and
+    table keys need tonumber() first."""
+    src = r'''
+    local ffi = require("ffi")
+    local a = ffi.new("long long[2]")
+    local u = ffi.new("unsigned long long[1]")
+    a[0] = 2^40 a[1] = -3
+    u[0] = 5
+    local x = a[0]
+    return type(x), tonumber(x), x == 2^40, x + 1 == 2^40 + 1, tostring(a[1]), tostring(u[0] - 6),
+           x > 1, tonumber(a[1] * 2), ("%d"):format(a[1])
+    '''
+    r = run(src)
+    assert r[:4] == ["cdata", 2.0 ** 40, True, True]
+    assert r[4] == "-3LL" and r[5] == "18446744073709551615ULL"
+    assert r[6] is True and r[7] == -6.0 and r[8] == "-3"
+    for bad, msg in [("math.max(a[0], 1)", "not supported between"), ("for i = 1, a[0] do end", "'for' initial value"),
+                     ("local t = {} t[a[0]] = 1", "table key"), ("local s = 'n=' .. a[0]", "concatenate")]:
+        with pytest.raises(Exception, match=msg):
+            run('local ffi = require("ffi") local a = ffi.new("long long[1]") ' + bad)
 
 
 def test_ffi_arrays_are_bounds_checked():
@@ -233,9 +257,9 @@ def test_ffi_call_into_libc_and_string():
     local C = ffi.load(...)
     local buf = ffi.new("char[16]")
     C.memset(buf, 65, 5)
-    return C.strlen(buf), ffi.string(buf), ffi.string(buf, 3)
+    return tonumber(C.strlen(buf)), type(C.strlen(buf)), ffi.string(buf), ffi.string(buf, 3)
     '''
-    assert run(src, libc) == [5.0, "AAAAA", "AAA"]
+    assert run(src, libc) == [5.0, "cdata", "AAAAA", "AAA"]     # size_t comes back boxed
     with pytest.raises(LuaError, match="missing declaration"):
         run('local ffi = require("ffi") local C = ffi.load(...) return C.strlen', libc)
     assert run('return pcall(require("ffi").load, "no_such_library_here")')[0] is False
