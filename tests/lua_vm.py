@@ -1,18 +1,20 @@
 """A small Lua 5.1 interpreter with a LuaJIT-style ``ffi`` over ctypes, written
-for the tests: it runs lanternl_amd/lua/luatl_adapter.lua itself (against the
-real library on the GPU) where no Lua runtime exists (none in this image or on
-the GPU box).
+for the tests: it runs lanternl_amd/lua/luatl_adapter.lua and
+lanternl_amd/lua/lanternl_lm.lua themselves (against the real library on the
+GPU) where no Lua runtime exists (none in this image or on the GPU box).
 
-It covers the language the adapter and its tests use: locals, closures,
-numeric and generic ``for``, ``while``, ``repeat``, multiple results,
-varargs, tables with metatables (``__index``, ``__newindex``, ``__call``),
-method calls, ``pcall``/``error``, and the parts of ``string``, ``table``,
-``math``, ``os`` and ``debug`` those files call.  ``ffi`` supports ``cdef``
-of C prototypes and plain structs, ``load``, ``new``, ``typeof``, ``cast``,
-``gc``, ``string``, pointer and array indexing, pointer arithmetic and NULL
-comparisons.  Anything outside that raises, so a test cannot pass on an
-unimplemented feature.  Test infrastructure only; it is not part of the
-product.
+It covers the language those modules and their tests use: locals, closures
+(each capturing the variables it names), numeric and generic ``for``,
+``while``, ``repeat``, multiple results, varargs, tables with metatables
+(``__index``, ``__newindex``, ``__call``), method calls, ``pcall``/``error``
+with Lua's position prefixes, and the parts of ``string``, ``table``,
+``math``, ``os`` and ``debug`` those files call.  ``ffi`` supports ``cdef`` of
+C prototypes and plain structs (a second declaration of a name raises, as in
+LuaJIT), ``load``, ``new``, ``typeof``, ``cast``, ``gc``, ``string``, pointer
+and array indexing, pointer arithmetic, NULL comparisons, Lua strings passed
+as ``const char*``, and 64-bit integers from C boxed as LuaJIT boxes them.
+Anything outside that raises, so a test cannot pass on an unimplemented
+feature.  Test infrastructure only; it is not part of the product.
 """
 import ctypes
 import math
@@ -25,10 +27,11 @@ from tests.lua_lint import BINPRI, UNARY_PRI, LuaSyntaxError, tokenize
 
 # ---------------------------------------------------------------- values
 class LuaError(Exception):
-    def __init__(self, value, traceback=""):
+    """A Lua error; `value` is what error() was given (any Lua value)."""
+
+    def __init__(self, value):
         super().__init__(value)
         self.value = value
-        self.lua_traceback = traceback
 
 
 class LuaTable:
@@ -42,6 +45,8 @@ class LuaTable:
     def key(k):
         if isinstance(k, float) and k.is_integer():
             return int(k)
+        if isinstance(k, float) and math.isnan(k):
+            raise LuaError("table index is NaN")
         if isinstance(k, CInt64):
             raise LuaError("a 64-bit integer cdata used as a table key (LuaJIT keys cdata by identity); "
                            "convert it with tonumber()")
@@ -50,6 +55,8 @@ class LuaTable:
         return k
 
     def rawget(self, k):
+        if isinstance(k, float) and math.isnan(k):
+            return None                 # reading t[NaN] is nil; only assignment raises
         return self.d.get(self.key(k))
 
     def rawset(self, k, v):

@@ -191,6 +191,9 @@ def test_table_keys_normalise_integral_floats():
     assert run("local t = {} t[1] = 'a' t[1.0] = 'b' t[2] = 'c' return #t, t[1]") == [2.0, "b"]
     with pytest.raises(LuaError, match="table index is nil"):
         run("local t = {} t[nil] = 1")
+    assert run("local t = {} return t[0/0]") == [None]
+    with pytest.raises(LuaError, match="table index is NaN"):
+        run("local t = {} t[0/0] = 1")
 
 
 # ----------------------------------------------------------------- the FFI
