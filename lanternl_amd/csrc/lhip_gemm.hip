@@ -355,9 +355,10 @@ sgemm_mfma_kernel(const GemmArgs g)
 // s takes the K chunks s, s+KS, ... with its own double-buffered LDS, so each
 // SIMD holds KS waves and each set's chain of dependent chunk loads is KS
 // times shorter; the sets' partial tiles meet in LDS (fixed order).  For long
-// K on one or two 64x64 tiles per CU (1024^3: 35.7 us on one wave set, 28.2
-// on four).  PF = 2: two register sets per wave set, so chunk kt + 2 KS is in
-// flight while chunk kt runs and chunk kt + KS goes to LDS.
+// K on one or two 64x64 tiles per CU (1024^3: 29.1, 28.9-29.1 and 27.6-27.7 us
+// on one, four and two wave sets; split-K slices take four).  PF = 2: two
+// register sets per wave set, so chunk kt + 2 KS is in flight while chunk kt
+// runs and chunk kt + KS goes to LDS.
 template <int BM, int BN, int BK, bool TA, bool TB, int KS, int PF = 1, bool FULL = false>
 __global__ void __launch_bounds__(kThreads * KS)
 sgemm_mfma_ks_kernel(const GemmArgs g)
@@ -2627,10 +2628,11 @@ int sgemm_run(int ta, int tb, int m, int n, int k, float alpha,
     // short K (e.g. the LM head, K = dim): the whole K range in one LDS tile,
     // so a workgroup waits on one load round trip instead of one per 32-deep chunk
     if (tiles64 >= cus) {
-        // long K at one or two 64x64 tiles per CU: four or two wave sets per tile
-        if (g.K >= 512 && tiles64 <= cus) return launch_cfg_ks<64, 64, 32, 4>(ta, tb, g, batch, stream);
-        // shorter K at exactly one tile per CU (the C2 tied head, 512x2000x128:
-        // 1 us less per step): two wave sets, one 32-deep chunk in two each
+        // exactly one 64x64 tile per CU: two wave sets per tile, each taking
+        // every other 32-deep chunk (the C2 tied head, 512x2000x128: 1 us less
+        // per step; 1024^3 27.6-27.7 us against 28.9-29.1 on four sets, and
+        // 3-5% at 512x2048x1024 and 2048x512x768); up to two tiles per CU with
+        // long K: two wave sets as well
         if (g.K >= 64 && tiles64 <= cus) return launch_cfg_ks<64, 64, 32, 2>(ta, tb, g, batch, stream);
         if (g.K >= 512 && tiles64 <= 2 * cus) return launch_cfg_ks<64, 64, 32, 2>(ta, tb, g, batch, stream);
         // otherwise one wave set: the same kernel's two-chunk-ahead,
