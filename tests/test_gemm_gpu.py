@@ -72,10 +72,10 @@ def test_gemm_split_band_on_four_wave_sets(m, k, n):
 @pytest.mark.parametrize("m,k,n", [(1024, 1024, 1024), (1000, 777, 1030), (2048, 1024, 1024), (512, 128, 2000),
                                    (500, 100, 2040), (500, 1024, 2000), (510, 512, 2044), (60, 2048, 2000)])
 def test_gemm_two_wave_set_tiles(m, k, n):
-    """Mid-size products with long K on one or two 64x64 tiles per CU (four or
-    two wave sets taking every fourth or second K chunk; K = 777 ragged with a
-    chunk count that is not a multiple of the set count), short K at one tile
-    per CU on two wave sets (the C2 tied head 512x2000x128; K = 100 ragged),
+    """Mid-size products with long K on one or two 64x64 tiles per CU (two
+    wave sets taking every second K chunk; K = 777 ragged with an odd chunk
+    count), short K at one tile per CU on two wave sets as well (the C2 tied
+    head 512x2000x128; K = 100 ragged),
     all four transposition variants, and alpha / beta.  Whole 32-deep chunks
     take the unconditional-load form with rows and columns past M and N
     clamped: 500x1024x2000 (edge tiles in M and N), 510x512x2044 (M % 4 != 0:
@@ -613,3 +613,55 @@ def test_gemm_skinny_strided_views_and_matrix_multiply_gate():
     got = C.download()[:, :n]
     ref = O.mm(np.ascontiguousarray(big_a[1:1 + m, 2:2 + k]), np.ascontiguousarray(big_b[1:1 + k, 3:3 + n]))
     assert rel_fro(got, ref) <= TOL
+
+
+def _sweep_cases(rng, count):
+    """Shapes that take every branch of the dispatcher, then random ones
+    (log-uniform sizes, at most 1.5 Gflop each)."""
+    cases = [(1, 4096, 3000), (2, 300, 4000), (16, 3000, 2000), (48, 2048, 4096), (64, 1024, 2048),
+             (1024, 1024, 1024), (1000, 1030, 600), (512, 2000, 128), (2048, 1536, 512), (300, 2500, 64),
+             (1536, 1536, 256), (257, 129, 1), (3, 5, 7)]
+    while len(cases) < count:
+        m, n, k = (int(np.exp(rng.uniform(0, np.log(x)))) for x in (2600, 2600, 4100))
+        if m * n * k <= 750_000_000:
+            cases.append((m, n, k))
+    return cases
+
+
+def test_gemm_random_dispatch_sweep():
+    """Seeded random products over every dispatch branch (skinny, split band,
+    16x16 / 32x32 / 64x64 tiles on one, two and four wave sets, 128x128 and
+    256x256 tiles, split-K with its reduce), each with random transposes,
+    alpha and beta, leading dimensions padded past the logical rows and
+    operands that start one element past a 16-byte boundary; against float64
+    at the GEMM bar, and every padding element of C left as it was."""
+    rng = np.random.default_rng(20261202)
+    for i, (m, n, k) in enumerate(_sweep_cases(rng, 44)):
+        ta, tb = bool(rng.integers(0, 2)), bool(rng.integers(0, 2))
+        pad = [int(rng.choice([0, 0, 3, 4, 9])) for _ in range(3)]
+        off = [int(rng.integers(0, 2)) for _ in range(3)]
+        alpha = float(rng.choice([1.0, 0.5, -1.25]))
+        beta = float(rng.choice([0.0, 0.0, 1.0, -0.5]))
+        announce("gemm sweep", i, (m, n, k), "ta" if ta else "", "tb" if tb else "", pad, off, alpha, beta)
+        a = f32(rng.uniform(-1, 1, (m, k)))
+        b = f32(rng.uniform(-1, 1, (k, n)))
+        c0 = f32(rng.uniform(-1, 1, (m, n)))
+        sa = np.ascontiguousarray(a.T) if ta else a          # stored operand
+        sb = np.ascontiguousarray(b.T) if tb else b
+        lda, ldb, ldc = sa.shape[1] + pad[0], sb.shape[1] + pad[1], n + pad[2]
+        bufs = []
+        for x, ld, o in ((sa, lda, off[0]), (sb, ldb, off[1]), (c0, ldc, off[2])):
+            store = np.full(o + x.shape[0] * ld + 4, 7.0, np.float32)
+            store[o:o + x.shape[0] * ld].reshape(x.shape[0], ld)[:, :x.shape[1]] = x
+            bufs.append((device.Buffer.from_numpy(store), store, o, ld))
+        (A, _, oa, _), (B, _, ob, _), (C, cst, oc, _) = bufs
+        kernels.sgemm_raw(int(ta), int(tb), m, n, k, alpha, A.offset(oa), lda, B.offset(ob), ldb, beta,
+                          C.offset(oc), ldc)
+        device.sync()
+        out = C.download()
+        got = out[oc:oc + m * ldc].reshape(m, ldc)
+        ref = alpha * (a.astype(np.float64) @ b.astype(np.float64)) + beta * c0.astype(np.float64)
+        assert rel_fro(got[:, :n], ref) <= TOL, (i, m, n, k, ta, tb)
+        untouched = np.ones(out.shape, bool)
+        untouched[oc:oc + m * ldc].reshape(m, ldc)[:, :n] = False
+        assert np.array_equal(out[untouched], cst[untouched]), ("C written outside its rows", i, m, n, k)
