@@ -151,6 +151,59 @@ def test_softmax_equal_logits_known_answer():
 
 
 # ------------------------------------------------------------------ SwiGLU
+# widths on both sides of every size class of the row kernels: float4s per
+# lane (1, 2, 4, 8, 16: 256, 512, 1024, 2048 and 4096 columns), the
+# workgroup-per-row forms (3072, 4096), the generic path past 4096 and for
+# widths that are not a multiple of 4
+SWEEP_COLS = [1, 3, 252, 255, 256, 260, 508, 512, 516, 1020, 1024, 1028, 2044, 2048, 2052, 3068, 3072, 3076,
+              4092, 4096, 4100]
+
+
+def test_row_kernels_size_class_sweep():
+    """RMSNorm, softmax (random scale, causal prefix, offset and group) and
+    SwiGLU, forward and backward, at every SWEEP_COLS width with random row
+    counts (one width with enough rows for two rows per wave), against the
+    oracle at the row bar."""
+    rng = np.random.default_rng(1202)
+    for i, cols in enumerate(SWEEP_COLS):
+        rows = 4099 if cols == 1020 else int(rng.integers(1, 130))
+        announce("row sweep", i, rows, cols)
+        x = f32(rng.standard_normal((rows, cols)))
+        w = f32(rng.normal(1.0, 0.1, cols))
+        g = f32(rng.standard_normal((rows, cols)))
+        eps = float(rng.choice([1e-5, 1e-6]))
+        y_ref, inv_ref = O.rmsnorm_fwd(x, w, eps)
+        X, W, Y, INV, G = to_dev(x), to_dev(w), device.Buffer((rows, cols)), device.Buffer((rows,)), to_dev(g)
+        call("lhip_rmsnorm_fwd", X.ptr, W.ptr, Y.ptr, INV.ptr, rows, cols, eps)
+        assert rel_fro(dl(Y), y_ref) <= EW and rel_fro(dl(INV), inv_ref) <= EW, ("rmsnorm", rows, cols)
+        dx_ref, dw_ref = O.rmsnorm_bwd(x, w, inv_ref, g)
+        DX, DW = device.Buffer((rows, cols)), device.Buffer((cols,))
+        call("lhip_rmsnorm_bwd", X.ptr, W.ptr, INV.ptr, G.ptr, DX.ptr, DW.ptr, rows, cols, 0)
+        assert rel_fro(dl(DX), dx_ref) <= EW and rel_fro(dl(DW), dw_ref) <= EW, ("rmsnorm bwd", rows, cols)
+        scale = float(rng.choice([1.0, 0.25, 0.7]))
+        causal = int(rng.integers(0, 2))
+        offset = int(rng.integers(-2, 4)) if causal else 0
+        group = int(rng.choice([0, max(1, rows // 2)])) if causal else 0
+        xs = f32(rng.normal(0, 2.0, (rows, cols)))
+        ys_ref = softmax_ref(xs, scale, causal, offset, group or None)
+        XS, YS = to_dev(xs), device.Buffer((rows, cols))
+        call("lhip_softmax_fwd", XS.ptr, YS.ptr, rows, cols, scale, causal, offset, group)
+        ys = dl(YS)
+        assert rel_fro(ys, ys_ref) <= EW, ("softmax", rows, cols, causal, offset, group)
+        dxs_ref = softmax_bwd_ref(ys_ref, g, scale, causal, offset, group or None)
+        DXS = device.Buffer((rows, cols))
+        call("lhip_softmax_bwd", YS.ptr, G.ptr, DXS.ptr, rows, cols, scale, causal, offset, group, 0)
+        assert rel_fro(dl(DXS), dxs_ref) <= EW, ("softmax bwd", rows, cols, causal, offset, group)
+        gate = f32(rng.standard_normal((rows, cols)) * 3)
+        GT, UP, H = to_dev(gate), to_dev(x), device.Buffer((rows, cols))
+        call("lhip_swiglu_fwd", GT.ptr, cols, UP.ptr, cols, H.ptr, cols, rows, cols)
+        assert rel_fro(dl(H), O.swiglu_fwd(gate, x)) <= EW, ("swiglu", rows, cols)
+        dg_ref, du_ref = O.swiglu_bwd(gate, x, g)
+        DG, DU = device.Buffer((rows, cols)), device.Buffer((rows, cols))
+        call("lhip_swiglu_bwd", GT.ptr, cols, UP.ptr, cols, G.ptr, cols, DG.ptr, cols, DU.ptr, cols, rows, cols, 0)
+        assert rel_fro(dl(DG), dg_ref) <= EW and rel_fro(dl(DU), du_ref) <= EW, ("swiglu bwd", rows, cols)
+
+
 @pytest.mark.parametrize("rows,cols", [(64, 256), (4096, 4096), (17, 33), (3, 20), (7, 1028)])
 def test_swiglu_fwd_bwd(rows, cols):
     announce("swiglu", rows, cols)
