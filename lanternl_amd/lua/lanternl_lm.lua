@@ -273,6 +273,9 @@ function Step:set_windows(windows, lo, hi)
         local w = windows[lo + b]
         local n = 0
         if b < nw then
+            if type(w) ~= "table" or type(w[1]) ~= "table" or type(w[2]) ~= "table" then
+                error(("lanternl_lm[set_windows]: window %d is not an { inp, tgt, n } table"):format(lo + b), 2)
+            end
             n = w[3] or #w[1]
             if n < 1 or n > T or #w[1] < n or #w[2] < n then
                 error(("lanternl_lm[set_windows]: window %d holds %s tokens (1..%d, with as many targets)")

@@ -212,6 +212,9 @@ def test_errors(L):
     three = windows_lua(np.zeros((3, 8), np.int64), np.zeros((3, 8), np.int64), [8, 8, 8])
     with pytest.raises(LuaError, match="3 windows for a batch of 2"):
         L.m(step, "set_windows", three)
+    one = windows_lua(np.zeros((1, 8), np.int64), np.zeros((1, 8), np.int64), [8])
+    with pytest.raises(LuaError, match=r"window 2 is not an \{ inp, tgt, n \} table"):
+        L.m(step, "set_windows", one, 1.0, 2.0)          # hi past the list's end
     with pytest.raises(LuaError, match="o.lr is required"):
         L.m(step, "sgd", opts({}))
     with pytest.raises(LuaError, match=r"lanternl_lm\[load\]: .*\((ARG|SHAPE|UNSUPPORTED|NULL|DEVICE)\)"):
