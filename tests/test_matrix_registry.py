@@ -2,7 +2,7 @@
 probe reasons, threshold gate, fault counting and disablement, forced
 backends, strict validation, and that the CPU loops agree with the oracle
 (ai/core/matrix.lua:19-202, 514-660).  Backends are stubs, as a Lua test would
-pre-load them (SURVEY: the registry's own degradation is the fake-backend hook)."""
+pre-load them: the registry's own degradation path is the hook for a fake backend."""
 import types
 
 import numpy as np
