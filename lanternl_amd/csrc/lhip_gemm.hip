@@ -466,9 +466,16 @@ sgemm_mfma_ks_kernel(const GemmArgs g)
             if (kt + KS < nk) lstore_from(sa, sb, cur ^ 1);
             __syncthreads();
         };
+        // FULL: no branch around the second body (past the last iteration it
+        // only reloads the last chunk; its MFMAs and LDS store are skipped),
+        // so every path through the loop has the same loads in flight and each
+        // LDS store waits for its own chunk alone; behind the branch the
+        // compiler made the stores wait for the next chunk's loads as well
+        // (tied head 512x2000x128 NT 7.04 -> 6.88 us, 512x2048x1024 27.05 ->
+        // 26.71; a third register set, chunks three ahead, was 8-15% slower)
         for (int it = 0; it < iters; it += 2) {
             body(it, std::integral_constant<int, 0>{});
-            if (it + 1 < iters) body(it + 1, std::integral_constant<int, 1>{});
+            if (FULL || it + 1 < iters) body(it + 1, std::integral_constant<int, 1>{});
         }
     } else {
         lstore(0);
