@@ -2079,7 +2079,17 @@ __device__ __forceinline__ void block_sumsq_out(double v, double* ss_out, double
 // Placement: XCD x (blocks b with b % 8 == x) takes tiles [x*tp, (x+1)*tp)
 // first and then cp workgroups of column-sum jobs, each running up to
 // cs_per_wg 32-column blocks in turn, so no XCD holds more tiles than CUs.
-template <int KS, int BK>
+// BUF: the chunk loads are buffer loads whose records end at each operand's
+// last element, so rows past K read as zeros from the hardware's range check
+// with no branch, and every chunk load is issued on every path (past the last
+// chunk a load fetches zeros); the compiler's memory-count waits then hold
+// each LDS store for its own chunk only.  (Behind the per-lane bounds branches
+// it waited for every load in flight, the chunk two ahead included, before
+// each store and again before each iteration's loads.)  Columns past M or N
+// read whatever lies there instead of zeros: they only reach output rows and
+// columns that are never stored or counted.  The host takes this form when
+// every operand's byte offsets stay below 2^31.
+template <int KS, int BK, bool BUF = false>
 __global__ void __launch_bounds__(256 * KS) sgemm_grouped_tn_lds64_kernel(const GroupedTNArgs ga)
 {
     constexpr int T = 64, P = BK / 16;
@@ -2130,7 +2140,24 @@ __global__ void __launch_bounds__(256 * KS) sgemm_grouped_tn_lds64_kernel(const 
     // two register sets: a set's next-but-one chunk is in flight while the
     // current chunk's MFMAs run and the next chunk goes to LDS
     float4 ra0[P], rb0[P], ra1[P], rb1[P];
+    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+    // buffer records: (K - 1) full rows plus the last row's M (N) columns
+    const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(e.A), 0, BUF ? ((K - 1) * e.lda + e.M) * 4 : 0, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsb = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(e.B), 0, BUF ? ((K - 1) * e.ldb + e.N) * 4 : 0, 0x00020000);
     auto gload = [&](int k0, float4 (&ra)[P], float4 (&rb)[P]) {
+        if constexpr (BUF) {
+#pragma unroll
+            for (int p = 0; p < P; ++p) {
+                const int k = k0 + lrow + 16 * p;
+                ra[p] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                       rsa, (k * e.lda + m0 + lc4) * 4, 0, 0));
+                rb[p] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                       rsb, (k * e.ldb + n0 + lc4) * 4, 0, 0));
+            }
+            return;
+        }
 #pragma unroll
         for (int p = 0; p < P; ++p) {
             const int k = k0 + lrow + 16 * p;
@@ -2198,7 +2225,7 @@ __global__ void __launch_bounds__(256 * KS) sgemm_grouped_tn_lds64_kernel(const 
     const int nk = (K + BK - 1) / BK;
     const int iters = (nk + KS - 1) / KS;   // every set passes the same barriers
     gload(grp * BK, ra0, rb0);
-    if (iters > 1) gload((grp + KS) * BK, ra1, rb1);
+    if (BUF || iters > 1) gload((grp + KS) * BK, ra1, rb1);
     float sv[SC];             // rows of the first SC matches, fetched during the products
     unsigned srel[SC / 4];    // their rows within the wave's 32, 8 bits each (0xff: none)
     int first_total = 0;
@@ -2241,12 +2268,12 @@ __global__ void __launch_bounds__(256 * KS) sgemm_grouped_tn_lds64_kernel(const 
     // stores chunk it+1 (loaded an iteration earlier) into the other buffer
     // and issues the loads of chunk it+2
     for (int it = 0; it < iters; it += 2) {
-        if (it + 2 < iters) gload(((it + 2) * KS + grp) * BK, ra0, rb0);
+        if (BUF || it + 2 < iters) gload(((it + 2) * KS + grp) * BK, ra0, rb0);
         chunk_mfma(0, it * KS + grp);
         if (it + 1 < iters) lstore(1, ra1, rb1);
         __syncthreads();
-        if (it + 1 >= iters) break;
-        if (it + 3 < iters) gload(((it + 3) * KS + grp) * BK, ra1, rb1);
+        if (!BUF && it + 1 >= iters) break;   // BUF: the second half's MFMAs skip themselves
+        if (BUF || it + 3 < iters) gload(((it + 3) * KS + grp) * BK, ra1, rb1);
         chunk_mfma(1, (it + 1) * KS + grp);
         if (it + 2 < iters) lstore(0, ra0, rb0);
         __syncthreads();
@@ -2397,8 +2424,21 @@ int sgemm_grouped_tn(const GroupedTN* g, int ngroups, int K, hipStream_t stream,
             ex->fused = 1;
             ex->ss_parts = static_cast<int>(grid);
         }
-        if (K >= 512) klaunch(sgemm_grouped_tn_lds64_kernel<4, 32>, grid, 1024, 0, stream, ga);
-        else klaunch(sgemm_grouped_tn_lds64_kernel<2, kGroupedBK>, grid, 512, 0, stream, ga);
+        // buffer loads when every byte offset a chunk load can form (rows up
+        // to K plus the loads past the last chunk) stays below 2^31
+        bool buf = true;
+        for (int i = 0; i < ngroups; ++i) {
+            const long long rows = static_cast<long long>(K) + 512;
+            buf = buf && (rows * g[i].lda + 64) * 4 < (1LL << 31) && (rows * g[i].ldb + 64) * 4 < (1LL << 31);
+        }
+        if (K >= 512) {
+            if (buf) klaunch(sgemm_grouped_tn_lds64_kernel<4, 32, true>, grid, 1024, 0, stream, ga);
+            else klaunch(sgemm_grouped_tn_lds64_kernel<4, 32>, grid, 1024, 0, stream, ga);
+        } else if (buf) {
+            klaunch(sgemm_grouped_tn_lds64_kernel<2, kGroupedBK, true>, grid, 512, 0, stream, ga);
+        } else {
+            klaunch(sgemm_grouped_tn_lds64_kernel<2, kGroupedBK>, grid, 512, 0, stream, ga);
+        }
     }
     else if (vec) klaunch(sgemm_grouped_tn_lds_kernel, grid, 256, 0, stream, ga);
     else if (K >= 256) klaunch(sgemm_grouped_tn_kernel<8>, grid, 512, 0, stream, ga);

@@ -137,6 +137,19 @@ def test_lm_step_c2_embedding_scatter(B, id_hi):
     gpu.close()
 
 
+@pytest.mark.parametrize("B,T", [(8, 60), (9, 60)])
+def test_lm_step_c2_token_counts_off_the_chunk_grid(B, T):
+    """C2's dimensions with 480 and 540 tokens: the grouped weight-gradient
+    launch (224 tiles of 64x64) reduces over K = 480 on two wave sets of
+    64-deep chunks (7.5 chunks) and K = 540 on four sets of 32-deep chunks
+    (16.9), so its last chunk is partial and every load past K, including the
+    loads issued beyond the last chunk, must read zeros."""
+    announce("lm C2 tokens", B, T)
+    gpu, res = _run_case(2000, 128, 4, 8, 256, B, T, steps=2, lr=0.1, std=0.02, seed=71 + B)
+    _check(res)
+    gpu.close()
+
+
 def test_lm_argmax_and_correct_count_bit_exact():
     announce("lm argmax")
     V, D, L, H, F, B, T = 50, 16, 1, 2, 32, 2, 8
