@@ -105,7 +105,9 @@ local PER_LAYER = { "ln1", "wq", "wk", "wv", "wo", "ln2", "w1", "w3", "w2" }
 local function make_config(o)
     local cfg = ffi.new("lhip_lm_config_t")
     for _, k in ipairs({ "vocab", "dim", "layers", "heads", "ffn", "batch", "seq" }) do
-        if type(o[k]) ~= "number" then error(("lanternl_lm.new: option %s must be a number"):format(k), 3) end
+        if type(o[k]) ~= "number" or o[k] < 1 or o[k] % 1 ~= 0 then
+            error(("lanternl_lm.new: option %s must be a positive integer, got %s"):format(k, tostring(o[k])), 3)
+        end
         cfg[k] = o[k]
     end
     cfg.causal = (o.causal == nil or o.causal) and 1 or 0
@@ -225,6 +227,11 @@ local function check_model(self, params, what)
             error(("lanternl_lm[%s]: tensor %d (%s) is %sx%s, the configuration needs %dx%d")
                   :format(what, i, L.name, tostring(mtx.rows), tostring(mtx.cols), L.rows, L.cols), 3)
         end
+        if type(mtx.data) ~= "table" or #mtx.data ~= L.rows * L.cols then
+            error(("lanternl_lm[%s]: tensor %d (%s) holds %s values, its %dx%d shape needs %d")
+                  :format(what, i, L.name, type(mtx.data) == "table" and tostring(#mtx.data) or "no",
+                          L.rows, L.cols, L.rows * L.cols), 3)
+        end
     end
 end
 
@@ -277,7 +284,7 @@ function Step:set_windows(windows, lo, hi)
                 error(("lanternl_lm[set_windows]: window %d is not an { inp, tgt, n } table"):format(lo + b), 2)
             end
             n = w[3] or #w[1]
-            if n < 1 or n > T or #w[1] < n or #w[2] < n then
+            if type(n) ~= "number" or n % 1 ~= 0 or n < 1 or n > T or #w[1] < n or #w[2] < n then
                 error(("lanternl_lm[set_windows]: window %d holds %s tokens (1..%d, with as many targets)")
                       :format(lo + b, tostring(n), T), 2)
             end

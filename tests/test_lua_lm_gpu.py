@@ -215,6 +215,17 @@ def test_errors(L):
     one = windows_lua(np.zeros((1, 8), np.int64), np.zeros((1, 8), np.int64), [8])
     with pytest.raises(LuaError, match=r"window 2 is not an \{ inp, tgt, n \} table"):
         L.m(step, "set_windows", one, 1.0, 2.0)          # hi past the list's end
+    half = windows_lua(np.zeros((1, 8), np.int64), np.zeros((1, 8), np.int64), [8])
+    half.rawget(1.0).rawset(3.0, 2.5)                               # n = 2.5 tokens
+    with pytest.raises(LuaError, match=r"window 1 holds 2.5 tokens"):
+        L.m(step, "set_windows", half)
+    params.rawset(12.0, None)
+    params.rawget(3.0).rawget("data").rawset("cols", 16.0)
+    params.rawget(5.0).rawget("data").rawget("data").rawset(256.0, None)   # wv.1 short by one value
+    with pytest.raises(LuaError, match=r"tensor 5 \(wv.1\) holds 255 values, its 16x16 shape needs 256"):
+        L.m(step, "load_model", model)
+    with pytest.raises(LuaError, match="option layers must be a positive integer, got 1.5"):
+        L.new(dict(TINY, layers=1.5))
     with pytest.raises(LuaError, match="o.lr is required"):
         L.m(step, "sgd", opts({}))
     with pytest.raises(LuaError, match=r"lanternl_lm\[load\]: .*\((ARG|SHAPE|UNSUPPORTED|NULL|DEVICE)\)"):
