@@ -269,6 +269,11 @@ def _doubles(x, need, what):
 
 def _host_product(code, a, m, k, b, n):
     """The product as a float64 array of its rows*cols numbers."""
+    for d in (m, k, n):
+        if isinstance(d, bool) or not isinstance(d, (int, float, np.integer, np.floating)) or d < 0 or d % 1:
+            raise ValueError(f"lanternl_hip: {_OPNAME[code]} dimensions must be non-negative integers, "
+                             f"got {m} x {k} x {n}")
+    m, k, n = int(m), int(k), int(n)
     na, nb, nc = _extents(code, m, k, n)
     ad = _doubles(a, na, f"{_OPNAME[code]} operand a")
     bd = _doubles(b, nb, f"{_OPNAME[code]} operand b")

@@ -384,6 +384,12 @@ end
 
 -- the product in the result lane (a cdata double array) and its element count
 local function host_product(code, a, m, k, b, n)
+    for _, d in ipairs({ m, k, n }) do
+        if type(d) ~= "number" or d < 0 or d % 1 ~= 0 then
+            error(("lanternl_hip: %s dimensions must be non-negative integers, got %s x %s x %s")
+                  :format(OPNAME[code], tostring(m), tostring(k), tostring(n)), 3)
+        end
+    end
     local na, nb, nc = extents(code, m, k, n)
     count_or_fail(a, na, OPNAME[code] .. " operand a", 3)
     count_or_fail(b, nb, OPNAME[code] .. " operand b", 3)

@@ -85,6 +85,12 @@ def test_pin_rejects_a_wrong_element_count():
         ad.pin([1, 2, 3, 4, 5], 2, 2)
     with pytest.raises(ValueError, match="needs 6 numbers, the table holds 4"):
         ad.matmul([1, 2, 3, 4], 2, 3, [1, 0, 0, 1, 1, 1], 2)
+    with pytest.raises(ValueError, match="matmul dimensions must be non-negative integers, got 2.5 x 3 x 2"):
+        ad.matmul([1.0] * 6, 2.5, 3, [1.0] * 6, 2)
+    rd = [0.0] * 6
+    with pytest.raises(ValueError, match="matmul_tn dimensions must be non-negative integers, got 2 x 3 x -2"):
+        ad.matmul_into("tn", [1.0] * 6, 2, 3, [1.0] * 6, -2, rd, True)
+    assert rd == [0.0] * 6
     h = ad.pin([1.0, 2.0, 3.0, 4.0], 2, 2)
     with pytest.raises(ValueError, match="needs 4 numbers"):
         h.upload([1.0])

@@ -197,7 +197,13 @@ def test_matmul_into_errors_leave_rd_untouched(L):
         L("matmul_into", "nn", a, 2.0, 3.0, b, 3.0, LuaTable.from_list([0.0] * 5), True)
     with pytest.raises(LuaError, match="matmul operand b needs 9 numbers, the table holds 4"):
         L("matmul_into", "nn", a, 2.0, 3.0, flat(np.ones(4)), 3.0, rd, True)
+    with pytest.raises(LuaError, match="matmul_tn dimensions must be non-negative integers, got 2 x 3 x 1.5"):
+        L("matmul_into", "tn", a, 2.0, 3.0, b, 1.5, rd, True)
     assert rd.to_list() == rd0
+    with pytest.raises(LuaError, match="matmul dimensions must be non-negative integers, got 2.5 x 3 x 3"):
+        L("matmul", a, 2.5, 3.0, b, 3.0)
+    with pytest.raises(LuaError, match="matmul_nt dimensions must be non-negative integers, got -1 x 3 x 3"):
+        L("matmul_nt", a, -1.0, 3.0, b, 3.0)
 
 
 # ----------------------------------------------------------- the matrix.lua patch with this backend
