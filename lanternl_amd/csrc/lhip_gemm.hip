@@ -546,10 +546,11 @@ sgemm_mfma_ks_kernel(const GemmArgs g)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int row = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * lk + (r & 3);
-                if (row < M) {
+                if (row < M) {   // streamed out, not left dirty in L2 for the kernel's end
                     const float v = g.alpha * acc[i][j][r];
-                    C[static_cast<long long>(row) * g.ldc + col] =
-                        (g.beta != 0.f) ? v + g.beta * R[static_cast<long long>(row) * ldr + col] : v;
+                    __builtin_nontemporal_store(
+                        (g.beta != 0.f) ? v + g.beta * R[static_cast<long long>(row) * ldr + col] : v,
+                        &C[static_cast<long long>(row) * g.ldc + col]);
                 }
             }
         }
@@ -2333,7 +2334,7 @@ __global__ void __launch_bounds__(256 * KS) sgemm_grouped_tn_lds64_kernel(const 
         for (int r = 0; r < 16; ++r) {
             const int orow = m0 + wm + 8 * (r >> 2) + 4 * lk + (r & 3);
             if (orow < e.M) {
-                e.C[static_cast<long long>(orow) * e.ldc + ocol] = acc[r];
+                __builtin_nontemporal_store(acc[r], &e.C[static_cast<long long>(orow) * e.ldc + ocol]);
                 sq += static_cast<double>(acc[r]) * acc[r];
             }
         }
