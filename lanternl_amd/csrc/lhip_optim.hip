@@ -126,6 +126,7 @@ __device__ __forceinline__ void sgd_elem(float& p, float& g, float& v, const Sgd
 // (after scale and clip) so callers can inspect it, as optim2 mutates grads.
 // With vec (p, g, v 16-byte aligned) the body runs on float4; a thread's first
 // float4 is fetched before the norm is reduced, so the loads overlap it.
+typedef float sgd_f4 __attribute__((ext_vector_type(4)));
 __global__ void __launch_bounds__(256)
 sgd_step_kernel(float* __restrict__ p, float* __restrict__ g, float* __restrict__ v, long long n,
                 const double* __restrict__ sumsq, int nparts, float lr, float momentum, float wd,
@@ -170,9 +171,11 @@ sgd_step_kernel(float* __restrict__ p, float* __restrict__ g, float* __restrict_
             sgd_elem(pk, gk, vk, hy, clipf);
             st_lane(pv, k, pk); st_lane(gv, k, gk); st_lane(vv, k, vk);
         }
-        g4[i] = gv;
-        if (momentum > 0.f) v4[i] = vv;
-        p4[i] = pv;
+        // streamed out: v is read again by the next step's update, g is
+        // overwritten by the next backward, p is read by every XCD
+        __builtin_nontemporal_store(sgd_f4{gv.x, gv.y, gv.z, gv.w}, reinterpret_cast<sgd_f4*>(g4 + i));
+        if (momentum > 0.f) __builtin_nontemporal_store(sgd_f4{vv.x, vv.y, vv.z, vv.w}, reinterpret_cast<sgd_f4*>(v4 + i));
+        __builtin_nontemporal_store(sgd_f4{pv.x, pv.y, pv.z, pv.w}, reinterpret_cast<sgd_f4*>(p4 + i));
     }
     for (long long i = 4 * n4 + t0; i < n; i += stride) {
         float pk = p[i], gk = g[i], vk = momentum > 0.f ? v[i] : 0.f;
