@@ -126,7 +126,7 @@ __device__ __forceinline__ void sgd_elem(float& p, float& g, float& v, const Sgd
 // (after scale and clip) so callers can inspect it, as optim2 mutates grads.
 // With vec (p, g, v 16-byte aligned) the body runs on float4; a thread's first
 // float4 is fetched before the norm is reduced, so the loads overlap it.
-typedef float sgd_f4 __attribute__((ext_vector_type(4)));
+typedef float nt_f4 __attribute__((ext_vector_type(4)));
 __global__ void __launch_bounds__(256)
 sgd_step_kernel(float* __restrict__ p, float* __restrict__ g, float* __restrict__ v, long long n,
                 const double* __restrict__ sumsq, int nparts, float lr, float momentum, float wd,
@@ -173,9 +173,9 @@ sgd_step_kernel(float* __restrict__ p, float* __restrict__ g, float* __restrict_
         }
         // streamed out: v is read again by the next step's update, g is
         // overwritten by the next backward, p is read by every XCD
-        __builtin_nontemporal_store(sgd_f4{gv.x, gv.y, gv.z, gv.w}, reinterpret_cast<sgd_f4*>(g4 + i));
-        if (momentum > 0.f) __builtin_nontemporal_store(sgd_f4{vv.x, vv.y, vv.z, vv.w}, reinterpret_cast<sgd_f4*>(v4 + i));
-        __builtin_nontemporal_store(sgd_f4{pv.x, pv.y, pv.z, pv.w}, reinterpret_cast<sgd_f4*>(p4 + i));
+        __builtin_nontemporal_store(nt_f4{gv.x, gv.y, gv.z, gv.w}, reinterpret_cast<nt_f4*>(g4 + i));
+        if (momentum > 0.f) __builtin_nontemporal_store(nt_f4{vv.x, vv.y, vv.z, vv.w}, reinterpret_cast<nt_f4*>(v4 + i));
+        __builtin_nontemporal_store(nt_f4{pv.x, pv.y, pv.z, pv.w}, reinterpret_cast<nt_f4*>(p4 + i));
     }
     for (long long i = 4 * n4 + t0; i < n; i += stride) {
         float pk = p[i], gk = g[i], vk = momentum > 0.f ? v[i] : 0.f;
@@ -200,18 +200,34 @@ adamw_step_kernel(float* __restrict__ p, float* __restrict__ g, float* __restric
                   long long n, const double* __restrict__ sumsq, int nparts, float lr, float beta1, float beta2,
                   float eps, float wd, float grad_scale, float clip_norm, int t_in, int* __restrict__ tcount,
                   int parity, float* __restrict__ gnorm_out, int* __restrict__ applied_out,
-                  const float* __restrict__ hyper)
+                  const float* __restrict__ hyper, int vec)
 {
     if (hyper) {
         lr = hyper[0]; wd = hyper[2]; clip_norm = hyper[3];
         beta1 = hyper[5]; beta2 = hyper[6]; eps = hyper[7]; parity = hyper[8] != 0.f ? 1 : 0;
         grad_scale = hyper[9];
     }
+    const long long t0 = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
+    // float4 lanes (vec: every buffer 16-byte aligned); the first float4 of
+    // each operand is fetched before the norm is summed, so its loads overlap
+    // that reduction
+    const long long n4 = vec ? (n >> 2) : 0;
+    float4* p4 = reinterpret_cast<float4*>(p);
+    float4* g4 = reinterpret_cast<float4*>(g);
+    float4* m4 = reinterpret_cast<float4*>(m);
+    float4* v4 = reinterpret_cast<float4*>(v);
+    const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 pv = z4, gv = z4, mv = z4, vv = z4;
+    if (t0 < n4) {
+        gv = g4[t0];
+        mv = m4[t0];
+        vv = v4[t0];
+        pv = p4[t0];
+    }
     const double norm = static_cast<double>(grad_scale) * sqrt(grad_total(sumsq, nparts));
     const bool finite = isfinite(norm);
     const int t_old = tcount ? tcount[parity] : t_in - 1;
     const int t = t_old + 1;
-    const long long t0 = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
     if (t0 == 0) {
         if (gnorm_out) gnorm_out[0] = static_cast<float>(norm);
         if (applied_out) applied_out[0] = finite ? 1 : 0;
@@ -226,18 +242,42 @@ adamw_step_kernel(float* __restrict__ p, float* __restrict__ g, float* __restric
     const float decay = wd != 0.f ? lr * wd : 0.f;
     const float c1 = 1.0f - beta1, c2 = 1.0f - beta2;
     const long long stride = static_cast<long long>(gridDim.x) * blockDim.x;
-    for (long long i = t0; i < n; i += stride) {
-        float gk = g[i] * grad_scale;
+    auto elem = [&](float& pk, float& gk, float& mk, float& vk) {
+        gk = gk * grad_scale;
         if (clipf != 1.0f) gk = gk * clipf;
+        mk = beta1 * mk + c1 * gk;
+        vk = beta2 * vk + c2 * gk * gk;
+        const float denom = sqrtf(vk * inv_bc2) + eps;
+        if (decay != 0.f) pk = pk - decay * pk;
+        pk = pk - step_size * mk / denom;
+    };
+    for (long long i = t0; i < n4; i += stride) {
+        if (i != t0) {
+            gv = g4[i];
+            mv = m4[i];
+            vv = v4[i];
+            pv = p4[i];
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            float pk = ld_lane(pv, k), gk = ld_lane(gv, k), mk = ld_lane(mv, k), vk = ld_lane(vv, k);
+            elem(pk, gk, mk, vk);
+            st_lane(pv, k, pk); st_lane(gv, k, gk); st_lane(mv, k, mk); st_lane(vv, k, vk);
+        }
+        // streamed out: the moments are read again by the next step's
+        // update, the gradient is overwritten by the next backward
+        __builtin_nontemporal_store(nt_f4{gv.x, gv.y, gv.z, gv.w}, reinterpret_cast<nt_f4*>(g4 + i));
+        __builtin_nontemporal_store(nt_f4{mv.x, mv.y, mv.z, mv.w}, reinterpret_cast<nt_f4*>(m4 + i));
+        __builtin_nontemporal_store(nt_f4{vv.x, vv.y, vv.z, vv.w}, reinterpret_cast<nt_f4*>(v4 + i));
+        __builtin_nontemporal_store(nt_f4{pv.x, pv.y, pv.z, pv.w}, reinterpret_cast<nt_f4*>(p4 + i));
+    }
+    for (long long i = 4 * n4 + t0; i < n; i += stride) {
+        float pk = p[i], gk = g[i], mk = m[i], vk = v[i];
+        elem(pk, gk, mk, vk);
         g[i] = gk;
-        const float mk = beta1 * m[i] + c1 * gk;
-        const float vk = beta2 * v[i] + c2 * gk * gk;
         m[i] = mk;
         v[i] = vk;
-        const float denom = sqrtf(vk * inv_bc2) + eps;
-        float pk = p[i];
-        if (decay != 0.f) pk = pk - decay * pk;
-        p[i] = pk - step_size * mk / denom;
+        p[i] = pk;
     }
 }
 
@@ -318,10 +358,12 @@ int adamw_step(float* p, float* g, float* m, float* v, long long n, const double
     const int cus = st().cu_count > 0 ? st().cu_count : 256;
     long long blocks = (n + 255) / 256;
     if (blocks > 4LL * cus) blocks = 4LL * cus;
+    const int vec = (aligned16(p) && aligned16(g) && aligned16(m) && aligned16(v)) ? 1 : 0;
+    if (vec) blocks = std::min<long long>((n / 4 + 255) / 256, 4LL * cus);
     if (blocks < 1) blocks = 1;
     klaunch(adamw_step_kernel, static_cast<int>(blocks), 256, 0, s, p, g, m, v, n, sumsq_dev, nparts, lr, beta1, beta2,
                                                              eps, wd, grad_scale, clip_norm, t_in, tcount, parity,
-                                                             gnorm_out, applied_out, hyper_dev);
+                                                             gnorm_out, applied_out, hyper_dev, vec);
     return check_launch("adamw_step");
 }
 
