@@ -150,6 +150,30 @@ def test_lm_step_c2_token_counts_off_the_chunk_grid(B, T):
     gpu.close()
 
 
+def _random_configs(seed, count):
+    rng = np.random.default_rng(seed)
+    for _ in range(count):
+        H = int(rng.choice([1, 2, 3, 4, 8]))
+        hd = 2 * int(rng.integers(1, 49))
+        F = int(rng.integers(1, 97)) * 4 if rng.uniform() < 0.75 else int(rng.integers(3, 300))
+        yield dict(V=int(rng.integers(5, 3000)), D=H * hd, H=H, F=F, L=int(rng.integers(1, 4)),
+                   B=int(rng.integers(1, 11)), T=int(rng.integers(1, 81)), causal=bool(rng.integers(2)))
+
+
+@pytest.mark.parametrize("i,cfg", list(enumerate(_random_configs(2024, 12))))
+def test_lm_step_random_configurations(i, cfg):
+    """Seeded random shapes away from the hand-picked ones: any head count
+    and even head_dim up to 96, ffn widths that are not multiples of 4 (a
+    quarter of the draws), any vocabulary, 1-3 layers, 1-10 windows of 1-80
+    tokens, causal or not; two SGD steps each against the oracle."""
+    announce("lm random", i, cfg)
+    c = cfg
+    gpu, res = _run_case(c["V"], c["D"], c["L"], c["H"], c["F"], c["B"], c["T"], steps=2, lr=0.1, std=0.02,
+                         seed=500 + i, causal=c["causal"])
+    _check(res)
+    gpu.close()
+
+
 def test_lm_argmax_and_correct_count_bit_exact():
     announce("lm argmax")
     V, D, L, H, F, B, T = 50, 16, 1, 2, 32, 2, 8
