@@ -238,7 +238,8 @@ __global__ void __launch_bounds__(kAttnThreads) attn_fwd_kernel(const AttnArgs a
     __shared__ float rmax[4][16], rsum[4][16];
     const int T = a.T, hd = a.hd;
     const int nbt = round16(T) >> 4, nbd = round16(hd) >> 4, hd4 = (hd + 3) & ~3;
-    const int c = blockIdx.x % nbt, bh = blockIdx.x / nbt, b = bh / a.H, h = bh - b * a.H;
+    const int pid = xcd_pid(blockIdx.x, gridDim.x);   // window-major, XCD-contiguous (as the GEMMs' rows)
+    const int c = pid % nbt, bh = pid / nbt, b = bh / a.H, h = bh - b * a.H;
     const int lane = threadIdx.x & 63, r = lane & 15, q = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform: scalar branches
     const int i0 = 16 * c;
@@ -342,7 +343,8 @@ __global__ void __launch_bounds__(64 * kWaveJobs) attn_fwd_wave_kernel(const Att
 {
     const int T = a.T, hd = a.hd, D = a.D, pairs = hd >> 1;
     const int nbt = (T + 15) >> 4;
-    const int job = blockIdx.x * kWaveJobs + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // window-major jobs, XCD-contiguous: window b's jobs share the XCD of its rows in the GEMMs
+    const int job = xcd_pid(blockIdx.x, gridDim.x) * kWaveJobs + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (job >= a.B * a.H * nbt) return;
     const int c = job % nbt, bh = job / nbt, b = bh / a.H, h = bh - b * a.H;
     const int lane = threadIdx.x & 63, r = lane & 15, q = lane >> 4;
@@ -484,7 +486,8 @@ __global__ void __launch_bounds__(kAttnThreads) attn_bwd_kernel(const AttnArgs a
     const int T = a.T, hd = a.hd, D = a.D;
     const int T16 = round16(T), hd16 = round16(hd);
     const int nbt = T16 >> 4, nbd = hd16 >> 4, hd4 = (hd + 3) & ~3, pairs = hd >> 1;
-    const int c = blockIdx.x % nbt, bh = blockIdx.x / nbt, b = bh / a.H, h = bh - b * a.H;
+    const int pid = xcd_pid(blockIdx.x, gridDim.x);   // window-major, XCD-contiguous (as the GEMMs' rows)
+    const int c = pid % nbt, bh = pid / nbt, b = bh / a.H, h = bh - b * a.H;
     const int lane = threadIdx.x & 63, r = lane & 15, q = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform: scalar branches
     const long long ND = static_cast<long long>(a.N) * D;

@@ -143,10 +143,20 @@ inline int ceil_div(long long a, long long b) { return static_cast<int>((a + b -
 // XCD-contiguous chunks: workgroups are dispatched round-robin over the 8
 // XCDs, so id p runs on XCD p % 8; giving each XCD one contiguous run of
 // tiles (whole row bands) keeps each A row band in one XCD's L2.
-__device__ __forceinline__ void xcd_tile(int pid, int nwg, int tiles_n, int& tm, int& tn)
+// Workgroups are dealt to the 8 XCDs round-robin by index, and an XCD's L2
+// keeps its lines across launches: the logical index (pid % 8) * (nwg / 8) +
+// pid / 8 gives XCD x the contiguous range [x nwg/8, (x+1) nwg/8), so kernels
+// that order their work the same way (for the LM step: window-major) read
+// the previous kernel's output from their own L2.
+__device__ __forceinline__ int xcd_pid(int pid, int nwg)
 {
     constexpr int kXcds = 8;
-    if ((nwg % kXcds) == 0) pid = (pid % kXcds) * (nwg / kXcds) + pid / kXcds;
+    return (nwg % kXcds) == 0 ? (pid % kXcds) * (nwg / kXcds) + pid / kXcds : pid;
+}
+
+__device__ __forceinline__ void xcd_tile(int pid, int nwg, int tiles_n, int& tm, int& tn)
+{
+    pid = xcd_pid(pid, nwg);
     tm = pid / tiles_n;
     tn = pid - tm * tiles_n;
 }
