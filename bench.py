@@ -130,6 +130,53 @@ def kernel_ms(fn, calls, warmup=1):
     return float(np.median(per_call)), kpc
 
 
+# Operand arena.  Every GEMM and bandwidth case carves its buffer sets from one
+# device allocation made once per process, so no case allocates or frees
+# device memory: freeing a case's sets (hundreds of MB) and allocating the
+# next case's slowed that next case's first calls -- the first 20 calls of an
+# in-place RoPE case right after the RMSNorm backward had freed its 528 MB of
+# sets took 7.0 us each against 6.44 us from the 25th call on, whichever RoPE
+# case came first, while a RoPE case after another RoPE case did not show it.
+_ARENA = {"buf": None, "top": 0, "cls": None}
+_ARENA_BYTES = 1 << 30          # the largest case (8192^3 GEMM, 3 x 256 MB) fits
+_ARENA_ALIGN = 2 << 20          # each array starts on a 2 MB boundary, as hipMalloc places large ones
+
+
+def arena_reset():
+    """Make the whole arena free again: the previous case's arrays are dead."""
+    from lanternl_amd import device
+    if _ARENA["buf"] is None:
+        _ARENA["buf"] = device.Buffer((_ARENA_BYTES // 4,))
+
+        class ArenaBuffer(device.Buffer):
+            """A device array inside the arena.  Same interface as Buffer; the
+            arena owns the memory, so free() only drops the address."""
+
+            def __init__(self, addr, shape, dtype):
+                self.shape = tuple(int(s) for s in shape)
+                self.dtype = np.dtype(dtype)
+                self.size = int(np.prod(self.shape)) if self.shape else 1
+                self.nbytes = self.size * self.dtype.itemsize
+                self._p = ctypes.c_void_p(addr)
+
+            def free(self):
+                self._p = None
+        _ARENA["cls"] = ArenaBuffer
+    _ARENA["top"] = 0
+
+
+def arena_take(shape, dtype=np.float32, host=None):
+    """A device array of `shape` from the arena, filled from `host` if given."""
+    shape = shape if isinstance(shape, tuple) else (shape,)
+    nbytes = int(np.prod(shape)) * np.dtype(dtype).itemsize
+    top = _ARENA["top"]
+    if top + nbytes > _ARENA_BYTES:
+        raise RuntimeError(f"bench arena: {top + nbytes} bytes needed, the arena holds {_ARENA_BYTES}")
+    _ARENA["top"] = top + -(-max(nbytes, 4) // _ARENA_ALIGN) * _ARENA_ALIGN
+    buf = _ARENA["cls"](_ARENA["buf"].ptr + top, shape, dtype)
+    return buf.upload(host) if host is not None else buf
+
+
 def xcd_traffic_floor(m, n, k, xcds=8):
     """Least bytes an m x n x k fp32 product moves between the XCDs' L2s and
     memory when each XCD computes a block of the output: an XCD taking 1/q of
@@ -167,11 +214,12 @@ def bench_gemm(m, n, k, ta=False, tb=False, steps=20, warmup=3, seed=0, rotate=F
     b_shape = (n, k) if tb else (k, n)
     nbytes = 4.0 * (m * k + k * n + m * n)
     nsets = max(1, -(-2 * MALL_BYTES // int(nbytes))) if rotate else 1
+    arena_reset()
     sets = []
     for _ in range(nsets):
-        A = device.Buffer.from_numpy(rng.uniform(-1, 1, a_shape).astype(np.float32))
-        B = device.Buffer.from_numpy(rng.uniform(-1, 1, b_shape).astype(np.float32))
-        sets.append((A, B, device.Buffer((m, n))))
+        A = arena_take(a_shape, host=rng.uniform(-1, 1, a_shape).astype(np.float32))
+        B = arena_take(b_shape, host=rng.uniform(-1, 1, b_shape).astype(np.float32))
+        sets.append((A, B, arena_take((m, n))))
 
     def run(i):
         A, B, C = sets[i % nsets]
@@ -500,25 +548,24 @@ def run_gemm_suite(args):
 # ------------------------------------------------------------ bandwidth kernels
 def bench_bandwidth(name, nbytes, make_set, launch, steps, warmup, only=None):
     """Rotate over enough independent buffer sets that one pass over them
-    exceeds the 256 MB Infinity Cache, so the timed traffic is HBM traffic."""
+    exceeds the 256 MB Infinity Cache, so the timed traffic is HBM traffic.
+    make_set(i) builds set i from the operand arena (arena_take)."""
     if only and only not in name:
         return None
     nsets = max(2, -(-2 * MALL_BYTES // int(nbytes)))
+    arena_reset()
     sets = [make_set(i) for i in range(nsets)]
 
     def run(i):
         launch(sets[i % nsets])
-    # one call on every set first: the sets are fresh allocations, and a
-    # set's first use pays its address translations, which a warm-up over
-    # fewer calls than sets left inside the timed calls
+    # one call on every set first: a set's first use pays its address
+    # translations, which a warm-up over fewer calls than sets left inside
+    # the timed calls
     for i in range(nsets):
         run(i)
     ms_events = time_launches(run, steps, warmup, recorded=True)
     ms, kpc = kernel_ms(run, steps)
     gbps = nbytes / (ms * 1e-3) / 1e9
-    for st_ in sets:
-        for buf in st_:
-            buf.free()
     return {"suite": "bandwidth", "kernel": name, "ms": ms, "ms_events": ms_events, "kernels_per_call": kpc,
             "bytes": nbytes, "gbps": gbps, "frac": gbps / PEAK_HBM_GBPS, "buffer_sets": nsets}
 
@@ -537,25 +584,29 @@ def bandwidth_cases(steps, warmup, only=None, references=True):
     T, Dm, Fm = 4096, 1024, 4096
     host = {}
 
-    def arr(*shape, scale=1.0, loc=0.0):
+    def host_arr(shape, scale, loc):
         key = (shape, scale, loc)
         if key not in host:
             host[key] = (rng.standard_normal(shape) * scale + loc).astype(np.float32)
-        return B.from_numpy(host[key])
+        return host[key]
+
+    def arr(*shape, scale=1.0, loc=0.0):   # a buffer set's input, in the arena
+        return arena_take(shape, host=host_arr(shape, scale, loc))
+    new = arena_take                       # a buffer set's output, in the arena
 
     out = []
     # RMSNorm 4096 x 1024 (eps 1e-6, gain N(1, 0.1))
-    w = arr(Dm, scale=0.1, loc=1.0)
+    w = B.from_numpy(host_arr((Dm,), 0.1, 1.0))
     nb = 4 * (2 * T * Dm + Dm + T)
     out.append(bench_bandwidth("rmsnorm_fwd 4096x1024", nb,
-                               lambda i: (arr(T, Dm), B((T, Dm)), B((T,))),
+                               lambda i: (arr(T, Dm), new((T, Dm)), new((T,))),
                                lambda s: call("lhip_rmsnorm_fwd", s[0].ptr, w.ptr, s[1].ptr, s[2].ptr, T, Dm, 1e-6),
                                steps, warmup, only))
     nb = 4 * (3 * T * Dm + 2 * Dm + T)
     inv = B.from_numpy(np.ones(T, np.float32))
     dw = B((Dm,))
     out.append(bench_bandwidth("rmsnorm_bwd 4096x1024", nb,
-                               lambda i: (arr(T, Dm), arr(T, Dm, scale=0.5), B((T, Dm))),
+                               lambda i: (arr(T, Dm), arr(T, Dm, scale=0.5), new((T, Dm))),
                                lambda s: call("lhip_rmsnorm_bwd", s[0].ptr, w.ptr, inv.ptr, s[1].ptr, s[2].ptr,
                                               dw.ptr, T, Dm, 0),
                                steps, warmup, only))
@@ -573,29 +624,29 @@ def bandwidth_cases(steps, warmup, only=None, references=True):
     # SwiGLU 4096 x 4096
     n = T * Fm
     out.append(bench_bandwidth("swiglu_fwd 4096x4096", 4 * 3 * n,
-                               lambda i: (arr(T, Fm), arr(T, Fm, scale=0.5), B((T, Fm))),
+                               lambda i: (arr(T, Fm), arr(T, Fm, scale=0.5), new((T, Fm))),
                                lambda s: call("lhip_swiglu_fwd", s[0].ptr, Fm, s[1].ptr, Fm, s[2].ptr, Fm, T, Fm),
                                steps, warmup, only))
     out.append(bench_bandwidth("swiglu_bwd 4096x4096", 4 * 5 * n,
-                               lambda i: (arr(T, Fm), arr(T, Fm, scale=0.5), arr(T, Fm, scale=0.25), B((T, Fm)),
-                                          B((T, Fm))),
+                               lambda i: (arr(T, Fm), arr(T, Fm, scale=0.5), arr(T, Fm, scale=0.25), new((T, Fm)),
+                                          new((T, Fm))),
                                lambda s: call("lhip_swiglu_bwd", s[0].ptr, Fm, s[1].ptr, Fm, s[2].ptr, Fm, s[3].ptr,
                                               Fm, s[4].ptr, Fm, T, Fm, 0),
                                steps, warmup, only))
     # row softmax 4096 x 4096, scores N(0, 4) (sigma 2)
     out.append(bench_bandwidth("softmax_fwd 4096x4096", 4 * 2 * n,
-                               lambda i: (arr(T, T, scale=2.0), B((T, T))),
+                               lambda i: (arr(T, T, scale=2.0), new((T, T))),
                                lambda s: call("lhip_softmax_fwd", s[0].ptr, s[1].ptr, T, T, 1.0, 0, 0, 0),
                                steps, warmup, only))
     out.append(bench_bandwidth("softmax_bwd 4096x4096", 4 * 3 * n,
-                               lambda i: (arr(T, T, scale=0.01, loc=1.0 / T), arr(T, T), B((T, T))),
+                               lambda i: (arr(T, T, scale=0.01, loc=1.0 / T), arr(T, T), new((T, T))),
                                lambda s: call("lhip_softmax_bwd", s[0].ptr, s[1].ptr, s[2].ptr, T, T, 1.0, 0, 0, 0, 0),
                                steps, warmup, only))
     # C3 fused softmax + CE: 512 x 32000 logits, labels uniform
     R, V = 512, 32000
     labels = B.from_numpy(rng.integers(0, V, R).astype(np.int32), np.int32)
     out.append(bench_bandwidth("ce_fused 512x32000", 4 * (2 * R * V + 2 * R),
-                               lambda i: (arr(R, V), B((R, V)), B((R,))),
+                               lambda i: (arr(R, V), new((R, V)), new((R,))),
                                lambda s: call("lhip_ce_fused", s[0].ptr, labels.ptr, s[2].ptr, s[1].ptr, R, V, -1,
                                               1.0 / R),
                                steps, warmup, only))
@@ -605,7 +656,7 @@ def bandwidth_cases(steps, warmup, only=None, references=True):
         for rows, cols in ((T, Dm), (T, Fm)):
             n = rows * cols
             out.append(bench_bandwidth(f"reference silu {rows}x{cols} (1 read + 1 write)", 4 * 2 * n,
-                                       lambda i, r_=rows, c_=cols: (arr(r_, c_), B((r_ * c_,))),
+                                       lambda i, r_=rows, c_=cols: (arr(r_, c_), new((r_ * c_,))),
                                        lambda s, n_=n: call("lhip_silu", s[0].ptr, s[1].ptr, n_),
                                        steps, warmup, only))
             out.append(bench_bandwidth(f"reference silu in place {rows}x{cols} (1 read + 1 write)", 4 * 2 * n,
@@ -614,7 +665,7 @@ def bandwidth_cases(steps, warmup, only=None, references=True):
                                        steps, warmup, only))
             out.append(bench_bandwidth(f"reference add {rows}x{cols} (2 reads + 1 write)", 4 * 3 * n,
                                        lambda i, r_=rows, c_=cols: (arr(r_, c_), arr(r_, c_, scale=0.5),
-                                                                    B((r_ * c_,))),
+                                                                    new((r_ * c_,))),
                                        lambda s, n_=n: call("lhip_add", s[0].ptr, s[1].ptr, s[2].ptr, n_),
                                        steps, warmup, only))
     return [r for r in out if r is not None]
