@@ -8,6 +8,7 @@ launched eagerly on the library stream (`--graph`: replayed from a captured
 hipGraph instead).  Prints ONE JSON line: steps/s, a `roofline` object
 for the step's dominant kernel (timed live on the library stream with the
 library's kernel timer), a `gemm4096` object (the 4096^3 NN GEMM measured in the same run),
+a `gemm_shapes` object (the GEMM suite's other C1/C3/C5 shapes, same run),
 a `bandwidth` object (the C3/C4 bandwidth kernels measured in the same run)
 and a `cpu_baseline` object (the CPU oracle -- a single-threaded C
 restatement of lanternl's pure-Lua loops in double -- timed on this host).
@@ -77,7 +78,10 @@ def _cpu_model():
     return platform.processor() or "unknown"
 
 
-def time_launches(fn, steps, warmup, recorded=False):
+SETTLE_MS = 30.0                # back-to-back GPU time before a per-call measurement (time_launches)
+
+
+def time_launches(fn, steps, warmup, recorded=False, settle_ms=0.0):
     """Average ms per call of fn(i) over `steps` back-to-back calls, bracketed by
     hipEvents recorded on the library stream (where fn enqueues its kernels).
 
@@ -85,7 +89,15 @@ def time_launches(fn, steps, warmup, recorded=False):
     the library workspace), the `steps` calls are recorded once as a program
     (lhip_program_begin/end) and the timed region is one replay of it, so the
     kernels run back to back on the device with no Python or host launch cost
-    between them.  fn must then only enqueue work."""
+    between them.  fn must then only enqueue work.
+
+    settle_ms (recorded only): before the timed replay, replay the program
+    until at least this much back-to-back GPU time has run.  The GPU's clocks
+    follow its recent load, so without it the timed replay and a per-call
+    measurement right after it (kernel_ms) would depend on `steps`: 1024^3 NN
+    read 26.3 us per call after a 20-call replay, 24.1-24.5 us after 10 ms of
+    back-to-back replays and 23.0-23.3 us after 30, 60 or 100 ms (the C3
+    logits product 53-55, 49 and 46.2 us), from the first call on."""
     from lanternl_amd import device
     for i in range(max(warmup, 1 if recorded else 0)):
         fn(i)
@@ -95,6 +107,15 @@ def time_launches(fn, steps, warmup, recorded=False):
         prog = device.Program.record(lambda: [fn(i) for i in range(steps)])
         prog.replay()            # first replay uploads the graph
         device.sync()
+        busy = 0.0
+        for _ in range(100000):
+            if busy >= settle_ms:
+                break
+            t.start()
+            prog.replay()
+            t.stop()
+            device.sync()
+            busy += t.ms()
         t.start()
         prog.replay()
         t.stop()
@@ -228,7 +249,7 @@ def bench_gemm(m, n, k, ta=False, tb=False, steps=20, warmup=3, seed=0, rotate=F
     # address translations; a shorter warm-up left that in the timed calls)
     for i in range(nsets):
         run(i)
-    ms_events = time_launches(run, steps, warmup, recorded=True)
+    ms_events = time_launches(run, steps, warmup, recorded=True, settle_ms=SETTLE_MS)
     ms, kpc = kernel_ms(run, steps)
     flops = 2.0 * m * n * k
     tflops = flops / (ms * 1e-3) / 1e12
@@ -277,7 +298,7 @@ def dominant_kernel_c2(steps, warmup):
     def run(_):
         kernels.sgemm_batched_reduce(0, 1, N, D, F, 1.0, dzu.ptr, F, N * F, w13.ptr, F, D * F, 0.0, out.ptr, D, 2)
     calls = max(steps, 50)
-    ms_events = time_launches(run, calls, warmup, recorded=True)
+    ms_events = time_launches(run, calls, warmup, recorded=True, settle_ms=SETTLE_MS)
     ms, kpc = kernel_ms(run, calls)
     flops = 2.0 * N * D * (2 * F)
     tflops = flops / (ms * 1e-3) / 1e12
@@ -370,6 +391,7 @@ def run_lm_workload(args):
                                          "kernel_ms_events: hipEvents around a recorded replay of back-to-back "
                                          "launches (includes launch gaps)"},
         "gemm4096": g4,
+        "gemm_shapes": gemm_shapes_object(args),
         "bandwidth": bandwidth_object(args),
         "cpu_baseline": cpu_baseline_lm(),
     }
@@ -509,23 +531,56 @@ def bench_host_spin(m=256, k=128, n=256, reps=200, gap_us=200.0):
     return out
 
 
-def run_gemm_suite(args):
-    from lanternl_amd import device
-    device.init(0)
-    cases = [(n, n, n, False, False) for n in (1024, 2048, 4096, 8192)]
+def gemm_cases(big=True):
+    """The GEMM suite's shapes (m, n, k, transa, transb): C5 squares (8192^3
+    with `big`), skinny M against a 4096x4096 operand, 4096^3 transposed,
+    C1 and the C3 LM-head products."""
+    cases = [(n, n, n, False, False) for n in ((1024, 2048, 4096, 8192) if big else (1024, 2048))]
     cases += [(m, 4096, 4096, False, False) for m in (1, 16, 64)]
     cases += [(4096, 4096, 4096, True, False), (4096, 4096, 4096, False, True)]
     cases += [(256, 256, 128, False, False), (256, 256, 128, True, False), (256, 256, 128, False, True)]
     # C3: LM head logits, dW (A^T.B) and dhidden (A.B^T)
     cases += [(512, 32000, 128, False, False), (128, 32000, 512, True, False), (512, 128, 32000, False, True)]
-    for m, n, k, ta, tb in cases:
-        steps = max(5, min(args.steps, int(4e12 / (2.0 * m * n * k)) + 5))
-        # the HBM-bound shapes (skinny M, C3's 32000-wide operands) rotate
-        # operand sets past the Infinity Cache
-        hbm = m <= 64 or max(m, n, k) == 32000
-        r = bench_gemm(m, n, k, ta, tb, steps=max(steps, 20) if hbm else steps, warmup=args.warmup, rotate=hbm)
-        r["hbm_gbps_algorithmic"] = r["bytes"] / (r["ms"] * 1e-3) / 1e9
-        r["hbm_frac"] = r["hbm_gbps_algorithmic"] / PEAK_HBM_GBPS
+    return cases
+
+
+def bench_gemm_case(m, n, k, ta, tb, steps, warmup):
+    """bench_gemm with the suite's call count (fewer calls for the long
+    products) and operand rotation for the HBM-bound shapes (skinny M, C3's
+    32000-wide operands), plus the algorithmic HBM rate."""
+    steps = max(5, min(steps, int(4e12 / (2.0 * m * n * k)) + 5))
+    hbm = m <= 64 or max(m, n, k) == 32000
+    r = bench_gemm(m, n, k, ta, tb, steps=max(steps, 20) if hbm else steps, warmup=warmup, rotate=hbm)
+    r["hbm_gbps_algorithmic"] = r["bytes"] / (r["ms"] * 1e-3) / 1e9
+    r["hbm_frac"] = r["hbm_gbps_algorithmic"] / PEAK_HBM_GBPS
+    return r
+
+
+def gemm_shapes_object(args):
+    """The GEMM suite's shapes other than 4096^3 NN (in `gemm4096`) and
+    8192^3, measured in the default run with the suite's method: kernel-timer
+    ms per call (every kernel the call launches), TFLOP/s and fraction of the
+    fp32 MFMA peak, algorithmic HBM fraction."""
+    t0 = time.perf_counter()
+    out = {}
+    for m, n, k, ta, tb in gemm_cases(big=False):
+        r = bench_gemm_case(m, n, k, ta, tb, min(max(args.steps, 5), 20), min(args.warmup, 3) or 1)
+        out[f"{m}x{n}x{k} {r['op']}"] = {"ms": round(r["ms"], 6), "tflops": round(r["tflops"], 2),
+                                         "frac": round(r["frac"], 4), "hbm_frac": round(r["hbm_frac"], 4),
+                                         "kernels_per_call": r["kernels_per_call"],
+                                         "buffer_sets": r["buffer_sets"]}
+    return {"peak_tflops": PEAK_FP32_MFMA_TFLOPS, "peak_gbps": PEAK_HBM_GBPS,
+            "method": "kernel timer (dispatch start to end, median over calls each launched alone, summed over "
+                      "the call's kernels, after at least 30 ms of back-to-back replays); operand sets rotated past the 256 MB Infinity Cache for M <= 64 and "
+                      "the 32000-wide C3 products; hbm_frac = (A + B + C fp32 bytes) / ms / 8 TB/s",
+            "seconds": round(time.perf_counter() - t0, 2), "shapes": out}
+
+
+def run_gemm_suite(args):
+    from lanternl_amd import device
+    device.init(0)
+    for m, n, k, ta, tb in gemm_cases():
+        r = bench_gemm_case(m, n, k, ta, tb, args.steps, args.warmup)
         print(json.dumps({"suite": "gemm", **r}), flush=True)
     # the host-table boundary (PCIe and fp64 <-> fp32 conversions included),
     # against the PCIe floor of its fp32 bytes plus the device GEMM
@@ -563,7 +618,7 @@ def bench_bandwidth(name, nbytes, make_set, launch, steps, warmup, only=None):
     # the timed calls
     for i in range(nsets):
         run(i)
-    ms_events = time_launches(run, steps, warmup, recorded=True)
+    ms_events = time_launches(run, steps, warmup, recorded=True, settle_ms=SETTLE_MS)
     ms, kpc = kernel_ms(run, steps)
     gbps = nbytes / (ms * 1e-3) / 1e9
     return {"suite": "bandwidth", "kernel": name, "ms": ms, "ms_events": ms_events, "kernels_per_call": kpc,
@@ -680,7 +735,7 @@ def bandwidth_object(args):
     kernels = {r["kernel"]: {"ms": round(r["ms"], 6), "bytes": r["bytes"], "gbps": round(r["gbps"], 1),
                              "frac": round(r["frac"], 4), "kernels_per_call": r["kernels_per_call"]} for r in res}
     return {"peak_gbps": PEAK_HBM_GBPS, "method": "kernel timer (dispatch start to end, median of 20 calls each "
-            "launched alone), buffer sets rotated past the 256 MB Infinity Cache; bytes = each input read once "
+            "launched alone, after at least 30 ms of back-to-back replays), buffer sets rotated past the 256 MB Infinity Cache; bytes = each input read once "
             "plus each output written once (fp32)", "seconds": round(time.perf_counter() - t0, 2),
             "kernels": kernels}
 
