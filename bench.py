@@ -91,13 +91,13 @@ def time_launches(fn, steps, warmup, recorded=False, settle_ms=0.0):
     kernels run back to back on the device with no Python or host launch cost
     between them.  fn must then only enqueue work.
 
-    settle_ms (recorded only): before the timed replay, replay the program
-    until at least this much back-to-back GPU time has run.  The GPU's clocks
-    follow its recent load, so without it the timed replay and a per-call
-    measurement right after it (kernel_ms) would depend on `steps`: 1024^3 NN
-    read 26.3 us per call after a 20-call replay, 24.1-24.5 us after 10 ms of
-    back-to-back replays and 23.0-23.3 us after 30, 60 or 100 ms (the C3
-    logits product 53-55, 49 and 46.2 us), from the first call on."""
+    settle_ms (recorded only): before the timed replay, launch the calls
+    eagerly until at least this much back-to-back GPU time has run.  The
+    GPU's clocks follow its recent load, so without it the timed replay and a
+    per-call measurement right after it (kernel_ms) would depend on `steps`:
+    1024^3 NN read 26.3 us per call after a 20-call replay, 24.1-24.7 us after
+    10 ms of back-to-back calls and 23.0-23.3 us after 30, 60 or 100 ms (the
+    C3 logits product 53-55, 49-50 and 46.2 us), from the first call on."""
     from lanternl_amd import device
     for i in range(max(warmup, 1 if recorded else 0)):
         fn(i)
@@ -107,12 +107,16 @@ def time_launches(fn, steps, warmup, recorded=False, settle_ms=0.0):
         prog = device.Program.record(lambda: [fn(i) for i in range(steps)])
         prog.replay()            # first replay uploads the graph
         device.sync()
+        # the settling calls are eager launches, not replays: thousands of
+        # graph launches under rocprofv3 --kernel-trace ended in a host
+        # SIGSEGV inside hipGraphLaunch, where two replays per case never had
         busy = 0.0
         for _ in range(100000):
             if busy >= settle_ms:
                 break
             t.start()
-            prog.replay()
+            for i in range(steps):
+                fn(i)
             t.stop()
             device.sync()
             busy += t.ms()
